@@ -1,0 +1,93 @@
+"""Compile the gfx950 HIP sources into ``edgerag_amd/libedgerag_amd.so``, in-tree.
+
+hipcc cross-compiles for gfx950 without a GPU, so this runs anywhere the ROCm toolchain is
+installed. Every call recompiles. Objects go to ``edgerag_amd/_build/`` (ignored by git); the
+shared library lands next to the package so it travels with the source tree.
+
+Flags that matter:
+
+* ``--offload-arch=gfx950`` only: this library targets MI355X and nothing else.
+* ``-mcode-object-version=5``: loadable by the ROCm 7.0 runtime that torch bundles as well as by
+  ROCm 7.2.
+* ``-Xclang -target-feature -Xclang -packed-fp32-ops``: keep the compiler from emitting packed
+  fp32 VALU instructions (v_pk_fma_f32 and friends), which are not used in this library.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PACKAGE_DIR = Path(__file__).resolve().parent
+CSRC = PACKAGE_DIR / "csrc"
+BUILD_DIR = PACKAGE_DIR / "_build"
+LIB_NAME = "libedgerag_amd.so"
+LIB_PATH = PACKAGE_DIR / LIB_NAME
+
+ARCH = "gfx950"
+COMMON_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-fPIC",
+    "-std=c++17",
+    "-mcode-object-version=5",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-function",
+    "-Wno-unused-command-line-argument",
+    f"-I{PACKAGE_DIR.parent / 'include'}",
+]
+
+
+def hipcc() -> str:
+    for candidate in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if candidate and Path(candidate).exists():
+            return candidate
+    raise RuntimeError("hipcc not found: the ROCm toolchain is required to build edgerag_amd")
+
+
+def sources() -> list[Path]:
+    return sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
+
+
+def _compile(src: Path, verbose: bool) -> Path:
+    obj = BUILD_DIR / (src.stem + ".o")
+    lang = ["-x", "hip"] if src.suffix == ".hip" else []
+    cmd = [hipcc(), *COMMON_FLAGS, *lang, "-c", str(src), "-o", str(obj)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src.name}:\n{proc.stdout}\n{proc.stderr}")
+    if verbose and proc.stderr.strip():
+        print(proc.stderr, file=sys.stderr)
+    return obj
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> Path:
+    """Compile every HIP source and link the shared library. Returns its path."""
+    BUILD_DIR.mkdir(exist_ok=True)
+    srcs = sources()
+    jobs = jobs or min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
+    with ThreadPoolExecutor(max_workers=jobs) as pool:
+        objs = list(pool.map(lambda s: _compile(s, verbose), srcs))
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link failed:\n{proc.stdout}\n{proc.stderr}")
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

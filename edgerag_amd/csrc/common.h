@@ -1,0 +1,81 @@
+// Shared helpers for the gfx950 kernels: element types, 16-byte vector access, wave reductions,
+// and the thread-local error state behind edgerag_last_error().
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <hip/hip_bf16.h>
+
+#include <cstdint>
+
+#include "../../include/edgerag_amd.h"
+
+namespace edgerag {
+
+// ---- error state (capi.cpp) -----------------------------------------------------------------
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+// Converts a pending launch error into EDGERAG_EHIP; returns EDGERAG_OK otherwise.
+int check_launch(const char* what);
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+constexpr int kWave = 64;
+
+// ---- element types ---------------------------------------------------------------------------
+using f16 = __half;
+using bf16 = __hip_bfloat16;
+
+template <typename T> __device__ __forceinline__ float to_f32(T v);
+template <> __device__ __forceinline__ float to_f32<float>(float v) { return v; }
+template <> __device__ __forceinline__ float to_f32<f16>(f16 v) { return __half2float(v); }
+template <> __device__ __forceinline__ float to_f32<bf16>(bf16 v) { return __bfloat162float(v); }
+
+// Round-to-nearest-even conversions, matching torch's Tensor.to(dtype).
+template <typename T> __device__ __forceinline__ T from_f32(float v);
+template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <> __device__ __forceinline__ f16 from_f32<f16>(float v) { return __float2half_rn(v); }
+template <> __device__ __forceinline__ bf16 from_f32<bf16>(float v) { return __float2bfloat16(v); }
+
+template <typename T> struct Same { static constexpr bool value = false; };
+
+// A plain 16-byte register payload. Loads/stores through it compile to dwordx4 accesses.
+struct alignas(16) Vec16 {
+  uint32_t w[4];
+};
+
+template <typename T>
+__device__ __forceinline__ Vec16 load16(const T* p) {
+  return *reinterpret_cast<const Vec16*>(p);
+}
+template <typename T>
+__device__ __forceinline__ void store16(T* p, const Vec16& v) {
+  *reinterpret_cast<Vec16*>(p) = v;
+}
+
+// Element i of a 16-byte payload viewed as an array of T, widened to fp32.
+template <typename T>
+__device__ __forceinline__ float vec_elem(const Vec16& v, int i) {
+  const T* e = reinterpret_cast<const T*>(&v);
+  return to_f32<T>(e[i]);
+}
+
+// ---- wave reductions (64 lanes) --------------------------------------------------------------
+// Butterfly over lane-index bits [lo_bit, hi_bit): after the call every lane holds the reduction
+// over the 2^(hi-lo) lanes that differ from it only in those bits.
+template <int LO_BIT, int HI_BIT>
+__device__ __forceinline__ float xor_sum(float v) {
+#pragma unroll
+  for (int b = LO_BIT; b < HI_BIT; ++b) v += __shfl_xor(v, 1 << b, kWave);
+  return v;
+}
+template <int LO_BIT, int HI_BIT>
+__device__ __forceinline__ float xor_max(float v) {
+#pragma unroll
+  for (int b = LO_BIT; b < HI_BIT; ++b) v = fmaxf(v, __shfl_xor(v, 1 << b, kWave));
+  return v;
+}
+
+constexpr int ilog2(int v) { return v <= 1 ? 0 : 1 + ilog2(v / 2); }
+
+}  // namespace edgerag

@@ -1,0 +1,375 @@
+"""Tensor-level wrappers over the C ABI in ``include/edgerag_amd.h``.
+
+Each function validates shapes, dtypes and devices on the host, takes torch's current stream and
+calls exactly one entry point of ``libedgerag_amd.so``. Nothing here computes on the CPU: tensors
+must already live on the HIP device.
+
+Metadata for a ragged step (slot mapping, block tables, cu_seqlens, context lengths and the
+attention work plan) is built on the host once per step and moved with a single pinned H2D copy
+(:func:`upload_int32`), which replaces the reference's per-layer ``torch.tensor(table.blocks)``
+uploads (``BUGS.md`` P-06 in the reference; ``edgerag/cache/paged.py:198-199``, ``:222``).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from edgerag_amd import _lib
+from edgerag_amd._lib import call, dtype_code, ptr, require_device, stream_ptr  # noqa: F401
+
+__all__ = [
+    "AttentionPlan",
+    "dequantize",
+    "kv_append",
+    "kv_copy_blocks",
+    "kv_gather",
+    "paged_attention",
+    "plan_attention",
+    "quant_linear",
+    "quantize",
+    "upload_int32",
+]
+
+
+def upload_int32(arrays: list[np.ndarray], device: torch.device) -> list[torch.Tensor]:
+    """Pack int32 host arrays into one pinned buffer, copy it to ``device`` once, return views.
+
+    Each view starts on a 16-element boundary. The copy is asynchronous on the current stream;
+    torch's pinned-memory cache keeps the host buffer alive until the copy has completed.
+    """
+    offsets, total = [], 0
+    for a in arrays:
+        offsets.append(total)
+        total += (int(a.size) + 15) // 16 * 16
+    host = torch.empty(max(total, 16), dtype=torch.int32, pin_memory=True)
+    host_np = host.numpy()
+    for a, off in zip(arrays, offsets):
+        host_np[off : off + a.size] = a.reshape(-1)
+    dev = host.to(device, non_blocking=True)
+    return [dev[off : off + a.size].view(a.shape) for a, off in zip(arrays, offsets)]
+
+
+# --- KV cache ---------------------------------------------------------------------------------
+
+
+def _check_pool(pool: torch.Tensor, name: str) -> None:
+    if pool.dim() != 4:
+        raise ValueError(f"{name} must be (kv_heads, num_blocks, block_size, head_dim)")
+    if not pool.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def kv_append(
+    key: torch.Tensor | None,
+    value: torch.Tensor | None,
+    slot_mapping: torch.Tensor,
+    key_pool: torch.Tensor | None,
+    value_pool: torch.Tensor | None,
+) -> None:
+    """Scatter ``key``/``value`` ``(tokens, kv_heads, head_dim)`` into their slots.
+
+    ``slot_mapping`` is device int32 ``(tokens,)``: slot = block * block_size + offset, negative
+    to skip a token. Head-major pools ``(kv_heads, num_blocks, block_size, head_dim)``.
+    """
+    pool = key_pool if key_pool is not None else value_pool
+    src = key if key is not None else value
+    if pool is None or src is None:
+        raise ValueError("kv_append needs at least one of key/value with its pool")
+    require_device(key, value, slot_mapping, key_pool, value_pool)
+    for p, name in ((key_pool, "key_pool"), (value_pool, "value_pool")):
+        if p is not None:
+            _check_pool(p, name)
+            if p.shape != pool.shape or p.dtype != pool.dtype:
+                raise ValueError("key_pool and value_pool must match in shape and dtype")
+    if key is not None and value is not None:
+        if key.shape != value.shape or key.stride() != value.stride() or key.dtype != value.dtype:
+            raise ValueError("key and value must share shape, strides and dtype")
+    n_heads, num_blocks, block_size, head_dim = pool.shape
+    if src.dim() != 3 or src.shape[1] != n_heads or src.shape[2] != head_dim:
+        raise ValueError(
+            f"source must be (tokens, {n_heads}, {head_dim}), got {tuple(src.shape)}"
+        )
+    if src.stride(2) != 1:
+        raise ValueError("the head_dim axis of the source must be contiguous")
+    if slot_mapping.dtype != torch.int32 or slot_mapping.dim() != 1:
+        raise ValueError("slot_mapping must be a 1-D int32 tensor")
+    if slot_mapping.shape[0] != src.shape[0]:
+        raise ValueError(
+            f"slot_mapping has {slot_mapping.shape[0]} entries for {src.shape[0]} tokens"
+        )
+    if not slot_mapping.is_contiguous():
+        slot_mapping = slot_mapping.contiguous()
+    call(
+        "edgerag_kv_append",
+        ptr(key), ptr(value), dtype_code(src.dtype), src.stride(0), src.stride(1),
+        slot_mapping.data_ptr(), src.shape[0], ptr(key_pool), ptr(value_pool),
+        dtype_code(pool.dtype), n_heads, num_blocks, block_size, head_dim,
+        stream_ptr(src.device),
+    )
+
+
+def kv_gather(pool: torch.Tensor, block_ids: torch.Tensor, seq_len: int) -> torch.Tensor:
+    """``(kv_heads, seq_len, head_dim)`` history of one sequence, copied out of the pool."""
+    require_device(pool, block_ids)
+    _check_pool(pool, "pool")
+    n_heads, num_blocks, block_size, head_dim = pool.shape
+    out = torch.empty((n_heads, seq_len, head_dim), dtype=pool.dtype, device=pool.device)
+    if seq_len == 0:
+        return out
+    if block_ids.dtype != torch.int32:
+        block_ids = block_ids.to(torch.int32)
+    block_ids = block_ids.contiguous()
+    need = math.ceil(seq_len / block_size)
+    if block_ids.numel() < need:
+        raise ValueError(f"{seq_len} tokens need {need} blocks, got {block_ids.numel()}")
+    call(
+        "edgerag_kv_gather", pool.data_ptr(), dtype_code(pool.dtype), n_heads, num_blocks,
+        block_size, head_dim, block_ids.data_ptr(), seq_len, out.data_ptr(),
+        stream_ptr(pool.device),
+    )
+    return out
+
+
+def kv_copy_blocks(pool: torch.Tensor, src: torch.Tensor, dst: torch.Tensor) -> None:
+    """``pool[:, dst[i]] = pool[:, src[i]]`` for every pair (device int32 ids)."""
+    require_device(pool, src, dst)
+    _check_pool(pool, "pool")
+    if src.shape != dst.shape or src.dim() != 1:
+        raise ValueError("src and dst must be 1-D and the same length")
+    n_heads, num_blocks, block_size, head_dim = pool.shape
+    src = src.to(torch.int32).contiguous()
+    dst = dst.to(torch.int32).contiguous()
+    call(
+        "edgerag_kv_copy_blocks", pool.data_ptr(), dtype_code(pool.dtype), n_heads, num_blocks,
+        block_size, head_dim, src.data_ptr(), dst.data_ptr(), src.numel(),
+        stream_ptr(pool.device),
+    )
+
+
+# --- ragged paged attention -------------------------------------------------------------------
+
+
+@dataclass
+class AttentionPlan:
+    """Host plan plus its device copy, and everything the run needs for one step.
+
+    Built once per step and reused by every layer: the metadata is identical across layers.
+    """
+
+    plan_host: np.ndarray
+    plan_dev: torch.Tensor
+    query_start_loc: torch.Tensor
+    context_lens: torch.Tensor
+    block_tables: torch.Tensor
+    workspace: torch.Tensor | None
+    workspace_bytes: int
+    num_reqs: int
+    num_tokens: int
+    n_q_heads: int
+    n_kv_heads: int
+    head_dim: int
+    block_size: int
+    dtype: torch.dtype
+
+    @property
+    def n_items(self) -> int:
+        return int(self.plan_host[2])
+
+
+def make_plan_host(
+    query_start_loc: np.ndarray,
+    context_lens: np.ndarray,
+    n_q_heads: int,
+    n_kv_heads: int,
+    head_dim: int,
+    block_size: int,
+    max_blocks_per_seq: int,
+    dtype: torch.dtype,
+) -> tuple[np.ndarray, int]:
+    """Run the native host planner. Returns ``(plan words, workspace bytes)``."""
+    lib = _lib.load()
+    qsl = np.ascontiguousarray(query_start_loc, dtype=np.int32)
+    ctx = np.ascontiguousarray(context_lens, dtype=np.int32)
+    num_reqs = ctx.size
+    if qsl.size != num_reqs + 1:
+        raise ValueError(f"query_start_loc needs {num_reqs + 1} entries, got {qsl.size}")
+    words, ws = ctypes.c_int64(0), ctypes.c_int64(0)
+    args = (
+        qsl.ctypes.data, ctx.ctypes.data, num_reqs, n_q_heads, n_kv_heads, head_dim, block_size,
+        max_blocks_per_seq, dtype_code(dtype),
+    )
+    call("edgerag_attn_plan", *args, None, 0, ctypes.byref(words), ctypes.byref(ws))
+    plan = np.empty(words.value, dtype=np.int32)
+    call(
+        "edgerag_attn_plan", *args, plan.ctypes.data, plan.size, ctypes.byref(words),
+        ctypes.byref(ws),
+    )
+    del lib
+    return plan, int(ws.value)
+
+
+def plan_attention(
+    query_start_loc: np.ndarray,
+    context_lens: np.ndarray,
+    block_tables: np.ndarray,
+    n_q_heads: int,
+    n_kv_heads: int,
+    head_dim: int,
+    block_size: int,
+    dtype: torch.dtype,
+    device: torch.device,
+    extra_int32: list[np.ndarray] | None = None,
+) -> tuple[AttentionPlan, list[torch.Tensor]]:
+    """Plan a ragged step on the host and upload all of its metadata in one copy.
+
+    ``extra_int32`` arrays (e.g. the step's slot mapping) ride along in the same copy; their
+    device views are returned second.
+    """
+    block_tables = np.ascontiguousarray(block_tables, dtype=np.int32)
+    if block_tables.ndim != 2:
+        raise ValueError("block_tables must be (num_reqs, max_blocks)")
+    plan, ws_bytes = make_plan_host(
+        query_start_loc, context_lens, n_q_heads, n_kv_heads, head_dim, block_size,
+        block_tables.shape[1], dtype,
+    )
+    extra = list(extra_int32 or [])
+    views = upload_int32(
+        [plan, np.asarray(query_start_loc, np.int32), np.asarray(context_lens, np.int32),
+         block_tables, *extra],
+        device,
+    )
+    workspace = (
+        torch.empty(ws_bytes, dtype=torch.uint8, device=device) if ws_bytes > 0 else None
+    )
+    num_reqs = int(np.asarray(context_lens).size)
+    ap = AttentionPlan(
+        plan_host=plan, plan_dev=views[0], query_start_loc=views[1], context_lens=views[2],
+        block_tables=views[3], workspace=workspace, workspace_bytes=ws_bytes, num_reqs=num_reqs,
+        num_tokens=int(np.asarray(query_start_loc)[-1]) if num_reqs else 0,
+        n_q_heads=n_q_heads, n_kv_heads=n_kv_heads, head_dim=head_dim, block_size=block_size,
+        dtype=dtype,
+    )
+    return ap, views[4:]
+
+
+def paged_attention(
+    query: torch.Tensor,
+    key_pool: torch.Tensor,
+    value_pool: torch.Tensor,
+    plan: AttentionPlan,
+    scale: float,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Ragged paged attention. ``query``/``out``: ``(num_tokens, n_q_heads, head_dim)``."""
+    require_device(query, key_pool, value_pool)
+    _check_pool(key_pool, "key_pool")
+    _check_pool(value_pool, "value_pool")
+    if key_pool.shape != value_pool.shape or key_pool.dtype != value_pool.dtype:
+        raise ValueError("key_pool and value_pool must match")
+    n_kv, num_blocks, block_size, head_dim = key_pool.shape
+    if query.dim() != 3 or query.shape[1] != plan.n_q_heads or query.shape[2] != head_dim:
+        raise ValueError(
+            f"query must be (tokens, {plan.n_q_heads}, {head_dim}), got {tuple(query.shape)}"
+        )
+    if query.dtype != key_pool.dtype:
+        raise ValueError(f"query dtype {query.dtype} != pool dtype {key_pool.dtype}")
+    if (n_kv, block_size, head_dim, query.dtype) != (
+        plan.n_kv_heads, plan.block_size, plan.head_dim, plan.dtype
+    ):
+        raise ValueError("the attention plan was built for a different pool shape")
+    if query.stride(2) != 1:
+        query = query.contiguous()
+    if out is None:
+        out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
+    elif out.shape != query.shape or out.dtype != query.dtype or out.stride(2) != 1:
+        raise ValueError("out must match query in shape and dtype, head_dim contiguous")
+    ws = plan.workspace
+    call(
+        "edgerag_paged_attention",
+        plan.plan_host.ctypes.data, plan.plan_dev.data_ptr(), plan.plan_host.size,
+        query.data_ptr(), query.stride(0), query.stride(1),
+        key_pool.data_ptr(), value_pool.data_ptr(), dtype_code(key_pool.dtype),
+        plan.block_tables.data_ptr(), plan.block_tables.stride(0),
+        plan.query_start_loc.data_ptr(), plan.context_lens.data_ptr(),
+        plan.num_reqs, query.shape[0], plan.n_q_heads, n_kv, head_dim, block_size, num_blocks,
+        float(scale), out.data_ptr(), out.stride(0), out.stride(1),
+        None if ws is None else ws.data_ptr(), plan.workspace_bytes, stream_ptr(query.device),
+    )
+    return out
+
+
+# --- quantisation -----------------------------------------------------------------------------
+
+
+def quantize(weight: torch.Tensor, bits: int, group_size: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """``(packed uint8, scales fp16)`` for ``weight (N, K)``; bit-identical to the reference."""
+    require_device(weight)
+    if weight.dim() != 2:
+        raise ValueError(f"expected a 2-D weight, got shape {tuple(weight.shape)}")
+    weight = weight.contiguous()
+    n, k = weight.shape
+    width = k // 2 if bits == 4 else k
+    packed = torch.empty((n, width), dtype=torch.uint8, device=weight.device)
+    scales = torch.empty((n, max(k // group_size, 0)), dtype=torch.float16, device=weight.device)
+    call(
+        "edgerag_quantize", weight.data_ptr(), dtype_code(weight.dtype), n, k, bits, group_size,
+        packed.data_ptr(), scales.data_ptr(), stream_ptr(weight.device),
+    )
+    return packed, scales
+
+
+def dequantize(packed: torch.Tensor, scales: torch.Tensor, in_features: int, bits: int,
+               group_size: int) -> torch.Tensor:
+    """fp16 ``(N, K)`` weight rebuilt from codes and scales, as the reference dequantizes."""
+    require_device(packed, scales)
+    n = packed.shape[0]
+    out = torch.empty((n, in_features), dtype=torch.float16, device=packed.device)
+    scales = scales.to(torch.float16).contiguous()
+    call(
+        "edgerag_dequantize", packed.contiguous().data_ptr(), scales.data_ptr(), n, in_features,
+        bits, group_size, out.data_ptr(), stream_ptr(packed.device),
+    )
+    return out
+
+
+def quant_linear(
+    x: torch.Tensor,
+    packed: torch.Tensor,
+    scales: torch.Tensor,
+    bias: torch.Tensor | None,
+    in_features: int,
+    out_features: int,
+    bits: int,
+    group_size: int,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """``x (..., K) -> (..., N)`` through the fused dequant + GEMV/GEMM kernels."""
+    require_device(x, packed, scales, bias)
+    if x.shape[-1] != in_features:
+        raise ValueError(f"input has {x.shape[-1]} features, layer expects {in_features}")
+    if x.dtype not in (torch.float16, torch.float32):
+        raise TypeError(f"quant_linear takes float16 or float32 activations, not {x.dtype}")
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, in_features)
+    if x2.stride(1) != 1 or (x2.stride(0) * x2.element_size()) % 16 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    m = x2.shape[0]
+    if out is None:
+        y = torch.empty((m, out_features), dtype=x.dtype, device=x.device)
+    else:
+        y = out.view(m, out_features)
+    if scales.dtype != torch.float16:
+        scales = scales.to(torch.float16)
+    if bias is not None and bias.dtype != torch.float16:
+        bias = bias.to(torch.float16)
+    call(
+        "edgerag_quant_linear", x2.data_ptr(), dtype_code(x2.dtype), x2.stride(0), m,
+        in_features, packed.data_ptr(), scales.contiguous().data_ptr(), ptr(bias),
+        out_features, bits, group_size, y.data_ptr(), y.stride(0), stream_ptr(x.device),
+    )
+    return y.view(*lead, out_features)

@@ -1,0 +1,191 @@
+/*
+ * edgerag_amd.h -- C ABI of the MI355X (gfx950) ragged decoder-step library.
+ *
+ * One shared library, libedgerag_amd.so, exports every entry point below. They take raw device
+ * pointers, explicit sizes and strides, and a hipStream_t passed as void*. No torch types cross
+ * this boundary, so any host language with a C FFI can bind it (ctypes, cgo, JNI, N-API).
+ *
+ * Conventions shared by every entry point:
+ *   - return 0 on success, a positive EDGERAG_E* code on failure; edgerag_last_error() then holds
+ *     a thread-local, human-readable message;
+ *   - nothing here allocates device memory or synchronises the stream: callers own every buffer,
+ *     including the attention workspace sized by edgerag_attn_plan();
+ *   - kernels are enqueued on `stream` and run asynchronously; the entry points are reentrant and
+ *     keep no mutable global state, so calls from different host threads on different streams do
+ *     not interact;
+ *   - element types are EDGERAG_F32 / EDGERAG_F16 / EDGERAG_BF16 (see below).
+ *
+ * The reference (Tejas544/edgerag) is pure Python/PyTorch and has no FFI; each declaration cites
+ * the Python seam it replaces (file:line in the reference checkout).
+ */
+#ifndef EDGERAG_AMD_H
+#define EDGERAG_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------------------------- */
+#define EDGERAG_OK 0
+#define EDGERAG_EINVAL 1        /* bad argument: null pointer, shape, dtype or range */
+#define EDGERAG_EHIP 2          /* the HIP runtime reported an error (launch, copy) */
+#define EDGERAG_EWORKSPACE 3    /* workspace or plan buffer smaller than required */
+#define EDGERAG_EUNSUPPORTED 4  /* valid request this build does not implement */
+
+/* ---- element types ----------------------------------------------------------------------- */
+#define EDGERAG_F32 0
+#define EDGERAG_F16 1
+#define EDGERAG_BF16 2
+
+/* Message describing the last failure on the calling thread ("" if none). */
+const char* edgerag_last_error(void);
+
+/* Library version string, e.g. "edgerag_amd 0.1.0 gfx950". */
+const char* edgerag_version(void);
+
+/* ==== KV cache: slot-mapped append, gather, block copy ====================================== */
+
+/*
+ * Slot-mapped KV append: for every token t with slot s = slot_mapping[t] >= 0,
+ *   key_pool  [h, s / block_size, s % block_size, :] = key  [t, h, :]
+ *   value_pool[h, s / block_size, s % block_size, :] = value[t, h, :]
+ * for h in [0, n_kv_heads). Pools are head-major [n_kv_heads, num_blocks, block_size, head_dim]
+ * and contiguous. Source element (t, h, x) lives at src + t*stride_tok + h*stride_head + x (in
+ * elements; the head_dim axis is contiguous). Conversion src_dtype -> pool_dtype rounds to
+ * nearest-even, exactly like torch's Tensor.to(). Slots < 0 are skipped (padding); slots at or
+ * beyond num_blocks*block_size are skipped too, so a bad slot can never write out of bounds.
+ * Either of key/value may be NULL (with its pool) to append only the other.
+ *
+ * Replaces PagedKVCache._write, edgerag/cache/paged.py:186-206, with the slot mapping
+ * slot = table[pos // block_size] * block_size + pos % block_size built once per step.
+ */
+int edgerag_kv_append(const void* key, const void* value, int32_t src_dtype,
+                      int64_t src_stride_tok, int64_t src_stride_head,
+                      const int32_t* slot_mapping, int32_t num_tokens,
+                      void* key_pool, void* value_pool, int32_t pool_dtype,
+                      int32_t n_kv_heads, int32_t num_blocks, int32_t block_size,
+                      int32_t head_dim, void* stream);
+
+/*
+ * Materialise one sequence's history: out[h, p, :] = pool[h, block_ids[p / bs], p % bs, :] for
+ * p < seq_len, out contiguous [n_kv_heads, seq_len, head_dim] in the pool's dtype. Block ids
+ * outside [0, num_blocks) produce zeros rather than an out-of-bounds read.
+ *
+ * Replaces PagedKVCache.gather/_gather_pool, edgerag/cache/paged.py:208-238 (including the
+ * [:seq_len] slice that keeps the final block's slack out of attention).
+ */
+int edgerag_kv_gather(const void* pool, int32_t dtype, int32_t n_kv_heads, int32_t num_blocks,
+                      int32_t block_size, int32_t head_dim, const int32_t* block_ids,
+                      int32_t seq_len, void* out, void* stream);
+
+/*
+ * Copy whole blocks inside one pool: pool[:, dst[i]] = pool[:, src[i]] for i < n_pairs, every
+ * head. Pairs must not overlap (no block is both a source and a destination). Ids outside
+ * [0, num_blocks) are skipped.
+ *
+ * Replaces the copy-on-write content copy of PagedKVCache._unshare_write_range,
+ * edgerag/cache/paged.py:179-182 (and the pool[:, blocks] copies of cache/preemption.py:125-126).
+ */
+int edgerag_kv_copy_blocks(void* pool, int32_t dtype, int32_t n_kv_heads, int32_t num_blocks,
+                           int32_t block_size, int32_t head_dim, const int32_t* src_blocks,
+                           const int32_t* dst_blocks, int32_t n_pairs, void* stream);
+
+/* ==== Ragged paged attention =============================================================== */
+
+/*
+ * Host-only planning for edgerag_paged_attention (no GPU call is made).
+ *
+ * The batch holds num_reqs requests packed token-major. Request r owns query tokens
+ * [query_start_loc[r], query_start_loc[r+1]) (c_r of them) and, after this step's append,
+ * context_lens[r] = L_r visible tokens. Query i of request r sits at logical position
+ * L_r - c_r + i and attends keys [0, L_r - c_r + i] -- causal within the chunk, full over the
+ * cached prefix. c_r = 1 is a decode; c_r = 0 contributes nothing.
+ *
+ * Writes the work list into plan[0 .. *plan_words) (int32 words; upload it to the device as-is)
+ * and the device workspace size the run needs into *workspace_bytes. With plan == NULL only the
+ * two sizes are computed. Fails with EDGERAG_EINVAL if c_r > L_r, L_r needs more than
+ * max_blocks_per_seq blocks, or the shape is unsupported, and with EDGERAG_EWORKSPACE if
+ * plan_capacity_words is too small.
+ *
+ * Together with edgerag_paged_attention this replaces, per request, build_causal_mask +
+ * sdpa_attention over PagedKVCache.gather (edgerag/core/layers.py:137-167, :227-254;
+ * edgerag/cache/paged.py:208-238) and, for c_r = 1, paged_attention_reference /
+ * fused_paged_attention (edgerag/cache/fused.py:89-167, :242-286).
+ */
+int edgerag_attn_plan(const int32_t* query_start_loc, const int32_t* context_lens,
+                      int32_t num_reqs, int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                      int32_t block_size, int32_t max_blocks_per_seq, int32_t dtype,
+                      int32_t* plan, int64_t plan_capacity_words, int64_t* plan_words,
+                      int64_t* workspace_bytes);
+
+/*
+ * Run the planned attention. plan_host is the plan edgerag_attn_plan wrote (read on the host for
+ * the launch configuration) and plan_dev its device copy (read by the kernels). q:
+ * [num_tokens, n_q_heads, head_dim] at q + t*q_stride_tok + h*q_stride_head; out likewise. Pools
+ * are head-major and contiguous; block_tables is [num_reqs, block_tables_stride] int32 on the
+ * device; query_start_loc and context_lens are the device copies of the arrays given to
+ * edgerag_attn_plan. scale multiplies q.k (1/sqrt(head_dim) in the reference). Query head h reads
+ * kv head h / (n_q_heads / n_kv_heads) (repeat_interleave order, layers.py:117-134).
+ * Accumulation is fp32; out is written in `dtype` (the dtype of q and the pools). A query row with
+ * no visible key is written as zeros, never NaN. Block ids outside [0, num_blocks) contribute
+ * nothing. workspace must hold the *workspace_bytes the plan reported (NULL if that is 0).
+ */
+int edgerag_paged_attention(const int32_t* plan_host, const int32_t* plan_dev, int64_t plan_words,
+                            const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                            const void* key_pool, const void* value_pool, int32_t dtype,
+                            const int32_t* block_tables, int64_t block_tables_stride,
+                            const int32_t* query_start_loc, const int32_t* context_lens,
+                            int32_t num_reqs, int32_t num_tokens, int32_t n_q_heads,
+                            int32_t n_kv_heads, int32_t head_dim, int32_t block_size,
+                            int32_t num_blocks, float scale,
+                            void* out, int64_t out_stride_tok, int64_t out_stride_head,
+                            void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ==== Weight-only INT8 / INT4 quantisation and linear ===================================== */
+
+/*
+ * Group-wise symmetric quantisation of weight [N, K] (row-major, `w_dtype`) along K:
+ *   amax = max |w| over each group of group_size; scale = amax / qmax (fp32, or 1.0 if amax == 0)
+ *   code = clamp(round_half_even(w / scale), -qmax, qmax), qmax = 7 (bits 4) or 127 (bits 8)
+ * packed: bits 8 -> [N, K] uint8 two's complement; bits 4 -> [N, K/2] uint8 with byte j holding
+ * (code[2j] + 8) | (code[2j+1] + 8) << 4. scales: [N, K/group_size] fp16 (rounded from fp32).
+ * Bit-identical to the reference. K % group_size must be 0 (and K even for bits 4).
+ *
+ * Replaces quantize_groupwise + pack_int4 (edgerag/core/quant.py:60-95, :110-125) as called by
+ * QuantLinear.load_weight (edgerag/core/linear.py:166-184).
+ */
+int edgerag_quantize(const void* weight, int32_t w_dtype, int32_t n, int32_t k, int32_t bits,
+                     int32_t group_size, uint8_t* packed, void* scales_f16, void* stream);
+
+/*
+ * Reconstruct the fp16 weight [N, K]: w = fp16(code) * scale, product rounded to fp16.
+ *
+ * Replaces QuantLinear.dequantized (edgerag/core/linear.py:186-192 -> unpack_int4,
+ * dequantize_groupwise, edgerag/core/quant.py:98-138).
+ */
+int edgerag_dequantize(const uint8_t* packed, const void* scales_f16, int32_t n, int32_t k,
+                       int32_t bits, int32_t group_size, void* weight_f16, void* stream);
+
+/*
+ * y[M, N] = x[M, K] . W^T (+ bias), W = fp16(code * scale) exactly as edgerag_dequantize builds
+ * it, fp32 accumulation, y rounded to x's dtype. x: row stride x_stride (elements), contiguous
+ * along K; y: row stride y_stride. x/y dtype: EDGERAG_F16 (all M) or EDGERAG_F32 (correctness
+ * path). bias: [N] fp16 or NULL. M = 0 is a no-op.
+ *
+ * Replaces QuantLinear.forward = F.linear(x, dequantized().to(x.dtype), bias)
+ * (edgerag/core/linear.py:194-196) without materialising the fp16 weight: packed weights are
+ * streamed from HBM once and dequantised in registers.
+ */
+int edgerag_quant_linear(const void* x, int32_t x_dtype, int64_t x_stride, int32_t m, int32_t k,
+                         const uint8_t* packed, const void* scales_f16, const void* bias_f16,
+                         int32_t n, int32_t bits, int32_t group_size, void* y, int64_t y_stride,
+                         void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EDGERAG_AMD_H */

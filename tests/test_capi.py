@@ -1,0 +1,161 @@
+"""The C ABI: the library loads, exports every declared symbol, and its host-only planner is
+correct. No GPU is touched: only entry points that validate and return before any HIP call run.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+from hypothesis import given, settings
+from hypothesis import strategies as st
+
+from edgerag_amd import _lib, kernels
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "edgerag_amd.h"
+
+
+def declared_symbols() -> set[str]:
+    text = HEADER.read_text()
+    return set(re.findall(r"^(?:int|const char\*)\s+(edgerag_\w+)\s*\(", text, flags=re.M))
+
+
+def test_library_exports_every_declared_symbol() -> None:
+    lib = _lib.load()
+    names = declared_symbols()
+    assert len(names) >= 10
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in the header but not exported"
+    assert names == set(_lib.SIGNATURES), "ctypes signatures and header diverged"
+    assert _lib.version().startswith("edgerag_amd")
+
+
+def test_validation_errors_come_back_as_messages() -> None:
+    with pytest.raises(_lib.EdgeragError, match="only 4- and 8-bit"):
+        _lib.call("edgerag_quant_linear", None, 1, 16, 1, 16, None, None, None, 4, 3, 16, None,
+                  4, None)
+    with pytest.raises(_lib.EdgeragError, match="not divisible by group_size"):
+        _lib.call("edgerag_quantize", None, 1, 4, 100, 4, 128, None, None, None)
+    with pytest.raises(_lib.EdgeragError, match="pool dims"):
+        _lib.call("edgerag_kv_append", None, None, 1, 0, 0, None, 1, None, None, 1, 0, 1, 16,
+                  64, None)
+    with pytest.raises(_lib.EdgeragError, match="not a plan"):
+        _lib.call(
+            "edgerag_paged_attention",
+            None, None, 0,          # plan_host, plan_dev, plan_words
+            None, 0, 0,             # q, strides
+            None, None, 1,          # pools, dtype
+            None, 0, None, None,    # block tables, stride, query_start_loc, context_lens
+            0, 0, 4, 4, 64, 16, 1,  # num_reqs, num_tokens, heads, head_dim, block, num_blocks
+            1.0, None, 0, 0,        # scale, out, strides
+            None, 0, None,          # workspace, bytes, stream
+        )
+
+
+def test_device_guard_refuses_cpu_tensors() -> None:
+    with pytest.raises(ValueError, match="MI355X only"):
+        kernels.kv_gather(torch.zeros(1, 1, 16, 8), torch.zeros(1, dtype=torch.int32), 1)
+
+
+# --- the host planner ---------------------------------------------------------------------------
+
+ITEM_WORDS, REQ_WORDS = 8, 4
+
+
+def decode_plan(plan: np.ndarray):
+    n_items, n_reqs, item_off, req_off = (int(plan[i]) for i in (2, 3, 4, 5))
+    items = plan[item_off : item_off + n_items * ITEM_WORDS].reshape(n_items, ITEM_WORDS)
+    reqs = plan[req_off : req_off + n_reqs * REQ_WORDS].reshape(n_reqs, REQ_WORDS)
+    return items, reqs
+
+
+def check_coverage(qsl, ctx, n_q, n_kv, bs=16):
+    """Every (token, q-head, visible key) is covered by exactly one (item, split)."""
+    plan, ws = kernels.make_plan_host(np.array(qsl, np.int32), np.array(ctx, np.int32), n_q, n_kv,
+                                      64, bs, max(1, -(-max(ctx + [1]) // bs)), torch.float16)
+    items, reqs = decode_plan(plan)
+    n_rep = n_q // n_kv
+    seen: dict[tuple[int, int, int], int] = {}
+    for r, h, qb, qc, kb, ke, split, _kind in items.tolist():
+        q0, c, L = qsl[r], qsl[r + 1] - qsl[r], ctx[r]
+        assert q0 <= qb and qb + qc <= q0 + c
+        nsplit, split_len = reqs[r][0], reqs[r][1]
+        assert kb == split * split_len and ke <= min(L, (split + 1) * split_len)
+        for t in range(qb, qb + qc):
+            lim = L - c + (t - q0)
+            for hq in range(h * n_rep, (h + 1) * n_rep):
+                key = (t, hq, split)
+                assert key not in seen
+                seen[key] = min(ke, lim + 1) - kb
+    n_partials = 0
+    for r in range(len(ctx)):
+        q0, c, L = qsl[r], qsl[r + 1] - qsl[r], ctx[r]
+        nsplit, split_len = int(reqs[r][0]), int(reqs[r][1])
+        if c and nsplit > 1:
+            n_partials += c * n_q * nsplit
+        for t in range(q0, q0 + c):
+            lim = L - c + (t - q0)
+            for hq in range(n_q):
+                covered = sum(max(0, seen.get((t, hq, s), 0)) for s in range(max(nsplit, 0)))
+                assert covered == lim + 1, (r, t, hq)
+    assert int(plan[6]) == n_partials
+    if n_partials == 0:
+        assert ws == 0
+    return items
+
+
+@given(
+    reqs=st.lists(
+        st.tuples(st.integers(0, 3000), st.integers(0, 600)), min_size=1, max_size=12
+    ),
+    heads=st.sampled_from([(4, 4), (9, 3), (8, 2), (32, 32)]),
+)
+@settings(max_examples=40, deadline=None)
+def test_plan_covers_every_visible_key_exactly_once(reqs, heads) -> None:
+    ctx, q_lens = [], []
+    for L, c in reqs:
+        c = min(c, L)
+        ctx.append(L)
+        q_lens.append(c)
+    qsl = [0]
+    for c in q_lens:
+        qsl.append(qsl[-1] + c)
+    check_coverage(qsl, ctx, *heads)
+
+
+def test_plan_for_cfg1_and_ordering() -> None:
+    items = check_coverage([0, 1, 2, 3, 4], [37, 128, 300, 511], 9, 3)
+    costs = (items[:, 5] - items[:, 4]).tolist()
+    assert costs == sorted(costs, reverse=True), "items must be heaviest first"
+
+
+def test_plan_rejects_bad_batches() -> None:
+    with pytest.raises(_lib.EdgeragError, match="queries but context"):
+        kernels.make_plan_host(np.array([0, 5], np.int32), np.array([4], np.int32), 4, 4, 64, 16,
+                               8, torch.float16)
+    with pytest.raises(_lib.EdgeragError, match="block table holds"):
+        kernels.make_plan_host(np.array([0, 1], np.int32), np.array([100], np.int32), 4, 4, 64,
+                               16, 2, torch.float16)
+    with pytest.raises(_lib.EdgeragError, match="query heads against"):
+        kernels.make_plan_host(np.array([0, 1], np.int32), np.array([10], np.int32), 6, 4, 64, 16,
+                               2, torch.float16)
+    with pytest.raises(_lib.EdgeragError, match="head_dim"):
+        kernels.make_plan_host(np.array([0, 1], np.int32), np.array([10], np.int32), 4, 4, 48, 16,
+                               2, torch.float16)
+
+
+def test_plan_size_query_without_buffer() -> None:
+    words, ws = ctypes.c_int64(0), ctypes.c_int64(0)
+    qsl = np.array([0, 1], np.int32)
+    ctx = np.array([5000], np.int32)
+    _lib.call("edgerag_attn_plan", qsl.ctypes.data, ctx.ctypes.data, 1, 32, 32, 64, 16, 400, 1,
+              None, 0, ctypes.byref(words), ctypes.byref(ws))
+    assert words.value > 16 and ws.value > 0
+    small = np.empty(4, np.int32)
+    with pytest.raises(_lib.EdgeragError, match="capacity"):
+        _lib.call("edgerag_attn_plan", qsl.ctypes.data, ctx.ctypes.data, 1, 32, 32, 64, 16, 400,
+                  1, small.ctypes.data, 4, ctypes.byref(words), ctypes.byref(ws))

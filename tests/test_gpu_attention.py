@@ -1,0 +1,304 @@
+"""Paged attention on the GPU against the oracle.
+
+Cases restate the reference's own tests (tests/test_fused_attention.py) and its GPU gate
+(scripts/colab_fused_attention.py:62, :132-133, :254), then widen to the ragged decode +
+chunked-prefill batches of BASELINE configs 1-3.
+
+Tolerances, written where they are used:
+* fp32 pools: 1e-5 (test_fused_attention.py:91);
+* fp16 pools: atol 2e-3 / rtol 1e-2 (north_star; colab_fused_attention.py:254).
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from edgerag_amd import kernels
+from edgerag_amd.cache.fused import fused_paged_attention, ragged_paged_attention
+from oracle import attention as oa
+from oracle import paged as op
+from tests.conftest import seeded
+
+pytestmark = pytest.mark.gpu
+
+BLOCK_SIZE = 16
+FP32_TOL = dict(rtol=1e-5, atol=1e-5)
+FP16_TOL = dict(rtol=1e-2, atol=2e-3)
+
+
+def _pool(n_kv_heads, num_blocks, head_dim, dtype, g):
+    shape = (n_kv_heads, num_blocks, BLOCK_SIZE, head_dim)
+    return torch.randn(shape, generator=g).to(dtype), torch.randn(shape, generator=g).to(dtype)
+
+
+# --- fused_paged_attention: the reference's own cases ------------------------------------------
+
+
+@pytest.mark.parametrize(
+    "seq_len", [1, 2, 15, 16, 17, 31, 32, 33, 47, 48, 49, 63, 64, 65, 100, 127, 128, 129]
+)
+def test_decode_matches_reference_across_block_boundaries(device, seq_len) -> None:
+    """test_fused_attention.py:71-91 (head_dim 8, fp32, 1e-5)."""
+    g = seeded(seq_len)
+    n_kv, d = 4, 8
+    nb = math.ceil(seq_len / BLOCK_SIZE)
+    kp, vp = _pool(n_kv, nb + 3, d, torch.float32, g)
+    ids = torch.randperm(nb + 3, generator=g)[:nb]
+    q = torch.randn(1, n_kv, 1, d, generator=g)
+    scale = d**-0.5
+    expected = oa.sdpa_over_gather(q, kp, vp, ids, seq_len, scale, 1)
+    spec = oa.paged_attention_reference(q, kp, vp, ids, seq_len, scale, 1)
+    torch.testing.assert_close(spec, expected, **FP32_TOL)
+    got = fused_paged_attention(q.to(device), kp.to(device), vp.to(device), ids.to(device),
+                                seq_len, scale)
+    assert got.shape == (1, 1, n_kv, d) and got.dtype == torch.float32
+    torch.testing.assert_close(got.cpu(), spec, **FP32_TOL)
+
+
+def test_unwritten_tail_of_final_block_is_never_attended(device) -> None:
+    """test_fused_attention.py:94-116: poison the slack with 1e4."""
+    g = seeded(17)
+    kp, vp = _pool(2, 4, 8, torch.float32, g)
+    ids = torch.tensor([0, 1])
+    q = torch.randn(1, 2, 1, 8, generator=g)
+    args = (ids.to(device), 17, 8**-0.5)
+    clean = fused_paged_attention(q.to(device), kp.to(device), vp.to(device), *args)
+    kp[:, 1, 1:] = 1e4
+    vp[:, 1, 1:] = 1e4
+    poisoned = fused_paged_attention(q.to(device), kp.to(device), vp.to(device), *args)
+    torch.testing.assert_close(poisoned, clean, rtol=1e-6, atol=1e-6)
+
+
+def test_blocks_past_the_written_region_are_not_read(device) -> None:
+    """test_fused_attention.py:119-131."""
+    g = seeded(20)
+    kp, vp = _pool(2, 6, 8, torch.float32, g)
+    kp[:, 2:] = 1e4
+    vp[:, 2:] = 1e4
+    q = torch.randn(1, 2, 1, 8, generator=g).to(device)
+    kp, vp = kp.to(device), vp.to(device)
+    a = fused_paged_attention(q, kp, vp, torch.tensor([0, 1], device=device), 20, 8**-0.5)
+    b = fused_paged_attention(q, kp, vp, torch.tensor([0, 1, 2, 3], device=device), 20, 8**-0.5)
+    torch.testing.assert_close(a, b, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("n_rep", [1, 2, 3, 4])
+def test_grouped_query_heads_map_consecutively(device, n_rep) -> None:
+    """test_fused_attention.py:134-154: kv_head = q_head // n_rep."""
+    g = seeded(40 + n_rep)
+    n_kv = 3
+    kp, vp = _pool(n_kv, 5, 8, torch.float32, g)
+    ids = torch.tensor([0, 1, 2])
+    q = torch.randn(1, n_kv * n_rep, 1, 8, generator=g)
+    expected = oa.sdpa_over_gather(q, kp, vp, ids, 40, 8**-0.5, n_rep)
+    got = fused_paged_attention(q.to(device), kp.to(device), vp.to(device), ids.to(device), 40,
+                                8**-0.5, n_rep)
+    torch.testing.assert_close(got.cpu(), expected, **FP32_TOL)
+
+
+def test_scattered_block_table(device) -> None:
+    """test_fused_attention.py:157-169."""
+    g = seeded(48)
+    kp, vp = _pool(2, 8, 8, torch.float32, g)
+    ids = torch.tensor([7, 2, 5])
+    q = torch.randn(1, 2, 1, 8, generator=g)
+    expected = oa.sdpa_over_gather(q, kp, vp, ids, 48, 8**-0.5, 1)
+    got = fused_paged_attention(q.to(device), kp.to(device), vp.to(device), ids.to(device), 48,
+                                8**-0.5)
+    torch.testing.assert_close(got.cpu(), expected, **FP32_TOL)
+
+
+def test_scores_that_would_overflow_a_naive_softmax_stay_finite(device) -> None:
+    """test_fused_attention.py:175-190."""
+    g = seeded(33)
+    kp, vp = _pool(2, 4, 8, torch.float32, g)
+    kp *= 200.0
+    q = torch.randn(1, 2, 1, 8, generator=g) * 200.0
+    ids = torch.tensor([0, 1, 2])
+    got = fused_paged_attention(q.to(device), kp.to(device), vp.to(device), ids.to(device), 33,
+                                8**-0.5)
+    assert torch.isfinite(got).all()
+    expected = oa.paged_attention_reference(q, kp, vp, ids, 33, 8**-0.5)
+    torch.testing.assert_close(got.cpu(), expected, rtol=1e-4, atol=1e-4)
+
+
+def test_empty_sequence_returns_zeros(device) -> None:
+    """test_fused_attention.py:193-201."""
+    g = seeded(0)
+    kp, vp = _pool(2, 2, 8, torch.float32, g)
+    out = fused_paged_attention(torch.randn(1, 2, 1, 8).to(device), kp.to(device), vp.to(device),
+                                torch.tensor([0], device=device), 0, 8**-0.5)
+    assert torch.isfinite(out).all() and torch.count_nonzero(out) == 0
+
+
+def test_guards(device) -> None:
+    """test_fused_attention.py:207-223: prefill refused; head mismatch refused."""
+    g = seeded(1)
+    kp, vp = _pool(2, 4, 8, torch.float32, g)
+    kp, vp = kp.to(device), vp.to(device)
+    with pytest.raises(ValueError, match="decode path"):
+        fused_paged_attention(torch.randn(1, 2, 7, 8, device=device), kp, vp,
+                              torch.tensor([0], device=device), 16, 8**-0.5)
+    with pytest.raises(ValueError, match="query heads"):
+        fused_paged_attention(torch.randn(1, 6, 1, 8, device=device), kp, vp,
+                              torch.tensor([0], device=device), 16, 8**-0.5, n_rep=1)
+
+
+@pytest.mark.parametrize(
+    "seq_len", [1, 2, 15, 16, 17, 31, 32, 33, 127, 128, 129, 511, 512, 513, 6758, 6759]
+)
+def test_fp16_gate_lengths_with_poisoned_slack(device, seq_len) -> None:
+    """colab_fused_attention.py:62 gate lengths, slack poisoned with 1e4 (:132-133), 2e-3."""
+    g = seeded(seq_len + 1000)
+    n_kv, d = 32, 64
+    nb = math.ceil(seq_len / BLOCK_SIZE)
+    kp, vp = _pool(n_kv, nb + 2, d, torch.float16, g)
+    ids = torch.randperm(nb + 2, generator=g)[:nb]
+    last, used = int(ids[-1]), seq_len - (nb - 1) * BLOCK_SIZE
+    kp[:, last, used:] = 1e4
+    vp[:, last, used:] = 1e4
+    q = torch.randn(1, n_kv, 1, d, generator=g).half()
+    expected = oa.paged_attention_reference(q.float(), kp.float(), vp.float(), ids, seq_len,
+                                            d**-0.5)
+    got = fused_paged_attention(q.to(device), kp.to(device), vp.to(device), ids.to(device),
+                                seq_len, d**-0.5)
+    assert got.dtype == torch.float16
+    torch.testing.assert_close(got.float().cpu(), expected, **FP16_TOL)
+
+
+# --- ragged batches ----------------------------------------------------------------------------
+
+
+def _ragged_case(lens, q_lens, n_q, n_kv, d, dtype, seed, pool_blocks=None, poison=True):
+    """Seeded ragged batch: pools, disjoint tables from one permutation, packed queries."""
+    g = seeded(seed)
+    nbs = [math.ceil(L / BLOCK_SIZE) for L in lens]
+    NB = pool_blocks or (sum(nbs) + 4)
+    kp, vp = _pool(n_kv, NB, d, dtype, g)
+    perm = torch.randperm(NB, generator=g).tolist()
+    tables, at = [], 0
+    for nb in nbs:
+        tables.append(perm[at : at + nb])
+        at += nb
+    if poison:
+        for L, t in zip(lens, tables):
+            if t and L % BLOCK_SIZE:
+                kp[:, t[-1], L % BLOCK_SIZE :] = 1e4
+                vp[:, t[-1], L % BLOCK_SIZE :] = 1e4
+    qsl = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    q = torch.randn(int(qsl[-1]), n_q, d, generator=g).to(dtype)
+    maxb = max(nbs + [1])
+    bt = np.full((len(lens), maxb), -1, np.int32)
+    for r, t in enumerate(tables):
+        bt[r, : len(t)] = t
+    return kp, vp, tables, qsl, q, bt
+
+
+def _run_ragged(device, kp, vp, qsl, lens, bt, q, scale):
+    return ragged_paged_attention(
+        q.to(device), kp.to(device), vp.to(device), qsl, np.asarray(lens, np.int32), bt, scale
+    ).cpu()
+
+
+def test_cfg1_gqa_decode_batch_fp32(device) -> None:
+    """lengths [37,128,300,511], 9/3 heads, d 64, pool 64, fp32, 1e-5."""
+    lens = [37, 128, 300, 511]
+    kp, vp, tables, qsl, q, bt = _ragged_case(lens, [1] * 4, 9, 3, 64, torch.float32, 11,
+                                              pool_blocks=64)
+    expected = oa.ragged_reference(q, kp, vp, qsl.tolist(), lens, tables, 0.125)
+    got = _run_ragged(device, kp, vp, qsl, lens, bt, q, 0.125)
+    torch.testing.assert_close(got, expected, **FP32_TOL)
+    # and against the blockwise spec per request
+    for r, L in enumerate(lens):
+        spec = oa.paged_attention_reference(
+            q[r][None, :, None], kp, vp, torch.tensor(tables[r]), L, 0.125, 3
+        )
+        torch.testing.assert_close(got[r], spec[0, 0], **FP32_TOL)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_mixed_prefill_chunks_and_decodes(device, dtype) -> None:
+    """A cfg3-shaped batch, scaled down: prefill slices (causal + prefix) beside decodes."""
+    lens = [40, 64 + 37, 300, 17, 1000, 5]
+    q_lens = [40, 37, 1, 1, 129, 5]  # chunk at offset 0, chunk at offset 64, decodes, ...
+    tol = FP32_TOL if dtype == torch.float32 else FP16_TOL
+    kp, vp, tables, qsl, q, bt = _ragged_case(lens, q_lens, 8, 4, 64, dtype, 77)
+    expected = oa.ragged_reference(q, kp, vp, qsl.tolist(), lens, tables, 0.125)
+    got = _run_ragged(device, kp, vp, qsl, lens, bt, q, 0.125)
+    torch.testing.assert_close(got.float(), expected, **tol)
+    # float64 textbook pin for one head of the offset chunk
+    r, h = 1, 5
+    k = op.gather_pool(kp.float(), tables[r], lens[r])[h // 2]
+    v = op.gather_pool(vp.float(), tables[r], lens[r])[h // 2]
+    ref64 = oa.attention_f64(q[qsl[r] : qsl[r + 1], h], k, v, lens[r] - q_lens[r], 0.125)
+    torch.testing.assert_close(got[qsl[r] : qsl[r + 1], h].double(), ref64, **{
+        k_: v_ * 2 for k_, v_ in tol.items()})
+
+
+def test_chunked_prefill_equals_single_shot(device) -> None:
+    """test_batched.py:80-119 restated: 3 chunks over the same pool == 1 chunk."""
+    L, d = 300, 64
+    kp, vp, tables, _, q, bt = _ragged_case([L], [L], 4, 4, d, torch.float32, 5)
+    one = _run_ragged(device, kp, vp, np.array([0, L], np.int32), [L], bt, q, 0.125)
+    parts = []
+    for start, end in ((0, 128), (128, 256), (256, 300)):
+        parts.append(_run_ragged(device, kp, vp, np.array([0, end - start], np.int32), [end], bt,
+                                 q[start:end], 0.125))
+    torch.testing.assert_close(torch.cat(parts), one, rtol=5e-5 * 3, atol=5e-5 * 3)
+
+
+def test_single_chunk_without_prefix_equals_causal_sdpa(device) -> None:
+    """Special case: past = 0 reduces to SDPA(is_causal=True), a library routine."""
+    L = 257
+    kp, vp, tables, qsl, q, bt = _ragged_case([L], [L], 4, 2, 64, torch.float32, 6)
+    k = op.gather_pool(kp, tables[0], L).repeat_interleave(2, dim=0)
+    v = op.gather_pool(vp, tables[0], L).repeat_interleave(2, dim=0)
+    ref = torch.nn.functional.scaled_dot_product_attention(
+        q.transpose(0, 1), k, v, is_causal=True, scale=0.125
+    ).transpose(0, 1)
+    got = _run_ragged(device, kp, vp, qsl, [L], bt, q, 0.125)
+    torch.testing.assert_close(got, ref, **FP32_TOL)
+
+
+def test_zero_query_requests_and_empty_batch(device) -> None:
+    lens = [33, 50, 20]
+    kp, vp, tables, qsl, q, bt = _ragged_case(lens, [1, 0, 2], 4, 4, 64, torch.float32, 8)
+    expected = oa.ragged_reference(q, kp, vp, qsl.tolist(), lens, tables, 0.125)
+    got = _run_ragged(device, kp, vp, qsl, lens, bt, q, 0.125)
+    torch.testing.assert_close(got, expected, **FP32_TOL)
+
+
+def test_plan_rejects_more_queries_than_context(device) -> None:
+    kp, vp, tables, qsl, q, bt = _ragged_case([10], [10], 4, 4, 64, torch.float32, 8)
+    with pytest.raises(kernels._lib.EdgeragError, match="queries but context"):
+        _run_ragged(device, kp, vp, np.array([0, 10], np.int32), [9], bt, q, 0.125)
+
+
+def test_cfg2_shape_decode_batch_fp16(device) -> None:
+    """BASELINE config 2 at full shape: 32 decodes, L ~ U[256, 7472], 32/32 heads, d 64,
+    16,384-block pool (1 GiB per pool), seeded-shuffled tables."""
+    g = seeded(2)
+    lens = torch.randint(256, 7473, (32,), generator=g).tolist()
+    nbs = [math.ceil(L / BLOCK_SIZE) for L in lens]
+    perm = torch.randperm(16384, generator=g).tolist()
+    tables, at = [], 0
+    for nb in nbs:
+        tables.append(perm[at : at + nb])
+        at += nb
+    gd = torch.Generator(device=device).manual_seed(2)
+    shape = (32, 16384, BLOCK_SIZE, 64)
+    kp_d = torch.randn(shape, generator=gd, device=device, dtype=torch.float16)
+    vp_d = torch.randn(shape, generator=gd, device=device, dtype=torch.float16)
+    q = torch.randn(32, 32, 64, generator=g).half()
+    qsl = np.arange(33, dtype=np.int32)
+    bt = np.full((32, max(nbs)), -1, np.int32)
+    for r, t in enumerate(tables):
+        bt[r, : len(t)] = t
+    got = ragged_paged_attention(q.to(device), kp_d, vp_d, qsl, np.asarray(lens, np.int32), bt,
+                                 0.125).cpu()
+    expected = oa.ragged_reference(q, kp_d.cpu(), vp_d.cpu(), qsl.tolist(), lens, tables, 0.125)
+    torch.testing.assert_close(got.float(), expected, **FP16_TOL)

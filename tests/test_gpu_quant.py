@@ -1,0 +1,146 @@
+"""INT8 / INT4 quantisation and quant linear on the GPU against the oracle.
+
+Bit-exact: quantize (codes + fp16 scales), pack, dequantize. Within fp16 rtol 1e-2 (north_star):
+the fused linear against dequant-then-matmul evaluated in fp32 on the same fp16 weights.
+Shapes are BASELINE config 4; KATs restate tests/test_quant.py.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from edgerag_amd import kernels
+from edgerag_amd.core.linear import FP16Linear, QuantLinear
+from edgerag_amd.core.quant import (
+    QuantConfig,
+    dequantize_groupwise,
+    pack_int4,
+    quantize_groupwise,
+    unpack_int4,
+)
+from oracle import quant as oq
+from tests.conftest import seeded
+
+pytestmark = pytest.mark.gpu
+
+LINEAR_TOL = dict(rtol=1e-2, atol=2e-3)
+
+CFG4 = [  # (K, N, bits, group) -- INT8 per-channel and INT4 g128
+    (2048, 2048, 8, 2048),
+    (2048, 8192, 8, 2048),
+    (8192, 2048, 8, 8192),
+    (1152, 1152, 4, 128),
+    (1152, 4608, 4, 128),
+]
+
+
+def _weight(n, k, seed, scale=0.02, dtype=torch.float16):
+    return (torch.randn(n, k, generator=seeded(seed)) * scale).to(dtype)
+
+
+@pytest.mark.parametrize(
+    "n,k,bits,g,dtype",
+    [
+        (64, 256, 4, 128, torch.float32),
+        (64, 256, 8, 128, torch.float32),
+        (64, 256, 8, 256, torch.float16),
+        (33, 120, 4, 120, torch.float32),
+        (17, 96, 4, 6, torch.bfloat16),
+        *[(n, k, b, g, torch.float16) for (k, n, b, g) in CFG4],
+    ],
+)
+def test_quantize_is_bit_exact(device, n, k, bits, g, dtype) -> None:
+    w = _weight(n, k, n * 7 + k, dtype=dtype)
+    cfg = oq.QuantConfig(group_size=g, bits=bits)
+    exp_packed, exp_scales = oq.quantize_for_layer(w, cfg)
+    packed, scales = kernels.quantize(w.to(device), bits, g)
+    assert torch.equal(packed.cpu(), exp_packed)
+    assert torch.equal(scales.cpu().view(torch.int16), exp_scales.view(torch.int16))
+    codes, sc = quantize_groupwise(w.to(device), QuantConfig(g, bits))
+    exp_codes, _ = oq.quantize_groupwise(w, cfg)
+    assert torch.equal(codes.cpu(), exp_codes)
+
+
+@pytest.mark.parametrize("n,k,bits,g", [(64, 256, 4, 128), (40, 512, 8, 512), (16, 1152, 4, 128)])
+def test_dequantize_is_bit_exact(device, n, k, bits, g) -> None:
+    w = _weight(n, k, 3)
+    cfg = oq.QuantConfig(g, bits)
+    packed, scales = oq.quantize_for_layer(w, cfg)
+    expected = oq.dequantized(packed, scales, k, cfg)
+    got = kernels.dequantize(packed.to(device), scales.to(device), k, bits, g)
+    assert torch.equal(got.cpu().view(torch.int16), expected.view(torch.int16))
+
+
+def test_known_answer_vectors(device) -> None:
+    """tests/test_quant.py:193-232: zero group, exactly representable levels, nibble signs."""
+    codes, scales = quantize_groupwise(torch.zeros(4, 128, device=device), QuantConfig())
+    assert torch.isfinite(scales).all()
+    assert torch.equal(dequantize_groupwise(codes, scales).cpu(), torch.zeros(4, 128).half())
+
+    w = torch.tensor([[float(v) for v in range(-7, 8)] * 8], device=device)
+    c, s = quantize_groupwise(w, QuantConfig(group_size=120))
+    torch.testing.assert_close(dequantize_groupwise(c, s, QuantConfig(120)).float(), w,
+                               atol=1e-3, rtol=1e-3)
+
+    kat = torch.tensor([[-7, 7, -1, 1, 0, -4, 4, -7]], dtype=torch.int8, device=device)
+    assert torch.equal(unpack_int4(pack_int4(kat), 8), kat)
+    assert torch.equal(pack_int4(kat).cpu(), oq.pack_int4(kat.cpu()))
+
+
+@pytest.mark.parametrize("k,n,bits,g", CFG4)
+@pytest.mark.parametrize("m", [1, 8, 32, 64, 512, 544])
+def test_quant_linear_cfg4(device, k, n, bits, g, m) -> None:
+    w = _weight(n, k, k + n)
+    cfg = oq.QuantConfig(g, bits)
+    packed, scales = oq.quantize_for_layer(w, cfg)
+    x = torch.randn(m, k, generator=seeded(m)).half()
+    expected = oq.quant_linear_reference(x, packed, scales, None, k, cfg)
+    y = kernels.quant_linear(x.to(device), packed.to(device), scales.to(device), None, k, n, bits, g)
+    assert y.dtype == torch.float16 and y.shape == (m, n)
+    torch.testing.assert_close(y.float().cpu(), expected, **LINEAR_TOL)
+
+
+@pytest.mark.parametrize("m", [1, 3, 7])
+def test_quant_linear_bias_fp32_and_generic_shapes(device, m) -> None:
+    """Bias, fp32 activations, and K / group sizes off the vector path (K=120, g=120; g=6)."""
+    for (n, k, bits, g, xdt) in [(64, 256, 4, 128, torch.float32), (33, 120, 8, 120, torch.float16),
+                                 (19, 96, 4, 6, torch.float16), (48, 512, 8, 512, torch.float32)]:
+        w = _weight(n, k, n + k + m)
+        cfg = oq.QuantConfig(g, bits)
+        packed, scales = oq.quantize_for_layer(w, cfg)
+        bias = (torch.randn(n, generator=seeded(n)) * 0.1).half()
+        x = torch.randn(m, k, generator=seeded(m + 1)).to(xdt)
+        expected = oq.quant_linear_reference(x, packed, scales, bias, k, cfg)
+        y = kernels.quant_linear(x.to(device), packed.to(device), scales.to(device),
+                                 bias.to(device), k, n, bits, g)
+        assert y.dtype == xdt
+        tol = LINEAR_TOL if xdt == torch.float16 else dict(rtol=1e-5, atol=1e-5)
+        torch.testing.assert_close(y.float().cpu(), expected, **tol)
+
+
+def test_quant_linear_module_matches_fp16_within_quantization_error(device) -> None:
+    """tests/test_quant.py:243-257 on the device module."""
+    w = (torch.randn(64, 256, generator=seeded(0)) * 0.02)
+    x = torch.randn(4, 256, generator=seeded(7)).half().to(device)
+    ref = FP16Linear(256, 64).half().to(device)
+    ref.load_weight(w.half().to(device))
+    layer = QuantLinear(256, 64, device=device)
+    layer.load_weight(w)
+    rel = (layer(x).float() - ref(x).float()).abs().mean() / ref(x).float().abs().mean()
+    assert float(rel) < 0.12
+    before = layer.packed.clone()
+    layer(x)
+    assert torch.equal(layer.packed, before)  # quantisation happens at load, not in forward
+    assert layer.weight_bytes() == 64 * 128 + 64 * 2 * 2
+
+
+def test_fused_concat_equals_separate_layers(device) -> None:
+    layers = []
+    for i, n in enumerate((64, 32, 32)):
+        layer = QuantLinear(256, n, config=QuantConfig(256, 8), device=device)
+        layer.load_weight(torch.randn(n, 256, generator=seeded(i)) * 0.02)
+        layers.append(layer)
+    fused = QuantLinear.concat(layers)
+    x = torch.randn(5, 256, generator=seeded(9)).half().to(device)
+    assert torch.equal(fused(x), torch.cat([layer(x) for layer in layers], dim=-1))
