@@ -123,6 +123,23 @@ def time_step(b, steps, warmup):
     return wall0.elapsed_time(wall1) / steps, attn_ms, step_ms
 
 
+def copy_bandwidth(device, nbytes=1 << 30, iters=20):
+    """Read+write GB/s of torch's device copy over 1 GiB: the practical streaming ceiling."""
+    src = torch.empty(nbytes // 2, dtype=torch.float16, device=device).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / iters
+    return round(2 * nbytes / us / 1e3, 1)
+
+
 def cfg2_lens():
     g = torch.Generator().manual_seed(2)
     return torch.randint(256, 7473, (32,), generator=g).tolist()
@@ -290,6 +307,8 @@ def main() -> None:
         },
     }
     del b
+    torch.cuda.empty_cache()
+    line["config"]["copy_gbs_1gib"] = copy_bandwidth(device)
     torch.cuda.empty_cache()
     if not args.no_extra:
         lens3, q3 = cfg3_lens()

@@ -57,10 +57,11 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
 
 
-def _compile(src: Path, verbose: bool) -> Path:
-    obj = BUILD_DIR / (src.stem + ".o")
+def _compile(src: Path, verbose: bool, build_dir: Path, defines: list[str]) -> Path:
+    obj = build_dir / (src.stem + ".o")
     lang = ["-x", "hip"] if src.suffix == ".hip" else []
-    cmd = [hipcc(), *COMMON_FLAGS, *lang, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *COMMON_FLAGS, *[f"-D{d}" for d in defines], *lang, "-c", str(src), "-o",
+           str(obj)]
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
@@ -71,22 +72,34 @@ def _compile(src: Path, verbose: bool) -> Path:
     return obj
 
 
-def build(verbose: bool = False, jobs: int | None = None) -> Path:
-    """Compile every HIP source and link the shared library. Returns its path."""
-    BUILD_DIR.mkdir(exist_ok=True)
+def build(
+    verbose: bool = False,
+    jobs: int | None = None,
+    defines: list[str] | None = None,
+    out: Path | None = None,
+    build_dir: Path | None = None,
+) -> Path:
+    """Compile every HIP source and link the shared library. Returns its path.
+
+    ``defines`` (``NAME=VALUE`` strings) override the tuning macros of the sources; ``out`` and
+    ``build_dir`` redirect the library and objects (the defaults are the in-tree locations).
+    """
+    out = Path(out) if out is not None else LIB_PATH
+    build_dir = Path(build_dir) if build_dir is not None else BUILD_DIR
+    build_dir.mkdir(parents=True, exist_ok=True)
     srcs = sources()
     jobs = jobs or min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
     with ThreadPoolExecutor(max_workers=jobs) as pool:
-        objs = list(pool.map(lambda s: _compile(s, verbose), srcs))
-    tmp = LIB_PATH.with_suffix(".so.tmp")
+        objs = list(pool.map(lambda s: _compile(s, verbose, build_dir, defines or []), srcs))
+    tmp = out.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stdout}\n{proc.stderr}")
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":

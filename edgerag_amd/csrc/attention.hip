@@ -8,21 +8,24 @@
 // paged_attention_reference (edgerag/cache/fused.py:89-167).
 //
 // Execution model:
-//   1. edgerag_attn_plan (host) cuts every (request, kv head) into KV splits and query tiles and
-//      writes a flat work list, heaviest items first. Long contexts are split so that a 32-way
-//      decode batch still yields thousands of independent waves for the 256 CUs.
-//   2. attn_rows_kernel: one wavefront per work item. The wave walks its KV split in steps of
-//      64 lanes x 16 bytes (fully coalesced 1 KiB loads straight out of the 2 KiB block rows),
-//      keeps the fp32 online-softmax state (m, l, acc) of up to kQR query vectors in registers,
-//      and reduces scores with cross-lane butterflies -- no LDS, no gather copy. All n_rep query
-//      heads of a GQA group share each K/V load.
-//   3. attn_combine_kernel merges the fp32 split partials (m, l, acc) of requests that were
-//      split; unsplit requests are written directly by step 2.
-// Scores are kept in the log2 domain (q pre-multiplied by scale * log2(e)) so every exponential
-// is a single v_exp_f32.
+//   1. edgerag_attn_plan (host) cuts every (request, kv head) into KV splits and writes a flat
+//      work list: "row" items (decodes: c * n_rep <= kMaxRowVecs query vectors) first, then
+//      "tile" items (prefill slices in query tiles), each group heaviest first. Long contexts are
+//      split so that a 32-way decode batch still yields thousands of independent waves.
+//   2. attn_decode_kernel: one wavefront per row item. Lanes are grouped LPT per token (16 bytes
+//      each, so a group covers one head_dim row); each load instruction covers TPW consecutive
+//      tokens = a fully coalesced 1 KiB slice of a 2 KiB block row, and U such slices are in
+//      flight per lane. Every lane group keeps its own fp32 online-softmax state (m, l, acc), so
+//      the K/V loop needs no cross-group communication; groups merge once at the end. Block ids
+//      of the split are held one per lane and broadcast with v_readlane. Q.K uses v_dot2_f32_f16.
+//   3. attn_rows_kernel: the general version of (2) for shapes the fast path does not cover
+//      (block_size not a multiple of the tokens-per-load, or prefill tiles before the MFMA path).
+//   4. attn_combine_kernel merges the fp32 split partials (m, l, acc) of split requests, one
+//      wave per (token, query head); unsplit requests are written directly by (2)/(3).
+// Scores are kept in the log2 domain (scaled by scale * log2(e)) so each exponential is one
+// v_exp_f32.
 #include <algorithm>
 #include <cmath>
-#include <numeric>
 #include <vector>
 
 #include "common.h"
@@ -32,8 +35,8 @@ namespace {
 
 // ---- plan layout (int32 words) -----------------------------------------------------------------
 constexpr int32_t kPlanMagic = 0x47415245;  // "ERAG"
-constexpr int32_t kPlanVersion = 1;
-constexpr int kHeaderWords = 16;
+constexpr int32_t kPlanVersion = 3;
+constexpr int kHeaderWords = 24;
 constexpr int kItemWords = 8;
 constexpr int kReqWords = 4;
 
@@ -51,38 +54,328 @@ enum Header {
   H_BLOCK_SIZE,
   H_DTYPE,
   H_NUM_TOKENS_HINT,
+  H_N_ROW_ITEMS,     // items [0, n_row) are row items, [n_row, n_items) tile items
+  H_MAX_ROW_VECS,    // largest c * n_rep among row items
+  H_MAX_SPLIT_BLOCKS,
+  H_N_COMBINE,        // rows (query tokens of split requests) attn_combine_kernel merges
+  H_COMBINE_OFF,      // word offset of the combine list
 };
-enum Item { I_REQ = 0, I_HEAD, I_QBEGIN, I_QCOUNT, I_KVBEGIN, I_KVEND, I_SPLIT, I_KIND };
+enum Item { I_REQ = 0, I_HEAD, I_QBEGIN, I_QCOUNT, I_KVBEGIN, I_KVEND, I_SPLIT, I_PAD };
 enum Req { R_NSPLIT = 0, R_SPLITLEN, R_PARTOFF, R_PAD };
+// One combine-list entry per query token of a split request: everything the merge needs in one
+// 32-byte load.
+constexpr int kCombineWords = 8;
+enum Combine { C_TOK = 0, C_Q0, C_C, C_L, C_NSPLIT, C_SPLITLEN, C_PARTOFF, C_PAD };
 
-constexpr int kQR = 4;          // query vectors carried per pass of a wave
-constexpr int kQTile = 16;      // query rows per work item on the row path
-constexpr int kMinSplit = 256;  // tokens: below this a split's partial write is not worth it
-constexpr int kTargetItems = 8192;
+// Tuning constants; the EDGERAG_* macros let a build override them for sweeps.
+#ifndef EDGERAG_MIN_SPLIT
+#define EDGERAG_MIN_SPLIT 256
+#endif
+#ifndef EDGERAG_TARGET_ITEMS
+#define EDGERAG_TARGET_ITEMS 4096
+#endif
+#ifndef EDGERAG_DECODE_U
+#define EDGERAG_DECODE_U 2
+#endif
+constexpr int kMaxRowVecs = 8;  // query vectors a decode item may carry (c * n_rep)
+constexpr int kQTile = 16;      // query rows per prefill tile item
+constexpr int kMinSplit = EDGERAG_MIN_SPLIT;  // tokens; shorter splits are not worth a partial
+constexpr int kTargetItems = EDGERAG_TARGET_ITEMS;  // decode work items a batch is cut into
+constexpr int kDecodeU = EDGERAG_DECODE_U;  // token loads in flight per lane group
+constexpr int kMaxSplitBlocks = 64;  // one block id per lane in the decode kernel
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Cross-lane moves inside a 16-lane row via DPP (plain VALU instructions, no LDS crossbar).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Reduce over the LPT consecutive lanes of a token group. xor 1 / xor 2 are quad permutes; after
+// them every lane of a quad holds the quad's value, so a half-row mirror (lane i <-> 7 - i)
+// completes 8 lanes and a row mirror (i <-> 15 - i) completes 16.
+template <int LPT, bool MAX>
+__device__ __forceinline__ float group_reduce(float v) {
+  auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+  if constexpr (LPT >= 2) v = op(v, dpp<0xB1>(v));
+  if constexpr (LPT >= 4) v = op(v, dpp<0x4E>(v));
+  if constexpr (LPT >= 8) v = op(v, dpp<0x141>(v));
+  if constexpr (LPT >= 16) v = op(v, dpp<0x140>(v));
+  if constexpr (LPT >= 32) v = op(v, __shfl_xor(v, 16, kWave));
+  if constexpr (LPT >= 64) v = op(v, __shfl_xor(v, 32, kWave));
+  return v;
+}
 
 template <typename T, int D>
 struct RowCfg {
   static constexpr int VEC = 16 / sizeof(T);
-  static constexpr int LPT = D / VEC;  // lanes sharing one token
-  static constexpr int TPW = kWave / LPT;  // tokens per wave step
+  static constexpr int LPT = D / VEC;      // lanes sharing one token
+  static constexpr int TPW = kWave / LPT;  // tokens per load instruction
   static constexpr int LOG_LPT = ilog2(LPT);
   static_assert(D % VEC == 0 && LPT >= 1 && LPT <= kWave, "unsupported head_dim");
 };
 
-template <typename T, int D>
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+// q . k over this lane's VEC elements (q already in registers), widened to fp32.
+template <typename T, int VEC>
+struct QReg {
+  float f[VEC];  // fp32 / bf16 path: pre-scaled by scale*log2(e)
+  half2_t h[VEC / 2 > 0 ? VEC / 2 : 1];  // fp16 path: raw fp16 values
+
+  __device__ __forceinline__ void load(const T* p, float scale_log2) {
+    if constexpr (__is_same(T, f16)) {
+      const Vec16 raw = load16(p);
+#pragma unroll
+      for (int i = 0; i < VEC / 2; ++i) h[i] = *reinterpret_cast<const half2_t*>(&raw.w[i]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) f[e] = to_f32<T>(p[e]) * scale_log2;
+    }
+  }
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) f[e] = 0.f;
+#pragma unroll
+    for (int i = 0; i < (VEC / 2 > 0 ? VEC / 2 : 1); ++i) h[i] = half2_t{0, 0};
+  }
+  // Partial dot product; the fp16 path is scaled after the group reduction.
+  __device__ __forceinline__ float dot(const Vec16& k) const {
+    float s = 0.f;
+    if constexpr (__is_same(T, f16)) {
+#pragma unroll
+      for (int i = 0; i < VEC / 2; ++i)
+        s = __builtin_amdgcn_fdot2(h[i], *reinterpret_cast<const half2_t*>(&k.w[i]), s, false);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) s = fmaf(f[e], vec_elem<T>(k, e), s);
+    }
+    return s;
+  }
+  static constexpr bool kScaleAfter = __is_same(T, f16);
+};
+
+// ---- merging split partials -----------------------------------------------------------------------
+// One wave merges the fp32 partials (m, l, acc[D]) of query row t / head hq: lanes load the split
+// maxima in parallel, then each lane owns D / 64 (at least one) output elements.
+template <typename T>
+__device__ __forceinline__ void combine_pair(int t, int hq, int q0, int c, int L, int nsplit,
+                                             int split_len, int part_off, int n_q_heads,
+                                             int head_dim, const float2* __restrict__ part_ml,
+                                             const float* __restrict__ part_acc, T* __restrict__ out,
+                                             int64_t o_st, int64_t o_sh, int lane) {
+  const int lim = L - c + (t - q0);
+  const int n_valid = lim < 0 ? 0 : min(nsplit, lim / split_len + 1);
+  const int64_t base = int64_t(part_off) + (int64_t(t - q0) * n_q_heads + hq) * nsplit;
+  float mmax = -INFINITY;
+  for (int s = lane; s < n_valid; s += kWave) mmax = fmaxf(mmax, part_ml[base + s].x);
+#pragma unroll
+  for (int b = 0; b < 6; ++b) mmax = fmaxf(mmax, __shfl_xor(mmax, 1 << b, kWave));
+  float lsum = 0.f;
+  float a[4] = {0.f, 0.f, 0.f, 0.f};  // head_dim <= 256
+  if (mmax != -INFINITY) {
+    for (int s0 = 0; s0 < n_valid; s0 += kWave) {
+      float w = 0.f;
+      if (s0 + lane < n_valid) {
+        const float2 ml = part_ml[base + s0 + lane];
+        w = exp2_fast(ml.x - mmax);
+        lsum = fmaf(w, ml.y, lsum);
+      }
+      const int cnt = min(kWave, n_valid - s0);
+      // Issue 8 splits' loads before consuming any, so their latencies overlap.
+      for (int sb = 0; sb < cnt; sb += 8) {
+        float vals[8][4];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const float* pa = part_acc + (base + s0 + sb + k) * head_dim;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int x = lane + i * kWave;
+            vals[k][i] = (sb + k < cnt && x < head_dim) ? pa[x] : 0.f;
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const float ws = __shfl(w, sb + k, kWave);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) a[i] = fmaf(ws, vals[k][i], a[i]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int b = 0; b < 6; ++b) lsum += __shfl_xor(lsum, 1 << b, kWave);
+  const float inv = 1.f / fmaxf(lsum, 1.17549435e-38f);
+  T* op = out + int64_t(t) * o_st + int64_t(hq) * o_sh;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int x = lane + i * kWave;
+    if (x < head_dim) op[x] = from_f32<T>(a[i] * inv);
+  }
+}
+
+// ---- fast decode kernel --------------------------------------------------------------------------
+// Requires block_size % TPW == 0 and at most kMaxSplitBlocks blocks per split (checked by the
+// launcher from the plan header).
+template <typename T, int D, int QR, int U>
+__global__ __launch_bounds__(kWave) void attn_decode_kernel(
+    const T* __restrict__ q, int64_t q_st, int64_t q_sh, const T* __restrict__ kpool,
+    const T* __restrict__ vpool, const int32_t* __restrict__ block_tables, int64_t bt_stride,
+    const int32_t* __restrict__ qsl, const int32_t* __restrict__ ctx,
+    const int32_t* __restrict__ plan, int32_t item_base, int32_t n_q_heads, int32_t n_kv_heads,
+    int32_t num_blocks, int32_t block_size, float scale_log2, T* __restrict__ out, int64_t o_st,
+    int64_t o_sh, float2* __restrict__ part_ml, float* __restrict__ part_acc) {
+  using C = RowCfg<T, D>;
+  constexpr int VEC = C::VEC, LPT = C::LPT, TPW = C::TPW, LOG_LPT = C::LOG_LPT;
+  constexpr int STEP = TPW * U;
+
+  const int32_t* it = plan + plan[H_ITEM_OFF] + int64_t(item_base + blockIdx.x) * kItemWords;
+  const int r = it[I_REQ], h = it[I_HEAD], qb = it[I_QBEGIN], qc = it[I_QCOUNT];
+  const int kb = it[I_KVBEGIN], ke = it[I_KVEND], split = it[I_SPLIT];
+  const int32_t* rq = plan + plan[H_REQ_OFF] + r * kReqWords;
+  const int nsplit = rq[R_NSPLIT], part_off = rq[R_PARTOFF];
+  const int q0 = qsl[r], c = qsl[r + 1] - q0, L = ctx[r];
+  const int n_rep = n_q_heads / n_kv_heads;
+
+  const int lane = threadIdx.x;
+  const int sub = lane & (LPT - 1);
+  const int tslot = lane >> LOG_LPT;
+  const int64_t head_base = int64_t(h) * num_blocks;
+
+  // Block ids of this split, one per lane; broadcast per load with v_readlane.
+  const int blk0 = kb / block_size;
+  const int nblk = (ke - kb + block_size - 1) / block_size;
+  int my_blk = -1;
+  if (lane < nblk) {
+    const int32_t b = block_tables[int64_t(r) * bt_stride + blk0 + lane];
+    my_blk = (b >= 0 && b < num_blocks) ? b : -1;
+  }
+
+  const int nvec = qc * n_rep;
+  for (int v0 = 0; v0 < nvec; v0 += QR) {
+    QReg<T, VEC> qr[QR];
+    float m[QR], l[QR], acc[QR][VEC];
+    int lim[QR];
+#pragma unroll
+    for (int j = 0; j < QR; ++j) {
+      const int v = v0 + j;
+      const int t = qb + v / n_rep;
+      const int hq = h * n_rep + (v % n_rep);
+      lim[j] = v < nvec ? L - c + (t - q0) : -1;  // -1: inactive slot, sees nothing
+      if (v < nvec)
+        qr[j].load(q + int64_t(t) * q_st + int64_t(hq) * q_sh + sub * VEC, scale_log2);
+      else
+        qr[j].zero();
+      m[j] = -INFINITY;
+      l[j] = 0.f;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc[j][e] = 0.f;
+    }
+
+    for (int g0 = kb; g0 < ke; g0 += STEP) {
+      Vec16 kr[U], vr[U];
+      int tok[U];
+      bool valid[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int first = g0 + u * TPW;  // wave-uniform
+        tok[u] = first + tslot;
+        const bool live = first < ke;
+        const int blk = __builtin_amdgcn_readlane(my_blk, live ? (first - kb) / block_size : 0);
+        valid[u] = live && tok[u] < ke && blk >= 0;
+        if (valid[u]) {
+          const int64_t off =
+              ((head_base + blk) * block_size + (tok[u] % block_size)) * D + sub * VEC;
+          kr[u] = load16(kpool + off);
+          vr[u] = load16(vpool + off);
+        } else {
+          kr[u] = Vec16{};
+          vr[u] = Vec16{};
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < QR; ++j) {
+        float s[U];
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          float d = group_reduce<LPT, false>(qr[j].dot(kr[u]));
+          if constexpr (QReg<T, VEC>::kScaleAfter) d *= scale_log2;
+          s[u] = (valid[u] && tok[u] <= lim[j]) ? d : -INFINITY;
+          mloc = fmaxf(mloc, s[u]);
+        }
+        const float mnew = fmaxf(m[j], mloc);
+        if (__any(mnew > m[j])) {
+          const float alpha = mnew == -INFINITY ? 1.f : exp2_fast(m[j] - mnew);
+          l[j] *= alpha;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) acc[j][e] *= alpha;
+          m[j] = mnew;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const float p = s[u] == -INFINITY ? 0.f : exp2_fast(s[u] - m[j]);
+          l[j] += p;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) acc[j][e] = fmaf(p, vec_elem<T>(vr[u], e), acc[j][e]);
+        }
+      }
+    }
+
+    // Merge the TPW lane groups of each query vector, then write.
+#pragma unroll
+    for (int j = 0; j < QR; ++j) {
+      const int v = v0 + j;
+      if (v >= nvec) break;
+      float mm = m[j];
+#pragma unroll
+      for (int b = LOG_LPT; b < 6; ++b) mm = fmaxf(mm, __shfl_xor(mm, 1 << b, kWave));
+      const float w = m[j] == -INFINITY ? 0.f : exp2_fast(m[j] - mm);
+      float lsum = w * l[j];
+#pragma unroll
+      for (int b = LOG_LPT; b < 6; ++b) lsum += __shfl_xor(lsum, 1 << b, kWave);
+      float a[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        a[e] = w * acc[j][e];
+#pragma unroll
+        for (int b = LOG_LPT; b < 6; ++b) a[e] += __shfl_xor(a[e], 1 << b, kWave);
+      }
+      if (tslot != 0) continue;
+      const int t = qb + v / n_rep;
+      const int hq = h * n_rep + (v % n_rep);
+      if (nsplit == 1) {
+        const float inv = 1.f / fmaxf(lsum, 1.17549435e-38f);
+        T* op = out + int64_t(t) * o_st + int64_t(hq) * o_sh + sub * VEC;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) op[e] = from_f32<T>(a[e] * inv);
+      } else {
+        const int64_t idx =
+            int64_t(part_off) + (int64_t(t - q0) * n_q_heads + hq) * nsplit + split;
+        if (sub == 0) part_ml[idx] = make_float2(mm, lsum);
+        float* pa = part_acc + idx * D + sub * VEC;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) pa[e] = a[e];
+      }
+    }
+  }
+}
+
+// ---- general row kernel ----------------------------------------------------------------------------
+// Any block size and split length; per-lane block lookups; QR query vectors per pass.
+template <typename T, int D, int QR>
 __global__ __launch_bounds__(kWave) void attn_rows_kernel(
     const T* __restrict__ q, int64_t q_st, int64_t q_sh, const T* __restrict__ kpool,
     const T* __restrict__ vpool, const int32_t* __restrict__ block_tables, int64_t bt_stride,
     const int32_t* __restrict__ qsl, const int32_t* __restrict__ ctx,
-    const int32_t* __restrict__ plan, int32_t n_q_heads, int32_t n_kv_heads, int32_t num_blocks,
-    int32_t block_size, float scale_log2, T* __restrict__ out, int64_t o_st, int64_t o_sh,
-    float2* __restrict__ part_ml, float* __restrict__ part_acc) {
+    const int32_t* __restrict__ plan, int32_t item_base, int32_t n_q_heads, int32_t n_kv_heads,
+    int32_t num_blocks, int32_t block_size, float scale_log2, T* __restrict__ out, int64_t o_st,
+    int64_t o_sh, float2* __restrict__ part_ml, float* __restrict__ part_acc) {
   using C = RowCfg<T, D>;
   constexpr int VEC = C::VEC, LPT = C::LPT, TPW = C::TPW, LOG_LPT = C::LOG_LPT;
 
-  const int32_t* it = plan + plan[H_ITEM_OFF] + int64_t(blockIdx.x) * kItemWords;
+  const int32_t* it = plan + plan[H_ITEM_OFF] + int64_t(item_base + blockIdx.x) * kItemWords;
   const int r = it[I_REQ], h = it[I_HEAD], qb = it[I_QBEGIN], qc = it[I_QCOUNT];
   const int kb = it[I_KVBEGIN], ke = it[I_KVEND], split = it[I_SPLIT];
   const int32_t* rq = plan + plan[H_REQ_OFF] + r * kReqWords;
@@ -97,25 +390,20 @@ __global__ __launch_bounds__(kWave) void attn_rows_kernel(
   const int64_t head_base = int64_t(h) * num_blocks;
 
   const int nvec = qc * n_rep;
-  for (int v0 = 0; v0 < nvec; v0 += kQR) {
-    float qv[kQR][VEC];
-    float m[kQR], l[kQR], acc[kQR][VEC];
-    int lim[kQR];
+  for (int v0 = 0; v0 < nvec; v0 += QR) {
+    QReg<T, VEC> qr[QR];
+    float m[QR], l[QR], acc[QR][VEC];
+    int lim[QR];
 #pragma unroll
-    for (int j = 0; j < kQR; ++j) {
+    for (int j = 0; j < QR; ++j) {
       const int v = v0 + j;
-      const int row = v / n_rep;
+      const int t = qb + v / n_rep;
       const int hq = h * n_rep + (v % n_rep);
-      const int t = qb + row;
-      lim[j] = v < nvec ? L - c + (t - q0) : -1;  // -1: inactive slot, sees nothing
-      if (v < nvec) {
-        const T* qp = q + int64_t(t) * q_st + int64_t(hq) * q_sh + sub * VEC;
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) qv[j][e] = to_f32<T>(qp[e]) * scale_log2;
-      } else {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) qv[j][e] = 0.f;
-      }
+      lim[j] = v < nvec ? L - c + (t - q0) : -1;
+      if (v < nvec)
+        qr[j].load(q + int64_t(t) * q_st + int64_t(hq) * q_sh + sub * VEC, scale_log2);
+      else
+        qr[j].zero();
       m[j] = -INFINITY;
       l[j] = 0.f;
 #pragma unroll
@@ -135,48 +423,48 @@ __global__ __launch_bounds__(kWave) void attn_rows_kernel(
           vr = load16(vpool + off);
         }
       }
-      float kf[VEC], vf[VEC];
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        kf[e] = vec_elem<T>(kr, e);
-        vf[e] = vec_elem<T>(vr, e);
-      }
-#pragma unroll
-      for (int j = 0; j < kQR; ++j) {
-        float s = 0.f;
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) s = fmaf(qv[j][e], kf[e], s);
-        s = xor_sum<0, LOG_LPT>(s);
+      for (int j = 0; j < QR; ++j) {
+        float s = group_reduce<LPT, false>(qr[j].dot(kr));
+        if constexpr (QReg<T, VEC>::kScaleAfter) s *= scale_log2;
         const bool vis = valid && tok <= lim[j];
         s = vis ? s : -INFINITY;
-        const float gmax = xor_max<LOG_LPT, 6>(s);
-        if (gmax == -INFINITY) continue;  // wave-uniform: nothing visible in this step
-        if (gmax > m[j]) {
-          const float alpha = exp2_fast(m[j] - gmax);  // m == -inf gives exactly 0
+        const float mnew = fmaxf(m[j], s);
+        if (__any(mnew > m[j])) {
+          const float alpha = mnew == -INFINITY ? 1.f : exp2_fast(m[j] - mnew);
           l[j] *= alpha;
 #pragma unroll
           for (int e = 0; e < VEC; ++e) acc[j][e] *= alpha;
-          m[j] = gmax;
+          m[j] = mnew;
         }
         const float p = vis ? exp2_fast(s - m[j]) : 0.f;
         l[j] += p;
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) acc[j][e] = fmaf(p, vf[e], acc[j][e]);
+        for (int e = 0; e < VEC; ++e) acc[j][e] = fmaf(p, vec_elem<T>(vr, e), acc[j][e]);
       }
     }
 
 #pragma unroll
-    for (int j = 0; j < kQR; ++j) {
+    for (int j = 0; j < QR; ++j) {
       const int v = v0 + j;
       if (v >= nvec) break;
-      const float lsum = xor_sum<LOG_LPT, 6>(l[j]);
+      float mm = m[j];
+#pragma unroll
+      for (int b = LOG_LPT; b < 6; ++b) mm = fmaxf(mm, __shfl_xor(mm, 1 << b, kWave));
+      const float w = m[j] == -INFINITY ? 0.f : exp2_fast(m[j] - mm);
+      float lsum = w * l[j];
+#pragma unroll
+      for (int b = LOG_LPT; b < 6; ++b) lsum += __shfl_xor(lsum, 1 << b, kWave);
       float a[VEC];
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) a[e] = xor_sum<LOG_LPT, 6>(acc[j][e]);
+      for (int e = 0; e < VEC; ++e) {
+        a[e] = w * acc[j][e];
+#pragma unroll
+        for (int b = LOG_LPT; b < 6; ++b) a[e] += __shfl_xor(a[e], 1 << b, kWave);
+      }
       if (tslot != 0) continue;
-      const int row = v / n_rep;
+      const int t = qb + v / n_rep;
       const int hq = h * n_rep + (v % n_rep);
-      const int t = qb + row;
       if (nsplit == 1) {
         const float inv = 1.f / fmaxf(lsum, 1.17549435e-38f);
         T* op = out + int64_t(t) * o_st + int64_t(hq) * o_sh + sub * VEC;
@@ -185,7 +473,7 @@ __global__ __launch_bounds__(kWave) void attn_rows_kernel(
       } else {
         const int64_t idx =
             int64_t(part_off) + (int64_t(t - q0) * n_q_heads + hq) * nsplit + split;
-        if (sub == 0) part_ml[idx] = make_float2(m[j], lsum);
+        if (sub == 0) part_ml[idx] = make_float2(mm, lsum);
         float* pa = part_acc + idx * D + sub * VEC;
 #pragma unroll
         for (int e = 0; e < VEC; ++e) pa[e] = a[e];
@@ -194,48 +482,22 @@ __global__ __launch_bounds__(kWave) void attn_rows_kernel(
   }
 }
 
-// One block per query token; threadIdx.y walks query heads, threadIdx.x the head dimension.
+// ---- combine -----------------------------------------------------------------------------------
+// Merges split partials: one wave per (combine-list row, query head). The list entry carries the
+// request's geometry, so a wave's dependent loads are entry -> (m, l) -> acc.
 template <typename T>
 __global__ __launch_bounds__(256) void attn_combine_kernel(
-    const int32_t* __restrict__ plan, const int32_t* __restrict__ qsl,
-    const int32_t* __restrict__ ctx, int32_t n_reqs, int32_t n_q_heads, int32_t head_dim,
+    const int32_t* __restrict__ plan, int32_t combine_off, int32_t n_q_heads, int32_t head_dim,
     const float2* __restrict__ part_ml, const float* __restrict__ part_acc, T* __restrict__ out,
     int64_t o_st, int64_t o_sh) {
-  const int t = blockIdx.x;
-  // Request owning token t: the last r with qsl[r] <= t (requests with c == 0 are skipped).
-  int lo = 0, hi = n_reqs - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (qsl[mid] <= t) lo = mid; else hi = mid - 1;
-  }
-  const int r = lo;
-  const int q0 = qsl[r], c = qsl[r + 1] - q0;
-  if (t < q0 || t >= q0 + c) return;
-  const int32_t* rq = plan + plan[H_REQ_OFF] + r * kReqWords;
-  const int nsplit = rq[R_NSPLIT], split_len = rq[R_SPLITLEN], part_off = rq[R_PARTOFF];
-  if (nsplit <= 1) return;
-  const int L = ctx[r];
-  const int lim = L - c + (t - q0);
-  const int n_valid = lim < 0 ? 0 : min(nsplit, lim / split_len + 1);
-  for (int hq = blockIdx.y * blockDim.y + threadIdx.y; hq < n_q_heads;
-       hq += gridDim.y * blockDim.y) {
-    const int64_t base = int64_t(part_off) + (int64_t(t - q0) * n_q_heads + hq) * nsplit;
-    float mmax = -INFINITY;
-    for (int s = 0; s < n_valid; ++s) mmax = fmaxf(mmax, part_ml[base + s].x);
-    for (int x = threadIdx.x; x < head_dim; x += blockDim.x) {
-      float lsum = 0.f, a = 0.f;
-      if (mmax != -INFINITY) {
-        for (int s = 0; s < n_valid; ++s) {
-          const float2 ml = part_ml[base + s];
-          const float w = exp2_fast(ml.x - mmax);
-          lsum = fmaf(w, ml.y, lsum);
-          a = fmaf(w, part_acc[(base + s) * head_dim + x], a);
-        }
-      }
-      out[int64_t(t) * o_st + int64_t(hq) * o_sh + x] =
-          from_f32<T>(a / fmaxf(lsum, 1.17549435e-38f));
-    }
-  }
+  const int hq = blockIdx.y * (blockDim.x / kWave) + threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  if (hq >= n_q_heads) return;
+  const int4* e4 = reinterpret_cast<const int4*>(plan + combine_off +
+                                                 int64_t(blockIdx.x) * kCombineWords);
+  const int4 a = e4[0], b = e4[1];  // {tok, q0, c, L}, {nsplit, split_len, part_off, pad}
+  combine_pair<T>(a.x, hq, a.y, a.z, a.w, b.x, b.y, b.z, n_q_heads, head_dim, part_ml, part_acc,
+                  out, o_st, o_sh, lane);
 }
 
 int elem_size(int32_t dtype) {
@@ -253,35 +515,113 @@ bool head_dim_supported(int32_t d) {
 
 int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 
+int pow2_at_least(int v) {
+  int p = 1;
+  while (p < v) p <<= 1;
+  return p;
+}
+
 struct PlanItem {
   int32_t w[kItemWords];
   int64_t cost;
 };
 
-template <typename T>
-int launch_rows(int32_t D, dim3 grid, hipStream_t s, const void* q, int64_t q_st, int64_t q_sh,
-                const void* kp, const void* vp, const int32_t* bt, int64_t bt_stride,
-                const int32_t* qsl, const int32_t* ctx, const int32_t* plan, int32_t hq,
-                int32_t hkv, int32_t nb, int32_t bs, float scale_log2, void* out, int64_t o_st,
-                int64_t o_sh, float2* ml, float* pacc) {
-#define EDGERAG_ROWS(DIM)                                                                         \
-  case DIM:                                                                                       \
-    hipLaunchKernelGGL((attn_rows_kernel<T, DIM>), grid, dim3(kWave), 0, s,                      \
-                       static_cast<const T*>(q), q_st, q_sh, static_cast<const T*>(kp),           \
-                       static_cast<const T*>(vp), bt, bt_stride, qsl, ctx, plan, hq, hkv, nb, bs, \
-                       scale_log2, static_cast<T*>(out), o_st, o_sh, ml, pacc);                   \
-    break;
-  switch (D) {
-    EDGERAG_ROWS(8)
-    EDGERAG_ROWS(16)
-    EDGERAG_ROWS(32)
-    EDGERAG_ROWS(64)
-    EDGERAG_ROWS(128)
-    EDGERAG_ROWS(256)
-    default: return fail(EDGERAG_EUNSUPPORTED, "edgerag_paged_attention: head_dim %d", D);
+// Workspace: [(m, l) pairs | acc rows] of the split partials.
+struct WorkspaceLayout {
+  int64_t acc_off, total;
+};
+
+WorkspaceLayout workspace_layout(int64_t n_partials, int64_t head_dim) {
+  WorkspaceLayout w{};
+  w.acc_off = round_up(n_partials * int64_t(sizeof(float2)), 256);
+  w.total = w.acc_off + round_up(n_partials * head_dim * int64_t(sizeof(float)), 256);
+  return w;
+}
+
+struct Launch {
+  hipStream_t s;
+  const void* q;
+  int64_t q_st, q_sh;
+  const void *kp, *vp;
+  const int32_t* bt;
+  int64_t bt_stride;
+  const int32_t *qsl, *ctx, *plan;
+  int32_t hq, hkv, nb, bs;
+  float scale_log2;
+  void* out;
+  int64_t o_st, o_sh;
+  float2* ml;
+  float* pacc;
+};
+
+template <typename T, int D, int QR, int U>
+void launch_decode(const Launch& a, int base, int count) {
+  hipLaunchKernelGGL((attn_decode_kernel<T, D, QR, U>), dim3(count), dim3(kWave), 0, a.s,
+                     static_cast<const T*>(a.q), a.q_st, a.q_sh, static_cast<const T*>(a.kp),
+                     static_cast<const T*>(a.vp), a.bt, a.bt_stride, a.qsl, a.ctx, a.plan, base,
+                     a.hq, a.hkv, a.nb, a.bs, a.scale_log2, static_cast<T*>(a.out), a.o_st, a.o_sh,
+                     a.ml, a.pacc);
+}
+
+template <typename T, int D, int QR>
+void launch_rows(const Launch& a, int base, int count) {
+  hipLaunchKernelGGL((attn_rows_kernel<T, D, QR>), dim3(count), dim3(kWave), 0, a.s,
+                     static_cast<const T*>(a.q), a.q_st, a.q_sh, static_cast<const T*>(a.kp),
+                     static_cast<const T*>(a.vp), a.bt, a.bt_stride, a.qsl, a.ctx, a.plan, base,
+                     a.hq, a.hkv, a.nb, a.bs, a.scale_log2, static_cast<T*>(a.out), a.o_st, a.o_sh,
+                     a.ml, a.pacc);
+}
+
+template <typename T, int D>
+void dispatch_decode_qr(const Launch& a, int qr, int base, int count) {
+  constexpr int U = D >= 256 ? 2 : kDecodeU;
+  switch (qr) {
+    case 1: launch_decode<T, D, 1, U>(a, base, count); break;
+    case 2: launch_decode<T, D, 2, U>(a, base, count); break;
+    case 4: launch_decode<T, D, 4, U>(a, base, count); break;
+    default: launch_decode<T, D, 8, 2>(a, base, count); break;
   }
-#undef EDGERAG_ROWS
-  return check_launch("edgerag_paged_attention(rows)");
+}
+
+template <typename T, int D>
+void dispatch_rows_qr(const Launch& a, int qr, int base, int count) {
+  switch (qr) {
+    case 1: launch_rows<T, D, 1>(a, base, count); break;
+    case 2: launch_rows<T, D, 2>(a, base, count); break;
+    case 4: launch_rows<T, D, 4>(a, base, count); break;
+    default: launch_rows<T, D, 8>(a, base, count); break;
+  }
+}
+
+// Row items: fast decode kernel when every split's load groups stay inside one block, the
+// general kernel otherwise. Tile items: general kernel with 8 query vectors per pass.
+template <typename T, int D>
+int run_items(const Launch& a, const int32_t* ph) {
+  using C = RowCfg<T, D>;
+  const int n_items = ph[H_N_ITEMS], n_row = ph[H_N_ROW_ITEMS];
+  const int qr = std::min(8, pow2_at_least(std::max(1, ph[H_MAX_ROW_VECS])));
+  const bool fast = a.bs % C::TPW == 0 && ph[H_MAX_SPLIT_BLOCKS] <= kMaxSplitBlocks;
+  if (n_row > 0) {
+    if (fast)
+      dispatch_decode_qr<T, D>(a, qr, 0, n_row);
+    else
+      dispatch_rows_qr<T, D>(a, qr, 0, n_row);
+  }
+  if (n_items > n_row) dispatch_rows_qr<T, D>(a, 8, n_row, n_items - n_row);
+  return check_launch("edgerag_paged_attention");
+}
+
+template <typename T>
+int run_dtype(const Launch& a, const int32_t* ph, int32_t D) {
+  switch (D) {
+    case 8: return run_items<T, 8>(a, ph);
+    case 16: return run_items<T, 16>(a, ph);
+    case 32: return run_items<T, 32>(a, ph);
+    case 64: return run_items<T, 64>(a, ph);
+    case 128: return run_items<T, 128>(a, ph);
+    case 256: return run_items<T, 256>(a, ph);
+  }
+  return fail(EDGERAG_EUNSUPPORTED, "edgerag_paged_attention: head_dim %d", D);
 }
 
 }  // namespace
@@ -313,8 +653,7 @@ extern "C" int edgerag_attn_plan(const int32_t* query_start_loc, const int32_t* 
                 max_blocks_per_seq);
 
   const int n_rep = n_q_heads / n_kv_heads;
-  // Total KV token-heads the batch reads, to size the splits.
-  int64_t work = 0;
+  int64_t work = 0;  // KV token-heads the batch reads, to size the splits
   for (int r = 0; r < num_reqs; ++r) {
     const int64_t c = int64_t(query_start_loc[r + 1]) - query_start_loc[r];
     const int64_t L = context_lens[r];
@@ -331,26 +670,40 @@ extern "C" int edgerag_attn_plan(const int32_t* query_start_loc, const int32_t* 
     if (c > 0) work += L * n_kv_heads;
   }
   int64_t split_len = std::max<int64_t>(kMinSplit, (work + kTargetItems - 1) / kTargetItems);
-  split_len = round_up(split_len, std::max(block_size, 16));
+  split_len = round_up(split_len, block_size);
+  split_len = std::min<int64_t>(split_len, int64_t(kMaxSplitBlocks) * block_size);
+  const int split_blocks = int((split_len + block_size - 1) / block_size);
 
-  std::vector<PlanItem> items;
+  std::vector<PlanItem> rows, tiles;
   std::vector<int32_t> reqs(size_t(num_reqs) * kReqWords, 0);
+  std::vector<int32_t> combine;
   int64_t n_partials = 0;
+  int max_row_vecs = 0;
   for (int r = 0; r < num_reqs; ++r) {
     const int q0 = query_start_loc[r];
     const int c = query_start_loc[r + 1] - q0;
     const int L = context_lens[r];
     int32_t* rq = reqs.data() + size_t(r) * kReqWords;
     const int nsplit = c == 0 ? 0 : int((L + split_len - 1) / split_len);
+    const bool row = c * n_rep <= kMaxRowVecs;
     rq[R_NSPLIT] = nsplit;
     rq[R_SPLITLEN] = int32_t(split_len);
     rq[R_PARTOFF] = int32_t(n_partials);
     if (c == 0) continue;
-    if (nsplit > 1) n_partials += int64_t(c) * n_q_heads * nsplit;
+    if (nsplit > 1) {
+      for (int t = q0; t < q0 + c; ++t) {
+        const int32_t e[kCombineWords] = {t, q0, c, L, nsplit, int32_t(split_len),
+                                          int32_t(n_partials), 0};
+        combine.insert(combine.end(), e, e + kCombineWords);
+      }
+      n_partials += int64_t(c) * n_q_heads * nsplit;
+    }
     if (n_partials > INT32_MAX)
       return fail(EDGERAG_EUNSUPPORTED, "edgerag_attn_plan: batch needs > 2^31 split partials");
-    for (int tile = 0; tile < c; tile += kQTile) {
-      const int qc = std::min(kQTile, c - tile);
+    const int tile_rows = row ? c : kQTile;
+    if (row) max_row_vecs = std::max(max_row_vecs, c * n_rep);
+    for (int tile = 0; tile < c; tile += tile_rows) {
+      const int qc = std::min(tile_rows, c - tile);
       const int last_visible = L - c + tile + qc - 1;  // causal limit of the tile's last row
       for (int s = 0; s < nsplit; ++s) {
         const int kb = int(s * split_len);
@@ -366,23 +719,24 @@ extern "C" int edgerag_attn_plan(const int32_t* query_start_loc, const int32_t* 
           p.w[I_KVBEGIN] = kb;
           p.w[I_KVEND] = ke_eff;
           p.w[I_SPLIT] = s;
-          p.w[I_KIND] = 0;
-          p.cost = int64_t(ke_eff - kb) * ((qc * n_rep + kQR - 1) / kQR);
-          items.push_back(p);
+          p.cost = int64_t(ke_eff - kb) * (row ? 1 : qc * n_rep);
+          (row ? rows : tiles).push_back(p);
         }
       }
     }
   }
   // Heaviest first: the dispatcher hands blocks out in index order, so this is LPT scheduling.
-  std::stable_sort(items.begin(), items.end(),
-                   [](const PlanItem& a, const PlanItem& b) { return a.cost > b.cost; });
+  auto heavier = [](const PlanItem& a, const PlanItem& b) { return a.cost > b.cost; };
+  std::stable_sort(rows.begin(), rows.end(), heavier);
+  std::stable_sort(tiles.begin(), tiles.end(), heavier);
 
+  const int64_t n_items = int64_t(rows.size() + tiles.size());
   const int64_t item_off = kHeaderWords;
-  const int64_t req_off = item_off + int64_t(items.size()) * kItemWords;
-  const int64_t words = req_off + int64_t(num_reqs) * kReqWords;
+  const int64_t req_off = item_off + n_items * kItemWords;
+  const int64_t combine_off = req_off + int64_t(num_reqs) * kReqWords;  // 16-byte aligned
+  const int64_t words = combine_off + int64_t(combine.size());
   *plan_words = words;
-  *workspace_bytes = round_up(n_partials * int64_t(sizeof(float2)), 256) +
-                     round_up(n_partials * head_dim * int64_t(sizeof(float)), 256);
+  *workspace_bytes = workspace_layout(n_partials, head_dim).total;
   if (plan == nullptr) return EDGERAG_OK;
   if (plan_capacity_words < words)
     return fail(EDGERAG_EWORKSPACE, "edgerag_attn_plan: plan needs %lld words, capacity %lld",
@@ -391,7 +745,7 @@ extern "C" int edgerag_attn_plan(const int32_t* query_start_loc, const int32_t* 
   std::fill(plan, plan + kHeaderWords, 0);
   plan[H_MAGIC] = kPlanMagic;
   plan[H_VERSION] = kPlanVersion;
-  plan[H_N_ITEMS] = int32_t(items.size());
+  plan[H_N_ITEMS] = int32_t(n_items);
   plan[H_N_REQS] = num_reqs;
   plan[H_ITEM_OFF] = int32_t(item_off);
   plan[H_REQ_OFF] = int32_t(req_off);
@@ -402,8 +756,18 @@ extern "C" int edgerag_attn_plan(const int32_t* query_start_loc, const int32_t* 
   plan[H_BLOCK_SIZE] = block_size;
   plan[H_DTYPE] = dtype;
   plan[H_NUM_TOKENS_HINT] = num_reqs > 0 ? query_start_loc[num_reqs] : 0;
-  for (size_t i = 0; i < items.size(); ++i)
-    std::copy(items[i].w, items[i].w + kItemWords, plan + item_off + int64_t(i) * kItemWords);
+  plan[H_N_ROW_ITEMS] = int32_t(rows.size());
+  plan[H_MAX_ROW_VECS] = max_row_vecs;
+  plan[H_MAX_SPLIT_BLOCKS] = split_blocks;
+  plan[H_N_COMBINE] = int32_t(combine.size() / kCombineWords);
+  plan[H_COMBINE_OFF] = int32_t(combine_off);
+  std::copy(combine.begin(), combine.end(), plan + combine_off);
+  int32_t* dst = plan + item_off;
+  for (const auto* group : {&rows, &tiles})
+    for (const PlanItem& p : *group) {
+      std::copy(p.w, p.w + kItemWords, dst);
+      dst += kItemWords;
+    }
   std::copy(reqs.begin(), reqs.end(), plan + req_off);
   return EDGERAG_OK;
 }
@@ -430,11 +794,10 @@ extern "C" int edgerag_paged_attention(
   if (num_blocks <= 0) return fail(EDGERAG_EINVAL, "edgerag_paged_attention: num_blocks <= 0");
   const int n_items = plan_host[H_N_ITEMS];
   const int64_t n_partials = plan_host[H_N_PARTIALS];
-  const int64_t ml_bytes = round_up(n_partials * int64_t(sizeof(float2)), 256);
-  const int64_t need = ml_bytes + round_up(n_partials * head_dim * int64_t(sizeof(float)), 256);
-  if (workspace_bytes < need || (need > 0 && workspace == nullptr))
+  const WorkspaceLayout ws = workspace_layout(n_partials, head_dim);
+  if (workspace_bytes < ws.total || (ws.total > 0 && workspace == nullptr))
     return fail(EDGERAG_EWORKSPACE, "edgerag_paged_attention: workspace %lld bytes, need %lld",
-                (long long)workspace_bytes, (long long)need);
+                (long long)workspace_bytes, (long long)ws.total);
   if (n_items == 0) return EDGERAG_OK;
   if (q == nullptr || key_pool == nullptr || value_pool == nullptr || out == nullptr ||
       block_tables == nullptr || query_start_loc == nullptr || context_lens == nullptr)
@@ -444,41 +807,45 @@ extern "C" int edgerag_paged_attention(
       (q_stride_tok * es) % 16 != 0 || (q_stride_head * es) % 16 != 0)
     return fail(EDGERAG_EINVAL, "edgerag_paged_attention: q and pools must be 16-byte aligned");
 
-  auto s = static_cast<hipStream_t>(stream);
-  float2* ml = static_cast<float2*>(workspace);
-  float* pacc = reinterpret_cast<float*>(static_cast<char*>(workspace) + ml_bytes);
-  const float scale_log2 = scale * 1.4426950408889634f;
+  Launch a{};
+  a.s = static_cast<hipStream_t>(stream);
+  a.q = q;
+  a.q_st = q_stride_tok;
+  a.q_sh = q_stride_head;
+  a.kp = key_pool;
+  a.vp = value_pool;
+  a.bt = block_tables;
+  a.bt_stride = block_tables_stride;
+  a.qsl = query_start_loc;
+  a.ctx = context_lens;
+  a.plan = plan_dev;
+  a.hq = n_q_heads;
+  a.hkv = n_kv_heads;
+  a.nb = num_blocks;
+  a.bs = block_size;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.out = out;
+  a.o_st = out_stride_tok;
+  a.o_sh = out_stride_head;
+  char* wsp = static_cast<char*>(workspace);
+  a.ml = reinterpret_cast<float2*>(wsp);
+  a.pacc = reinterpret_cast<float*>(wsp + ws.acc_off);
   int rc = EDGERAG_OK;
-  const dim3 grid(n_items);
   switch (dtype) {
-    case EDGERAG_F32:
-      rc = launch_rows<float>(head_dim, grid, s, q, q_stride_tok, q_stride_head, key_pool,
-                              value_pool, block_tables, block_tables_stride, query_start_loc,
-                              context_lens, plan_dev, n_q_heads, n_kv_heads, num_blocks, block_size,
-                              scale_log2, out, out_stride_tok, out_stride_head, ml, pacc);
-      break;
-    case EDGERAG_F16:
-      rc = launch_rows<f16>(head_dim, grid, s, q, q_stride_tok, q_stride_head, key_pool,
-                            value_pool, block_tables, block_tables_stride, query_start_loc,
-                            context_lens, plan_dev, n_q_heads, n_kv_heads, num_blocks, block_size,
-                            scale_log2, out, out_stride_tok, out_stride_head, ml, pacc);
-      break;
-    case EDGERAG_BF16:
-      rc = launch_rows<bf16>(head_dim, grid, s, q, q_stride_tok, q_stride_head, key_pool,
-                             value_pool, block_tables, block_tables_stride, query_start_loc,
-                             context_lens, plan_dev, n_q_heads, n_kv_heads, num_blocks, block_size,
-                             scale_log2, out, out_stride_tok, out_stride_head, ml, pacc);
-      break;
-    default:
-      return fail(EDGERAG_EINVAL, "edgerag_paged_attention: dtype %d", dtype);
+    case EDGERAG_F32: rc = run_dtype<float>(a, plan_host, head_dim); break;
+    case EDGERAG_F16: rc = run_dtype<f16>(a, plan_host, head_dim); break;
+    case EDGERAG_BF16: rc = run_dtype<bf16>(a, plan_host, head_dim); break;
+    default: return fail(EDGERAG_EINVAL, "edgerag_paged_attention: dtype %d", dtype);
   }
-  if (rc != EDGERAG_OK || n_partials == 0) return rc;
+  const int n_combine = plan_host[H_N_COMBINE];
+  if (rc != EDGERAG_OK || n_combine == 0) return rc;
 
-  const dim3 cblock(64, 4);
-  const dim3 cgrid(num_tokens, (n_q_heads + 3) / 4);
+  const int waves = 4;
+  const dim3 cblock(kWave * waves);
+  const dim3 cgrid(n_combine, (n_q_heads + waves - 1) / waves);
 #define EDGERAG_COMBINE(TYPE)                                                                     \
-  hipLaunchKernelGGL((attn_combine_kernel<TYPE>), cgrid, cblock, 0, s, plan_dev, query_start_loc, \
-                     context_lens, num_reqs, n_q_heads, head_dim, ml, pacc,                       \
+  hipLaunchKernelGGL((attn_combine_kernel<TYPE>), cgrid, cblock, 0, a.s, plan_dev,                \
+                     plan_host[H_COMBINE_OFF], n_q_heads, head_dim, a.ml, a.pacc,                 \
                      static_cast<TYPE*>(out), out_stride_tok, out_stride_head)
   switch (dtype) {
     case EDGERAG_F32: EDGERAG_COMBINE(float); break;

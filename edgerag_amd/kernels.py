@@ -181,6 +181,22 @@ class AttentionPlan:
         return int(self.plan_host[2])
 
 
+_WORKSPACES: dict[torch.device, torch.Tensor] = {}
+
+
+def attention_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """A per-device attention workspace (split partials) of at least ``nbytes``, reused across
+    steps so a step allocates nothing. Launches that share it must be ordered on one stream,
+    which is how the executor and the benchmark use it."""
+    device = torch.device(device)
+    buf = _WORKSPACES.get(device)
+    if buf is None or buf.numel() < nbytes:
+        size = max(nbytes, 2 * buf.numel() if buf is not None else 0, 1 << 20)
+        buf = torch.empty(size, dtype=torch.uint8, device=device)
+        _WORKSPACES[device] = buf
+    return buf
+
+
 def make_plan_host(
     query_start_loc: np.ndarray,
     context_lens: np.ndarray,
@@ -243,9 +259,7 @@ def plan_attention(
          block_tables, *extra],
         device,
     )
-    workspace = (
-        torch.empty(ws_bytes, dtype=torch.uint8, device=device) if ws_bytes > 0 else None
-    )
+    workspace = attention_workspace(device, ws_bytes) if ws_bytes > 0 else None
     num_reqs = int(np.asarray(context_lens).size)
     ap = AttentionPlan(
         plan_host=plan, plan_dev=views[0], query_start_loc=views[1], context_lens=views[2],

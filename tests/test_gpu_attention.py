@@ -272,6 +272,27 @@ def test_zero_query_requests_and_empty_batch(device) -> None:
     torch.testing.assert_close(got, expected, **FP32_TOL)
 
 
+def test_repeated_launches_with_a_shared_workspace_agree(device) -> None:
+    """Split partials live in a workspace reused across launches and plans: back-to-back
+    launches (with another plan's launch in between) must agree bit for bit."""
+    lens = [2000, 1500, 3000, 700]
+    kp, vp, tables, qsl, q, bt = _ragged_case(lens, [1] * 4, 8, 4, 64, torch.float16, 12)
+    kd, vd, qd = kp.to(device), vp.to(device), q.to(device)
+    plan, _ = kernels.plan_attention(qsl, np.asarray(lens, np.int32), bt, 8, 4, 64, BLOCK_SIZE,
+                                     torch.float16, device)
+    assert int(plan.plan_host[16]) > 0, "the case must exercise split merging"
+    other, _ = kernels.plan_attention(qsl[:3], np.asarray(lens[:2], np.int32), bt[:2], 8, 4, 64,
+                                      BLOCK_SIZE, torch.float16, device)
+    outs = []
+    for _ in range(3):
+        outs.append(kernels.paged_attention(qd, kd, vd, plan, 0.125).clone())
+        kernels.paged_attention(qd[:2], kd, vd, other, 0.125)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
+    expected = oa.ragged_reference(q, kp, vp, qsl.tolist(), lens, tables, 0.125)
+    torch.testing.assert_close(outs[0].float().cpu(), expected, **FP16_TOL)
+
+
 def test_plan_rejects_more_queries_than_context(device) -> None:
     kp, vp, tables, qsl, q, bt = _ragged_case([10], [10], 4, 4, 64, torch.float32, 8)
     with pytest.raises(kernels._lib.EdgeragError, match="queries but context"):
