@@ -246,6 +246,28 @@ def cpu_baseline(lens, budget_s=15.0):
     }
 
 
+def run_cfg3(device, args):
+    """Config 3: 3 prefill slices + 24 decodes in one step (append + attention)."""
+    lens3, q3 = cfg3_lens()
+    b3 = make_batch(lens3, q3, 16384, 3, device)
+    s3, a3, _ = time_step(b3, max(5, args.steps // 2), max(2, args.warmup // 2))
+    kv3, ap3, qo3, tb3 = step_bytes(lens3, q3, b3["bt"])
+    step_bytes_total = kv3 + ap3 + qo3 + tb3
+    res = {
+        "workload": "3 prefill slices (512 at offsets 0/3584/6656) + 24 decodes, 1560 tokens",
+        "ms_per_step": round(s3, 4),
+        "step_bytes": int(step_bytes_total),
+        "step_gbs": round(step_bytes_total / (s3 * 1e-3) / 1e9, 1),
+        "hbm_frac": round(step_bytes_total / (s3 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "attn_us": round(a3 * 1e3, 1),
+        "prefill_gflop": 46.18,
+        "attn_items": b3["plan"].n_items,
+    }
+    del b3
+    torch.cuda.empty_cache()
+    return res
+
+
 # --- main ------------------------------------------------------------------------------------------
 
 
@@ -256,6 +278,8 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-extra", action="store_true", help="skip configs 3 and 4")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", choices=["cfg3", "cfg4"], default=None,
+                    help="run just one secondary config (for profiling); prints its record")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: the ragged decoder step has no "
@@ -263,6 +287,12 @@ def main() -> None:
         sys.exit(2)
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
+    if args.only == "cfg3":
+        print(json.dumps({"cfg3": run_cfg3(device, args)}), flush=True)
+        return
+    if args.only == "cfg4":
+        print(json.dumps({"cfg4": bench_quant(device)}), flush=True)
+        return
 
     lens = cfg2_lens()
     b = make_batch(lens, [1] * 32, 16384, 2, device)
@@ -311,20 +341,7 @@ def main() -> None:
     line["config"]["copy_gbs_1gib"] = copy_bandwidth(device)
     torch.cuda.empty_cache()
     if not args.no_extra:
-        lens3, q3 = cfg3_lens()
-        b3 = make_batch(lens3, q3, 16384, 3, device)
-        s3, a3, _ = time_step(b3, max(5, args.steps // 2), max(2, args.warmup // 2))
-        kv3, ap3, qo3, tb3 = step_bytes(lens3, q3, b3["bt"])
-        line["cfg3"] = {
-            "workload": "3 prefill slices (512 at offsets 0/3584/6656) + 24 decodes, 1560 tokens",
-            "ms_per_step": round(s3, 4),
-            "step_gbs": round((kv3 + ap3 + qo3 + tb3) / (s3 * 1e-3) / 1e9, 1),
-            "hbm_frac": round((kv3 + ap3 + qo3 + tb3) / (s3 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "attn_us": round(a3 * 1e3, 1),
-            "prefill_tflops": round(46.18e9 / (a3 * 1e-3) / 1e12, 2),
-        }
-        del b3
-        torch.cuda.empty_cache()
+        line["cfg3"] = run_cfg3(device, args)
         line["cfg4"] = bench_quant(device)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(lens)

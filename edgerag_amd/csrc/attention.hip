@@ -28,44 +28,14 @@
 #include <cmath>
 #include <vector>
 
-#include "common.h"
+#include "attention_plan.h"
 
 namespace edgerag {
 namespace {
 
-// ---- plan layout (int32 words) -----------------------------------------------------------------
-constexpr int32_t kPlanMagic = 0x47415245;  // "ERAG"
-constexpr int32_t kPlanVersion = 3;
-constexpr int kHeaderWords = 24;
-constexpr int kItemWords = 8;
-constexpr int kReqWords = 4;
-
-enum Header {
-  H_MAGIC = 0,
-  H_VERSION,
-  H_N_ITEMS,
-  H_N_REQS,
-  H_ITEM_OFF,
-  H_REQ_OFF,
-  H_N_PARTIALS,
-  H_N_Q_HEADS,
-  H_N_KV_HEADS,
-  H_HEAD_DIM,
-  H_BLOCK_SIZE,
-  H_DTYPE,
-  H_NUM_TOKENS_HINT,
-  H_N_ROW_ITEMS,     // items [0, n_row) are row items, [n_row, n_items) tile items
-  H_MAX_ROW_VECS,    // largest c * n_rep among row items
-  H_MAX_SPLIT_BLOCKS,
-  H_N_COMBINE,        // rows (query tokens of split requests) attn_combine_kernel merges
-  H_COMBINE_OFF,      // word offset of the combine list
-};
-enum Item { I_REQ = 0, I_HEAD, I_QBEGIN, I_QCOUNT, I_KVBEGIN, I_KVEND, I_SPLIT, I_PAD };
-enum Req { R_NSPLIT = 0, R_SPLITLEN, R_PARTOFF, R_PAD };
-// One combine-list entry per query token of a split request: everything the merge needs in one
-// 32-byte load.
-constexpr int kCombineWords = 8;
-enum Combine { C_TOK = 0, C_Q0, C_C, C_L, C_NSPLIT, C_SPLITLEN, C_PARTOFF, C_PAD };
+using namespace plan;
+constexpr int32_t kPlanMagic = plan::kMagic;
+constexpr int32_t kPlanVersion = plan::kVersion;
 
 // Tuning constants; the EDGERAG_* macros let a build override them for sweeps.
 #ifndef EDGERAG_MIN_SPLIT
@@ -83,6 +53,14 @@ constexpr int kMinSplit = EDGERAG_MIN_SPLIT;  // tokens; shorter splits are not 
 constexpr int kTargetItems = EDGERAG_TARGET_ITEMS;  // decode work items a batch is cut into
 constexpr int kDecodeU = EDGERAG_DECODE_U;  // token loads in flight per lane group
 constexpr int kMaxSplitBlocks = 64;  // one block id per lane in the decode kernel
+#ifndef EDGERAG_TARGET_TILES
+#define EDGERAG_TARGET_TILES 512
+#endif
+#ifndef EDGERAG_MIN_TILE_SPLIT
+#define EDGERAG_MIN_TILE_SPLIT 1024
+#endif
+constexpr int kMinTileSplit = EDGERAG_MIN_TILE_SPLIT;  // keys: tiles split no finer than this
+constexpr int kTargetTiles = EDGERAG_TARGET_TILES;  // prefill tile items a batch aims for
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -538,21 +516,7 @@ WorkspaceLayout workspace_layout(int64_t n_partials, int64_t head_dim) {
   return w;
 }
 
-struct Launch {
-  hipStream_t s;
-  const void* q;
-  int64_t q_st, q_sh;
-  const void *kp, *vp;
-  const int32_t* bt;
-  int64_t bt_stride;
-  const int32_t *qsl, *ctx, *plan;
-  int32_t hq, hkv, nb, bs;
-  float scale_log2;
-  void* out;
-  int64_t o_st, o_sh;
-  float2* ml;
-  float* pacc;
-};
+using Launch = AttnLaunch;
 
 template <typename T, int D, int QR, int U>
 void launch_decode(const Launch& a, int base, int count) {
@@ -593,12 +557,24 @@ void dispatch_rows_qr(const Launch& a, int qr, int base, int count) {
   }
 }
 
-// Row items: fast decode kernel when every split's load groups stay inside one block, the
-// general kernel otherwise. Tile items: general kernel with 8 query vectors per pass.
+// Tile items (prefill slices) first: the MFMA tile kernel for fp16 / head_dim 64, the general
+// row kernel with 8 query vectors per pass otherwise. Row items: the fast decode kernel when
+// every split's load groups stay inside one block, the general kernel otherwise.
 template <typename T, int D>
 int run_items(const Launch& a, const int32_t* ph) {
   using C = RowCfg<T, D>;
   const int n_items = ph[H_N_ITEMS], n_row = ph[H_N_ROW_ITEMS];
+  if (n_items > n_row) {
+    if constexpr (__is_same(T, f16) && D == 64) {
+      if (ph[H_TILE_KIND] == 1 && prefill_tiles_supported(a.nb, a.bs)) {
+        launch_prefill_tiles_f16_d64(a, n_row, n_items - n_row);
+      } else {
+        dispatch_rows_qr<T, D>(a, 8, n_row, n_items - n_row);
+      }
+    } else {
+      dispatch_rows_qr<T, D>(a, 8, n_row, n_items - n_row);
+    }
+  }
   const int qr = std::min(8, pow2_at_least(std::max(1, ph[H_MAX_ROW_VECS])));
   const bool fast = a.bs % C::TPW == 0 && ph[H_MAX_SPLIT_BLOCKS] <= kMaxSplitBlocks;
   if (n_row > 0) {
@@ -607,7 +583,6 @@ int run_items(const Launch& a, const int32_t* ph) {
     else
       dispatch_rows_qr<T, D>(a, qr, 0, n_row);
   }
-  if (n_items > n_row) dispatch_rows_qr<T, D>(a, 8, n_row, n_items - n_row);
   return check_launch("edgerag_paged_attention");
 }
 
@@ -653,7 +628,13 @@ extern "C" int edgerag_attn_plan(const int32_t* query_start_loc, const int32_t* 
                 max_blocks_per_seq);
 
   const int n_rep = n_q_heads / n_kv_heads;
-  int64_t work = 0;  // KV token-heads the batch reads, to size the splits
+  // Prefill tiles run on MFMA for fp16 / head_dim 64: 128 virtual rows (token x head-in-group).
+  const bool mfma_tiles = dtype == EDGERAG_F16 && head_dim == 64 && n_rep <= kMfmaTileRows;
+  const int tile_rows = mfma_tiles ? kMfmaTileRows / n_rep : kQTile;
+  int64_t work = 0;       // KV token-heads the decode rows read, to size their splits
+  int64_t tile_work = 0;  // tile x keys of the prefill slices, to size theirs
+  int64_t n_tiles = 0;    // prefill tile items before any KV split
+  int64_t max_len = 0;
   for (int r = 0; r < num_reqs; ++r) {
     const int64_t c = int64_t(query_start_loc[r + 1]) - query_start_loc[r];
     const int64_t L = context_lens[r];
@@ -667,12 +648,29 @@ extern "C" int edgerag_attn_plan(const int32_t* query_start_loc, const int32_t* 
       return fail(EDGERAG_EINVAL,
                   "edgerag_attn_plan: request %d needs %lld blocks, block table holds %d", r,
                   (long long)((L + block_size - 1) / block_size), max_blocks_per_seq);
-    if (c > 0) work += L * n_kv_heads;
+    if (c > 0 && c * n_rep <= kMaxRowVecs) work += L * n_kv_heads;
+    if (c * n_rep > kMaxRowVecs) {
+      tile_work += (c + tile_rows - 1) / tile_rows * n_kv_heads * L;
+      n_tiles += (c + tile_rows - 1) / tile_rows * n_kv_heads;
+    }
+    max_len = std::max(max_len, L);
   }
   int64_t split_len = std::max<int64_t>(kMinSplit, (work + kTargetItems - 1) / kTargetItems);
   split_len = round_up(split_len, block_size);
   split_len = std::min<int64_t>(split_len, int64_t(kMaxSplitBlocks) * block_size);
   const int split_blocks = int((split_len + block_size - 1) / block_size);
+  // Prefill tiles: split the keys only when there are too few tiles to fill the GPU, and then
+  // only as far as needed for about kTargetTiles items, in whole 64-key LDS tiles; every extra
+  // split costs a partial write and a merge.
+  // A split may span at most kMaxTileBlocks blocks (the MFMA tile kernel stages its block ids).
+  const int64_t tile_split_cap =
+      std::max<int64_t>(64, int64_t(kMaxTileBlocks - 1) * block_size / 64 * 64);
+  const int64_t tile_split_len = std::min(
+      tile_split_cap,
+      n_tiles >= kTargetTiles
+          ? round_up(std::max<int64_t>(max_len, 1), 64)
+          : round_up(std::max<int64_t>(kMinTileSplit,
+                                       (tile_work + kTargetTiles - 1) / kTargetTiles), 64));
 
   std::vector<PlanItem> rows, tiles;
   std::vector<int32_t> reqs(size_t(num_reqs) * kReqWords, 0);
@@ -684,15 +682,16 @@ extern "C" int edgerag_attn_plan(const int32_t* query_start_loc, const int32_t* 
     const int c = query_start_loc[r + 1] - q0;
     const int L = context_lens[r];
     int32_t* rq = reqs.data() + size_t(r) * kReqWords;
-    const int nsplit = c == 0 ? 0 : int((L + split_len - 1) / split_len);
     const bool row = c * n_rep <= kMaxRowVecs;
+    const int64_t slen = row ? split_len : tile_split_len;
+    const int nsplit = c == 0 ? 0 : int((L + slen - 1) / slen);
     rq[R_NSPLIT] = nsplit;
-    rq[R_SPLITLEN] = int32_t(split_len);
+    rq[R_SPLITLEN] = int32_t(slen);
     rq[R_PARTOFF] = int32_t(n_partials);
     if (c == 0) continue;
     if (nsplit > 1) {
       for (int t = q0; t < q0 + c; ++t) {
-        const int32_t e[kCombineWords] = {t, q0, c, L, nsplit, int32_t(split_len),
+        const int32_t e[kCombineWords] = {t, q0, c, L, nsplit, int32_t(slen),
                                           int32_t(n_partials), 0};
         combine.insert(combine.end(), e, e + kCombineWords);
       }
@@ -700,15 +699,15 @@ extern "C" int edgerag_attn_plan(const int32_t* query_start_loc, const int32_t* 
     }
     if (n_partials > INT32_MAX)
       return fail(EDGERAG_EUNSUPPORTED, "edgerag_attn_plan: batch needs > 2^31 split partials");
-    const int tile_rows = row ? c : kQTile;
+    const int rows_per_item = row ? c : tile_rows;
     if (row) max_row_vecs = std::max(max_row_vecs, c * n_rep);
-    for (int tile = 0; tile < c; tile += tile_rows) {
-      const int qc = std::min(tile_rows, c - tile);
+    for (int tile = 0; tile < c; tile += rows_per_item) {
+      const int qc = std::min(rows_per_item, c - tile);
       const int last_visible = L - c + tile + qc - 1;  // causal limit of the tile's last row
       for (int s = 0; s < nsplit; ++s) {
-        const int kb = int(s * split_len);
+        const int kb = int(s * slen);
         if (kb > last_visible) break;
-        const int ke = int(std::min<int64_t>(L, (s + 1) * split_len));
+        const int ke = int(std::min<int64_t>(L, (s + 1) * slen));
         const int ke_eff = std::min(ke, last_visible + 1);
         for (int h = 0; h < n_kv_heads; ++h) {
           PlanItem p{};
@@ -761,6 +760,7 @@ extern "C" int edgerag_attn_plan(const int32_t* query_start_loc, const int32_t* 
   plan[H_MAX_SPLIT_BLOCKS] = split_blocks;
   plan[H_N_COMBINE] = int32_t(combine.size() / kCombineWords);
   plan[H_COMBINE_OFF] = int32_t(combine_off);
+  plan[H_TILE_KIND] = mfma_tiles ? 1 : 0;
   std::copy(combine.begin(), combine.end(), plan + combine_off);
   int32_t* dst = plan + item_off;
   for (const auto* group : {&rows, &tiles})
@@ -792,6 +792,8 @@ extern "C" int edgerag_paged_attention(
     return fail(EDGERAG_EINVAL, "edgerag_paged_attention: plan covers %d tokens, q holds %d",
                 plan_host[H_NUM_TOKENS_HINT], num_tokens);
   if (num_blocks <= 0) return fail(EDGERAG_EINVAL, "edgerag_paged_attention: num_blocks <= 0");
+  if (!(scale > 0.f) || !std::isfinite(scale))
+    return fail(EDGERAG_EINVAL, "edgerag_paged_attention: scale must be positive and finite");
   const int n_items = plan_host[H_N_ITEMS];
   const int64_t n_partials = plan_host[H_N_PARTIALS];
   const WorkspaceLayout ws = workspace_layout(n_partials, head_dim);

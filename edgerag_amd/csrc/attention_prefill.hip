@@ -1,0 +1,350 @@
+// Chunked-prefill attention tiles on CDNA4 matrix cores (fp16, head_dim 64).
+//
+// A work item is (request, kv head, query tile of up to kMfmaTileRows virtual rows, KV split).
+// Virtual row rho is query token qb + rho / n_rep of query head h * n_rep + rho % n_rep, so all
+// heads of a GQA group share every K/V tile. Each wave owns 32 rows.
+//
+// Per 64-key tile:
+//   * the workgroup stages K row-major and V transposed (V^T[dim][key]) into one of two LDS
+//     buffers straight from the paged pool with raw buffer loads: keys without a valid block get
+//     an out-of-range offset and load zeros, no branch. The next tile's loads are issued before
+//     the current tile is computed, so HBM/L2 latency overlaps the matrix work; one barrier per
+//     tile. LDS rows are 128 bytes with the 16-byte chunk index XOR-swizzled by the row, so the
+//     MFMA operand reads and the staging writes are bank-conflict free.
+//   * each wave computes S^T = K Q^T with v_mfma_f32_32x32x16_f16: A = 32 keys x 16 dims from
+//     LDS, B = Q^T from registers (loaded once per item): per lane, 16 keys of one query.
+//   * online softmax in the log2 domain: the running max is kept on raw scores, the scale is
+//     folded into the exponent's FMA, and the max is only raised when a score beats it by 2^8
+//     (lazy rescale; p <= 256 stays exact in fp16). Masks (causal k <= L - c + i, split end,
+//     invalid blocks) are applied only on tiles that need them.
+//   * O^T += V^T P^T with the same MFMA: the probabilities, packed to fp16, are already in the
+//     B-operand layout once the contraction index is permuted; V^T is stored in that permuted key
+//     order, so each A operand is one 16-byte LDS read. l accumulates the same fp16 p (v_dot2).
+// The output is O / l (fp16) or, for split items, fp32 partials merged by attn_combine_kernel.
+#include "attention_plan.h"
+
+namespace edgerag {
+namespace {
+
+using namespace plan;
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kD = 64;
+constexpr int kKeys = 64;            // keys per LDS tile
+constexpr int kRow = 64;             // halves per LDS row (K: one key; V^T: one dim)
+constexpr float kRescaleLog2 = 8.f;  // lazy rescale: p may grow to 2^8 before the max moves
+constexpr int kWaves = kMfmaTileRows / 32;
+constexpr int kThreads = kWaves * kWave;
+constexpr int kKChunks = kKeys * kD * 2 / 16;  // 16-byte chunks of a K tile (512)
+constexpr int kKPerThread = kKChunks / kThreads;
+constexpr int kVPairs = (kKeys / 4) * (kD / 8);  // (key quad, dim chunk) pairs of a V tile (128)
+constexpr int kVPerThread = (kVPairs + kThreads - 1) / kThreads;
+static_assert(kKChunks % kThreads == 0, "K staging split");
+
+// Byte offset handed to buffer loads for keys with no valid block: beyond num_records, so the
+// load returns zeros without a branch (the launcher keeps a head's pool slice below it).
+constexpr uint32_t kOutOfRange = 0xFFFFFFF0u;
+
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ f32x16 mfma32(h8 a, h8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ h8 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, uint32_t byte_off) {
+  return __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(rsrc, byte_off, 0, 0));
+}
+
+// Halves offset of 16-byte chunk `chunk` (0..7) of LDS row `row`, chunk index XOR-swizzled.
+__device__ __forceinline__ int lds_chunk(int row, int chunk) {
+  return row * kRow + ((chunk ^ (row & 7)) << 3);
+}
+
+// V^T keeps keys in the order the P.V k-steps consume them: within every 16 keys, bits 2 and 3
+// of the key index are swapped, so lane group g's keys {0-3, 8-11} + 4g of a k-step are one
+// contiguous 16-byte run.
+__device__ __forceinline__ int vt_slot(int key) {
+  return (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1);
+}
+
+struct StageRegs {
+  h8 k[kKPerThread];
+  h8 v[4 * kVPerThread];
+};
+
+struct Geometry {
+  int kb, ke, blk0, bs_shift, bs_mask;
+};
+
+// Byte offset of (pos, 16-byte dim chunk dc) in one kv head's pool slice, or kOutOfRange.
+__device__ __forceinline__ uint32_t pool_offset(const Geometry& geo, const int* __restrict__ sblk,
+                                                int pos, int dc) {
+  const int i = (pos >> geo.bs_shift) - geo.blk0;
+  const int blk = (pos < geo.ke && i < kMaxTileBlocks) ? sblk[i] : -1;
+  return blk >= 0 ? ((uint32_t(blk) << geo.bs_shift) + uint32_t(pos & geo.bs_mask)) *
+                            uint32_t(kD * 2) + uint32_t(16 * dc)
+                  : kOutOfRange;
+}
+
+// K: chunk c = tid + kThreads * j is key c / 8, dim chunk c % 8 (8 lanes fill one key row).
+// V: pair p = tid + kThreads * j is key quad p % 16, dim chunk p / 16 (16 lanes fill one V^T row).
+__device__ __forceinline__ void stage_load(StageRegs& st, int tid, int k0, const Geometry& geo,
+                                           const int* __restrict__ sblk,
+                                           __amdgpu_buffer_rsrc_t krs, __amdgpu_buffer_rsrc_t vrs) {
+#pragma unroll
+  for (int j = 0; j < kKPerThread; ++j) {
+    const int c = tid + kThreads * j;
+    st.k[j] = buffer_load16(krs, pool_offset(geo, sblk, k0 + c / 8, c % 8));
+  }
+#pragma unroll
+  for (int j = 0; j < kVPerThread; ++j) {
+    const int p = tid + kThreads * j;
+    if (kVPairs % kThreads != 0 && p >= kVPairs) break;
+    const int a = p % 16, b = p / 16;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      st.v[4 * j + kk] = buffer_load16(vrs, pool_offset(geo, sblk, k0 + 4 * a + kk, b));
+  }
+}
+
+__device__ __forceinline__ void stage_store(const StageRegs& st, int tid,
+                                            _Float16* __restrict__ sk, _Float16* __restrict__ svt) {
+#pragma unroll
+  for (int j = 0; j < kKPerThread; ++j) {
+    const int c = tid + kThreads * j;
+    *reinterpret_cast<h8*>(sk + lds_chunk(c / 8, c % 8)) = st.k[j];
+  }
+#pragma unroll
+  for (int j = 0; j < kVPerThread; ++j) {
+    const int p = tid + kThreads * j;
+    if (kVPairs % kThreads != 0 && p >= kVPairs) break;
+    const int a = p % 16, b = p / 16;
+    const int slot = vt_slot(4 * a);  // 4-aligned: the 4 keys stay contiguous
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      const int row = 8 * b + d;
+      const h4 col4 = {st.v[4 * j][d], st.v[4 * j + 1][d], st.v[4 * j + 2][d],
+                       st.v[4 * j + 3][d]};
+      *reinterpret_cast<h4*>(svt + lds_chunk(row, slot >> 3) + (slot & 7)) = col4;
+    }
+  }
+}
+
+// Two waves per SIMD: the register budget (256 per lane) keeps S, O and the staged tile in VGPRs.
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void attn_prefill_mfma_kernel(
+    const _Float16* __restrict__ q, int64_t q_st, int64_t q_sh,
+    const _Float16* __restrict__ kpool, const _Float16* __restrict__ vpool,
+    const int32_t* __restrict__ block_tables, int64_t bt_stride,
+    const int32_t* __restrict__ qsl, const int32_t* __restrict__ ctx,
+    const int32_t* __restrict__ plan, int32_t item_base, int32_t n_q_heads, int32_t n_kv_heads,
+    int32_t num_blocks, int32_t bs_shift, float scale_log2, _Float16* __restrict__ out,
+    int64_t o_st, int64_t o_sh, float2* __restrict__ part_ml, float* __restrict__ part_acc) {
+  __shared__ __align__(16) _Float16 sk[2][kKeys * kRow];
+  __shared__ __align__(16) _Float16 svt[2][kD * kRow];
+  __shared__ int sblk[kMaxTileBlocks];
+
+  const int32_t* it = plan + plan[H_ITEM_OFF] + int64_t(item_base + blockIdx.x) * kItemWords;
+  const int r = it[I_REQ], h = it[I_HEAD], qb = it[I_QBEGIN], qc = it[I_QCOUNT];
+  const int kb = it[I_KVBEGIN], ke = it[I_KVEND], split = it[I_SPLIT];
+  const int32_t* rq = plan + plan[H_REQ_OFF] + r * kReqWords;
+  const int nsplit = rq[R_NSPLIT], part_off = rq[R_PARTOFF];
+  const int q0 = qsl[r], c = qsl[r + 1] - q0, L = ctx[r];
+  const int n_rep = n_q_heads / n_kv_heads;
+  const int32_t* table = block_tables + int64_t(r) * bt_stride;
+  const int64_t head_base = int64_t(h) * num_blocks;
+  const int block_size = 1 << bs_shift;
+
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int g = lane / 32, col = lane % 32;
+  const int nrows = qc * n_rep;
+  const int rho = wave * 32 + col;
+  const bool active = rho < nrows;
+  const int t = qb + (active ? rho / n_rep : 0);
+  const int hq = h * n_rep + (active ? rho % n_rep : 0);
+  const int lim = active ? L - c + (t - q0) : -1;  // last visible key position of this row
+  const bool wave_live = wave * 32 < nrows;
+  // Smallest causal limit among the wave's rows: tiles ending at or below it need no mask.
+  const int first_row = min(wave * 32, nrows - 1);
+  const int wave_min_lim = L - c + (qb + first_row / n_rep - q0);
+
+  Geometry geo;
+  geo.kb = kb;
+  geo.ke = ke;
+  geo.blk0 = kb >> bs_shift;
+  geo.bs_shift = bs_shift;
+  geo.bs_mask = block_size - 1;
+  // Block ids of the whole split, once (the planner caps a split at kMaxTileBlocks blocks).
+  {
+    const int nblk = min(((ke - 1) >> bs_shift) - geo.blk0 + 1, kMaxTileBlocks);
+    for (int i = tid; i < nblk; i += kThreads) {
+      const int32_t b = table[geo.blk0 + i];
+      sblk[i] = (b >= 0 && b < num_blocks) ? b : -1;
+    }
+  }
+  __syncthreads();
+
+  // Q^T as the B operand: k-step ks covers dims 16*ks + 8*g .. +7 of this lane's query.
+  h8 qop[4];
+  {
+    const _Float16* qp = q + int64_t(t) * q_st + int64_t(hq) * q_sh;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      qop[ks] = active ? *reinterpret_cast<const h8*>(qp + 16 * ks + 8 * g) : h8{};
+  }
+  f32x16 o0 = {}, o1 = {};  // O^T dims 0-31 and 32-63 of this lane's query
+  float m = -INFINITY;      // reference max of raw (unscaled) scores
+  float l = 0.f;
+  const h2 ones = {_Float16(1.f), _Float16(1.f)};
+
+  const uint32_t head_bytes = uint32_t(int64_t(num_blocks) * block_size * kD * 2);
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<_Float16*>(kpool + head_base * block_size * kD), 0, head_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<_Float16*>(vpool + head_base * block_size * kD), 0, head_bytes, 0x00020000);
+
+  StageRegs st;
+  stage_load(st, tid, kb, geo, sblk, krs, vrs);
+  int buf = 0;
+  for (int k0 = kb; k0 < ke; k0 += kKeys, buf ^= 1) {
+    stage_store(st, tid, sk[buf], svt[buf]);
+    __syncthreads();
+    if (k0 + kKeys < ke) stage_load(st, tid, k0 + kKeys, geo, sblk, krs, vrs);
+    if (!wave_live) continue;
+    const _Float16* skb = sk[buf];
+    const _Float16* svb = svt[buf];
+
+    // S^T = K Q^T: two 32-key tiles, 4 k-steps of 16 dims (dim chunk 2ks + g).
+    f32x16 s[2] = {{}, {}};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        const h8 ka = *reinterpret_cast<const h8*>(skb + lds_chunk(32 * kt + col, 2 * ks + g));
+        s[kt] = mfma32(ka, qop[ks], s[kt]);
+      }
+    }
+    // Register i of tile kt holds key 32kt + (i%4) + 8(i/4) + 4g.
+    const int key_end = min(ke - k0, kKeys);  // keys of this tile inside the split
+    if (k0 + kKeys - 1 > wave_min_lim || key_end < kKeys) {
+      const int vis_end = min(key_end, lim - k0 + 1);  // keys [0, vis_end) are visible
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (32 * kt + (i & 3) + 8 * (i >> 2) + 4 * g >= vis_end) s[kt][i] = -INFINITY;
+    }
+    // Keys whose block id is invalid (never in a well-formed table): masked too.
+    const int bi = min(((k0 + min(lane, key_end - 1)) >> bs_shift) - geo.blk0, kMaxTileBlocks - 1);
+    const uint64_t bad = __ballot(lane < key_end && sblk[bi] < 0);
+    if (bad != 0) {
+      // Lane group g's keys of tile kt are bits (i%4) + 8(i/4) of (bad_kt >> 4g).
+      const uint32_t b0 = uint32_t(bad) >> (4 * g), b1 = uint32_t(bad >> 32) >> (4 * g);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int bit = (i & 3) + 8 * (i >> 2);
+        if ((b0 >> bit) & 1u) s[0][i] = -INFINITY;
+        if ((b1 >> bit) & 1u) s[1][i] = -INFINITY;
+      }
+    }
+    float tmax = s[0][0];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, s[kt][i]);
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));  // the other 16 keys of each 32-key tile
+    // Lazy rescale: the reference max m only moves when a score beats it by 2^kRescaleLog2.
+    const bool up = m == -INFINITY ? tmax != -INFINITY : (tmax - m) * scale_log2 > kRescaleLog2;
+    if (__any(up)) {
+      const float m_new = up ? tmax : m;
+      const float alpha = m == -INFINITY ? (up ? 0.f : 1.f) : exp2_fast((m - m_new) * scale_log2);
+      m = m_new;
+      l *= alpha;
+      o0 *= alpha;
+      o1 *= alpha;
+    }
+    const float bias = m == -INFINITY ? 0.f : -m * scale_log2;
+
+    // P = exp2(s * scale - m * scale), packed to fp16 in the B-operand order of each k-step.
+    float lsum = 0.f;
+#pragma unroll
+    for (int st4 = 0; st4 < 4; ++st4) {
+      const int kt = st4 >> 1, half = st4 & 1;
+      h8 pb;
+#pragma unroll
+      for (int j = 0; j < 8; j += 2) {
+        const float p0 = exp2_fast(fmaf(s[kt][8 * half + j], scale_log2, bias));
+        const float p1 = exp2_fast(fmaf(s[kt][8 * half + j + 1], scale_log2, bias));
+        const h2 pp = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(p0, p1));
+        pb[j] = pp[0];
+        pb[j + 1] = pp[1];
+        lsum = __builtin_amdgcn_fdot2(pp, ones, lsum, false);
+      }
+      const int vchunk = 4 * kt + 2 * half + g;  // permuted V^T slots of this k-step
+      o0 = mfma32(*reinterpret_cast<const h8*>(svb + lds_chunk(col, vchunk)), pb, o0);
+      o1 = mfma32(*reinterpret_cast<const h8*>(svb + lds_chunk(32 + col, vchunk)), pb, o1);
+    }
+    lsum += __shfl_xor(lsum, 32, kWave);
+    l += lsum;
+  }
+
+  if (!active) return;
+  // O^T register i of dim tile dt holds dim 32dt + (i%4) + 8(i/4) + 4g of this lane's query.
+  if (nsplit == 1) {
+    const float inv = 1.f / fmaxf(l, 1.17549435e-38f);
+    _Float16* op = out + int64_t(t) * o_st + int64_t(hq) * o_sh;
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      const int d0 = 8 * qd + 4 * g;
+      *reinterpret_cast<h4*>(op + d0) =
+          h4{_Float16(o0[4 * qd] * inv), _Float16(o0[4 * qd + 1] * inv),
+             _Float16(o0[4 * qd + 2] * inv), _Float16(o0[4 * qd + 3] * inv)};
+      *reinterpret_cast<h4*>(op + 32 + d0) =
+          h4{_Float16(o1[4 * qd] * inv), _Float16(o1[4 * qd + 1] * inv),
+             _Float16(o1[4 * qd + 2] * inv), _Float16(o1[4 * qd + 3] * inv)};
+    }
+  } else {
+    // Partials carry the max in the same log2 domain as the decode kernels: m * scale_log2.
+    const int64_t idx = int64_t(part_off) + (int64_t(t - q0) * n_q_heads + hq) * nsplit + split;
+    if (g == 0) part_ml[idx] = make_float2(m == -INFINITY ? m : m * scale_log2, l);
+    float* pa = part_acc + idx * kD;
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      const int d0 = 8 * qd + 4 * g;
+      *reinterpret_cast<float4*>(pa + d0) =
+          make_float4(o0[4 * qd], o0[4 * qd + 1], o0[4 * qd + 2], o0[4 * qd + 3]);
+      *reinterpret_cast<float4*>(pa + 32 + d0) =
+          make_float4(o1[4 * qd], o1[4 * qd + 1], o1[4 * qd + 2], o1[4 * qd + 3]);
+    }
+  }
+}
+
+int log2_exact(int v) {
+  int s = 0;
+  while ((1 << s) < v) ++s;
+  return (1 << s) == v ? s : -1;
+}
+
+}  // namespace
+
+bool prefill_tiles_supported(int32_t num_blocks, int32_t block_size) {
+  // Power-of-two blocks (shift addressing), and one kv head's slice of a pool must fit a
+  // buffer resource, below kOutOfRange.
+  return log2_exact(block_size) >= 0 &&
+         int64_t(num_blocks) * block_size * kD * 2 < int64_t(kOutOfRange);
+}
+
+void launch_prefill_tiles_f16_d64(const AttnLaunch& a, int item_base, int count) {
+  hipLaunchKernelGGL(attn_prefill_mfma_kernel, dim3(count), dim3(kThreads), 0, a.s,
+                     static_cast<const _Float16*>(a.q), a.q_st, a.q_sh,
+                     static_cast<const _Float16*>(a.kp), static_cast<const _Float16*>(a.vp), a.bt,
+                     a.bt_stride, a.qsl, a.ctx, a.plan, item_base, a.hq, a.hkv, a.nb,
+                     log2_exact(a.bs), a.scale_log2, static_cast<_Float16*>(a.out), a.o_st,
+                     a.o_sh, a.ml, a.pacc);
+}
+
+}  // namespace edgerag

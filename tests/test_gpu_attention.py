@@ -299,6 +299,30 @@ def test_plan_rejects_more_queries_than_context(device) -> None:
         _run_ragged(device, kp, vp, np.array([0, 10], np.int32), [9], bt, q, 0.125)
 
 
+@pytest.mark.parametrize("n_q,n_kv", [(32, 32), (9, 3), (8, 1)])
+def test_cfg3_shape_mixed_batch_fp16(device, n_q, n_kv) -> None:
+    """prefill slices of 512 at offsets 0 / 3584 / 6656 beside 24 decodes
+    with L ~ U[512, 7472]; fp16, d 64 (the MFMA tile path), plus GQA groupings."""
+    g = seeded(3)
+    dec = torch.randint(512, 7473, (24,), generator=g).tolist()
+    lens = [512, 3584 + 512, 6656 + 512] + dec
+    q_lens = [512, 512, 512] + [1] * 24
+    kp, vp, tables, qsl, q, bt = _ragged_case(lens, q_lens, n_q, n_kv, 64, torch.float16, 31)
+    got = _run_ragged(device, kp, vp, qsl, lens, bt, q, 0.125)
+    expected = oa.ragged_reference(q, kp, vp, qsl.tolist(), lens, tables, 0.125)
+    torch.testing.assert_close(got.float(), expected, **FP16_TOL)
+
+
+@pytest.mark.parametrize("c,past", [(1, 0), (7, 0), (64, 0), (65, 13), (130, 200), (512, 3584)])
+def test_fp16_prefill_chunk_edges(device, c, past) -> None:
+    """Tile edges: partial 128-row tiles, chunks shorter than one 64-key tile, ragged prefixes."""
+    L = past + c
+    kp, vp, tables, qsl, q, bt = _ragged_case([L], [c], 4, 4, 64, torch.float16, c + past)
+    got = _run_ragged(device, kp, vp, qsl, [L], bt, q, 0.125)
+    expected = oa.ragged_reference(q, kp, vp, qsl.tolist(), [L], tables, 0.125)
+    torch.testing.assert_close(got.float(), expected, **FP16_TOL)
+
+
 def test_cfg2_shape_decode_batch_fp16(device) -> None:
     """BASELINE config 2 at full shape: 32 decodes, L ~ U[256, 7472], 32/32 heads, d 64,
     16,384-block pool (1 GiB per pool), seeded-shuffled tables."""
