@@ -8,6 +8,7 @@
 // the reference's dequantize_groupwise produces) and accumulates x . w in fp32 with
 // v_dot2_f32_f16. Weight bytes dominate traffic for M <= 64, so the kernel is HBM-bound there.
 #include "common.h"
+#include "quant_mfma.h"
 
 namespace edgerag {
 namespace {
@@ -327,6 +328,12 @@ extern "C" int edgerag_quant_linear(const void* x, int32_t x_dtype, int64_t x_st
                 (long long)x_stride, (long long)y_stride);
   auto s = static_cast<hipStream_t>(stream);
   if (x_dtype == EDGERAG_F16) {
+    if (qlinear_mfma_supported(k, bits, group_size, x, x_stride, packed)) {
+      launch_qlinear_mfma(static_cast<const f16*>(x), x_stride, m, k, packed,
+                          static_cast<const f16*>(scales_f16), static_cast<const f16*>(bias_f16),
+                          n, bits, group_size, static_cast<f16*>(y), y_stride, s);
+      return check_launch("edgerag_quant_linear");
+    }
     return bits == 8 ? launch_linear<8, f16>(x, x_stride, m, k, packed, scales_f16, bias_f16, n,
                                              group_size, y, y_stride, s)
                      : launch_linear<4, f16>(x, x_stride, m, k, packed, scales_f16, bias_f16, n,

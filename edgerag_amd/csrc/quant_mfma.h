@@ -1,0 +1,21 @@
+// Launchers of the MFMA weight-only linear kernels (quant_mfma.hip), called by
+// edgerag_quant_linear for fp16 activations.
+#pragma once
+
+#include "common.h"
+
+namespace edgerag {
+
+// Whether the MFMA kernels take this shape: K a whole number of 16-byte lane loads per row
+// (64 k for INT8, 128 k for INT4), one scale per lane load (group_size % 16 for INT8, % 32 for
+// INT4), 16-byte aligned weights and activations.
+bool qlinear_mfma_supported(int32_t k, int32_t bits, int32_t g, const void* x, int64_t x_stride,
+                            const void* packed);
+
+// y[M, N] = x[M, K] . W^T (+ bias) with W = fp16(code) * fp16(scale) rounded once, like the
+// reference's dequantize_groupwise; fp32 accumulation on v_mfma_f32_*_f16. Enqueues on `s`.
+void launch_qlinear_mfma(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
+                         const f16* scales, const f16* bias, int32_t n, int32_t bits, int32_t g,
+                         f16* y, int64_t ys, hipStream_t s);
+
+}  // namespace edgerag

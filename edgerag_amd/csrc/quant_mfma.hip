@@ -1,0 +1,504 @@
+// Weight-only INT8 / INT4 linear layers on CDNA4 matrix cores (fp16 activations).
+//
+// Both kernels rebuild each weight exactly as the reference's dequantize_groupwise does
+// (edgerag/core/quant.py:98-107): the code becomes an fp16 integer exactly (a byte or nibble is
+// OR-ed into the mantissa of 1024.0 and the bias is subtracted, both exact), then one fp16
+// multiply by the fp16 group scale rounds once, like `codes.half() * scales`. x . W^T then runs on
+// v_mfma_f32_*_f16 with fp32 accumulation, as F.linear does on fp16 tensors
+// (edgerag/core/linear.py:194-196). The fp16 weight matrix is never written to memory.
+//
+// * qlinear_skinny_kernel (M <= 32, the decode GEMVs): HBM-bound. A wave owns 16 or 32 output
+//   rows and one K chunk; every lane streams 16 bytes of packed weights per load (4 lanes cover
+//   64 contiguous bytes of a row), U loads deep, and feeds them to v_mfma_f32_16x16x32_f16 as the
+//   A operand straight from registers (no LDS). The activations (B operand, up to 32 rows) come
+//   from L2. The waves of a workgroup split K; their partial sums are added in LDS in a fixed order.
+//   Only the lane-to-k assignment inside a k-step differs from textbook order, identically for
+//   both operands: INT4 nibbles decode to the k order (0,4,1,5,2,6,3,7), so the activations are
+//   permuted the same way in registers.
+// * qlinear_gemm_kernel (M > 32, prefill slices): MFMA-bound. A 256-thread workgroup computes a
+//   BN x BM tile of y^T through v_mfma_f32_32x32x16_f16; per 64-k step it stages the dequantised
+//   weights and the activations in double-buffered, XOR-swizzled LDS, loading the next step's
+//   bytes from global memory while the current one is computed.
+#include "quant_mfma.h"
+
+#ifndef EDGERAG_SKINNY_MAX_M
+#define EDGERAG_SKINNY_MAX_M 32
+#endif
+
+namespace edgerag {
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ f32x4 mfma16(h8 a, h8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma32(h8 a, h8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
+__device__ __forceinline__ uint32_t as_u32(h2 v) { return __builtin_bit_cast(uint32_t, v); }
+
+__device__ __forceinline__ h8 pack_h8(h2 a, h2 b, h2 c, h2 d) {
+  return h8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+// Four INT8 codes (two's complement bytes of `w`) times the scale, in k order: two fp16 pairs.
+// Byte b becomes the fp16 1024 + (b ^ 0x80) via v_perm_b32; subtracting 1152 leaves the signed
+// code exactly.
+__device__ __forceinline__ void deq_i8_word(uint32_t w, h2 s2, h2& lo, h2& hi) {
+  const uint32_t wx = w ^ 0x80808080u;
+  const h2 bias = {_Float16(1152.f), _Float16(1152.f)};
+  lo = (as_h2(__builtin_amdgcn_perm(0x64646464u, wx, 0x04010400u)) - bias) * s2;
+  hi = (as_h2(__builtin_amdgcn_perm(0x64646464u, wx, 0x04030402u)) - bias) * s2;
+}
+
+// Eight INT4 codes of `w` (nibble i = k i, biased by 8) times the scale, as one MFMA operand in
+// the k order (0,4,1,5,2,6,3,7): nibbles i and i + 4 sit 16 bits apart, so one mask per pair.
+__device__ __forceinline__ h8 deq_i4_word_perm(uint32_t w, h2 s2) {
+  const h2 bias = {_Float16(1032.f), _Float16(1032.f)};
+  const h2 p0 = (as_h2((w & 0x000F000Fu) | 0x64006400u) - bias) * s2;
+  const h2 p1 = (as_h2(((w >> 4) & 0x000F000Fu) | 0x64006400u) - bias) * s2;
+  const h2 p2 = (as_h2(((w >> 8) & 0x000F000Fu) | 0x64006400u) - bias) * s2;
+  const h2 p3 = (as_h2(((w >> 12) & 0x000F000Fu) | 0x64006400u) - bias) * s2;
+  return pack_h8(p0, p1, p2, p3);
+}
+
+// Eight INT4 codes of `w` times the scale in natural k order (0..7), as four fp16 pairs.
+__device__ __forceinline__ void deq_i4_word(uint32_t w, h2 s2, h2 (&p)[4]) {
+  const h2 bias = {_Float16(1032.f), _Float16(1032.f)};
+  const uint32_t lo = w & 0x0F0F0F0Fu;         // k 0, 2, 4, 6 in bytes 0..3
+  const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;  // k 1, 3, 5, 7
+  // byte 0 <- lo.b_i (k 2i), byte 2 <- hi.b_i (k 2i+1); bytes 1 and 3 <- 0 (selector 0x0c).
+  p[0] = (as_h2(__builtin_amdgcn_perm(hi, lo, 0x0C040C00u) | 0x64006400u) - bias) * s2;
+  p[1] = (as_h2(__builtin_amdgcn_perm(hi, lo, 0x0C050C01u) | 0x64006400u) - bias) * s2;
+  p[2] = (as_h2(__builtin_amdgcn_perm(hi, lo, 0x0C060C02u) | 0x64006400u) - bias) * s2;
+  p[3] = (as_h2(__builtin_amdgcn_perm(hi, lo, 0x0C070C03u) | 0x64006400u) - bias) * s2;
+}
+
+// Activations x0..x7 (16 bytes) reordered to (0,4,1,5,2,6,3,7), matching deq_i4_word_perm.
+__device__ __forceinline__ h8 perm_x_i4(uint4 d) {
+  const uint32_t e0 = __builtin_amdgcn_perm(d.z, d.x, 0x05040100u);
+  const uint32_t e1 = __builtin_amdgcn_perm(d.z, d.x, 0x07060302u);
+  const uint32_t e2 = __builtin_amdgcn_perm(d.w, d.y, 0x05040100u);
+  const uint32_t e3 = __builtin_amdgcn_perm(d.w, d.y, 0x07060302u);
+  return pack_h8(as_h2(e0), as_h2(e1), as_h2(e2), as_h2(e3));
+}
+
+__device__ __forceinline__ uint4 ldg16(const void* p) {
+  return *reinterpret_cast<const uint4*>(p);
+}
+
+// ---- skinny kernel (M <= 32) ----------------------------------------------------------------
+constexpr int kMaxSkinnyWaves = 8;
+
+template <int BITS>
+struct SkinnyCfg {
+  static constexpr int KB = BITS == 8 ? 64 : 128;  // k covered by one 16-byte load per lane
+  static constexpr int STEPS = BITS == 8 ? 2 : 4;  // MFMA k-steps (8 k per lane) per load
+};
+
+template <int BITS, int NT, int MT, int U>
+struct SkinnyBatch {
+  uint4 w[U][NT];
+  f16 s[U][NT];
+  h8 x[U][MT][SkinnyCfg<BITS>::STEPS];
+};
+
+// Issue the loads of U consecutive 64-byte row chunks (one per lane group) for NT row tiles and
+// the matching activations of MT 16-row tiles.
+template <int BITS, int NT, int MT, int U>
+__device__ __forceinline__ void skinny_load(SkinnyBatch<BITS, NT, MT, U>& b, int kb,
+                                            const uint8_t* const (&wp)[NT],
+                                            const f16* const (&sp)[NT], bool per_group, int g,
+                                            const f16* const (&xp)[MT], const bool (&xv)[MT],
+                                            int lg) {
+  using C = SkinnyCfg<BITS>;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int kk = kb + u;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      b.w[u][t] = ldg16(wp[t] + int64_t(kk) * 64);
+      if (per_group) b.s[u][t] = sp[t][(kk * C::KB + lg * (C::KB / 4)) / g];
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const f16* xk = xp[mt] + int64_t(kk) * C::KB;
+#pragma unroll
+      for (int st = 0; st < C::STEPS; ++st) {
+        if (xv[mt]) {
+          const uint4 raw = ldg16(xk + 8 * st);
+          b.x[u][mt][st] = BITS == 8 ? __builtin_bit_cast(h8, raw) : perm_x_i4(raw);
+        } else {
+          b.x[u][mt][st] = h8{};
+        }
+      }
+    }
+  }
+}
+
+template <int BITS, int NT, int MT, int U>
+__device__ __forceinline__ void skinny_compute(const SkinnyBatch<BITS, NT, MT, U>& b,
+                                               bool per_group, const f16 (&s_row)[NT],
+                                               f32x4 (&acc)[NT][MT]) {
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const f16 sc = per_group ? b.s[u][t] : s_row[t];
+      const _Float16 s1 = __builtin_bit_cast(_Float16, sc);
+      const h2 s2 = {s1, s1};
+      const uint32_t words[4] = {b.w[u][t].x, b.w[u][t].y, b.w[u][t].z, b.w[u][t].w};
+      if constexpr (BITS == 8) {
+        h2 p[8];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) deq_i8_word(words[q], s2, p[2 * q], p[2 * q + 1]);
+        const h8 a0 = pack_h8(p[0], p[1], p[2], p[3]);
+        const h8 a1 = pack_h8(p[4], p[5], p[6], p[7]);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          acc[t][mt] = mfma16(a0, b.x[u][mt][0], acc[t][mt]);
+          acc[t][mt] = mfma16(a1, b.x[u][mt][1], acc[t][mt]);
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const h8 a = deq_i4_word_perm(words[q], s2);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) acc[t][mt] = mfma16(a, b.x[u][mt][q], acc[t][mt]);
+        }
+      }
+    }
+  }
+}
+
+// One workgroup: 16*NT output rows, all M <= 16*MT activation rows, K split across its waves
+// (blockDim.x / 64 of them). Lane l feeds row l % 16 of a tile (A operand) and activation row
+// l % 16 of an m-tile (B operand); lane group l / 16 owns bytes [16 (l/16), +16) of every 64-byte
+// row chunk.
+template <int BITS, int NT, int MT, int U>
+__global__ __launch_bounds__(kMaxSkinnyWaves * kWave) void qlinear_skinny_kernel(
+    const f16* __restrict__ x, int64_t xs, int32_t m, int32_t k,
+    const uint8_t* __restrict__ packed, const f16* __restrict__ scales,
+    const f16* __restrict__ bias, int32_t n, int32_t g, f16* __restrict__ y, int64_t ys) {
+  using C = SkinnyCfg<BITS>;
+  __shared__ float red[kMaxSkinnyWaves * NT * MT * 4 * kWave];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int kw = blockDim.x >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const int nkb = k / C::KB;
+  const int per = (nkb + kw - 1) / kw;
+  const int kb0 = min(nkb, wave * per), kb1 = min(nkb, kb0 + per);
+  const int64_t row_bytes = BITS == 8 ? k : k / 2;
+  const int groups = k / g;
+  const bool per_group = groups > 1;
+  const int n0 = blockIdx.x * 16 * NT;
+
+  const uint8_t* wp[NT];
+  const f16* sp[NT];
+  f16 s_row[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int row = min(n0 + 16 * t + li, n - 1);  // rows past N compute garbage, never stored
+    wp[t] = packed + int64_t(row) * row_bytes + 16 * lg;
+    sp[t] = scales + int64_t(row) * groups;
+    s_row[t] = sp[t][0];
+  }
+  const f16* xp[MT];
+  bool xv[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int mrow = 16 * mt + li;
+    xv[mt] = mrow < m;
+    xp[mt] = x + int64_t(xv[mt] ? mrow : 0) * xs + lg * (C::KB / 4);
+  }
+
+  f32x4 acc[NT][MT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[t][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  int kb = kb0;
+  for (; kb + U <= kb1; kb += U) {
+    SkinnyBatch<BITS, NT, MT, U> b;
+    skinny_load<BITS, NT, MT, U>(b, kb, wp, sp, per_group, g, xp, xv, lg);
+    skinny_compute<BITS, NT, MT, U>(b, per_group, s_row, acc);
+  }
+  for (; kb < kb1; ++kb) {
+    SkinnyBatch<BITS, NT, MT, 1> b;
+    skinny_load<BITS, NT, MT, 1>(b, kb, wp, sp, per_group, g, xp, xv, lg);
+    skinny_compute<BITS, NT, MT, 1>(b, per_group, s_row, acc);
+  }
+
+  // Sum the waves' partials in wave order (deterministic), then write y[m][n] (+ bias).
+  constexpr int kVals = NT * MT * 4;
+  constexpr int kElems = kVals * kWave;
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        red[(wave * kVals + (t * MT + mt) * 4 + r) * kWave + lane] = acc[t][mt][r];
+  __syncthreads();
+  for (int e = threadIdx.x; e < kElems; e += blockDim.x) {
+    const int l = e & 63, v = e >> 6;
+    const int r = v & 3, mt = (v >> 2) % MT, t = (v >> 2) / MT;
+    const int nrow = n0 + 16 * t + 4 * (l >> 4) + r;
+    const int mrow = 16 * mt + (l & 15);
+    if (nrow >= n || mrow >= m) continue;
+    float sum = 0.f;
+    for (int w = 0; w < kw; ++w) sum += red[w * kElems + e];
+    const float bv = bias != nullptr ? __half2float(bias[nrow]) : 0.f;
+    y[int64_t(mrow) * ys + nrow] = __float2half_rn(sum + bv);
+  }
+}
+
+// ---- tiled GEMM (M > 32) --------------------------------------------------------------------
+constexpr int kGemmThreads = 256;
+constexpr int kBK = 64;     // k per LDS stage
+constexpr int kLdsRow = 64;  // halves per LDS row (one row of a 64-k stage)
+
+// Halves offset of 16-byte chunk `c` (0..7) of LDS row `row`, chunk index XOR-swizzled by the row
+// so that 32 lanes reading one chunk column of 32 rows hit distinct banks.
+__device__ __forceinline__ int lds_off(int row, int c) { return row * kLdsRow + ((c ^ (row & 7)) << 3); }
+
+template <int BITS, int BN, int BM>
+struct GemmCfg {
+  static constexpr int W_ROW_BYTES = BITS == 8 ? kBK : kBK / 2;    // packed bytes per row, per stage
+  static constexpr int W_BPT = BN * W_ROW_BYTES / kGemmThreads;     // packed bytes per thread
+  static constexpr int W_TPR = W_ROW_BYTES / W_BPT;                 // threads per weight row
+  static constexpr int W_K = BITS == 8 ? W_BPT : 2 * W_BPT;         // k per thread (16 or 32)
+  static constexpr int X_BPT = BM * kBK * 2 / kGemmThreads;         // activation bytes per thread
+  static constexpr int X_TPR = kBK * 2 / X_BPT;                     // threads per activation row
+  static constexpr int TN = BN / 64, TM = BM / 64;                  // 32x32 tiles per wave
+  static_assert(W_BPT == 8 || W_BPT == 16 || W_BPT == 32, "weight staging split");
+  static_assert(X_BPT == 32 || X_BPT == 64, "activation staging split");
+};
+
+template <int BITS, int BN, int BM>
+struct GemmStage {
+  uint32_t w[GemmCfg<BITS, BN, BM>::W_BPT / 4];
+  f16 s;
+  uint4 x[GemmCfg<BITS, BN, BM>::X_BPT / 16];
+};
+
+// Loads one 64-k stage of this thread's weight segment (and its group scale) and activation
+// segment into registers.
+template <int BITS, int BN, int BM>
+__device__ __forceinline__ void gemm_load(GemmStage<BITS, BN, BM>& st, int k0, const uint8_t* wrow,
+                                          const f16* srow, int g, int wk_off, const f16* xrow,
+                                          bool xvalid) {
+  using C = GemmCfg<BITS, BN, BM>;
+  const uint8_t* wp = wrow + (BITS == 8 ? k0 : k0 / 2);
+  if constexpr (C::W_BPT == 8) {
+    const uint2 v = *reinterpret_cast<const uint2*>(wp);
+    st.w[0] = v.x;
+    st.w[1] = v.y;
+  } else {
+#pragma unroll
+    for (int i = 0; i < C::W_BPT / 16; ++i) {
+      const uint4 v = ldg16(wp + 16 * i);
+      st.w[4 * i] = v.x;
+      st.w[4 * i + 1] = v.y;
+      st.w[4 * i + 2] = v.z;
+      st.w[4 * i + 3] = v.w;
+    }
+  }
+  // A segment never straddles a group: it is 16 or 32 k, aligned, and g % 32 == 0.
+  st.s = srow[(k0 + wk_off) / g];
+#pragma unroll
+  for (int i = 0; i < C::X_BPT / 16; ++i)
+    st.x[i] = xvalid ? ldg16(xrow + k0 + 8 * i) : uint4{0, 0, 0, 0};
+}
+
+template <int BITS, int BN, int BM>
+__device__ __forceinline__ void gemm_store(const GemmStage<BITS, BN, BM>& st, _Float16* sw,
+                                           _Float16* sx, int wr, int wc0, int xr, int xc0) {
+  using C = GemmCfg<BITS, BN, BM>;
+  const _Float16 s1 = __builtin_bit_cast(_Float16, st.s);
+  const h2 s2 = {s1, s1};
+  // Dequantised weights: W_K halves = W_K / 8 chunks starting at chunk wc0.
+  if constexpr (BITS == 8) {
+#pragma unroll
+    for (int c = 0; c < C::W_K / 8; ++c) {
+      h2 p[4];
+      deq_i8_word(st.w[2 * c], s2, p[0], p[1]);
+      deq_i8_word(st.w[2 * c + 1], s2, p[2], p[3]);
+      *reinterpret_cast<h8*>(sw + lds_off(wr, wc0 + c)) = pack_h8(p[0], p[1], p[2], p[3]);
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < C::W_K / 8; ++c) {
+      h2 p[4];
+      deq_i4_word(st.w[c], s2, p);
+      *reinterpret_cast<h8*>(sw + lds_off(wr, wc0 + c)) = pack_h8(p[0], p[1], p[2], p[3]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < C::X_BPT / 16; ++i)
+    *reinterpret_cast<uint4*>(sx + lds_off(xr, xc0 + i)) = st.x[i];
+}
+
+// y[M, N] = x . W^T for one BN x BM tile of y^T. Waves form a 2 x 2 grid; wave (wn, wm) owns
+// rows [wn BN/2, +BN/2) of the weight tile and [wm BM/2, +BM/2) of the activation tile, as
+// TN x TM 32x32 MFMA tiles. Operand lane layout of v_mfma_f32_32x32x16_f16: lane l reads row
+// l % 32, k chunk 2 ks + l / 32 of a 16-k step; accumulator register i of lane l holds
+// row 8 (i / 4) + 4 (l / 32) + i % 4 of A (weight row) and column l % 32 (activation row).
+template <int BITS, int BN, int BM>
+__global__ __launch_bounds__(kGemmThreads) void qlinear_gemm_kernel(
+    const f16* __restrict__ x, int64_t xs, int32_t m, int32_t k,
+    const uint8_t* __restrict__ packed, const f16* __restrict__ scales,
+    const f16* __restrict__ bias, int32_t n, int32_t g, f16* __restrict__ y, int64_t ys) {
+  using C = GemmCfg<BITS, BN, BM>;
+  __shared__ __attribute__((aligned(16))) _Float16 sw[2][BN * kLdsRow];
+  __shared__ __attribute__((aligned(16))) _Float16 sx[2][BM * kLdsRow];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wn = wave & 1, wm = wave >> 1;
+  const int nb = blockIdx.x * BN, mb = blockIdx.y * BM;
+  const int64_t row_bytes = BITS == 8 ? k : k / 2;
+  const int groups = k / g;
+
+  // Staging roles: weight row wr (segment wseg), activation row xr (segment xseg).
+  const int wr = tid / C::W_TPR, wseg = tid % C::W_TPR;
+  const int xr = tid / C::X_TPR, xseg = tid % C::X_TPR;
+  const int wrow_g = min(nb + wr, n - 1);
+  const uint8_t* wrow = packed + int64_t(wrow_g) * row_bytes + wseg * C::W_BPT;
+  const f16* srow = scales + int64_t(wrow_g) * groups;
+  const int wk_off = wseg * C::W_K;  // k offset of this thread's weight segment in a stage
+  const bool xvalid = mb + xr < m;
+  const f16* xrow = x + int64_t(xvalid ? mb + xr : 0) * xs + xseg * (C::X_BPT / 2);
+  const int wc0 = wk_off / 8, xc0 = xseg * (C::X_BPT / 16);
+
+  f32x16 acc[C::TN][C::TM];
+#pragma unroll
+  for (int i = 0; i < C::TN; ++i)
+#pragma unroll
+    for (int j = 0; j < C::TM; ++j) acc[i][j] = f32x16{};
+
+  const int nk = k / kBK;
+  GemmStage<BITS, BN, BM> st;
+  // The scale index uses the segment's first k; a segment never straddles a group (g % 32 == 0).
+  gemm_load<BITS, BN, BM>(st, 0, wrow, srow, g, wk_off, xrow, xvalid);
+  const int col = lane & 31, half = lane >> 5;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    gemm_store<BITS, BN, BM>(st, sw[buf], sx[buf], wr, wc0, xr, xc0);
+    __syncthreads();
+    if (kt + 1 < nk) gemm_load<BITS, BN, BM>(st, (kt + 1) * kBK, wrow, srow, g, wk_off, xrow, xvalid);
+    const _Float16* swb = sw[buf];
+    const _Float16* sxb = sx[buf];
+#pragma unroll
+    for (int ks = 0; ks < kBK / 16; ++ks) {
+      h8 a[C::TN], b[C::TM];
+#pragma unroll
+      for (int i = 0; i < C::TN; ++i)
+        a[i] = *reinterpret_cast<const h8*>(swb + lds_off(wn * (BN / 2) + 32 * i + col, 2 * ks + half));
+#pragma unroll
+      for (int j = 0; j < C::TM; ++j)
+        b[j] = *reinterpret_cast<const h8*>(sxb + lds_off(wm * (BM / 2) + 32 * j + col, 2 * ks + half));
+#pragma unroll
+      for (int i = 0; i < C::TN; ++i)
+#pragma unroll
+        for (int j = 0; j < C::TM; ++j) acc[i][j] = mfma32(a[i], b[j], acc[i][j]);
+    }
+  }
+
+  // Epilogue: register r of tile (i, j) is y[mrow][nrow] with 4 consecutive nrow per r / 4.
+#pragma unroll
+  for (int i = 0; i < C::TN; ++i) {
+#pragma unroll
+    for (int j = 0; j < C::TM; ++j) {
+      const int mrow = mb + wm * (BM / 2) + 32 * j + col;
+      if (mrow >= m) continue;
+      f16* yr = y + int64_t(mrow) * ys;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int nrow = nb + wn * (BN / 2) + 32 * i + 8 * q + 4 * half;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if (nrow + r < n) {
+            const float bv = bias != nullptr ? __half2float(bias[nrow + r]) : 0.f;
+            yr[nrow + r] = __float2half_rn(acc[i][j][4 * q + r] + bv);
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int BITS, int NT, int MT>
+void launch_skinny(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
+                   const f16* scales, const f16* bias, int32_t n, int32_t g, f16* y, int64_t ys,
+                   int kw, hipStream_t s) {
+  constexpr int U = BITS == 8 ? 4 : 2;
+  const unsigned blocks = unsigned((n + 16 * NT - 1) / (16 * NT));
+  hipLaunchKernelGGL((qlinear_skinny_kernel<BITS, NT, MT, U>), dim3(blocks), dim3(kw * kWave), 0,
+                     s, x, xs, m, k, packed, scales, bias, n, g, y, ys);
+}
+
+template <int BITS, int BN, int BM>
+void launch_gemm(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
+                 const f16* scales, const f16* bias, int32_t n, int32_t g, f16* y, int64_t ys,
+                 hipStream_t s) {
+  const dim3 grid(unsigned((n + BN - 1) / BN), unsigned((m + BM - 1) / BM));
+  hipLaunchKernelGGL((qlinear_gemm_kernel<BITS, BN, BM>), grid, dim3(kGemmThreads), 0, s, x, xs,
+                     m, k, packed, scales, bias, n, g, y, ys);
+}
+
+template <int BITS>
+void dispatch(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
+              const f16* scales, const f16* bias, int32_t n, int32_t g, f16* y, int64_t ys,
+              hipStream_t s) {
+  if (m <= EDGERAG_SKINNY_MAX_M) {
+    // Waves per workgroup split K; chosen from K alone, so a row's summation order (and so its
+    // bits) does not depend on N or on which other rows share the launch.
+    const int nkb = k / SkinnyCfg<BITS>::KB;
+    int kw = 1;
+    while (kw < kMaxSkinnyWaves && nkb / (2 * kw) >= 2) kw *= 2;
+    const bool wide = (n + 31) / 32 >= 256;  // enough workgroups with 32 rows each
+    if (m <= 16) {
+      if (wide) launch_skinny<BITS, 2, 1>(x, xs, m, k, packed, scales, bias, n, g, y, ys, kw, s);
+      else launch_skinny<BITS, 1, 1>(x, xs, m, k, packed, scales, bias, n, g, y, ys, kw, s);
+    } else {
+      if (wide) launch_skinny<BITS, 2, 2>(x, xs, m, k, packed, scales, bias, n, g, y, ys, kw, s);
+      else launch_skinny<BITS, 1, 2>(x, xs, m, k, packed, scales, bias, n, g, y, ys, kw, s);
+    }
+    return;
+  }
+  // Tiles: the largest whose grid still covers the 256 CUs.
+  const int64_t t128 = int64_t((n + 127) / 128) * ((m + 127) / 128);
+  const int64_t t128x64 = int64_t((n + 127) / 128) * ((m + 63) / 64);
+  if (t128 >= 256)
+    launch_gemm<BITS, 128, 128>(x, xs, m, k, packed, scales, bias, n, g, y, ys, s);
+  else if (t128x64 >= 256)
+    launch_gemm<BITS, 128, 64>(x, xs, m, k, packed, scales, bias, n, g, y, ys, s);
+  else
+    launch_gemm<BITS, 64, 64>(x, xs, m, k, packed, scales, bias, n, g, y, ys, s);
+}
+
+}  // namespace
+
+bool qlinear_mfma_supported(int32_t k, int32_t bits, int32_t g, const void* x, int64_t x_stride,
+                            const void* packed) {
+  const int kb = bits == 8 ? 64 : 128;
+  return (bits == 8 || bits == 4) && k % kb == 0 && g % 32 == 0 && aligned16(x) &&
+         aligned16(packed) && (x_stride * 2) % 16 == 0;
+}
+
+void launch_qlinear_mfma(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
+                         const f16* scales, const f16* bias, int32_t n, int32_t bits, int32_t g,
+                         f16* y, int64_t ys, hipStream_t s) {
+  if (bits == 8)
+    dispatch<8>(x, xs, m, k, packed, scales, bias, n, g, y, ys, s);
+  else
+    dispatch<4>(x, xs, m, k, packed, scales, bias, n, g, y, ys, s);
+}
+
+}  // namespace edgerag

@@ -144,3 +144,20 @@ def test_fused_concat_equals_separate_layers(device) -> None:
     fused = QuantLinear.concat(layers)
     x = torch.randn(5, 256, generator=seeded(9)).half().to(device)
     assert torch.equal(fused(x), torch.cat([layer(x) for layer in layers], dim=-1))
+
+
+@pytest.mark.parametrize("bits,k,g", [(8, 256, 256), (8, 512, 64), (4, 256, 128), (4, 1152, 32)])
+@pytest.mark.parametrize("m", [1, 2, 5, 16, 17, 31, 32, 33, 63, 64, 65, 100, 130])
+def test_quant_linear_mfma_edges(device, bits, k, g, m) -> None:
+    """Both MFMA paths (M <= 32 streaming, M > 32 tiled) on ragged M, N not a multiple of any
+    tile (37, 200), bias, and K / group sizes that exercise per-group scales."""
+    for n in (37, 200):
+        w = _weight(n, k, n * 3 + k + bits)
+        cfg = oq.QuantConfig(g, bits)
+        packed, scales = oq.quantize_for_layer(w, cfg)
+        bias = (torch.randn(n, generator=seeded(n + m)) * 0.1).half()
+        x = torch.randn(m, k, generator=seeded(m * 11 + n)).half()
+        expected = oq.quant_linear_reference(x, packed, scales, bias, k, cfg)
+        y = kernels.quant_linear(x.to(device), packed.to(device), scales.to(device),
+                                 bias.to(device), k, n, bits, g)
+        torch.testing.assert_close(y.float().cpu(), expected, **LINEAR_TOL)
