@@ -7,22 +7,22 @@
 // v_mfma_f32_*_f16 with fp32 accumulation, as F.linear does on fp16 tensors
 // (edgerag/core/linear.py:194-196). The fp16 weight matrix is never written to memory.
 //
-// * qlinear_skinny_kernel (M <= 32, the decode GEMVs): HBM-bound. A wave owns 16 or 32 output
+// * qlinear_skinny_kernel (M <= 64, the decode GEMVs): HBM-bound. A wave owns 16 or 32 output
 //   rows and one K chunk; every lane streams 16 bytes of packed weights per load (4 lanes cover
 //   64 contiguous bytes of a row), U loads deep, and feeds them to v_mfma_f32_16x16x32_f16 as the
-//   A operand straight from registers (no LDS). The activations (B operand, up to 32 rows) come
+//   A operand straight from registers (no LDS). The activations (B operand, up to 64 rows) come
 //   from L2. The waves of a workgroup split K; their partial sums are added in LDS in a fixed order.
 //   Only the lane-to-k assignment inside a k-step differs from textbook order, identically for
 //   both operands: INT4 nibbles decode to the k order (0,4,1,5,2,6,3,7), so the activations are
 //   permuted the same way in registers.
-// * qlinear_gemm_kernel (M > 32, prefill slices): MFMA-bound. A 256-thread workgroup computes a
+// * qlinear_gemm_kernel (M > 64, prefill slices): MFMA-bound. A 256-thread workgroup computes a
 //   BN x BM tile of y^T through v_mfma_f32_32x32x16_f16; per 64-k step it stages the dequantised
 //   weights and the activations in double-buffered, XOR-swizzled LDS, loading the next step's
 //   bytes from global memory while the current one is computed.
 #include "quant_mfma.h"
 
 #ifndef EDGERAG_SKINNY_MAX_M
-#define EDGERAG_SKINNY_MAX_M 32
+#define EDGERAG_SKINNY_MAX_M 64
 #endif
 
 namespace edgerag {
@@ -93,7 +93,11 @@ __device__ __forceinline__ uint4 ldg16(const void* p) {
   return *reinterpret_cast<const uint4*>(p);
 }
 
-// ---- skinny kernel (M <= 32) ----------------------------------------------------------------
+// Compiler-only fence: keeps the loads issued above it from being sunk below it (next to their
+// first use), which would serialise memory latency with the compute they are meant to overlap.
+__device__ __forceinline__ void issue_fence() { asm volatile("" ::: "memory"); }
+
+// ---- skinny kernel (M <= 64) ----------------------------------------------------------------
 constexpr int kMaxSkinnyWaves = 8;
 
 template <int BITS>
@@ -105,53 +109,65 @@ struct SkinnyCfg {
 template <int BITS, int NT, int MT, int U>
 struct SkinnyBatch {
   uint4 w[U][NT];
-  f16 s[U][NT];
-  h8 x[U][MT][SkinnyCfg<BITS>::STEPS];
+  uint32_t s[U][NT];  // raw fp16 scale bits (a plain integer keeps it in a register)
+  uint4 x[U][MT][SkinnyCfg<BITS>::STEPS];  // raw activations; masked and permuted when used
 };
 
 // Issue the loads of U consecutive 64-byte row chunks (one per lane group) for NT row tiles and
-// the matching activations of MT 16-row tiles.
-template <int BITS, int NT, int MT, int U>
-__device__ __forceinline__ void skinny_load(SkinnyBatch<BITS, NT, MT, U>& b, int kb,
+// the matching activations of MT 16-row tiles. Every load is unconditional (chunk indices are
+// clamped into the row, activation rows into [0, M)) so that no value is selected right after its
+// load, which would make the wave wait for it; the masks are applied in skinny_compute.
+template <int BITS, int NT, int MT, int U, bool PG>
+__device__ __forceinline__ void skinny_load(SkinnyBatch<BITS, NT, MT, U>& b, int kb, int nkb,
                                             const uint8_t* const (&wp)[NT],
-                                            const f16* const (&sp)[NT], bool per_group, int g,
+                                            const f16* const (&sp)[NT], int g,
                                             const f16* const (&xp)[MT], const bool (&xv)[MT],
                                             int lg) {
   using C = SkinnyCfg<BITS>;
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const int kk = kb + u;
+    const int kk = min(kb + u, nkb - 1);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       b.w[u][t] = ldg16(wp[t] + int64_t(kk) * 64);
-      if (per_group) b.s[u][t] = sp[t][(kk * C::KB + lg * (C::KB / 4)) / g];
+      if constexpr (PG)
+        b.s[u][t] = reinterpret_cast<const uint16_t*>(sp[t])[(kk * C::KB + lg * (C::KB / 4)) / g];
     }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      const f16* xk = xp[mt] + int64_t(kk) * C::KB;
+      // Only lanes of real activation rows load (exec-masked); the others' registers are
+      // ignored by skinny_compute.
+      if (xv[mt]) {
+        const f16* xk = xp[mt] + int64_t(kk) * C::KB;
 #pragma unroll
-      for (int st = 0; st < C::STEPS; ++st) {
-        if (xv[mt]) {
-          const uint4 raw = ldg16(xk + 8 * st);
-          b.x[u][mt][st] = BITS == 8 ? __builtin_bit_cast(h8, raw) : perm_x_i4(raw);
-        } else {
-          b.x[u][mt][st] = h8{};
-        }
+        for (int st = 0; st < C::STEPS; ++st) b.x[u][mt][st] = ldg16(xk + 8 * st);
       }
     }
   }
 }
 
-template <int BITS, int NT, int MT, int U>
-__device__ __forceinline__ void skinny_compute(const SkinnyBatch<BITS, NT, MT, U>& b,
-                                               bool per_group, const f16 (&s_row)[NT],
+// Chunks kb + u at or past kb_end (the end of this wave's K range) and activation rows past M
+// contribute zero activations, so their MFMAs add exact zeros.
+template <int BITS, int NT, int MT, int U, bool PG>
+__device__ __forceinline__ void skinny_compute(const SkinnyBatch<BITS, NT, MT, U>& b, int kb,
+                                               int kb_end, const bool (&xv)[MT],
+                                               const uint32_t (&s_row)[NT],
                                                f32x4 (&acc)[NT][MT]) {
 #pragma unroll
   for (int u = 0; u < U; ++u) {
+    const bool on = kb + u < kb_end;
+    h8 xo[MT][SkinnyCfg<BITS>::STEPS];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int st = 0; st < SkinnyCfg<BITS>::STEPS; ++st) {
+        const uint4 raw = (on && xv[mt]) ? b.x[u][mt][st] : uint4{0, 0, 0, 0};
+        xo[mt][st] = BITS == 8 ? __builtin_bit_cast(h8, raw) : perm_x_i4(raw);
+      }
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const f16 sc = per_group ? b.s[u][t] : s_row[t];
-      const _Float16 s1 = __builtin_bit_cast(_Float16, sc);
+      const _Float16 s1 =
+          __builtin_bit_cast(_Float16, uint16_t(PG ? b.s[u][t] : s_row[t]));
       const h2 s2 = {s1, s1};
       const uint32_t words[4] = {b.w[u][t].x, b.w[u][t].y, b.w[u][t].z, b.w[u][t].w};
       if constexpr (BITS == 8) {
@@ -162,15 +178,15 @@ __device__ __forceinline__ void skinny_compute(const SkinnyBatch<BITS, NT, MT, U
         const h8 a1 = pack_h8(p[4], p[5], p[6], p[7]);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          acc[t][mt] = mfma16(a0, b.x[u][mt][0], acc[t][mt]);
-          acc[t][mt] = mfma16(a1, b.x[u][mt][1], acc[t][mt]);
+          acc[t][mt] = mfma16(a0, xo[mt][0], acc[t][mt]);
+          acc[t][mt] = mfma16(a1, xo[mt][1], acc[t][mt]);
         }
       } else {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const h8 a = deq_i4_word_perm(words[q], s2);
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt) acc[t][mt] = mfma16(a, b.x[u][mt][q], acc[t][mt]);
+          for (int mt = 0; mt < MT; ++mt) acc[t][mt] = mfma16(a, xo[mt][q], acc[t][mt]);
         }
       }
     }
@@ -181,7 +197,7 @@ __device__ __forceinline__ void skinny_compute(const SkinnyBatch<BITS, NT, MT, U
 // (blockDim.x / 64 of them). Lane l feeds row l % 16 of a tile (A operand) and activation row
 // l % 16 of an m-tile (B operand); lane group l / 16 owns bytes [16 (l/16), +16) of every 64-byte
 // row chunk.
-template <int BITS, int NT, int MT, int U>
+template <int BITS, int NT, int MT, int U, int NB, bool PG>
 __global__ __launch_bounds__(kMaxSkinnyWaves * kWave) void qlinear_skinny_kernel(
     const f16* __restrict__ x, int64_t xs, int32_t m, int32_t k,
     const uint8_t* __restrict__ packed, const f16* __restrict__ scales,
@@ -196,18 +212,17 @@ __global__ __launch_bounds__(kMaxSkinnyWaves * kWave) void qlinear_skinny_kernel
   const int kb0 = min(nkb, wave * per), kb1 = min(nkb, kb0 + per);
   const int64_t row_bytes = BITS == 8 ? k : k / 2;
   const int groups = k / g;
-  const bool per_group = groups > 1;
   const int n0 = blockIdx.x * 16 * NT;
 
   const uint8_t* wp[NT];
   const f16* sp[NT];
-  f16 s_row[NT];
+  uint32_t s_row[NT];  // raw bits of the row's only scale when PG is false (one group spans K)
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     const int row = min(n0 + 16 * t + li, n - 1);  // rows past N compute garbage, never stored
     wp[t] = packed + int64_t(row) * row_bytes + 16 * lg;
     sp[t] = scales + int64_t(row) * groups;
-    s_row[t] = sp[t][0];
+    s_row[t] = PG ? 0u : reinterpret_cast<const uint16_t*>(sp[t])[0];
   }
   const f16* xp[MT];
   bool xv[MT];
@@ -215,7 +230,7 @@ __global__ __launch_bounds__(kMaxSkinnyWaves * kWave) void qlinear_skinny_kernel
   for (int mt = 0; mt < MT; ++mt) {
     const int mrow = 16 * mt + li;
     xv[mt] = mrow < m;
-    xp[mt] = x + int64_t(xv[mt] ? mrow : 0) * xs + lg * (C::KB / 4);
+    xp[mt] = x + int64_t(xv[mt] ? mrow : m - 1) * xs + lg * (C::KB / 4);
   }
 
   f32x4 acc[NT][MT];
@@ -224,16 +239,18 @@ __global__ __launch_bounds__(kMaxSkinnyWaves * kWave) void qlinear_skinny_kernel
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[t][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  int kb = kb0;
-  for (; kb + U <= kb1; kb += U) {
-    SkinnyBatch<BITS, NT, MT, U> b;
-    skinny_load<BITS, NT, MT, U>(b, kb, wp, sp, per_group, g, xp, xv, lg);
-    skinny_compute<BITS, NT, MT, U>(b, per_group, s_row, acc);
-  }
-  for (; kb < kb1; ++kb) {
-    SkinnyBatch<BITS, NT, MT, 1> b;
-    skinny_load<BITS, NT, MT, 1>(b, kb, wp, sp, per_group, g, xp, xv, lg);
-    skinny_compute<BITS, NT, MT, 1>(b, per_group, s_row, acc);
+  // Super-batches of NB x U chunks: every load of a super-batch is issued before any of its
+  // chunks is computed, so a wave pays one memory round trip per super-batch. The host sizes
+  // the K split so that most waves need a single super-batch.
+  for (int kb = kb0; kb < kb1; kb += NB * U) {
+    SkinnyBatch<BITS, NT, MT, U> b[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+      skinny_load<BITS, NT, MT, U, PG>(b[i], kb + i * U, nkb, wp, sp, g, xp, xv, lg);
+    issue_fence();
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+      skinny_compute<BITS, NT, MT, U, PG>(b[i], kb + i * U, kb1, xv, s_row, acc);
   }
 
   // Sum the waves' partials in wave order (deterministic), then write y[m][n] (+ bias).
@@ -260,7 +277,7 @@ __global__ __launch_bounds__(kMaxSkinnyWaves * kWave) void qlinear_skinny_kernel
   }
 }
 
-// ---- tiled GEMM (M > 32) --------------------------------------------------------------------
+// ---- tiled GEMM (M > 64) --------------------------------------------------------------------
 constexpr int kGemmThreads = 256;
 constexpr int kBK = 64;     // k per LDS stage
 constexpr int kLdsRow = 64;  // halves per LDS row (one row of a 64-k stage)
@@ -293,8 +310,7 @@ struct GemmStage {
 // segment into registers.
 template <int BITS, int BN, int BM>
 __device__ __forceinline__ void gemm_load(GemmStage<BITS, BN, BM>& st, int k0, const uint8_t* wrow,
-                                          const f16* srow, int g, int wk_off, const f16* xrow,
-                                          bool xvalid) {
+                                          const f16* srow, int g, int wk_off, const f16* xrow) {
   using C = GemmCfg<BITS, BN, BM>;
   const uint8_t* wp = wrow + (BITS == 8 ? k0 : k0 / 2);
   if constexpr (C::W_BPT == 8) {
@@ -314,13 +330,13 @@ __device__ __forceinline__ void gemm_load(GemmStage<BITS, BN, BM>& st, int k0, c
   // A segment never straddles a group: it is 16 or 32 k, aligned, and g % 32 == 0.
   st.s = srow[(k0 + wk_off) / g];
 #pragma unroll
-  for (int i = 0; i < C::X_BPT / 16; ++i)
-    st.x[i] = xvalid ? ldg16(xrow + k0 + 8 * i) : uint4{0, 0, 0, 0};
+  for (int i = 0; i < C::X_BPT / 16; ++i) st.x[i] = ldg16(xrow + k0 + 8 * i);
 }
 
 template <int BITS, int BN, int BM>
 __device__ __forceinline__ void gemm_store(const GemmStage<BITS, BN, BM>& st, _Float16* sw,
-                                           _Float16* sx, int wr, int wc0, int xr, int xc0) {
+                                           _Float16* sx, int wr, int wc0, int xr, int xc0,
+                                           bool xvalid) {
   using C = GemmCfg<BITS, BN, BM>;
   const _Float16 s1 = __builtin_bit_cast(_Float16, st.s);
   const h2 s2 = {s1, s1};
@@ -341,9 +357,10 @@ __device__ __forceinline__ void gemm_store(const GemmStage<BITS, BN, BM>& st, _F
       *reinterpret_cast<h8*>(sw + lds_off(wr, wc0 + c)) = pack_h8(p[0], p[1], p[2], p[3]);
     }
   }
+  // Activation rows past M were loaded from row M - 1 (no branch at the load); stage zeros.
 #pragma unroll
   for (int i = 0; i < C::X_BPT / 16; ++i)
-    *reinterpret_cast<uint4*>(sx + lds_off(xr, xc0 + i)) = st.x[i];
+    *reinterpret_cast<uint4*>(sx + lds_off(xr, xc0 + i)) = xvalid ? st.x[i] : uint4{0, 0, 0, 0};
 }
 
 // y[M, N] = x . W^T for one BN x BM tile of y^T. Waves form a 2 x 2 grid; wave (wn, wm) owns
@@ -373,7 +390,7 @@ __global__ __launch_bounds__(kGemmThreads) void qlinear_gemm_kernel(
   const f16* srow = scales + int64_t(wrow_g) * groups;
   const int wk_off = wseg * C::W_K;  // k offset of this thread's weight segment in a stage
   const bool xvalid = mb + xr < m;
-  const f16* xrow = x + int64_t(xvalid ? mb + xr : 0) * xs + xseg * (C::X_BPT / 2);
+  const f16* xrow = x + int64_t(xvalid ? mb + xr : m - 1) * xs + xseg * (C::X_BPT / 2);
   const int wc0 = wk_off / 8, xc0 = xseg * (C::X_BPT / 16);
 
   f32x16 acc[C::TN][C::TM];
@@ -383,17 +400,9 @@ __global__ __launch_bounds__(kGemmThreads) void qlinear_gemm_kernel(
     for (int j = 0; j < C::TM; ++j) acc[i][j] = f32x16{};
 
   const int nk = k / kBK;
-  GemmStage<BITS, BN, BM> st;
-  // The scale index uses the segment's first k; a segment never straddles a group (g % 32 == 0).
-  gemm_load<BITS, BN, BM>(st, 0, wrow, srow, g, wk_off, xrow, xvalid);
   const int col = lane & 31, half = lane >> 5;
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    gemm_store<BITS, BN, BM>(st, sw[buf], sx[buf], wr, wc0, xr, xc0);
-    __syncthreads();
-    if (kt + 1 < nk) gemm_load<BITS, BN, BM>(st, (kt + 1) * kBK, wrow, srow, g, wk_off, xrow, xvalid);
-    const _Float16* swb = sw[buf];
-    const _Float16* sxb = sx[buf];
+  // One 64-k step on the staged LDS tiles.
+  auto compute = [&](const _Float16* swb, const _Float16* sxb) {
 #pragma unroll
     for (int ks = 0; ks < kBK / 16; ++ks) {
       h8 a[C::TN], b[C::TM];
@@ -408,9 +417,36 @@ __global__ __launch_bounds__(kGemmThreads) void qlinear_gemm_kernel(
 #pragma unroll
         for (int j = 0; j < C::TM; ++j) acc[i][j] = mfma32(a[i], b[j], acc[i][j]);
     }
+  };
+  // Register stages st0 / st1 hold steps kt and kt + 1; a step's global loads are issued two
+  // steps before it is stored to LDS, so each load has two compute steps to land. One barrier per
+  // step: LDS buffer kt & 1 is rewritten only after every wave has passed the barrier that follows
+  // its previous compute.
+  // Loads are unconditional (a step past the end reloads the last one) so that the compiler never
+  // has to wait for a load right after issuing it.
+  GemmStage<BITS, BN, BM> st0, st1;
+  const int last = (nk - 1) * kBK;
+  gemm_load<BITS, BN, BM>(st0, 0, wrow, srow, g, wk_off, xrow);
+  gemm_load<BITS, BN, BM>(st1, min(kBK, last), wrow, srow, g, wk_off, xrow);
+  issue_fence();
+  // Steps go in pairs with no early exit (an odd last step pairs with a zero step: its staged
+  // activations are zero), so the compiler cannot sink a step's loads behind a branch.
+  for (int kt = 0; kt < nk; kt += 2) {
+    gemm_store<BITS, BN, BM>(st0, sw[0], sx[0], wr, wc0, xr, xc0, xvalid);
+    __syncthreads();
+    gemm_load<BITS, BN, BM>(st0, min((kt + 2) * kBK, last), wrow, srow, g, wk_off, xrow);
+    issue_fence();
+    compute(sw[0], sx[0]);
+    gemm_store<BITS, BN, BM>(st1, sw[1], sx[1], wr, wc0, xr, xc0, xvalid && kt + 1 < nk);
+    __syncthreads();
+    gemm_load<BITS, BN, BM>(st1, min((kt + 3) * kBK, last), wrow, srow, g, wk_off, xrow);
+    issue_fence();
+    compute(sw[1], sx[1]);
   }
 
-  // Epilogue: register r of tile (i, j) is y[mrow][nrow] with 4 consecutive nrow per r / 4.
+  // Epilogue: register 4q + r of tile (i, j) is y[mrow][nrow + r], 4 consecutive outputs per q,
+  // stored as one 8-byte write when the row stride and the tile edge allow.
+  const bool vec_out = (ys % 4) == 0 && (reinterpret_cast<uintptr_t>(y) & 7) == 0;
 #pragma unroll
   for (int i = 0; i < C::TN; ++i) {
 #pragma unroll
@@ -421,26 +457,61 @@ __global__ __launch_bounds__(kGemmThreads) void qlinear_gemm_kernel(
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int nrow = nb + wn * (BN / 2) + 32 * i + 8 * q + 4 * half;
+        float v[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          if (nrow + r < n) {
-            const float bv = bias != nullptr ? __half2float(bias[nrow + r]) : 0.f;
-            yr[nrow + r] = __float2half_rn(acc[i][j][4 * q + r] + bv);
-          }
+          const float bv = (bias != nullptr && nrow + r < n) ? __half2float(bias[nrow + r]) : 0.f;
+          v[r] = acc[i][j][4 * q + r] + bv;
+        }
+        if (vec_out && nrow + 3 < n) {
+          const h2 lo = {_Float16(v[0]), _Float16(v[1])}, hi = {_Float16(v[2]), _Float16(v[3])};
+          *reinterpret_cast<uint2*>(yr + nrow) = uint2{as_u32(lo), as_u32(hi)};
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (nrow + r < n) yr[nrow + r] = __float2half_rn(v[r]);
         }
       }
     }
   }
 }
 
+// Loads in flight per batch, bounded by the activation registers (MT m-tiles x k-steps).
+template <int BITS, int MT>
+constexpr int skinny_u() {
+  return BITS == 8 ? (MT <= 2 ? 4 : 2) : (MT <= 2 ? 2 : 1);
+}
+
 template <int BITS, int NT, int MT>
 void launch_skinny(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
                    const f16* scales, const f16* bias, int32_t n, int32_t g, f16* y, int64_t ys,
-                   int kw, hipStream_t s) {
-  constexpr int U = BITS == 8 ? 4 : 2;
+                   hipStream_t s) {
+  constexpr int U = skinny_u<BITS, MT>();
+  // Waves per workgroup split K, chosen from K alone (so a row's summation order, and so its
+  // bits, does not depend on N or on the other rows of the launch): enough waves that each
+  // holds about one batch of U chunks, at most kMaxSkinnyWaves.
+  const int nkb = k / SkinnyCfg<BITS>::KB;
+  int kw = 1;
+  while (kw < kMaxSkinnyWaves && kw * U < nkb) kw *= 2;
+  const int per_wave = (nkb + kw - 1) / kw;
+  if constexpr (NT > 1) {
+    // Two super-batches of two row tiles would not fit the register file: one tile per wave.
+    if (per_wave > U) {
+      launch_skinny<BITS, 1, MT>(x, xs, m, k, packed, scales, bias, n, g, y, ys, s);
+      return;
+    }
+  }
   const unsigned blocks = unsigned((n + 16 * NT - 1) / (16 * NT));
-  hipLaunchKernelGGL((qlinear_skinny_kernel<BITS, NT, MT, U>), dim3(blocks), dim3(kw * kWave), 0,
-                     s, x, xs, m, k, packed, scales, bias, n, g, y, ys);
+  const bool pg = k / g > 1;
+#define EDGERAG_SKINNY(NB, PG)                                                                 \
+  hipLaunchKernelGGL((qlinear_skinny_kernel<BITS, NT, MT, U, NB, PG>), dim3(blocks),           \
+                     dim3(kw * kWave), 0, s, x, xs, m, k, packed, scales, bias, n, g, y, ys)
+  if (per_wave <= U) {
+    if (pg) EDGERAG_SKINNY(1, true); else EDGERAG_SKINNY(1, false);
+  } else {
+    if (pg) EDGERAG_SKINNY(2, true); else EDGERAG_SKINNY(2, false);
+  }
+#undef EDGERAG_SKINNY
 }
 
 template <int BITS, int BN, int BM>
@@ -457,18 +528,14 @@ void dispatch(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* pac
               const f16* scales, const f16* bias, int32_t n, int32_t g, f16* y, int64_t ys,
               hipStream_t s) {
   if (m <= EDGERAG_SKINNY_MAX_M) {
-    // Waves per workgroup split K; chosen from K alone, so a row's summation order (and so its
-    // bits) does not depend on N or on which other rows share the launch.
-    const int nkb = k / SkinnyCfg<BITS>::KB;
-    int kw = 1;
-    while (kw < kMaxSkinnyWaves && nkb / (2 * kw) >= 2) kw *= 2;
     const bool wide = (n + 31) / 32 >= 256;  // enough workgroups with 32 rows each
     if (m <= 16) {
-      if (wide) launch_skinny<BITS, 2, 1>(x, xs, m, k, packed, scales, bias, n, g, y, ys, kw, s);
-      else launch_skinny<BITS, 1, 1>(x, xs, m, k, packed, scales, bias, n, g, y, ys, kw, s);
+      if (wide) launch_skinny<BITS, 2, 1>(x, xs, m, k, packed, scales, bias, n, g, y, ys, s);
+      else launch_skinny<BITS, 1, 1>(x, xs, m, k, packed, scales, bias, n, g, y, ys, s);
+    } else if (m <= 32) {
+      launch_skinny<BITS, 1, 2>(x, xs, m, k, packed, scales, bias, n, g, y, ys, s);
     } else {
-      if (wide) launch_skinny<BITS, 2, 2>(x, xs, m, k, packed, scales, bias, n, g, y, ys, kw, s);
-      else launch_skinny<BITS, 1, 2>(x, xs, m, k, packed, scales, bias, n, g, y, ys, kw, s);
+      launch_skinny<BITS, 1, 4>(x, xs, m, k, packed, scales, bias, n, g, y, ys, s);
     }
     return;
   }
