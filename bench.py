@@ -140,6 +140,17 @@ def copy_bandwidth(device, nbytes=1 << 30, iters=20):
     return round(2 * nbytes / us / 1e3, 1)
 
 
+def measured_traffic(name: str) -> int | None:
+    """HBM bytes per launch recorded by the rocprofv3 PMC runs summarised in ``profiles/``."""
+    path = ROOT / "profiles" / name
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":", 1)[1])
+    return None
+
+
 def cfg2_lens():
     g = torch.Generator().manual_seed(2)
     return torch.randint(256, 7473, (32,), generator=g).tolist()
@@ -339,12 +350,14 @@ def main() -> None:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "paged attention launch (attn_rows_kernel + attn_combine_kernel)",
+            "kernel": "paged attention launch: attn_decode_kernel + attn_combine_kernel",
             "achieved": round(attn_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic("attn_decode_cfg2.md"),
+            "traffic_source": "profiles/attn_decode_cfg2.md (rocprofv3 --pmc FETCH_SIZE / "
+            "WRITE_SIZE, scaled by a 1 GiB copy)",
             "algorithmic_bytes": int(attn_bytes),
             "launch_us": round(attn_ms * 1e3, 2),
         },

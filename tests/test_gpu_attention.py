@@ -280,7 +280,7 @@ def test_repeated_launches_with_a_shared_workspace_agree(device) -> None:
     kd, vd, qd = kp.to(device), vp.to(device), q.to(device)
     plan, _ = kernels.plan_attention(qsl, np.asarray(lens, np.int32), bt, 8, 4, 64, BLOCK_SIZE,
                                      torch.float16, device)
-    assert int(plan.plan_host[16]) > 0, "the case must exercise split merging"
+    assert int(plan.plan_host[6]) > 0, "the case must exercise split merging (partials)"
     other, _ = kernels.plan_attention(qsl[:3], np.asarray(lens[:2], np.int32), bt[:2], 8, 4, 64,
                                       BLOCK_SIZE, torch.float16, device)
     outs = []
@@ -291,6 +291,52 @@ def test_repeated_launches_with_a_shared_workspace_agree(device) -> None:
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
     expected = oa.ragged_reference(q, kp, vp, qsl.tolist(), lens, tables, 0.125)
     torch.testing.assert_close(outs[0].float().cpu(), expected, **FP16_TOL)
+
+
+def test_graph_replays_match_eager_with_split_merge(device) -> None:
+    """The decode kernel and the split merge captured in a HIP graph, replayed several times with
+    eager launches and synchronisations in between, reproduce the eager result on every replay."""
+    lens = [3000, 257, 4100, 1800, 900, 6000]
+    kp, vp, tables, qsl, q, bt = _ragged_case(lens, [1] * 6, 8, 8, 64, torch.float16, 21)
+    kd, vd, qd = kp.to(device), vp.to(device), q.to(device)
+    plan, _ = kernels.plan_attention(qsl, np.asarray(lens, np.int32), bt, 8, 8, 64, BLOCK_SIZE,
+                                     torch.float16, device)
+    assert int(plan.plan_host[6]) > 0 and int(plan.plan_host[16]) > 0
+    eager = kernels.paged_attention(qd, kd, vd, plan, 0.125).clone()
+    out = torch.empty_like(qd)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        kernels.paged_attention(qd, kd, vd, plan, 0.125, out=out)
+    for _ in range(4):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        again = kernels.paged_attention(qd, kd, vd, plan, 0.125)
+        torch.cuda.synchronize()
+        assert torch.equal(again, eager)
+    expected = oa.ragged_reference(q, kp, vp, qsl.tolist(), lens, tables, 0.125)
+    torch.testing.assert_close(eager.float().cpu(), expected, **FP16_TOL)
+
+
+def test_plans_of_different_sizes_share_one_workspace(device) -> None:
+    """Plans of different sizes (different partial layouts) alternate on one shared workspace."""
+    small = [2600, 3100]
+    large = [700 + 137 * i for i in range(40)]
+    cases = []
+    for lens, seed in ((small, 31), (large, 32)):
+        kp, vp, tables, qsl, q, bt = _ragged_case(lens, [1] * len(lens), 8, 8, 64, torch.float16,
+                                                  seed)
+        plan, _ = kernels.plan_attention(qsl, np.asarray(lens, np.int32), bt, 8, 8, 64,
+                                         BLOCK_SIZE, torch.float16, device)
+        assert int(plan.plan_host[6]) > 0
+        expected = oa.ragged_reference(q, kp, vp, qsl.tolist(), lens, tables, 0.125)
+        cases.append((kp.to(device), vp.to(device), q.to(device), plan, expected))
+    for _ in range(2):
+        for kd, vd, qd, plan, expected in cases:
+            got = kernels.paged_attention(qd, kd, vd, plan, 0.125)
+            torch.testing.assert_close(got.float().cpu(), expected, **FP16_TOL)
 
 
 def test_plan_rejects_more_queries_than_context(device) -> None:
