@@ -292,6 +292,52 @@ def run_cfg3(device, args):
     return res
 
 
+# --- config 5: end-to-end serving ---------------------------------------------------------------
+
+
+def run_cfg5(device, n_requests: int = 64):
+    """Config 5: the 24-layer SmolLM2-1.7B-shaped decoder (INT8 per-channel linears, fp16
+    embeddings / norms / lm_head, random init) serving a seeded Poisson trace (12 req/min,
+    lognormal prompts median 3000 clamped to [256, 7472], 64-256 greedy tokens) through the
+    scheduler (max batch 8, one 512-token prefill chunk per iteration, CoW reserve 4) and the
+    ragged executor. ``offered_load`` replays the arrivals on a virtual clock (idle gaps skipped);
+    ``saturated`` submits every request at t = 0 (capacity)."""
+    from edgerag_amd.cache.allocator import BlockAllocator
+    from edgerag_amd.core.model import EdgeRagDecoder
+    from edgerag_amd.core.spec import SMOLLM2_1_7B
+    from edgerag_amd.sched.scheduler import Scheduler, SchedulerConfig
+    from edgerag_amd.serve.executor import ModelExecutor
+    from edgerag_amd.serve.replay import poisson_arrivals, replay, synthetic_requests
+
+    spec = SMOLLM2_1_7B
+    t0 = time.perf_counter()
+    model = EdgeRagDecoder(spec, bits=8, group_size=None, device=device, dtype=torch.float16)
+    model.init_random(seed=5)
+    torch.cuda.synchronize()
+    init_s = time.perf_counter() - t0
+    num_blocks = 8 * math.ceil((7472 + 256) / BS) + 64
+    alloc = BlockAllocator(num_blocks, BS)
+    executor = ModelExecutor(model, spec, alloc, device, torch.float16, chunk_size=512)
+    warm = synthetic_requests(2, spec.vocab_size, seed=99, median=700, sigma=0.01, min_new=4,
+                              max_new=4)
+    replay(Scheduler(alloc, SchedulerConfig()), executor, warm, None, "saturated")
+    reqs = synthetic_requests(n_requests, spec.vocab_size, seed=5)
+    arrivals = poisson_arrivals(len(reqs), 12.0 / 60.0, seed=5)
+    offered = replay(Scheduler(alloc, SchedulerConfig()), executor, reqs, arrivals, "virtual")
+    reqs = synthetic_requests(n_requests, spec.vocab_size, seed=5)
+    saturated = replay(Scheduler(alloc, SchedulerConfig()), executor, reqs, None, "saturated")
+    return {
+        "workload": f"{n_requests} requests, Poisson 12 req/min, prompts lognormal(3000, 0.6) "
+        "in [256, 7472], 64-256 greedy tokens; 24-layer SmolLM2-1.7B shape, INT8 per-channel",
+        "metric": "decoder output tok/s",
+        "offered_load": offered.summary(),
+        "saturated": saturated.summary(),
+        "weight_bytes": model.weight_bytes(),
+        "kv_pool_bytes": executor.pool_bytes,
+        "init_s": round(init_s, 2),
+    }
+
+
 # --- main ------------------------------------------------------------------------------------------
 
 
@@ -302,7 +348,9 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-extra", action="store_true", help="skip configs 3 and 4")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["cfg3", "cfg4"], default=None,
+    ap.add_argument("--no-cfg5", action="store_true", help="skip the end-to-end serving run")
+    ap.add_argument("--cfg5-requests", type=int, default=64)
+    ap.add_argument("--only", choices=["cfg3", "cfg4", "cfg5"], default=None,
                     help="run just one secondary config (for profiling); prints its record")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -316,6 +364,9 @@ def main() -> None:
         return
     if args.only == "cfg4":
         print(json.dumps({"cfg4": bench_quant(device)}), flush=True)
+        return
+    if args.only == "cfg5":
+        print(json.dumps({"cfg5": run_cfg5(device, args.cfg5_requests)}), flush=True)
         return
 
     lens = cfg2_lens()
@@ -369,6 +420,8 @@ def main() -> None:
     if not args.no_extra:
         line["cfg3"] = run_cfg3(device, args)
         line["cfg4"] = bench_quant(device)
+        if not args.no_cfg5:
+            line["cfg5"] = run_cfg5(device, args.cfg5_requests)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(lens)
     print(json.dumps(line), flush=True)

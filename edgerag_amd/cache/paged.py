@@ -90,11 +90,18 @@ class PagedKVCache:
         call it directly before a forward.
         """
         self._pending_tokens = n_new
-        self.table.append(n_new)
-        self._unshare_write_range(self.seq_len - n_new, n_new)
-        slots = self.table.slots(self.seq_len - n_new, n_new)
+        slots = self.reserve(n_new)
         blocks = np.asarray(self.table.blocks, dtype=np.int32)
         self._slots, self._blocks = kernels.upload_int32([slots, blocks], self.device)
+
+    def reserve(self, n_new: int) -> np.ndarray:
+        """Grow the table by ``n_new`` tokens, copy-on-write any shared block in the write range
+        (every layer), and return the int32 pool slots of positions ``[seq_len - n_new,
+        seq_len)``. The host half of :meth:`begin_append`, for callers that upload several
+        sequences' metadata at once (the ragged executor)."""
+        self.table.append(n_new)
+        self._unshare_write_range(self.seq_len - n_new, n_new)
+        return self.table.slots(self.seq_len - n_new, n_new)
 
     def append(self, key: torch.Tensor, value: torch.Tensor, layer_idx: int) -> None:
         """Write this step's post-RoPE K/V ``(1, kv_heads, n_new, head_dim)``; no gather."""

@@ -1,0 +1,187 @@
+"""The language decoder over a packed ragged batch: embeddings -> N blocks -> norm -> lm_head.
+
+Same architecture and arithmetic as the reference ``EdgeRagDecoder`` (``edgerag/core/model.py:
+31-152``, blocks from ``edgerag/core/layers.py:257-374``): pre-norm blocks, grouped-query attention
+with RoPE applied before the cache write (keys are cached post-RoPE, ``layers.py:301-306``),
+SwiGLU MLP, fp16 embeddings / norms / lm_head (the quantisation skip list, ``linear.py:229-241``)
+and weight-only INT8 or INT4 projections.
+
+What changes is the execution shape. The reference runs one request per forward and one forward
+per request per iteration (``serve/executor.py:116-154``). Here every request of an iteration --
+chunked-prefill slices and single-token decodes alike -- is packed token-major into one forward:
+
+* q/k/v are one fused quant linear (their rows stacked: exact, each row keeps its codes and scale),
+  gate/up another, so a layer runs four weight-streaming launches whatever the batch holds;
+* K/V of every new token are scattered into the shared paged pool by slot (``kv_append``);
+* attention is one ragged launch over all requests (``paged_attention`` with the step's plan):
+  causal inside each chunk, full over the cached prefix, per request -- exactly the per-request
+  ``build_causal_mask`` + SDPA of the reference;
+* only the rows whose logits are read (each request's last token) go through the final norm and
+  the lm_head (the reference's ``last_token_only``, ``model.py:150-152``).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+from torch import nn
+
+from edgerag_amd import kernels
+from edgerag_amd.core.layers import RMSNorm, RotaryTable, apply_rope, silu_mul
+from edgerag_amd.core.linear import QuantLinear
+from edgerag_amd.core.quant import QuantConfig
+from edgerag_amd.core.spec import ModelSpec
+
+
+@dataclass
+class StepInputs:
+    """Device-side inputs of one packed forward (built and uploaded once per step)."""
+
+    token_ids: torch.Tensor  # (T,) int32
+    positions: torch.Tensor  # (T,) int32 logical positions
+    slots: torch.Tensor  # (T,) int32 pool slot of every new token
+    logit_rows: torch.Tensor  # (R',) int32 rows of the packed batch whose logits are needed
+    plan: kernels.AttentionPlan
+
+
+def _config(bits: int, group_size: int | None, in_features: int) -> QuantConfig:
+    """``group_size=None`` is per-output-channel quantisation: one group spanning the input."""
+    return QuantConfig(group_size=in_features if group_size is None else group_size, bits=bits)
+
+
+class DecoderLayer(nn.Module):
+    def __init__(self, spec: ModelSpec, bits: int, group_size: int | None, device, dtype) -> None:
+        super().__init__()
+        h, d = spec.hidden_size, spec.head_dim
+        self.q_out, self.kv_out = spec.n_q_heads * d, spec.n_kv_heads * d
+        self.intermediate = inter = spec.intermediate_size
+        self.qkv = QuantLinear(h, self.q_out + 2 * self.kv_out, config=_config(bits, group_size, h),
+                               device=device)
+        self.o_proj = QuantLinear(self.q_out, h, config=_config(bits, group_size, self.q_out),
+                                  device=device)
+        self.gate_up = QuantLinear(h, 2 * inter, config=_config(bits, group_size, h), device=device)
+        self.down_proj = QuantLinear(inter, h, config=_config(bits, group_size, inter),
+                                     device=device)
+        self.input_layernorm = RMSNorm(h, spec.rms_norm_eps, device, dtype)
+        self.post_attention_layernorm = RMSNorm(h, spec.rms_norm_eps, device, dtype)
+
+    def load(self, q, k, v, o, gate, up, down) -> None:
+        """Quantise the reference's seven projection weights (``(out, in)`` each) into the fused
+        layout: rows of q/k/v stacked, rows of gate/up stacked."""
+        self.qkv.load_weight(torch.cat([q, k, v], dim=0))
+        self.o_proj.load_weight(o)
+        self.gate_up.load_weight(torch.cat([gate, up], dim=0))
+        self.down_proj.load_weight(down)
+
+
+class EdgeRagDecoder(nn.Module):
+    def __init__(
+        self,
+        spec: ModelSpec,
+        bits: int = 8,
+        group_size: int | None = None,
+        device: torch.device | str = "cuda",
+        dtype: torch.dtype = torch.float16,
+    ) -> None:
+        """``bits`` 8 or 4; ``group_size=None`` quantises per output channel (
+        INT8 per-channel), an integer gives group-wise scales along K."""
+        super().__init__()
+        self.spec = spec
+        self.device = torch.device(device)
+        self.dtype = dtype
+        self.bits, self.group_size = bits, group_size
+        h = spec.hidden_size
+        self.embed_tokens = nn.Parameter(
+            torch.zeros(spec.vocab_size, h, device=self.device, dtype=dtype), requires_grad=False
+        )
+        self.layers = nn.ModuleList(
+            [DecoderLayer(spec, bits, group_size, self.device, dtype) for _ in range(spec.n_layers)]
+        )
+        self.norm = RMSNorm(h, spec.rms_norm_eps, self.device, dtype)
+        self.lm_head = nn.Parameter(
+            torch.zeros(spec.vocab_size, h, device=self.device, dtype=dtype), requires_grad=False
+        )
+        self.rotary = RotaryTable(spec.head_dim, spec.rope_theta, spec.max_position_embeddings,
+                                  self.device, dtype)
+        self.scaling = spec.head_dim**-0.5
+
+    # --- weights ----------------------------------------------------------------------------------
+
+    @torch.no_grad()
+    def init_random(self, seed: int = 0, std: float = 0.02) -> None:
+        """Seeded random weights (no checkpoint is available offline): N(0, std) projections,
+        embeddings and lm_head, quantised on the device with the reference's rule; unit norms."""
+        g = torch.Generator(device=self.device).manual_seed(seed)
+        spec = self.spec
+        h, inter = spec.hidden_size, spec.intermediate_size
+        q_out, kv_out = spec.n_q_heads * spec.head_dim, spec.n_kv_heads * spec.head_dim
+
+        def w(n, k):
+            return torch.randn(n, k, generator=g, device=self.device) * std
+
+        self.embed_tokens.copy_(w(spec.vocab_size, h).to(self.dtype))
+        for layer in self.layers:
+            layer.load(w(q_out, h), w(kv_out, h), w(kv_out, h), w(h, q_out), w(inter, h),
+                       w(inter, h), w(h, inter))
+            layer.input_layernorm.weight.fill_(1.0)
+            layer.post_attention_layernorm.weight.fill_(1.0)
+        self.norm.weight.fill_(1.0)
+        self.lm_head.copy_(w(spec.vocab_size, h).to(self.dtype))
+
+    @torch.no_grad()
+    def load_quantized(self, weights) -> None:
+        """Take already-quantised weights laid out like this decoder (per layer ``qkv``,
+        ``o_proj``, ``gate_up``, ``down_proj`` with ``packed``/``scales``, norm weights, fp16
+        ``embed_tokens`` and ``lm_head``) without re-quantising."""
+        for layer, src in zip(self.layers, weights.layers):
+            for name in ("qkv", "o_proj", "gate_up", "down_proj"):
+                lin = getattr(src, name)
+                getattr(layer, name).load_quantized(lin.packed.to(self.device),
+                                                    lin.scales.to(self.device))
+            layer.input_layernorm.weight.copy_(src.input_layernorm.weight)
+            layer.post_attention_layernorm.weight.copy_(src.post_attention_layernorm.weight)
+        self.norm.weight.copy_(weights.norm.weight)
+        self.embed_tokens.copy_(weights.embed_tokens)
+        self.lm_head.copy_(weights.lm_head)
+
+    def weight_bytes(self) -> int:
+        total = 0
+        for layer in self.layers:
+            for lin in (layer.qkv, layer.o_proj, layer.gate_up, layer.down_proj):
+                total += lin.weight_bytes()
+        total += 2 * self.embed_tokens.numel() * self.embed_tokens.element_size()
+        return total
+
+    # --- forward --------------------------------------------------------------------------------
+
+    @torch.inference_mode()
+    def forward_hidden(self, step: StepInputs, key_pool: list[torch.Tensor],
+                       value_pool: list[torch.Tensor]) -> torch.Tensor:
+        """Run every layer over the packed batch; return the final-norm hidden of ``logit_rows``."""
+        spec = self.spec
+        T = step.token_ids.shape[0]
+        d = spec.head_dim
+        hidden = self.embed_tokens[step.token_ids.long()]
+        cos, sin = self.rotary(step.positions.long())
+        attn_out = torch.empty((T, spec.n_q_heads, d), device=self.device, dtype=self.dtype)
+        for idx, layer in enumerate(self.layers):
+            x = layer.input_layernorm(hidden)
+            qkv = layer.qkv(x)
+            q = qkv[:, : layer.q_out].view(T, spec.n_q_heads, d)
+            k = qkv[:, layer.q_out : layer.q_out + layer.kv_out].view(T, spec.n_kv_heads, d)
+            v = qkv[:, layer.q_out + layer.kv_out :].view(T, spec.n_kv_heads, d)
+            q = apply_rope(q, cos, sin)
+            k = apply_rope(k, cos, sin)  # post-RoPE keys are what the cache holds
+            kernels.kv_append(k, v.contiguous(), step.slots, key_pool[idx], value_pool[idx])
+            kernels.paged_attention(q, key_pool[idx], value_pool[idx], step.plan, self.scaling,
+                                    out=attn_out)
+            hidden = hidden + layer.o_proj(attn_out.view(T, layer.q_out))
+            x = layer.post_attention_layernorm(hidden)
+            hidden = hidden + layer.down_proj(silu_mul(layer.gate_up(x), layer.intermediate))
+        return self.norm(hidden[step.logit_rows.long()])
+
+    @torch.inference_mode()
+    def logits(self, step: StepInputs, key_pool, value_pool) -> torch.Tensor:
+        """``(R', vocab)`` logits of the rows in ``step.logit_rows``."""
+        return nn.functional.linear(self.forward_hidden(step, key_pool, value_pool), self.lm_head)

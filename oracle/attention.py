@@ -36,7 +36,8 @@ def build_causal_mask(seq_len: int, past_len: int, dtype: torch.dtype) -> torch.
     total = past_len + seq_len
     q_pos = torch.arange(past_len, total).unsqueeze(1)
     k_pos = torch.arange(total).unsqueeze(0)
-    mask = torch.where(k_pos <= q_pos, 0.0, torch.finfo(dtype).min).to(dtype)
+    mask = torch.zeros((seq_len, total), dtype=dtype).masked_fill_(k_pos > q_pos,
+                                                                   torch.finfo(dtype).min)
     return mask[None, None]
 
 
