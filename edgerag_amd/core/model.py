@@ -42,7 +42,7 @@ class StepInputs:
     positions: torch.Tensor  # (T,) int32 logical positions
     slots: torch.Tensor  # (T,) int32 pool slot of every new token
     logit_rows: torch.Tensor  # (R',) int32 rows of the packed batch whose logits are needed
-    plan: kernels.AttentionPlan
+    plan: kernels.AttentionPlan | kernels.FixedAttention  # eager plan, or graph-stable staging
 
 
 def _config(bits: int, group_size: int | None, in_features: int) -> QuantConfig:
@@ -174,8 +174,11 @@ class EdgeRagDecoder(nn.Module):
             q = apply_rope(q, cos, sin)
             k = apply_rope(k, cos, sin)  # post-RoPE keys are what the cache holds
             kernels.kv_append(k, v.contiguous(), step.slots, key_pool[idx], value_pool[idx])
-            kernels.paged_attention(q, key_pool[idx], value_pool[idx], step.plan, self.scaling,
-                                    out=attn_out)
+            if isinstance(step.plan, kernels.FixedAttention):
+                step.plan.launch(q, key_pool[idx], value_pool[idx], self.scaling, attn_out)
+            else:
+                kernels.paged_attention(q, key_pool[idx], value_pool[idx], step.plan,
+                                        self.scaling, out=attn_out)
             hidden = hidden + layer.o_proj(attn_out.view(T, layer.q_out))
             x = layer.post_attention_layernorm(hidden)
             hidden = hidden + layer.down_proj(silu_mul(layer.gate_up(x), layer.intermediate))

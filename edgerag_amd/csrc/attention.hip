@@ -201,13 +201,17 @@ __global__ __launch_bounds__(kWave) void attn_decode_kernel(
     const T* __restrict__ q, int64_t q_st, int64_t q_sh, const T* __restrict__ kpool,
     const T* __restrict__ vpool, const int32_t* __restrict__ block_tables, int64_t bt_stride,
     const int32_t* __restrict__ qsl, const int32_t* __restrict__ ctx,
-    const int32_t* __restrict__ plan, int32_t item_base, int32_t n_q_heads, int32_t n_kv_heads,
-    int32_t num_blocks, int32_t block_size, float scale_log2, T* __restrict__ out, int64_t o_st,
-    int64_t o_sh, float2* __restrict__ part_ml, float* __restrict__ part_acc) {
+    const int32_t* __restrict__ plan, int32_t item_base, int32_t limit_word, int32_t n_q_heads,
+    int32_t n_kv_heads, int32_t num_blocks, int32_t block_size, float scale_log2,
+    T* __restrict__ out, int64_t o_st, int64_t o_sh, float2* __restrict__ part_ml,
+    float* __restrict__ part_acc) {
   using C = RowCfg<T, D>;
   constexpr int VEC = C::VEC, LPT = C::LPT, TPW = C::TPW, LOG_LPT = C::LOG_LPT;
   constexpr int STEP = TPW * U;
 
+  // The grid may exceed the work list (fixed-size launches replayed from a graph): the item
+  // count of this launch's kind is read from the device plan.
+  if (item_base + int(blockIdx.x) >= plan[limit_word]) return;
   const int32_t* it = plan + plan[H_ITEM_OFF] + int64_t(item_base + blockIdx.x) * kItemWords;
   const int r = it[I_REQ], h = it[I_HEAD], qb = it[I_QBEGIN], qc = it[I_QCOUNT];
   const int kb = it[I_KVBEGIN], ke = it[I_KVEND], split = it[I_SPLIT];
@@ -347,12 +351,16 @@ __global__ __launch_bounds__(kWave) void attn_rows_kernel(
     const T* __restrict__ q, int64_t q_st, int64_t q_sh, const T* __restrict__ kpool,
     const T* __restrict__ vpool, const int32_t* __restrict__ block_tables, int64_t bt_stride,
     const int32_t* __restrict__ qsl, const int32_t* __restrict__ ctx,
-    const int32_t* __restrict__ plan, int32_t item_base, int32_t n_q_heads, int32_t n_kv_heads,
-    int32_t num_blocks, int32_t block_size, float scale_log2, T* __restrict__ out, int64_t o_st,
-    int64_t o_sh, float2* __restrict__ part_ml, float* __restrict__ part_acc) {
+    const int32_t* __restrict__ plan, int32_t item_base, int32_t limit_word, int32_t n_q_heads,
+    int32_t n_kv_heads, int32_t num_blocks, int32_t block_size, float scale_log2,
+    T* __restrict__ out, int64_t o_st, int64_t o_sh, float2* __restrict__ part_ml,
+    float* __restrict__ part_acc) {
   using C = RowCfg<T, D>;
   constexpr int VEC = C::VEC, LPT = C::LPT, TPW = C::TPW, LOG_LPT = C::LOG_LPT;
 
+  // The grid may exceed the work list (fixed-size launches replayed from a graph): the item
+  // count of this launch's kind is read from the device plan.
+  if (item_base + int(blockIdx.x) >= plan[limit_word]) return;
   const int32_t* it = plan + plan[H_ITEM_OFF] + int64_t(item_base + blockIdx.x) * kItemWords;
   const int r = it[I_REQ], h = it[I_HEAD], qb = it[I_QBEGIN], qc = it[I_QCOUNT];
   const int kb = it[I_KVBEGIN], ke = it[I_KVEND], split = it[I_SPLIT];
@@ -470,9 +478,10 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(
     int64_t o_st, int64_t o_sh) {
   const int hq = blockIdx.y * (blockDim.x / kWave) + threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
-  if (hq >= n_q_heads) return;
-  const int4* e4 = reinterpret_cast<const int4*>(plan + combine_off +
-                                                 int64_t(blockIdx.x) * kCombineWords);
+  if (hq >= n_q_heads || int(blockIdx.x) >= plan[H_N_COMBINE]) return;
+  // combine_off < 0: read the list's offset from the device plan (fixed-capacity launches).
+  const int off = combine_off >= 0 ? combine_off : plan[H_COMBINE_OFF];
+  const int4* e4 = reinterpret_cast<const int4*>(plan + off + int64_t(blockIdx.x) * kCombineWords);
   const int4 a = e4[0], b = e4[1];  // {tok, q0, c, L}, {nsplit, split_len, part_off, pad}
   combine_pair<T>(a.x, hq, a.y, a.z, a.w, b.x, b.y, b.z, n_q_heads, head_dim, part_ml, part_acc,
                   out, o_st, o_sh, lane);
@@ -519,41 +528,41 @@ WorkspaceLayout workspace_layout(int64_t n_partials, int64_t head_dim) {
 using Launch = AttnLaunch;
 
 template <typename T, int D, int QR, int U>
-void launch_decode(const Launch& a, int base, int count) {
+void launch_decode(const Launch& a, int base, int count, int limit_word) {
   hipLaunchKernelGGL((attn_decode_kernel<T, D, QR, U>), dim3(count), dim3(kWave), 0, a.s,
                      static_cast<const T*>(a.q), a.q_st, a.q_sh, static_cast<const T*>(a.kp),
                      static_cast<const T*>(a.vp), a.bt, a.bt_stride, a.qsl, a.ctx, a.plan, base,
-                     a.hq, a.hkv, a.nb, a.bs, a.scale_log2, static_cast<T*>(a.out), a.o_st, a.o_sh,
-                     a.ml, a.pacc);
+                     limit_word, a.hq, a.hkv, a.nb, a.bs, a.scale_log2, static_cast<T*>(a.out),
+                     a.o_st, a.o_sh, a.ml, a.pacc);
 }
 
 template <typename T, int D, int QR>
-void launch_rows(const Launch& a, int base, int count) {
+void launch_rows(const Launch& a, int base, int count, int limit_word) {
   hipLaunchKernelGGL((attn_rows_kernel<T, D, QR>), dim3(count), dim3(kWave), 0, a.s,
                      static_cast<const T*>(a.q), a.q_st, a.q_sh, static_cast<const T*>(a.kp),
                      static_cast<const T*>(a.vp), a.bt, a.bt_stride, a.qsl, a.ctx, a.plan, base,
-                     a.hq, a.hkv, a.nb, a.bs, a.scale_log2, static_cast<T*>(a.out), a.o_st, a.o_sh,
-                     a.ml, a.pacc);
+                     limit_word, a.hq, a.hkv, a.nb, a.bs, a.scale_log2, static_cast<T*>(a.out),
+                     a.o_st, a.o_sh, a.ml, a.pacc);
 }
 
 template <typename T, int D>
-void dispatch_decode_qr(const Launch& a, int qr, int base, int count) {
+void dispatch_decode_qr(const Launch& a, int qr, int base, int count, int limit_word) {
   constexpr int U = D >= 256 ? 2 : kDecodeU;
   switch (qr) {
-    case 1: launch_decode<T, D, 1, U>(a, base, count); break;
-    case 2: launch_decode<T, D, 2, U>(a, base, count); break;
-    case 4: launch_decode<T, D, 4, U>(a, base, count); break;
-    default: launch_decode<T, D, 8, 2>(a, base, count); break;
+    case 1: launch_decode<T, D, 1, U>(a, base, count, limit_word); break;
+    case 2: launch_decode<T, D, 2, U>(a, base, count, limit_word); break;
+    case 4: launch_decode<T, D, 4, U>(a, base, count, limit_word); break;
+    default: launch_decode<T, D, 8, 2>(a, base, count, limit_word); break;
   }
 }
 
 template <typename T, int D>
-void dispatch_rows_qr(const Launch& a, int qr, int base, int count) {
+void dispatch_rows_qr(const Launch& a, int qr, int base, int count, int limit_word) {
   switch (qr) {
-    case 1: launch_rows<T, D, 1>(a, base, count); break;
-    case 2: launch_rows<T, D, 2>(a, base, count); break;
-    case 4: launch_rows<T, D, 4>(a, base, count); break;
-    default: launch_rows<T, D, 8>(a, base, count); break;
+    case 1: launch_rows<T, D, 1>(a, base, count, limit_word); break;
+    case 2: launch_rows<T, D, 2>(a, base, count, limit_word); break;
+    case 4: launch_rows<T, D, 4>(a, base, count, limit_word); break;
+    default: launch_rows<T, D, 8>(a, base, count, limit_word); break;
   }
 }
 
@@ -569,19 +578,19 @@ int run_items(const Launch& a, const int32_t* ph) {
       if (ph[H_TILE_KIND] == 1 && prefill_tiles_supported(a.nb, a.bs)) {
         launch_prefill_tiles_f16_d64(a, n_row, n_items - n_row);
       } else {
-        dispatch_rows_qr<T, D>(a, 8, n_row, n_items - n_row);
+        dispatch_rows_qr<T, D>(a, 8, n_row, n_items - n_row, H_N_ITEMS);
       }
     } else {
-      dispatch_rows_qr<T, D>(a, 8, n_row, n_items - n_row);
+      dispatch_rows_qr<T, D>(a, 8, n_row, n_items - n_row, H_N_ITEMS);
     }
   }
   const int qr = std::min(8, pow2_at_least(std::max(1, ph[H_MAX_ROW_VECS])));
   const bool fast = a.bs % C::TPW == 0 && ph[H_MAX_SPLIT_BLOCKS] <= kMaxSplitBlocks;
   if (n_row > 0) {
     if (fast)
-      dispatch_decode_qr<T, D>(a, qr, 0, n_row);
+      dispatch_decode_qr<T, D>(a, qr, 0, n_row, H_N_ROW_ITEMS);
     else
-      dispatch_rows_qr<T, D>(a, qr, 0, n_row);
+      dispatch_rows_qr<T, D>(a, qr, 0, n_row, H_N_ROW_ITEMS);
   }
   return check_launch("edgerag_paged_attention");
 }
@@ -856,4 +865,121 @@ extern "C" int edgerag_paged_attention(
   }
 #undef EDGERAG_COMBINE
   return check_launch("edgerag_paged_attention(combine)");
+}
+
+namespace edgerag {
+namespace {
+
+// Decode-row items of a fixed-capacity launch: the fast decode kernel when every load group of a
+// split stays inside one block, the general row kernel otherwise (both bound-checked on device).
+template <typename T, int D>
+void run_rows_fixed(const Launch& a, int qr, int max_items) {
+  using C = RowCfg<T, D>;
+  if (a.bs % C::TPW == 0)
+    dispatch_decode_qr<T, D>(a, qr, 0, max_items, H_N_ROW_ITEMS);
+  else
+    dispatch_rows_qr<T, D>(a, qr, 0, max_items, H_N_ROW_ITEMS);
+}
+
+template <typename T>
+int run_fixed_dtype(const Launch& a, int32_t D, int qr, int max_items) {
+  switch (D) {
+    case 8: run_rows_fixed<T, 8>(a, qr, max_items); break;
+    case 16: run_rows_fixed<T, 16>(a, qr, max_items); break;
+    case 32: run_rows_fixed<T, 32>(a, qr, max_items); break;
+    case 64: run_rows_fixed<T, 64>(a, qr, max_items); break;
+    case 128: run_rows_fixed<T, 128>(a, qr, max_items); break;
+    case 256: run_rows_fixed<T, 256>(a, qr, max_items); break;
+    default: return fail(EDGERAG_EUNSUPPORTED, "edgerag_paged_attention_fixed: head_dim %d", D);
+  }
+  return check_launch("edgerag_paged_attention_fixed");
+}
+
+}  // namespace
+}  // namespace edgerag
+
+extern "C" int edgerag_paged_attention_fixed(
+    const int32_t* plan_dev, int32_t max_row_items, int32_t max_combine_rows,
+    int32_t max_row_vecs, int64_t max_partials, const void* q, int64_t q_stride_tok,
+    int64_t q_stride_head, const void* key_pool, const void* value_pool, int32_t dtype,
+    const int32_t* block_tables, int64_t block_tables_stride, const int32_t* query_start_loc,
+    const int32_t* context_lens, int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+    int32_t block_size, int32_t num_blocks, float scale, void* out, int64_t out_stride_tok,
+    int64_t out_stride_head, void* workspace, int64_t workspace_bytes, void* stream) {
+  clear_error();
+  if (plan_dev == nullptr || q == nullptr || key_pool == nullptr || value_pool == nullptr ||
+      out == nullptr || block_tables == nullptr || query_start_loc == nullptr ||
+      context_lens == nullptr)
+    return fail(EDGERAG_EINVAL, "edgerag_paged_attention_fixed: NULL pointer");
+  if (max_row_items < 0 || max_combine_rows < 0 || max_partials < 0 || max_row_vecs < 1 ||
+      max_row_vecs > kMaxRowVecs)
+    return fail(EDGERAG_EINVAL,
+                "edgerag_paged_attention_fixed: capacities (items %d, combine rows %d, row "
+                "vectors %d, partials %lld) out of range",
+                max_row_items, max_combine_rows, max_row_vecs, (long long)max_partials);
+  if (n_q_heads <= 0 || n_kv_heads <= 0 || n_q_heads % n_kv_heads != 0 ||
+      !head_dim_supported(head_dim) || block_size <= 0 || num_blocks <= 0)
+    return fail(EDGERAG_EINVAL, "edgerag_paged_attention_fixed: bad shape");
+  if (!(scale > 0.f) || !std::isfinite(scale))
+    return fail(EDGERAG_EINVAL, "edgerag_paged_attention_fixed: scale must be positive");
+  const int es = elem_size(dtype);
+  if (es == 0) return fail(EDGERAG_EINVAL, "edgerag_paged_attention_fixed: dtype %d", dtype);
+  if (!aligned16(key_pool) || !aligned16(value_pool) || !aligned16(q) ||
+      (q_stride_tok * es) % 16 != 0 || (q_stride_head * es) % 16 != 0)
+    return fail(EDGERAG_EINVAL, "edgerag_paged_attention_fixed: q and pools must be 16-byte aligned");
+  const int64_t acc_off = round_up(max_partials * int64_t(sizeof(float2)), 256);
+  const int64_t need = max_partials > 0
+                           ? acc_off + round_up(max_partials * head_dim * int64_t(sizeof(float)), 256)
+                           : 0;
+  if (workspace_bytes < need || (need > 0 && workspace == nullptr))
+    return fail(EDGERAG_EWORKSPACE, "edgerag_paged_attention_fixed: workspace %lld bytes, need %lld",
+                (long long)workspace_bytes, (long long)need);
+  Launch a{};
+  a.s = static_cast<hipStream_t>(stream);
+  a.q = q;
+  a.q_st = q_stride_tok;
+  a.q_sh = q_stride_head;
+  a.kp = key_pool;
+  a.vp = value_pool;
+  a.bt = block_tables;
+  a.bt_stride = block_tables_stride;
+  a.qsl = query_start_loc;
+  a.ctx = context_lens;
+  a.plan = plan_dev;
+  a.hq = n_q_heads;
+  a.hkv = n_kv_heads;
+  a.nb = num_blocks;
+  a.bs = block_size;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.out = out;
+  a.o_st = out_stride_tok;
+  a.o_sh = out_stride_head;
+  a.ml = reinterpret_cast<float2*>(workspace);
+  a.pacc = reinterpret_cast<float*>(static_cast<char*>(workspace) + acc_off);
+  const int qr = std::min(8, pow2_at_least(max_row_vecs));
+  int rc = EDGERAG_OK;
+  if (max_row_items > 0) {
+    switch (dtype) {
+      case EDGERAG_F32: rc = run_fixed_dtype<float>(a, head_dim, qr, max_row_items); break;
+      case EDGERAG_F16: rc = run_fixed_dtype<f16>(a, head_dim, qr, max_row_items); break;
+      case EDGERAG_BF16: rc = run_fixed_dtype<bf16>(a, head_dim, qr, max_row_items); break;
+    }
+  }
+  if (rc != EDGERAG_OK || max_combine_rows == 0) return rc;
+  const int waves = 4;
+  const dim3 cblock(kWave * waves);
+  const dim3 cgrid(max_combine_rows, (n_q_heads + waves - 1) / waves);
+  // No host plan here: combine_off = -1 makes the kernel read the list's offset from the device
+  // header.
+#define EDGERAG_COMBINE_FIXED(TYPE)                                                               \
+  hipLaunchKernelGGL((attn_combine_kernel<TYPE>), cgrid, cblock, 0, a.s, plan_dev, -1, n_q_heads,  \
+                     head_dim, a.ml, a.pacc, static_cast<TYPE*>(out), out_stride_tok,             \
+                     out_stride_head)
+  switch (dtype) {
+    case EDGERAG_F32: EDGERAG_COMBINE_FIXED(float); break;
+    case EDGERAG_F16: EDGERAG_COMBINE_FIXED(f16); break;
+    case EDGERAG_BF16: EDGERAG_COMBINE_FIXED(bf16); break;
+  }
+#undef EDGERAG_COMBINE_FIXED
+  return check_launch("edgerag_paged_attention_fixed(combine)");
 }

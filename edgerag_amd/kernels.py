@@ -24,6 +24,7 @@ from edgerag_amd._lib import call, dtype_code, ptr, require_device, stream_ptr  
 
 __all__ = [
     "AttentionPlan",
+    "FixedAttention",
     "dequantize",
     "kv_append",
     "kv_copy_blocks",
@@ -315,6 +316,109 @@ def paged_attention(
         None if ws is None else ws.data_ptr(), plan.workspace_bytes, stream_ptr(query.device),
     )
     return out
+
+
+class FixedAttention:
+    """Decode-only ragged attention with a launch shape fixed at construction, for HIP graphs.
+
+    All step metadata lives in one static device buffer, rewritten in place before every replay
+    by :meth:`update` (one pinned H2D copy): cu_seqlens, context lengths, block tables with a
+    fixed row stride, caller-defined extra int32 arrays (token ids, positions, slots, ...) and the
+    plan. :meth:`launch` calls ``edgerag_paged_attention_fixed``, whose grid depends only on the
+    capacities, so a graph that captured it stays valid for every plan :meth:`update` accepts.
+    The pinned host staging buffer is reused: the caller must have synchronised with the previous
+    step (the executor does, when it reads the tokens back) before calling :meth:`update` again.
+    """
+
+    def __init__(self, device, n_q_heads: int, n_kv_heads: int, head_dim: int, block_size: int,
+                 dtype: torch.dtype, max_reqs: int, max_blocks_per_seq: int,
+                 extra_capacities: list[int], max_items: int = 16384,
+                 min_split: int = 256) -> None:
+        self.device = torch.device(device)
+        self.n_q_heads, self.n_kv_heads, self.head_dim = n_q_heads, n_kv_heads, head_dim
+        self.block_size, self.dtype = block_size, dtype
+        self.max_reqs, self.max_blocks = max_reqs, max_blocks_per_seq
+        self.max_row_vecs = min(8, max(1, n_q_heads // n_kv_heads))
+        self.max_items = max_items
+        self.max_combine = max_reqs
+        max_splits = -(-max_blocks_per_seq * block_size // min_split)
+        self.max_partials = max_reqs * n_q_heads * max_splits
+        self.plan_words = 24 + 8 * max_items + 4 * max_reqs + 8 * self.max_combine + 64
+
+        def pad(n: int) -> int:
+            return (n + 15) // 16 * 16
+
+        sizes = [pad(max_reqs + 1), pad(max_reqs), max_reqs * max_blocks_per_seq,
+                 *[pad(c) for c in extra_capacities]]
+        offs, at = [], 0
+        for n in sizes:
+            offs.append(at)
+            at += pad(n)
+        self._plan_off = at
+        total = at + self.plan_words
+        self.buf = torch.zeros(total, dtype=torch.int32, device=self.device)
+        self.host = torch.zeros(total, dtype=torch.int32, pin_memory=True)
+        self._host_np = self.host.numpy()
+        self.qsl = self.buf[offs[0] : offs[0] + max_reqs + 1]
+        self.ctx = self.buf[offs[1] : offs[1] + max_reqs]
+        self.block_tables = self.buf[offs[2] : offs[2] + max_reqs * max_blocks_per_seq].view(
+            max_reqs, max_blocks_per_seq)
+        self.extras = [self.buf[o : o + c] for o, c in zip(offs[3:], extra_capacities)]
+        self._offs, self._caps = offs, extra_capacities
+        self.plan = self.buf[self._plan_off :]
+        acc_off = (self.max_partials * 8 + 255) // 256 * 256
+        ws = acc_off + (self.max_partials * head_dim * 4 + 255) // 256 * 256
+        self.workspace = torch.empty(ws, dtype=torch.uint8, device=self.device)
+        self.num_reqs = 0
+
+    def update(self, query_start_loc: np.ndarray, context_lens: np.ndarray,
+               block_tables: np.ndarray, extras: list[np.ndarray]) -> bool:
+        """Plan the step and stage it; False (nothing written) if it exceeds a capacity or has
+        prefill tiles -- the caller then runs the eager path."""
+        R = int(np.asarray(context_lens).size)
+        bt = np.asarray(block_tables, np.int32)
+        if R > self.max_reqs or bt.shape[1] > self.max_blocks:
+            return False
+        if any(int(e.size) > c for e, c in zip(extras, self._caps)):
+            return False
+        plan, _ = make_plan_host(query_start_loc, context_lens, self.n_q_heads, self.n_kv_heads,
+                                 self.head_dim, self.block_size, self.max_blocks, self.dtype)
+        n_items, n_row, n_partials = int(plan[2]), int(plan[13]), int(plan[6])
+        if (n_items != n_row or n_row > self.max_items or int(plan[16]) > self.max_combine
+                or int(plan[14]) > self.max_row_vecs or n_partials > self.max_partials
+                or plan.size > self.plan_words):
+            return False
+        h = self._host_np
+        o = self._offs
+        h[o[0] : o[0] + R + 1] = query_start_loc
+        h[o[1] : o[1] + R] = context_lens
+        tbl = h[o[2] : o[2] + self.max_reqs * self.max_blocks].reshape(self.max_reqs,
+                                                                        self.max_blocks)
+        tbl[:R] = -1
+        tbl[:R, : bt.shape[1]] = bt
+        for e, off in zip(extras, o[3:]):
+            h[off : off + e.size] = e.reshape(-1)
+        h[self._plan_off : self._plan_off + plan.size] = plan
+        used = self._plan_off + plan.size
+        self.buf[:used].copy_(self.host[:used], non_blocking=True)
+        self.num_reqs = R
+        return True
+
+    def launch(self, query: torch.Tensor, key_pool: torch.Tensor, value_pool: torch.Tensor,
+               scale: float, out: torch.Tensor) -> torch.Tensor:
+        n_kv, num_blocks, block_size, head_dim = key_pool.shape
+        if query.stride(2) != 1 or out.stride(2) != 1:
+            raise ValueError("query and out need a contiguous head_dim axis")
+        call(
+            "edgerag_paged_attention_fixed", self.plan.data_ptr(), self.max_items,
+            self.max_combine, self.max_row_vecs, self.max_partials, query.data_ptr(),
+            query.stride(0), query.stride(1), key_pool.data_ptr(), value_pool.data_ptr(),
+            dtype_code(key_pool.dtype), self.block_tables.data_ptr(), self.max_blocks,
+            self.qsl.data_ptr(), self.ctx.data_ptr(), self.n_q_heads, n_kv, head_dim, block_size,
+            num_blocks, float(scale), out.data_ptr(), out.stride(0), out.stride(1),
+            self.workspace.data_ptr(), self.workspace.numel(), stream_ptr(query.device),
+        )
+        return out
 
 
 # --- quantisation -----------------------------------------------------------------------------

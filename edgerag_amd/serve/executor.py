@@ -50,7 +50,11 @@ class ModelExecutor:
         device: torch.device,
         dtype: torch.dtype = torch.float16,
         chunk_size: int = DEFAULT_CHUNK_SIZE,
+        decode_graphs: bool = True,
+        max_decode_batch: int = 8,
     ) -> None:
+        """``decode_graphs``: replay decode-only iterations (up to ``max_decode_batch`` requests)
+        from HIP graphs captured per batch size; iterations with a prefill chunk run eagerly."""
         if chunk_size <= 0:
             raise ValueError(f"chunk_size must be positive, got {chunk_size}")
         self.decoder = decoder
@@ -66,6 +70,11 @@ class ModelExecutor:
                            for _ in range(spec.n_layers)]
         #: Logits of the last step's emitting rows (kept for inspection; no copy is made).
         self.last_logits: torch.Tensor | None = None
+        self.decode_graphs = decode_graphs and self.device.type == "cuda"
+        self.max_decode_batch = max_decode_batch
+        self._fixed: kernels.FixedAttention | None = None
+        self._graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor]] = {}
+        self.graph_steps = 0
 
     @property
     def pool_bytes(self) -> int:
@@ -118,11 +127,21 @@ class ModelExecutor:
         for r, t in enumerate(tables):
             bt[r, : len(t)] = t
         spec = self.spec
+        extras = [np.concatenate(slots).astype(np.int32), np.concatenate(pos),
+                  np.asarray(ids, np.int32), np.asarray(rows, np.int32)]
+        if (self.decode_graphs and not batch.prefill and len(entries) <= self.max_decode_batch
+                and self._stage_fixed(qsl, ctx, bt, extras)):
+            logits = self._replay_decode(len(entries))
+            self.last_logits = logits
+            tokens = logits.argmax(dim=-1).to(torch.int32).cpu().tolist()
+            for request, token in zip(emitting, tokens):
+                output.tokens[request.request_id] = int(token)
+            self.graph_steps += 1
+            return output
         plan, (slot_d, pos_d, ids_d, rows_d) = kernels.plan_attention(
             np.asarray(qsl, np.int32), np.asarray(ctx, np.int32), bt, spec.n_q_heads,
             spec.n_kv_heads, spec.head_dim, self.allocator.block_size, self.dtype, self.device,
-            [np.concatenate(slots).astype(np.int32), np.concatenate(pos),
-             np.asarray(ids, np.int32), np.asarray(rows, np.int32)],
+            extras,
         )
         step = StepInputs(ids_d, pos_d, slot_d, rows_d, plan)
         if emitting:
@@ -137,6 +156,42 @@ class ModelExecutor:
             if is_prefill:
                 output.prefilled[request.request_id] = len(toks)
         return output
+
+    # --- decode iterations replayed from HIP graphs ------------------------------------------
+
+    def _stage_fixed(self, qsl, ctx, bt, extras) -> bool:
+        if self._fixed is None:
+            spec = self.spec
+            max_blocks = -(-spec.max_position_embeddings // self.allocator.block_size)
+            cap = self.max_decode_batch
+            self._fixed = kernels.FixedAttention(
+                self.device, spec.n_q_heads, spec.n_kv_heads, spec.head_dim,
+                self.allocator.block_size, self.dtype, cap, max_blocks, [cap, cap, cap, cap])
+        return self._fixed.update(np.asarray(qsl, np.int32), np.asarray(ctx, np.int32), bt,
+                                  extras)
+
+    def _replay_decode(self, n: int) -> torch.Tensor:
+        """Logits ``(n, vocab)`` of a staged decode-only step of ``n`` requests."""
+        entry = self._graphs.get(n)
+        if entry is None:
+            fx = self._fixed
+            slots, pos, ids, rows = (e[:n] for e in fx.extras)
+            step = StepInputs(ids, pos, slots, rows, fx)
+            stream = torch.cuda.Stream(self.device)
+            stream.wait_stream(torch.cuda.current_stream(self.device))
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.stream(stream):
+                # The staged metadata is already valid, so run once eagerly first (lets torch and
+                # hipBLASLt settle their workspaces outside the capture); it computes this step's
+                # logits, which the replay below recomputes identically.
+                self.decoder.logits(step, self.key_pool, self.value_pool)
+                with torch.cuda.graph(graph, stream=stream):
+                    logits = self.decoder.logits(step, self.key_pool, self.value_pool)
+            torch.cuda.current_stream(self.device).wait_stream(stream)
+            entry = self._graphs[n] = (graph, logits)
+        graph, logits = entry
+        graph.replay()
+        return logits
 
     def to_dict(self) -> dict[str, Any]:
         return {

@@ -144,6 +144,34 @@ int edgerag_paged_attention(const int32_t* plan_host, const int32_t* plan_dev, i
                             void* out, int64_t out_stride_tok, int64_t out_stride_head,
                             void* workspace, int64_t workspace_bytes, void* stream);
 
+/*
+ * Fixed-capacity form of edgerag_paged_attention for decode-only batches, for HIP graph capture.
+ * The launch configuration depends only on the capacities, never on the plan: max_row_items
+ * waves run the decode-row kernel and max_combine_rows x ceil(n_q_heads/4) the split merge, and
+ * every wave reads its item (or returns) from the plan in device memory. A caller can therefore
+ * capture this call once and, before each replay, rewrite plan_dev, query_start_loc,
+ * context_lens and block_tables in place with a new edgerag_attn_plan output, provided that plan
+ * has no prefill tiles (every request has c * n_q_heads / n_kv_heads <= 8 query vectors), at most
+ * max_row_items items, at most max_combine_rows combine rows, at most max_partials split
+ * partials and no request with more than max_row_vecs query vectors. The workspace holds
+ * max_partials partials: (m, l) pairs at offset 0, accumulators at round_up(8 * max_partials,
+ * 256); size it with that formula. Semantics are those of edgerag_paged_attention.
+ *
+ * No counterpart in the reference: it exists so that the decode step of the serving loop
+ * (edgerag/serve/executor.py:138-154 replaced by one packed forward) can be replayed from a graph.
+ */
+int edgerag_paged_attention_fixed(const int32_t* plan_dev, int32_t max_row_items,
+                                  int32_t max_combine_rows, int32_t max_row_vecs,
+                                  int64_t max_partials, const void* q, int64_t q_stride_tok,
+                                  int64_t q_stride_head, const void* key_pool,
+                                  const void* value_pool, int32_t dtype,
+                                  const int32_t* block_tables, int64_t block_tables_stride,
+                                  const int32_t* query_start_loc, const int32_t* context_lens,
+                                  int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                                  int32_t block_size, int32_t num_blocks, float scale,
+                                  void* out, int64_t out_stride_tok, int64_t out_stride_head,
+                                  void* workspace, int64_t workspace_bytes, void* stream);
+
 /* ==== Weight-only INT8 / INT4 quantisation and linear ===================================== */
 
 /*

@@ -103,3 +103,31 @@ def test_fp16_at_smollm2_width_agrees_with_the_oracle(device) -> None:
     top2 = torch.topk(ref, 2).values
     if float(top2[0] - top2[1]) > 0.05:
         assert got[0] == int(ref.argmax())
+
+
+def _generate_mode(model, spec, prompts, max_new, chunk, device, graphs):
+    alloc = BlockAllocator(256, 16)
+    executor = ModelExecutor(model, spec, alloc, device, model.dtype, chunk_size=chunk,
+                             decode_graphs=graphs)
+    sched = Scheduler(alloc, SchedulerConfig(max_batch_size=8))
+    reqs = [Request(f"r{i}", p, max_new_tokens=n) for i, (p, n) in enumerate(zip(prompts, max_new))]
+    for r in reqs:
+        sched.add_request(r)
+    steps = []
+    drive(sched, executor, on_step=lambda b, o: steps.append(dict(o.tokens)))
+    return [r.generated_token_ids for r in reqs], executor, steps
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_decode_graph_replays_equal_the_eager_path(device, dtype) -> None:
+    """Decode-only iterations replayed from HIP graphs (one per batch size, rewritten metadata
+    between replays, requests finishing so the batch shrinks) produce exactly the eager path's
+    tokens at every step."""
+    model, _ = _model(device, seed=6, dtype=dtype)
+    prompts = [_prompt(n, 20 + n) for n in (12, 40, 7, 90, 25)]
+    max_new = [9, 4, 12, 6, 15]
+    eager, ex_e, steps_e = _generate_mode(model, TOY, prompts, max_new, 16, device, False)
+    graph, ex_g, steps_g = _generate_mode(model, TOY, prompts, max_new, 16, device, True)
+    assert ex_e.graph_steps == 0 and ex_g.graph_steps > 5 and len(ex_g._graphs) >= 2
+    assert steps_g == steps_e
+    assert graph == eager
