@@ -63,6 +63,17 @@ SIGNATURES: dict[str, tuple[list, object]] = {
          c_vp],
         c_i32,
     ),
+    "edgerag_rmsnorm": (
+        [c_vp, c_i64, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_i32, c_i32, c_f32, c_i32,
+         c_vp],
+        c_i32,
+    ),
+    "edgerag_rope_append": (
+        [c_vp, c_i64, c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_i64, c_vp,
+         c_vp, c_vp, c_i32, c_i32, c_i32, c_vp],
+        c_i32,
+    ),
+    "edgerag_silu_mul": ([c_vp, c_i64, c_i32, c_i32, c_vp, c_i64, c_i32, c_vp], c_i32),
     "edgerag_quantize": ([c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp, c_vp], c_i32),
     "edgerag_dequantize": ([c_vp, c_vp, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp], c_i32),
     "edgerag_quant_linear": (

@@ -12,8 +12,9 @@ The arithmetic follows the reference layer by layer (``edgerag/core/layers.py``)
   ``rotate_half(x) = [-x2, x1]`` (``layers.py:93-114``);
 * :func:`silu_mul` -- ``silu(gate) * up`` of SwiGLU (``layers.py:341``).
 
-These run as PyTorch-ROCm elementwise ops: they move a few MB per step against the 1.6 GB of
-weights and the KV the HIP kernels stream, and are not on the north_star kernel list.
+The decoder's forward runs the fused HIP kernels (``edgerag_rmsnorm`` with the residual add,
+``edgerag_rope_append``, ``edgerag_silu_mul``); the modules here hold the parameters and tables
+those kernels read, and their ``forward`` methods state the same arithmetic in PyTorch.
 """
 
 from __future__ import annotations

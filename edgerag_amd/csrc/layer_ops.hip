@@ -1,0 +1,246 @@
+// Fused elementwise ops around the hot path of one decoder layer, on packed token-major rows.
+//
+// * rmsnorm_kernel: optional residual add, then RMSNorm, one workgroup per row:
+//     h = x (+ delta), rounded to T once like the reference's `hidden + attn_out`
+//     y = weight * T(h * rsqrt(mean(h^2) + eps))   (edgerag/core/layers.py:40-47: fp32 variance,
+//                                                   cast back before the weight multiply)
+// * rope_append_kernel: the fused q/k/v projection output -> RoPE on q and k (halves convention,
+//   out = T(T(x * cos) + T(rotate_half(x) * sin)), layers.py:93-114), q written token-major for
+//   the attention kernel, post-RoPE k and raw v scattered into the paged pools by slot
+//   (layers.py:301-306 -> paged.py:186-206). Same roundings as the reference's fp16 tensor ops.
+// * silu_mul_kernel: SwiGLU's act = T(T(silu(gate)) * up) on the fused [gate | up] projection
+//   (layers.py:341).
+// All three are memory-bound and small (a few MB per step); their point is the launch count.
+#include "common.h"
+
+namespace edgerag {
+namespace {
+
+constexpr int kNormThreads = 256;
+
+template <typename T>
+__device__ __forceinline__ T round_to(float v) {
+  return from_f32<T>(v);
+}
+
+// One workgroup per row. Each thread holds up to kPer elements of the row in registers.
+template <typename T, int kPer>
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(
+    const T* __restrict__ x, const T* __restrict__ delta, const T* __restrict__ weight,
+    T* __restrict__ h_out, T* __restrict__ y, int32_t width, int64_t x_stride, int64_t d_stride,
+    int64_t h_stride, int64_t y_stride, float eps) {
+#pragma clang fp contract(off)
+  const int64_t row = blockIdx.x;
+  const T* xr = x + row * x_stride;
+  const T* dr = delta != nullptr ? delta + row * d_stride : nullptr;
+  float v[kPer];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int c = threadIdx.x + j * kNormThreads;
+    float hv = 0.f;
+    if (c < width) {
+      hv = to_f32<T>(xr[c]);
+      if (dr != nullptr) hv = to_f32<T>(round_to<T>(hv + to_f32<T>(dr[c])));
+    }
+    v[j] = hv;
+    ss = fmaf(hv, hv, ss);
+  }
+  ss = xor_sum<0, 6>(ss);
+  __shared__ float part[kNormThreads / kWave];
+  if ((threadIdx.x & (kWave - 1)) == 0) part[threadIdx.x / kWave] = ss;
+  __syncthreads();
+  float total = 0.f;
+#pragma unroll
+  for (int w = 0; w < kNormThreads / kWave; ++w) total += part[w];
+  const float r = rsqrtf(total / float(width) + eps);
+  T* hr = h_out != nullptr ? h_out + row * h_stride : nullptr;
+  T* yr = y + row * y_stride;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int c = threadIdx.x + j * kNormThreads;
+    if (c < width) {
+      if (hr != nullptr) hr[c] = round_to<T>(v[j]);
+      const float nv = to_f32<T>(round_to<T>(v[j] * r));
+      yr[c] = round_to<T>(to_f32<T>(weight[c]) * nv);
+    }
+  }
+}
+
+// One thread per (token, head, pair i in [0, d/2)) of the q, k and v heads of the fused
+// projection row [q heads | k heads | v heads].
+template <typename T>
+__global__ __launch_bounds__(256) void rope_append_kernel(
+    const T* __restrict__ qkv, int64_t qkv_stride, const int32_t* __restrict__ positions,
+    const T* __restrict__ cos_t, const T* __restrict__ sin_t, int32_t max_pos, int32_t n_tokens,
+    int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim, T* __restrict__ q_out,
+    int64_t q_stride_tok, const int32_t* __restrict__ slots, T* __restrict__ kpool,
+    T* __restrict__ vpool, int32_t num_blocks, int32_t block_size) {
+#pragma clang fp contract(off)
+  const int half = head_dim / 2;
+  const int heads = n_q_heads + 2 * n_kv_heads;
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= int64_t(n_tokens) * heads * half) return;
+  const int p = int(i % half);
+  const int64_t th = i / half;
+  const int hd = int(th % heads);
+  const int t = int(th / heads);
+  const T* src = qkv + int64_t(t) * qkv_stride + int64_t(hd) * head_dim;
+  const float x1 = to_f32<T>(src[p]), x2 = to_f32<T>(src[p + half]);
+  if (hd >= n_q_heads + n_kv_heads) {  // v: copied as is
+    const int64_t slot = slots[t];
+    if (slot < 0 || slot >= int64_t(num_blocks) * block_size) return;
+    const int h = hd - n_q_heads - n_kv_heads;
+    T* dst = vpool + ((int64_t(h) * num_blocks + slot / block_size) * block_size +
+                      slot % block_size) * head_dim;
+    dst[p] = src[p];
+    dst[p + half] = src[p + half];
+    return;
+  }
+  int pos = positions[t];
+  pos = pos < 0 ? 0 : (pos >= max_pos ? max_pos - 1 : pos);
+  const T* cr = cos_t + int64_t(pos) * head_dim;
+  const T* sr = sin_t + int64_t(pos) * head_dim;
+  // out[p] = x1 cos[p] + (-x2) sin[p]; out[p + half] = x2 cos[p + half] + x1 sin[p + half]
+  // No contraction (pragma above): each product is rounded before the add, like the
+  // reference's separate tensor ops, also on the fp32 path.
+  const float a1 = to_f32<T>(round_to<T>(x1 * to_f32<T>(cr[p])));
+  const float b1 = to_f32<T>(round_to<T>(-x2 * to_f32<T>(sr[p])));
+  const float a2 = to_f32<T>(round_to<T>(x2 * to_f32<T>(cr[p + half])));
+  const float b2 = to_f32<T>(round_to<T>(x1 * to_f32<T>(sr[p + half])));
+  const T o1 = round_to<T>(a1 + b1), o2 = round_to<T>(a2 + b2);
+  if (hd < n_q_heads) {
+    T* dst = q_out + int64_t(t) * q_stride_tok + int64_t(hd) * head_dim;
+    dst[p] = o1;
+    dst[p + half] = o2;
+  } else {
+    const int64_t slot = slots[t];
+    if (slot < 0 || slot >= int64_t(num_blocks) * block_size) return;
+    const int h = hd - n_q_heads;
+    T* dst = kpool + ((int64_t(h) * num_blocks + slot / block_size) * block_size +
+                      slot % block_size) * head_dim;
+    dst[p] = o1;
+    dst[p + half] = o2;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void silu_mul_kernel(const T* __restrict__ gu, int64_t gu_stride,
+                                                       int32_t n_tokens, int32_t inter,
+                                                       T* __restrict__ out, int64_t out_stride) {
+#pragma clang fp contract(off)
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= int64_t(n_tokens) * inter) return;
+  const int64_t t = i / inter;
+  const int c = int(i % inter);
+  const float g = to_f32<T>(gu[t * gu_stride + c]);
+  const float u = to_f32<T>(gu[t * gu_stride + inter + c]);
+  const float s = to_f32<T>(round_to<T>(g / (1.f + expf(-g))));
+  out[t * out_stride + c] = round_to<T>(s * u);
+}
+
+template <typename T>
+int launch_rmsnorm(const void* x, const void* delta, const void* weight, void* h_out, void* y,
+                   int32_t rows, int32_t width, int64_t xs, int64_t ds, int64_t hs, int64_t ys,
+                   float eps, hipStream_t s) {
+  const int per = (width + kNormThreads - 1) / kNormThreads;
+#define EDGERAG_NORM(P)                                                                         \
+  hipLaunchKernelGGL((rmsnorm_kernel<T, P>), dim3(rows), dim3(kNormThreads), 0, s,              \
+                     static_cast<const T*>(x), static_cast<const T*>(delta),                    \
+                     static_cast<const T*>(weight), static_cast<T*>(h_out), static_cast<T*>(y), \
+                     width, xs, ds, hs, ys, eps)
+  if (per <= 4) EDGERAG_NORM(4);
+  else if (per <= 8) EDGERAG_NORM(8);
+  else if (per <= 16) EDGERAG_NORM(16);
+  else if (per <= 32) EDGERAG_NORM(32);
+  else return fail(EDGERAG_EUNSUPPORTED, "edgerag_rmsnorm: width %d above 8192", width);
+#undef EDGERAG_NORM
+  return check_launch("edgerag_rmsnorm");
+}
+
+}  // namespace
+}  // namespace edgerag
+
+using namespace edgerag;
+
+extern "C" int edgerag_rmsnorm(const void* x, int64_t x_stride, const void* delta,
+                               int64_t delta_stride, const void* weight, void* h_out,
+                               int64_t h_stride, void* y, int64_t y_stride, int32_t rows,
+                               int32_t width, float eps, int32_t dtype, void* stream) {
+  clear_error();
+  if (rows < 0 || width <= 0) return fail(EDGERAG_EINVAL, "edgerag_rmsnorm: rows %d width %d", rows, width);
+  if (rows == 0) return EDGERAG_OK;
+  if (x == nullptr || weight == nullptr || y == nullptr)
+    return fail(EDGERAG_EINVAL, "edgerag_rmsnorm: NULL pointer");
+  if (delta != nullptr && h_out == nullptr)
+    return fail(EDGERAG_EINVAL, "edgerag_rmsnorm: a residual add needs h_out");
+  auto s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case EDGERAG_F32: return launch_rmsnorm<float>(x, delta, weight, h_out, y, rows, width, x_stride, delta_stride, h_stride, y_stride, eps, s);
+    case EDGERAG_F16: return launch_rmsnorm<f16>(x, delta, weight, h_out, y, rows, width, x_stride, delta_stride, h_stride, y_stride, eps, s);
+    case EDGERAG_BF16: return launch_rmsnorm<bf16>(x, delta, weight, h_out, y, rows, width, x_stride, delta_stride, h_stride, y_stride, eps, s);
+  }
+  return fail(EDGERAG_EINVAL, "edgerag_rmsnorm: dtype %d", dtype);
+}
+
+extern "C" int edgerag_rope_append(const void* qkv, int64_t qkv_stride, const int32_t* positions,
+                                   const void* cos_table, const void* sin_table, int32_t max_pos,
+                                   int32_t n_tokens, int32_t n_q_heads, int32_t n_kv_heads,
+                                   int32_t head_dim, void* q_out, int64_t q_stride_tok,
+                                   const int32_t* slots, void* key_pool, void* value_pool,
+                                   int32_t num_blocks, int32_t block_size, int32_t dtype,
+                                   void* stream) {
+  clear_error();
+  if (n_tokens < 0 || n_q_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0 || head_dim % 2 ||
+      max_pos <= 0 || num_blocks <= 0 || block_size <= 0)
+    return fail(EDGERAG_EINVAL, "edgerag_rope_append: bad shape");
+  if (n_tokens == 0) return EDGERAG_OK;
+  if (qkv == nullptr || positions == nullptr || cos_table == nullptr || sin_table == nullptr ||
+      q_out == nullptr || slots == nullptr || key_pool == nullptr || value_pool == nullptr)
+    return fail(EDGERAG_EINVAL, "edgerag_rope_append: NULL pointer");
+  const int64_t total = int64_t(n_tokens) * (n_q_heads + 2 * n_kv_heads) * (head_dim / 2);
+  const dim3 grid(unsigned((total + 255) / 256)), block(256);
+  auto s = static_cast<hipStream_t>(stream);
+#define EDGERAG_ROPE(TYPE)                                                                      \
+  hipLaunchKernelGGL((rope_append_kernel<TYPE>), grid, block, 0, s,                             \
+                     static_cast<const TYPE*>(qkv), qkv_stride, positions,                     \
+                     static_cast<const TYPE*>(cos_table), static_cast<const TYPE*>(sin_table), \
+                     max_pos, n_tokens, n_q_heads, n_kv_heads, head_dim,                       \
+                     static_cast<TYPE*>(q_out), q_stride_tok, slots,                           \
+                     static_cast<TYPE*>(key_pool), static_cast<TYPE*>(value_pool), num_blocks,  \
+                     block_size)
+  switch (dtype) {
+    case EDGERAG_F32: EDGERAG_ROPE(float); break;
+    case EDGERAG_F16: EDGERAG_ROPE(f16); break;
+    case EDGERAG_BF16: EDGERAG_ROPE(bf16); break;
+    default: return fail(EDGERAG_EINVAL, "edgerag_rope_append: dtype %d", dtype);
+  }
+#undef EDGERAG_ROPE
+  return check_launch("edgerag_rope_append");
+}
+
+extern "C" int edgerag_silu_mul(const void* gate_up, int64_t gate_up_stride, int32_t n_tokens,
+                                int32_t intermediate, void* out, int64_t out_stride,
+                                int32_t dtype, void* stream) {
+  clear_error();
+  if (n_tokens < 0 || intermediate <= 0)
+    return fail(EDGERAG_EINVAL, "edgerag_silu_mul: bad shape");
+  if (n_tokens == 0) return EDGERAG_OK;
+  if (gate_up == nullptr || out == nullptr)
+    return fail(EDGERAG_EINVAL, "edgerag_silu_mul: NULL pointer");
+  const int64_t total = int64_t(n_tokens) * intermediate;
+  const dim3 grid(unsigned((total + 255) / 256)), block(256);
+  auto s = static_cast<hipStream_t>(stream);
+#define EDGERAG_SILU(TYPE)                                                                      \
+  hipLaunchKernelGGL((silu_mul_kernel<TYPE>), grid, block, 0, s,                                \
+                     static_cast<const TYPE*>(gate_up), gate_up_stride, n_tokens, intermediate, \
+                     static_cast<TYPE*>(out), out_stride)
+  switch (dtype) {
+    case EDGERAG_F32: EDGERAG_SILU(float); break;
+    case EDGERAG_F16: EDGERAG_SILU(f16); break;
+    case EDGERAG_BF16: EDGERAG_SILU(bf16); break;
+    default: return fail(EDGERAG_EINVAL, "edgerag_silu_mul: dtype %d", dtype);
+  }
+#undef EDGERAG_SILU
+  return check_launch("edgerag_silu_mul");
+}

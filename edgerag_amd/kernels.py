@@ -25,6 +25,9 @@ from edgerag_amd._lib import call, dtype_code, ptr, require_device, stream_ptr  
 __all__ = [
     "AttentionPlan",
     "FixedAttention",
+    "rmsnorm",
+    "rope_append",
+    "silu_mul",
     "dequantize",
     "kv_append",
     "kv_copy_blocks",
@@ -419,6 +422,74 @@ class FixedAttention:
             self.workspace.data_ptr(), self.workspace.numel(), stream_ptr(query.device),
         )
         return out
+
+
+# --- fused layer ops ----------------------------------------------------------------------------
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, delta: torch.Tensor | None = None,
+            h_out: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``out = RMSNorm(x (+ delta))`` row-wise over ``(rows, width)``; with ``delta`` the sum
+    is also written to ``h_out`` (which may be ``x``)."""
+    require_device(x, weight, delta, h_out, out)
+    if x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError("rmsnorm takes (rows, width) with contiguous rows")
+    rows, width = x.shape
+    if out is None:
+        out = torch.empty_like(x)
+    if delta is not None:
+        if delta.shape != x.shape or delta.stride(1) != 1 or h_out is None:
+            raise ValueError("delta must match x, and h_out is required with delta")
+    call(
+        "edgerag_rmsnorm", x.data_ptr(), x.stride(0), ptr(delta),
+        delta.stride(0) if delta is not None else 0, weight.data_ptr(), ptr(h_out),
+        h_out.stride(0) if h_out is not None else 0, out.data_ptr(), out.stride(0), rows, width,
+        float(eps), dtype_code(x.dtype), stream_ptr(x.device),
+    )
+    return out
+
+
+def rope_append(qkv: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                n_q_heads: int, n_kv_heads: int, head_dim: int, slots: torch.Tensor,
+                key_pool: torch.Tensor, value_pool: torch.Tensor,
+                q_out: torch.Tensor | None = None) -> torch.Tensor:
+    """RoPE on the fused projection rows; q returned ``(T, n_q_heads, head_dim)``, post-RoPE k
+    and v written into the pools at ``slots``."""
+    require_device(qkv, positions, cos, sin, slots, key_pool, value_pool, q_out)
+    T = qkv.shape[0]
+    if qkv.dim() != 2 or qkv.stride(1) != 1 or qkv.shape[1] != (n_q_heads + 2 * n_kv_heads) * head_dim:
+        raise ValueError("qkv must be (tokens, (n_q + 2 n_kv) * head_dim) with contiguous rows")
+    for p in (key_pool, value_pool):
+        _check_pool(p, "pool")
+    nkv, num_blocks, block_size, d = key_pool.shape
+    if nkv != n_kv_heads or d != head_dim or cos.shape != sin.shape or cos.shape[1] != head_dim:
+        raise ValueError("pool / rotary table shapes do not match the heads")
+    if positions.dtype != torch.int32 or slots.dtype != torch.int32:
+        raise ValueError("positions and slots must be int32")
+    if q_out is None:
+        q_out = torch.empty((T, n_q_heads, head_dim), dtype=qkv.dtype, device=qkv.device)
+    call(
+        "edgerag_rope_append", qkv.data_ptr(), qkv.stride(0), positions.data_ptr(),
+        cos.data_ptr(), sin.data_ptr(), cos.shape[0], T, n_q_heads, n_kv_heads, head_dim,
+        q_out.data_ptr(), q_out.stride(0), slots.data_ptr(), key_pool.data_ptr(),
+        value_pool.data_ptr(), num_blocks, block_size, dtype_code(qkv.dtype),
+        stream_ptr(qkv.device),
+    )
+    return q_out
+
+
+def silu_mul(gate_up: torch.Tensor, intermediate: int,
+             out: torch.Tensor | None = None) -> torch.Tensor:
+    """SwiGLU activation of the fused ``[gate | up]`` rows: ``(T, 2I) -> (T, I)``."""
+    require_device(gate_up, out)
+    T = gate_up.shape[0]
+    if gate_up.dim() != 2 or gate_up.stride(1) != 1 or gate_up.shape[1] != 2 * intermediate:
+        raise ValueError("gate_up must be (tokens, 2 * intermediate) with contiguous rows")
+    if out is None:
+        out = torch.empty((T, intermediate), dtype=gate_up.dtype, device=gate_up.device)
+    call("edgerag_silu_mul", gate_up.data_ptr(), gate_up.stride(0), T, intermediate,
+         out.data_ptr(), out.stride(0), dtype_code(gate_up.dtype), stream_ptr(gate_up.device))
+    return out
 
 
 # --- quantisation -----------------------------------------------------------------------------

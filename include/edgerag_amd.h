@@ -212,6 +212,46 @@ int edgerag_quant_linear(const void* x, int32_t x_dtype, int64_t x_stride, int32
                          int32_t n, int32_t bits, int32_t group_size, void* y, int64_t y_stride,
                          void* stream);
 
+/* ==== Fused elementwise ops of a decoder layer ============================================ */
+
+/*
+ * Row-wise residual add + RMSNorm over `rows` rows of `width` elements (`dtype`):
+ *   h = x (+ delta)                     rounded to dtype once; written to h_out when delta != NULL
+ *   y = weight * dtype(h * rsqrt(mean(h^2) + eps))   variance and scaling in fp32
+ * h_out may alias x. Replaces `hidden = hidden + out` followed by RMSNorm.forward
+ * (edgerag/core/layers.py:40-47, :372-373). width <= 8192.
+ */
+int edgerag_rmsnorm(const void* x, int64_t x_stride, const void* delta, int64_t delta_stride,
+                    const void* weight, void* h_out, int64_t h_stride, void* y, int64_t y_stride,
+                    int32_t rows, int32_t width, float eps, int32_t dtype, void* stream);
+
+/*
+ * RoPE on the fused q/k/v projection output and the KV append, in one launch. Row t of qkv holds
+ * [n_q_heads | n_kv_heads | n_kv_heads] heads of head_dim elements. For position p =
+ * positions[t] (clamped to the table), q and k heads become dtype(dtype(x * cos[p]) +
+ * dtype(rotate_half(x) * sin[p])) with rotate_half(x) = [-x2, x1] (the halves convention); q is
+ * written to q_out[t, h, :] (row stride q_stride_tok, head stride head_dim), k and the raw v to
+ * key_pool / value_pool [n_kv_heads, num_blocks, block_size, head_dim] at slot slots[t] (skipped
+ * when negative or outside the pool). cos/sin tables are [max_pos, head_dim] in dtype.
+ * Replaces apply_rope + cache.update's write (edgerag/core/layers.py:93-114, :301-306;
+ * edgerag/cache/paged.py:186-206).
+ */
+int edgerag_rope_append(const void* qkv, int64_t qkv_stride, const int32_t* positions,
+                        const void* cos_table, const void* sin_table, int32_t max_pos,
+                        int32_t n_tokens, int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                        void* q_out, int64_t q_stride_tok, const int32_t* slots, void* key_pool,
+                        void* value_pool, int32_t num_blocks, int32_t block_size, int32_t dtype,
+                        void* stream);
+
+/*
+ * SwiGLU activation of the fused [gate | up] projection: out[t, c] = dtype(dtype(silu(g)) * u),
+ * g = gate_up[t, c], u = gate_up[t, intermediate + c]. Replaces silu(gate_proj(x)) * up_proj(x)
+ * (edgerag/core/layers.py:341).
+ */
+int edgerag_silu_mul(const void* gate_up, int64_t gate_up_stride, int32_t n_tokens,
+                     int32_t intermediate, void* out, int64_t out_stride, int32_t dtype,
+                     void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,91 @@
+"""Fused layer ops (residual add + RMSNorm, RoPE + KV append, SiLU * up) against the decoder
+oracle's restatement of ``edgerag/core/layers.py`` on the same inputs."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from edgerag_amd import kernels
+from edgerag_amd.core.layers import RotaryTable
+from oracle import model as om
+from tests.conftest import seeded
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("width", [128, 2048, 8192, 1000])
+def test_add_rmsnorm(device, dtype, width) -> None:
+    g = seeded(width)
+    x = torch.randn(13, width, generator=g).to(dtype)
+    delta = torch.randn(13, width, generator=g).to(dtype)
+    w = (1 + 0.1 * torch.randn(width, generator=g)).to(dtype)
+    h_ref = x + delta  # rounded to dtype, like the reference's residual add
+    y_ref = om.rms_norm(h_ref, w, 1e-5)
+    xd = x.to(device)
+    y = kernels.rmsnorm(xd, w.to(device), 1e-5, delta=delta.to(device), h_out=xd)
+    assert torch.equal(xd.cpu(), h_ref)
+    tol = dict(rtol=0, atol=0) if dtype == torch.float32 else dict(rtol=2e-3, atol=2e-3)
+    if dtype == torch.float32:
+        torch.testing.assert_close(y.cpu(), y_ref, rtol=1e-5, atol=1e-5)
+    else:
+        torch.testing.assert_close(y.cpu().float(), y_ref.float(), **tol)
+    y2 = kernels.rmsnorm(x.to(device), w.to(device), 1e-5)
+    torch.testing.assert_close(y2.cpu().float(), om.rms_norm(x, w, 1e-5).float(),
+                               rtol=2e-3, atol=2e-3)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("n_q,n_kv", [(32, 32), (9, 3)])
+def test_rope_append_matches_reference_rope_and_slot_write(device, dtype, n_q, n_kv) -> None:
+    d, T, theta, bs, nb = 64, 11, 130000.0, 16, 8
+    g = seeded(n_q)
+    qkv = torch.randn(T, (n_q + 2 * n_kv) * d, generator=g).to(dtype)
+    positions = torch.tensor([0, 1, 5, 17, 300, 301, 4095, 4096, 7000, 7471, 12], dtype=torch.int32)
+    perm = torch.randperm(nb * bs, generator=g)[:T]
+    slots = perm.to(torch.int32)
+    slots[3] = -1  # padding: skipped
+    table = RotaryTable(d, theta, 8192, device, dtype)
+    kp = torch.zeros(n_kv, nb, bs, d, dtype=dtype, device=device)
+    vp = torch.zeros_like(kp)
+    q = kernels.rope_append(qkv.to(device), positions.to(device), table.cos, table.sin, n_q, n_kv,
+                            d, slots.to(device), kp, vp)
+    # The kernel's arithmetic is checked bit for bit on the table's own cos/sin values; the table
+    # against the reference's per-step cos/sin within a few ulp (torch's CPU cos differs by an
+    # ulp between vectorised and scalar paths, so the values themselves are not bit-stable).
+    cos, sin = table.cos[positions.long()].cpu(), table.sin[positions.long()].cpu()
+    ref_cos, ref_sin = om.rope_cos_sin(positions.long(), d, theta, dtype)
+    torch.testing.assert_close(cos.float(), ref_cos.float(), rtol=0, atol=2e-3 if dtype == torch.float16 else 1e-6)
+    torch.testing.assert_close(sin.float(), ref_sin.float(), rtol=0, atol=2e-3 if dtype == torch.float16 else 1e-6)
+    heads = qkv.view(T, n_q + 2 * n_kv, d)
+    q_ref = om.apply_rope(heads[:, :n_q].transpose(0, 1)[None], cos, sin)[0].transpose(0, 1)
+    k_ref = om.apply_rope(heads[:, n_q : n_q + n_kv].transpose(0, 1)[None], cos, sin)[0]
+    v_ref = heads[:, n_q + n_kv :].transpose(0, 1)
+    assert torch.equal(q.cpu(), q_ref)
+    kc, vc = kp.cpu(), vp.cpu()
+    for t in range(T):
+        s = int(slots[t])
+        if s < 0:
+            continue
+        assert torch.equal(kc[:, s // bs, s % bs], k_ref[:, t])
+        assert torch.equal(vc[:, s // bs, s % bs], v_ref[:, t])
+    written = np.zeros((nb, bs), bool)
+    for s in slots.tolist():
+        if s >= 0:
+            written[s // bs, s % bs] = True
+    assert float(kc[:, ~written].abs().sum()) == 0.0
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_silu_mul(device, dtype) -> None:
+    g = seeded(7)
+    gu = (torch.randn(9, 2 * 8192, generator=g) * 3).to(dtype)
+    out = kernels.silu_mul(gu.to(device), 8192).cpu()
+    ref = F.silu(gu[:, :8192]) * gu[:, 8192:]
+    if dtype == torch.float32:
+        torch.testing.assert_close(out, ref, rtol=1e-6, atol=1e-6)
+    else:
+        torch.testing.assert_close(out.float(), ref.float(), rtol=2e-3, atol=2e-3)
