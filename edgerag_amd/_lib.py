@@ -32,6 +32,8 @@ EDGERAG_EHIP = 2
 EDGERAG_EWORKSPACE = 3
 EDGERAG_EUNSUPPORTED = 4
 
+ATTN_TILES, ATTN_ROWS, ATTN_COMBINE, ATTN_ALL = 1, 2, 4, 7
+
 DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 
 #: name -> (argtypes, restype). Mirrors include/edgerag_amd.h one to one.
@@ -54,7 +56,8 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     ),
     "edgerag_paged_attention": (
         [c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_vp, c_vp, c_i32, c_vp, c_i64, c_vp, c_vp, c_i32,
-         c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_f32, c_vp, c_i64, c_i64, c_vp, c_i64, c_vp],
+         c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_f32, c_vp, c_i64, c_i64, c_vp, c_i64, c_i32,
+         c_vp],
         c_i32,
     ),
     "edgerag_paged_attention_fixed": (

@@ -570,10 +570,10 @@ void dispatch_rows_qr(const Launch& a, int qr, int base, int count, int limit_wo
 // row kernel with 8 query vectors per pass otherwise. Row items: the fast decode kernel when
 // every split's load groups stay inside one block, the general kernel otherwise.
 template <typename T, int D>
-int run_items(const Launch& a, const int32_t* ph) {
+int run_items(const Launch& a, const int32_t* ph, int parts) {
   using C = RowCfg<T, D>;
   const int n_items = ph[H_N_ITEMS], n_row = ph[H_N_ROW_ITEMS];
-  if (n_items > n_row) {
+  if ((parts & EDGERAG_ATTN_TILES) && n_items > n_row) {
     if constexpr (__is_same(T, f16) && D == 64) {
       if (ph[H_TILE_KIND] == 1 && prefill_tiles_supported(a.nb, a.bs)) {
         launch_prefill_tiles_f16_d64(a, n_row, n_items - n_row);
@@ -586,7 +586,7 @@ int run_items(const Launch& a, const int32_t* ph) {
   }
   const int qr = std::min(8, pow2_at_least(std::max(1, ph[H_MAX_ROW_VECS])));
   const bool fast = a.bs % C::TPW == 0 && ph[H_MAX_SPLIT_BLOCKS] <= kMaxSplitBlocks;
-  if (n_row > 0) {
+  if ((parts & EDGERAG_ATTN_ROWS) && n_row > 0) {
     if (fast)
       dispatch_decode_qr<T, D>(a, qr, 0, n_row, H_N_ROW_ITEMS);
     else
@@ -596,14 +596,14 @@ int run_items(const Launch& a, const int32_t* ph) {
 }
 
 template <typename T>
-int run_dtype(const Launch& a, const int32_t* ph, int32_t D) {
+int run_dtype(const Launch& a, const int32_t* ph, int32_t D, int parts) {
   switch (D) {
-    case 8: return run_items<T, 8>(a, ph);
-    case 16: return run_items<T, 16>(a, ph);
-    case 32: return run_items<T, 32>(a, ph);
-    case 64: return run_items<T, 64>(a, ph);
-    case 128: return run_items<T, 128>(a, ph);
-    case 256: return run_items<T, 256>(a, ph);
+    case 8: return run_items<T, 8>(a, ph, parts);
+    case 16: return run_items<T, 16>(a, ph, parts);
+    case 32: return run_items<T, 32>(a, ph, parts);
+    case 64: return run_items<T, 64>(a, ph, parts);
+    case 128: return run_items<T, 128>(a, ph, parts);
+    case 256: return run_items<T, 256>(a, ph, parts);
   }
   return fail(EDGERAG_EUNSUPPORTED, "edgerag_paged_attention: head_dim %d", D);
 }
@@ -788,8 +788,11 @@ extern "C" int edgerag_paged_attention(
     const int32_t* query_start_loc, const int32_t* context_lens, int32_t num_reqs,
     int32_t num_tokens, int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
     int32_t block_size, int32_t num_blocks, float scale, void* out, int64_t out_stride_tok,
-    int64_t out_stride_head, void* workspace, int64_t workspace_bytes, void* stream) {
+    int64_t out_stride_head, void* workspace, int64_t workspace_bytes, int32_t parts,
+    void* stream) {
   clear_error();
+  if (parts <= 0 || (parts & ~EDGERAG_ATTN_ALL) != 0)
+    return fail(EDGERAG_EINVAL, "edgerag_paged_attention: parts mask %d", parts);
   if (plan_host == nullptr || plan_dev == nullptr || plan_words < kHeaderWords ||
       plan_host[H_MAGIC] != kPlanMagic || plan_host[H_VERSION] != kPlanVersion)
     return fail(EDGERAG_EINVAL, "edgerag_paged_attention: not a plan from edgerag_attn_plan");
@@ -843,13 +846,13 @@ extern "C" int edgerag_paged_attention(
   a.pacc = reinterpret_cast<float*>(wsp + ws.acc_off);
   int rc = EDGERAG_OK;
   switch (dtype) {
-    case EDGERAG_F32: rc = run_dtype<float>(a, plan_host, head_dim); break;
-    case EDGERAG_F16: rc = run_dtype<f16>(a, plan_host, head_dim); break;
-    case EDGERAG_BF16: rc = run_dtype<bf16>(a, plan_host, head_dim); break;
+    case EDGERAG_F32: rc = run_dtype<float>(a, plan_host, head_dim, parts); break;
+    case EDGERAG_F16: rc = run_dtype<f16>(a, plan_host, head_dim, parts); break;
+    case EDGERAG_BF16: rc = run_dtype<bf16>(a, plan_host, head_dim, parts); break;
     default: return fail(EDGERAG_EINVAL, "edgerag_paged_attention: dtype %d", dtype);
   }
   const int n_combine = plan_host[H_N_COMBINE];
-  if (rc != EDGERAG_OK || n_combine == 0) return rc;
+  if (rc != EDGERAG_OK || n_combine == 0 || !(parts & EDGERAG_ATTN_COMBINE)) return rc;
 
   const int waves = 4;
   const dim3 cblock(kWave * waves);

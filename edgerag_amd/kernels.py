@@ -282,8 +282,12 @@ def paged_attention(
     plan: AttentionPlan,
     scale: float,
     out: torch.Tensor | None = None,
+    overlap: bool = True,
 ) -> torch.Tensor:
-    """Ragged paged attention. ``query``/``out``: ``(num_tokens, n_q_heads, head_dim)``."""
+    """Ragged paged attention. ``query``/``out``: ``(num_tokens, n_q_heads, head_dim)``.
+
+    With ``overlap`` and a batch holding both prefill tiles and decode rows, the two run on two
+    streams (joined before the split merge), so MFMA work overlaps the KV streaming."""
     require_device(query, key_pool, value_pool)
     _check_pool(key_pool, "key_pool")
     _check_pool(value_pool, "value_pool")
@@ -307,8 +311,7 @@ def paged_attention(
     elif out.shape != query.shape or out.dtype != query.dtype or out.stride(2) != 1:
         raise ValueError("out must match query in shape and dtype, head_dim contiguous")
     ws = plan.workspace
-    call(
-        "edgerag_paged_attention",
+    args = (
         plan.plan_host.ctypes.data, plan.plan_dev.data_ptr(), plan.plan_host.size,
         query.data_ptr(), query.stride(0), query.stride(1),
         key_pool.data_ptr(), value_pool.data_ptr(), dtype_code(key_pool.dtype),
@@ -316,9 +319,38 @@ def paged_attention(
         plan.query_start_loc.data_ptr(), plan.context_lens.data_ptr(),
         plan.num_reqs, query.shape[0], plan.n_q_heads, n_kv, head_dim, block_size, num_blocks,
         float(scale), out.data_ptr(), out.stride(0), out.stride(1),
-        None if ws is None else ws.data_ptr(), plan.workspace_bytes, stream_ptr(query.device),
+        None if ws is None else ws.data_ptr(), plan.workspace_bytes,
     )
+    device = query.device
+    n_items, n_row = int(plan.plan_host[2]), int(plan.plan_host[13])
+    if overlap and 0 < n_row < n_items:
+        # Prefill tiles (MFMA-bound) on a side stream beside the decode rows (HBM-bound); the
+        # merge of split partials waits for both.
+        main = torch.cuda.current_stream(device)
+        side = _side_stream(device)
+        side.wait_stream(main)
+        # Rows first: their many short waves spread over every CU, and the tile workgroups
+        # (which fill a CU's register file) take CUs as the row waves retire.
+        call("edgerag_paged_attention", *args, _lib.ATTN_ROWS, stream_ptr(device))
+        with torch.cuda.stream(side):
+            call("edgerag_paged_attention", *args, _lib.ATTN_TILES, stream_ptr(device))
+        main.wait_stream(side)
+        call("edgerag_paged_attention", *args, _lib.ATTN_COMBINE, stream_ptr(device))
+    else:
+        call("edgerag_paged_attention", *args, _lib.ATTN_ALL, stream_ptr(device))
     return out
+
+
+_SIDE_STREAMS: dict[torch.device, torch.cuda.Stream] = {}
+
+
+def _side_stream(device: torch.device) -> torch.cuda.Stream:
+    """One extra stream per device (default priority) for work that overlaps the current one."""
+    device = torch.device(device)
+    stream = _SIDE_STREAMS.get(device)
+    if stream is None:
+        stream = _SIDE_STREAMS[device] = torch.cuda.Stream(device)
+    return stream
 
 
 class FixedAttention:

@@ -35,6 +35,12 @@ extern "C" {
 #define EDGERAG_EWORKSPACE 3    /* workspace or plan buffer smaller than required */
 #define EDGERAG_EUNSUPPORTED 4  /* valid request this build does not implement */
 
+/* ---- parts of a paged-attention launch (edgerag_paged_attention) ------------------------- */
+#define EDGERAG_ATTN_TILES 1
+#define EDGERAG_ATTN_ROWS 2
+#define EDGERAG_ATTN_COMBINE 4
+#define EDGERAG_ATTN_ALL 7
+
 /* ---- element types ----------------------------------------------------------------------- */
 #define EDGERAG_F32 0
 #define EDGERAG_F16 1
@@ -132,6 +138,14 @@ int edgerag_attn_plan(const int32_t* query_start_loc, const int32_t* context_len
  * Accumulation is fp32; out is written in `dtype` (the dtype of q and the pools). A query row with
  * no visible key is written as zeros, never NaN. Block ids outside [0, num_blocks) contribute
  * nothing. workspace must hold the *workspace_bytes the plan reported (NULL if that is 0).
+ *
+ * parts selects what is enqueued, so a caller can overlap the two kinds of work on two streams:
+ *   EDGERAG_ATTN_TILES    prefill query tiles (MFMA-bound);
+ *   EDGERAG_ATTN_ROWS     decode rows (HBM-bound);
+ *   EDGERAG_ATTN_COMBINE  the merge of split partials (of tiles and of rows alike), which must be
+ *                         enqueued after both of the other parts have completed;
+ *   EDGERAG_ATTN_ALL      all three in order on `stream`.
+ * Tiles and rows write disjoint outputs and partials.
  */
 int edgerag_paged_attention(const int32_t* plan_host, const int32_t* plan_dev, int64_t plan_words,
                             const void* q, int64_t q_stride_tok, int64_t q_stride_head,
@@ -142,7 +156,8 @@ int edgerag_paged_attention(const int32_t* plan_host, const int32_t* plan_dev, i
                             int32_t n_kv_heads, int32_t head_dim, int32_t block_size,
                             int32_t num_blocks, float scale,
                             void* out, int64_t out_stride_tok, int64_t out_stride_head,
-                            void* workspace, int64_t workspace_bytes, void* stream);
+                            void* workspace, int64_t workspace_bytes, int32_t parts,
+                            void* stream);
 
 /*
  * Fixed-capacity form of edgerag_paged_attention for decode-only batches, for HIP graph capture.

@@ -52,8 +52,22 @@ def test_validation_errors_come_back_as_messages() -> None:
             None, 0, None, None,    # block tables, stride, query_start_loc, context_lens
             0, 0, 4, 4, 64, 16, 1,  # num_reqs, num_tokens, heads, head_dim, block, num_blocks
             1.0, None, 0, 0,        # scale, out, strides
-            None, 0, None,          # workspace, bytes, stream
+            None, 0, 7, None,       # workspace, bytes, parts (all), stream
         )
+    with pytest.raises(_lib.EdgeragError, match="parts mask"):
+        _lib.call("edgerag_paged_attention", None, None, 0, None, 0, 0, None, None, 1, None, 0,
+                  None, None, 0, 0, 4, 4, 64, 16, 1, 1.0, None, 0, 0, None, 0, 8, None)
+    with pytest.raises(_lib.EdgeragError, match="capacities"):
+        _lib.call("edgerag_paged_attention_fixed", 16, -1, 0, 1, 0, 16, 0, 0, 16, 16, 1, 16, 0,
+                  16, 16, 4, 4, 64, 16, 1, 1.0, 16, 0, 0, None, 0, None)
+    with pytest.raises(_lib.EdgeragError, match="width"):
+        _lib.call("edgerag_rmsnorm", None, 0, None, 0, None, None, 0, None, 0, 1, 0, 1e-5, 1,
+                  None)
+    with pytest.raises(_lib.EdgeragError, match="bad shape"):
+        _lib.call("edgerag_rope_append", None, 0, None, None, None, 8, 1, 4, 4, 63, None, 0, None,
+                  None, None, 1, 16, 1, None)
+    with pytest.raises(_lib.EdgeragError, match="bad shape"):
+        _lib.call("edgerag_silu_mul", None, 0, 1, 0, None, 0, 1, None)
 
 
 def test_device_guard_refuses_cpu_tensors() -> None:
