@@ -24,6 +24,12 @@
 #ifndef EDGERAG_SKINNY_MAX_M
 #define EDGERAG_SKINNY_MAX_M 64
 #endif
+#ifndef EDGERAG_GEMM_MIN_WG
+#define EDGERAG_GEMM_MIN_WG 1  // workgroups per CU the GEMM's register budget must allow
+#endif
+#ifndef EDGERAG_GEMM_TARGET_WGS
+#define EDGERAG_GEMM_TARGET_WGS 256  // the tile is the largest whose grid reaches this many
+#endif
 
 namespace edgerag {
 namespace {
@@ -197,13 +203,13 @@ __device__ __forceinline__ void skinny_compute(const SkinnyBatch<BITS, NT, MT, U
 // (blockDim.x / 64 of them). Lane l feeds row l % 16 of a tile (A operand) and activation row
 // l % 16 of an m-tile (B operand); lane group l / 16 owns bytes [16 (l/16), +16) of every 64-byte
 // row chunk.
-template <int BITS, int NT, int MT, int U, int NB, bool PG>
-__global__ __launch_bounds__(kMaxSkinnyWaves * kWave) void qlinear_skinny_kernel(
+template <int BITS, int NT, int MT, int U, int NB, bool PG, int KWMAX>
+__global__ __launch_bounds__(KWMAX * kWave) void qlinear_skinny_kernel(
     const f16* __restrict__ x, int64_t xs, int32_t m, int32_t k,
     const uint8_t* __restrict__ packed, const f16* __restrict__ scales,
     const f16* __restrict__ bias, int32_t n, int32_t g, f16* __restrict__ y, int64_t ys) {
   using C = SkinnyCfg<BITS>;
-  __shared__ float red[kMaxSkinnyWaves * NT * MT * 4 * kWave];
+  __shared__ float red[KWMAX * NT * MT * 4 * kWave];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int kw = blockDim.x >> 6;
   const int li = lane & 15, lg = lane >> 4;
@@ -369,7 +375,7 @@ __device__ __forceinline__ void gemm_store(const GemmStage<BITS, BN, BM>& st, _F
 // l % 32, k chunk 2 ks + l / 32 of a 16-k step; accumulator register i of lane l holds
 // row 8 (i / 4) + 4 (l / 32) + i % 4 of A (weight row) and column l % 32 (activation row).
 template <int BITS, int BN, int BM>
-__global__ __launch_bounds__(kGemmThreads) void qlinear_gemm_kernel(
+__global__ __launch_bounds__(kGemmThreads, EDGERAG_GEMM_MIN_WG) void qlinear_gemm_kernel(
     const f16* __restrict__ x, int64_t xs, int32_t m, int32_t k,
     const uint8_t* __restrict__ packed, const f16* __restrict__ scales,
     const f16* __restrict__ bias, int32_t n, int32_t g, f16* __restrict__ y, int64_t ys) {
@@ -489,10 +495,13 @@ void launch_skinny(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t
   constexpr int U = skinny_u<BITS, MT>();
   // Waves per workgroup split K, chosen from K alone (so a row's summation order, and so its
   // bits, does not depend on N or on the other rows of the launch): enough waves that each
-  // holds about one batch of U chunks, at most kMaxSkinnyWaves.
+  // holds about one batch of U chunks, at most kMaxSkinnyWaves -- or 16 for one-tile,
+  // one-m-tile launches over a long K (the down projection), where 1024-thread workgroups still
+  // fit the register file and halve the round trips per wave.
   const int nkb = k / SkinnyCfg<BITS>::KB;
+  const int kw_max = (NT == 1 && MT == 1 && nkb > kMaxSkinnyWaves * U) ? 16 : kMaxSkinnyWaves;
   int kw = 1;
-  while (kw < kMaxSkinnyWaves && kw * U < nkb) kw *= 2;
+  while (kw < kw_max && kw * U < nkb) kw *= 2;
   const int per_wave = (nkb + kw - 1) / kw;
   if constexpr (NT > 1) {
     // Two super-batches of two row tiles would not fit the register file: one tile per wave.
@@ -503,13 +512,21 @@ void launch_skinny(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t
   }
   const unsigned blocks = unsigned((n + 16 * NT - 1) / (16 * NT));
   const bool pg = k / g > 1;
-#define EDGERAG_SKINNY(NB, PG)                                                                 \
-  hipLaunchKernelGGL((qlinear_skinny_kernel<BITS, NT, MT, U, NB, PG>), dim3(blocks),           \
+#define EDGERAG_SKINNY(NB, PG, KWM)                                                            \
+  hipLaunchKernelGGL((qlinear_skinny_kernel<BITS, NT, MT, U, NB, PG, KWM>), dim3(blocks),      \
                      dim3(kw * kWave), 0, s, x, xs, m, k, packed, scales, bias, n, g, y, ys)
-  if (per_wave <= U) {
-    if (pg) EDGERAG_SKINNY(1, true); else EDGERAG_SKINNY(1, false);
+  if (kw > kMaxSkinnyWaves) {
+    if constexpr (NT == 1 && MT == 1) {
+      if (per_wave <= U) {
+        if (pg) EDGERAG_SKINNY(1, true, 16); else EDGERAG_SKINNY(1, false, 16);
+      } else {
+        if (pg) EDGERAG_SKINNY(2, true, 16); else EDGERAG_SKINNY(2, false, 16);
+      }
+    }
+  } else if (per_wave <= U) {
+    if (pg) EDGERAG_SKINNY(1, true, 8); else EDGERAG_SKINNY(1, false, 8);
   } else {
-    if (pg) EDGERAG_SKINNY(2, true); else EDGERAG_SKINNY(2, false);
+    if (pg) EDGERAG_SKINNY(2, true, 8); else EDGERAG_SKINNY(2, false, 8);
   }
 #undef EDGERAG_SKINNY
 }
@@ -542,9 +559,9 @@ void dispatch(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* pac
   // Tiles: the largest whose grid still covers the 256 CUs.
   const int64_t t128 = int64_t((n + 127) / 128) * ((m + 127) / 128);
   const int64_t t128x64 = int64_t((n + 127) / 128) * ((m + 63) / 64);
-  if (t128 >= 256)
+  if (t128 >= EDGERAG_GEMM_TARGET_WGS)
     launch_gemm<BITS, 128, 128>(x, xs, m, k, packed, scales, bias, n, g, y, ys, s);
-  else if (t128x64 >= 256)
+  else if (t128x64 >= EDGERAG_GEMM_TARGET_WGS)
     launch_gemm<BITS, 128, 64>(x, xs, m, k, packed, scales, bias, n, g, y, ys, s);
   else
     launch_gemm<BITS, 64, 64>(x, xs, m, k, packed, scales, bias, n, g, y, ys, s);
