@@ -101,7 +101,12 @@ __device__ __forceinline__ uint4 ldg16(const void* p) {
 
 // Compiler-only fence: keeps the loads issued above it from being sunk below it (next to their
 // first use), which would serialise memory latency with the compute they are meant to overlap.
-__device__ __forceinline__ void issue_fence() { asm volatile("" ::: "memory"); }
+// The memory clobber stops IR-level code motion; the scheduling barrier stops the machine
+// scheduler, which otherwise moves each load next to its first use to save registers.
+__device__ __forceinline__ void issue_fence() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
 
 // ---- skinny kernel (M <= 64) ----------------------------------------------------------------
 constexpr int kMaxSkinnyWaves = 8;
@@ -172,8 +177,11 @@ __device__ __forceinline__ void skinny_compute(const SkinnyBatch<BITS, NT, MT, U
       }
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const _Float16 s1 =
-          __builtin_bit_cast(_Float16, uint16_t(PG ? b.s[u][t] : s_row[t]));
+      // The row scale is loop-invariant: passing it through an empty asm keeps its first use
+      // (and so the wait for its load) inside the loop, after the batch's loads are issued.
+      uint32_t sr = PG ? b.s[u][t] : s_row[t];
+      if constexpr (!PG) asm volatile("" : "+v"(sr));
+      const _Float16 s1 = __builtin_bit_cast(_Float16, uint16_t(sr));
       const h2 s2 = {s1, s1};
       const uint32_t words[4] = {b.w[u][t].x, b.w[u][t].y, b.w[u][t].z, b.w[u][t].w};
       if constexpr (BITS == 8) {
