@@ -24,6 +24,12 @@
 #ifndef EDGERAG_SKINNY_MAX_M
 #define EDGERAG_SKINNY_MAX_M 64
 #endif
+#ifndef EDGERAG_STREAM_MAX_M
+#define EDGERAG_STREAM_MAX_M 16  // per-channel INT8 launches up to this M use the streaming kernel
+#endif
+#ifndef EDGERAG_STREAM_NT2_TILES
+#define EDGERAG_STREAM_NT2_TILES 512  // 16-row tiles from which a workgroup takes two
+#endif
 #ifndef EDGERAG_GEMM_MIN_WG
 #define EDGERAG_GEMM_MIN_WG 1  // workgroups per CU the GEMM's register budget must allow
 #endif
@@ -291,6 +297,132 @@ __global__ __launch_bounds__(KWMAX * kWave) void qlinear_skinny_kernel(
   }
 }
 
+// ---- streaming kernel (INT8 per-channel, M <= 16) --------------------------------------------
+// One workgroup owns NT tiles of R = 16 / F weight rows and all M <= MT R activation rows; its KW
+// waves split K. The 16 A rows of v_mfma_f32_16x16x32_f16 are F k-slices x R weight rows and the
+// 16 B columns of m-tile t are F k-slices x R activation rows (t R + [0, R)): lane row li = f R + r
+// streams row r at 64-byte chunks c F + f, so each load instruction covers F x 64 contiguous bytes
+// of R rows, and a workgroup needs only NT R rows (N / R workgroups fill the chip even for
+// N = 2048). The NT row tiles of a wave share its activation registers.
+// D[(f, r)][(f, j)] of tile (n-tile, t) is the slice-f partial of y[t R + j][r]; the off-diagonal
+// blocks pair different k-slices and are never read.
+// The dequantised weight is the exact integer code (no scale): the row's scale multiplies the fp32
+// sum once, scale * sum(code * x), instead of rounding every code * scale to fp16 first.
+template <int F, int NT, int MT, int KW, int U, bool EXACT>
+__global__ __launch_bounds__(KW * kWave) void qlinear_stream_kernel(
+    const f16* __restrict__ x, int64_t xs, int32_t m, int32_t k,
+    const uint8_t* __restrict__ packed, const f16* __restrict__ scales,
+    const f16* __restrict__ bias, int32_t n, f16* __restrict__ y, int64_t ys) {
+  constexpr int R = 16 / F;
+  constexpr int CB = 64 * F;               // bytes (= k) of one chunk step of a row
+  constexpr int OUTS = NT * MT * R * R;    // outputs (token, row) of a workgroup
+  static_assert(OUTS <= KW * kWave, "one output per thread");
+  __shared__ float red[KW * NT * MT * 4 * kWave];
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63;
+  const int li = lane & 15, lg = lane >> 4;
+  const int f = li / R, r = li % R;
+  const int n0 = blockIdx.x * (NT * R);
+  const int nc = k / CB;  // chunk steps: >= U, and a multiple of KW * U when EXACT
+  const int per = (nc + KW - 1) / KW;
+  const int c0 = min(nc, wave * per), c1 = min(nc, c0 + per);
+
+  // A lane of n-tile tn: weight row n0 + tn R + r; B lane of m-tile t: activation row t R + r.
+  // Rows past N or M re-read the last row: they only feed D rows / columns that are never read.
+  const uint8_t* wp[NT];
+#pragma unroll
+  for (int tn = 0; tn < NT; ++tn)
+    wp[tn] = packed + int64_t(min(n0 + tn * R + r, n - 1)) * k + f * 64 + 16 * lg;
+  const f16* xp[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) xp[t] = x + int64_t(min(t * R + r, m - 1)) * xs + f * 64 + 16 * lg;
+
+  // Thread e < OUTS writes row n0 + e % (NT R) of token e / (NT R). Its scale and bias are loaded
+  // now and first waited for after the first batch's loads are issued.
+  const int e = threadIdx.x;
+  const int e_row = min(n0 + (e < OUTS ? e % (NT * R) : 0), n - 1);
+  uint32_t s_bits = reinterpret_cast<const uint16_t*>(scales)[e_row];
+  uint32_t b_bits = bias != nullptr ? reinterpret_cast<const uint16_t*>(bias)[e_row] : 0u;
+
+  f32x4 acc[NT][MT];
+#pragma unroll
+  for (int tn = 0; tn < NT; ++tn)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[tn][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const h2 bias2 = {_Float16(1152.f), _Float16(1152.f)};
+  for (int cb = c0; cb < c1; cb += U) {
+    // A batch of U steps starting no later than nc - U, so every load is in bounds and its
+    // offsets are immediates. Unless EXACT (every wave owns whole batches), steps outside
+    // [cb, c1) (already done, or another wave's) keep the accumulators unchanged.
+    const int cs = min(cb, nc - U);
+    uint4 w[U][NT], xa[U][MT], xc[U][MT];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {  // in step order, so step u waits only for its own loads
+#pragma unroll
+      for (int tn = 0; tn < NT; ++tn) w[u][tn] = ldg16(wp[tn] + int64_t(cs) * CB + u * CB);
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        const f16* xb = xp[t] + int64_t(cs) * CB + u * CB;
+        xa[u][t] = ldg16(xb);
+        xc[u][t] = ldg16(xb + 8);
+      }
+    }
+    issue_fence();
+    if (cb == c0) asm volatile("" : "+v"(s_bits), "+v"(b_bits));
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool on = EXACT || (cs + u >= cb && cs + u < c1);
+#pragma unroll
+      for (int tn = 0; tn < NT; ++tn) {
+        const uint4 wq = w[u][tn];
+        const uint32_t words[4] = {wq.x ^ 0x80808080u, wq.y ^ 0x80808080u, wq.z ^ 0x80808080u,
+                                   wq.w ^ 0x80808080u};
+        h2 p[8];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          // Byte b (offset binary after the xor) becomes the fp16 1024 + b; minus 1152 is the
+          // code.
+          p[2 * q] = as_h2(__builtin_amdgcn_perm(0x64646464u, words[q], 0x04010400u)) - bias2;
+          p[2 * q + 1] = as_h2(__builtin_amdgcn_perm(0x64646464u, words[q], 0x04030402u)) - bias2;
+        }
+        const h8 a0 = pack_h8(p[0], p[1], p[2], p[3]), a1 = pack_h8(p[4], p[5], p[6], p[7]);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          f32x4 v = mfma16(a0, __builtin_bit_cast(h8, xa[u][t]), acc[tn][t]);
+          v = mfma16(a1, __builtin_bit_cast(h8, xc[u][t]), v);
+          acc[tn][t] = on ? v : acc[tn][t];
+        }
+      }
+    }
+  }
+
+  // Sum slices and waves in a fixed order, then y[m][n] = scale[n] * sum (+ bias[n]).
+  // Accumulator register i of lane l holds D row 4 (l / 16) + i, column l % 16.
+#pragma unroll
+  for (int tn = 0; tn < NT; ++tn)
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        red[(((wave * NT + tn) * MT + t) * 4 + i) * kWave + lane] = acc[tn][t][i];
+  __syncthreads();
+  const int tok = e / (NT * R), row_in = e % (NT * R);
+  const int tn = row_in / R, rr = row_in % R;
+  const int t = tok / R, jj = tok % R;
+  const int nrow = n0 + row_in;
+  if (e >= OUTS || tok >= m || nrow >= n) return;
+  float sum = 0.f;
+#pragma unroll
+  for (int fs = 0; fs < F; ++fs) {
+    const int drow = fs * R + rr, dcol = fs * R + jj;
+    const int l = 16 * (drow >> 2) + dcol, i = drow & 3;
+    for (int wv = 0; wv < KW; ++wv) sum += red[(((wv * NT + tn) * MT + t) * 4 + i) * kWave + l];
+  }
+  float v = float(__builtin_bit_cast(_Float16, uint16_t(s_bits))) * sum;
+  if (bias != nullptr) v += float(__builtin_bit_cast(_Float16, uint16_t(b_bits)));
+  y[int64_t(tok) * ys + nrow] = __float2half_rn(v);
+}
+
 // ---- tiled GEMM (M > 64) --------------------------------------------------------------------
 constexpr int kGemmThreads = 256;
 constexpr int kBK = 64;     // k per LDS stage
@@ -548,10 +680,87 @@ void launch_gemm(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* 
                      m, k, packed, scales, bias, n, g, y, ys);
 }
 
+// The streaming kernel's shape: k-slices F and row tiles NT from N alone (two k-slices when
+// 16-row tiles would leave CUs idle, two row tiles when 32-row tiles still cover them), waves KW and
+// steps per batch U from K alone, so that a row's summation order, and so its bits, do not depend
+// on M or on the other rows of the launch. Returns false when the shape does not fit (the caller
+// then uses the skinny kernel).
+template <int F, int NT, int MT, int KW, int U>
+void launch_stream(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
+                   const f16* scales, const f16* bias, int32_t n, f16* y, int64_t ys,
+                   hipStream_t s) {
+  constexpr int rows = NT * 16 / F;
+  const unsigned blocks = unsigned((n + rows - 1) / rows);
+  if ((k / (64 * F)) % (KW * U) == 0)
+    hipLaunchKernelGGL((qlinear_stream_kernel<F, NT, MT, KW, U, true>), dim3(blocks),
+                       dim3(KW * kWave), 0, s, x, xs, m, k, packed, scales, bias, n, y, ys);
+  else
+    hipLaunchKernelGGL((qlinear_stream_kernel<F, NT, MT, KW, U, false>), dim3(blocks),
+                       dim3(KW * kWave), 0, s, x, xs, m, k, packed, scales, bias, n, y, ys);
+}
+
+template <int F, int NT, int MT>
+void launch_stream_k(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
+                     const f16* scales, const f16* bias, int32_t n, f16* y, int64_t ys,
+                     hipStream_t s) {
+  // One batch of at most 8 steps per wave; at least 4 waves (one per SIMD), or 8 for two row
+  // tiles (one output per thread); at most 16, or 8 for two row or m tiles, whose registers
+  // would not fit 16 waves.
+  const int nc = k / (64 * F);
+  constexpr int kw_min = NT == 1 ? 4 : 8;
+  constexpr int kw_max = NT == 1 && MT == 1 ? 16 : 8;
+  int kw = kw_min;
+  while (kw < kw_max && kw * 8 < nc) kw *= 2;
+  const bool u8 = (nc + kw - 1) / kw > 4 && nc >= 8;
+#define EDGERAG_STREAM(KW)                                                                      \
+  do {                                                                                         \
+    if (u8) launch_stream<F, NT, MT, KW, 8>(x, xs, m, k, packed, scales, bias, n, y, ys, s);   \
+    else launch_stream<F, NT, MT, KW, 4>(x, xs, m, k, packed, scales, bias, n, y, ys, s);      \
+  } while (0)
+  if constexpr (kw_min == 4) {
+    if (kw == 4) {
+      EDGERAG_STREAM(4);
+      return;
+    }
+  }
+  if constexpr (kw_max == 16) {
+    if (kw == 16) {
+      EDGERAG_STREAM(16);
+      return;
+    }
+  }
+  EDGERAG_STREAM(8);
+#undef EDGERAG_STREAM
+}
+
+bool dispatch_stream(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
+                     const f16* scales, const f16* bias, int32_t n, f16* y, int64_t ys,
+                     hipStream_t s) {
+  if (m > 16) return false;
+  const int64_t tiles16 = (n + 15) / 16;
+  if (tiles16 < 256) {  // 16-row tiles would not cover the 256 CUs: two k-slices, 8-row tiles
+    if (k % 128 != 0 || k / 128 < 4) return false;
+    if (m <= 8) launch_stream_k<2, 1, 1>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
+    else launch_stream_k<2, 1, 2>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
+    return true;
+  }
+  if (k % 64 != 0 || k / 64 < 4) return false;
+  if (tiles16 >= EDGERAG_STREAM_NT2_TILES)  // 32-row workgroups still cover the CUs
+    launch_stream_k<1, 2, 1>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
+  else
+    launch_stream_k<1, 1, 1>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
+  return true;
+}
+
 template <int BITS>
 void dispatch(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
               const f16* scales, const f16* bias, int32_t n, int32_t g, f16* y, int64_t ys,
               hipStream_t s) {
+  if constexpr (BITS == 8) {
+    if (g == k && m <= EDGERAG_STREAM_MAX_M &&
+        dispatch_stream(x, xs, m, k, packed, scales, bias, n, y, ys, s))
+      return;
+  }
   if (m <= EDGERAG_SKINNY_MAX_M) {
     const bool wide = (n + 31) / 32 >= 256;  // enough workgroups with 32 rows each
     if (m <= 16) {

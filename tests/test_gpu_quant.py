@@ -161,3 +161,28 @@ def test_quant_linear_mfma_edges(device, bits, k, g, m) -> None:
         y = kernels.quant_linear(x.to(device), packed.to(device), scales.to(device),
                                  bias.to(device), k, n, bits, g)
         torch.testing.assert_close(y.float().cpu(), expected, **LINEAR_TOL)
+
+
+@pytest.mark.parametrize("k", [640, 1152, 2048, 8192])
+@pytest.mark.parametrize("n", [37, 2048, 4104, 8200])
+def test_quant_linear_int8_per_channel_streaming(device, k, n) -> None:
+    """The per-channel INT8 streaming GEMV (M <= 16): two k-slices per MFMA tile for narrow N,
+    one for wide N; K both a whole number of per-wave batches (2048, 8192) and not (640, 1152,
+    where the last batch of a wave overlaps the one before); N not a multiple of the row tile;
+    bias; activations with a row stride larger than K. The row scale multiplies the fp32 sum,
+    so the check is against the reference dequant-then-matmul at the linear tolerance."""
+    w = _weight(n, k, n + 7 * k)
+    cfg = oq.QuantConfig(k, 8)
+    packed, scales = oq.quantize_for_layer(w, cfg)
+    bias = (torch.randn(n, generator=seeded(n + k)) * 0.1).half()
+    for m in (1, 2, 5, 8, 9, 16):
+        xfull = torch.randn(m, k + 64, generator=seeded(m * 13 + k)).half()
+        x = xfull[:, :k]
+        expected = oq.quant_linear_reference(x, packed, scales, bias, k, cfg)
+        y = kernels.quant_linear(xfull.to(device)[:, :k], packed.to(device), scales.to(device),
+                                 bias.to(device), k, n, 8, k)
+        torch.testing.assert_close(y.float().cpu(), expected, **LINEAR_TOL)
+        # Token rows are independent: each row alone gives the same bits as in the batch.
+        y1 = kernels.quant_linear(xfull.to(device)[m - 1 : m, :k], packed.to(device),
+                                  scales.to(device), bias.to(device), k, n, 8, k)
+        assert torch.equal(y1[0], y[m - 1])
