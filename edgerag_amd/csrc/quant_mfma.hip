@@ -428,9 +428,14 @@ constexpr int kGemmThreads = 256;
 constexpr int kBK = 64;     // k per LDS stage
 constexpr int kLdsRow = 64;  // halves per LDS row (one row of a 64-k stage)
 
-// Halves offset of 16-byte chunk `c` (0..7) of LDS row `row`, chunk index XOR-swizzled by the row
-// so that 32 lanes reading one chunk column of 32 rows hit distinct banks.
-__device__ __forceinline__ int lds_off(int row, int c) { return row * kLdsRow + ((c ^ (row & 7)) << 3); }
+// Halves offset of 16-byte chunk `c` (k 8c .. 8c + 7 of the stage) of LDS row `row`. The stage is
+// stored in MFMA operand order: for each 32-row tile and 16-k step, the 64 lanes' operands
+// (lane = 32 (c & 1) + row % 32) are 64 consecutive 16-byte slots, so every operand read is one
+// contiguous 1 KiB ds_read_b128 (no bank conflicts), and the stagers' writes are runs of 16 or 32
+// consecutive slots.
+__device__ __forceinline__ int lds_off(int row, int c) {
+  return ((((row >> 5) * 4 + (c >> 1)) * 2 + (c & 1)) * 32 + (row & 31)) * 8;
+}
 
 template <int BITS, int BN, int BM>
 struct GemmCfg {
@@ -479,34 +484,42 @@ __device__ __forceinline__ void gemm_load(GemmStage<BITS, BN, BM>& st, int k0, c
   for (int i = 0; i < C::X_BPT / 16; ++i) st.x[i] = ldg16(xrow + k0 + 8 * i);
 }
 
-template <int BITS, int BN, int BM>
-__device__ __forceinline__ void gemm_store(const GemmStage<BITS, BN, BM>& st, _Float16* sw,
-                                           _Float16* sx, int wr, int wc0, int xr, int xc0,
-                                           bool xvalid) {
-  using C = GemmCfg<BITS, BN, BM>;
-  const _Float16 s1 = __builtin_bit_cast(_Float16, st.s);
-  const h2 s2 = {s1, s1};
-  // Dequantised weights: W_K halves = W_K / 8 chunks starting at chunk wc0.
+// Writes weight chunk c (8 k) of this thread's staged segment to LDS, dequantised: the exact
+// integer code when PC (per-channel scales, applied to the fp32 sums in the epilogue), else
+// code * scale rounded to fp16 once, as the reference's dequantize_groupwise does.
+template <int BITS, int BN, int BM, bool PC>
+__device__ __forceinline__ void gemm_store_w(const GemmStage<BITS, BN, BM>& st, int c,
+                                             _Float16* sw, int wr, int wc0) {
+  h2 p[4];
   if constexpr (BITS == 8) {
+    if constexpr (PC) {
+      const h2 bias = {_Float16(1152.f), _Float16(1152.f)};
 #pragma unroll
-    for (int c = 0; c < C::W_K / 8; ++c) {
-      h2 p[4];
+      for (int q = 0; q < 2; ++q) {
+        const uint32_t wx = st.w[2 * c + q] ^ 0x80808080u;
+        p[2 * q] = as_h2(__builtin_amdgcn_perm(0x64646464u, wx, 0x04010400u)) - bias;
+        p[2 * q + 1] = as_h2(__builtin_amdgcn_perm(0x64646464u, wx, 0x04030402u)) - bias;
+      }
+    } else {
+      const _Float16 s1 = __builtin_bit_cast(_Float16, st.s);
+      const h2 s2 = {s1, s1};
       deq_i8_word(st.w[2 * c], s2, p[0], p[1]);
       deq_i8_word(st.w[2 * c + 1], s2, p[2], p[3]);
-      *reinterpret_cast<h8*>(sw + lds_off(wr, wc0 + c)) = pack_h8(p[0], p[1], p[2], p[3]);
     }
   } else {
-#pragma unroll
-    for (int c = 0; c < C::W_K / 8; ++c) {
-      h2 p[4];
-      deq_i4_word(st.w[c], s2, p);
-      *reinterpret_cast<h8*>(sw + lds_off(wr, wc0 + c)) = pack_h8(p[0], p[1], p[2], p[3]);
-    }
+    const _Float16 s1 = __builtin_bit_cast(_Float16, st.s);
+    const h2 s2 = {s1, s1};
+    deq_i4_word(st.w[c], s2, p);
   }
-  // Activation rows past M were loaded from row M - 1 (no branch at the load); stage zeros.
-#pragma unroll
-  for (int i = 0; i < C::X_BPT / 16; ++i)
-    *reinterpret_cast<uint4*>(sx + lds_off(xr, xc0 + i)) = xvalid ? st.x[i] : uint4{0, 0, 0, 0};
+  *reinterpret_cast<h8*>(sw + lds_off(wr, wc0 + c)) = pack_h8(p[0], p[1], p[2], p[3]);
+}
+
+// Writes activation chunk i (8 k) of this thread's staged segment to LDS. Activation rows past M
+// were loaded from row M - 1: they only feed accumulator columns that are never stored.
+template <int BITS, int BN, int BM>
+__device__ __forceinline__ void gemm_store_x(const GemmStage<BITS, BN, BM>& st, int i,
+                                             _Float16* sx, int xr, int xc0) {
+  *reinterpret_cast<uint4*>(sx + lds_off(xr, xc0 + i)) = st.x[i];
 }
 
 // y[M, N] = x . W^T for one BN x BM tile of y^T. Waves form a 2 x 2 grid; wave (wn, wm) owns
@@ -514,12 +527,14 @@ __device__ __forceinline__ void gemm_store(const GemmStage<BITS, BN, BM>& st, _F
 // TN x TM 32x32 MFMA tiles. Operand lane layout of v_mfma_f32_32x32x16_f16: lane l reads row
 // l % 32, k chunk 2 ks + l / 32 of a 16-k step; accumulator register i of lane l holds
 // row 8 (i / 4) + 4 (l / 32) + i % 4 of A (weight row) and column l % 32 (activation row).
-template <int BITS, int BN, int BM>
+// PC: per-channel INT8 (one scale per weight row), applied to the fp32 sums.
+template <int BITS, int BN, int BM, bool PC>
 __global__ __launch_bounds__(kGemmThreads, EDGERAG_GEMM_MIN_WG) void qlinear_gemm_kernel(
     const f16* __restrict__ x, int64_t xs, int32_t m, int32_t k,
     const uint8_t* __restrict__ packed, const f16* __restrict__ scales,
     const f16* __restrict__ bias, int32_t n, int32_t g, f16* __restrict__ y, int64_t ys) {
   using C = GemmCfg<BITS, BN, BM>;
+  constexpr int NWC = C::W_K / 8, NXC = C::X_BPT / 16;  // LDS chunks this thread stages per step
   __shared__ __attribute__((aligned(16))) _Float16 sw[2][BN * kLdsRow];
   __shared__ __attribute__((aligned(16))) _Float16 sx[2][BM * kLdsRow];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -528,15 +543,17 @@ __global__ __launch_bounds__(kGemmThreads, EDGERAG_GEMM_MIN_WG) void qlinear_gem
   const int64_t row_bytes = BITS == 8 ? k : k / 2;
   const int groups = k / g;
 
-  // Staging roles: weight row wr (segment wseg), activation row xr (segment xseg).
-  const int wr = tid / C::W_TPR, wseg = tid % C::W_TPR;
-  const int xr = tid / C::X_TPR, xseg = tid % C::X_TPR;
+  // Staging roles: weight row wr (segment wseg), activation row xr (segment xseg). Consecutive
+  // lanes take consecutive rows of one segment, so that each 16-lane group of an LDS write fills
+  // 16 consecutive operand slots (256 contiguous bytes: no bank conflicts).
+  constexpr int WROWS = 64 / C::W_TPR, XROWS = 64 / C::X_TPR;  // rows staged per wave
+  const int wr = wave * WROWS + lane % WROWS, wseg = lane / WROWS;
+  const int xr = wave * XROWS + lane % XROWS, xseg = lane / XROWS;
   const int wrow_g = min(nb + wr, n - 1);
   const uint8_t* wrow = packed + int64_t(wrow_g) * row_bytes + wseg * C::W_BPT;
   const f16* srow = scales + int64_t(wrow_g) * groups;
   const int wk_off = wseg * C::W_K;  // k offset of this thread's weight segment in a stage
-  const bool xvalid = mb + xr < m;
-  const f16* xrow = x + int64_t(xvalid ? mb + xr : m - 1) * xs + xseg * (C::X_BPT / 2);
+  const f16* xrow = x + int64_t(min(mb + xr, m - 1)) * xs + xseg * (C::X_BPT / 2);
   const int wc0 = wk_off / 8, xc0 = xseg * (C::X_BPT / 16);
 
   f32x16 acc[C::TN][C::TM];
@@ -547,68 +564,108 @@ __global__ __launch_bounds__(kGemmThreads, EDGERAG_GEMM_MIN_WG) void qlinear_gem
 
   const int nk = k / kBK;
   const int col = lane & 31, half = lane >> 5;
-  // One 64-k step on the staged LDS tiles.
-  auto compute = [&](const _Float16* swb, const _Float16* sxb) {
+  // One 64-k step on the staged LDS buffers (swb, sxb), interleaved with staging the next step's
+  // registers `st` into the other buffers (dw, dx): each of the four 16-k MFMA steps is paired
+  // with a share of the dequantisation and LDS writes, so the VALU and LDS work of the next step
+  // overlaps this step's matrix-core work. The operands of 16-k step ks + 1 are read from LDS
+  // before the MFMAs of step ks are issued, so their latency hides behind those MFMAs.
+  auto read_ops = [&](const _Float16* swb, const _Float16* sxb, int ks, h8 (&a)[C::TN],
+                      h8 (&b)[C::TM]) {
+#pragma unroll
+    for (int i = 0; i < C::TN; ++i)
+      a[i] = *reinterpret_cast<const h8*>(swb + lds_off(wn * (BN / 2) + 32 * i + col, 2 * ks + half));
+#pragma unroll
+    for (int j = 0; j < C::TM; ++j)
+      b[j] = *reinterpret_cast<const h8*>(sxb + lds_off(wm * (BM / 2) + 32 * j + col, 2 * ks + half));
+  };
+  auto step = [&](const _Float16* swb, const _Float16* sxb, const GemmStage<BITS, BN, BM>& st,
+                  _Float16* dw, _Float16* dx) {
+    h8 a[2][C::TN], b[2][C::TM];
+    read_ops(swb, sxb, 0, a[0], b[0]);
 #pragma unroll
     for (int ks = 0; ks < kBK / 16; ++ks) {
-      h8 a[C::TN], b[C::TM];
+      if (ks + 1 < kBK / 16) read_ops(swb, sxb, ks + 1, a[(ks + 1) & 1], b[(ks + 1) & 1]);
+#pragma unroll
+      for (int c = ks * NWC / 4; c < (ks + 1) * NWC / 4; ++c)
+        gemm_store_w<BITS, BN, BM, PC>(st, c, dw, wr, wc0);
+#pragma unroll
+      for (int i = ks * NXC / 4; i < (ks + 1) * NXC / 4; ++i)
+        gemm_store_x<BITS, BN, BM>(st, i, dx, xr, xc0);
 #pragma unroll
       for (int i = 0; i < C::TN; ++i)
-        a[i] = *reinterpret_cast<const h8*>(swb + lds_off(wn * (BN / 2) + 32 * i + col, 2 * ks + half));
 #pragma unroll
-      for (int j = 0; j < C::TM; ++j)
-        b[j] = *reinterpret_cast<const h8*>(sxb + lds_off(wm * (BM / 2) + 32 * j + col, 2 * ks + half));
-#pragma unroll
-      for (int i = 0; i < C::TN; ++i)
-#pragma unroll
-        for (int j = 0; j < C::TM; ++j) acc[i][j] = mfma32(a[i], b[j], acc[i][j]);
+        for (int j = 0; j < C::TM; ++j) acc[i][j] = mfma32(a[ks & 1][i], b[ks & 1][j], acc[i][j]);
     }
   };
-  // Register stages st0 / st1 hold steps kt and kt + 1; a step's global loads are issued two
-  // steps before it is stored to LDS, so each load has two compute steps to land. One barrier per
-  // step: LDS buffer kt & 1 is rewritten only after every wave has passed the barrier that follows
-  // its previous compute.
+  // Register stages st0 / st1 alternate; a step's global loads are issued about two steps before
+  // it is staged to LDS. One barrier per step: it orders this step's LDS writes (the next step's
+  // operands) before their reads, and every wave's reads of a buffer before its next rewrite.
   // Loads are unconditional (a step past the end reloads the last one) so that the compiler never
-  // has to wait for a load right after issuing it.
+  // has to wait for a load right after issuing it. Steps go in pairs whose loads are issued on
+  // every path (an odd last step skips only the second half's LDS and matrix work, under a
+  // wave-uniform branch), so the compiler cannot sink a step's loads behind a branch.
+  // Epilogue operands: thread t < BN loads the scale (PC) and bias of weight row nb + t now (row
+  // clamped into [0, N)), waits for them once the first stages' loads are in flight, and puts
+  // them in LDS after the main loop for the lanes that write that row.
+  __shared__ uint32_t ep_lds[BN];  // scale bits | bias bits << 16
+  const uint16_t* scales16 = reinterpret_cast<const uint16_t*>(scales);
+  const uint16_t* bias16 = reinterpret_cast<const uint16_t*>(bias);
+  const int ep_row = min(nb + (tid < BN ? tid : 0), n - 1);
+  uint32_t ep_s = PC ? scales16[ep_row] : 0u;
+  uint32_t ep_b = bias != nullptr ? bias16[ep_row] : 0u;
+
   GemmStage<BITS, BN, BM> st0, st1;
   const int last = (nk - 1) * kBK;
   gemm_load<BITS, BN, BM>(st0, 0, wrow, srow, g, wk_off, xrow);
   gemm_load<BITS, BN, BM>(st1, min(kBK, last), wrow, srow, g, wk_off, xrow);
   issue_fence();
-  // Steps go in pairs with no early exit (an odd last step pairs with a zero step: its staged
-  // activations are zero), so the compiler cannot sink a step's loads behind a branch.
+  asm volatile("" : "+v"(ep_s), "+v"(ep_b));
+#pragma unroll
+  for (int c = 0; c < NWC; ++c) gemm_store_w<BITS, BN, BM, PC>(st0, c, sw[0], wr, wc0);
+#pragma unroll
+  for (int i = 0; i < NXC; ++i) gemm_store_x<BITS, BN, BM>(st0, i, sx[0], xr, xc0);
+  __syncthreads();
+  gemm_load<BITS, BN, BM>(st0, min(2 * kBK, last), wrow, srow, g, wk_off, xrow);
+  issue_fence();
   for (int kt = 0; kt < nk; kt += 2) {
-    gemm_store<BITS, BN, BM>(st0, sw[0], sx[0], wr, wc0, xr, xc0, xvalid);
-    __syncthreads();
-    gemm_load<BITS, BN, BM>(st0, min((kt + 2) * kBK, last), wrow, srow, g, wk_off, xrow);
-    issue_fence();
-    compute(sw[0], sx[0]);
-    gemm_store<BITS, BN, BM>(st1, sw[1], sx[1], wr, wc0, xr, xc0, xvalid && kt + 1 < nk);
+    step(sw[0], sx[0], st1, sw[1], sx[1]);
     __syncthreads();
     gemm_load<BITS, BN, BM>(st1, min((kt + 3) * kBK, last), wrow, srow, g, wk_off, xrow);
     issue_fence();
-    compute(sw[1], sx[1]);
+    if (kt + 1 < nk) step(sw[1], sx[1], st0, sw[0], sx[0]);
+    __syncthreads();
+    gemm_load<BITS, BN, BM>(st0, min((kt + 4) * kBK, last), wrow, srow, g, wk_off, xrow);
+    issue_fence();
   }
 
   // Epilogue: register 4q + r of tile (i, j) is y[mrow][nrow + r], 4 consecutive outputs per q,
-  // stored as one 8-byte write when the row stride and the tile edge allow.
+  // stored as one 8-byte write when the row stride and the tile edge allow. (The main loop ended
+  // with a barrier, so ep_lds is free of other uses.)
+  if (tid < BN) ep_lds[tid] = ep_s | (ep_b << 16);
+  __syncthreads();
   const bool vec_out = (ys % 4) == 0 && (reinterpret_cast<uintptr_t>(y) & 7) == 0;
 #pragma unroll
   for (int i = 0; i < C::TN; ++i) {
 #pragma unroll
-    for (int j = 0; j < C::TM; ++j) {
-      const int mrow = mb + wm * (BM / 2) + 32 * j + col;
-      if (mrow >= m) continue;
-      f16* yr = y + int64_t(mrow) * ys;
+    for (int q = 0; q < 4; ++q) {
+      const int nrow_l = wn * (BN / 2) + 32 * i + 8 * q + 4 * half;  // row within the tile
+      const int nrow = nb + nrow_l;
+      float sc[4], bv[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int nrow = nb + wn * (BN / 2) + 32 * i + 8 * q + 4 * half;
+      for (int r = 0; r < 4; ++r) {
+        const uint32_t e = ep_lds[nrow_l + r];
+        sc[r] = float(__builtin_bit_cast(_Float16, uint16_t(e & 0xFFFFu)));
+        bv[r] = float(__builtin_bit_cast(_Float16, uint16_t(e >> 16)));
+      }
+#pragma unroll
+      for (int j = 0; j < C::TM; ++j) {
+        const int mrow = mb + wm * (BM / 2) + 32 * j + col;
+        if (mrow >= m) continue;
+        f16* yr = y + int64_t(mrow) * ys;
         float v[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float bv = (bias != nullptr && nrow + r < n) ? __half2float(bias[nrow + r]) : 0.f;
-          v[r] = acc[i][j][4 * q + r] + bv;
-        }
+        for (int r = 0; r < 4; ++r) v[r] = PC ? sc[r] * acc[i][j][4 * q + r] + bv[r]
+                                              : acc[i][j][4 * q + r] + bv[r];
         if (vec_out && nrow + 3 < n) {
           const h2 lo = {_Float16(v[0]), _Float16(v[1])}, hi = {_Float16(v[2]), _Float16(v[3])};
           *reinterpret_cast<uint2*>(yr + nrow) = uint2{as_u32(lo), as_u32(hi)};
@@ -676,8 +733,12 @@ void launch_gemm(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* 
                  const f16* scales, const f16* bias, int32_t n, int32_t g, f16* y, int64_t ys,
                  hipStream_t s) {
   const dim3 grid(unsigned((n + BN - 1) / BN), unsigned((m + BM - 1) / BM));
-  hipLaunchKernelGGL((qlinear_gemm_kernel<BITS, BN, BM>), grid, dim3(kGemmThreads), 0, s, x, xs,
-                     m, k, packed, scales, bias, n, g, y, ys);
+  if (BITS == 8 && g == k)
+    hipLaunchKernelGGL((qlinear_gemm_kernel<BITS, BN, BM, BITS == 8>), grid, dim3(kGemmThreads),
+                       0, s, x, xs, m, k, packed, scales, bias, n, g, y, ys);
+  else
+    hipLaunchKernelGGL((qlinear_gemm_kernel<BITS, BN, BM, false>), grid, dim3(kGemmThreads), 0,
+                       s, x, xs, m, k, packed, scales, bias, n, g, y, ys);
 }
 
 // The streaming kernel's shape: k-slices F and row tiles NT from N alone (two k-slices when
@@ -771,6 +832,16 @@ void dispatch(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* pac
     } else {
       launch_skinny<BITS, 1, 4>(x, xs, m, k, packed, scales, bias, n, g, y, ys, s);
     }
+    return;
+  }
+  // A remainder of at most 16 rows past a whole number of 64-row tiles (the decode tokens packed
+  // after a prefill chunk) would cost a mostly empty extra row of workgroups: it runs on the
+  // streaming (or skinny) path as a second launch instead.
+  const int rem = m % 64;
+  if (rem > 0 && rem <= 16 && m - rem >= 128) {
+    dispatch<BITS>(x, xs, m - rem, k, packed, scales, bias, n, g, y, ys, s);
+    dispatch<BITS>(x + int64_t(m - rem) * xs, xs, rem, k, packed, scales, bias, n, g,
+                   y + int64_t(m - rem) * ys, ys, s);
     return;
   }
   // Tiles: the largest whose grid still covers the 256 CUs.
