@@ -67,6 +67,74 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(
   }
 }
 
+// Vector form for rows of 16-byte-aligned chunks (E = 16 / sizeof(T) elements): thread t owns
+// chunks t, t + 256, ... of the row. Every load of the row (x, delta and weight) is issued before
+// any is used, so a row costs one memory round trip; chunks past the row re-read its last chunk
+// and are masked.
+template <typename T, int NV>
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_vec_kernel(
+    const T* __restrict__ x, const T* __restrict__ delta, const T* __restrict__ weight,
+    T* __restrict__ h_out, T* __restrict__ y, int32_t width, int64_t x_stride, int64_t d_stride,
+    int64_t h_stride, int64_t y_stride, float eps) {
+#pragma clang fp contract(off)
+  constexpr int E = 16 / sizeof(T);
+  const int64_t row = blockIdx.x;
+  const int nch = width / E;
+  const T* xr = x + row * x_stride;
+  const T* dr = delta != nullptr ? delta + row * d_stride : nullptr;
+  Vec16 xv[NV], dv[NV], wv[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int ch = min(int(threadIdx.x) + j * kNormThreads, nch - 1);
+    xv[j] = load16(xr + ch * E);
+    dv[j] = dr != nullptr ? load16(dr + ch * E) : Vec16{};
+    wv[j] = load16(weight + ch * E);
+  }
+  // Consuming the loaded words here keeps the compiler from moving any load below the reduction.
+#pragma unroll
+  for (int j = 0; j < NV; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      asm volatile("" : "+v"(xv[j].w[q]), "+v"(dv[j].w[q]), "+v"(wv[j].w[q]));
+  float h[NV][E];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const bool in = int(threadIdx.x) + j * kNormThreads < nch;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      float hv = vec_elem<T>(xv[j], e);
+      if (dr != nullptr) hv = to_f32<T>(round_to<T>(hv + vec_elem<T>(dv[j], e)));
+      h[j][e] = in ? hv : 0.f;
+      ss = fmaf(h[j][e], h[j][e], ss);
+    }
+  }
+  ss = xor_sum<0, 6>(ss);
+  __shared__ float part[kNormThreads / kWave];
+  if ((threadIdx.x & (kWave - 1)) == 0) part[threadIdx.x / kWave] = ss;
+  __syncthreads();
+  float total = 0.f;
+#pragma unroll
+  for (int w = 0; w < kNormThreads / kWave; ++w) total += part[w];
+  const float r = rsqrtf(total / float(width) + eps);
+  T* hr = h_out != nullptr ? h_out + row * h_stride : nullptr;
+  T* yr = y + row * y_stride;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int ch = int(threadIdx.x) + j * kNormThreads;
+    if (ch >= nch) continue;
+    T ho[E], yo[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      ho[e] = round_to<T>(h[j][e]);
+      const float nv = to_f32<T>(round_to<T>(h[j][e] * r));
+      yo[e] = round_to<T>(vec_elem<T>(wv[j], e) * nv);
+    }
+    if (hr != nullptr) store16(hr + ch * E, *reinterpret_cast<const Vec16*>(ho));
+    store16(yr + ch * E, *reinterpret_cast<const Vec16*>(yo));
+  }
+}
+
 // One thread per (token, head, pair i in [0, d/2)) of the q, k and v heads of the fused
 // projection row [q heads | k heads | v heads].
 template <typename T>
@@ -139,10 +207,58 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const T* __restrict__ gu,
   out[t * out_stride + c] = round_to<T>(s * u);
 }
 
+// Vector form: one thread per 16-byte chunk of the intermediate width (both halves loaded
+// before either is used).
+template <typename T>
+__global__ __launch_bounds__(256) void silu_mul_vec_kernel(const T* __restrict__ gu,
+                                                           int64_t gu_stride, int32_t n_tokens,
+                                                           int32_t inter, T* __restrict__ out,
+                                                           int64_t out_stride) {
+#pragma clang fp contract(off)
+  constexpr int E = 16 / sizeof(T);
+  const int nch = inter / E;
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= int64_t(n_tokens) * nch) return;
+  const int64_t t = i / nch;
+  const int c = int(i % nch) * E;
+  const Vec16 gv = load16(gu + t * gu_stride + c);
+  const Vec16 uv = load16(gu + t * gu_stride + inter + c);
+  T o[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const float g = vec_elem<T>(gv, e);
+    const float sv = to_f32<T>(round_to<T>(g / (1.f + expf(-g))));
+    o[e] = round_to<T>(sv * vec_elem<T>(uv, e));
+  }
+  store16(out + t * out_stride + c, *reinterpret_cast<const Vec16*>(o));
+}
+
+inline bool aligned_rows(const void* p, int64_t stride_elems, int elem_size) {
+  return p == nullptr || (aligned16(p) && (stride_elems * elem_size) % 16 == 0);
+}
+
 template <typename T>
 int launch_rmsnorm(const void* x, const void* delta, const void* weight, void* h_out, void* y,
                    int32_t rows, int32_t width, int64_t xs, int64_t ds, int64_t hs, int64_t ys,
                    float eps, hipStream_t s) {
+  constexpr int E = 16 / sizeof(T);
+  const int nch = width / E;
+  if (width % E == 0 && aligned_rows(x, xs, sizeof(T)) && aligned_rows(delta, ds, sizeof(T)) &&
+      aligned_rows(weight, 0, sizeof(T)) && aligned_rows(h_out, hs, sizeof(T)) &&
+      aligned_rows(y, ys, sizeof(T)) && nch <= 8 * kNormThreads) {
+    const int nv = (nch + kNormThreads - 1) / kNormThreads;
+#define EDGERAG_NORMV(NV)                                                                       \
+  hipLaunchKernelGGL((rmsnorm_vec_kernel<T, NV>), dim3(rows), dim3(kNormThreads), 0, s,         \
+                     static_cast<const T*>(x), static_cast<const T*>(delta),                    \
+                     static_cast<const T*>(weight), static_cast<T*>(h_out), static_cast<T*>(y), \
+                     width, xs, ds, hs, ys, eps)
+    if (nv <= 1) EDGERAG_NORMV(1);
+    else if (nv <= 2) EDGERAG_NORMV(2);
+    else if (nv <= 4) EDGERAG_NORMV(4);
+    else EDGERAG_NORMV(8);
+#undef EDGERAG_NORMV
+    return check_launch("edgerag_rmsnorm");
+  }
   const int per = (width + kNormThreads - 1) / kNormThreads;
 #define EDGERAG_NORM(P)                                                                         \
   hipLaunchKernelGGL((rmsnorm_kernel<T, P>), dim3(rows), dim3(kNormThreads), 0, s,              \
@@ -228,13 +344,21 @@ extern "C" int edgerag_silu_mul(const void* gate_up, int64_t gate_up_stride, int
   if (n_tokens == 0) return EDGERAG_OK;
   if (gate_up == nullptr || out == nullptr)
     return fail(EDGERAG_EINVAL, "edgerag_silu_mul: NULL pointer");
-  const int64_t total = int64_t(n_tokens) * intermediate;
+  const int es = dtype == EDGERAG_F32 ? 4 : 2;
+  const bool vec = (intermediate * es) % 16 == 0 && aligned_rows(gate_up, gate_up_stride, es) &&
+                   aligned_rows(out, out_stride, es);
+  const int64_t total = int64_t(n_tokens) * (vec ? intermediate * es / 16 : intermediate);
   const dim3 grid(unsigned((total + 255) / 256)), block(256);
   auto s = static_cast<hipStream_t>(stream);
 #define EDGERAG_SILU(TYPE)                                                                      \
-  hipLaunchKernelGGL((silu_mul_kernel<TYPE>), grid, block, 0, s,                                \
-                     static_cast<const TYPE*>(gate_up), gate_up_stride, n_tokens, intermediate, \
-                     static_cast<TYPE*>(out), out_stride)
+  if (vec)                                                                                     \
+    hipLaunchKernelGGL((silu_mul_vec_kernel<TYPE>), grid, block, 0, s,                          \
+                       static_cast<const TYPE*>(gate_up), gate_up_stride, n_tokens,             \
+                       intermediate, static_cast<TYPE*>(out), out_stride);                      \
+  else                                                                                         \
+    hipLaunchKernelGGL((silu_mul_kernel<TYPE>), grid, block, 0, s,                              \
+                       static_cast<const TYPE*>(gate_up), gate_up_stride, n_tokens,             \
+                       intermediate, static_cast<TYPE*>(out), out_stride)
   switch (dtype) {
     case EDGERAG_F32: EDGERAG_SILU(float); break;
     case EDGERAG_F16: EDGERAG_SILU(f16); break;
