@@ -167,11 +167,97 @@ def cfg3_lens():
 # --- config 4: quant linears ---------------------------------------------------------------------
 
 
+# --- access-pattern ceilings (include/edgerag_probe.h) --------------------------------------------
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def probe_read_us(buffers, nbytes, n_launch=256, shapes=((512, 2), (1024, 2), (2048, 1))):
+    """Launch-to-launch time of the streaming-read probe over `nbytes` of each buffer in turn
+    (graph replay of `n_launch` launches, like the cfg4 timings): the best a kernel that only
+    reads the same bytes can do. The fastest of the (workgroups, unroll) launch shapes is kept."""
+    from edgerag_amd import _lib
+
+    sink = torch.zeros(1, dtype=torch.int32, device=buffers[0].device)
+    best = None
+    for wgs, unroll in shapes:
+        def launch(buf):
+            _lib.call("edgerag_probe_read", buf.data_ptr(), nbytes, wgs, unroll, sink.data_ptr(),
+                      _stream())
+
+        launch(buffers[0])
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(n_launch):
+                launch(buffers[i % len(buffers)])
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(3):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (3 * n_launch)
+        del graph
+        best = us if best is None else min(best, us)
+    return best
+
+
+def measure_ceilings(device, gather_bytes):
+    """HBM ceilings of the two access patterns on this GPU (rooflines read against them as well as
+    against the datasheet 8 TB/s): a 1 GiB contiguous stream, and `gather_bytes` read as random
+    2 KiB chunks of a 2 GiB buffer (the paged pool's (head, block) rows) -- the cfg2 decode
+    launch's pattern and byte count."""
+    from edgerag_amd import _lib
+
+    out = {}
+    buf = torch.empty(1 << 30, dtype=torch.uint8, device=device)
+    buf.fill_(1)
+    big = ((1024, 2), (4096, 2), (8192, 4), (16384, 2))
+    out["stream_read_1GiB_gbs"] = round(
+        (1 << 30) / probe_read_us([buf], 1 << 30, 8, shapes=big) / 1e3, 1)
+    del buf
+    pool = torch.empty(2 << 30, dtype=torch.uint8, device=device)
+    pool.fill_(1)
+    per_wave = 128
+    n_chunks = int(gather_bytes // 2048) // per_wave * per_wave
+    gen = torch.Generator(device=device).manual_seed(5)
+    ids = torch.randint(0, (2 << 30) // 2048, (n_chunks,), generator=gen, device=device,
+                        dtype=torch.int32)
+    sink = torch.zeros(1, dtype=torch.int32, device=device)
+
+    def launch():
+        _lib.call("edgerag_probe_gather", pool.data_ptr(), ids.data_ptr(), n_chunks // per_wave,
+                  per_wave, 2048, sink.data_ptr(), _stream())
+
+    launch()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(10):
+        launch()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / 10
+    out["gather_2KiB_gbs"] = round(n_chunks * 2048 / us / 1e3, 1)
+    out["source"] = "bench.py measure_ceilings: edgerag_probe_read / edgerag_probe_gather"
+    del pool, ids
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_quant(device, iters=None):
     """Config 4. Each timing replays a HIP graph of back-to-back launches, one per weight replica
     (>= 1 GiB of distinct packed weights in rotation, so the weights stream from HBM rather than
     the Infinity Cache); the graph removes the host's per-call cost from the launch-to-launch gap.
-    ``us`` is the average launch-to-launch time on the GPU, events on the capture stream."""
+    ``us`` is the average launch-to-launch time on the GPU, events on the capture stream.
+    ``read_us`` is the streaming-read probe over the same packed-weight replicas, the same way:
+    the time any kernel needs just to read those bytes at this size (``read_frac`` = read_us /
+    us for the HBM-bound rows)."""
     shapes = [(2048, 2048, 8, 2048), (2048, 8192, 8, 2048), (8192, 2048, 8, 8192),
               (1152, 1152, 4, 128), (1152, 4608, 4, 128)]
     results = []
@@ -183,6 +269,7 @@ def bench_quant(device, iters=None):
         packed = torch.randint(0, 256, (reps, n, width), generator=gen, device=device,
                                dtype=torch.uint8)
         scales = (torch.rand((reps, n, k // g), generator=gen, device=device) * 1e-3 + 1e-4).half()
+        read_us = probe_read_us([packed[r] for r in range(reps)], n * width, min(reps, 512))
         for m in (1, 8, 32, 64, 512, 544):
             x = torch.randn(m, k, generator=gen, device=device, dtype=torch.float16)
             y = torch.empty(m, n, device=device, dtype=torch.float16)
@@ -212,9 +299,12 @@ def bench_quant(device, iters=None):
             tflops = flops / us / 1e6
             bound = "hbm" if m <= 64 else "mfma"
             frac = gbs / HBM_PEAK_GBS if bound == "hbm" else tflops / MFMA_F16_PEAK_TFLOPS
-            results.append(dict(k=k, n=n, bits=bits, group=g, m=m, us=round(us, 2),
-                                gbs=round(gbs, 1), tflops=round(tflops, 2), bound=bound,
-                                frac=round(frac, 4)))
+            row = dict(k=k, n=n, bits=bits, group=g, m=m, us=round(us, 2),
+                       gbs=round(gbs, 1), tflops=round(tflops, 2), bound=bound,
+                       frac=round(frac, 4), read_us=round(read_us, 2))
+            if bound == "hbm":
+                row["read_frac"] = round(read_us / us, 4)
+            results.append(row)
         del packed, scales
         torch.cuda.empty_cache()
     return results
@@ -416,6 +506,9 @@ def main() -> None:
     del b
     torch.cuda.empty_cache()
     line["config"]["copy_gbs_1gib"] = copy_bandwidth(device)
+    ceilings = measure_ceilings(device, attn_bytes)
+    line["ceilings"] = ceilings
+    line["roofline"]["frac_of_gather_ceiling"] = round(attn_gbs / ceilings["gather_2KiB_gbs"], 4)
     torch.cuda.empty_cache()
     if not args.no_extra:
         line["cfg3"] = run_cfg3(device, args)

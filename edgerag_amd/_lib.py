@@ -36,7 +36,7 @@ ATTN_TILES, ATTN_ROWS, ATTN_COMBINE, ATTN_ALL = 1, 2, 4, 7
 
 DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 
-#: name -> (argtypes, restype). Mirrors include/edgerag_amd.h one to one.
+#: name -> (argtypes, restype). Mirrors the declarations of include/*.h one to one.
 SIGNATURES: dict[str, tuple[list, object]] = {
     "edgerag_last_error": ([], ctypes.c_char_p),
     "edgerag_version": ([], ctypes.c_char_p),
@@ -84,6 +84,9 @@ SIGNATURES: dict[str, tuple[list, object]] = {
          c_vp],
         c_i32,
     ),
+    # include/edgerag_probe.h: measurement probes for the rooflines bench.py reports.
+    "edgerag_probe_read": ([c_vp, c_i64, c_i32, c_i32, c_vp, c_vp], c_i32),
+    "edgerag_probe_gather": ([c_vp, c_vp, c_i32, c_i32, c_i32, c_vp, c_vp], c_i32),
 }
 
 

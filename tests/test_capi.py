@@ -16,12 +16,15 @@ from hypothesis import strategies as st
 
 from edgerag_amd import _lib, kernels
 
-HEADER = Path(__file__).resolve().parents[1] / "include" / "edgerag_amd.h"
+HEADERS = sorted((Path(__file__).resolve().parents[1] / "include").glob("*.h"))
 
 
 def declared_symbols() -> set[str]:
-    text = HEADER.read_text()
-    return set(re.findall(r"^(?:int|const char\*)\s+(edgerag_\w+)\s*\(", text, flags=re.M))
+    names: set[str] = set()
+    for header in HEADERS:
+        text = header.read_text()
+        names |= set(re.findall(r"^(?:int|const char\*)\s+(edgerag_\w+)\s*\(", text, flags=re.M))
+    return names
 
 
 def test_library_exports_every_declared_symbol() -> None:
