@@ -30,6 +30,9 @@
 #ifndef EDGERAG_STREAM_NT2_TILES
 #define EDGERAG_STREAM_NT2_TILES 512  // 16-row tiles from which a workgroup takes two
 #endif
+#ifndef EDGERAG_GEMM_THREADS_128
+#define EDGERAG_GEMM_THREADS_128 256  // threads of a 128x128 GEMM workgroup (256 or 512)
+#endif
 #ifndef EDGERAG_GEMM_MIN_WG
 #define EDGERAG_GEMM_MIN_WG 1  // workgroups per CU the GEMM's register budget must allow
 #endif
@@ -424,7 +427,6 @@ __global__ __launch_bounds__(KW * kWave) void qlinear_stream_kernel(
 }
 
 // ---- tiled GEMM (M > 64) --------------------------------------------------------------------
-constexpr int kGemmThreads = 256;
 constexpr int kBK = 64;     // k per LDS stage
 constexpr int kLdsRow = 64;  // halves per LDS row (one row of a 64-k stage)
 
@@ -437,32 +439,38 @@ __device__ __forceinline__ int lds_off(int row, int c) {
   return ((((row >> 5) * 4 + (c >> 1)) * 2 + (c & 1)) * 32 + (row & 31)) * 8;
 }
 
-template <int BITS, int BN, int BM>
+// A BN x BM tile computed by NTH threads: waves in a 2 x (NTH / 128) grid (N x M), each owning
+// TN x TM 32x32 MFMA tiles. With 512 threads two waves share each SIMD, so one wave's memory
+// and LDS waits overlap the other's matrix work.
+template <int BITS_, int BN_, int BM_, int NTH_>
 struct GemmCfg {
+  static constexpr int BITS = BITS_, BN = BN_, BM = BM_, NTH = NTH_;
+  static constexpr int NWN = 2, NWM = NTH / 128;                    // wave grid
   static constexpr int W_ROW_BYTES = BITS == 8 ? kBK : kBK / 2;    // packed bytes per row, per stage
-  static constexpr int W_BPT = BN * W_ROW_BYTES / kGemmThreads;     // packed bytes per thread
+  static constexpr int W_BPT = BN * W_ROW_BYTES / NTH;              // packed bytes per thread
   static constexpr int W_TPR = W_ROW_BYTES / W_BPT;                 // threads per weight row
-  static constexpr int W_K = BITS == 8 ? W_BPT : 2 * W_BPT;         // k per thread (16 or 32)
-  static constexpr int X_BPT = BM * kBK * 2 / kGemmThreads;         // activation bytes per thread
+  static constexpr int W_K = BITS == 8 ? W_BPT : 2 * W_BPT;         // k per thread (8, 16 or 32)
+  static constexpr int X_BPT = BM * kBK * 2 / NTH;                  // activation bytes per thread
   static constexpr int X_TPR = kBK * 2 / X_BPT;                     // threads per activation row
-  static constexpr int TN = BN / 64, TM = BM / 64;                  // 32x32 tiles per wave
+  static constexpr int TN = BN / (32 * NWN), TM = BM / (32 * NWM);  // 32x32 tiles per wave
+  static_assert(TN >= 1 && TM >= 1, "tile too small for the wave grid");
   static_assert(W_BPT == 8 || W_BPT == 16 || W_BPT == 32, "weight staging split");
   static_assert(X_BPT == 32 || X_BPT == 64, "activation staging split");
 };
 
-template <int BITS, int BN, int BM>
+template <class C>
 struct GemmStage {
-  uint32_t w[GemmCfg<BITS, BN, BM>::W_BPT / 4];
+  uint32_t w[C::W_BPT / 4];
   f16 s;
-  uint4 x[GemmCfg<BITS, BN, BM>::X_BPT / 16];
+  uint4 x[C::X_BPT / 16];
 };
 
 // Loads one 64-k stage of this thread's weight segment (and its group scale) and activation
 // segment into registers.
-template <int BITS, int BN, int BM>
-__device__ __forceinline__ void gemm_load(GemmStage<BITS, BN, BM>& st, int k0, const uint8_t* wrow,
+template <class C>
+__device__ __forceinline__ void gemm_load(GemmStage<C>& st, int k0, const uint8_t* wrow,
                                           const f16* srow, int g, int wk_off, const f16* xrow) {
-  using C = GemmCfg<BITS, BN, BM>;
+  constexpr int BITS = C::BITS;
   const uint8_t* wp = wrow + (BITS == 8 ? k0 : k0 / 2);
   if constexpr (C::W_BPT == 8) {
     const uint2 v = *reinterpret_cast<const uint2*>(wp);
@@ -487,9 +495,10 @@ __device__ __forceinline__ void gemm_load(GemmStage<BITS, BN, BM>& st, int k0, c
 // Writes weight chunk c (8 k) of this thread's staged segment to LDS, dequantised: the exact
 // integer code when PC (per-channel scales, applied to the fp32 sums in the epilogue), else
 // code * scale rounded to fp16 once, as the reference's dequantize_groupwise does.
-template <int BITS, int BN, int BM, bool PC>
-__device__ __forceinline__ void gemm_store_w(const GemmStage<BITS, BN, BM>& st, int c,
-                                             _Float16* sw, int wr, int wc0) {
+template <class C, bool PC>
+__device__ __forceinline__ void gemm_store_w(const GemmStage<C>& st, int c, _Float16* sw, int wr,
+                                             int wc0) {
+  constexpr int BITS = C::BITS;
   h2 p[4];
   if constexpr (BITS == 8) {
     if constexpr (PC) {
@@ -516,9 +525,9 @@ __device__ __forceinline__ void gemm_store_w(const GemmStage<BITS, BN, BM>& st, 
 
 // Writes activation chunk i (8 k) of this thread's staged segment to LDS. Activation rows past M
 // were loaded from row M - 1: they only feed accumulator columns that are never stored.
-template <int BITS, int BN, int BM>
-__device__ __forceinline__ void gemm_store_x(const GemmStage<BITS, BN, BM>& st, int i,
-                                             _Float16* sx, int xr, int xc0) {
+template <class C>
+__device__ __forceinline__ void gemm_store_x(const GemmStage<C>& st, int i, _Float16* sx, int xr,
+                                             int xc0) {
   *reinterpret_cast<uint4*>(sx + lds_off(xr, xc0 + i)) = st.x[i];
 }
 
@@ -528,27 +537,25 @@ __device__ __forceinline__ void gemm_store_x(const GemmStage<BITS, BN, BM>& st, 
 // l % 32, k chunk 2 ks + l / 32 of a 16-k step; accumulator register i of lane l holds
 // row 8 (i / 4) + 4 (l / 32) + i % 4 of A (weight row) and column l % 32 (activation row).
 // PC: per-channel INT8 (one scale per weight row), applied to the fp32 sums.
-template <int BITS, int BN, int BM, bool PC>
-__global__ __launch_bounds__(kGemmThreads, EDGERAG_GEMM_MIN_WG) void qlinear_gemm_kernel(
+template <int BITS, int BN, int BM, bool PC, int NTH>
+__global__ __launch_bounds__(NTH, EDGERAG_GEMM_MIN_WG) void qlinear_gemm_kernel(
     const f16* __restrict__ x, int64_t xs, int32_t m, int32_t k,
     const uint8_t* __restrict__ packed, const f16* __restrict__ scales,
     const f16* __restrict__ bias, int32_t n, int32_t g, f16* __restrict__ y, int64_t ys) {
-  using C = GemmCfg<BITS, BN, BM>;
+  using C = GemmCfg<BITS, BN, BM, NTH>;
   constexpr int NWC = C::W_K / 8, NXC = C::X_BPT / 16;  // LDS chunks this thread stages per step
   __shared__ __attribute__((aligned(16))) _Float16 sw[2][BN * kLdsRow];
   __shared__ __attribute__((aligned(16))) _Float16 sx[2][BM * kLdsRow];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wn = wave & 1, wm = wave >> 1;
+  const int wn = wave % C::NWN, wm = wave / C::NWN;
   const int nb = blockIdx.x * BN, mb = blockIdx.y * BM;
   const int64_t row_bytes = BITS == 8 ? k : k / 2;
   const int groups = k / g;
 
-  // Staging roles: weight row wr (segment wseg), activation row xr (segment xseg). Consecutive
-  // lanes take consecutive rows of one segment, so that each 16-lane group of an LDS write fills
-  // 16 consecutive operand slots (256 contiguous bytes: no bank conflicts).
-  constexpr int WROWS = 64 / C::W_TPR, XROWS = 64 / C::X_TPR;  // rows staged per wave
-  const int wr = wave * WROWS + lane % WROWS, wseg = lane / WROWS;
-  const int xr = wave * XROWS + lane % XROWS, xseg = lane / XROWS;
+  // Staging roles: weight row wr (segment wseg), activation row xr (segment xseg); the threads
+  // of one row are adjacent lanes, so each global load instruction touches few cache lines.
+  const int wr = tid / C::W_TPR, wseg = tid % C::W_TPR;
+  const int xr = tid / C::X_TPR, xseg = tid % C::X_TPR;
   const int wrow_g = min(nb + wr, n - 1);
   const uint8_t* wrow = packed + int64_t(wrow_g) * row_bytes + wseg * C::W_BPT;
   const f16* srow = scales + int64_t(wrow_g) * groups;
@@ -573,12 +580,12 @@ __global__ __launch_bounds__(kGemmThreads, EDGERAG_GEMM_MIN_WG) void qlinear_gem
                       h8 (&b)[C::TM]) {
 #pragma unroll
     for (int i = 0; i < C::TN; ++i)
-      a[i] = *reinterpret_cast<const h8*>(swb + lds_off(wn * (BN / 2) + 32 * i + col, 2 * ks + half));
+      a[i] = *reinterpret_cast<const h8*>(swb + lds_off(wn * (32 * C::TN) + 32 * i + col, 2 * ks + half));
 #pragma unroll
     for (int j = 0; j < C::TM; ++j)
-      b[j] = *reinterpret_cast<const h8*>(sxb + lds_off(wm * (BM / 2) + 32 * j + col, 2 * ks + half));
+      b[j] = *reinterpret_cast<const h8*>(sxb + lds_off(wm * (32 * C::TM) + 32 * j + col, 2 * ks + half));
   };
-  auto step = [&](const _Float16* swb, const _Float16* sxb, const GemmStage<BITS, BN, BM>& st,
+  auto step = [&](const _Float16* swb, const _Float16* sxb, const GemmStage<C>& st,
                   _Float16* dw, _Float16* dx) {
     h8 a[2][C::TN], b[2][C::TM];
     read_ops(swb, sxb, 0, a[0], b[0]);
@@ -587,10 +594,10 @@ __global__ __launch_bounds__(kGemmThreads, EDGERAG_GEMM_MIN_WG) void qlinear_gem
       if (ks + 1 < kBK / 16) read_ops(swb, sxb, ks + 1, a[(ks + 1) & 1], b[(ks + 1) & 1]);
 #pragma unroll
       for (int c = ks * NWC / 4; c < (ks + 1) * NWC / 4; ++c)
-        gemm_store_w<BITS, BN, BM, PC>(st, c, dw, wr, wc0);
+        gemm_store_w<C, PC>(st, c, dw, wr, wc0);
 #pragma unroll
       for (int i = ks * NXC / 4; i < (ks + 1) * NXC / 4; ++i)
-        gemm_store_x<BITS, BN, BM>(st, i, dx, xr, xc0);
+        gemm_store_x<C>(st, i, dx, xr, xc0);
 #pragma unroll
       for (int i = 0; i < C::TN; ++i)
 #pragma unroll
@@ -614,27 +621,27 @@ __global__ __launch_bounds__(kGemmThreads, EDGERAG_GEMM_MIN_WG) void qlinear_gem
   uint32_t ep_s = PC ? scales16[ep_row] : 0u;
   uint32_t ep_b = bias != nullptr ? bias16[ep_row] : 0u;
 
-  GemmStage<BITS, BN, BM> st0, st1;
+  GemmStage<C> st0, st1;
   const int last = (nk - 1) * kBK;
-  gemm_load<BITS, BN, BM>(st0, 0, wrow, srow, g, wk_off, xrow);
-  gemm_load<BITS, BN, BM>(st1, min(kBK, last), wrow, srow, g, wk_off, xrow);
+  gemm_load<C>(st0, 0, wrow, srow, g, wk_off, xrow);
+  gemm_load<C>(st1, min(kBK, last), wrow, srow, g, wk_off, xrow);
   issue_fence();
   asm volatile("" : "+v"(ep_s), "+v"(ep_b));
 #pragma unroll
-  for (int c = 0; c < NWC; ++c) gemm_store_w<BITS, BN, BM, PC>(st0, c, sw[0], wr, wc0);
+  for (int c = 0; c < NWC; ++c) gemm_store_w<C, PC>(st0, c, sw[0], wr, wc0);
 #pragma unroll
-  for (int i = 0; i < NXC; ++i) gemm_store_x<BITS, BN, BM>(st0, i, sx[0], xr, xc0);
+  for (int i = 0; i < NXC; ++i) gemm_store_x<C>(st0, i, sx[0], xr, xc0);
   __syncthreads();
-  gemm_load<BITS, BN, BM>(st0, min(2 * kBK, last), wrow, srow, g, wk_off, xrow);
+  gemm_load<C>(st0, min(2 * kBK, last), wrow, srow, g, wk_off, xrow);
   issue_fence();
   for (int kt = 0; kt < nk; kt += 2) {
     step(sw[0], sx[0], st1, sw[1], sx[1]);
     __syncthreads();
-    gemm_load<BITS, BN, BM>(st1, min((kt + 3) * kBK, last), wrow, srow, g, wk_off, xrow);
+    gemm_load<C>(st1, min((kt + 3) * kBK, last), wrow, srow, g, wk_off, xrow);
     issue_fence();
     if (kt + 1 < nk) step(sw[1], sx[1], st0, sw[0], sx[0]);
     __syncthreads();
-    gemm_load<BITS, BN, BM>(st0, min((kt + 4) * kBK, last), wrow, srow, g, wk_off, xrow);
+    gemm_load<C>(st0, min((kt + 4) * kBK, last), wrow, srow, g, wk_off, xrow);
     issue_fence();
   }
 
@@ -648,7 +655,7 @@ __global__ __launch_bounds__(kGemmThreads, EDGERAG_GEMM_MIN_WG) void qlinear_gem
   for (int i = 0; i < C::TN; ++i) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int nrow_l = wn * (BN / 2) + 32 * i + 8 * q + 4 * half;  // row within the tile
+      const int nrow_l = wn * (32 * C::TN) + 32 * i + 8 * q + 4 * half;  // row within the tile
       const int nrow = nb + nrow_l;
       float sc[4], bv[4];
 #pragma unroll
@@ -659,7 +666,7 @@ __global__ __launch_bounds__(kGemmThreads, EDGERAG_GEMM_MIN_WG) void qlinear_gem
       }
 #pragma unroll
       for (int j = 0; j < C::TM; ++j) {
-        const int mrow = mb + wm * (BM / 2) + 32 * j + col;
+        const int mrow = mb + wm * (32 * C::TM) + 32 * j + col;
         if (mrow >= m) continue;
         f16* yr = y + int64_t(mrow) * ys;
         float v[4];
@@ -728,17 +735,17 @@ void launch_skinny(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t
 #undef EDGERAG_SKINNY
 }
 
-template <int BITS, int BN, int BM>
+template <int BITS, int BN, int BM, int NTH = 256>
 void launch_gemm(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
                  const f16* scales, const f16* bias, int32_t n, int32_t g, f16* y, int64_t ys,
                  hipStream_t s) {
   const dim3 grid(unsigned((n + BN - 1) / BN), unsigned((m + BM - 1) / BM));
   if (BITS == 8 && g == k)
-    hipLaunchKernelGGL((qlinear_gemm_kernel<BITS, BN, BM, BITS == 8>), grid, dim3(kGemmThreads),
-                       0, s, x, xs, m, k, packed, scales, bias, n, g, y, ys);
+    hipLaunchKernelGGL((qlinear_gemm_kernel<BITS, BN, BM, BITS == 8, NTH>), grid, dim3(NTH), 0, s,
+                       x, xs, m, k, packed, scales, bias, n, g, y, ys);
   else
-    hipLaunchKernelGGL((qlinear_gemm_kernel<BITS, BN, BM, false>), grid, dim3(kGemmThreads), 0,
-                       s, x, xs, m, k, packed, scales, bias, n, g, y, ys);
+    hipLaunchKernelGGL((qlinear_gemm_kernel<BITS, BN, BM, false, NTH>), grid, dim3(NTH), 0, s, x,
+                       xs, m, k, packed, scales, bias, n, g, y, ys);
 }
 
 // The streaming kernel's shape: k-slices F and row tiles NT from N alone (two k-slices when
@@ -848,7 +855,8 @@ void dispatch(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* pac
   const int64_t t128 = int64_t((n + 127) / 128) * ((m + 127) / 128);
   const int64_t t128x64 = int64_t((n + 127) / 128) * ((m + 63) / 64);
   if (t128 >= EDGERAG_GEMM_TARGET_WGS)
-    launch_gemm<BITS, 128, 128>(x, xs, m, k, packed, scales, bias, n, g, y, ys, s);
+    launch_gemm<BITS, 128, 128, EDGERAG_GEMM_THREADS_128>(x, xs, m, k, packed, scales, bias, n, g,
+                                                          y, ys, s);
   else if (t128x64 >= EDGERAG_GEMM_TARGET_WGS)
     launch_gemm<BITS, 128, 64>(x, xs, m, k, packed, scales, bias, n, g, y, ys, s);
   else
