@@ -25,7 +25,7 @@
 #define EDGERAG_SKINNY_MAX_M 64
 #endif
 #ifndef EDGERAG_STREAM_MAX_M
-#define EDGERAG_STREAM_MAX_M 16  // per-channel INT8 launches up to this M use the streaming kernel
+#define EDGERAG_STREAM_MAX_M 64  // per-channel INT8 launches up to this M use the streaming kernel
 #endif
 #ifndef EDGERAG_STREAM_NT2_TILES
 #define EDGERAG_STREAM_NT2_TILES 512  // 16-row tiles from which a workgroup takes two
@@ -312,14 +312,15 @@ __global__ __launch_bounds__(KWMAX * kWave) void qlinear_skinny_kernel(
 // The dequantised weight is the exact integer code (no scale): the row's scale multiplies the fp32
 // sum once, scale * sum(code * x), instead of rounding every code * scale to fp16 first.
 template <int F, int NT, int MT, int KW, int U, bool EXACT>
-__global__ __launch_bounds__(KW * kWave) void qlinear_stream_kernel(
+__global__ __launch_bounds__(KW * kWave)
+__attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlinear_stream_kernel(
     const f16* __restrict__ x, int64_t xs, int32_t m, int32_t k,
     const uint8_t* __restrict__ packed, const f16* __restrict__ scales,
     const f16* __restrict__ bias, int32_t n, f16* __restrict__ y, int64_t ys) {
   constexpr int R = 16 / F;
   constexpr int CB = 64 * F;               // bytes (= k) of one chunk step of a row
   constexpr int OUTS = NT * MT * R * R;    // outputs (token, row) of a workgroup
-  static_assert(OUTS <= KW * kWave, "one output per thread");
+  static_assert((KW * kWave) % (NT * R) == 0, "a thread's outputs share one weight row");
   __shared__ float red[KW * NT * MT * 4 * kWave];
   const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63;
@@ -340,12 +341,19 @@ __global__ __launch_bounds__(KW * kWave) void qlinear_stream_kernel(
 #pragma unroll
   for (int t = 0; t < MT; ++t) xp[t] = x + int64_t(min(t * R + r, m - 1)) * xs + f * 64 + 16 * lg;
 
-  // Thread e < OUTS writes row n0 + e % (NT R) of token e / (NT R). Its scale and bias are loaded
-  // now and first waited for after the first batch's loads are issued.
-  const int e = threadIdx.x;
-  const int e_row = min(n0 + (e < OUTS ? e % (NT * R) : 0), n - 1);
-  uint32_t s_bits = reinterpret_cast<const uint16_t*>(scales)[e_row];
-  uint32_t b_bits = bias != nullptr ? reinterpret_cast<const uint16_t*>(bias)[e_row] : 0u;
+  // Output e (e = thread, thread + KW 64, ...) is row n0 + e % (NT R) of token e / (NT R): all
+  // of a thread's outputs share one row, whose scale and bias are loaded now and first waited for
+  // after the first batch is computed.
+  // Whole aligned 32-bit words are loaded (nothing is computed on them before the pins), and the
+  // bias word unconditionally -- from the scales when there is no bias -- so that no branch sits
+  // between these loads and the batch loads (either would cost the batch its progressive waits).
+  const int e_row = min(n0 + int(threadIdx.x) % (NT * R), n - 1);
+  const f16* b_src = bias != nullptr ? bias : scales;
+  const int s_mis = int(reinterpret_cast<uintptr_t>(scales) >> 1) & 1;  // base at an odd half
+  const int b_mis = int(reinterpret_cast<uintptr_t>(b_src) >> 1) & 1;
+  const int s_idx = e_row + s_mis, b_idx = e_row + b_mis;
+  uint32_t s_bits = reinterpret_cast<const uint32_t*>(scales - s_mis)[s_idx >> 1];
+  uint32_t b_bits = reinterpret_cast<const uint32_t*>(b_src - b_mis)[b_idx >> 1];
 
   f32x4 acc[NT][MT];
 #pragma unroll
@@ -371,7 +379,6 @@ __global__ __launch_bounds__(KW * kWave) void qlinear_stream_kernel(
       }
     }
     issue_fence();
-    if (cb == c0) asm volatile("" : "+v"(s_bits), "+v"(b_bits));
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const bool on = EXACT || (cs + u >= cb && cs + u < c1);
@@ -397,6 +404,8 @@ __global__ __launch_bounds__(KW * kWave) void qlinear_stream_kernel(
         }
       }
     }
+    // The epilogue's scale and bias are waited for here, once the first batch is computed.
+    if (cb == c0) asm volatile("" : "+v"(s_bits), "+v"(b_bits));
   }
 
   // Sum slices and waves in a fixed order, then y[m][n] = scale[n] * sum (+ bias[n]).
@@ -409,21 +418,29 @@ __global__ __launch_bounds__(KW * kWave) void qlinear_stream_kernel(
       for (int i = 0; i < 4; ++i)
         red[(((wave * NT + tn) * MT + t) * 4 + i) * kWave + lane] = acc[tn][t][i];
   __syncthreads();
-  const int tok = e / (NT * R), row_in = e % (NT * R);
-  const int tn = row_in / R, rr = row_in % R;
-  const int t = tok / R, jj = tok % R;
-  const int nrow = n0 + row_in;
-  if (e >= OUTS || tok >= m || nrow >= n) return;
-  float sum = 0.f;
+  // (Consumed again here so that the conversions below are not hoisted above the main loop,
+  // which would wait for the loads before the first batch is issued.)
+  asm volatile("" : "+v"(s_bits), "+v"(b_bits));
+  const int sh_s = (s_idx & 1) * 16, sh_b = (b_idx & 1) * 16;
+  const float scale = float(__builtin_bit_cast(_Float16, uint16_t(s_bits >> sh_s)));
+  const float bv =
+      bias != nullptr ? float(__builtin_bit_cast(_Float16, uint16_t(b_bits >> sh_b))) : 0.f;
+  for (int e = threadIdx.x; e < OUTS; e += KW * kWave) {
+    const int tok = e / (NT * R), row_in = e % (NT * R);
+    const int tn = row_in / R, rr = row_in % R;
+    const int t = tok / R, jj = tok % R;
+    const int nrow = n0 + row_in;
+    if (tok >= m || nrow >= n) continue;
+    float sum = 0.f;
 #pragma unroll
-  for (int fs = 0; fs < F; ++fs) {
-    const int drow = fs * R + rr, dcol = fs * R + jj;
-    const int l = 16 * (drow >> 2) + dcol, i = drow & 3;
-    for (int wv = 0; wv < KW; ++wv) sum += red[(((wv * NT + tn) * MT + t) * 4 + i) * kWave + l];
+    for (int fs = 0; fs < F; ++fs) {
+      const int drow = fs * R + rr, dcol = fs * R + jj;
+      const int l = 16 * (drow >> 2) + dcol, i = drow & 3;
+      for (int wv = 0; wv < KW; ++wv)
+        sum += red[(((wv * NT + tn) * MT + t) * 4 + i) * kWave + l];
+    }
+    y[int64_t(tok) * ys + nrow] = __float2half_rn(scale * sum + bv);
   }
-  float v = float(__builtin_bit_cast(_Float16, uint16_t(s_bits))) * sum;
-  if (bias != nullptr) v += float(__builtin_bit_cast(_Float16, uint16_t(b_bits)));
-  y[int64_t(tok) * ys + nrow] = __float2half_rn(v);
 }
 
 // ---- tiled GEMM (M > 64) --------------------------------------------------------------------
@@ -774,16 +791,25 @@ void launch_stream_k(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8
   // One batch of at most 8 steps per wave; at least 4 waves (one per SIMD), or 8 for two row
   // tiles (one output per thread); at most 16, or 8 for two row or m tiles, whose registers
   // would not fit 16 waves.
+  // The waves (so the K split, so the bits) depend on K, F and NT only, except that 16-wave
+  // workgroups (K > 64 F steps) drop to 8 where their registers would not fit (F = 2 with two
+  // m-tiles, four m-tiles); several m-tiles take batches of 4 steps to bound their activation
+  // registers.
   const int nc = k / (64 * F);
   constexpr int kw_min = NT == 1 ? 4 : 8;
-  constexpr int kw_max = NT == 1 && MT == 1 ? 16 : 8;
+  constexpr int kw_max = NT == 1 && MT < 4 && !(F == 2 && MT == 2) ? 16 : 8;
   int kw = kw_min;
   while (kw < kw_max && kw * 8 < nc) kw *= 2;
-  const bool u8 = (nc + kw - 1) / kw > 4 && nc >= 8;
+  const bool u8 = MT == 1 && (nc + kw - 1) / kw > 4 && nc >= 8;
 #define EDGERAG_STREAM(KW)                                                                      \
   do {                                                                                         \
-    if (u8) launch_stream<F, NT, MT, KW, 8>(x, xs, m, k, packed, scales, bias, n, y, ys, s);   \
-    else launch_stream<F, NT, MT, KW, 4>(x, xs, m, k, packed, scales, bias, n, y, ys, s);      \
+    if constexpr (MT == 1) {                                                                   \
+      if (u8) {                                                                                \
+        launch_stream<F, NT, MT, KW, 8>(x, xs, m, k, packed, scales, bias, n, y, ys, s);       \
+        break;                                                                                 \
+      }                                                                                        \
+    }                                                                                          \
+    launch_stream<F, NT, MT, KW, 4>(x, xs, m, k, packed, scales, bias, n, y, ys, s);           \
   } while (0)
   if constexpr (kw_min == 4) {
     if (kw == 4) {
@@ -804,8 +830,20 @@ void launch_stream_k(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8
 bool dispatch_stream(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
                      const f16* scales, const f16* bias, int32_t n, f16* y, int64_t ys,
                      hipStream_t s) {
-  if (m > 16) return false;
+  if (m > 64) return false;
   const int64_t tiles16 = (n + 15) / 16;
+  if (m > 16) {  // 17..64 tokens: one k-slice, up to four 16-token m-tiles
+    if (k % 64 != 0 || k / 64 < 4) return false;
+    const bool two = tiles16 >= EDGERAG_STREAM_NT2_TILES;
+    if (m <= 32) {
+      if (two) launch_stream_k<1, 2, 2>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
+      else launch_stream_k<1, 1, 2>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
+    } else {
+      if (two) launch_stream_k<1, 2, 4>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
+      else launch_stream_k<1, 1, 4>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
+    }
+    return true;
+  }
   if (tiles16 < 256) {  // 16-row tiles would not cover the 256 CUs: two k-slices, 8-row tiles
     if (k % 128 != 0 || k / 128 < 4) return false;
     if (m <= 8) launch_stream_k<2, 1, 1>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
