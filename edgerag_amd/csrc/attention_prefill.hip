@@ -7,8 +7,8 @@
 // Per 64-key tile:
 //   * the workgroup stages K row-major and V transposed (V^T[dim][key]) into one of two LDS
 //     buffers straight from the paged pool with raw buffer loads: keys without a valid block get
-//     an out-of-range offset and load zeros, no branch. The next tile's loads are issued before
-//     the current tile is computed, so HBM/L2 latency overlaps the matrix work; one barrier per
+//     an out-of-range offset and load zeros, no branch. A tile's loads are issued two tiles
+//     before it is staged, so HBM/L2 latency overlaps two tiles of matrix work; one barrier per
 //     tile. LDS rows are 128 bytes with the 16-byte chunk index XOR-swizzled by the row, so the
 //     MFMA operand reads and the staging writes are bank-conflict free.
 //   * each wave computes S^T = K Q^T with v_mfma_f32_32x32x16_f16: A = 32 keys x 16 dims from
@@ -105,9 +105,15 @@ __device__ __forceinline__ void stage_load(StageRegs& st, int tid, int k0, const
     const int p = tid + kThreads * j;
     if (kVPairs % kThreads != 0 && p >= kVPairs) break;
     const int a = p % 16, b = p / 16;
+    // The 4 keys of a quad share one block (blocks hold a multiple of 4 keys): one lookup, then
+    // consecutive rows; keys past the split still get the out-of-range offset.
+    const int pos = k0 + 4 * a;
+    const uint32_t base = pool_offset(geo, sblk, pos, b);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
-      st.v[4 * j + kk] = buffer_load16(vrs, pool_offset(geo, sblk, k0 + 4 * a + kk, b));
+      st.v[4 * j + kk] = buffer_load16(
+          vrs, (base != kOutOfRange && pos + kk < geo.ke) ? base + uint32_t(kk * kD * 2)
+                                                          : kOutOfRange);
   }
 }
 
@@ -179,14 +185,19 @@ void attn_prefill_mfma_kernel(
   geo.bs_shift = bs_shift;
   geo.bs_mask = block_size - 1;
   // Block ids of the whole split, once (the planner caps a split at kMaxTileBlocks blocks).
+  // Whether any of them is invalid (never in a well-formed table) decides once per item whether
+  // tiles check for invalid keys.
+  int any_bad = 0;
   {
     const int nblk = min(((ke - 1) >> bs_shift) - geo.blk0 + 1, kMaxTileBlocks);
     for (int i = tid; i < nblk; i += kThreads) {
       const int32_t b = table[geo.blk0 + i];
-      sblk[i] = (b >= 0 && b < num_blocks) ? b : -1;
+      const bool ok = b >= 0 && b < num_blocks;
+      sblk[i] = ok ? b : -1;
+      any_bad |= ok ? 0 : 1;
     }
   }
-  __syncthreads();
+  const bool item_has_bad = __syncthreads_or(any_bad) != 0;
 
   // Q^T as the B operand: k-step ks covers dims 16*ks + 8*g .. +7 of this lane's query.
   h8 qop[4];
@@ -207,17 +218,8 @@ void attn_prefill_mfma_kernel(
   const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<_Float16*>(vpool + head_base * block_size * kD), 0, head_bytes, 0x00020000);
 
-  StageRegs st;
-  stage_load(st, tid, kb, geo, sblk, krs, vrs);
-  int buf = 0;
-  for (int k0 = kb; k0 < ke; k0 += kKeys, buf ^= 1) {
-    stage_store(st, tid, sk[buf], svt[buf]);
-    __syncthreads();
-    if (k0 + kKeys < ke) stage_load(st, tid, k0 + kKeys, geo, sblk, krs, vrs);
-    if (!wave_live) continue;
-    const _Float16* skb = sk[buf];
-    const _Float16* svb = svt[buf];
-
+  // One 64-key tile on staged LDS buffers (skb, svb).
+  auto tile = [&](int k0, const _Float16* skb, const _Float16* svb) {
     // S^T = K Q^T: two 32-key tiles, 4 k-steps of 16 dims (dim chunk 2ks + g).
     f32x16 s[2] = {{}, {}};
 #pragma unroll
@@ -239,8 +241,12 @@ void attn_prefill_mfma_kernel(
           if (32 * kt + (i & 3) + 8 * (i >> 2) + 4 * g >= vis_end) s[kt][i] = -INFINITY;
     }
     // Keys whose block id is invalid (never in a well-formed table): masked too.
-    const int bi = min(((k0 + min(lane, key_end - 1)) >> bs_shift) - geo.blk0, kMaxTileBlocks - 1);
-    const uint64_t bad = __ballot(lane < key_end && sblk[bi] < 0);
+    uint64_t bad = 0;
+    if (item_has_bad) {
+      const int bi =
+          min(((k0 + min(lane, key_end - 1)) >> bs_shift) - geo.blk0, kMaxTileBlocks - 1);
+      bad = __ballot(lane < key_end && sblk[bi] < 0);
+    }
     if (bad != 0) {
       // Lane group g's keys of tile kt are bits (i%4) + 8(i/4) of (bad_kt >> 4g).
       const uint32_t b0 = uint32_t(bad) >> (4 * g), b1 = uint32_t(bad >> 32) >> (4 * g);
@@ -290,6 +296,26 @@ void attn_prefill_mfma_kernel(
     }
     lsum += __shfl_xor(lsum, 32, kWave);
     l += lsum;
+  };
+
+  // Register stages st0 / st1 alternate, so a tile's loads are issued two tiles before it is
+  // staged to LDS and have two tiles of matrix work to land. Loads past the split need no branch:
+  // their positions get out-of-range offsets and load zeros. One barrier per tile: it orders the
+  // tile's LDS writes before its reads, and every wave's reads of a buffer before its rewrite.
+  StageRegs st0, st1;
+  stage_load(st0, tid, kb, geo, sblk, krs, vrs);
+  stage_load(st1, tid, kb + kKeys, geo, sblk, krs, vrs);
+  for (int k0 = kb; k0 < ke; k0 += 2 * kKeys) {
+    stage_store(st0, tid, sk[0], svt[0]);
+    __syncthreads();
+    stage_load(st0, tid, k0 + 2 * kKeys, geo, sblk, krs, vrs);
+    if (wave_live) tile(k0, sk[0], svt[0]);
+    if (k0 + kKeys < ke) {
+      stage_store(st1, tid, sk[1], svt[1]);
+      __syncthreads();
+      stage_load(st1, tid, k0 + 3 * kKeys, geo, sblk, krs, vrs);
+      if (wave_live) tile(k0 + kKeys, sk[1], svt[1]);
+    }
   }
 
   if (!active) return;
@@ -332,9 +358,9 @@ int log2_exact(int v) {
 }  // namespace
 
 bool prefill_tiles_supported(int32_t num_blocks, int32_t block_size) {
-  // Power-of-two blocks (shift addressing), and one kv head's slice of a pool must fit a
-  // buffer resource, below kOutOfRange.
-  return log2_exact(block_size) >= 0 &&
+  // Power-of-two blocks of at least 4 keys (shift addressing; a V key quad never straddles a
+  // block), and one kv head's slice of a pool must fit a buffer resource, below kOutOfRange.
+  return log2_exact(block_size) >= 2 &&
          int64_t(num_blocks) * block_size * kD * 2 < int64_t(kOutOfRange);
 }
 

@@ -393,3 +393,30 @@ def test_cfg2_shape_decode_batch_fp16(device) -> None:
                                  0.125).cpu()
     expected = oa.ragged_reference(q, kp_d.cpu(), vp_d.cpu(), qsl.tolist(), lens, tables, 0.125)
     torch.testing.assert_close(got.float(), expected, **FP16_TOL)
+
+
+@pytest.mark.parametrize("q_len", [1, 200])
+def test_invalid_block_ids_mask_their_keys(device, q_len) -> None:
+    """A block id outside [0, num_blocks) (never produced by the allocator) hides its 16 keys
+    instead of reading out of bounds; the decode row kernel (q_len 1) and the MFMA prefill tiles
+    (q_len 200) agree with a float64 softmax that excludes exactly those keys."""
+    L, n_q, n_kv, d = 600, 8, 4, 64
+    kp, vp, tables, qsl, q, bt = _ragged_case([L], [q_len], n_q, n_kv, d, torch.float16, 91,
+                                              poison=False)
+    NB = kp.shape[1]
+    bt[0, 5] = -1
+    bt[0, 20] = NB + 3
+    bad = torch.zeros(L, dtype=torch.bool)
+    bad[5 * BLOCK_SIZE : 6 * BLOCK_SIZE] = True
+    bad[20 * BLOCK_SIZE : 21 * BLOCK_SIZE] = True
+    got = _run_ragged(device, kp, vp, qsl, [L], bt, q, 0.125)
+    k = op.gather_pool(kp.double(), tables[0], L)  # (n_kv, L, d), real contents of every block
+    v = op.gather_pool(vp.double(), tables[0], L)
+    pos = torch.arange(L)
+    for h in range(n_q):
+        qh = q[:, h].double()  # (q_len, d)
+        s = qh @ k[h // 2].T * 0.125
+        visible = (pos[None, :] <= (L - q_len + torch.arange(q_len))[:, None]) & ~bad[None, :]
+        s = s.masked_fill(~visible, float("-inf"))
+        ref = torch.softmax(s, dim=-1) @ v[h // 2]
+        torch.testing.assert_close(got[:, h].double(), ref, rtol=1e-2, atol=2e-3)
