@@ -21,7 +21,8 @@
 //   3. attn_rows_kernel: the general version of (2) for shapes the fast path does not cover
 //      (block_size not a multiple of the tokens-per-load, or prefill tiles before the MFMA path).
 //   4. attn_combine_kernel merges the fp32 split partials (m, l, acc) of split requests, one
-//      wave per (token, query head); unsplit requests are written directly by (2)/(3).
+//      thread per (token, query head, 4 output elements); unsplit requests are written directly
+//      by (2)/(3).
 // Scores are kept in the log2 domain (scaled by scale * log2(e)) so each exponential is one
 // v_exp_f32.
 #include <algorithm>
@@ -133,65 +134,6 @@ struct QReg {
   }
   static constexpr bool kScaleAfter = __is_same(T, f16);
 };
-
-// ---- merging split partials -----------------------------------------------------------------------
-// One wave merges the fp32 partials (m, l, acc[D]) of query row t / head hq: lanes load the split
-// maxima in parallel, then each lane owns D / 64 (at least one) output elements.
-template <typename T>
-__device__ __forceinline__ void combine_pair(int t, int hq, int q0, int c, int L, int nsplit,
-                                             int split_len, int part_off, int n_q_heads,
-                                             int head_dim, const float2* __restrict__ part_ml,
-                                             const float* __restrict__ part_acc, T* __restrict__ out,
-                                             int64_t o_st, int64_t o_sh, int lane) {
-  const int lim = L - c + (t - q0);
-  const int n_valid = lim < 0 ? 0 : min(nsplit, lim / split_len + 1);
-  const int64_t base = int64_t(part_off) + (int64_t(t - q0) * n_q_heads + hq) * nsplit;
-  float mmax = -INFINITY;
-  for (int s = lane; s < n_valid; s += kWave) mmax = fmaxf(mmax, part_ml[base + s].x);
-#pragma unroll
-  for (int b = 0; b < 6; ++b) mmax = fmaxf(mmax, __shfl_xor(mmax, 1 << b, kWave));
-  float lsum = 0.f;
-  float a[4] = {0.f, 0.f, 0.f, 0.f};  // head_dim <= 256
-  if (mmax != -INFINITY) {
-    for (int s0 = 0; s0 < n_valid; s0 += kWave) {
-      float w = 0.f;
-      if (s0 + lane < n_valid) {
-        const float2 ml = part_ml[base + s0 + lane];
-        w = exp2_fast(ml.x - mmax);
-        lsum = fmaf(w, ml.y, lsum);
-      }
-      const int cnt = min(kWave, n_valid - s0);
-      // Issue 8 splits' loads before consuming any, so their latencies overlap.
-      for (int sb = 0; sb < cnt; sb += 8) {
-        float vals[8][4];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const float* pa = part_acc + (base + s0 + sb + k) * head_dim;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int x = lane + i * kWave;
-            vals[k][i] = (sb + k < cnt && x < head_dim) ? pa[x] : 0.f;
-          }
-        }
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const float ws = __shfl(w, sb + k, kWave);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) a[i] = fmaf(ws, vals[k][i], a[i]);
-        }
-      }
-    }
-  }
-#pragma unroll
-  for (int b = 0; b < 6; ++b) lsum += __shfl_xor(lsum, 1 << b, kWave);
-  const float inv = 1.f / fmaxf(lsum, 1.17549435e-38f);
-  T* op = out + int64_t(t) * o_st + int64_t(hq) * o_sh;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int x = lane + i * kWave;
-    if (x < head_dim) op[x] = from_f32<T>(a[i] * inv);
-  }
-}
 
 // ---- fast decode kernel --------------------------------------------------------------------------
 // Requires block_size % TPW == 0 and at most kMaxSplitBlocks blocks per split (checked by the
@@ -469,22 +411,113 @@ __global__ __launch_bounds__(kWave) void attn_rows_kernel(
 }
 
 // ---- combine -----------------------------------------------------------------------------------
-// Merges split partials: one wave per (combine-list row, query head). The list entry carries the
-// request's geometry, so a wave's dependent loads are entry -> (m, l) -> acc.
-template <typename T>
+// Merges split partials (m, l, acc[D]) into the output: one thread per (combine-list row, query
+// head, 4 consecutive output elements), so a (row, head) pair takes D / 4 adjacent lanes and every
+// partial load is one 16-byte access. A thread issues the (m, l) and acc loads of up to
+// kCombineBatch splits together (the acc loads do not depend on (m, l)), so the chain of dependent
+// loads is entry -> {(m, l), acc}; more splits are merged batch by batch with a running maximum.
+// n_rows < 0 / combine_off < 0: read the list's length / offset from the device plan header
+// (fixed-capacity launches).
+constexpr int kCombineBatch = 8;
+
+template <typename T, bool VEC_OUT>
 __global__ __launch_bounds__(256) void attn_combine_kernel(
-    const int32_t* __restrict__ plan, int32_t combine_off, int32_t n_q_heads, int32_t head_dim,
-    const float2* __restrict__ part_ml, const float* __restrict__ part_acc, T* __restrict__ out,
-    int64_t o_st, int64_t o_sh) {
-  const int hq = blockIdx.y * (blockDim.x / kWave) + threadIdx.x / kWave;
-  const int lane = threadIdx.x % kWave;
-  if (hq >= n_q_heads || int(blockIdx.x) >= plan[H_N_COMBINE]) return;
-  // combine_off < 0: read the list's offset from the device plan (fixed-capacity launches).
+    const int32_t* __restrict__ plan, int32_t n_rows, int32_t combine_off, int32_t n_q_heads,
+    int32_t ch_log2, const float2* __restrict__ part_ml, const float4* __restrict__ part_acc,
+    T* __restrict__ out, int64_t o_st, int64_t o_sh) {
+  const int gid = int(blockIdx.x) * int(blockDim.x) + int(threadIdx.x);
+  const int ch = gid & ((1 << ch_log2) - 1);
+  const int pair = gid >> ch_log2;
+  const int row = pair / n_q_heads;
+  const int hq = pair - row * n_q_heads;
+  if (row >= (n_rows >= 0 ? n_rows : plan[H_N_COMBINE])) return;
   const int off = combine_off >= 0 ? combine_off : plan[H_COMBINE_OFF];
-  const int4* e4 = reinterpret_cast<const int4*>(plan + off + int64_t(blockIdx.x) * kCombineWords);
-  const int4 a = e4[0], b = e4[1];  // {tok, q0, c, L}, {nsplit, split_len, part_off, pad}
-  combine_pair<T>(a.x, hq, a.y, a.z, a.w, b.x, b.y, b.z, n_q_heads, head_dim, part_ml, part_acc,
-                  out, o_st, o_sh, lane);
+  const int4* e4 = reinterpret_cast<const int4*>(plan + off + int64_t(row) * kCombineWords);
+  const int4 ea = e4[0], eb = e4[1];  // {tok, q0, c, L}, {nsplit, split_len, part_off, pad}
+  const int t = ea.x, q0 = ea.y, c = ea.z, L = ea.w;
+  const int nsplit = eb.x, split_len = eb.y, part_off = eb.z;
+  // Splits that start past this row's causal limit were never computed (lim >= 0 for every row
+  // the planner writes, since c <= L; the clamp keeps the arithmetic branch-free).
+  const int lim = max(L - c + (t - q0), 0);
+  const int n_valid = min(nsplit, lim / split_len + 1);
+  const int64_t base = int64_t(part_off) + (int64_t(t - q0) * n_q_heads + hq) * nsplit;
+  float m = -INFINITY, l = 0.f;
+  float4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < n_valid; s0 += kCombineBatch) {
+    float2 ml[kCombineBatch];
+    float4 v[kCombineBatch];
+#pragma unroll
+    for (int k = 0; k < kCombineBatch; ++k) {
+      const int64_t p = base + min(s0 + k, n_valid - 1);  // clamped: extra splits weigh 0
+      ml[k] = part_ml[p];
+      v[k] = part_acc[(p << ch_log2) + ch];
+    }
+    float mb = m;
+#pragma unroll
+    for (int k = 0; k < kCombineBatch; ++k)
+      if (s0 + k < n_valid) mb = fmaxf(mb, ml[k].x);
+    // No branch on mb == -inf (no split so far has seen a key): every weight below is then 0, and
+    // a branch here would make the compiler sink the acc loads behind the (m, l) wait.
+    const float r = m == -INFINITY ? 0.f : exp2_fast(m - mb);
+    l *= r;
+    acc.x *= r;
+    acc.y *= r;
+    acc.z *= r;
+    acc.w *= r;
+#pragma unroll
+    for (int k = 0; k < kCombineBatch; ++k) {
+      const float w = (s0 + k < n_valid && ml[k].x != -INFINITY) ? exp2_fast(ml[k].x - mb) : 0.f;
+      l = fmaf(w, ml[k].y, l);
+      acc.x = fmaf(w, v[k].x, acc.x);
+      acc.y = fmaf(w, v[k].y, acc.y);
+      acc.z = fmaf(w, v[k].z, acc.z);
+      acc.w = fmaf(w, v[k].w, acc.w);
+    }
+    m = mb;
+  }
+  const float inv = 1.f / fmaxf(l, 1.17549435e-38f);
+  T* op = out + int64_t(t) * o_st + int64_t(hq) * o_sh + ch * 4;
+  const T o0 = from_f32<T>(acc.x * inv), o1 = from_f32<T>(acc.y * inv),
+          o2 = from_f32<T>(acc.z * inv), o3 = from_f32<T>(acc.w * inv);
+  if constexpr (VEC_OUT) {
+    struct alignas(4 * sizeof(T)) Quad {
+      T e[4];
+    };
+    *reinterpret_cast<Quad*>(op) = Quad{{o0, o1, o2, o3}};
+  } else {
+    op[0] = o0;
+    op[1] = o1;
+    op[2] = o2;
+    op[3] = o3;
+  }
+}
+
+// Enqueues the merge of n_rows combine-list rows (n_rows < 0: capacity `cap_rows`, length read
+// on the device).
+template <typename T>
+int launch_combine(hipStream_t s, const int32_t* plan_dev, int32_t n_rows, int32_t cap_rows,
+                   int32_t combine_off, int32_t n_q_heads, int32_t head_dim, const float2* ml,
+                   const float* pacc, void* out, int64_t o_st, int64_t o_sh) {
+  const int rows = n_rows >= 0 ? n_rows : cap_rows;
+  const int ch_log2 = log2_exact(head_dim / 4);
+  const int64_t threads = (int64_t(rows) * n_q_heads) << ch_log2;
+  if (ch_log2 < 0 || head_dim % 4 != 0)
+    return fail(EDGERAG_EUNSUPPORTED, "attention combine: head_dim %d", head_dim);
+  if (threads > INT32_MAX - 256)
+    return fail(EDGERAG_EUNSUPPORTED, "attention combine: %d rows x %d heads too many", rows,
+                n_q_heads);
+  const dim3 block(256), grid(unsigned((threads + 255) / 256));
+  const auto* acc4 = reinterpret_cast<const float4*>(pacc);
+  T* o = static_cast<T*>(out);
+  const bool vec = reinterpret_cast<uintptr_t>(out) % (4 * sizeof(T)) == 0 && o_st % 4 == 0 &&
+                   o_sh % 4 == 0;
+  if (vec)
+    hipLaunchKernelGGL((attn_combine_kernel<T, true>), grid, block, 0, s, plan_dev, n_rows,
+                       combine_off, n_q_heads, ch_log2, ml, acc4, o, o_st, o_sh);
+  else
+    hipLaunchKernelGGL((attn_combine_kernel<T, false>), grid, block, 0, s, plan_dev, n_rows,
+                       combine_off, n_q_heads, ch_log2, ml, acc4, o, o_st, o_sh);
+  return EDGERAG_OK;
 }
 
 int elem_size(int32_t dtype) {
@@ -854,19 +887,17 @@ extern "C" int edgerag_paged_attention(
   const int n_combine = plan_host[H_N_COMBINE];
   if (rc != EDGERAG_OK || n_combine == 0 || !(parts & EDGERAG_ATTN_COMBINE)) return rc;
 
-  const int waves = 4;
-  const dim3 cblock(kWave * waves);
-  const dim3 cgrid(n_combine, (n_q_heads + waves - 1) / waves);
-#define EDGERAG_COMBINE(TYPE)                                                                     \
-  hipLaunchKernelGGL((attn_combine_kernel<TYPE>), cgrid, cblock, 0, a.s, plan_dev,                \
-                     plan_host[H_COMBINE_OFF], n_q_heads, head_dim, a.ml, a.pacc,                 \
-                     static_cast<TYPE*>(out), out_stride_tok, out_stride_head)
   switch (dtype) {
+#define EDGERAG_COMBINE(TYPE)                                                                     \
+  rc = launch_combine<TYPE>(a.s, plan_dev, n_combine, n_combine, plan_host[H_COMBINE_OFF],          \
+                            n_q_heads, head_dim, a.ml, a.pacc, out, out_stride_tok,               \
+                            out_stride_head)
     case EDGERAG_F32: EDGERAG_COMBINE(float); break;
     case EDGERAG_F16: EDGERAG_COMBINE(f16); break;
     case EDGERAG_BF16: EDGERAG_COMBINE(bf16); break;
-  }
 #undef EDGERAG_COMBINE
+  }
+  if (rc != EDGERAG_OK) return rc;
   return check_launch("edgerag_paged_attention(combine)");
 }
 
@@ -969,20 +1000,16 @@ extern "C" int edgerag_paged_attention_fixed(
     }
   }
   if (rc != EDGERAG_OK || max_combine_rows == 0) return rc;
-  const int waves = 4;
-  const dim3 cblock(kWave * waves);
-  const dim3 cgrid(max_combine_rows, (n_q_heads + waves - 1) / waves);
-  // No host plan here: combine_off = -1 makes the kernel read the list's offset from the device
-  // header.
-#define EDGERAG_COMBINE_FIXED(TYPE)                                                               \
-  hipLaunchKernelGGL((attn_combine_kernel<TYPE>), cgrid, cblock, 0, a.s, plan_dev, -1, n_q_heads,  \
-                     head_dim, a.ml, a.pacc, static_cast<TYPE*>(out), out_stride_tok,             \
-                     out_stride_head)
+  // No host plan here: the kernel reads the list's length and offset from the device header.
   switch (dtype) {
+#define EDGERAG_COMBINE_FIXED(TYPE)                                                               \
+  rc = launch_combine<TYPE>(a.s, plan_dev, -1, max_combine_rows, -1, n_q_heads, head_dim, a.ml,  \
+                            a.pacc, out, out_stride_tok, out_stride_head)
     case EDGERAG_F32: EDGERAG_COMBINE_FIXED(float); break;
     case EDGERAG_F16: EDGERAG_COMBINE_FIXED(f16); break;
     case EDGERAG_BF16: EDGERAG_COMBINE_FIXED(bf16); break;
-  }
 #undef EDGERAG_COMBINE_FIXED
+  }
+  if (rc != EDGERAG_OK) return rc;
   return check_launch("edgerag_paged_attention_fixed(combine)");
 }

@@ -33,6 +33,10 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
+#ifndef EDGERAG_TILE_DYN_LDS
+#define EDGERAG_TILE_DYN_LDS 0
+#endif
+
 constexpr int kD = 64;
 constexpr int kKeys = 64;            // keys per LDS tile
 constexpr int kRow = 64;             // halves per LDS row (K: one key; V^T: one dim)
@@ -349,12 +353,6 @@ void attn_prefill_mfma_kernel(
   }
 }
 
-int log2_exact(int v) {
-  int s = 0;
-  while ((1 << s) < v) ++s;
-  return (1 << s) == v ? s : -1;
-}
-
 }  // namespace
 
 bool prefill_tiles_supported(int32_t num_blocks, int32_t block_size) {
@@ -365,7 +363,7 @@ bool prefill_tiles_supported(int32_t num_blocks, int32_t block_size) {
 }
 
 void launch_prefill_tiles_f16_d64(const AttnLaunch& a, int item_base, int count) {
-  hipLaunchKernelGGL(attn_prefill_mfma_kernel, dim3(count), dim3(kThreads), 0, a.s,
+  hipLaunchKernelGGL(attn_prefill_mfma_kernel, dim3(count), dim3(kThreads), EDGERAG_TILE_DYN_LDS, a.s,
                      static_cast<const _Float16*>(a.q), a.q_st, a.q_sh,
                      static_cast<const _Float16*>(a.kp), static_cast<const _Float16*>(a.vp), a.bt,
                      a.bt_stride, a.qsl, a.ctx, a.plan, item_base, a.hq, a.hkv, a.nb,

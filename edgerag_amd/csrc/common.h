@@ -78,4 +78,12 @@ __device__ __forceinline__ float xor_max(float v) {
 
 constexpr int ilog2(int v) { return v <= 1 ? 0 : 1 + ilog2(v / 2); }
 
+// log2 of a power of two, -1 for anything else.
+inline int log2_exact(int v) {
+  if (v <= 0) return -1;
+  int s = 0;
+  while ((1 << s) < v) ++s;
+  return (1 << s) == v ? s : -1;
+}
+
 }  // namespace edgerag
