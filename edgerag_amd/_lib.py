@@ -33,6 +33,7 @@ EDGERAG_EWORKSPACE = 3
 EDGERAG_EUNSUPPORTED = 4
 
 ATTN_TILES, ATTN_ROWS, ATTN_COMBINE, ATTN_ALL = 1, 2, 4, 7
+ATTN_TILES_SHARED = 8  # modifier of ATTN_TILES: one tile workgroup per CU, beside decode rows
 
 DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 

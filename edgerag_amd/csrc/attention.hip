@@ -609,7 +609,8 @@ int run_items(const Launch& a, const int32_t* ph, int parts) {
   if ((parts & EDGERAG_ATTN_TILES) && n_items > n_row) {
     if constexpr (__is_same(T, f16) && D == 64) {
       if (ph[H_TILE_KIND] == 1 && prefill_tiles_supported(a.nb, a.bs)) {
-        launch_prefill_tiles_f16_d64(a, n_row, n_items - n_row);
+        launch_prefill_tiles_f16_d64(a, n_row, n_items - n_row,
+                                     (parts & EDGERAG_ATTN_TILES_SHARED) != 0);
       } else {
         dispatch_rows_qr<T, D>(a, 8, n_row, n_items - n_row, H_N_ITEMS);
       }
@@ -824,7 +825,8 @@ extern "C" int edgerag_paged_attention(
     int64_t out_stride_head, void* workspace, int64_t workspace_bytes, int32_t parts,
     void* stream) {
   clear_error();
-  if (parts <= 0 || (parts & ~EDGERAG_ATTN_ALL) != 0)
+  if (parts <= 0 || (parts & ~(EDGERAG_ATTN_ALL | EDGERAG_ATTN_TILES_SHARED)) != 0 ||
+      (parts & EDGERAG_ATTN_ALL) == 0)
     return fail(EDGERAG_EINVAL, "edgerag_paged_attention: parts mask %d", parts);
   if (plan_host == nullptr || plan_dev == nullptr || plan_words < kHeaderWords ||
       plan_host[H_MAGIC] != kPlanMagic || plan_host[H_VERSION] != kPlanVersion)

@@ -66,7 +66,8 @@ struct AttnLaunch {
 // Virtual query rows (token x head-in-group) per MFMA tile workgroup: 32 per wave.
 constexpr int kMfmaTileRows = EDGERAG_TILE_ROWS;
 constexpr int kMaxTileBlocks = 512;  // block ids one tile item stages in LDS (caps its split)
-void launch_prefill_tiles_f16_d64(const AttnLaunch& a, int item_base, int count);
+// shared: one workgroup per CU (the rest of each CU is left to concurrently running rows).
+void launch_prefill_tiles_f16_d64(const AttnLaunch& a, int item_base, int count, bool shared);
 // Whether a pool of this size can use the MFMA tile kernel (buffer-resource addressing).
 bool prefill_tiles_supported(int32_t num_blocks, int32_t block_size);
 

@@ -33,11 +33,8 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-#ifndef EDGERAG_TILE_DYN_LDS
-#define EDGERAG_TILE_DYN_LDS 0
-#endif
-
 constexpr int kD = 64;
+constexpr unsigned kSharedLdsPad = 48 * 1024;
 constexpr int kKeys = 64;            // keys per LDS tile
 constexpr int kRow = 64;             // halves per LDS row (K: one key; V^T: one dim)
 constexpr float kRescaleLog2 = 8.f;  // lazy rescale: p may grow to 2^8 before the max moves
@@ -48,6 +45,9 @@ constexpr int kKPerThread = kKChunks / kThreads;
 constexpr int kVPairs = (kKeys / 4) * (kD / 8);  // (key quad, dim chunk) pairs of a V tile (128)
 constexpr int kVPerThread = (kVPairs + kThreads - 1) / kThreads;
 static_assert(kKChunks % kThreads == 0, "K staging split");
+constexpr unsigned kStaticLds = 2 * kKeys * kRow * 2 + 2 * kD * kRow * 2 + kMaxTileBlocks * 4;
+static_assert(2 * (kStaticLds + kSharedLdsPad) > 160 * 1024 && kStaticLds + kSharedLdsPad <= 160 * 1024,
+              "shared mode: exactly one tile workgroup per CU");
 
 // Byte offset handed to buffer loads for keys with no valid block: beyond num_records, so the
 // load returns zeros without a branch (the launcher keeps a head's pool slice below it).
@@ -362,8 +362,12 @@ bool prefill_tiles_supported(int32_t num_blocks, int32_t block_size) {
          int64_t(num_blocks) * block_size * kD * 2 < int64_t(kOutOfRange);
 }
 
-void launch_prefill_tiles_f16_d64(const AttnLaunch& a, int item_base, int count) {
-  hipLaunchKernelGGL(attn_prefill_mfma_kernel, dim3(count), dim3(kThreads), EDGERAG_TILE_DYN_LDS, a.s,
+void launch_prefill_tiles_f16_d64(const AttnLaunch& a, int item_base, int count, bool shared) {
+  // Shared mode reserves unused dynamic LDS so that a second workgroup no longer fits a CU's
+  // 160 KiB (the static arrays take ~34 KiB): the tiles then hold one of each SIMD's two register
+  // halves and decode waves keep the other.
+  const unsigned pad = shared ? kSharedLdsPad : 0;
+  hipLaunchKernelGGL(attn_prefill_mfma_kernel, dim3(count), dim3(kThreads), pad, a.s,
                      static_cast<const _Float16*>(a.q), a.q_st, a.q_sh,
                      static_cast<const _Float16*>(a.kp), static_cast<const _Float16*>(a.vp), a.bt,
                      a.bt_stride, a.qsl, a.ctx, a.plan, item_base, a.hq, a.hkv, a.nb,

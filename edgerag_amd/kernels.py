@@ -324,16 +324,18 @@ def paged_attention(
     device = query.device
     n_items, n_row = int(plan.plan_host[2]), int(plan.plan_host[13])
     if overlap and 0 < n_row < n_items:
-        # Prefill tiles (MFMA-bound) on a side stream beside the decode rows (HBM-bound); the
-        # merge of split partials waits for both.
+        # Prefill tiles (MFMA-bound) beside the decode rows (HBM-bound) on a side stream; the
+        # merge of split partials waits for both. The tiles go first, on the current stream (the
+        # side stream starts a few microseconds later, after its event wait), at one workgroup per
+        # CU: launched second, or at two per CU, they found every CU's registers taken by row
+        # waves and ran mostly after the rows.
         main = torch.cuda.current_stream(device)
         side = _side_stream(device)
         side.wait_stream(main)
-        # Rows first: their many short waves spread over every CU, and the tile workgroups
-        # (which fill a CU's register file) take CUs as the row waves retire.
-        call("edgerag_paged_attention", *args, _lib.ATTN_ROWS, stream_ptr(device))
+        call("edgerag_paged_attention", *args, _lib.ATTN_TILES | _lib.ATTN_TILES_SHARED,
+             stream_ptr(device))
         with torch.cuda.stream(side):
-            call("edgerag_paged_attention", *args, _lib.ATTN_TILES, stream_ptr(device))
+            call("edgerag_paged_attention", *args, _lib.ATTN_ROWS, stream_ptr(device))
         main.wait_stream(side)
         call("edgerag_paged_attention", *args, _lib.ATTN_COMBINE, stream_ptr(device))
     else:

@@ -40,6 +40,7 @@ extern "C" {
 #define EDGERAG_ATTN_ROWS 2
 #define EDGERAG_ATTN_COMBINE 4
 #define EDGERAG_ATTN_ALL 7
+#define EDGERAG_ATTN_TILES_SHARED 8 /* modifier of EDGERAG_ATTN_TILES, see below */
 
 /* ---- element types ----------------------------------------------------------------------- */
 #define EDGERAG_F32 0
@@ -145,7 +146,10 @@ int edgerag_attn_plan(const int32_t* query_start_loc, const int32_t* context_len
  *   EDGERAG_ATTN_COMBINE  the merge of split partials (of tiles and of rows alike), which must be
  *                         enqueued after both of the other parts have completed;
  *   EDGERAG_ATTN_ALL      all three in order on `stream`.
- * Tiles and rows write disjoint outputs and partials.
+ * Tiles and rows write disjoint outputs and partials. EDGERAG_ATTN_TILES_SHARED, added to
+ * EDGERAG_ATTN_TILES, runs the MFMA tiles at one workgroup per CU, which leaves the rest of every
+ * CU's registers to decode rows enqueued on another stream; enqueue the tiles first. It changes
+ * nothing in the results.
  */
 int edgerag_paged_attention(const int32_t* plan_host, const int32_t* plan_dev, int64_t plan_words,
                             const void* q, int64_t q_stride_tok, int64_t q_stride_head,

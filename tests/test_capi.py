@@ -57,9 +57,10 @@ def test_validation_errors_come_back_as_messages() -> None:
             1.0, None, 0, 0,        # scale, out, strides
             None, 0, 7, None,       # workspace, bytes, parts (all), stream
         )
-    with pytest.raises(_lib.EdgeragError, match="parts mask"):
-        _lib.call("edgerag_paged_attention", None, None, 0, None, 0, 0, None, None, 1, None, 0,
-                  None, None, 0, 0, 4, 4, 64, 16, 1, 1.0, None, 0, 0, None, 0, 8, None)
+    for parts in (8, 16, 0):  # the shared modifier alone, an unknown bit, nothing
+        with pytest.raises(_lib.EdgeragError, match="parts mask"):
+            _lib.call("edgerag_paged_attention", None, None, 0, None, 0, 0, None, None, 1, None,
+                      0, None, None, 0, 0, 4, 4, 64, 16, 1, 1.0, None, 0, 0, None, 0, parts, None)
     with pytest.raises(_lib.EdgeragError, match="capacities"):
         _lib.call("edgerag_paged_attention_fixed", 16, -1, 0, 1, 0, 16, 0, 0, 16, 16, 1, 16, 0,
                   16, 16, 4, 4, 64, 16, 1, 1.0, 16, 0, 0, None, 0, None)
