@@ -40,6 +40,11 @@ class LinearBase(nn.Module):
     @abstractmethod
     def weight_bytes(self) -> int: ...
 
+    def swiglu(self, x: torch.Tensor) -> torch.Tensor:
+        """``silu(gate(x)) * up(x)`` for a layer whose rows are ``[gate; up]``:
+        ``(T, K) -> (T, N / 2)``."""
+        return kernels.silu_mul(self(x).reshape(-1, self.out_features), self.out_features // 2)
+
 
 class FP16Linear(LinearBase):
     """Dense layer (used for the fp16 lm_head and as the unquantised baseline)."""
@@ -163,6 +168,14 @@ class QuantLinear(LinearBase):
         return kernels.quant_linear(
             x, self.packed, self.scales, self.bias, self.in_features, self.out_features,
             self.config.bits, self.config.group_size, out=out,
+        )
+
+    def swiglu(self, x: torch.Tensor) -> torch.Tensor:
+        """``silu(gate(x)) * up(x)`` for a ``concat([gate, up])`` layer: ``(T, K) -> (T, N / 2)``,
+        one launch for decode batches."""
+        return kernels.quant_linear_swiglu(
+            x, self.packed, self.scales, self.bias, self.in_features, self.out_features,
+            self.config.bits, self.config.group_size,
         )
 
     def weight_bytes(self) -> int:

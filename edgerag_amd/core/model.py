@@ -161,8 +161,8 @@ class EdgeRagDecoder(nn.Module):
         """Run every layer over the packed batch; return the final-norm hidden of ``logit_rows``.
 
         Per layer: fused q/k/v linear -> RoPE + KV append (one launch) -> ragged attention ->
-        o_proj -> residual add + RMSNorm (one launch) -> fused gate/up linear -> SiLU * up ->
-        down_proj -> residual add + the next RMSNorm (one launch)."""
+        o_proj -> residual add + RMSNorm (one launch) -> fused gate/up linear with SiLU * up (one
+        launch for decode batches) -> down_proj -> residual add + the next RMSNorm (one launch)."""
         spec = self.spec
         T = step.token_ids.shape[0]
         d, eps = spec.head_dim, spec.rms_norm_eps
@@ -184,7 +184,7 @@ class EdgeRagDecoder(nn.Module):
             o = layer.o_proj(attn_out.view(T, layer.q_out))
             x = kernels.rmsnorm(hidden, layer.post_attention_layernorm.weight, eps, delta=o,
                                 h_out=hidden)
-            down = layer.down_proj(kernels.silu_mul(layer.gate_up(x), layer.intermediate))
+            down = layer.down_proj(layer.gate_up.swiglu(x))
             next_norm = (self.layers[idx + 1].input_layernorm.weight if idx + 1 < n_layers
                          else self.norm.weight)
             x = kernels.rmsnorm(hidden, next_norm, eps, delta=down, h_out=hidden)

@@ -76,6 +76,12 @@ __device__ __forceinline__ float xor_max(float v) {
   return v;
 }
 
+// SwiGLU's gate activation rounded as the reference's fp16 F.silu: fp16(g / (1 + exp(-g))), with
+// the quotient and exp in fp32 (layers.py:341).
+__device__ __forceinline__ float silu_rounded_f16(float g) {
+  return __half2float(__float2half_rn(g / (1.f + expf(-g))));
+}
+
 constexpr int ilog2(int v) { return v <= 1 ? 0 : 1 + ilog2(v / 2); }
 
 // log2 of a power of two, -1 for anything else.

@@ -347,3 +347,40 @@ extern "C" int edgerag_quant_linear(const void* x, int32_t x_dtype, int64_t x_st
   }
   return fail(EDGERAG_EUNSUPPORTED, "edgerag_quant_linear: activation dtype %d", x_dtype);
 }
+
+extern "C" int edgerag_quant_linear_swiglu_supported(int32_t x_dtype, int32_t m, int32_t k,
+                                                     int32_t n, int32_t bits,
+                                                     int32_t group_size) {
+  // Alignment is the caller's part of the contract; a 16-byte aligned stand-in checks the rest.
+  const void* aligned = reinterpret_cast<const void*>(uintptr_t(256));
+  return x_dtype == EDGERAG_F16 && n > 0 && k > 0 && group_size == k &&
+                 qlinear_swiglu_supported(m, k, n, bits, group_size, aligned, k, aligned)
+             ? 1
+             : 0;
+}
+
+extern "C" int edgerag_quant_linear_swiglu(const void* x, int32_t x_dtype, int64_t x_stride,
+                                           int32_t m, int32_t k, const uint8_t* packed,
+                                           const void* scales_f16, const void* bias_f16, int32_t n,
+                                           int32_t bits, int32_t group_size, void* y,
+                                           int64_t y_stride, void* stream) {
+  clear_error();
+  if (int rc = check_quant_shape("edgerag_quant_linear_swiglu", n, k, bits, group_size)) return rc;
+  if (m < 0) return fail(EDGERAG_EINVAL, "edgerag_quant_linear_swiglu: M < 0");
+  if (m == 0) return EDGERAG_OK;
+  if (x == nullptr || packed == nullptr || scales_f16 == nullptr || y == nullptr)
+    return fail(EDGERAG_EINVAL, "edgerag_quant_linear_swiglu: NULL pointer");
+  if (x_stride < k || y_stride < n / 2)
+    return fail(EDGERAG_EINVAL, "edgerag_quant_linear_swiglu: row strides (%lld, %lld) below K/I",
+                (long long)x_stride, (long long)y_stride);
+  if (x_dtype != EDGERAG_F16 ||
+      !qlinear_swiglu_supported(m, k, n, bits, group_size, x, x_stride, packed))
+    return fail(EDGERAG_EUNSUPPORTED,
+                "edgerag_quant_linear_swiglu: shape not covered (dtype %d, M %d, K %d, N %d, "
+                "bits %d, group %d); use edgerag_quant_linear + edgerag_silu_mul",
+                x_dtype, m, k, n, bits, group_size);
+  launch_qlinear_swiglu(static_cast<const f16*>(x), x_stride, m, k, packed,
+                        static_cast<const f16*>(scales_f16), static_cast<const f16*>(bias_f16), n,
+                        static_cast<f16*>(y), y_stride, static_cast<hipStream_t>(stream));
+  return check_launch("edgerag_quant_linear_swiglu");
+}

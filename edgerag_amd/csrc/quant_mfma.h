@@ -18,4 +18,14 @@ void launch_qlinear_mfma(const f16* x, int64_t xs, int32_t m, int32_t k, const u
                          const f16* scales, const f16* bias, int32_t n, int32_t bits, int32_t g,
                          f16* y, int64_t ys, hipStream_t s);
 
+// SwiGLU form for decode batches: W = [gate; up] (N = 2 I rows, INT8 per-channel), y[M, I] =
+// fp16(fp16(silu(g)) * u) with g, u the fp16 outputs launch_qlinear_mfma would write for the same
+// shape. Covered: M <= 64, K a multiple of 64 (at least 256), N at least 8192 (two 16-row tiles
+// per workgroup).
+bool qlinear_swiglu_supported(int32_t m, int32_t k, int32_t n, int32_t bits, int32_t g,
+                              const void* x, int64_t x_stride, const void* packed);
+void launch_qlinear_swiglu(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
+                           const f16* scales, const f16* bias, int32_t n, f16* y, int64_t ys,
+                           hipStream_t s);
+
 }  // namespace edgerag

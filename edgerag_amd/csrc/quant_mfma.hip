@@ -311,7 +311,12 @@ __global__ __launch_bounds__(KWMAX * kWave) void qlinear_skinny_kernel(
 // blocks pair different k-slices and are never read.
 // The dequantised weight is the exact integer code (no scale): the row's scale multiplies the fp32
 // sum once, scale * sum(code * x), instead of rounding every code * scale to fp16 first.
-template <int F, int NT, int MT, int KW, int U, bool EXACT>
+//
+// SW (SwiGLU, NT == 2): the weight is [gate; up] (N = 2 I rows) and row tile 1 is the up twin of
+// tile 0 (rows I + n0 + [0, R)), so every workgroup holds gate and up of the same R columns and
+// writes act[t][j] = fp16(fp16(silu(g)) * u) to y (T x I) instead of the projection. g and u are
+// the fp16 outputs the plain launch would write: same tiles, waves, batches and summation order.
+template <int F, int NT, int MT, int KW, int U, bool EXACT, bool SW>
 __global__ __launch_bounds__(KW * kWave)
 __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlinear_stream_kernel(
     const f16* __restrict__ x, int64_t xs, int32_t m, int32_t k,
@@ -321,33 +326,41 @@ __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlin
   constexpr int CB = 64 * F;               // bytes (= k) of one chunk step of a row
   constexpr int OUTS = NT * MT * R * R;    // outputs (token, row) of a workgroup
   static_assert((KW * kWave) % (NT * R) == 0, "a thread's outputs share one weight row");
+  static_assert(!SW || (NT == 2 && kWave % (NT * R) == 0),
+                "SwiGLU pairs tile 0 with tile 1 inside one wave");
   __shared__ float red[KW * NT * MT * 4 * kWave];
   const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63;
   const int li = lane & 15, lg = lane >> 4;
   const int f = li / R, r = li % R;
-  const int n0 = blockIdx.x * (NT * R);
+  const int half = n >> 1;  // SW: gate rows [0, half), up rows [half, n)
+  const int n0 = blockIdx.x * (SW ? R : NT * R);
   const int nc = k / CB;  // chunk steps: >= U, and a multiple of KW * U when EXACT
   const int per = (nc + KW - 1) / KW;
   const int c0 = min(nc, wave * per), c1 = min(nc, c0 + per);
+  // Weight row of lane row rr in tile tn. Rows past N (past I in a SW half) re-read the last
+  // row: they only feed D rows that are never read.
+  auto wrow = [&](int tn, int rr) {
+    return SW ? min(n0 + rr, half - 1) + tn * half : min(n0 + tn * R + rr, n - 1);
+  };
 
-  // A lane of n-tile tn: weight row n0 + tn R + r; B lane of m-tile t: activation row t R + r.
-  // Rows past N or M re-read the last row: they only feed D rows / columns that are never read.
+  // A lane of n-tile tn: weight row wrow(tn, r); B lane of m-tile t: activation row t R + r.
+  // Rows past M re-read the last row: they only feed D columns that are never read.
   const uint8_t* wp[NT];
 #pragma unroll
-  for (int tn = 0; tn < NT; ++tn)
-    wp[tn] = packed + int64_t(min(n0 + tn * R + r, n - 1)) * k + f * 64 + 16 * lg;
+  for (int tn = 0; tn < NT; ++tn) wp[tn] = packed + int64_t(wrow(tn, r)) * k + f * 64 + 16 * lg;
   const f16* xp[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t) xp[t] = x + int64_t(min(t * R + r, m - 1)) * xs + f * 64 + 16 * lg;
 
-  // Output e (e = thread, thread + KW 64, ...) is row n0 + e % (NT R) of token e / (NT R): all
-  // of a thread's outputs share one row, whose scale and bias are loaded now and first waited for
-  // after the first batch is computed.
+  // Output e (e = thread, thread + KW 64, ...) is lane row e % R of tile e % (NT R) / R, token
+  // e / (NT R): all of a thread's outputs share one row, whose scale and bias are loaded now and
+  // first waited for after the first batch is computed.
   // Whole aligned 32-bit words are loaded (nothing is computed on them before the pins), and the
   // bias word unconditionally -- from the scales when there is no bias -- so that no branch sits
   // between these loads and the batch loads (either would cost the batch its progressive waits).
-  const int e_row = min(n0 + int(threadIdx.x) % (NT * R), n - 1);
+  const int e_in = int(threadIdx.x) % (NT * R);
+  const int e_row = wrow(e_in / R, e_in % R);
   const f16* b_src = bias != nullptr ? bias : scales;
   const int s_mis = int(reinterpret_cast<uintptr_t>(scales) >> 1) & 1;  // base at an odd half
   const int b_mis = int(reinterpret_cast<uintptr_t>(b_src) >> 1) & 1;
@@ -425,12 +438,8 @@ __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlin
   const float scale = float(__builtin_bit_cast(_Float16, uint16_t(s_bits >> sh_s)));
   const float bv =
       bias != nullptr ? float(__builtin_bit_cast(_Float16, uint16_t(b_bits >> sh_b))) : 0.f;
-  for (int e = threadIdx.x; e < OUTS; e += KW * kWave) {
-    const int tok = e / (NT * R), row_in = e % (NT * R);
-    const int tn = row_in / R, rr = row_in % R;
+  auto out_sum = [&](int tok, int tn, int rr) {
     const int t = tok / R, jj = tok % R;
-    const int nrow = n0 + row_in;
-    if (tok >= m || nrow >= n) continue;
     float sum = 0.f;
 #pragma unroll
     for (int fs = 0; fs < F; ++fs) {
@@ -439,7 +448,27 @@ __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlin
       for (int wv = 0; wv < KW; ++wv)
         sum += red[(((wv * NT + tn) * MT + t) * 4 + i) * kWave + l];
     }
-    y[int64_t(tok) * ys + nrow] = __float2half_rn(scale * sum + bv);
+    return __float2half_rn(__builtin_fmaf(scale, sum, bv));
+  };
+  if constexpr (!SW) {
+    for (int e = threadIdx.x; e < OUTS; e += KW * kWave) {
+      const int tok = e / (NT * R), row_in = e % (NT * R);
+      const int nrow = n0 + row_in;
+      if (tok >= m || nrow >= n) continue;
+      y[int64_t(tok) * ys + nrow] = out_sum(tok, row_in / R, row_in % R);
+    }
+  } else {
+    // The up output of gate lane l sits in lane l + R of the same wave (same token, tile 1). OUTS
+    // and the stride are multiples of 64, so whole waves run each iteration and the shuffle sees
+    // every lane.
+    for (int e = threadIdx.x; e < OUTS; e += KW * kWave) {
+      const int tok = e / (NT * R), row_in = e % (NT * R);
+      const int tn = row_in / R, rr = row_in % R;
+      const float v = __half2float(out_sum(tok, tn, rr));
+      const float u = __shfl_down(v, R, kWave);
+      if (tn == 0 && tok < m && n0 + rr < half)
+        y[int64_t(tok) * ys + n0 + rr] = __float2half_rn(silu_rounded_f16(v) * u);
+    }
   }
 }
 
@@ -770,21 +799,23 @@ void launch_gemm(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* 
 // steps per batch U from K alone, so that a row's summation order, and so its bits, do not depend
 // on M or on the other rows of the launch. Returns false when the shape does not fit (the caller
 // then uses the skinny kernel).
-template <int F, int NT, int MT, int KW, int U>
+template <int F, int NT, int MT, int KW, int U, bool SW>
 void launch_stream(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
                    const f16* scales, const f16* bias, int32_t n, f16* y, int64_t ys,
                    hipStream_t s) {
   constexpr int rows = NT * 16 / F;
-  const unsigned blocks = unsigned((n + rows - 1) / rows);
+  // SW: one workgroup per 16 / F columns of the activation (a gate tile and its up twin).
+  const unsigned blocks = SW ? unsigned((n / 2 + 16 / F - 1) / (16 / F))
+                             : unsigned((n + rows - 1) / rows);
   if ((k / (64 * F)) % (KW * U) == 0)
-    hipLaunchKernelGGL((qlinear_stream_kernel<F, NT, MT, KW, U, true>), dim3(blocks),
+    hipLaunchKernelGGL((qlinear_stream_kernel<F, NT, MT, KW, U, true, SW>), dim3(blocks),
                        dim3(KW * kWave), 0, s, x, xs, m, k, packed, scales, bias, n, y, ys);
   else
-    hipLaunchKernelGGL((qlinear_stream_kernel<F, NT, MT, KW, U, false>), dim3(blocks),
+    hipLaunchKernelGGL((qlinear_stream_kernel<F, NT, MT, KW, U, false, SW>), dim3(blocks),
                        dim3(KW * kWave), 0, s, x, xs, m, k, packed, scales, bias, n, y, ys);
 }
 
-template <int F, int NT, int MT>
+template <int F, int NT, int MT, bool SW = false>
 void launch_stream_k(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
                      const f16* scales, const f16* bias, int32_t n, f16* y, int64_t ys,
                      hipStream_t s) {
@@ -805,11 +836,11 @@ void launch_stream_k(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8
   do {                                                                                         \
     if constexpr (MT == 1) {                                                                   \
       if (u8) {                                                                                \
-        launch_stream<F, NT, MT, KW, 8>(x, xs, m, k, packed, scales, bias, n, y, ys, s);       \
+        launch_stream<F, NT, MT, KW, 8, SW>(x, xs, m, k, packed, scales, bias, n, y, ys, s);   \
         break;                                                                                 \
       }                                                                                        \
     }                                                                                          \
-    launch_stream<F, NT, MT, KW, 4>(x, xs, m, k, packed, scales, bias, n, y, ys, s);           \
+    launch_stream<F, NT, MT, KW, 4, SW>(x, xs, m, k, packed, scales, bias, n, y, ys, s);       \
   } while (0)
   if constexpr (kw_min == 4) {
     if (kw == 4) {
@@ -856,6 +887,25 @@ bool dispatch_stream(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8
   else
     launch_stream_k<1, 1, 1>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
   return true;
+}
+
+// The streaming shapes with two row tiles of one k-slice: the only ones the SwiGLU form covers.
+// dispatch_stream picks exactly these for the same (M, K, N), so the fused launch computes the
+// same gate and up bits as the plain one.
+bool stream_swiglu_shape(int32_t m, int32_t k, int32_t n) {
+  return m >= 1 && m <= 64 && m <= EDGERAG_STREAM_MAX_M && n % 2 == 0 && k % 64 == 0 &&
+         k / 64 >= 4 && (int64_t(n) + 15) / 16 >= EDGERAG_STREAM_NT2_TILES;
+}
+
+void dispatch_stream_swiglu(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
+                            const f16* scales, const f16* bias, int32_t n, f16* y, int64_t ys,
+                            hipStream_t s) {
+  if (m <= 16)
+    launch_stream_k<1, 2, 1, true>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
+  else if (m <= 32)
+    launch_stream_k<1, 2, 2, true>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
+  else
+    launch_stream_k<1, 2, 4, true>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
 }
 
 template <int BITS>
@@ -908,6 +958,18 @@ bool qlinear_mfma_supported(int32_t k, int32_t bits, int32_t g, const void* x, i
   const int kb = bits == 8 ? 64 : 128;
   return (bits == 8 || bits == 4) && k % kb == 0 && g % 32 == 0 && aligned16(x) &&
          aligned16(packed) && (x_stride * 2) % 16 == 0;
+}
+
+bool qlinear_swiglu_supported(int32_t m, int32_t k, int32_t n, int32_t bits, int32_t g,
+                              const void* x, int64_t x_stride, const void* packed) {
+  return bits == 8 && g == k && qlinear_mfma_supported(k, bits, g, x, x_stride, packed) &&
+         stream_swiglu_shape(m, k, n);
+}
+
+void launch_qlinear_swiglu(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
+                           const f16* scales, const f16* bias, int32_t n, f16* y, int64_t ys,
+                           hipStream_t s) {
+  dispatch_stream_swiglu(x, xs, m, k, packed, scales, bias, n, y, ys, s);
 }
 
 void launch_qlinear_mfma(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,

@@ -526,6 +526,57 @@ def silu_mul(gate_up: torch.Tensor, intermediate: int,
     return out
 
 
+def quant_swiglu_fused(m: int, k: int, n: int, bits: int, group_size: int,
+                       dtype: torch.dtype = torch.float16) -> bool:
+    """Whether ``quant_linear_swiglu`` runs as one launch for this shape (16-byte aligned rows)."""
+    return bool(_lib.load().edgerag_quant_linear_swiglu_supported(
+        dtype_code(dtype) if dtype in (torch.float16, torch.float32) else -1, m, k, n, bits,
+        group_size))
+
+
+def quant_linear_swiglu(
+    x: torch.Tensor,
+    packed: torch.Tensor,
+    scales: torch.Tensor,
+    bias: torch.Tensor | None,
+    in_features: int,
+    out_features: int,
+    bits: int,
+    group_size: int,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """SwiGLU of the fused ``[gate; up]`` quant linear: ``x (T, K) -> (T, out_features / 2)``.
+
+    One launch where the native library covers the shape (decode batches of INT8 per-channel
+    weights); otherwise the projection and ``silu_mul`` as two launches. Both give the same bits.
+    """
+    require_device(x, packed, scales, bias, out)
+    inter = out_features // 2
+    if out_features % 2:
+        raise ValueError("a fused [gate; up] weight has an even number of rows")
+    x2 = x.reshape(-1, in_features)
+    if x2.stride(1) != 1 or (x2.stride(0) * x2.element_size()) % 16 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    m = x2.shape[0]
+    if m == 0 or x2.dtype != torch.float16 or packed.data_ptr() % 16 or not quant_swiglu_fused(
+            m, in_features, out_features, bits, group_size):
+        gu = quant_linear(x2, packed, scales, bias, in_features, out_features, bits, group_size)
+        return silu_mul(gu, inter, out=out)
+    y = out if out is not None else torch.empty((m, inter), dtype=x.dtype, device=x.device)
+    if y.shape != (m, inter) or y.stride(1) != 1:
+        raise ValueError(f"out must be ({m}, {inter}) with contiguous rows")
+    if scales.dtype != torch.float16:
+        scales = scales.to(torch.float16)
+    if bias is not None and bias.dtype != torch.float16:
+        bias = bias.to(torch.float16)
+    call(
+        "edgerag_quant_linear_swiglu", x2.data_ptr(), dtype_code(x2.dtype), x2.stride(0), m,
+        in_features, packed.data_ptr(), scales.contiguous().data_ptr(), ptr(bias), out_features,
+        bits, group_size, y.data_ptr(), y.stride(0), stream_ptr(x.device),
+    )
+    return y
+
+
 # --- quantisation -----------------------------------------------------------------------------
 
 

@@ -231,6 +231,28 @@ int edgerag_quant_linear(const void* x, int32_t x_dtype, int64_t x_stride, int32
                          int32_t n, int32_t bits, int32_t group_size, void* y, int64_t y_stride,
                          void* stream);
 
+/*
+ * SwiGLU through one launch: W = [gate; up] is the packed INT8 per-channel weight of N = 2 I rows
+ * (gate rows 0..I-1, up rows I..N-1), and
+ *   y[t][j] = fp16(fp16(silu(g)) * u),  g = (x . W^T + bias)[t][j],  u = (...)[t][I + j]
+ * with g and u exactly the fp16 values edgerag_quant_linear would write for the same arguments.
+ * y: [M, I] fp16, row stride y_stride. Covered: fp16 x, bits 8 with group_size == K, 1 <= M <= 64,
+ * K a multiple of 64 (at least 256), N even and at least 8192, 16-byte aligned x rows and W.
+ * Anything else returns EDGERAG_EUNSUPPORTED (edgerag_quant_linear_swiglu_supported says so
+ * beforehand); the caller then runs edgerag_quant_linear and edgerag_silu_mul.
+ *
+ * Replaces `down_proj(F.silu(gate_proj(x)) * up_proj(x))`'s first half (edgerag/core/layers.py:341)
+ * for decode batches: the [M, N] projection never goes through HBM, and one launch goes away.
+ */
+int edgerag_quant_linear_swiglu(const void* x, int32_t x_dtype, int64_t x_stride, int32_t m,
+                                int32_t k, const uint8_t* packed, const void* scales_f16,
+                                const void* bias_f16, int32_t n, int32_t bits, int32_t group_size,
+                                void* y, int64_t y_stride, void* stream);
+/* 1 when edgerag_quant_linear_swiglu covers (x_dtype, M, K, N, bits, group_size) for 16-byte
+ * aligned x rows and W, else 0. */
+int edgerag_quant_linear_swiglu_supported(int32_t x_dtype, int32_t m, int32_t k, int32_t n,
+                                          int32_t bits, int32_t group_size);
+
 /* ==== Fused elementwise ops of a decoder layer ============================================ */
 
 /*

@@ -37,6 +37,23 @@ def test_library_exports_every_declared_symbol() -> None:
     assert _lib.version().startswith("edgerag_amd")
 
 
+def test_swiglu_support_query() -> None:
+    """The fused SwiGLU linear covers decode batches of wide INT8 per-channel [gate; up]
+    weights; the query answers without touching a GPU."""
+    q = _lib.load().edgerag_quant_linear_swiglu_supported
+    F16, F32 = 1, 0
+    assert q(F16, 8, 2048, 16384, 8, 2048) == 1  # config 5's gate/up, a decode batch
+    assert q(F16, 64, 2048, 16384, 8, 2048) == 1
+    assert q(F16, 65, 2048, 16384, 8, 2048) == 0  # prefill-sized M
+    assert q(F16, 0, 2048, 16384, 8, 2048) == 0
+    assert q(F16, 8, 2048, 4096, 8, 2048) == 0  # one 16-row tile per workgroup
+    assert q(F16, 8, 2048, 16383, 8, 2048) == 0  # odd N: no [gate; up] split
+    assert q(F16, 8, 2048, 16384, 4, 128) == 0  # INT4
+    assert q(F16, 8, 2048, 16384, 8, 128) == 0  # grouped INT8
+    assert q(F32, 8, 2048, 16384, 8, 2048) == 0
+    assert q(F16, 8, 200, 16384, 8, 200) == 0  # K not a multiple of 64
+
+
 def test_validation_errors_come_back_as_messages() -> None:
     with pytest.raises(_lib.EdgeragError, match="only 4- and 8-bit"):
         _lib.call("edgerag_quant_linear", None, 1, 16, 1, 16, None, None, None, 4, 3, 16, None,

@@ -163,6 +163,55 @@ def test_quant_linear_mfma_edges(device, bits, k, g, m) -> None:
         torch.testing.assert_close(y.float().cpu(), expected, **LINEAR_TOL)
 
 
+@pytest.mark.parametrize("k,n", [(2048, 16384), (640, 8200), (1152, 8192)])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_quant_linear_swiglu_fused(device, k, n, with_bias) -> None:
+    """SwiGLU in the streaming GEMV's epilogue (decode batches, [gate; up] INT8 per-channel):
+    bit-identical to the projection followed by silu_mul for M = 1..64 (one launch against two),
+    and within the linear tolerance of silu(gate) * up from the oracle's dequant-then-matmul.
+    K a whole number of per-wave batches (2048) and not (640, 1152); I = N / 2 not a multiple of
+    the 16-row tile (4100); strided activations."""
+    w = _weight(n, k, n + 3 * k)
+    cfg = oq.QuantConfig(k, 8)
+    packed, scales = oq.quantize_for_layer(w, cfg)
+    bias = (torch.randn(n, generator=seeded(n - k)) * 0.1).half() if with_bias else None
+    inter = n // 2
+    pd, sd = packed.to(device), scales.to(device)
+    bd = bias.to(device) if bias is not None else None
+    for m in (1, 3, 8, 16, 17, 32, 40, 64):
+        assert kernels.quant_swiglu_fused(m, k, n, 8, k)
+        xfull = torch.randn(m, k + 64, generator=seeded(m * 29 + k)).half()
+        xd = xfull.to(device)[:, :k]
+        fused = kernels.quant_linear_swiglu(xd, pd, sd, bd, k, n, 8, k)
+        gu = kernels.quant_linear(xd, pd, sd, bd, k, n, 8, k)
+        plain = kernels.silu_mul(gu, inter)
+        assert fused.shape == (m, inter)
+        assert torch.equal(fused, plain), f"M={m}: fused SwiGLU differs from projection + silu_mul"
+        ref_gu = oq.quant_linear_reference(xfull[:, :k], packed, scales, bias, k, cfg)
+        ref = torch.nn.functional.silu(ref_gu[:, :inter]) * ref_gu[:, inter:]
+        torch.testing.assert_close(fused.float().cpu(), ref, **LINEAR_TOL)
+
+
+def test_quant_linear_swiglu_falls_back_outside_its_shapes(device) -> None:
+    """Shapes the fused launch does not cover (M > 64, N below two tiles per workgroup, INT4)
+    run as projection + silu_mul through the same entry, and the C entry point says why."""
+    k, n = 1024, 2048
+    w = _weight(n, k, 77)
+    for bits, g, m in ((8, k, 4), (8, k, 80), (4, 128, 4)):
+        cfg = oq.QuantConfig(g, bits)
+        packed, scales = oq.quantize_for_layer(w, cfg)
+        assert not kernels.quant_swiglu_fused(m, k, n, bits, g)
+        x = torch.randn(m, k, generator=seeded(m + bits)).half().to(device)
+        pd, sd = packed.to(device), scales.to(device)
+        y = kernels.quant_linear_swiglu(x, pd, sd, None, k, n, bits, g)
+        gu = kernels.quant_linear(x, pd, sd, None, k, n, bits, g)
+        assert torch.equal(y, kernels.silu_mul(gu, n // 2))
+    with pytest.raises(kernels._lib.EdgeragError, match="not covered"):
+        kernels.call("edgerag_quant_linear_swiglu", x.data_ptr(), 1, k, 4, k, pd.data_ptr(),
+                     sd.data_ptr(), None, n, 4, 128, y.data_ptr(), n // 2,
+                     kernels.stream_ptr(x.device))
+
+
 @pytest.mark.parametrize("k", [640, 1152, 2048, 8192])
 @pytest.mark.parametrize("n", [37, 2048, 4104, 8200])
 def test_quant_linear_int8_per_channel_streaming(device, k, n) -> None:
