@@ -45,6 +45,15 @@ class LinearBase(nn.Module):
         ``(T, K) -> (T, N / 2)``."""
         return kernels.silu_mul(self(x).reshape(-1, self.out_features), self.out_features // 2)
 
+    def rope_append(self, x: torch.Tensor, positions, cos, sin, n_q_heads: int, n_kv_heads: int,
+                    head_dim: int, slots, key_pool, value_pool, q_out=None,
+                    rows=None) -> torch.Tensor:
+        """For a fused ``[q | k | v]`` layer: RoPE on q and k, k and v appended to the pools at
+        ``slots``; returns q ``(T, n_q_heads, head_dim)``. ``rows``: ``kernels.rope_rows``."""
+        qkv = self(x).reshape(-1, self.out_features)
+        return kernels.rope_append(qkv, positions, cos, sin, n_q_heads, n_kv_heads, head_dim,
+                                   slots, key_pool, value_pool, q_out=q_out)
+
 
 class FP16Linear(LinearBase):
     """Dense layer (used for the fp16 lm_head and as the unquantised baseline)."""
@@ -168,6 +177,16 @@ class QuantLinear(LinearBase):
         return kernels.quant_linear(
             x, self.packed, self.scales, self.bias, self.in_features, self.out_features,
             self.config.bits, self.config.group_size, out=out,
+        )
+
+    def rope_append(self, x: torch.Tensor, positions, cos, sin, n_q_heads: int, n_kv_heads: int,
+                    head_dim: int, slots, key_pool, value_pool, q_out=None,
+                    rows=None) -> torch.Tensor:
+        """``LinearBase.rope_append`` in one launch for decode batches (``rows`` given)."""
+        return kernels.quant_linear_rope_append(
+            x, self.packed, self.scales, self.bias, self.in_features, self.config.bits,
+            self.config.group_size, positions, cos, sin, n_q_heads, n_kv_heads, head_dim, slots,
+            key_pool, value_pool, q_out=q_out, rows=rows,
         )
 
     def swiglu(self, x: torch.Tensor) -> torch.Tensor:

@@ -160,7 +160,8 @@ class EdgeRagDecoder(nn.Module):
                        value_pool: list[torch.Tensor]) -> torch.Tensor:
         """Run every layer over the packed batch; return the final-norm hidden of ``logit_rows``.
 
-        Per layer: fused q/k/v linear -> RoPE + KV append (one launch) -> ragged attention ->
+        Per layer: fused q/k/v linear with RoPE + KV append (one launch for decode batches, two
+        otherwise) -> ragged attention ->
         o_proj -> residual add + RMSNorm (one launch) -> fused gate/up linear with SiLU * up (one
         launch for decode batches) -> down_proj -> residual add + the next RMSNorm (one launch)."""
         spec = self.spec
@@ -171,11 +172,16 @@ class EdgeRagDecoder(nn.Module):
         q = torch.empty((T, spec.n_q_heads, d), device=self.device, dtype=self.dtype)
         attn_out = torch.empty_like(q)
         n_layers = len(self.layers)
+        qkv0 = self.layers[0].qkv
+        rows = None
+        if isinstance(qkv0, QuantLinear) and kernels.quant_rope_fused(
+                T, qkv0.in_features, qkv0.config.bits, qkv0.config.group_size, spec.n_q_heads,
+                spec.n_kv_heads, d, self.dtype):
+            rows = kernels.rope_rows(step.positions, self.rotary.cos, self.rotary.sin)
         for idx, layer in enumerate(self.layers):
-            qkv = layer.qkv(x)
-            kernels.rope_append(qkv, step.positions, self.rotary.cos, self.rotary.sin,
-                                spec.n_q_heads, spec.n_kv_heads, d, step.slots, key_pool[idx],
-                                value_pool[idx], q_out=q)
+            layer.qkv.rope_append(x, step.positions, self.rotary.cos, self.rotary.sin,
+                                  spec.n_q_heads, spec.n_kv_heads, d, step.slots, key_pool[idx],
+                                  value_pool[idx], q_out=q, rows=rows)
             if isinstance(step.plan, kernels.FixedAttention):
                 step.plan.launch(q, key_pool[idx], value_pool[idx], self.scaling, attn_out)
             else:

@@ -384,3 +384,69 @@ extern "C" int edgerag_quant_linear_swiglu(const void* x, int32_t x_dtype, int64
                         static_cast<f16*>(y), y_stride, static_cast<hipStream_t>(stream));
   return check_launch("edgerag_quant_linear_swiglu");
 }
+
+extern "C" int edgerag_quant_linear_rope_append_supported(int32_t x_dtype, int32_t m, int32_t k,
+                                                         int32_t bits, int32_t group_size,
+                                                         int32_t n_q_heads, int32_t n_kv_heads,
+                                                         int32_t head_dim) {
+  if (x_dtype != EDGERAG_F16 || n_q_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0 || k <= 0 ||
+      group_size != k)
+    return 0;
+  const int64_t heads = int64_t(n_q_heads) + 2 * int64_t(n_kv_heads);
+  if (heads * head_dim > INT32_MAX) return 0;
+  const void* aligned = reinterpret_cast<const void*>(uintptr_t(256));
+  return qlinear_rope_supported(m, k, int32_t(heads * head_dim), bits, group_size, int32_t(heads),
+                                head_dim, aligned, k, aligned)
+             ? 1
+             : 0;
+}
+
+extern "C" int edgerag_quant_linear_rope_append(
+    const void* x, int32_t x_dtype, int64_t x_stride, int32_t m, int32_t k, const uint8_t* packed,
+    const void* scales_f16, const void* bias_f16, int32_t bits, int32_t group_size,
+    const void* cos_tok, const void* sin_tok, int32_t n_q_heads, int32_t n_kv_heads,
+    int32_t head_dim, void* q_out, int64_t q_stride_tok, const int32_t* slots, void* key_pool,
+    void* value_pool, int32_t num_blocks, int32_t block_size, void* stream) {
+  clear_error();
+  if (m < 0 || n_q_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0 || head_dim % 2 ||
+      num_blocks <= 0 || block_size <= 0)
+    return fail(EDGERAG_EINVAL, "edgerag_quant_linear_rope_append: bad shape");
+  const int64_t heads = int64_t(n_q_heads) + 2 * int64_t(n_kv_heads);
+  if (heads * head_dim > INT32_MAX)
+    return fail(EDGERAG_EINVAL, "edgerag_quant_linear_rope_append: projection too wide");
+  const int32_t n = int32_t(heads * head_dim);
+  if (int rc = check_quant_shape("edgerag_quant_linear_rope_append", n, k, bits, group_size))
+    return rc;
+  if (m == 0) return EDGERAG_OK;
+  if (x == nullptr || packed == nullptr || scales_f16 == nullptr || cos_tok == nullptr ||
+      sin_tok == nullptr || q_out == nullptr || slots == nullptr || key_pool == nullptr ||
+      value_pool == nullptr)
+    return fail(EDGERAG_EINVAL, "edgerag_quant_linear_rope_append: NULL pointer");
+  if (x_stride < k || q_stride_tok < int64_t(n_q_heads) * head_dim)
+    return fail(EDGERAG_EINVAL, "edgerag_quant_linear_rope_append: row strides (%lld, %lld) too small",
+                (long long)x_stride, (long long)q_stride_tok);
+  if (x_dtype != EDGERAG_F16 ||
+      !qlinear_rope_supported(m, k, n, bits, group_size, int32_t(heads), head_dim, x, x_stride,
+                              packed))
+    return fail(EDGERAG_EUNSUPPORTED,
+                "edgerag_quant_linear_rope_append: shape not covered (dtype %d, M %d, K %d, N %d, "
+                "bits %d, group %d, head_dim %d); use edgerag_quant_linear + edgerag_rope_append",
+                x_dtype, m, k, n, bits, group_size, head_dim);
+  EpiArgs ea{};
+  ea.cos_tok = static_cast<const f16*>(cos_tok);
+  ea.sin_tok = static_cast<const f16*>(sin_tok);
+  ea.slots = slots;
+  ea.q_out = static_cast<f16*>(q_out);
+  ea.q_st = q_stride_tok;
+  ea.kpool = static_cast<f16*>(key_pool);
+  ea.vpool = static_cast<f16*>(value_pool);
+  ea.num_blocks = num_blocks;
+  ea.block_size = block_size;
+  ea.n_q_heads = n_q_heads;
+  ea.n_kv_heads = n_kv_heads;
+  ea.head_dim = head_dim;
+  launch_qlinear_rope(static_cast<const f16*>(x), x_stride, m, k, packed,
+                      static_cast<const f16*>(scales_f16), static_cast<const f16*>(bias_f16), n, ea,
+                      static_cast<hipStream_t>(stream));
+  return check_launch("edgerag_quant_linear_rope_append");
+}

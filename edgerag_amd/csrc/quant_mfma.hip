@@ -312,36 +312,64 @@ __global__ __launch_bounds__(KWMAX * kWave) void qlinear_skinny_kernel(
 // The dequantised weight is the exact integer code (no scale): the row's scale multiplies the fp32
 // sum once, scale * sum(code * x), instead of rounding every code * scale to fp16 first.
 //
-// SW (SwiGLU, NT == 2): the weight is [gate; up] (N = 2 I rows) and row tile 1 is the up twin of
-// tile 0 (rows I + n0 + [0, R)), so every workgroup holds gate and up of the same R columns and
-// writes act[t][j] = fp16(fp16(silu(g)) * u) to y (T x I) instead of the projection. g and u are
-// the fp16 outputs the plain launch would write: same tiles, waves, batches and summation order.
-template <int F, int NT, int MT, int KW, int U, bool EXACT, bool SW>
+// Epilogues (EPI):
+// * kEpiPlain: y = the projection.
+// * kEpiSwiglu (NT == 2): the weight is [gate; up] (N = 2 I rows) and row tile 1 is the up twin of
+//   tile 0 (rows I + n0 + [0, R)), so every workgroup holds gate and up of the same R columns and
+//   writes act[t][j] = fp16(fp16(silu(g)) * u) to y (T x I) instead of the projection.
+// * kEpiRope (NT == 2, F == 1): the weight is the fused [q heads | k heads | v heads] projection
+//   and the two row tiles are the two halves of one head (rows head D + tn D / 2 + j + [0, 16)),
+//   so every rotate_half pair (d, d + D / 2) sits in one wave; q heads are rotated into q_out, k
+//   heads rotated and v heads copied into the paged pools at the token's slot.
+// The fp16 projection values the epilogues start from are the ones the plain launch of the same
+// shape writes: the host gives the fused launches the same waves, batches and k-slices, so the
+// summation order, and so the bits, are the same.
+constexpr int kEpiPlain = 0, kEpiSwiglu = 1, kEpiRope = 2;
+
+// The reference's rotate_half RoPE on one element (fp16 ops, each product rounded before the add):
+// first half: x1 cos - x2 sin; second half: x2 cos + x1 sin (x1 = element d, x2 = element d + D/2).
+__device__ __forceinline__ f16 rope_elem(float own, float partner, bool second, float c, float sn) {
+#pragma clang fp contract(off)
+  const float a = __half2float(__float2half_rn(own * c));
+  const float b = __half2float(__float2half_rn((second ? partner : -partner) * sn));
+  return __float2half_rn(a + b);
+}
+
+template <int F, int NT, int MT, int KW, int U, bool EXACT, int EPI>
 __global__ __launch_bounds__(KW * kWave)
 __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlinear_stream_kernel(
     const f16* __restrict__ x, int64_t xs, int32_t m, int32_t k,
     const uint8_t* __restrict__ packed, const f16* __restrict__ scales,
-    const f16* __restrict__ bias, int32_t n, f16* __restrict__ y, int64_t ys) {
+    const f16* __restrict__ bias, int32_t n, f16* __restrict__ y, int64_t ys, const EpiArgs ea) {
   constexpr int R = 16 / F;
   constexpr int CB = 64 * F;               // bytes (= k) of one chunk step of a row
   constexpr int OUTS = NT * MT * R * R;    // outputs (token, row) of a workgroup
+  constexpr int NO = (OUTS + KW * kWave - 1) / (KW * kWave);  // outputs per thread
   static_assert((KW * kWave) % (NT * R) == 0, "a thread's outputs share one weight row");
-  static_assert(!SW || (NT == 2 && kWave % (NT * R) == 0),
-                "SwiGLU pairs tile 0 with tile 1 inside one wave");
+  static_assert(EPI == kEpiPlain || (NT == 2 && kWave % (NT * R) == 0),
+                "paired epilogues pair tile 0 with tile 1 inside one wave");
+  static_assert(EPI != kEpiRope || F == 1, "RoPE pairs 16-row tiles");
   __shared__ float red[KW * NT * MT * 4 * kWave];
   const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63;
   const int li = lane & 15, lg = lane >> 4;
   const int f = li / R, r = li % R;
-  const int half = n >> 1;  // SW: gate rows [0, half), up rows [half, n)
-  const int n0 = blockIdx.x * (SW ? R : NT * R);
+  // kEpiSwiglu: gate rows [0, half), up rows [half, n). kEpiRope: head_dim / 2.
+  const int half = EPI == kEpiRope ? ea.head_dim >> 1 : n >> 1;
+  const int per_head = half / 16;  // kEpiRope: workgroups per head
+  const int rope_head = EPI == kEpiRope ? int(blockIdx.x) / per_head : 0;
+  const int rope_j = EPI == kEpiRope ? (int(blockIdx.x) % per_head) * 16 : 0;
+  const int n0 = EPI == kEpiRope ? rope_head * ea.head_dim + rope_j
+                                 : int(blockIdx.x) * (EPI == kEpiSwiglu ? R : NT * R);
   const int nc = k / CB;  // chunk steps: >= U, and a multiple of KW * U when EXACT
   const int per = (nc + KW - 1) / KW;
   const int c0 = min(nc, wave * per), c1 = min(nc, c0 + per);
-  // Weight row of lane row rr in tile tn. Rows past N (past I in a SW half) re-read the last
-  // row: they only feed D rows that are never read.
+  // Weight row of lane row rr in tile tn. Rows past N (past I in a SwiGLU half) re-read the last
+  // row: they only feed D rows that are never read. (kEpiRope launches cover N exactly.)
   auto wrow = [&](int tn, int rr) {
-    return SW ? min(n0 + rr, half - 1) + tn * half : min(n0 + tn * R + rr, n - 1);
+    if constexpr (EPI == kEpiPlain) return min(n0 + tn * R + rr, n - 1);
+    else if constexpr (EPI == kEpiSwiglu) return min(n0 + rr, half - 1) + tn * half;
+    else return n0 + tn * half + rr;
   };
 
   // A lane of n-tile tn: weight row wrow(tn, r); B lane of m-tile t: activation row t R + r.
@@ -367,6 +395,23 @@ __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlin
   const int s_idx = e_row + s_mis, b_idx = e_row + b_mis;
   uint32_t s_bits = reinterpret_cast<const uint32_t*>(scales - s_mis)[s_idx >> 1];
   uint32_t b_bits = reinterpret_cast<const uint32_t*>(b_src - b_mis)[b_idx >> 1];
+  // kEpiRope: every output of this thread is element e_d of its head for token e / (NT R); the
+  // token's cos / sin at e_d and its slot are loaded now as well (tokens past M re-read the last).
+  const int e_d = (e_in / R) * half + rope_j + e_in % R;
+  // (Raw loads only, nothing computed on them before the pins, like the scale and bias words.)
+  int32_t rope_slot[EPI == kEpiRope ? NO : 1];
+  uint32_t rope_c[EPI == kEpiRope ? NO : 1], rope_s[EPI == kEpiRope ? NO : 1];
+  if constexpr (EPI == kEpiRope) {
+    const uint16_t* cos_u = reinterpret_cast<const uint16_t*>(ea.cos_tok);
+    const uint16_t* sin_u = reinterpret_cast<const uint16_t*>(ea.sin_tok);
+#pragma unroll
+    for (int o = 0; o < NO; ++o) {
+      const int tok = min((int(threadIdx.x) + o * KW * kWave) / (NT * R), m - 1);
+      rope_slot[o] = ea.slots[tok];
+      rope_c[o] = cos_u[int64_t(tok) * ea.head_dim + e_d];
+      rope_s[o] = sin_u[int64_t(tok) * ea.head_dim + e_d];
+    }
+  }
 
   f32x4 acc[NT][MT];
 #pragma unroll
@@ -418,7 +463,14 @@ __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlin
       }
     }
     // The epilogue's scale and bias are waited for here, once the first batch is computed.
-    if (cb == c0) asm volatile("" : "+v"(s_bits), "+v"(b_bits));
+    if (cb == c0) {
+      asm volatile("" : "+v"(s_bits), "+v"(b_bits));
+      if constexpr (EPI == kEpiRope) {
+#pragma unroll
+        for (int o = 0; o < NO; ++o)
+          asm volatile("" : "+v"(rope_slot[o]), "+v"(rope_c[o]), "+v"(rope_s[o]));
+      }
+    }
   }
 
   // Sum slices and waves in a fixed order, then y[m][n] = scale[n] * sum (+ bias[n]).
@@ -450,14 +502,14 @@ __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlin
     }
     return __float2half_rn(__builtin_fmaf(scale, sum, bv));
   };
-  if constexpr (!SW) {
+  if constexpr (EPI == kEpiPlain) {
     for (int e = threadIdx.x; e < OUTS; e += KW * kWave) {
       const int tok = e / (NT * R), row_in = e % (NT * R);
       const int nrow = n0 + row_in;
       if (tok >= m || nrow >= n) continue;
       y[int64_t(tok) * ys + nrow] = out_sum(tok, row_in / R, row_in % R);
     }
-  } else {
+  } else if constexpr (EPI == kEpiSwiglu) {
     // The up output of gate lane l sits in lane l + R of the same wave (same token, tile 1). OUTS
     // and the stride are multiples of 64, so whole waves run each iteration and the shuffle sees
     // every lane.
@@ -468,6 +520,38 @@ __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlin
       const float u = __shfl_down(v, R, kWave);
       if (tn == 0 && tok < m && n0 + rr < half)
         y[int64_t(tok) * ys + n0 + rr] = __float2half_rn(silu_rounded_f16(v) * u);
+    }
+  } else {
+    // Element d of a head sits in lane l and its rotate_half partner d +- D/2 in lane l ^ 16.
+    const int tn = e_in / R;
+    const int nq = ea.n_q_heads, nkv = ea.n_kv_heads;
+    const int64_t pool_rows = int64_t(ea.num_blocks) * ea.block_size;
+#pragma unroll
+    for (int o = 0; o < NO; ++o) {
+      const int e = int(threadIdx.x) + o * KW * kWave;
+      if (e >= OUTS) break;  // uniform per wave
+      const int tok = e / (NT * R);
+      const float v = __half2float(out_sum(tok, tn, e_in % R));
+      const float partner = __shfl_xor(v, 16, kWave);
+      if (tok >= m) continue;
+      const float c = __half2float(__builtin_bit_cast(f16, uint16_t(rope_c[o])));
+      const float sn = __half2float(__builtin_bit_cast(f16, uint16_t(rope_s[o])));
+      const int head = rope_head;
+      if (head < nq) {
+        ea.q_out[int64_t(tok) * ea.q_st + int64_t(head) * ea.head_dim + e_d] =
+            rope_elem(v, partner, tn == 1, c, sn);
+        continue;
+      }
+      const int64_t slot = rope_slot[o];
+      if (slot < 0 || slot >= pool_rows) continue;
+      const int kvh = head < nq + nkv ? head - nq : head - nq - nkv;
+      const int64_t off =
+          ((int64_t(kvh) * ea.num_blocks + slot / ea.block_size) * ea.block_size +
+           slot % ea.block_size) * ea.head_dim + e_d;
+      if (head < nq + nkv)
+        ea.kpool[off] = rope_elem(v, partner, tn == 1, c, sn);
+      else
+        ea.vpool[off] = __float2half_rn(v);
     }
   }
 }
@@ -799,63 +883,79 @@ void launch_gemm(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* 
 // steps per batch U from K alone, so that a row's summation order, and so its bits, do not depend
 // on M or on the other rows of the launch. Returns false when the shape does not fit (the caller
 // then uses the skinny kernel).
-template <int F, int NT, int MT, int KW, int U, bool SW>
+template <int F, int NT, int MT, int KW, int U, int EPI>
 void launch_stream(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
                    const f16* scales, const f16* bias, int32_t n, f16* y, int64_t ys,
-                   hipStream_t s) {
+                   const EpiArgs& ea, hipStream_t s) {
   constexpr int rows = NT * 16 / F;
-  // SW: one workgroup per 16 / F columns of the activation (a gate tile and its up twin).
-  const unsigned blocks = SW ? unsigned((n / 2 + 16 / F - 1) / (16 / F))
-                             : unsigned((n + rows - 1) / rows);
+  // SwiGLU: one workgroup per 16 / F activation columns (a gate tile and its up twin); RoPE: one
+  // per 16 elements of a head's first half (that tile and its rotate_half twin).
+  const unsigned blocks = EPI == kEpiSwiglu ? unsigned((n / 2 + 16 / F - 1) / (16 / F))
+                          : EPI == kEpiRope ? unsigned(n / 32)
+                                            : unsigned((n + rows - 1) / rows);
   if ((k / (64 * F)) % (KW * U) == 0)
-    hipLaunchKernelGGL((qlinear_stream_kernel<F, NT, MT, KW, U, true, SW>), dim3(blocks),
-                       dim3(KW * kWave), 0, s, x, xs, m, k, packed, scales, bias, n, y, ys);
+    hipLaunchKernelGGL((qlinear_stream_kernel<F, NT, MT, KW, U, true, EPI>), dim3(blocks),
+                       dim3(KW * kWave), 0, s, x, xs, m, k, packed, scales, bias, n, y, ys, ea);
   else
-    hipLaunchKernelGGL((qlinear_stream_kernel<F, NT, MT, KW, U, false, SW>), dim3(blocks),
-                       dim3(KW * kWave), 0, s, x, xs, m, k, packed, scales, bias, n, y, ys);
+    hipLaunchKernelGGL((qlinear_stream_kernel<F, NT, MT, KW, U, false, EPI>), dim3(blocks),
+                       dim3(KW * kWave), 0, s, x, xs, m, k, packed, scales, bias, n, y, ys, ea);
 }
 
-template <int F, int NT, int MT, bool SW = false>
-void launch_stream_k(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
-                     const f16* scales, const f16* bias, int32_t n, f16* y, int64_t ys,
-                     hipStream_t s) {
-  // One batch of at most 8 steps per wave; at least 4 waves (one per SIMD), or 8 for two row
-  // tiles (one output per thread); at most 16, or 8 for two row or m tiles, whose registers
-  // would not fit 16 waves.
-  // The waves (so the K split, so the bits) depend on K, F and NT only, except that 16-wave
-  // workgroups (K > 64 F steps) drop to 8 where their registers would not fit (F = 2 with two
-  // m-tiles, four m-tiles); several m-tiles take batches of 4 steps to bound their activation
-  // registers.
-  const int nc = k / (64 * F);
-  constexpr int kw_min = NT == 1 ? 4 : 8;
-  constexpr int kw_max = NT == 1 && MT < 4 && !(F == 2 && MT == 2) ? 16 : 8;
+// Waves per workgroup and steps per batch of the streaming kernel for F k-slices, NT row tiles
+// and MT m-tiles: one batch of at most 8 steps per wave; at least 4 waves (one per SIMD), or 8
+// for two row tiles (one output per thread); at most 16, or 8 for two row or m tiles, whose
+// registers would not fit 16 waves. They depend on K, F, NT and MT only (so a row's summation
+// order, and so its bits, on the shape alone), except that 16-wave workgroups (K > 64 F steps)
+// drop to 8 where their registers would not fit (F = 2 with two m-tiles, four m-tiles); several
+// m-tiles take batches of 4 steps to bound their activation registers.
+struct StreamWaves {
+  int kw;
+  bool u8;
+};
+StreamWaves stream_waves(int f, int nt, int mt, int k) {
+  const int nc = k / (64 * f);
+  const int kw_min = nt == 1 ? 4 : 8;
+  const int kw_max = nt == 1 && mt < 4 && !(f == 2 && mt == 2) ? 16 : 8;
   int kw = kw_min;
   while (kw < kw_max && kw * 8 < nc) kw *= 2;
-  const bool u8 = MT == 1 && (nc + kw - 1) / kw > 4 && nc >= 8;
+  return {kw, mt == 1 && (nc + kw - 1) / kw > 4 && nc >= 8};
+}
+
+// Launches the shape with the given waves (KW in {4, 8, 16}) and batch (U in {4, 8}).
+template <int F, int NT, int MT, int EPI>
+void launch_stream_w(StreamWaves sw, const f16* x, int64_t xs, int32_t m, int32_t k,
+                     const uint8_t* packed, const f16* scales, const f16* bias, int32_t n, f16* y,
+                     int64_t ys, const EpiArgs& ea, hipStream_t s) {
 #define EDGERAG_STREAM(KW)                                                                      \
   do {                                                                                         \
     if constexpr (MT == 1) {                                                                   \
-      if (u8) {                                                                                \
-        launch_stream<F, NT, MT, KW, 8, SW>(x, xs, m, k, packed, scales, bias, n, y, ys, s);   \
-        break;                                                                                 \
+      if (sw.u8) {                                                                             \
+        launch_stream<F, NT, MT, KW, 8, EPI>(x, xs, m, k, packed, scales, bias, n, y, ys, ea,  \
+                                             s);                                               \
+        return;                                                                                \
       }                                                                                        \
     }                                                                                          \
-    launch_stream<F, NT, MT, KW, 4, SW>(x, xs, m, k, packed, scales, bias, n, y, ys, s);       \
+    launch_stream<F, NT, MT, KW, 4, EPI>(x, xs, m, k, packed, scales, bias, n, y, ys, ea, s);  \
+    return;                                                                                    \
   } while (0)
-  if constexpr (kw_min == 4) {
-    if (kw == 4) {
-      EDGERAG_STREAM(4);
-      return;
-    }
+  // Only the combinations stream_waves can pick are instantiated: 4 waves for one row tile (and
+  // for RoPE launches, which take the waves of the plain one-tile launch), 16 where registers fit.
+  if constexpr (NT == 1 || EPI == kEpiRope) {
+    if (sw.kw == 4) EDGERAG_STREAM(4);
   }
-  if constexpr (kw_max == 16) {
-    if (kw == 16) {
-      EDGERAG_STREAM(16);
-      return;
-    }
+  if constexpr (NT == 1 && MT < 4 && !(F == 2 && MT == 2)) {
+    if (sw.kw == 16) EDGERAG_STREAM(16);
   }
   EDGERAG_STREAM(8);
 #undef EDGERAG_STREAM
+}
+
+template <int F, int NT, int MT, int EPI = kEpiPlain>
+void launch_stream_k(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
+                     const f16* scales, const f16* bias, int32_t n, f16* y, int64_t ys,
+                     hipStream_t s, const EpiArgs& ea = EpiArgs{}) {
+  launch_stream_w<F, NT, MT, EPI>(stream_waves(F, NT, MT, k), x, xs, m, k, packed, scales, bias,
+                                  n, y, ys, ea, s);
 }
 
 bool dispatch_stream(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
@@ -901,11 +1001,11 @@ void dispatch_stream_swiglu(const f16* x, int64_t xs, int32_t m, int32_t k, cons
                             const f16* scales, const f16* bias, int32_t n, f16* y, int64_t ys,
                             hipStream_t s) {
   if (m <= 16)
-    launch_stream_k<1, 2, 1, true>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
+    launch_stream_k<1, 2, 1, kEpiSwiglu>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
   else if (m <= 32)
-    launch_stream_k<1, 2, 2, true>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
+    launch_stream_k<1, 2, 2, kEpiSwiglu>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
   else
-    launch_stream_k<1, 2, 4, true>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
+    launch_stream_k<1, 2, 4, kEpiSwiglu>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
 }
 
 template <int BITS>
@@ -958,6 +1058,46 @@ bool qlinear_mfma_supported(int32_t k, int32_t bits, int32_t g, const void* x, i
   const int kb = bits == 8 ? 64 : 128;
   return (bits == 8 || bits == 4) && k % kb == 0 && g % 32 == 0 && aligned16(x) &&
          aligned16(packed) && (x_stride * 2) % 16 == 0;
+}
+
+// The fused RoPE launch takes the waves and batch of the plain launch of the same (M, K, N), which
+// must itself be a one-k-slice streaming launch: then every q / k / v value it rotates or copies
+// has the plain launch's bits.
+bool stream_rope_shape(int32_t m, int32_t k, int32_t n, int32_t heads, int32_t head_dim) {
+  if (m < 1 || m > 64 || m > EDGERAG_STREAM_MAX_M || k % 64 != 0 || k / 64 < 4) return false;
+  if (head_dim % 32 != 0 || int64_t(heads) * head_dim != n) return false;
+  const int64_t tiles16 = (int64_t(n) + 15) / 16;
+  if (m <= 16 && tiles16 < 256) return false;  // the plain launch would use two k-slices
+  const int nt = tiles16 >= EDGERAG_STREAM_NT2_TILES ? 2 : 1;
+  const int mt = m <= 16 ? 1 : m <= 32 ? 2 : 4;
+  return stream_waves(1, nt, mt, k).kw <= 8;
+}
+
+template <int MT>
+void launch_rope(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
+                 const f16* scales, const f16* bias, int32_t n, const EpiArgs& ea,
+                 hipStream_t s) {
+  const int nt = (int64_t(n) + 15) / 16 >= EDGERAG_STREAM_NT2_TILES ? 2 : 1;
+  launch_stream_w<1, 2, MT, kEpiRope>(stream_waves(1, nt, MT, k), x, xs, m, k, packed, scales,
+                                      bias, n, nullptr, 0, ea, s);
+}
+
+bool qlinear_rope_supported(int32_t m, int32_t k, int32_t n, int32_t bits, int32_t g,
+                            int32_t heads, int32_t head_dim, const void* x, int64_t x_stride,
+                            const void* packed) {
+  return bits == 8 && g == k && qlinear_mfma_supported(k, bits, g, x, x_stride, packed) &&
+         stream_rope_shape(m, k, n, heads, head_dim);
+}
+
+void launch_qlinear_rope(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
+                         const f16* scales, const f16* bias, int32_t n, const EpiArgs& ea,
+                         hipStream_t s) {
+  if (m <= 16)
+    launch_rope<1>(x, xs, m, k, packed, scales, bias, n, ea, s);
+  else if (m <= 32)
+    launch_rope<2>(x, xs, m, k, packed, scales, bias, n, ea, s);
+  else
+    launch_rope<4>(x, xs, m, k, packed, scales, bias, n, ea, s);
 }
 
 bool qlinear_swiglu_supported(int32_t m, int32_t k, int32_t n, int32_t bits, int32_t g,

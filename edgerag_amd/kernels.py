@@ -512,6 +512,77 @@ def rope_append(qkv: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor, s
     return q_out
 
 
+def rope_rows(positions: torch.Tensor, cos: torch.Tensor,
+              sin: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """The rotary table rows at each token's position (clamped to the table), ``(T, head_dim)``
+    each: what ``quant_linear_rope_append`` reads. Gathered once per forward, shared by layers."""
+    idx = positions.long().clamp(0, cos.shape[0] - 1)
+    return cos.index_select(0, idx), sin.index_select(0, idx)
+
+
+def quant_rope_fused(m: int, k: int, bits: int, group_size: int, n_q_heads: int,
+                     n_kv_heads: int, head_dim: int, dtype: torch.dtype = torch.float16) -> bool:
+    """Whether ``quant_linear_rope_append`` runs as one launch (16-byte aligned rows)."""
+    return bool(_lib.load().edgerag_quant_linear_rope_append_supported(
+        dtype_code(dtype) if dtype in (torch.float16, torch.float32) else -1, m, k, bits,
+        group_size, n_q_heads, n_kv_heads, head_dim))
+
+
+def quant_linear_rope_append(
+    x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, bias: torch.Tensor | None,
+    in_features: int, bits: int, group_size: int, positions: torch.Tensor, cos: torch.Tensor,
+    sin: torch.Tensor, n_q_heads: int, n_kv_heads: int, head_dim: int, slots: torch.Tensor,
+    key_pool: torch.Tensor, value_pool: torch.Tensor, q_out: torch.Tensor | None = None,
+    rows: tuple[torch.Tensor, torch.Tensor] | None = None,
+) -> torch.Tensor:
+    """The fused q/k/v quant linear, RoPE and KV append; returns q ``(T, n_q_heads, head_dim)``.
+
+    One launch where the native library covers the shape and ``rows`` (``rope_rows`` of the
+    step) is given; otherwise ``quant_linear`` then ``rope_append``. Both give the same bits."""
+    require_device(x, packed, scales, bias, positions, cos, sin, slots, key_pool, value_pool,
+                   q_out)
+    n = (n_q_heads + 2 * n_kv_heads) * head_dim
+    x2 = x.reshape(-1, in_features)
+    if x2.stride(1) != 1 or (x2.stride(0) * x2.element_size()) % 16 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    T = x2.shape[0]
+    if q_out is None:
+        q_out = torch.empty((T, n_q_heads, head_dim), dtype=x.dtype, device=x.device)
+    fused = (
+        rows is not None and T > 0 and x2.dtype == torch.float16 and packed.data_ptr() % 16 == 0
+        and key_pool.dtype == torch.float16 and slots.dtype == torch.int32
+        and quant_rope_fused(T, in_features, bits, group_size, n_q_heads, n_kv_heads, head_dim)
+    )
+    if not fused:
+        qkv = quant_linear(x2, packed, scales, bias, in_features, n, bits, group_size)
+        return rope_append(qkv, positions, cos, sin, n_q_heads, n_kv_heads, head_dim, slots,
+                           key_pool, value_pool, q_out=q_out)
+    _check_pool(key_pool, "key_pool")
+    _check_pool(value_pool, "value_pool")
+    nkv, num_blocks, block_size, d = key_pool.shape
+    if (nkv, d) != (n_kv_heads, head_dim) or value_pool.shape != key_pool.shape:
+        raise ValueError("pools do not match the heads")
+    cos_tok, sin_tok = rows
+    if cos_tok.shape != (T, head_dim) or sin_tok.shape != (T, head_dim) or \
+            cos_tok.dtype != torch.float16 or not (cos_tok.is_contiguous() and sin_tok.is_contiguous()):
+        raise ValueError(f"rope rows must be contiguous fp16 ({T}, {head_dim})")
+    if q_out.shape != (T, n_q_heads, head_dim) or q_out.stride(2) != 1 or \
+            q_out.stride(1) != head_dim:
+        raise ValueError("q_out must be (tokens, n_q_heads, head_dim) with packed heads")
+    if scales.dtype != torch.float16:
+        scales = scales.to(torch.float16)
+    if bias is not None and bias.dtype != torch.float16:
+        bias = bias.to(torch.float16)
+    call(
+        "edgerag_quant_linear_rope_append", x2.data_ptr(), dtype_code(x2.dtype), x2.stride(0), T,
+        in_features, packed.data_ptr(), scales.contiguous().data_ptr(), ptr(bias), bits,
+        group_size, cos_tok.data_ptr(), sin_tok.data_ptr(), n_q_heads, n_kv_heads, head_dim,
+        q_out.data_ptr(), q_out.stride(0), slots.data_ptr(), key_pool.data_ptr(),
+        value_pool.data_ptr(), num_blocks, block_size, stream_ptr(x.device),
+    )
+    return q_out
+
+
 def silu_mul(gate_up: torch.Tensor, intermediate: int,
              out: torch.Tensor | None = None) -> torch.Tensor:
     """SwiGLU activation of the fused ``[gate | up]`` rows: ``(T, 2I) -> (T, I)``."""

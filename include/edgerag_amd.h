@@ -253,6 +253,35 @@ int edgerag_quant_linear_swiglu(const void* x, int32_t x_dtype, int64_t x_stride
 int edgerag_quant_linear_swiglu_supported(int32_t x_dtype, int32_t m, int32_t k, int32_t n,
                                           int32_t bits, int32_t group_size);
 
+/*
+ * The fused q/k/v quant linear followed by RoPE and the KV append, in one launch. W is the packed
+ * INT8 per-channel [n_q_heads | n_kv_heads | n_kv_heads] x head_dim projection (N = heads x
+ * head_dim rows). Each projection value is exactly what edgerag_quant_linear writes for the same
+ * arguments; the rest is edgerag_rope_append on those values, except that the tables come as one
+ * row per token: cos_tok / sin_tok are [M, head_dim] (row t = the table row at token t's
+ * position, already clamped), fp16. q heads go to q_out (row stride q_stride_tok, head stride
+ * head_dim), rotated k and raw v heads to the pools at slots[t] (skipped when negative or
+ * outside the pool). Covered: fp16 x, bits 8 with group_size == K, 1 <= M <= 64, K a multiple of
+ * 64 (at least 256) handled by at most 8 waves, head_dim a multiple of 32, and N at least 4096
+ * when M <= 16; edgerag_quant_linear_rope_append_supported says so beforehand. Anything else
+ * returns EDGERAG_EUNSUPPORTED (then run edgerag_quant_linear and edgerag_rope_append).
+ *
+ * Replaces the decode iteration's q/k/v projections + apply_rope + cache.update's write
+ * (edgerag/core/layers.py:93-114, :289-306; edgerag/cache/paged.py:186-206).
+ */
+int edgerag_quant_linear_rope_append(const void* x, int32_t x_dtype, int64_t x_stride, int32_t m,
+                                     int32_t k, const uint8_t* packed, const void* scales_f16,
+                                     const void* bias_f16, int32_t bits, int32_t group_size,
+                                     const void* cos_tok, const void* sin_tok, int32_t n_q_heads,
+                                     int32_t n_kv_heads, int32_t head_dim, void* q_out,
+                                     int64_t q_stride_tok, const int32_t* slots, void* key_pool,
+                                     void* value_pool, int32_t num_blocks, int32_t block_size,
+                                     void* stream);
+/* 1 when edgerag_quant_linear_rope_append covers the shape for 16-byte aligned x rows and W. */
+int edgerag_quant_linear_rope_append_supported(int32_t x_dtype, int32_t m, int32_t k, int32_t bits,
+                                               int32_t group_size, int32_t n_q_heads,
+                                               int32_t n_kv_heads, int32_t head_dim);
+
 /* ==== Fused elementwise ops of a decoder layer ============================================ */
 
 /*

@@ -54,6 +54,21 @@ def test_swiglu_support_query() -> None:
     assert q(F16, 8, 200, 16384, 8, 200) == 0  # K not a multiple of 64
 
 
+def test_rope_append_support_query() -> None:
+    """The fused q/k/v + RoPE + KV append covers decode batches whose plain projection launch
+    streams with one k-slice; the query answers without touching a GPU."""
+    q = _lib.load().edgerag_quant_linear_rope_append_supported
+    F16 = 1
+    assert q(F16, 8, 2048, 8, 2048, 32, 32, 64) == 1  # config 5's q/k/v, a decode batch
+    assert q(F16, 64, 2048, 8, 2048, 32, 8, 64) == 1  # GQA, N 3072: one k-slice from M > 16
+    assert q(F16, 8, 2048, 8, 2048, 32, 8, 64) == 0  # N 3072 at M <= 16: two k-slices
+    assert q(F16, 65, 2048, 8, 2048, 32, 32, 64) == 0
+    assert q(F16, 8, 2048, 8, 2048, 32, 32, 48) == 0  # head_dim not a multiple of 32
+    assert q(F16, 8, 2048, 4, 128, 32, 32, 64) == 0  # INT4
+    assert q(0, 8, 2048, 8, 2048, 32, 32, 64) == 0  # fp32 activations
+    assert q(F16, 8, 16384, 8, 16384, 32, 32, 64) == 0  # K needing 16 waves
+
+
 def test_validation_errors_come_back_as_messages() -> None:
     with pytest.raises(_lib.EdgeragError, match="only 4- and 8-bit"):
         _lib.call("edgerag_quant_linear", None, 1, 16, 1, 16, None, None, None, 4, 3, 16, None,

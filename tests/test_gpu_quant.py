@@ -192,6 +192,61 @@ def test_quant_linear_swiglu_fused(device, k, n, with_bias) -> None:
         torch.testing.assert_close(fused.float().cpu(), ref, **LINEAR_TOL)
 
 
+@pytest.mark.parametrize("n_q,n_kv,d,k", [(32, 32, 64, 2048), (32, 8, 128, 1024),
+                                           (16, 4, 64, 640)])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_quant_linear_rope_append_fused(device, n_q, n_kv, d, k, with_bias) -> None:
+    """q/k/v projection + RoPE + KV append in the streaming GEMV's epilogue: q_out and both pools
+    bit-identical to quant_linear followed by rope_append, for decode batches (M <= 16) and
+    M up to 64; GQA and head_dim 128 (four workgroups per head); slots that are padding (-1) or
+    past the pool leave the pools untouched. Shapes whose plain launch uses two k-slices (N < 4096
+    at M <= 16) take the two-launch path through the same entry."""
+    from edgerag_amd.core.layers import RotaryTable
+
+    n = (n_q + 2 * n_kv) * d
+    w = _weight(n, k, n + k + d)
+    cfg = oq.QuantConfig(k, 8)
+    packed, scales = oq.quantize_for_layer(w, cfg)
+    bias = (torch.randn(n, generator=seeded(n + 1)) * 0.1).half() if with_bias else None
+    pd, sd = packed.to(device), scales.to(device)
+    bd = bias.to(device) if bias is not None else None
+    bs, nb = 16, 64
+    table = RotaryTable(d, 130000.0, 8192, device, torch.float16)
+    for m in (1, 3, 8, 16, 17, 33, 64):
+        g = seeded(m * 7 + d)
+        x = torch.randn(m, k, generator=g).half().to(device)
+        positions = torch.randint(0, 9000, (m,), generator=g, dtype=torch.int32)  # some clamped
+        slots = torch.randperm(nb * bs, generator=g)[:m].to(torch.int32)
+        slots[0] = -1
+        if m > 2:
+            slots[2] = nb * bs + 5
+        pos_d, slots_d = positions.to(device), slots.to(device)
+        rows = kernels.rope_rows(pos_d, table.cos, table.sin)
+        fused = kernels.quant_rope_fused(m, k, 8, k, n_q, n_kv, d)
+        assert fused == (m > 16 or n >= 4096)
+        pools = []
+        qs = []
+        for use_rows in (rows, None):  # fused launch, then the two-launch path
+            kp = torch.full((n_kv, nb, bs, d), 7.0, dtype=torch.float16, device=device)
+            vp = torch.full_like(kp, -3.0)
+            q = kernels.quant_linear_rope_append(
+                x, pd, sd, bd, k, 8, k, pos_d, table.cos, table.sin, n_q, n_kv, d, slots_d, kp, vp,
+                rows=use_rows)
+            qs.append(q)
+            pools.append((kp, vp))
+        assert torch.equal(qs[0], qs[1]), f"M={m}: q differs from the two-launch path"
+        assert torch.equal(pools[0][0], pools[1][0]), f"M={m}: key pool differs"
+        assert torch.equal(pools[0][1], pools[1][1]), f"M={m}: value pool differs"
+        # Padding and out-of-pool slots wrote nothing; every valid slot was written.
+        kc = pools[0][0].cpu()
+        valid = [int(s) for s in slots if 0 <= int(s) < nb * bs]
+        for s_ in valid:
+            assert not torch.all(kc[:, s_ // bs, s_ % bs] == 7.0)
+        untouched = torch.ones(nb * bs, dtype=torch.bool)
+        untouched[valid] = False
+        assert torch.all(kc.reshape(n_kv, nb * bs, d)[:, untouched] == 7.0)
+
+
 def test_quant_linear_swiglu_falls_back_outside_its_shapes(device) -> None:
     """Shapes the fused launch does not cover (M > 64, N below two tiles per workgroup, INT4)
     run as projection + silu_mul through the same entry, and the C entry point says why."""
