@@ -27,6 +27,9 @@
 #ifndef EDGERAG_STREAM_MAX_M
 #define EDGERAG_STREAM_MAX_M 64  // per-channel INT8 launches up to this M use the streaming kernel
 #endif
+#ifndef EDGERAG_STREAM_NARROW_F2
+#define EDGERAG_STREAM_NARROW_F2 1  // 17..32 tokens on narrow N: two k-slices (see dispatch_stream)
+#endif
 #ifndef EDGERAG_STREAM_NT2_TILES
 #define EDGERAG_STREAM_NT2_TILES 512  // 16-row tiles from which a workgroup takes two
 #endif
@@ -958,34 +961,44 @@ void launch_stream_k(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8
                                   n, y, ys, ea, s);
 }
 
+// The k-slices (1 or 2) dispatch_stream uses for (M, K, N), 0 when it does not take the shape:
+// two (8-row tiles) when 16-row tiles would leave CUs idle (N < 4096) for up to 16 tokens, and for
+// 17..32 tokens (M = 32, K 8192 -> N 2048: 21.4 -> 18.8 us; for 33..64 tokens two such launches
+// measured slower than one k-slice).
+int stream_slices(int32_t m, int32_t k, int32_t n) {
+  const int64_t tiles16 = (int64_t(n) + 15) / 16;
+  const bool one = k % 64 == 0 && k / 64 >= 4, two = k % 128 == 0 && k / 128 >= 4;
+  if (m < 1 || m > 64) return 0;
+  if (EDGERAG_STREAM_NARROW_F2 && m > 16 && m <= 32 && tiles16 < 256 && two) return 2;
+  if (m > 16) return one ? 1 : 0;
+  if (tiles16 < 256) return two ? 2 : 0;
+  return one ? 1 : 0;
+}
+
 bool dispatch_stream(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
                      const f16* scales, const f16* bias, int32_t n, f16* y, int64_t ys,
                      hipStream_t s) {
-  if (m > 64) return false;
-  const int64_t tiles16 = (n + 15) / 16;
-  if (m > 16) {  // 17..64 tokens: one k-slice, up to four 16-token m-tiles
-    if (k % 64 != 0 || k / 64 < 4) return false;
-    const bool two = tiles16 >= EDGERAG_STREAM_NT2_TILES;
-    if (m <= 32) {
-      if (two) launch_stream_k<1, 2, 2>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
-      else launch_stream_k<1, 1, 2>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
-    } else {
-      if (two) launch_stream_k<1, 2, 4>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
-      else launch_stream_k<1, 1, 4>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
-    }
-    return true;
-  }
-  if (tiles16 < 256) {  // 16-row tiles would not cover the 256 CUs: two k-slices, 8-row tiles
-    if (k % 128 != 0 || k / 128 < 4) return false;
+  const int slices = stream_slices(m, k, n);
+  if (slices == 0) return false;
+  if (slices == 2) {  // 8-row tiles and 8-token m-tiles
     if (m <= 8) launch_stream_k<2, 1, 1>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
-    else launch_stream_k<2, 1, 2>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
+    else if (m <= 16) launch_stream_k<2, 1, 2>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
+    else launch_stream_k<2, 1, 4>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
     return true;
   }
-  if (k % 64 != 0 || k / 64 < 4) return false;
-  if (tiles16 >= EDGERAG_STREAM_NT2_TILES)  // 32-row workgroups still cover the CUs
-    launch_stream_k<1, 2, 1>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
-  else
-    launch_stream_k<1, 1, 1>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
+  // One k-slice: 16-row tiles (two per workgroup when 32-row workgroups still cover the CUs),
+  // up to four 16-token m-tiles.
+  const bool two = (int64_t(n) + 15) / 16 >= EDGERAG_STREAM_NT2_TILES;
+  if (m <= 16) {
+    if (two) launch_stream_k<1, 2, 1>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
+    else launch_stream_k<1, 1, 1>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
+  } else if (m <= 32) {
+    if (two) launch_stream_k<1, 2, 2>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
+    else launch_stream_k<1, 1, 2>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
+  } else {
+    if (two) launch_stream_k<1, 2, 4>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
+    else launch_stream_k<1, 1, 4>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
+  }
   return true;
 }
 
@@ -993,8 +1006,8 @@ bool dispatch_stream(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8
 // dispatch_stream picks exactly these for the same (M, K, N), so the fused launch computes the
 // same gate and up bits as the plain one.
 bool stream_swiglu_shape(int32_t m, int32_t k, int32_t n) {
-  return m >= 1 && m <= 64 && m <= EDGERAG_STREAM_MAX_M && n % 2 == 0 && k % 64 == 0 &&
-         k / 64 >= 4 && (int64_t(n) + 15) / 16 >= EDGERAG_STREAM_NT2_TILES;
+  return m <= EDGERAG_STREAM_MAX_M && stream_slices(m, k, n) == 1 && n % 2 == 0 &&
+         (int64_t(n) + 15) / 16 >= EDGERAG_STREAM_NT2_TILES;
 }
 
 void dispatch_stream_swiglu(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
@@ -1064,10 +1077,9 @@ bool qlinear_mfma_supported(int32_t k, int32_t bits, int32_t g, const void* x, i
 // must itself be a one-k-slice streaming launch: then every q / k / v value it rotates or copies
 // has the plain launch's bits.
 bool stream_rope_shape(int32_t m, int32_t k, int32_t n, int32_t heads, int32_t head_dim) {
-  if (m < 1 || m > 64 || m > EDGERAG_STREAM_MAX_M || k % 64 != 0 || k / 64 < 4) return false;
+  if (m > EDGERAG_STREAM_MAX_M || stream_slices(m, k, n) != 1) return false;
   if (head_dim % 32 != 0 || int64_t(heads) * head_dim != n) return false;
   const int64_t tiles16 = (int64_t(n) + 15) / 16;
-  if (m <= 16 && tiles16 < 256) return false;  // the plain launch would use two k-slices
   const int nt = tiles16 >= EDGERAG_STREAM_NT2_TILES ? 2 : 1;
   const int mt = m <= 16 ? 1 : m <= 32 ? 2 : 4;
   return stream_waves(1, nt, mt, k).kw <= 8;

@@ -60,8 +60,9 @@ def test_rope_append_support_query() -> None:
     q = _lib.load().edgerag_quant_linear_rope_append_supported
     F16 = 1
     assert q(F16, 8, 2048, 8, 2048, 32, 32, 64) == 1  # config 5's q/k/v, a decode batch
-    assert q(F16, 64, 2048, 8, 2048, 32, 8, 64) == 1  # GQA, N 3072: one k-slice from M > 16
-    assert q(F16, 8, 2048, 8, 2048, 32, 8, 64) == 0  # N 3072 at M <= 16: two k-slices
+    assert q(F16, 64, 2048, 8, 2048, 32, 8, 64) == 1  # GQA, N 3072: one k-slice from M > 32
+    assert q(F16, 8, 2048, 8, 2048, 32, 8, 64) == 0  # N 3072 at M <= 32: two k-slices
+    assert q(F16, 24, 2048, 8, 2048, 32, 8, 64) == 0
     assert q(F16, 65, 2048, 8, 2048, 32, 32, 64) == 0
     assert q(F16, 8, 2048, 8, 2048, 32, 32, 48) == 0  # head_dim not a multiple of 32
     assert q(F16, 8, 2048, 4, 128, 32, 32, 64) == 0  # INT4
