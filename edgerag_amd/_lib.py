@@ -87,18 +87,26 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     ),
     "edgerag_quant_linear_swiglu": (
         [c_vp, c_i32, c_i64, c_i32, c_i32, c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_vp, c_i64,
-         c_vp],
+         c_vp, c_i32, c_f32, c_vp],
         c_i32,
     ),
-    "edgerag_quant_linear_swiglu_supported": ([c_i32, c_i32, c_i32, c_i32, c_i32, c_i32], c_i32),
+    "edgerag_quant_linear_swiglu_supported": (
+        [c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32], c_i32,
+    ),
     "edgerag_quant_linear_rope_append": (
         [c_vp, c_i32, c_i64, c_i32, c_i32, c_vp, c_vp, c_vp, c_i32, c_i32, c_vp, c_vp, c_i32,
-         c_i32, c_i32, c_vp, c_i64, c_vp, c_vp, c_vp, c_i32, c_i32, c_vp],
+         c_i32, c_i32, c_vp, c_i64, c_vp, c_vp, c_vp, c_i32, c_i32, c_vp, c_i32, c_f32, c_vp],
         c_i32,
     ),
     "edgerag_quant_linear_rope_append_supported": (
-        [c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32], c_i32,
+        [c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32], c_i32,
     ),
+    "edgerag_quant_linear_residual": (
+        [c_vp, c_i32, c_i64, c_i32, c_i32, c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_vp, c_i64,
+         c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_vp],
+        c_i32,
+    ),
+    "edgerag_quant_linear_residual_parts": ([c_i32, c_i32, c_i32, c_i32, c_i32, c_i32], c_i32),
     # include/edgerag_probe.h: measurement probes for the rooflines bench.py reports.
     "edgerag_probe_read": ([c_vp, c_i64, c_i32, c_i32, c_vp, c_vp], c_i32),
     "edgerag_probe_gather": ([c_vp, c_vp, c_i32, c_i32, c_i32, c_vp, c_vp], c_i32),

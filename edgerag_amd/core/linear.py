@@ -40,16 +40,20 @@ class LinearBase(nn.Module):
     @abstractmethod
     def weight_bytes(self) -> int: ...
 
-    def swiglu(self, x: torch.Tensor) -> torch.Tensor:
+    def swiglu(self, x: torch.Tensor, norm=None) -> torch.Tensor:
         """``silu(gate(x)) * up(x)`` for a layer whose rows are ``[gate; up]``:
         ``(T, K) -> (T, N / 2)``."""
+        if norm is not None:
+            raise ValueError(f"{type(self).__name__} takes no normed input")
         return kernels.silu_mul(self(x).reshape(-1, self.out_features), self.out_features // 2)
 
     def rope_append(self, x: torch.Tensor, positions, cos, sin, n_q_heads: int, n_kv_heads: int,
-                    head_dim: int, slots, key_pool, value_pool, q_out=None,
-                    rows=None) -> torch.Tensor:
+                    head_dim: int, slots, key_pool, value_pool, q_out=None, rows=None,
+                    norm=None) -> torch.Tensor:
         """For a fused ``[q | k | v]`` layer: RoPE on q and k, k and v appended to the pools at
         ``slots``; returns q ``(T, n_q_heads, head_dim)``. ``rows``: ``kernels.rope_rows``."""
+        if norm is not None:
+            raise ValueError(f"{type(self).__name__} takes no normed input")
         qkv = self(x).reshape(-1, self.out_features)
         return kernels.rope_append(qkv, positions, cos, sin, n_q_heads, n_kv_heads, head_dim,
                                    slots, key_pool, value_pool, q_out=q_out)
@@ -180,21 +184,34 @@ class QuantLinear(LinearBase):
         )
 
     def rope_append(self, x: torch.Tensor, positions, cos, sin, n_q_heads: int, n_kv_heads: int,
-                    head_dim: int, slots, key_pool, value_pool, q_out=None,
-                    rows=None) -> torch.Tensor:
-        """``LinearBase.rope_append`` in one launch for decode batches (``rows`` given)."""
+                    head_dim: int, slots, key_pool, value_pool, q_out=None, rows=None,
+                    norm=None) -> torch.Tensor:
+        """``LinearBase.rope_append`` in one launch for decode batches (``rows`` given);
+        ``norm`` (``kernels.NormedInput``): x is a residual producer's ``xw``, normalised on the
+        fly."""
         return kernels.quant_linear_rope_append(
             x, self.packed, self.scales, self.bias, self.in_features, self.config.bits,
             self.config.group_size, positions, cos, sin, n_q_heads, n_kv_heads, head_dim, slots,
-            key_pool, value_pool, q_out=q_out, rows=rows,
+            key_pool, value_pool, q_out=q_out, rows=rows, norm=norm,
         )
 
-    def swiglu(self, x: torch.Tensor) -> torch.Tensor:
+    def swiglu(self, x: torch.Tensor, norm=None) -> torch.Tensor:
         """``silu(gate(x)) * up(x)`` for a ``concat([gate, up])`` layer: ``(T, K) -> (T, N / 2)``,
-        one launch for decode batches."""
+        one launch for decode batches; ``norm`` as in ``rope_append``."""
         return kernels.quant_linear_swiglu(
             x, self.packed, self.scales, self.bias, self.in_features, self.out_features,
-            self.config.bits, self.config.group_size,
+            self.config.bits, self.config.group_size, norm=norm,
+        )
+
+    def residual(self, x: torch.Tensor, hidden: torch.Tensor, partials: torch.Tensor,
+                 next_norm_weight: torch.Tensor | None = None,
+                 xw: torch.Tensor | None = None) -> int:
+        """``hidden += self(x)`` in place plus what a normed input reads: the sums of squares and
+        ``xw = fp16(next_norm_weight * hidden)`` (``kernels.quant_linear_residual``); returns the
+        sums' count per token."""
+        return kernels.quant_linear_residual(
+            x, self.packed, self.scales, self.bias, self.in_features, self.out_features,
+            self.config.bits, self.config.group_size, hidden, partials, next_norm_weight, xw,
         )
 
     def weight_bytes(self) -> int:

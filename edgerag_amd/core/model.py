@@ -155,15 +155,36 @@ class EdgeRagDecoder(nn.Module):
 
     # --- forward --------------------------------------------------------------------------------
 
+    def _norm_fused(self, T: int) -> bool:
+        """Whether a batch of T tokens runs residual add + RMSNorm inside the projections (decode
+        batches: producers ``quant_linear_residual``, consumers with a normed input)."""
+        spec, layer = self.spec, self.layers[0]
+        h, cfg = spec.hidden_size, layer.o_proj.config
+        if self.dtype != torch.float16 or cfg.bits != 8 or T > 16:
+            return False
+        parts = [kernels.quant_residual_parts(T, lin.in_features, h, 8, lin.config.group_size)
+                 for lin in (layer.o_proj, layer.down_proj)]
+        gu = layer.gate_up
+        return (
+            all(0 < p <= 256 for p in parts)
+            and kernels.quant_swiglu_fused(T, gu.in_features, gu.out_features, gu.config.bits,
+                                           gu.config.group_size, normed=True)
+            and kernels.quant_rope_fused(T, layer.qkv.in_features, layer.qkv.config.bits,
+                                         layer.qkv.config.group_size, spec.n_q_heads,
+                                         spec.n_kv_heads, spec.head_dim, normed=True)
+        )
+
     @torch.inference_mode()
     def forward_hidden(self, step: StepInputs, key_pool: list[torch.Tensor],
                        value_pool: list[torch.Tensor]) -> torch.Tensor:
         """Run every layer over the packed batch; return the final-norm hidden of ``logit_rows``.
 
         Per layer: fused q/k/v linear with RoPE + KV append (one launch for decode batches, two
-        otherwise) -> ragged attention ->
-        o_proj -> residual add + RMSNorm (one launch) -> fused gate/up linear with SiLU * up (one
-        launch for decode batches) -> down_proj -> residual add + the next RMSNorm (one launch)."""
+        otherwise) -> ragged attention -> o_proj -> residual add + RMSNorm -> fused gate/up linear
+        with SiLU * up (one launch for decode batches) -> down_proj -> residual add + the next
+        RMSNorm. Decode batches of up to 16 tokens fold each residual add into o_proj / down_proj
+        (which update the residual stream in place and leave per-workgroup sums of squares) and
+        each RMSNorm into the next projection; otherwise the residual add + RMSNorm is one launch."""
         spec = self.spec
         T = step.token_ids.shape[0]
         d, eps = spec.head_dim, spec.rms_norm_eps
@@ -178,21 +199,39 @@ class EdgeRagDecoder(nn.Module):
                 T, qkv0.in_features, qkv0.config.bits, qkv0.config.group_size, spec.n_q_heads,
                 spec.n_kv_heads, d, self.dtype):
             rows = kernels.rope_rows(step.positions, self.rotary.cos, self.rotary.sin)
+        fused = rows is not None and self._norm_fused(T)
+        partials = (torch.empty(T * 256, dtype=torch.float32, device=self.device) if fused
+                    else None)
+        xw = torch.empty_like(hidden) if fused else None  # fp16(norm weight * hidden)
+        norm = None  # the normed input of the next q/k/v projection (None: x is normalised)
         for idx, layer in enumerate(self.layers):
-            layer.qkv.rope_append(x, step.positions, self.rotary.cos, self.rotary.sin,
-                                  spec.n_q_heads, spec.n_kv_heads, d, step.slots, key_pool[idx],
-                                  value_pool[idx], q_out=q, rows=rows)
+            layer.qkv.rope_append(xw if norm is not None else x, step.positions,
+                                  self.rotary.cos, self.rotary.sin, spec.n_q_heads,
+                                  spec.n_kv_heads, d, step.slots, key_pool[idx], value_pool[idx],
+                                  q_out=q, rows=rows, norm=norm)
             if isinstance(step.plan, kernels.FixedAttention):
                 step.plan.launch(q, key_pool[idx], value_pool[idx], self.scaling, attn_out)
             else:
                 kernels.paged_attention(q, key_pool[idx], value_pool[idx], step.plan,
                                         self.scaling, out=attn_out)
+            next_norm = (self.layers[idx + 1].input_layernorm.weight if idx + 1 < n_layers
+                         else self.norm.weight)
+            if fused:
+                parts = layer.o_proj.residual(attn_out.view(T, layer.q_out), hidden, partials,
+                                              layer.post_attention_layernorm.weight, xw)
+                act = layer.gate_up.swiglu(xw, norm=kernels.NormedInput(partials, parts, eps))
+                last = idx + 1 == n_layers
+                parts = layer.down_proj.residual(act, hidden, partials,
+                                                 None if last else next_norm, None if last else xw)
+                if last:
+                    x = kernels.rmsnorm(hidden, next_norm, eps)
+                else:
+                    norm = kernels.NormedInput(partials, parts, eps)
+                continue
             o = layer.o_proj(attn_out.view(T, layer.q_out))
             x = kernels.rmsnorm(hidden, layer.post_attention_layernorm.weight, eps, delta=o,
                                 h_out=hidden)
             down = layer.down_proj(layer.gate_up.swiglu(x))
-            next_norm = (self.layers[idx + 1].input_layernorm.weight if idx + 1 < n_layers
-                         else self.norm.weight)
             x = kernels.rmsnorm(hidden, next_norm, eps, delta=down, h_out=hidden)
         return x[step.logit_rows.long()]
 

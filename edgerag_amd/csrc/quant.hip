@@ -7,6 +7,8 @@
 // from HBM once, rebuilds w = fp16(code) * scale in registers (one fp16 rounding, the same value
 // the reference's dequantize_groupwise produces) and accumulates x . w in fp32 with
 // v_dot2_f32_f16. Weight bytes dominate traffic for M <= 64, so the kernel is HBM-bound there.
+#include <cmath>
+
 #include "common.h"
 #include "quant_mfma.h"
 
@@ -348,12 +350,37 @@ extern "C" int edgerag_quant_linear(const void* x, int32_t x_dtype, int64_t x_st
   return fail(EDGERAG_EUNSUPPORTED, "edgerag_quant_linear: activation dtype %d", x_dtype);
 }
 
+namespace edgerag {
+namespace {
+
+// The optional RMSNorm operands of the fused entry points: NULL norm_partials means a plain input.
+// Returns EDGERAG_OK or an error code (with the message set).
+int set_norm(const char* fn, int32_t m, const float* norm_partials, int32_t norm_parts, float eps,
+             EpiArgs& ea) {
+  if (norm_partials == nullptr) return EDGERAG_OK;
+  if (norm_parts <= 0 || norm_parts > kNormMaxParts || m > 16 || !(eps >= 0.f) ||
+      !std::isfinite(eps))
+    return fail(EDGERAG_EUNSUPPORTED,
+                "%s: normed input needs M <= 16 (got %d), 1..%d partial sums per token (got %d) "
+                "and a finite eps >= 0",
+                fn, m, kNormMaxParts, norm_parts);
+  ea.norm_part = norm_partials;
+  ea.norm_parts = norm_parts;
+  ea.eps = eps;
+  return EDGERAG_OK;
+}
+
+const void* aligned_stand_in() { return reinterpret_cast<const void*>(uintptr_t(256)); }
+
+}  // namespace
+}  // namespace edgerag
+
 extern "C" int edgerag_quant_linear_swiglu_supported(int32_t x_dtype, int32_t m, int32_t k,
-                                                     int32_t n, int32_t bits,
-                                                     int32_t group_size) {
+                                                     int32_t n, int32_t bits, int32_t group_size,
+                                                     int32_t normed) {
   // Alignment is the caller's part of the contract; a 16-byte aligned stand-in checks the rest.
-  const void* aligned = reinterpret_cast<const void*>(uintptr_t(256));
-  return x_dtype == EDGERAG_F16 && n > 0 && k > 0 && group_size == k &&
+  const void* aligned = aligned_stand_in();
+  return x_dtype == EDGERAG_F16 && n > 0 && k > 0 && group_size == k && (!normed || m <= 16) &&
                  qlinear_swiglu_supported(m, k, n, bits, group_size, aligned, k, aligned)
              ? 1
              : 0;
@@ -363,7 +390,8 @@ extern "C" int edgerag_quant_linear_swiglu(const void* x, int32_t x_dtype, int64
                                            int32_t m, int32_t k, const uint8_t* packed,
                                            const void* scales_f16, const void* bias_f16, int32_t n,
                                            int32_t bits, int32_t group_size, void* y,
-                                           int64_t y_stride, void* stream) {
+                                           int64_t y_stride, const float* norm_partials,
+                                           int32_t norm_parts, float eps, void* stream) {
   clear_error();
   if (int rc = check_quant_shape("edgerag_quant_linear_swiglu", n, k, bits, group_size)) return rc;
   if (m < 0) return fail(EDGERAG_EINVAL, "edgerag_quant_linear_swiglu: M < 0");
@@ -379,22 +407,25 @@ extern "C" int edgerag_quant_linear_swiglu(const void* x, int32_t x_dtype, int64
                 "edgerag_quant_linear_swiglu: shape not covered (dtype %d, M %d, K %d, N %d, "
                 "bits %d, group %d); use edgerag_quant_linear + edgerag_silu_mul",
                 x_dtype, m, k, n, bits, group_size);
+  EpiArgs ea{};
+  if (int rc = set_norm("edgerag_quant_linear_swiglu", m, norm_partials, norm_parts, eps, ea))
+    return rc;
   launch_qlinear_swiglu(static_cast<const f16*>(x), x_stride, m, k, packed,
                         static_cast<const f16*>(scales_f16), static_cast<const f16*>(bias_f16), n,
-                        static_cast<f16*>(y), y_stride, static_cast<hipStream_t>(stream));
+                        static_cast<f16*>(y), y_stride, ea, static_cast<hipStream_t>(stream));
   return check_launch("edgerag_quant_linear_swiglu");
 }
 
 extern "C" int edgerag_quant_linear_rope_append_supported(int32_t x_dtype, int32_t m, int32_t k,
                                                          int32_t bits, int32_t group_size,
                                                          int32_t n_q_heads, int32_t n_kv_heads,
-                                                         int32_t head_dim) {
+                                                         int32_t head_dim, int32_t normed) {
   if (x_dtype != EDGERAG_F16 || n_q_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0 || k <= 0 ||
-      group_size != k)
+      group_size != k || (normed && m > 16))
     return 0;
   const int64_t heads = int64_t(n_q_heads) + 2 * int64_t(n_kv_heads);
   if (heads * head_dim > INT32_MAX) return 0;
-  const void* aligned = reinterpret_cast<const void*>(uintptr_t(256));
+  const void* aligned = aligned_stand_in();
   return qlinear_rope_supported(m, k, int32_t(heads * head_dim), bits, group_size, int32_t(heads),
                                 head_dim, aligned, k, aligned)
              ? 1
@@ -406,7 +437,8 @@ extern "C" int edgerag_quant_linear_rope_append(
     const void* scales_f16, const void* bias_f16, int32_t bits, int32_t group_size,
     const void* cos_tok, const void* sin_tok, int32_t n_q_heads, int32_t n_kv_heads,
     int32_t head_dim, void* q_out, int64_t q_stride_tok, const int32_t* slots, void* key_pool,
-    void* value_pool, int32_t num_blocks, int32_t block_size, void* stream) {
+    void* value_pool, int32_t num_blocks, int32_t block_size, const float* norm_partials,
+    int32_t norm_parts, float eps, void* stream) {
   clear_error();
   if (m < 0 || n_q_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0 || head_dim % 2 ||
       num_blocks <= 0 || block_size <= 0)
@@ -433,6 +465,9 @@ extern "C" int edgerag_quant_linear_rope_append(
                 "bits %d, group %d, head_dim %d); use edgerag_quant_linear + edgerag_rope_append",
                 x_dtype, m, k, n, bits, group_size, head_dim);
   EpiArgs ea{};
+  if (int rc = set_norm("edgerag_quant_linear_rope_append", m, norm_partials, norm_parts, eps,
+                        ea))
+    return rc;
   ea.cos_tok = static_cast<const f16*>(cos_tok);
   ea.sin_tok = static_cast<const f16*>(sin_tok);
   ea.slots = slots;
@@ -449,4 +484,60 @@ extern "C" int edgerag_quant_linear_rope_append(
                       static_cast<const f16*>(scales_f16), static_cast<const f16*>(bias_f16), n, ea,
                       static_cast<hipStream_t>(stream));
   return check_launch("edgerag_quant_linear_rope_append");
+}
+
+extern "C" int edgerag_quant_linear_residual_parts(int32_t x_dtype, int32_t m, int32_t k, int32_t n,
+                                                   int32_t bits, int32_t group_size) {
+  if (x_dtype != EDGERAG_F16 || m < 1 || k <= 0 || n <= 0) return 0;
+  const void* aligned = aligned_stand_in();
+  return qlinear_residual_parts(m, k, n, bits, group_size, aligned, k, aligned);
+}
+
+extern "C" int edgerag_quant_linear_residual(const void* x, int32_t x_dtype, int64_t x_stride,
+                                             int32_t m, int32_t k, const uint8_t* packed,
+                                             const void* scales_f16, const void* bias_f16,
+                                             int32_t n, int32_t bits, int32_t group_size,
+                                             void* hidden, int64_t hidden_stride, float* partials,
+                                             int64_t partials_capacity, int32_t* n_parts,
+                                             const void* next_norm_weight, void* xw,
+                                             int64_t xw_stride, void* stream) {
+  clear_error();
+  if (int rc = check_quant_shape("edgerag_quant_linear_residual", n, k, bits, group_size))
+    return rc;
+  if (m < 0) return fail(EDGERAG_EINVAL, "edgerag_quant_linear_residual: M < 0");
+  if (n_parts != nullptr) *n_parts = 0;
+  if (m == 0) return EDGERAG_OK;
+  if (x == nullptr || packed == nullptr || scales_f16 == nullptr || hidden == nullptr ||
+      partials == nullptr)
+    return fail(EDGERAG_EINVAL, "edgerag_quant_linear_residual: NULL pointer");
+  if (x_stride < k || hidden_stride < n)
+    return fail(EDGERAG_EINVAL, "edgerag_quant_linear_residual: row strides (%lld, %lld) below K/N",
+                (long long)x_stride, (long long)hidden_stride);
+  const int parts = x_dtype == EDGERAG_F16
+                        ? qlinear_residual_parts(m, k, n, bits, group_size, x, x_stride, packed)
+                        : 0;
+  if (parts == 0)
+    return fail(EDGERAG_EUNSUPPORTED,
+                "edgerag_quant_linear_residual: shape not covered (dtype %d, M %d, K %d, N %d, "
+                "bits %d, group %d); use edgerag_quant_linear + edgerag_rmsnorm",
+                x_dtype, m, k, n, bits, group_size);
+  if (partials_capacity < int64_t(m) * parts)
+    return fail(EDGERAG_EWORKSPACE, "edgerag_quant_linear_residual: partials hold %lld floats, need %lld",
+                (long long)partials_capacity, (long long)(int64_t(m) * parts));
+  if ((next_norm_weight == nullptr) != (xw == nullptr) || (xw != nullptr && xw_stride < n))
+    return fail(EDGERAG_EINVAL,
+                "edgerag_quant_linear_residual: next_norm_weight and xw go together (xw row stride "
+                ">= N)");
+  EpiArgs ea{};
+  ea.hidden = static_cast<f16*>(hidden);
+  ea.hid_st = hidden_stride;
+  ea.part = partials;
+  ea.next_w = static_cast<const f16*>(next_norm_weight);
+  ea.xw = static_cast<f16*>(xw);
+  ea.xw_st = xw_stride;
+  launch_qlinear_residual(static_cast<const f16*>(x), x_stride, m, k, packed,
+                          static_cast<const f16*>(scales_f16), static_cast<const f16*>(bias_f16), n,
+                          ea, static_cast<hipStream_t>(stream));
+  if (n_parts != nullptr) *n_parts = parts;
+  return check_launch("edgerag_quant_linear_residual");
 }

@@ -18,7 +18,7 @@ void launch_qlinear_mfma(const f16* x, int64_t xs, int32_t m, int32_t k, const u
                          const f16* scales, const f16* bias, int32_t n, int32_t bits, int32_t g,
                          f16* y, int64_t ys, hipStream_t s);
 
-// Operands of the fused RoPE + KV-append epilogue (unused by the other epilogues).
+// Operands of the fused epilogues and of normed inputs (zero when unused).
 struct EpiArgs {
   const f16* cos_tok;    // [m, head_dim]: cos table row at each token's position
   const f16* sin_tok;    // [m, head_dim]
@@ -28,7 +28,25 @@ struct EpiArgs {
   f16* kpool;  // head-major [n_kv_heads, num_blocks, block_size, head_dim]
   f16* vpool;
   int32_t num_blocks, block_size, n_q_heads, n_kv_heads, head_dim;
+  // Residual epilogue (the projection feeding a residual add + RMSNorm): hidden[t][n] =
+  // fp16(hidden[t][n] + y[t][n]) in place, part[t * grid + workgroup] = the sum of the new values
+  // squared over the workgroup's rows (fp32, a fixed order), and, when xw != NULL,
+  // xw[t][n] = fp16(next_w[n] * hidden[t][n]): the next RMSNorm's weight applied, its 1 / rms not.
+  f16* hidden;
+  int64_t hid_st;
+  float* part;
+  const f16* next_w;
+  f16* xw;
+  int64_t xw_st;
+  // Normed input (a projection after RMSNorm, x = a residual producer's xw): r_t =
+  // rsqrt(sum of norm_part[t][0, norm_parts) / K + eps) multiplies token t's fp32 sums.
+  const float* norm_part;
+  int32_t norm_parts;
+  float eps;
 };
+
+// Partial sums per token a normed launch can read (norm_parts).
+constexpr int kNormMaxParts = 256;
 
 // RoPE + KV-append form for decode batches: W is the fused [q heads | k heads | v heads]
 // projection (N = heads * head_dim rows, INT8 per-channel); q heads are rotated into q_out, k
@@ -51,6 +69,15 @@ bool qlinear_swiglu_supported(int32_t m, int32_t k, int32_t n, int32_t bits, int
                               const void* x, int64_t x_stride, const void* packed);
 void launch_qlinear_swiglu(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
                            const f16* scales, const f16* bias, int32_t n, f16* y, int64_t ys,
-                           hipStream_t s);
+                           const EpiArgs& ea, hipStream_t s);
+
+// Residual form for decode batches (M <= 16, INT8 per-channel): the plain launch's y is added to
+// ea.hidden in place and per-(token, workgroup) sums of squares go to ea.part. Returns the number
+// of partial sums per token (workgroups) for the shape, 0 when it is not covered.
+int qlinear_residual_parts(int32_t m, int32_t k, int32_t n, int32_t bits, int32_t g,
+                           const void* x, int64_t x_stride, const void* packed);
+void launch_qlinear_residual(const f16* x, int64_t xs, int32_t m, int32_t k,
+                             const uint8_t* packed, const f16* scales, const f16* bias, int32_t n,
+                             const EpiArgs& ea, hipStream_t s);
 
 }  // namespace edgerag

@@ -324,10 +324,37 @@ __global__ __launch_bounds__(KWMAX * kWave) void qlinear_skinny_kernel(
 //   and the two row tiles are the two halves of one head (rows head D + tn D / 2 + j + [0, 16)),
 //   so every rotate_half pair (d, d + D / 2) sits in one wave; q heads are rotated into q_out, k
 //   heads rotated and v heads copied into the paged pools at the token's slot.
+// * kEpiResidual: hidden[t][n] = fp16(hidden[t][n] + y[t][n]) in place (y itself is not written),
+//   optionally xw[t][n] = fp16(w[n] * hidden[t][n]) with the next RMSNorm's weight w, plus one fp32
+//   sum of squares of the new values per (token, workgroup): the partials a normed launch turns
+//   into the RMSNorm factor, so that residual add + RMSNorm need no launch of their own and no
+//   workgroup waits for another.
 // The fp16 projection values the epilogues start from are the ones the plain launch of the same
 // shape writes: the host gives the fused launches the same waves, batches and k-slices, so the
 // summation order, and so the bits, are the same.
-constexpr int kEpiPlain = 0, kEpiSwiglu = 1, kEpiRope = 2;
+// NORM (with kEpiSwiglu / kEpiRope): the activation is a residual producer's xw = fp16(w * h) and
+// the projection is of RMSNorm(h) = fp16(w * fp16(h * r)); computed as r * sum(code * xw) with r
+// applied to the fp32 sum (one fp16 rounding moved, within the linear tolerance of the reference).
+constexpr int kEpiPlain = 0, kEpiSwiglu = 1, kEpiRope = 2, kEpiResidual = 3;
+
+// Sum of v over aligned groups of G lanes (G = 8, 16, 32 or 64), in the same order on every lane
+// of a group (so every lane gets the same bits): DPP adds within a 16-lane row (mirror pairs, then
+// the two lanes of each pair of quads), cross-row shuffles only above 16.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int G>
+__device__ __forceinline__ float lane_group_sum(float v) {
+  static_assert(G == 8 || G == 16 || G == 32 || G == 64, "lane group");
+  if constexpr (G >= 16) v += dpp_f<0x140>(v);  // row_mirror: lane i + lane 15 - i
+  v += dpp_f<0x141>(v);                          // row_half_mirror: i + 7 - i within 8
+  v += dpp_f<0x4E>(v);                           // quad_perm [2, 3, 0, 1]
+  v += dpp_f<0xB1>(v);                           // quad_perm [1, 0, 3, 2]
+  if constexpr (G >= 32) v += __shfl_xor(v, 16, kWave);
+  if constexpr (G >= 64) v += __shfl_xor(v, 32, kWave);
+  return v;
+}
 
 // The reference's rotate_half RoPE on one element (fp16 ops, each product rounded before the add):
 // first half: x1 cos - x2 sin; second half: x2 cos + x1 sin (x1 = element d, x2 = element d + D/2).
@@ -338,7 +365,7 @@ __device__ __forceinline__ f16 rope_elem(float own, float partner, bool second, 
   return __float2half_rn(a + b);
 }
 
-template <int F, int NT, int MT, int KW, int U, bool EXACT, int EPI>
+template <int F, int NT, int MT, int KW, int U, bool EXACT, int EPI, bool NORM>
 __global__ __launch_bounds__(KW * kWave)
 __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlinear_stream_kernel(
     const f16* __restrict__ x, int64_t xs, int32_t m, int32_t k,
@@ -349,10 +376,15 @@ __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlin
   constexpr int OUTS = NT * MT * R * R;    // outputs (token, row) of a workgroup
   constexpr int NO = (OUTS + KW * kWave - 1) / (KW * kWave);  // outputs per thread
   static_assert((KW * kWave) % (NT * R) == 0, "a thread's outputs share one weight row");
-  static_assert(EPI == kEpiPlain || (NT == 2 && kWave % (NT * R) == 0),
+  static_assert(EPI == kEpiPlain || EPI == kEpiResidual || (NT == 2 && kWave % (NT * R) == 0),
                 "paired epilogues pair tile 0 with tile 1 inside one wave");
   static_assert(EPI != kEpiRope || F == 1, "RoPE pairs 16-row tiles");
+  static_assert(EPI != kEpiResidual || kWave % (NT * R) == 0, "a token's rows share one wave");
+  static_assert(!NORM || ((EPI == kEpiSwiglu || EPI == kEpiRope) && F == 1), "normed inputs");
+  constexpr int NPQ = kNormMaxParts / kWave;           // partials per lane and token
+  constexpr int TOKW = NORM ? (MT * R + KW - 1) / KW : 1;  // tokens whose factor a wave sums
   __shared__ float red[KW * NT * MT * 4 * kWave];
+  __shared__ float rnorm[NORM ? MT * R : 1];
   const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63;
   const int li = lane & 15, lg = lane >> 4;
@@ -370,7 +402,7 @@ __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlin
   // Weight row of lane row rr in tile tn. Rows past N (past I in a SwiGLU half) re-read the last
   // row: they only feed D rows that are never read. (kEpiRope launches cover N exactly.)
   auto wrow = [&](int tn, int rr) {
-    if constexpr (EPI == kEpiPlain) return min(n0 + tn * R + rr, n - 1);
+    if constexpr (EPI == kEpiPlain || EPI == kEpiResidual) return min(n0 + tn * R + rr, n - 1);
     else if constexpr (EPI == kEpiSwiglu) return min(n0 + rr, half - 1) + tn * half;
     else return n0 + tn * half + rr;
   };
@@ -413,6 +445,34 @@ __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlin
       rope_slot[o] = ea.slots[tok];
       rope_c[o] = cos_u[int64_t(tok) * ea.head_dim + e_d];
       rope_s[o] = sin_u[int64_t(tok) * ea.head_dim + e_d];
+    }
+  }
+  // kEpiResidual: the residual-stream value of each output. NORM: wave w sums the partials of
+  // tokens w, w + KW, ..., lane l those with index l + 64 q (clamped; masked when summed).
+  uint32_t hid_pre[EPI == kEpiResidual ? NO : 1];
+  uint32_t nw_pre = 0;  // kEpiResidual with xw: the next norm's weight at this thread's row
+  float norm_pre[NORM ? TOKW * NPQ : 1];
+  if constexpr (EPI == kEpiResidual) {
+    const uint16_t* hid_u = reinterpret_cast<const uint16_t*>(ea.hidden);
+#pragma unroll
+    for (int o = 0; o < NO; ++o) {
+      const int tok = min((int(threadIdx.x) + o * KW * kWave) / (NT * R), m - 1);
+      hid_pre[o] = hid_u[int64_t(tok) * ea.hid_st + e_row];
+    }
+    // Loaded unconditionally (from the hidden row when there is no xw) so no branch sits
+    // between these loads and the batch loads.
+    const uint16_t* nw_u = reinterpret_cast<const uint16_t*>(ea.next_w != nullptr ? ea.next_w
+                                                                                  : ea.hidden);
+    nw_pre = nw_u[e_row];
+  }
+  if constexpr (NORM) {
+#pragma unroll
+    for (int j = 0; j < TOKW; ++j) {
+      const int tok = min(wave + KW * j, m - 1);
+#pragma unroll
+      for (int q = 0; q < NPQ; ++q)
+        norm_pre[j * NPQ + q] =
+            ea.norm_part[int64_t(tok) * ea.norm_parts + min(lane + kWave * q, ea.norm_parts - 1)];
     }
   }
 
@@ -473,6 +533,15 @@ __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlin
         for (int o = 0; o < NO; ++o)
           asm volatile("" : "+v"(rope_slot[o]), "+v"(rope_c[o]), "+v"(rope_s[o]));
       }
+      if constexpr (EPI == kEpiResidual) {
+#pragma unroll
+        for (int o = 0; o < NO; ++o) asm volatile("" : "+v"(hid_pre[o]));
+        asm volatile("" : "+v"(nw_pre));
+      }
+      if constexpr (NORM) {
+#pragma unroll
+        for (int i = 0; i < TOKW * NPQ; ++i) asm volatile("" : "+v"(norm_pre[i]));
+      }
     }
   }
 
@@ -485,6 +554,28 @@ __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlin
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         red[(((wave * NT + tn) * MT + t) * 4 + i) * kWave + lane] = acc[tn][t][i];
+  if constexpr (NORM) {
+    // r_t = rsqrt(mean(h^2) + eps) from the producer's partials, summed in a fixed order (per
+    // lane, then lane_group_sum), so every workgroup derives the same bits.
+    float sq[TOKW];
+#pragma unroll
+    for (int j = 0; j < TOKW; ++j) {  // the tokens' reductions interleave
+      sq[j] = 0.f;
+#pragma unroll
+      for (int q = 0; q < NPQ; ++q) {
+        float v = norm_pre[j * NPQ + q];
+        asm volatile("" : "+v"(v));
+        sq[j] += lane + kWave * q < ea.norm_parts ? v : 0.f;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < TOKW; ++j) sq[j] = lane_group_sum<kWave>(sq[j]);
+#pragma unroll
+    for (int j = 0; j < TOKW; ++j) {
+      const int tok = wave + KW * j;  // wave-uniform
+      if (tok < MT * R && lane == 0) rnorm[tok] = rsqrtf(sq[j] / float(k) + ea.eps);
+    }
+  }
   __syncthreads();
   // (Consumed again here so that the conversions below are not hoisted above the main loop,
   // which would wait for the loads before the first batch is issued.)
@@ -503,7 +594,8 @@ __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlin
       for (int wv = 0; wv < KW; ++wv)
         sum += red[(((wv * NT + tn) * MT + t) * 4 + i) * kWave + l];
     }
-    return __float2half_rn(__builtin_fmaf(scale, sum, bv));
+    const float sc = NORM ? scale * rnorm[tok] : scale;
+    return __float2half_rn(__builtin_fmaf(sc, sum, bv));
   };
   if constexpr (EPI == kEpiPlain) {
     for (int e = threadIdx.x; e < OUTS; e += KW * kWave) {
@@ -511,6 +603,30 @@ __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlin
       const int nrow = n0 + row_in;
       if (tok >= m || nrow >= n) continue;
       y[int64_t(tok) * ys + nrow] = out_sum(tok, row_in / R, row_in % R);
+    }
+  } else if constexpr (EPI == kEpiResidual) {
+    // h = fp16(hidden + y); the NT R lanes of one token (consecutive, aligned) then sum their h^2,
+    // and the token's first lane writes the workgroup's partial.
+#pragma unroll
+    for (int o = 0; o < NO; ++o) {
+      const int e = int(threadIdx.x) + o * KW * kWave;
+      if (e >= OUTS) break;  // uniform per wave
+      const int tok = e / (NT * R), row_in = e % (NT * R);
+      const int nrow = n0 + row_in;
+      const bool ok = tok < m && nrow < n;
+      float sq = 0.f;
+      if (ok) {
+        const float hv = __half2float(__builtin_bit_cast(f16, uint16_t(hid_pre[o])));
+        const f16 h = __float2half_rn(hv + __half2float(out_sum(tok, row_in / R, row_in % R)));
+        ea.hidden[int64_t(tok) * ea.hid_st + nrow] = h;
+        const float hf = __half2float(h);
+        sq = hf * hf;
+        if (ea.xw != nullptr)  // w * h is exact in fp32 (two fp16 factors): one rounding
+          ea.xw[int64_t(tok) * ea.xw_st + nrow] =
+              __float2half_rn(__half2float(__builtin_bit_cast(f16, uint16_t(nw_pre))) * hf);
+      }
+      sq = lane_group_sum<NT * R>(sq);
+      if (row_in == 0 && tok < m) ea.part[int64_t(tok) * gridDim.x + blockIdx.x] = sq;
     }
   } else if constexpr (EPI == kEpiSwiglu) {
     // The up output of gate lane l sits in lane l + R of the same wave (same token, tile 1). OUTS
@@ -886,7 +1002,7 @@ void launch_gemm(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* 
 // steps per batch U from K alone, so that a row's summation order, and so its bits, do not depend
 // on M or on the other rows of the launch. Returns false when the shape does not fit (the caller
 // then uses the skinny kernel).
-template <int F, int NT, int MT, int KW, int U, int EPI>
+template <int F, int NT, int MT, int KW, int U, int EPI, bool NORM>
 void launch_stream(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
                    const f16* scales, const f16* bias, int32_t n, f16* y, int64_t ys,
                    const EpiArgs& ea, hipStream_t s) {
@@ -897,10 +1013,10 @@ void launch_stream(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t
                           : EPI == kEpiRope ? unsigned(n / 32)
                                             : unsigned((n + rows - 1) / rows);
   if ((k / (64 * F)) % (KW * U) == 0)
-    hipLaunchKernelGGL((qlinear_stream_kernel<F, NT, MT, KW, U, true, EPI>), dim3(blocks),
+    hipLaunchKernelGGL((qlinear_stream_kernel<F, NT, MT, KW, U, true, EPI, NORM>), dim3(blocks),
                        dim3(KW * kWave), 0, s, x, xs, m, k, packed, scales, bias, n, y, ys, ea);
   else
-    hipLaunchKernelGGL((qlinear_stream_kernel<F, NT, MT, KW, U, false, EPI>), dim3(blocks),
+    hipLaunchKernelGGL((qlinear_stream_kernel<F, NT, MT, KW, U, false, EPI, NORM>), dim3(blocks),
                        dim3(KW * kWave), 0, s, x, xs, m, k, packed, scales, bias, n, y, ys, ea);
 }
 
@@ -925,7 +1041,7 @@ StreamWaves stream_waves(int f, int nt, int mt, int k) {
 }
 
 // Launches the shape with the given waves (KW in {4, 8, 16}) and batch (U in {4, 8}).
-template <int F, int NT, int MT, int EPI>
+template <int F, int NT, int MT, int EPI, bool NORM = false>
 void launch_stream_w(StreamWaves sw, const f16* x, int64_t xs, int32_t m, int32_t k,
                      const uint8_t* packed, const f16* scales, const f16* bias, int32_t n, f16* y,
                      int64_t ys, const EpiArgs& ea, hipStream_t s) {
@@ -933,12 +1049,13 @@ void launch_stream_w(StreamWaves sw, const f16* x, int64_t xs, int32_t m, int32_
   do {                                                                                         \
     if constexpr (MT == 1) {                                                                   \
       if (sw.u8) {                                                                             \
-        launch_stream<F, NT, MT, KW, 8, EPI>(x, xs, m, k, packed, scales, bias, n, y, ys, ea,  \
-                                             s);                                               \
+        launch_stream<F, NT, MT, KW, 8, EPI, NORM>(x, xs, m, k, packed, scales, bias, n, y, ys, \
+                                                   ea, s);                                     \
         return;                                                                                \
       }                                                                                        \
     }                                                                                          \
-    launch_stream<F, NT, MT, KW, 4, EPI>(x, xs, m, k, packed, scales, bias, n, y, ys, ea, s);  \
+    launch_stream<F, NT, MT, KW, 4, EPI, NORM>(x, xs, m, k, packed, scales, bias, n, y, ys, ea,  \
+                                               s);                                             \
     return;                                                                                    \
   } while (0)
   // Only the combinations stream_waves can pick are instantiated: 4 waves for one row tile (and
@@ -953,12 +1070,12 @@ void launch_stream_w(StreamWaves sw, const f16* x, int64_t xs, int32_t m, int32_
 #undef EDGERAG_STREAM
 }
 
-template <int F, int NT, int MT, int EPI = kEpiPlain>
+template <int F, int NT, int MT, int EPI = kEpiPlain, bool NORM = false>
 void launch_stream_k(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
                      const f16* scales, const f16* bias, int32_t n, f16* y, int64_t ys,
                      hipStream_t s, const EpiArgs& ea = EpiArgs{}) {
-  launch_stream_w<F, NT, MT, EPI>(stream_waves(F, NT, MT, k), x, xs, m, k, packed, scales, bias,
-                                  n, y, ys, ea, s);
+  launch_stream_w<F, NT, MT, EPI, NORM>(stream_waves(F, NT, MT, k), x, xs, m, k, packed, scales,
+                                        bias, n, y, ys, ea, s);
 }
 
 // The k-slices (1 or 2) dispatch_stream uses for (M, K, N), 0 when it does not take the shape:
@@ -1002,6 +1119,33 @@ bool dispatch_stream(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8
   return true;
 }
 
+// The residual-epilogue form of the plain launch for decode batches (M <= 16): same shapes, so the
+// same bits of y. Returns the number of workgroups (partial sums per token), 0 if not covered.
+int residual_parts(int32_t m, int32_t k, int32_t n) {
+  if (m > 16 || m > EDGERAG_STREAM_MAX_M) return 0;
+  const int slices = stream_slices(m, k, n);
+  if (slices == 0) return 0;
+  const int rows = slices == 2 ? 8 : ((int64_t(n) + 15) / 16 >= EDGERAG_STREAM_NT2_TILES ? 32 : 16);
+  return (n + rows - 1) / rows;
+}
+
+void dispatch_stream_residual(const f16* x, int64_t xs, int32_t m, int32_t k,
+                              const uint8_t* packed, const f16* scales, const f16* bias, int32_t n,
+                              const EpiArgs& ea, hipStream_t s) {
+  if (stream_slices(m, k, n) == 2) {
+    if (m <= 8)
+      launch_stream_k<2, 1, 1, kEpiResidual>(x, xs, m, k, packed, scales, bias, n, nullptr, 0, s,
+                                             ea);
+    else
+      launch_stream_k<2, 1, 2, kEpiResidual>(x, xs, m, k, packed, scales, bias, n, nullptr, 0, s,
+                                             ea);
+  } else if ((int64_t(n) + 15) / 16 >= EDGERAG_STREAM_NT2_TILES) {
+    launch_stream_k<1, 2, 1, kEpiResidual>(x, xs, m, k, packed, scales, bias, n, nullptr, 0, s, ea);
+  } else {
+    launch_stream_k<1, 1, 1, kEpiResidual>(x, xs, m, k, packed, scales, bias, n, nullptr, 0, s, ea);
+  }
+}
+
 // The streaming shapes with two row tiles of one k-slice: the only ones the SwiGLU form covers.
 // dispatch_stream picks exactly these for the same (M, K, N), so the fused launch computes the
 // same gate and up bits as the plain one.
@@ -1012,8 +1156,10 @@ bool stream_swiglu_shape(int32_t m, int32_t k, int32_t n) {
 
 void dispatch_stream_swiglu(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
                             const f16* scales, const f16* bias, int32_t n, f16* y, int64_t ys,
-                            hipStream_t s) {
-  if (m <= 16)
+                            const EpiArgs& ea, hipStream_t s) {
+  if (ea.norm_part != nullptr)  // normed input: decode batches of up to 16 tokens
+    launch_stream_k<1, 2, 1, kEpiSwiglu, true>(x, xs, m, k, packed, scales, bias, n, y, ys, s, ea);
+  else if (m <= 16)
     launch_stream_k<1, 2, 1, kEpiSwiglu>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
   else if (m <= 32)
     launch_stream_k<1, 2, 2, kEpiSwiglu>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
@@ -1085,13 +1231,13 @@ bool stream_rope_shape(int32_t m, int32_t k, int32_t n, int32_t heads, int32_t h
   return stream_waves(1, nt, mt, k).kw <= 8;
 }
 
-template <int MT>
+template <int MT, bool NORM = false>
 void launch_rope(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
                  const f16* scales, const f16* bias, int32_t n, const EpiArgs& ea,
                  hipStream_t s) {
   const int nt = (int64_t(n) + 15) / 16 >= EDGERAG_STREAM_NT2_TILES ? 2 : 1;
-  launch_stream_w<1, 2, MT, kEpiRope>(stream_waves(1, nt, MT, k), x, xs, m, k, packed, scales,
-                                      bias, n, nullptr, 0, ea, s);
+  launch_stream_w<1, 2, MT, kEpiRope, NORM>(stream_waves(1, nt, MT, k), x, xs, m, k, packed,
+                                            scales, bias, n, nullptr, 0, ea, s);
 }
 
 bool qlinear_rope_supported(int32_t m, int32_t k, int32_t n, int32_t bits, int32_t g,
@@ -1104,7 +1250,9 @@ bool qlinear_rope_supported(int32_t m, int32_t k, int32_t n, int32_t bits, int32
 void launch_qlinear_rope(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
                          const f16* scales, const f16* bias, int32_t n, const EpiArgs& ea,
                          hipStream_t s) {
-  if (m <= 16)
+  if (ea.norm_part != nullptr)  // normed input: decode batches of up to 16 tokens
+    launch_rope<1, true>(x, xs, m, k, packed, scales, bias, n, ea, s);
+  else if (m <= 16)
     launch_rope<1>(x, xs, m, k, packed, scales, bias, n, ea, s);
   else if (m <= 32)
     launch_rope<2>(x, xs, m, k, packed, scales, bias, n, ea, s);
@@ -1120,8 +1268,20 @@ bool qlinear_swiglu_supported(int32_t m, int32_t k, int32_t n, int32_t bits, int
 
 void launch_qlinear_swiglu(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
                            const f16* scales, const f16* bias, int32_t n, f16* y, int64_t ys,
-                           hipStream_t s) {
-  dispatch_stream_swiglu(x, xs, m, k, packed, scales, bias, n, y, ys, s);
+                           const EpiArgs& ea, hipStream_t s) {
+  dispatch_stream_swiglu(x, xs, m, k, packed, scales, bias, n, y, ys, ea, s);
+}
+
+int qlinear_residual_parts(int32_t m, int32_t k, int32_t n, int32_t bits, int32_t g,
+                           const void* x, int64_t x_stride, const void* packed) {
+  if (bits != 8 || g != k || !qlinear_mfma_supported(k, bits, g, x, x_stride, packed)) return 0;
+  return residual_parts(m, k, n);
+}
+
+void launch_qlinear_residual(const f16* x, int64_t xs, int32_t m, int32_t k,
+                             const uint8_t* packed, const f16* scales, const f16* bias, int32_t n,
+                             const EpiArgs& ea, hipStream_t s) {
+  dispatch_stream_residual(x, xs, m, k, packed, scales, bias, n, ea, s);
 }
 
 void launch_qlinear_mfma(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,

@@ -521,11 +521,78 @@ def rope_rows(positions: torch.Tensor, cos: torch.Tensor,
 
 
 def quant_rope_fused(m: int, k: int, bits: int, group_size: int, n_q_heads: int,
-                     n_kv_heads: int, head_dim: int, dtype: torch.dtype = torch.float16) -> bool:
+                     n_kv_heads: int, head_dim: int, dtype: torch.dtype = torch.float16,
+                     normed: bool = False) -> bool:
     """Whether ``quant_linear_rope_append`` runs as one launch (16-byte aligned rows)."""
     return bool(_lib.load().edgerag_quant_linear_rope_append_supported(
         dtype_code(dtype) if dtype in (torch.float16, torch.float32) else -1, m, k, bits,
-        group_size, n_q_heads, n_kv_heads, head_dim))
+        group_size, n_q_heads, n_kv_heads, head_dim, int(normed)))
+
+
+@dataclass
+class NormedInput:
+    """A projection input ``xw = fp16(w * h)`` written by ``quant_linear_residual`` (w: the norm
+    weight, h: the residual stream), plus the producer's per-(token, workgroup) sums of squares of
+    h and eps: the projection is then of RMSNorm(h)."""
+
+    partials: torch.Tensor
+    n_parts: int
+    eps: float
+
+    def args(self, m: int) -> tuple:
+        """The C arguments for an m-token input (shapes checked)."""
+        if self.partials.dtype != torch.float32 or self.partials.numel() < m * self.n_parts:
+            raise ValueError(f"partials must hold {m} x {self.n_parts} float32 sums")
+        return (self.partials.data_ptr(), self.n_parts, float(self.eps))
+
+
+_NO_NORM = (None, 0, 0.0)
+
+
+def quant_residual_parts(m: int, k: int, n: int, bits: int, group_size: int,
+                         dtype: torch.dtype = torch.float16) -> int:
+    """Partial sums per token ``quant_linear_residual`` writes for this shape; 0 if not covered."""
+    return int(_lib.load().edgerag_quant_linear_residual_parts(
+        dtype_code(dtype) if dtype in (torch.float16, torch.float32) else -1, m, k, n, bits,
+        group_size))
+
+
+def quant_linear_residual(
+    x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, bias: torch.Tensor | None,
+    in_features: int, out_features: int, bits: int, group_size: int, hidden: torch.Tensor,
+    partials: torch.Tensor, next_norm_weight: torch.Tensor | None = None,
+    xw: torch.Tensor | None = None,
+) -> int:
+    """``hidden += x . W^T`` in place (fp16) plus the per-(token, workgroup) sums of squares of
+    the new ``hidden`` rows in ``partials``, and ``xw = fp16(next_norm_weight * hidden)`` when
+    given (the input of the next normed projection); returns the sums' count per token. Decode
+    batches only (``quant_residual_parts`` > 0): raises otherwise."""
+    require_device(x, packed, scales, bias, hidden, partials, next_norm_weight, xw)
+    if (next_norm_weight is None) != (xw is None):
+        raise ValueError("next_norm_weight and xw go together")
+    if xw is not None and (xw.shape != hidden.shape or xw.stride(1) != 1 or
+                           xw.dtype != torch.float16 or next_norm_weight.shape != (out_features,)
+                           or next_norm_weight.dtype != torch.float16):
+        raise ValueError("xw must match hidden; next_norm_weight must be fp16 (out_features,)")
+    x2 = x.reshape(-1, in_features)
+    if x2.stride(1) != 1 or (x2.stride(0) * x2.element_size()) % 16 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    m = x2.shape[0]
+    if hidden.shape != (m, out_features) or hidden.stride(1) != 1 or hidden.dtype != torch.float16:
+        raise ValueError(f"hidden must be fp16 ({m}, {out_features}) with contiguous rows")
+    if partials.dtype != torch.float32 or not partials.is_contiguous():
+        raise ValueError("partials must be a contiguous float32 tensor")
+    if scales.dtype != torch.float16:
+        scales = scales.to(torch.float16)
+    n_parts = ctypes.c_int32(0)
+    call(
+        "edgerag_quant_linear_residual", x2.data_ptr(), dtype_code(x2.dtype), x2.stride(0), m,
+        in_features, packed.data_ptr(), scales.contiguous().data_ptr(), ptr(bias), out_features,
+        bits, group_size, hidden.data_ptr(), hidden.stride(0), partials.data_ptr(),
+        partials.numel(), ctypes.addressof(n_parts), ptr(next_norm_weight), ptr(xw),
+        xw.stride(0) if xw is not None else 0, stream_ptr(x.device),
+    )
+    return int(n_parts.value)
 
 
 def quant_linear_rope_append(
@@ -533,12 +600,14 @@ def quant_linear_rope_append(
     in_features: int, bits: int, group_size: int, positions: torch.Tensor, cos: torch.Tensor,
     sin: torch.Tensor, n_q_heads: int, n_kv_heads: int, head_dim: int, slots: torch.Tensor,
     key_pool: torch.Tensor, value_pool: torch.Tensor, q_out: torch.Tensor | None = None,
-    rows: tuple[torch.Tensor, torch.Tensor] | None = None,
+    rows: tuple[torch.Tensor, torch.Tensor] | None = None, norm: NormedInput | None = None,
 ) -> torch.Tensor:
     """The fused q/k/v quant linear, RoPE and KV append; returns q ``(T, n_q_heads, head_dim)``.
 
     One launch where the native library covers the shape and ``rows`` (``rope_rows`` of the
-    step) is given; otherwise ``quant_linear`` then ``rope_append``. Both give the same bits."""
+    step) is given; otherwise ``quant_linear`` then ``rope_append``. Both give the same bits.
+    ``norm``: x is a residual producer's ``xw`` and the projection is of RMSNorm of its residual
+    stream (one launch only)."""
     require_device(x, packed, scales, bias, positions, cos, sin, slots, key_pool, value_pool,
                    q_out)
     n = (n_q_heads + 2 * n_kv_heads) * head_dim
@@ -551,8 +620,11 @@ def quant_linear_rope_append(
     fused = (
         rows is not None and T > 0 and x2.dtype == torch.float16 and packed.data_ptr() % 16 == 0
         and key_pool.dtype == torch.float16 and slots.dtype == torch.int32
-        and quant_rope_fused(T, in_features, bits, group_size, n_q_heads, n_kv_heads, head_dim)
+        and quant_rope_fused(T, in_features, bits, group_size, n_q_heads, n_kv_heads, head_dim,
+                             normed=norm is not None)
     )
+    if norm is not None and not fused:
+        raise ValueError("a normed input needs the one-launch path (decode batch, rope rows)")
     if not fused:
         qkv = quant_linear(x2, packed, scales, bias, in_features, n, bits, group_size)
         return rope_append(qkv, positions, cos, sin, n_q_heads, n_kv_heads, head_dim, slots,
@@ -578,7 +650,8 @@ def quant_linear_rope_append(
         in_features, packed.data_ptr(), scales.contiguous().data_ptr(), ptr(bias), bits,
         group_size, cos_tok.data_ptr(), sin_tok.data_ptr(), n_q_heads, n_kv_heads, head_dim,
         q_out.data_ptr(), q_out.stride(0), slots.data_ptr(), key_pool.data_ptr(),
-        value_pool.data_ptr(), num_blocks, block_size, stream_ptr(x.device),
+        value_pool.data_ptr(), num_blocks, block_size,
+        *(norm.args(T) if norm is not None else _NO_NORM), stream_ptr(x.device),
     )
     return q_out
 
@@ -598,11 +671,11 @@ def silu_mul(gate_up: torch.Tensor, intermediate: int,
 
 
 def quant_swiglu_fused(m: int, k: int, n: int, bits: int, group_size: int,
-                       dtype: torch.dtype = torch.float16) -> bool:
+                       dtype: torch.dtype = torch.float16, normed: bool = False) -> bool:
     """Whether ``quant_linear_swiglu`` runs as one launch for this shape (16-byte aligned rows)."""
     return bool(_lib.load().edgerag_quant_linear_swiglu_supported(
         dtype_code(dtype) if dtype in (torch.float16, torch.float32) else -1, m, k, n, bits,
-        group_size))
+        group_size, int(normed)))
 
 
 def quant_linear_swiglu(
@@ -615,11 +688,14 @@ def quant_linear_swiglu(
     bits: int,
     group_size: int,
     out: torch.Tensor | None = None,
+    norm: NormedInput | None = None,
 ) -> torch.Tensor:
     """SwiGLU of the fused ``[gate; up]`` quant linear: ``x (T, K) -> (T, out_features / 2)``.
 
     One launch where the native library covers the shape (decode batches of INT8 per-channel
     weights); otherwise the projection and ``silu_mul`` as two launches. Both give the same bits.
+    ``norm``: x is a residual producer's ``xw`` and the projection is of RMSNorm of its residual
+    stream (one launch only).
     """
     require_device(x, packed, scales, bias, out)
     inter = out_features // 2
@@ -629,8 +705,12 @@ def quant_linear_swiglu(
     if x2.stride(1) != 1 or (x2.stride(0) * x2.element_size()) % 16 or x2.data_ptr() % 16:
         x2 = x2.contiguous()
     m = x2.shape[0]
-    if m == 0 or x2.dtype != torch.float16 or packed.data_ptr() % 16 or not quant_swiglu_fused(
-            m, in_features, out_features, bits, group_size):
+    fused = not (m == 0 or x2.dtype != torch.float16 or packed.data_ptr() % 16
+                 or not quant_swiglu_fused(m, in_features, out_features, bits, group_size,
+                                           normed=norm is not None))
+    if norm is not None and not fused:
+        raise ValueError("a normed input needs the one-launch path (decode batch)")
+    if not fused:
         gu = quant_linear(x2, packed, scales, bias, in_features, out_features, bits, group_size)
         return silu_mul(gu, inter, out=out)
     y = out if out is not None else torch.empty((m, inter), dtype=x.dtype, device=x.device)
@@ -643,7 +723,8 @@ def quant_linear_swiglu(
     call(
         "edgerag_quant_linear_swiglu", x2.data_ptr(), dtype_code(x2.dtype), x2.stride(0), m,
         in_features, packed.data_ptr(), scales.contiguous().data_ptr(), ptr(bias), out_features,
-        bits, group_size, y.data_ptr(), y.stride(0), stream_ptr(x.device),
+        bits, group_size, y.data_ptr(), y.stride(0),
+        *(norm.args(m) if norm is not None else _NO_NORM), stream_ptr(x.device),
     )
     return y
 

@@ -247,11 +247,12 @@ int edgerag_quant_linear(const void* x, int32_t x_dtype, int64_t x_stride, int32
 int edgerag_quant_linear_swiglu(const void* x, int32_t x_dtype, int64_t x_stride, int32_t m,
                                 int32_t k, const uint8_t* packed, const void* scales_f16,
                                 const void* bias_f16, int32_t n, int32_t bits, int32_t group_size,
-                                void* y, int64_t y_stride, void* stream);
+                                void* y, int64_t y_stride, const float* norm_partials,
+                                int32_t norm_parts, float eps, void* stream);
 /* 1 when edgerag_quant_linear_swiglu covers (x_dtype, M, K, N, bits, group_size) for 16-byte
- * aligned x rows and W, else 0. */
+ * aligned x rows and W (normed != 0: with a normed input), else 0. */
 int edgerag_quant_linear_swiglu_supported(int32_t x_dtype, int32_t m, int32_t k, int32_t n,
-                                          int32_t bits, int32_t group_size);
+                                          int32_t bits, int32_t group_size, int32_t normed);
 
 /*
  * The fused q/k/v quant linear followed by RoPE and the KV append, in one launch. W is the packed
@@ -276,11 +277,47 @@ int edgerag_quant_linear_rope_append(const void* x, int32_t x_dtype, int64_t x_s
                                      int32_t n_kv_heads, int32_t head_dim, void* q_out,
                                      int64_t q_stride_tok, const int32_t* slots, void* key_pool,
                                      void* value_pool, int32_t num_blocks, int32_t block_size,
+                                     const float* norm_partials, int32_t norm_parts, float eps,
                                      void* stream);
-/* 1 when edgerag_quant_linear_rope_append covers the shape for 16-byte aligned x rows and W. */
+/* 1 when edgerag_quant_linear_rope_append covers the shape for 16-byte aligned x rows and W
+ * (normed != 0: with a normed input). */
 int edgerag_quant_linear_rope_append_supported(int32_t x_dtype, int32_t m, int32_t k, int32_t bits,
                                                int32_t group_size, int32_t n_q_heads,
-                                               int32_t n_kv_heads, int32_t head_dim);
+                                               int32_t n_kv_heads, int32_t head_dim,
+                                               int32_t normed);
+
+/*
+ * Residual add + RMSNorm without launches of their own, for decode batches (M <= 16 tokens, fp16,
+ * INT8 per-channel W, the streaming shapes).
+ *
+ * edgerag_quant_linear_residual is the producer: it computes y = x . W^T (+ bias) exactly as
+ * edgerag_quant_linear would, but instead of writing y it adds it to the residual stream in place,
+ * hidden[t][j] = fp16(hidden[t][j] + y[t][j]), writes partials[t * P + p] = the fp32 sum of the
+ * new hidden values squared over the columns workgroup p owns, and, when next_norm_weight and xw
+ * are given, xw[t][j] = fp16(next_norm_weight[j] * hidden[t][j]) (row stride xw_stride). P (the
+ * workgroups, at most ceil(N / 8)) goes to *n_parts; partials must hold M * P floats.
+ * edgerag_quant_linear_residual_parts returns P for a shape, 0 when it is not covered.
+ *
+ * The consumer is edgerag_quant_linear_swiglu / edgerag_quant_linear_rope_append with
+ * norm_partials != NULL and x = the producer's xw: the projection is then of RMSNorm(hidden) with
+ * the weight given to the producer and variance sum_p partials[t][p] / K (summed in a fixed
+ * order, so every workgroup and every run gets the same factor). It is computed as
+ * r_t * sum_k code * xw[t][k], r_t = rsqrt(variance + eps) applied to the fp32 sum: the reference
+ * rounds hidden * r_t to fp16 before the weight multiply, so outputs agree within the linear
+ * tolerance, not bit for bit. norm_parts (P) must be at most 256; M at most 16.
+ *
+ * Replaces `hidden = hidden + out` + RMSNorm.forward between the projections of a decoder layer
+ * (edgerag/core/layers.py:40-47, :372-373) for the decode iteration.
+ */
+int edgerag_quant_linear_residual(const void* x, int32_t x_dtype, int64_t x_stride, int32_t m,
+                                  int32_t k, const uint8_t* packed, const void* scales_f16,
+                                  const void* bias_f16, int32_t n, int32_t bits,
+                                  int32_t group_size, void* hidden, int64_t hidden_stride,
+                                  float* partials, int64_t partials_capacity, int32_t* n_parts,
+                                  const void* next_norm_weight, void* xw, int64_t xw_stride,
+                                  void* stream);
+int edgerag_quant_linear_residual_parts(int32_t x_dtype, int32_t m, int32_t k, int32_t n,
+                                        int32_t bits, int32_t group_size);
 
 /* ==== Fused elementwise ops of a decoder layer ============================================ */
 

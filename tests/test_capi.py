@@ -39,19 +39,21 @@ def test_library_exports_every_declared_symbol() -> None:
 
 def test_swiglu_support_query() -> None:
     """The fused SwiGLU linear covers decode batches of wide INT8 per-channel [gate; up]
-    weights; the query answers without touching a GPU."""
+    weights (normed inputs up to 16 tokens); the query answers without touching a GPU."""
     q = _lib.load().edgerag_quant_linear_swiglu_supported
     F16, F32 = 1, 0
-    assert q(F16, 8, 2048, 16384, 8, 2048) == 1  # config 5's gate/up, a decode batch
-    assert q(F16, 64, 2048, 16384, 8, 2048) == 1
-    assert q(F16, 65, 2048, 16384, 8, 2048) == 0  # prefill-sized M
-    assert q(F16, 0, 2048, 16384, 8, 2048) == 0
-    assert q(F16, 8, 2048, 4096, 8, 2048) == 0  # one 16-row tile per workgroup
-    assert q(F16, 8, 2048, 16383, 8, 2048) == 0  # odd N: no [gate; up] split
-    assert q(F16, 8, 2048, 16384, 4, 128) == 0  # INT4
-    assert q(F16, 8, 2048, 16384, 8, 128) == 0  # grouped INT8
-    assert q(F32, 8, 2048, 16384, 8, 2048) == 0
-    assert q(F16, 8, 200, 16384, 8, 200) == 0  # K not a multiple of 64
+    assert q(F16, 8, 2048, 16384, 8, 2048, 0) == 1  # config 5's gate/up, a decode batch
+    assert q(F16, 8, 2048, 16384, 8, 2048, 1) == 1  # ... with the RMSNorm folded in
+    assert q(F16, 64, 2048, 16384, 8, 2048, 0) == 1
+    assert q(F16, 17, 2048, 16384, 8, 2048, 1) == 0  # normed: at most 16 tokens
+    assert q(F16, 65, 2048, 16384, 8, 2048, 0) == 0  # prefill-sized M
+    assert q(F16, 0, 2048, 16384, 8, 2048, 0) == 0
+    assert q(F16, 8, 2048, 4096, 8, 2048, 0) == 0  # one 16-row tile per workgroup
+    assert q(F16, 8, 2048, 16383, 8, 2048, 0) == 0  # odd N: no [gate; up] split
+    assert q(F16, 8, 2048, 16384, 4, 128, 0) == 0  # INT4
+    assert q(F16, 8, 2048, 16384, 8, 128, 0) == 0  # grouped INT8
+    assert q(F32, 8, 2048, 16384, 8, 2048, 0) == 0
+    assert q(F16, 8, 200, 16384, 8, 200, 0) == 0  # K not a multiple of 64
 
 
 def test_rope_append_support_query() -> None:
@@ -59,15 +61,31 @@ def test_rope_append_support_query() -> None:
     streams with one k-slice; the query answers without touching a GPU."""
     q = _lib.load().edgerag_quant_linear_rope_append_supported
     F16 = 1
-    assert q(F16, 8, 2048, 8, 2048, 32, 32, 64) == 1  # config 5's q/k/v, a decode batch
-    assert q(F16, 64, 2048, 8, 2048, 32, 8, 64) == 1  # GQA, N 3072: one k-slice from M > 32
-    assert q(F16, 8, 2048, 8, 2048, 32, 8, 64) == 0  # N 3072 at M <= 32: two k-slices
-    assert q(F16, 24, 2048, 8, 2048, 32, 8, 64) == 0
-    assert q(F16, 65, 2048, 8, 2048, 32, 32, 64) == 0
-    assert q(F16, 8, 2048, 8, 2048, 32, 32, 48) == 0  # head_dim not a multiple of 32
-    assert q(F16, 8, 2048, 4, 128, 32, 32, 64) == 0  # INT4
-    assert q(0, 8, 2048, 8, 2048, 32, 32, 64) == 0  # fp32 activations
-    assert q(F16, 8, 16384, 8, 16384, 32, 32, 64) == 0  # K needing 16 waves
+    assert q(F16, 8, 2048, 8, 2048, 32, 32, 64, 0) == 1  # config 5's q/k/v, a decode batch
+    assert q(F16, 8, 2048, 8, 2048, 32, 32, 64, 1) == 1  # ... with the RMSNorm folded in
+    assert q(F16, 20, 2048, 8, 2048, 32, 32, 64, 1) == 0  # normed: at most 16 tokens
+    assert q(F16, 64, 2048, 8, 2048, 32, 8, 64, 0) == 1  # GQA, N 3072: one k-slice from M > 32
+    assert q(F16, 8, 2048, 8, 2048, 32, 8, 64, 0) == 0  # N 3072 at M <= 32: two k-slices
+    assert q(F16, 24, 2048, 8, 2048, 32, 8, 64, 0) == 0
+    assert q(F16, 65, 2048, 8, 2048, 32, 32, 64, 0) == 0
+    assert q(F16, 8, 2048, 8, 2048, 32, 32, 48, 0) == 0  # head_dim not a multiple of 32
+    assert q(F16, 8, 2048, 4, 128, 32, 32, 64, 0) == 0  # INT4
+    assert q(0, 8, 2048, 8, 2048, 32, 32, 64, 0) == 0  # fp32 activations
+    assert q(F16, 8, 16384, 8, 16384, 32, 32, 64, 0) == 0  # K needing 16 waves
+
+
+def test_residual_parts_query() -> None:
+    """The residual-add producer covers decode batches (up to 16 tokens) of the streaming
+    shapes and reports how many partial sums per token it writes: one per workgroup."""
+    q = _lib.load().edgerag_quant_linear_residual_parts
+    F16 = 1
+    assert q(F16, 8, 2048, 2048, 8, 2048) == 256  # o_proj: 8-row tiles (two k-slices)
+    assert q(F16, 8, 8192, 2048, 8, 8192) == 256  # down_proj
+    assert q(F16, 1, 2048, 4096, 8, 2048) == 256  # 16-row tiles
+    assert q(F16, 16, 2048, 8192, 8, 2048) == 256  # two 16-row tiles per workgroup
+    assert q(F16, 17, 2048, 2048, 8, 2048) == 0  # more than 16 tokens
+    assert q(F16, 8, 2048, 2048, 4, 128) == 0  # INT4
+    assert q(0, 8, 2048, 2048, 8, 2048) == 0
 
 
 def test_validation_errors_come_back_as_messages() -> None:

@@ -264,8 +264,123 @@ def test_quant_linear_swiglu_falls_back_outside_its_shapes(device) -> None:
         assert torch.equal(y, kernels.silu_mul(gu, n // 2))
     with pytest.raises(kernels._lib.EdgeragError, match="not covered"):
         kernels.call("edgerag_quant_linear_swiglu", x.data_ptr(), 1, k, 4, k, pd.data_ptr(),
-                     sd.data_ptr(), None, n, 4, 128, y.data_ptr(), n // 2,
+                     sd.data_ptr(), None, n, 4, 128, y.data_ptr(), n // 2, None, 0, 0.0,
                      kernels.stream_ptr(x.device))
+
+
+@pytest.mark.parametrize("k,n", [(2048, 2048), (8192, 2048), (2048, 4096), (2048, 8192),
+                                 (640, 1004)])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_quant_linear_residual(device, k, n, with_bias) -> None:
+    """The residual producer (decode batches): hidden becomes fp16(hidden + y) bit for bit, with y
+    exactly the plain launch's output, xw = fp16(w * hidden) bit for bit, and the per-workgroup
+    partials sum to the new rows' sum of squares. Shapes cover 8-row tiles (two k-slices), 16-row and two-tile workgroups, and a last
+    workgroup with fewer rows than its tile (N 1004)."""
+    w = _weight(n, k, n * 3 + k)
+    cfg = oq.QuantConfig(k, 8)
+    packed, scales = oq.quantize_for_layer(w, cfg)
+    bias = (torch.randn(n, generator=seeded(n + 5)) * 0.1).half() if with_bias else None
+    pd, sd = packed.to(device), scales.to(device)
+    bd = bias.to(device) if bias is not None else None
+    for m in (1, 3, 8, 16):
+        parts = kernels.quant_residual_parts(m, k, n, 8, k)
+        assert parts > 0
+        g = seeded(m + k + n)
+        x = torch.randn(m, k, generator=g).half().to(device)
+        hidden0 = (torch.randn(m, n, generator=g) * 4).half()
+        y = kernels.quant_linear(x, pd, sd, bd, k, n, 8, k).cpu()
+        expected = (hidden0.float() + y.float()).half()
+        hidden = hidden0.to(device)
+        partials = torch.full((m * parts,), float("nan"), dtype=torch.float32, device=device)
+        nw = (1.0 + 0.3 * torch.randn(n, generator=g)).half()
+        xw = torch.full((m, n), float("nan"), dtype=torch.float16, device=device)
+        got = kernels.quant_linear_residual(x, pd, sd, bd, k, n, 8, k, hidden, partials,
+                                            nw.to(device), xw)
+        assert got == parts
+        assert torch.equal(hidden.cpu(), expected), f"M={m}: residual add differs"
+        assert torch.equal(xw.cpu(), (nw.float() * expected.float()).half())
+        ss = partials.view(m, parts).double().cpu().sum(1)
+        torch.testing.assert_close(ss, expected.double().pow(2).sum(1), rtol=1e-5, atol=1e-6)
+    assert kernels.quant_residual_parts(17, k, n, 8, k) == 0
+
+
+def _partials_of(h: torch.Tensor, parts: int) -> torch.Tensor:
+    """Sums of squares of h's rows over `parts` contiguous column ranges, (M * parts,) fp32."""
+    m, k = h.shape
+    edges = torch.linspace(0, k, parts + 1).round().long()
+    hf = h.float()
+    cols = [hf[:, int(edges[p]):int(edges[p + 1])].pow(2).sum(1) for p in range(parts)]
+    return torch.stack(cols, 1).reshape(-1).contiguous()
+
+
+@pytest.mark.parametrize("parts", [256, 250, 7])
+def test_quant_linear_normed_inputs(device, parts) -> None:
+    """Normed inputs (decode batches): the fused SwiGLU and q/k/v + RoPE launches given
+    xw = fp16(w * h) (the residual producer's output) and the partial sums of squares of h compute
+    the projection of RMSNorm(h) -- against the float64 oracle and against the two-launch path (rmsnorm kernel, then
+    the plain fused launch) within the linear tolerance. Partial counts: the producers' 256, and
+    counts that are not a multiple of the 64 lanes."""
+    from edgerag_amd.core.layers import RotaryTable
+    from oracle import model as om
+
+    k, eps = 2048, 1e-5
+    nw = (1.0 + 0.2 * torch.randn(k, generator=seeded(11))).half()
+    nwd = nw.to(device)
+    # SwiGLU: [gate; up] of 2 x 8192 rows.
+    n = 16384
+    wgu = _weight(n, k, 21)
+    cfg = oq.QuantConfig(k, 8)
+    packed, scales = oq.quantize_for_layer(wgu, cfg)
+    pd, sd = packed.to(device), scales.to(device)
+    for m in (1, 5, 8, 16):
+        h = (torch.randn(m, k, generator=seeded(m * 3 + parts)) * 3).half()
+        hd = h.to(device)
+        part = _partials_of(h, parts).to(device)
+        xw = (nw.float() * h.float()).half().to(device)  # what the residual producer writes
+        normed = kernels.NormedInput(part, parts, eps)
+        got = kernels.quant_linear_swiglu(xw, pd, sd, None, k, n, 8, k, norm=normed).float().cpu()
+        xn = om.rms_norm(h, nw, eps)
+        ref_gu = oq.quant_linear_reference(xn, packed, scales, None, k, cfg)
+        ref = torch.nn.functional.silu(ref_gu[:, : n // 2]) * ref_gu[:, n // 2 :]
+        two = kernels.quant_linear_swiglu(kernels.rmsnorm(hd, nwd, eps), pd, sd, None, k, n, 8,
+                                          k).float().cpu()
+        # silu(g) * u compounds the linear tolerance of g and u (|u| ~ 1 here). The fused path
+        # rounds fp16(w * h) where the reference rounds fp16(w * fp16(h * r)): one moved rounding,
+        # which may cost at most twice the two-launch path's error against float64.
+        err, err_two = (got - ref).abs(), (two - ref).abs()
+        assert float(err.max()) <= max(2 * float(err_two.max()), 4e-3), (
+            f"M={m}: max error {float(err.max()):.2e} (two-launch {float(err_two.max()):.2e})")
+        assert float(err.mean()) <= 2 * float(err_two.mean()) + 1e-6
+        torch.testing.assert_close(got, ref, rtol=1e-2, atol=4e-3)
+    # q/k/v + RoPE + KV append: 32 / 32 heads of 64.
+    n_q = n_kv = 32
+    d = 64
+    n = (n_q + 2 * n_kv) * d
+    wq = _weight(n, k, 23)
+    packed, scales = oq.quantize_for_layer(wq, cfg)
+    pd, sd = packed.to(device), scales.to(device)
+    table = RotaryTable(d, 130000.0, 8192, device, torch.float16)
+    bs, nb = 16, 32
+    for m in (1, 8, 16):
+        h = (torch.randn(m, k, generator=seeded(m * 5 + parts)) * 3).half()
+        hd = h.to(device)
+        part = _partials_of(h, parts).to(device)
+        xw = (nw.float() * h.float()).half().to(device)
+        positions = torch.arange(100, 100 + m, dtype=torch.int32).to(device)
+        slots = torch.randperm(nb * bs, generator=seeded(m))[:m].to(torch.int32).to(device)
+        rows = kernels.rope_rows(positions, table.cos, table.sin)
+        outs = []
+        for normed in (True, False):
+            kp = torch.zeros((n_kv, nb, bs, d), dtype=torch.float16, device=device)
+            vp = torch.zeros_like(kp)
+            xin = xw if normed else kernels.rmsnorm(hd, nwd, eps)
+            norm = kernels.NormedInput(part, parts, eps) if normed else None
+            q = kernels.quant_linear_rope_append(
+                xin, pd, sd, None, k, 8, k, positions, table.cos, table.sin, n_q, n_kv, d, slots,
+                kp, vp, rows=rows, norm=norm)
+            outs.append((q.float(), kp.float(), vp.float()))
+        for a, b in zip(outs[0], outs[1]):  # rotated q / k and v: linear outputs (|x| ~ 1)
+            torch.testing.assert_close(a, b, rtol=1e-2, atol=4e-3)
 
 
 @pytest.mark.parametrize("k", [640, 1152, 2048, 8192])
