@@ -138,7 +138,10 @@ struct QReg {
 // ---- fast decode kernel --------------------------------------------------------------------------
 // Requires block_size % TPW == 0 and at most kMaxSplitBlocks blocks per split (checked by the
 // launcher from the plan header).
-template <typename T, int D, int QR, int U>
+// APPEND: the step's own tokens (positions L - c .. L - 1 of each request) are read from the new
+// K/V rows instead of the pools, and the split that reads them also writes them to the pools at
+// their slots (kv_append fused in: no other wave reads those pool rows in this launch).
+template <typename T, int D, int QR, int U, bool APPEND>
 __global__ __launch_bounds__(kWave) void attn_decode_kernel(
     const T* __restrict__ q, int64_t q_st, int64_t q_sh, const T* __restrict__ kpool,
     const T* __restrict__ vpool, const int32_t* __restrict__ block_tables, int64_t bt_stride,
@@ -146,7 +149,9 @@ __global__ __launch_bounds__(kWave) void attn_decode_kernel(
     const int32_t* __restrict__ plan, int32_t item_base, int32_t limit_word, int32_t n_q_heads,
     int32_t n_kv_heads, int32_t num_blocks, int32_t block_size, float scale_log2,
     T* __restrict__ out, int64_t o_st, int64_t o_sh, float2* __restrict__ part_ml,
-    float* __restrict__ part_acc) {
+    float* __restrict__ part_acc, const T* __restrict__ nk, const T* __restrict__ nv,
+    int64_t n_st, int64_t n_sh, const int32_t* __restrict__ slots, T* __restrict__ kdst,
+    T* __restrict__ vdst) {
   using C = RowCfg<T, D>;
   constexpr int VEC = C::VEC, LPT = C::LPT, TPW = C::TPW, LOG_LPT = C::LOG_LPT;
   constexpr int STEP = TPW * U;
@@ -208,7 +213,19 @@ __global__ __launch_bounds__(kWave) void attn_decode_kernel(
         const bool live = first < ke;
         const int blk = __builtin_amdgcn_readlane(my_blk, live ? (first - kb) / block_size : 0);
         valid[u] = live && tok[u] < ke && blk >= 0;
-        if (valid[u]) {
+        const int i_new = tok[u] - (L - c);  // >= 0: one of this step's tokens
+        if (APPEND && valid[u] && i_new >= 0) {
+          const int64_t noff = int64_t(q0 + i_new) * n_st + int64_t(h) * n_sh + sub * VEC;
+          kr[u] = load16(nk + noff);
+          vr[u] = load16(nv + noff);
+          const int64_t slot = slots[q0 + i_new];
+          if (slot >= 0 && slot < int64_t(num_blocks) * block_size) {
+            const int64_t doff =
+                ((head_base + slot / block_size) * block_size + slot % block_size) * D + sub * VEC;
+            store16(kdst + doff, kr[u]);
+            store16(vdst + doff, vr[u]);
+          }
+        } else if (valid[u]) {
           const int64_t off =
               ((head_base + blk) * block_size + (tok[u] % block_size)) * D + sub * VEC;
           kr[u] = load16(kpool + off);
@@ -562,11 +579,22 @@ using Launch = AttnLaunch;
 
 template <typename T, int D, int QR, int U>
 void launch_decode(const Launch& a, int base, int count, int limit_word) {
-  hipLaunchKernelGGL((attn_decode_kernel<T, D, QR, U>), dim3(count), dim3(kWave), 0, a.s,
-                     static_cast<const T*>(a.q), a.q_st, a.q_sh, static_cast<const T*>(a.kp),
-                     static_cast<const T*>(a.vp), a.bt, a.bt_stride, a.qsl, a.ctx, a.plan, base,
-                     limit_word, a.hq, a.hkv, a.nb, a.bs, a.scale_log2, static_cast<T*>(a.out),
-                     a.o_st, a.o_sh, a.ml, a.pacc);
+  if (a.nk != nullptr)
+    hipLaunchKernelGGL((attn_decode_kernel<T, D, QR, U, true>), dim3(count), dim3(kWave), 0, a.s,
+                       static_cast<const T*>(a.q), a.q_st, a.q_sh, static_cast<const T*>(a.kp),
+                       static_cast<const T*>(a.vp), a.bt, a.bt_stride, a.qsl, a.ctx, a.plan, base,
+                       limit_word, a.hq, a.hkv, a.nb, a.bs, a.scale_log2,
+                       static_cast<T*>(a.out), a.o_st, a.o_sh, a.ml, a.pacc,
+                       static_cast<const T*>(a.nk), static_cast<const T*>(a.nv), a.n_st, a.n_sh,
+                       a.slots, static_cast<T*>(const_cast<void*>(a.kp)),
+                       static_cast<T*>(const_cast<void*>(a.vp)));
+  else
+    hipLaunchKernelGGL((attn_decode_kernel<T, D, QR, U, false>), dim3(count), dim3(kWave), 0,
+                       a.s, static_cast<const T*>(a.q), a.q_st, a.q_sh,
+                       static_cast<const T*>(a.kp), static_cast<const T*>(a.vp), a.bt,
+                       a.bt_stride, a.qsl, a.ctx, a.plan, base, limit_word, a.hq, a.hkv, a.nb,
+                       a.bs, a.scale_log2, static_cast<T*>(a.out), a.o_st, a.o_sh, a.ml, a.pacc,
+                       nullptr, nullptr, 0, 0, nullptr, nullptr, nullptr);
 }
 
 template <typename T, int D, int QR>
@@ -815,7 +843,27 @@ extern "C" int edgerag_attn_plan(const int32_t* query_start_loc, const int32_t* 
   return EDGERAG_OK;
 }
 
-extern "C" int edgerag_paged_attention(
+namespace edgerag {
+namespace {
+
+// The new K/V rows of an append fused into the decode rows.
+struct FusedAppend {
+  const void *k, *v;
+  int64_t st, sh;
+  const int32_t* slots;
+};
+
+// Whether the decode rows of this plan run on the fast decode kernel (the one that can fuse the
+// append): block_size a multiple of its tokens per load, splits within its block-id registers.
+bool fast_decode_rows(int32_t dtype, int32_t head_dim, int32_t block_size, const int32_t* ph) {
+  const int es = elem_size(dtype);
+  if (es == 0 || head_dim <= 0 || head_dim % (16 / es) != 0) return false;
+  const int lpt = head_dim / (16 / es);
+  if (lpt < 1 || lpt > kWave) return false;
+  return block_size % (kWave / lpt) == 0 && ph[H_MAX_SPLIT_BLOCKS] <= kMaxSplitBlocks;
+}
+
+int paged_attention_impl(
     const int32_t* plan_host, const int32_t* plan_dev, int64_t plan_words, const void* q,
     int64_t q_stride_tok, int64_t q_stride_head, const void* key_pool, const void* value_pool,
     int32_t dtype, const int32_t* block_tables, int64_t block_tables_stride,
@@ -823,8 +871,7 @@ extern "C" int edgerag_paged_attention(
     int32_t num_tokens, int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
     int32_t block_size, int32_t num_blocks, float scale, void* out, int64_t out_stride_tok,
     int64_t out_stride_head, void* workspace, int64_t workspace_bytes, int32_t parts,
-    void* stream) {
-  clear_error();
+    void* stream, const FusedAppend* app) {
   if (parts <= 0 || (parts & ~(EDGERAG_ATTN_ALL | EDGERAG_ATTN_TILES_SHARED)) != 0 ||
       (parts & EDGERAG_ATTN_ALL) == 0)
     return fail(EDGERAG_EINVAL, "edgerag_paged_attention: parts mask %d", parts);
@@ -879,6 +926,13 @@ extern "C" int edgerag_paged_attention(
   char* wsp = static_cast<char*>(workspace);
   a.ml = reinterpret_cast<float2*>(wsp);
   a.pacc = reinterpret_cast<float*>(wsp + ws.acc_off);
+  if (app != nullptr) {
+    a.nk = app->k;
+    a.nv = app->v;
+    a.n_st = app->st;
+    a.n_sh = app->sh;
+    a.slots = app->slots;
+  }
   int rc = EDGERAG_OK;
   switch (dtype) {
     case EDGERAG_F32: rc = run_dtype<float>(a, plan_host, head_dim, parts); break;
@@ -901,6 +955,71 @@ extern "C" int edgerag_paged_attention(
   }
   if (rc != EDGERAG_OK) return rc;
   return check_launch("edgerag_paged_attention(combine)");
+}
+
+}  // namespace
+}  // namespace edgerag
+
+extern "C" int edgerag_paged_attention(
+    const int32_t* plan_host, const int32_t* plan_dev, int64_t plan_words, const void* q,
+    int64_t q_stride_tok, int64_t q_stride_head, const void* key_pool, const void* value_pool,
+    int32_t dtype, const int32_t* block_tables, int64_t block_tables_stride,
+    const int32_t* query_start_loc, const int32_t* context_lens, int32_t num_reqs,
+    int32_t num_tokens, int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+    int32_t block_size, int32_t num_blocks, float scale, void* out, int64_t out_stride_tok,
+    int64_t out_stride_head, void* workspace, int64_t workspace_bytes, int32_t parts,
+    void* stream) {
+  clear_error();
+  return paged_attention_impl(plan_host, plan_dev, plan_words, q, q_stride_tok, q_stride_head,
+                              key_pool, value_pool, dtype, block_tables, block_tables_stride,
+                              query_start_loc, context_lens, num_reqs, num_tokens, n_q_heads,
+                              n_kv_heads, head_dim, block_size, num_blocks, scale, out,
+                              out_stride_tok, out_stride_head, workspace, workspace_bytes, parts,
+                              stream, nullptr);
+}
+
+extern "C" int edgerag_paged_attention_append(
+    const void* new_key, const void* new_value, int32_t new_dtype, int64_t new_stride_tok,
+    int64_t new_stride_head, const int32_t* slot_mapping, const int32_t* plan_host,
+    const int32_t* plan_dev, int64_t plan_words, const void* q, int64_t q_stride_tok,
+    int64_t q_stride_head, void* key_pool, void* value_pool, int32_t dtype,
+    const int32_t* block_tables, int64_t block_tables_stride, const int32_t* query_start_loc,
+    const int32_t* context_lens, int32_t num_reqs, int32_t num_tokens, int32_t n_q_heads,
+    int32_t n_kv_heads, int32_t head_dim, int32_t block_size, int32_t num_blocks, float scale,
+    void* out, int64_t out_stride_tok, int64_t out_stride_head, void* workspace,
+    int64_t workspace_bytes, void* stream) {
+  clear_error();
+  if (new_key == nullptr || new_value == nullptr || slot_mapping == nullptr)
+    return fail(EDGERAG_EINVAL, "edgerag_paged_attention_append: NULL new K/V or slot mapping");
+  if (plan_host == nullptr || plan_words < kHeaderWords || plan_host[H_MAGIC] != kPlanMagic)
+    return fail(EDGERAG_EINVAL, "edgerag_paged_attention_append: not a plan from edgerag_attn_plan");
+  const int es = elem_size(dtype);
+  // One launch when every item is a decode row on the fast decode kernel and the new rows are
+  // in the pool dtype, 16-byte aligned; otherwise the append, then the attention.
+  const bool fused = plan_host[H_N_ITEMS] == plan_host[H_N_ROW_ITEMS] && new_dtype == dtype &&
+                     es > 0 && aligned16(new_key) && aligned16(new_value) &&
+                     (new_stride_tok * es) % 16 == 0 && (new_stride_head * es) % 16 == 0 &&
+                     fast_decode_rows(dtype, head_dim, block_size, plan_host);
+  if (!fused) {
+    const int32_t n_new = num_reqs > 0 ? plan_host[H_NUM_TOKENS_HINT] : 0;
+    if (int rc = edgerag_kv_append(new_key, new_value, new_dtype, new_stride_tok,
+                                   new_stride_head, slot_mapping, n_new, key_pool, value_pool,
+                                   dtype, n_kv_heads, num_blocks, block_size, head_dim, stream))
+      return rc;
+    return paged_attention_impl(plan_host, plan_dev, plan_words, q, q_stride_tok, q_stride_head,
+                                key_pool, value_pool, dtype, block_tables, block_tables_stride,
+                                query_start_loc, context_lens, num_reqs, num_tokens, n_q_heads,
+                                n_kv_heads, head_dim, block_size, num_blocks, scale, out,
+                                out_stride_tok, out_stride_head, workspace, workspace_bytes,
+                                EDGERAG_ATTN_ALL, stream, nullptr);
+  }
+  const FusedAppend app{new_key, new_value, new_stride_tok, new_stride_head, slot_mapping};
+  return paged_attention_impl(plan_host, plan_dev, plan_words, q, q_stride_tok, q_stride_head,
+                              key_pool, value_pool, dtype, block_tables, block_tables_stride,
+                              query_start_loc, context_lens, num_reqs, num_tokens, n_q_heads,
+                              n_kv_heads, head_dim, block_size, num_blocks, scale, out,
+                              out_stride_tok, out_stride_head, workspace, workspace_bytes,
+                              EDGERAG_ATTN_ALL, stream, &app);
 }
 
 namespace edgerag {

@@ -57,6 +57,11 @@ struct AttnLaunch {
   int64_t o_st, o_sh;
   float2* ml;
   float* pacc;
+  // Append fused into the decode rows (nk == NULL: off): the step's new K/V rows, [tokens,
+  // n_kv_heads, head_dim] at nk + t * n_st + h * n_sh, written to the pools at slots[t].
+  const void *nk, *nv;
+  int64_t n_st, n_sh;
+  const int32_t* slots;
 };
 
 // Prefill tiles on MFMA (attention_prefill.hip): fp16, head_dim 64.

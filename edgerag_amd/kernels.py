@@ -184,6 +184,11 @@ class AttentionPlan:
     def n_items(self) -> int:
         return int(self.plan_host[2])
 
+    @property
+    def decode_only(self) -> bool:
+        """Every work item is a decode row (no prefill tiles): the append can fuse in."""
+        return int(self.plan_host[2]) == int(self.plan_host[13])
+
 
 _WORKSPACES: dict[torch.device, torch.Tensor] = {}
 
@@ -340,6 +345,66 @@ def paged_attention(
         call("edgerag_paged_attention", *args, _lib.ATTN_COMBINE, stream_ptr(device))
     else:
         call("edgerag_paged_attention", *args, _lib.ATTN_ALL, stream_ptr(device))
+    return out
+
+
+def paged_attention_append(
+    key: torch.Tensor,
+    value: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    query: torch.Tensor,
+    key_pool: torch.Tensor,
+    value_pool: torch.Tensor,
+    plan: AttentionPlan,
+    scale: float,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """``kv_append(key, value, slot_mapping, pools)`` then ``paged_attention(query, ...)``, with the
+    same results; one launch for decode batches (the waves reaching a request's new positions read
+    them from ``key``/``value`` and write them to the pools)."""
+    require_device(key, value, slot_mapping, query, key_pool, value_pool)
+    _check_pool(key_pool, "key_pool")
+    _check_pool(value_pool, "value_pool")
+    if key_pool.shape != value_pool.shape or key_pool.dtype != value_pool.dtype:
+        raise ValueError("key_pool and value_pool must match")
+    n_kv, num_blocks, block_size, head_dim = key_pool.shape
+    if key.shape != value.shape or key.stride() != value.stride() or key.dtype != value.dtype:
+        raise ValueError("key and value must share shape, strides and dtype")
+    if key.dim() != 3 or key.shape[1:] != (n_kv, head_dim) or key.stride(2) != 1:
+        raise ValueError(f"new K/V must be (tokens, {n_kv}, {head_dim}), head_dim contiguous")
+    if slot_mapping.dtype != torch.int32 or slot_mapping.shape != (key.shape[0],):
+        raise ValueError("slot_mapping must be int32 with one entry per new token")
+    if query.dim() != 3 or query.shape[1] != plan.n_q_heads or query.shape[2] != head_dim:
+        raise ValueError(
+            f"query must be (tokens, {plan.n_q_heads}, {head_dim}), got {tuple(query.shape)}"
+        )
+    if key.shape[0] != query.shape[0]:
+        raise ValueError("one new K/V row per query token")
+    if query.dtype != key_pool.dtype:
+        raise ValueError(f"query dtype {query.dtype} != pool dtype {key_pool.dtype}")
+    if (n_kv, block_size, head_dim, query.dtype) != (
+        plan.n_kv_heads, plan.block_size, plan.head_dim, plan.dtype
+    ):
+        raise ValueError("the attention plan was built for a different pool shape")
+    if query.stride(2) != 1:
+        query = query.contiguous()
+    if out is None:
+        out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
+    elif out.shape != query.shape or out.dtype != query.dtype or out.stride(2) != 1:
+        raise ValueError("out must match query in shape and dtype, head_dim contiguous")
+    ws = plan.workspace
+    call(
+        "edgerag_paged_attention_append", key.data_ptr(), value.data_ptr(),
+        dtype_code(key.dtype), key.stride(0), key.stride(1), slot_mapping.contiguous().data_ptr(),
+        plan.plan_host.ctypes.data, plan.plan_dev.data_ptr(), plan.plan_host.size,
+        query.data_ptr(), query.stride(0), query.stride(1),
+        key_pool.data_ptr(), value_pool.data_ptr(), dtype_code(key_pool.dtype),
+        plan.block_tables.data_ptr(), plan.block_tables.stride(0),
+        plan.query_start_loc.data_ptr(), plan.context_lens.data_ptr(),
+        plan.num_reqs, query.shape[0], plan.n_q_heads, n_kv, head_dim, block_size, num_blocks,
+        float(scale), out.data_ptr(), out.stride(0), out.stride(1),
+        None if ws is None else ws.data_ptr(), plan.workspace_bytes, stream_ptr(query.device),
+    )
     return out
 
 

@@ -164,6 +164,31 @@ int edgerag_paged_attention(const int32_t* plan_host, const int32_t* plan_dev, i
                             void* stream);
 
 /*
+ * The decode step's KV append and its attention in one call: exactly edgerag_kv_append(new_key,
+ * new_value, new_dtype, new_stride_tok, new_stride_head, slot_mapping, num_tokens, key_pool,
+ * value_pool, dtype, ...) followed by edgerag_paged_attention(..., EDGERAG_ATTN_ALL), with the
+ * same results. When every work item of the plan is a decode row on the fast decode kernel (the
+ * usual decode batch) and the new rows are in the pool dtype and 16-byte aligned, it is one
+ * launch: the waves that reach a request's new positions read them from new_key / new_value and
+ * write them to the pools at their slots; the attention treats a token's new K/V as sitting at
+ * its position in the block table, as slot_mapping does when built from the tables. Otherwise
+ * (prefill tiles in the batch, other layouts) it enqueues the two launches.
+ *
+ * Replaces PagedKVCache._write followed by fused_paged_attention for a decode step
+ * (edgerag/cache/paged.py:186-206; edgerag/cache/fused.py:242-286).
+ */
+int edgerag_paged_attention_append(
+    const void* new_key, const void* new_value, int32_t new_dtype, int64_t new_stride_tok,
+    int64_t new_stride_head, const int32_t* slot_mapping, const int32_t* plan_host,
+    const int32_t* plan_dev, int64_t plan_words, const void* q, int64_t q_stride_tok,
+    int64_t q_stride_head, void* key_pool, void* value_pool, int32_t dtype,
+    const int32_t* block_tables, int64_t block_tables_stride, const int32_t* query_start_loc,
+    const int32_t* context_lens, int32_t num_reqs, int32_t num_tokens, int32_t n_q_heads,
+    int32_t n_kv_heads, int32_t head_dim, int32_t block_size, int32_t num_blocks, float scale,
+    void* out, int64_t out_stride_tok, int64_t out_stride_head, void* workspace,
+    int64_t workspace_bytes, void* stream);
+
+/*
  * Fixed-capacity form of edgerag_paged_attention for decode-only batches, for HIP graph capture.
  * The launch configuration depends only on the capacities, never on the plan: max_row_items
  * waves run the decode-row kernel and max_combine_rows x ceil(n_q_heads/4) the split merge, and

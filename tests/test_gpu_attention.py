@@ -420,3 +420,56 @@ def test_invalid_block_ids_mask_their_keys(device, q_len) -> None:
         s = s.masked_fill(~visible, float("-inf"))
         ref = torch.softmax(s, dim=-1) @ v[h // 2]
         torch.testing.assert_close(got[:, h].double(), ref, rtol=1e-2, atol=2e-3)
+
+
+@pytest.mark.parametrize("dtype,n_q,n_kv,d,q_lens", [
+    (torch.float16, 32, 32, 64, None),     # config-2-shaped decode batch
+    (torch.float32, 8, 2, 64, None),       # GQA, fp32
+    (torch.bfloat16, 8, 2, 128, None),     # GQA, head_dim 128
+    (torch.float16, 8, 4, 64, "multi"),    # 2-token rows (2 * n_rep <= 8 query vectors)
+    (torch.float16, 8, 4, 64, "mixed"),    # a prefill slice in the batch: two launches
+])
+def test_append_fused_into_attention_equals_append_then_attention(device, dtype, n_q, n_kv, d,
+                                                                  q_lens) -> None:
+    """paged_attention_append == kv_append followed by paged_attention, bit for bit: outputs,
+    key pool and value pool. Decode batches run as one launch (the new positions are read from
+    the new rows and written to their slots by the waves that reach them); a batch with a
+    prefill slice takes the two-launch path through the same entry."""
+    g = seeded(len(str(q_lens)) + d + n_q)
+    lens = [int(x) for x in torch.randint(1, 1500, (24,), generator=g)]
+    if q_lens is None:
+        q_lens = [1] * len(lens)
+    elif q_lens == "multi":
+        q_lens = [min(2, L) for L in lens]
+    else:
+        lens[3], lens[7] = 700, 200
+        q_lens = [1] * len(lens)
+        q_lens[3] = 200  # a 200-token chunk after a 500-token prefix
+    kp, vp, tables, qsl, q, bt = _ragged_case(lens, q_lens, n_q, n_kv, d, dtype, 31,
+                                              poison=False)
+    T = int(qsl[-1])
+    nk = torch.randn(T, n_kv, d, generator=g).to(dtype)
+    nv = torch.randn(T, n_kv, d, generator=g).to(dtype)
+    slots = []
+    for r, (L, c) in enumerate(zip(lens, q_lens)):
+        for pos in range(L - c, L):
+            slots.append(tables[r][pos // BLOCK_SIZE] * BLOCK_SIZE + pos % BLOCK_SIZE)
+    slots = torch.tensor(slots, dtype=torch.int32)
+    plan, (slots_d,) = kernels.plan_attention(qsl, np.asarray(lens, np.int32), bt, n_q, n_kv, d,
+                                              BLOCK_SIZE, dtype, device, [slots.numpy()])
+    scale = d ** -0.5
+    qd, nkd, nvd = q.to(device), nk.to(device), nv.to(device)
+    kp1, vp1 = kp.to(device), vp.to(device)
+    kernels.kv_append(nkd, nvd, slots_d, kp1, vp1)
+    ref = kernels.paged_attention(qd, kp1, vp1, plan, scale, overlap=False)
+    kp2, vp2 = kp.to(device), vp.to(device)
+    got = kernels.paged_attention_append(nkd, nvd, slots_d, qd, kp2, vp2, plan, scale)
+    assert torch.equal(got, ref)
+    assert torch.equal(kp2, kp1) and torch.equal(vp2, vp1)
+    # and the result is attention over the appended pools (float64 pin on one request)
+    r = 5
+    kh = op.gather_pool(kp1.cpu().float(), tables[r], lens[r])[0]
+    vh = op.gather_pool(vp1.cpu().float(), tables[r], lens[r])[0]
+    ref64 = oa.attention_f64(q[qsl[r] : qsl[r + 1], 0], kh, vh, lens[r] - q_lens[r], scale)
+    tol = FP32_TOL if dtype == torch.float32 else {k_: v_ * 4 for k_, v_ in FP16_TOL.items()}
+    torch.testing.assert_close(got[qsl[r] : qsl[r + 1], 0].cpu().double(), ref64, **tol)
