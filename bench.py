@@ -263,6 +263,33 @@ def measure_ceilings(device, gather_bytes):
     return out
 
 
+def vendor_gemm_us(x, packed, scales, k, bits, g, n_w=8, n_launch=64):
+    """torch's fp16 ``x @ W^T`` (hipBLASLt) over ``n_w`` dequantised weight replicas, replayed
+    from a HIP graph of ``n_launch`` back-to-back launches: average launch-to-launch time, µs.
+    The weights are stored (K, N) contiguous, so the product is a plain mm."""
+    n_w = min(n_w, packed.shape[0])
+    wt = [kernels.dequantize(packed[r], scales[r], k, bits, g).t().contiguous() for r in range(n_w)]
+    y = torch.empty(x.shape[0], wt[0].shape[1], device=x.device, dtype=torch.float16)
+    for r in range(n_w):
+        torch.mm(x, wt[r], out=y)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(n_launch):
+            torch.mm(x, wt[i % n_w], out=y)
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(3):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (3 * n_launch)
+    del graph, wt, y
+    return us
+
+
 def bench_quant(device, iters=None):
     """Config 4. Each timing replays a HIP graph of back-to-back launches, one per weight replica
     (>= 1 GiB of distinct packed weights in rotation, so the weights stream from HBM rather than
@@ -270,7 +297,9 @@ def bench_quant(device, iters=None):
     ``us`` is the average launch-to-launch time on the GPU, events on the capture stream.
     ``read_us`` is the streaming-read probe over the same packed-weight replicas, the same way:
     the time any kernel needs just to read those bytes at this size (``read_frac`` = read_us /
-    us for the HBM-bound rows)."""
+    us for the HBM-bound rows). For the MFMA-bound rows, ``vendor_fp16_us`` is torch's fp16
+    GEMM (hipBLASLt) on the dequantised weights of the same shape, timed the same way:
+    what the vendor library needs for the matrix product alone, with no dequantisation."""
     shapes = [(2048, 2048, 8, 2048), (2048, 8192, 8, 2048), (8192, 2048, 8, 8192),
               (1152, 1152, 4, 128), (1152, 4608, 4, 128)]
     results = []
@@ -317,6 +346,8 @@ def bench_quant(device, iters=None):
                        frac=round(frac, 4), read_us=round(read_us, 2))
             if bound == "hbm":
                 row["read_frac"] = round(read_us / us, 4)
+            else:
+                row["vendor_fp16_us"] = round(vendor_gemm_us(x, packed, scales, k, bits, g), 2)
             results.append(row)
         del packed, scales
         torch.cuda.empty_cache()

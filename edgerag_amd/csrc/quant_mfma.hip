@@ -39,6 +39,23 @@
 #ifndef EDGERAG_GEMM_MIN_WG
 #define EDGERAG_GEMM_MIN_WG 1  // workgroups per CU the GEMM's register budget must allow
 #endif
+// Per tile shape: threads and register stages in flight of the GEMM workgroup (the 64x64 tiles,
+// one workgroup per CU, need a deeper ring than the larger ones).
+#ifndef EDGERAG_GEMM_STAGES_128
+#define EDGERAG_GEMM_STAGES_128 2
+#endif
+#ifndef EDGERAG_GEMM_THREADS_128x64
+#define EDGERAG_GEMM_THREADS_128x64 256
+#endif
+#ifndef EDGERAG_GEMM_STAGES_128x64
+#define EDGERAG_GEMM_STAGES_128x64 2
+#endif
+#ifndef EDGERAG_GEMM_THREADS_64
+#define EDGERAG_GEMM_THREADS_64 256
+#endif
+#ifndef EDGERAG_GEMM_STAGES_64
+#define EDGERAG_GEMM_STAGES_64 4
+#endif
 #ifndef EDGERAG_GEMM_TARGET_WGS
 #define EDGERAG_GEMM_TARGET_WGS 256  // the tile is the largest whose grid reaches this many
 #endif
@@ -680,12 +697,21 @@ constexpr int kBK = 64;     // k per LDS stage
 constexpr int kLdsRow = 64;  // halves per LDS row (one row of a 64-k stage)
 
 // Halves offset of 16-byte chunk `c` (k 8c .. 8c + 7 of the stage) of LDS row `row`. The stage is
-// stored in MFMA operand order: for each 32-row tile and 16-k step, the 64 lanes' operands
-// (lane = 32 (c & 1) + row % 32) are 64 consecutive 16-byte slots, so every operand read is one
-// contiguous 1 KiB ds_read_b128 (no bank conflicts), and the stagers' writes are runs of 16 or 32
-// consecutive slots.
+// stored in MFMA operand order: for each 32-row tile and 16-k step ks = c / 2, the 64 lanes'
+// operands (lane = 32 (c & 1) + row % 32) fill one block of 64 16-byte slots, so every operand
+// read is one 1 KiB ds_read_b128. Inside a block the lane's slot is XOR-ed with
+// lds_swizzle(ks) (bits 1..3 only, so each aligned group of 8 or 16 lanes still covers every
+// bank once): the stagers write 2 or 4 chunks of the same row from adjacent lanes, i.e. to
+// blocks with different ks, and without the swizzle those writes would land on the same banks
+// (slots 512 B apart). With it, any 8 or 16 adjacent stager lanes hit distinct banks for both
+// stager shapes (4 lanes per row, ks = lane % 4; 2 lanes per row, ks / 2 = lane % 2).
+__device__ __forceinline__ constexpr int lds_swizzle(int ks) {
+  return ((ks & 2) << 2) | ((((ks >> 1) ^ ks) & 1) << 2) | ((ks & 1) << 1);
+}
 __device__ __forceinline__ int lds_off(int row, int c) {
-  return ((((row >> 5) * 4 + (c >> 1)) * 2 + (c & 1)) * 32 + (row & 31)) * 8;
+  const int ks = c >> 1;
+  const int lane = (c & 1) * 32 + (row & 31);
+  return (((row >> 5) * 4 + ks) * 64 + (lane ^ lds_swizzle(ks))) * 8;
 }
 
 // A BN x BM tile computed by NTH threads: waves in a 2 x (NTH / 128) grid (N x M), each owning
@@ -786,12 +812,13 @@ __device__ __forceinline__ void gemm_store_x(const GemmStage<C>& st, int i, _Flo
 // l % 32, k chunk 2 ks + l / 32 of a 16-k step; accumulator register i of lane l holds
 // row 8 (i / 4) + 4 (l / 32) + i % 4 of A (weight row) and column l % 32 (activation row).
 // PC: per-channel INT8 (one scale per weight row), applied to the fp32 sums.
-template <int BITS, int BN, int BM, bool PC, int NTH>
+template <int BITS, int BN, int BM, bool PC, int NTH, int NS>
 __global__ __launch_bounds__(NTH, EDGERAG_GEMM_MIN_WG) void qlinear_gemm_kernel(
     const f16* __restrict__ x, int64_t xs, int32_t m, int32_t k,
     const uint8_t* __restrict__ packed, const f16* __restrict__ scales,
     const f16* __restrict__ bias, int32_t n, int32_t g, f16* __restrict__ y, int64_t ys) {
   using C = GemmCfg<BITS, BN, BM, NTH>;
+  static_assert(NS % 2 == 0, "the register ring must keep the LDS buffer parity of a step");
   constexpr int NWC = C::W_K / 8, NXC = C::X_BPT / 16;  // LDS chunks this thread stages per step
   __shared__ __attribute__((aligned(16))) _Float16 sw[2][BN * kLdsRow];
   __shared__ __attribute__((aligned(16))) _Float16 sx[2][BM * kLdsRow];
@@ -820,11 +847,6 @@ __global__ __launch_bounds__(NTH, EDGERAG_GEMM_MIN_WG) void qlinear_gemm_kernel(
 
   const int nk = k / kBK;
   const int col = lane & 31, half = lane >> 5;
-  // One 64-k step on the staged LDS buffers (swb, sxb), interleaved with staging the next step's
-  // registers `st` into the other buffers (dw, dx): each of the four 16-k MFMA steps is paired
-  // with a share of the dequantisation and LDS writes, so the VALU and LDS work of the next step
-  // overlaps this step's matrix-core work. The operands of 16-k step ks + 1 are read from LDS
-  // before the MFMAs of step ks are issued, so their latency hides behind those MFMAs.
   auto read_ops = [&](const _Float16* swb, const _Float16* sxb, int ks, h8 (&a)[C::TN],
                       h8 (&b)[C::TM]) {
 #pragma unroll
@@ -834,32 +856,34 @@ __global__ __launch_bounds__(NTH, EDGERAG_GEMM_MIN_WG) void qlinear_gemm_kernel(
     for (int j = 0; j < C::TM; ++j)
       b[j] = *reinterpret_cast<const h8*>(sxb + lds_off(wm * (32 * C::TM) + 32 * j + col, 2 * ks + half));
   };
-  auto step = [&](const _Float16* swb, const _Float16* sxb, const GemmStage<C>& st,
-                  _Float16* dw, _Float16* dx) {
+  // One 64-k step on the LDS buffers of parity p, interleaved with staging the next step's
+  // registers `stn` into the buffers of parity p ^ 1: each of the four 16-k MFMA steps is paired
+  // with a share of the dequantisation and LDS writes, so the VALU and LDS work of the next step
+  // overlaps this step's matrix-core work. The operands of 16-k step ks + 1 are read from LDS
+  // before the MFMAs of step ks are issued, so their latency hides behind those MFMAs.
+  auto step = [&](int p, const GemmStage<C>& stn) {
     h8 a[2][C::TN], b[2][C::TM];
-    read_ops(swb, sxb, 0, a[0], b[0]);
+    read_ops(sw[p], sx[p], 0, a[0], b[0]);
 #pragma unroll
     for (int ks = 0; ks < kBK / 16; ++ks) {
-      if (ks + 1 < kBK / 16) read_ops(swb, sxb, ks + 1, a[(ks + 1) & 1], b[(ks + 1) & 1]);
+      if (ks + 1 < kBK / 16) read_ops(sw[p], sx[p], ks + 1, a[(ks + 1) & 1], b[(ks + 1) & 1]);
 #pragma unroll
       for (int c = ks * NWC / 4; c < (ks + 1) * NWC / 4; ++c)
-        gemm_store_w<C, PC>(st, c, dw, wr, wc0);
+        gemm_store_w<C, PC>(stn, c, sw[p ^ 1], wr, wc0);
 #pragma unroll
       for (int i = ks * NXC / 4; i < (ks + 1) * NXC / 4; ++i)
-        gemm_store_x<C>(st, i, dx, xr, xc0);
+        gemm_store_x<C>(stn, i, sx[p ^ 1], xr, xc0);
 #pragma unroll
       for (int i = 0; i < C::TN; ++i)
 #pragma unroll
         for (int j = 0; j < C::TM; ++j) acc[i][j] = mfma32(a[ks & 1][i], b[ks & 1][j], acc[i][j]);
     }
   };
-  // Register stages st0 / st1 alternate; a step's global loads are issued about two steps before
-  // it is staged to LDS. One barrier per step: it orders this step's LDS writes (the next step's
-  // operands) before their reads, and every wave's reads of a buffer before its next rewrite.
-  // Loads are unconditional (a step past the end reloads the last one) so that the compiler never
-  // has to wait for a load right after issuing it. Steps go in pairs whose loads are issued on
-  // every path (an odd last step skips only the second half's LDS and matrix work, under a
-  // wave-uniform branch), so the compiler cannot sink a step's loads behind a branch.
+  // One barrier per step: it orders this step's LDS writes (the next step's operands) before
+  // their reads, and every wave's reads of a buffer before its next rewrite. Loads are
+  // unconditional (a step past the end reloads the last one) so that the compiler never has to
+  // wait for a load right after issuing it, and a step's loads are issued on every path (a last
+  // partial round of the ring skips only LDS and matrix work, under a wave-uniform branch).
   // Epilogue operands: thread t < BN loads the scale (PC) and bias of weight row nb + t now (row
   // clamped into [0, N)), waits for them once the first stages' loads are in flight, and puts
   // them in LDS after the main loop for the lanes that write that row.
@@ -870,28 +894,34 @@ __global__ __launch_bounds__(NTH, EDGERAG_GEMM_MIN_WG) void qlinear_gemm_kernel(
   uint32_t ep_s = PC ? scales16[ep_row] : 0u;
   uint32_t ep_b = bias != nullptr ? bias16[ep_row] : 0u;
 
-  GemmStage<C> st0, st1;
+  // NS register stages form a ring: step t is loaded into st[t % NS] right after the barrier that
+  // ends step t - NS - 1 and is staged to LDS during step t - 1, so NS - 1 whole steps of matrix
+  // work cover each load's latency. The loop is unrolled by NS so that every ring index is a
+  // compile-time register name (and, NS being even, every LDS buffer parity a constant).
+  GemmStage<C> st[NS];
   const int last = (nk - 1) * kBK;
-  gemm_load<C>(st0, 0, wrow, srow, g, wk_off, xrow);
-  gemm_load<C>(st1, min(kBK, last), wrow, srow, g, wk_off, xrow);
+  auto load = [&](GemmStage<C>& dst, int t) {
+    gemm_load<C>(dst, min(t * kBK, last), wrow, srow, g, wk_off, xrow);
+  };
+#pragma unroll
+  for (int j = 0; j < NS; ++j) load(st[j], j);
   issue_fence();
   asm volatile("" : "+v"(ep_s), "+v"(ep_b));
 #pragma unroll
-  for (int c = 0; c < NWC; ++c) gemm_store_w<C, PC>(st0, c, sw[0], wr, wc0);
+  for (int c = 0; c < NWC; ++c) gemm_store_w<C, PC>(st[0], c, sw[0], wr, wc0);
 #pragma unroll
-  for (int i = 0; i < NXC; ++i) gemm_store_x<C>(st0, i, sx[0], xr, xc0);
+  for (int i = 0; i < NXC; ++i) gemm_store_x<C>(st[0], i, sx[0], xr, xc0);
   __syncthreads();
-  gemm_load<C>(st0, min(2 * kBK, last), wrow, srow, g, wk_off, xrow);
+  load(st[0], NS);
   issue_fence();
-  for (int kt = 0; kt < nk; kt += 2) {
-    step(sw[0], sx[0], st1, sw[1], sx[1]);
-    __syncthreads();
-    gemm_load<C>(st1, min((kt + 3) * kBK, last), wrow, srow, g, wk_off, xrow);
-    issue_fence();
-    if (kt + 1 < nk) step(sw[1], sx[1], st0, sw[0], sx[0]);
-    __syncthreads();
-    gemm_load<C>(st0, min((kt + 4) * kBK, last), wrow, srow, g, wk_off, xrow);
-    issue_fence();
+  for (int kt = 0; kt < nk; kt += NS) {
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+      if (j == 0 || kt + j < nk) step(j & 1, st[(j + 1) % NS]);
+      __syncthreads();
+      load(st[(j + 1) % NS], kt + j + NS + 1);
+      issue_fence();
+    }
   }
 
   // Epilogue: register 4q + r of tile (i, j) is y[mrow][nrow + r], 4 consecutive outputs per q,
@@ -984,17 +1014,17 @@ void launch_skinny(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t
 #undef EDGERAG_SKINNY
 }
 
-template <int BITS, int BN, int BM, int NTH = 256>
+template <int BITS, int BN, int BM, int NTH, int NS>
 void launch_gemm(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
                  const f16* scales, const f16* bias, int32_t n, int32_t g, f16* y, int64_t ys,
                  hipStream_t s) {
   const dim3 grid(unsigned((n + BN - 1) / BN), unsigned((m + BM - 1) / BM));
   if (BITS == 8 && g == k)
-    hipLaunchKernelGGL((qlinear_gemm_kernel<BITS, BN, BM, BITS == 8, NTH>), grid, dim3(NTH), 0, s,
-                       x, xs, m, k, packed, scales, bias, n, g, y, ys);
+    hipLaunchKernelGGL((qlinear_gemm_kernel<BITS, BN, BM, BITS == 8, NTH, NS>), grid, dim3(NTH),
+                       0, s, x, xs, m, k, packed, scales, bias, n, g, y, ys);
   else
-    hipLaunchKernelGGL((qlinear_gemm_kernel<BITS, BN, BM, false, NTH>), grid, dim3(NTH), 0, s, x,
-                       xs, m, k, packed, scales, bias, n, g, y, ys);
+    hipLaunchKernelGGL((qlinear_gemm_kernel<BITS, BN, BM, false, NTH, NS>), grid, dim3(NTH), 0, s,
+                       x, xs, m, k, packed, scales, bias, n, g, y, ys);
 }
 
 // The streaming kernel's shape: k-slices F and row tiles NT from N alone (two k-slices when
@@ -1202,12 +1232,14 @@ void dispatch(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* pac
   const int64_t t128 = int64_t((n + 127) / 128) * ((m + 127) / 128);
   const int64_t t128x64 = int64_t((n + 127) / 128) * ((m + 63) / 64);
   if (t128 >= EDGERAG_GEMM_TARGET_WGS)
-    launch_gemm<BITS, 128, 128, EDGERAG_GEMM_THREADS_128>(x, xs, m, k, packed, scales, bias, n, g,
-                                                          y, ys, s);
+    launch_gemm<BITS, 128, 128, EDGERAG_GEMM_THREADS_128, EDGERAG_GEMM_STAGES_128>(
+        x, xs, m, k, packed, scales, bias, n, g, y, ys, s);
   else if (t128x64 >= EDGERAG_GEMM_TARGET_WGS)
-    launch_gemm<BITS, 128, 64>(x, xs, m, k, packed, scales, bias, n, g, y, ys, s);
+    launch_gemm<BITS, 128, 64, EDGERAG_GEMM_THREADS_128x64, EDGERAG_GEMM_STAGES_128x64>(
+        x, xs, m, k, packed, scales, bias, n, g, y, ys, s);
   else
-    launch_gemm<BITS, 64, 64>(x, xs, m, k, packed, scales, bias, n, g, y, ys, s);
+    launch_gemm<BITS, 64, 64, EDGERAG_GEMM_THREADS_64, EDGERAG_GEMM_STAGES_64>(
+        x, xs, m, k, packed, scales, bias, n, g, y, ys, s);
 }
 
 }  // namespace
