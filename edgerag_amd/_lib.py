@@ -34,6 +34,7 @@ EDGERAG_EUNSUPPORTED = 4
 
 ATTN_TILES, ATTN_ROWS, ATTN_COMBINE, ATTN_ALL = 1, 2, 4, 7
 ATTN_TILES_SHARED = 8  # modifier of ATTN_TILES: one tile workgroup per CU, beside decode rows
+QUANT_WORKSPACE_MAX = 8 * 1024 * 1024  # bound of edgerag_quant_linear_workspace_bytes
 
 DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 
@@ -91,6 +92,12 @@ SIGNATURES: dict[str, tuple[list, object]] = {
          c_vp],
         c_i32,
     ),
+    "edgerag_quant_linear_ws": (
+        [c_vp, c_i32, c_i64, c_i32, c_i32, c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_vp, c_i64,
+         c_vp, c_i64, c_vp],
+        c_i32,
+    ),
+    "edgerag_quant_linear_workspace_bytes": ([c_i32, c_i32, c_i32, c_i32, c_i32], c_i64),
     "edgerag_quant_linear_swiglu": (
         [c_vp, c_i32, c_i64, c_i32, c_i32, c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_vp, c_i64,
          c_vp, c_i32, c_f32, c_vp],

@@ -23,13 +23,14 @@ chunked-prefill slices and single-token decodes alike -- is packed token-major i
 from __future__ import annotations
 
 from dataclasses import dataclass
+from functools import partial
 
 import torch
 from torch import nn
 
 from edgerag_amd import kernels
 from edgerag_amd.core.layers import RMSNorm, RotaryTable
-from edgerag_amd.core.linear import QuantLinear
+from edgerag_amd.core.linear import LinearBase, QuantLinear
 from edgerag_amd.core.quant import QuantConfig
 from edgerag_amd.core.spec import ModelSpec
 
@@ -76,6 +77,9 @@ class DecoderLayer(nn.Module):
 
 
 class EdgeRagDecoder(nn.Module):
+    # Largest batch whose q/k/v and gate/up projections use the fused streaming epilogues.
+    STREAM_EPILOGUE_MAX_TOKENS = 32
+
     def __init__(
         self,
         spec: ModelSpec,
@@ -195,7 +199,11 @@ class EdgeRagDecoder(nn.Module):
         n_layers = len(self.layers)
         qkv0 = self.layers[0].qkv
         rows = None
-        if isinstance(qkv0, QuantLinear) and kernels.quant_rope_fused(
+        # The fused streaming epilogues (q/k/v + RoPE + append, gate/up + SiLU * up) serve batches
+        # of up to 32 tokens; larger batches run the tiled GEMM and the elementwise launch apart,
+        # which is faster there.
+        stream_epi = T <= self.STREAM_EPILOGUE_MAX_TOKENS
+        if stream_epi and isinstance(qkv0, QuantLinear) and kernels.quant_rope_fused(
                 T, qkv0.in_features, qkv0.config.bits, qkv0.config.group_size, spec.n_q_heads,
                 spec.n_kv_heads, d, self.dtype):
             rows = kernels.rope_rows(step.positions, self.rotary.cos, self.rotary.sin)
@@ -205,10 +213,11 @@ class EdgeRagDecoder(nn.Module):
         xw = torch.empty_like(hidden) if fused else None  # fp16(norm weight * hidden)
         norm = None  # the normed input of the next q/k/v projection (None: x is normalised)
         for idx, layer in enumerate(self.layers):
-            layer.qkv.rope_append(xw if norm is not None else x, step.positions,
-                                  self.rotary.cos, self.rotary.sin, spec.n_q_heads,
-                                  spec.n_kv_heads, d, step.slots, key_pool[idx], value_pool[idx],
-                                  q_out=q, rows=rows, norm=norm)
+            rope_append = layer.qkv.rope_append if stream_epi else partial(
+                LinearBase.rope_append, layer.qkv)
+            rope_append(xw if norm is not None else x, step.positions, self.rotary.cos,
+                        self.rotary.sin, spec.n_q_heads, spec.n_kv_heads, d, step.slots,
+                        key_pool[idx], value_pool[idx], q_out=q, rows=rows, norm=norm)
             if isinstance(step.plan, kernels.FixedAttention):
                 step.plan.launch(q, key_pool[idx], value_pool[idx], self.scaling, attn_out)
             else:
@@ -231,7 +240,9 @@ class EdgeRagDecoder(nn.Module):
             o = layer.o_proj(attn_out.view(T, layer.q_out))
             x = kernels.rmsnorm(hidden, layer.post_attention_layernorm.weight, eps, delta=o,
                                 h_out=hidden)
-            down = layer.down_proj(layer.gate_up.swiglu(x))
+            act = (layer.gate_up.swiglu(x) if stream_epi
+                   else LinearBase.swiglu(layer.gate_up, x))
+            down = layer.down_proj(act)
             x = kernels.rmsnorm(hidden, next_norm, eps, delta=down, h_out=hidden)
         return x[step.logit_rows.long()]
 

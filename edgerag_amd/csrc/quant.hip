@@ -315,6 +315,33 @@ extern "C" int edgerag_dequantize(const uint8_t* packed, const void* scales_f16,
   return check_launch("edgerag_dequantize");
 }
 
+extern "C" int64_t edgerag_quant_linear_workspace_bytes(int32_t m, int32_t k, int32_t n,
+                                                        int32_t bits, int32_t group_size) {
+  return qlinear_split_plan(m, k, n, bits, group_size).bytes;
+}
+
+extern "C" int edgerag_quant_linear_ws(const void* x, int32_t x_dtype, int64_t x_stride, int32_t m,
+                                       int32_t k, const uint8_t* packed, const void* scales_f16,
+                                       const void* bias_f16, int32_t n, int32_t bits,
+                                       int32_t group_size, void* y, int64_t y_stride,
+                                       void* workspace, int64_t workspace_bytes, void* stream) {
+  clear_error();
+  if (workspace_bytes < 0 || (workspace_bytes > 0 && workspace == nullptr))
+    return fail(EDGERAG_EINVAL, "edgerag_quant_linear_ws: workspace of %lld bytes at NULL",
+                (long long)workspace_bytes);
+  if (x_dtype == EDGERAG_F16 && m > 0 && x != nullptr && packed != nullptr &&
+      scales_f16 != nullptr && y != nullptr && x_stride >= k && y_stride >= n &&
+      check_quant_shape("edgerag_quant_linear_ws", n, k, bits, group_size) == EDGERAG_OK &&
+      qlinear_mfma_supported(k, bits, group_size, x, x_stride, packed) &&
+      launch_qlinear_split(static_cast<const f16*>(x), x_stride, m, k, packed,
+                           static_cast<const f16*>(scales_f16), static_cast<const f16*>(bias_f16),
+                           n, bits, group_size, static_cast<f16*>(y), y_stride, workspace,
+                           workspace_bytes, static_cast<hipStream_t>(stream)))
+    return check_launch("edgerag_quant_linear_ws");
+  return edgerag_quant_linear(x, x_dtype, x_stride, m, k, packed, scales_f16, bias_f16, n, bits,
+                              group_size, y, y_stride, stream);
+}
+
 extern "C" int edgerag_quant_linear(const void* x, int32_t x_dtype, int64_t x_stride, int32_t m,
                                     int32_t k, const uint8_t* packed, const void* scales_f16,
                                     const void* bias_f16, int32_t n, int32_t bits,

@@ -18,6 +18,22 @@ void launch_qlinear_mfma(const f16* x, int64_t xs, int32_t m, int32_t k, const u
                          const f16* scales, const f16* bias, int32_t n, int32_t bits, int32_t g,
                          f16* y, int64_t ys, hipStream_t s);
 
+// Workspace route of the tiled GEMM for (M, K, N, bits, group_size): `splits` = 0 when the
+// plain launch is used, 1 for 64x64 tiles without a split, else the number of k ranges; `bytes`
+// is the workspace a split needs (its fp32 partial tiles: at most 8 MiB).
+struct SplitPlan {
+  int splits;
+  int64_t bytes;
+};
+SplitPlan qlinear_split_plan(int32_t m, int32_t k, int32_t n, int32_t bits, int32_t g);
+
+// Runs the workspace route when the plan takes the shape (a split: two launches, the k ranges'
+// partial tiles into the workspace, then their sum in split order and the epilogue) and the
+// workspace holds `bytes`; returns false, enqueuing nothing, otherwise.
+bool launch_qlinear_split(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
+                          const f16* scales, const f16* bias, int32_t n, int32_t bits, int32_t g,
+                          f16* y, int64_t ys, void* ws, int64_t ws_bytes, hipStream_t s);
+
 // Operands of the fused epilogues and of normed inputs (zero when unused).
 struct EpiArgs {
   const f16* cos_tok;    // [m, head_dim]: cos table row at each token's position

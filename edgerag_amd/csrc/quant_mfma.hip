@@ -17,8 +17,11 @@
 //   permuted the same way in registers.
 // * qlinear_gemm_kernel (M > 64, prefill slices): MFMA-bound. A 256-thread workgroup computes a
 //   BN x BM tile of y^T through v_mfma_f32_32x32x16_f16; per 64-k step it stages the dequantised
-//   weights and the activations in double-buffered, XOR-swizzled LDS, loading the next step's
-//   bytes from global memory while the current one is computed.
+//   weights and the activations in double-buffered, XOR-swizzled LDS, loading the next steps'
+//   bytes from global memory while the current one is computed. With a workspace
+//   (edgerag_quant_linear_ws) it also takes decode batches past the streaming GEMV's crossover,
+//   and splits K over the workgroups when the 64x64 tiles alone would leave CUs idle
+//   (qlinear_split_reduce_kernel adds the k ranges' partial tiles in order).
 #include "quant_mfma.h"
 
 #ifndef EDGERAG_SKINNY_MAX_M
@@ -55,6 +58,15 @@
 #endif
 #ifndef EDGERAG_GEMM_STAGES_64
 #define EDGERAG_GEMM_STAGES_64 4
+#endif
+#ifndef EDGERAG_SPLITK_MAX
+#define EDGERAG_SPLITK_MAX 16  // most k splits
+#endif
+#ifndef EDGERAG_SPLITK_MIN_STEPS
+#define EDGERAG_SPLITK_MIN_STEPS 2  // fewest 64-k steps per split
+#endif
+#ifndef EDGERAG_SPLITK_FIXED_STEPS
+#define EDGERAG_SPLITK_FIXED_STEPS 20  // cost of a split launch's partials and second launch
 #endif
 #ifndef EDGERAG_GEMM_TARGET_WGS
 #define EDGERAG_GEMM_TARGET_WGS 256  // the tile is the largest whose grid reaches this many
@@ -812,11 +824,19 @@ __device__ __forceinline__ void gemm_store_x(const GemmStage<C>& st, int i, _Flo
 // l % 32, k chunk 2 ks + l / 32 of a 16-k step; accumulator register i of lane l holds
 // row 8 (i / 4) + 4 (l / 32) + i % 4 of A (weight row) and column l % 32 (activation row).
 // PC: per-channel INT8 (one scale per weight row), applied to the fp32 sums.
-template <int BITS, int BN, int BM, bool PC, int NTH, int NS>
+// SPLIT: blockIdx.z is one of gridDim.z equal k ranges (split K). The workgroup writes its fp32
+// partial tile to sk.part and stops; qlinear_split_reduce_kernel, the next launch on the stream,
+// adds the partials in split order and applies the epilogue.
+struct SplitArgs {
+  float* part;  // [tiles][splits][BN * BM] fp32 partial tiles
+};
+
+template <int BITS, int BN, int BM, bool PC, int NTH, int NS, bool SPLIT = false>
 __global__ __launch_bounds__(NTH, EDGERAG_GEMM_MIN_WG) void qlinear_gemm_kernel(
     const f16* __restrict__ x, int64_t xs, int32_t m, int32_t k,
     const uint8_t* __restrict__ packed, const f16* __restrict__ scales,
-    const f16* __restrict__ bias, int32_t n, int32_t g, f16* __restrict__ y, int64_t ys) {
+    const f16* __restrict__ bias, int32_t n, int32_t g, f16* __restrict__ y, int64_t ys,
+    SplitArgs sk) {
   using C = GemmCfg<BITS, BN, BM, NTH>;
   static_assert(NS % 2 == 0, "the register ring must keep the LDS buffer parity of a step");
   constexpr int NWC = C::W_K / 8, NXC = C::X_BPT / 16;  // LDS chunks this thread stages per step
@@ -845,7 +865,8 @@ __global__ __launch_bounds__(NTH, EDGERAG_GEMM_MIN_WG) void qlinear_gemm_kernel(
 #pragma unroll
     for (int j = 0; j < C::TM; ++j) acc[i][j] = f32x16{};
 
-  const int nk = k / kBK;
+  const int nk = SPLIT ? k / kBK / int(gridDim.z) : k / kBK;  // 64-k steps of this workgroup
+  const int kbase = SPLIT ? int(blockIdx.z) * nk * kBK : 0;
   const int col = lane & 31, half = lane >> 5;
   auto read_ops = [&](const _Float16* swb, const _Float16* sxb, int ks, h8 (&a)[C::TN],
                       h8 (&b)[C::TM]) {
@@ -899,9 +920,9 @@ __global__ __launch_bounds__(NTH, EDGERAG_GEMM_MIN_WG) void qlinear_gemm_kernel(
   // work cover each load's latency. The loop is unrolled by NS so that every ring index is a
   // compile-time register name (and, NS being even, every LDS buffer parity a constant).
   GemmStage<C> st[NS];
-  const int last = (nk - 1) * kBK;
+  const int last = kbase + (nk - 1) * kBK;
   auto load = [&](GemmStage<C>& dst, int t) {
-    gemm_load<C>(dst, min(t * kBK, last), wrow, srow, g, wk_off, xrow);
+    gemm_load<C>(dst, min(kbase + t * kBK, last), wrow, srow, g, wk_off, xrow);
   };
 #pragma unroll
   for (int j = 0; j < NS; ++j) load(st[j], j);
@@ -922,6 +943,24 @@ __global__ __launch_bounds__(NTH, EDGERAG_GEMM_MIN_WG) void qlinear_gemm_kernel(
       load(st[(j + 1) % NS], kt + j + NS + 1);
       issue_fence();
     }
+  }
+
+  if constexpr (SPLIT) {
+    // Register group r of tile (i, j) of wave w: 64 consecutive float4 (one per lane) at
+    // ((w TN + i) TM + j) 256 + 64 r, so the partial writes are contiguous 1 KiB stores.
+    const int tile = int(blockIdx.y * gridDim.x + blockIdx.x);
+    float4* part = reinterpret_cast<float4*>(sk.part) +
+                   (int64_t(tile) * gridDim.z + blockIdx.z) * (BN * BM / 4);
+#pragma unroll
+    for (int i = 0; i < C::TN; ++i)
+#pragma unroll
+      for (int j = 0; j < C::TM; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          part[((wave * C::TN + i) * C::TM + j) * 256 + r * 64 + lane] =
+              float4{acc[i][j][4 * r], acc[i][j][4 * r + 1], acc[i][j][4 * r + 2],
+                     acc[i][j][4 * r + 3]};
+    return;
   }
 
   // Epilogue: register 4q + r of tile (i, j) is y[mrow][nrow + r], 4 consecutive outputs per q,
@@ -1019,12 +1058,93 @@ void launch_gemm(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* 
                  const f16* scales, const f16* bias, int32_t n, int32_t g, f16* y, int64_t ys,
                  hipStream_t s) {
   const dim3 grid(unsigned((n + BN - 1) / BN), unsigned((m + BM - 1) / BM));
+  const SplitArgs none{nullptr};
   if (BITS == 8 && g == k)
     hipLaunchKernelGGL((qlinear_gemm_kernel<BITS, BN, BM, BITS == 8, NTH, NS>), grid, dim3(NTH),
-                       0, s, x, xs, m, k, packed, scales, bias, n, g, y, ys);
+                       0, s, x, xs, m, k, packed, scales, bias, n, g, y, ys, none);
   else
     hipLaunchKernelGGL((qlinear_gemm_kernel<BITS, BN, BM, false, NTH, NS>), grid, dim3(NTH), 0, s,
-                       x, xs, m, k, packed, scales, bias, n, g, y, ys);
+                       x, xs, m, k, packed, scales, bias, n, g, y, ys, none);
+}
+
+// Split-K launches use 64x64 tiles: the tile grid alone would leave CUs idle.
+constexpr int kSplitTile = 64;
+
+// Sums the split partials of the 64x64 tiles (as qlinear_gemm_kernel<..., SPLIT> wrote them, with
+// its 2 x 2 grid of 32x32 wave tiles) in split order and writes y = fp16(scale * sum + bias)
+// (PC) or fp16(sum + bias). Thread t of a tile owns float4 t: wave w = t / 256, register group
+// r = t / 64 % 4, lane l = t % 64, i.e. weight rows 32 (w % 2) + 8 r + 4 (l / 32) + 0..3 and token
+// row 32 (w / 2) + l % 32 of the tile: four consecutive outputs, one 8-byte store.
+template <bool PC>
+__global__ __launch_bounds__(256) void qlinear_split_reduce_kernel(
+    const float4* __restrict__ part, int32_t splits, int32_t tiles_x, int32_t m, int32_t n,
+    const f16* __restrict__ scales, const f16* __restrict__ bias, f16* __restrict__ y,
+    int64_t ys) {
+  constexpr int kTileF4 = kSplitTile * kSplitTile / 4;  // 1024 float4 per tile
+  const int tile = int(blockIdx.x) / (kTileF4 / 256);
+  const int t = (int(blockIdx.x) % (kTileF4 / 256)) * 256 + int(threadIdx.x);
+  const int w = t / 256, r = (t / 64) % 4, l = t % 64;
+  const int nrow = (tile % tiles_x) * kSplitTile + 32 * (w % 2) + 8 * r + 4 * (l / 32);
+  const int mrow = (tile / tiles_x) * kSplitTile + 32 * (w / 2) + l % 32;
+  const float4* p = part + int64_t(tile) * splits * kTileF4 + t;
+  float4 sum = p[0];
+  for (int z = 1; z < splits; ++z) {
+    const float4 v = p[int64_t(z) * kTileF4];
+    sum.x += v.x;
+    sum.y += v.y;
+    sum.z += v.z;
+    sum.w += v.w;
+  }
+  if (mrow >= m) return;
+  const float s4[4] = {sum.x, sum.y, sum.z, sum.w};
+  float v[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int row = min(nrow + q, n - 1);
+    const float sc = PC ? __half2float(scales[row]) : 1.f;
+    const float b = bias != nullptr ? __half2float(bias[row]) : 0.f;
+    v[q] = PC ? sc * s4[q] + b : s4[q] + b;
+  }
+  f16* yr = y + int64_t(mrow) * ys;
+  if (nrow + 3 < n && (ys % 4) == 0 && (reinterpret_cast<uintptr_t>(y) & 7) == 0) {
+    const h2 lo = {_Float16(v[0]), _Float16(v[1])}, hi = {_Float16(v[2]), _Float16(v[3])};
+    *reinterpret_cast<uint2*>(yr + nrow) = uint2{as_u32(lo), as_u32(hi)};
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (nrow + q < n) yr[nrow + q] = __float2half_rn(v[q]);
+  }
+}
+
+template <int BITS>
+void launch_gemm_split(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
+                       const f16* scales, const f16* bias, int32_t n, int32_t g, f16* y,
+                       int64_t ys, const SplitPlan& p, void* ws, hipStream_t s) {
+  const int tiles_x = (n + kSplitTile - 1) / kSplitTile;
+  const dim3 grid(unsigned(tiles_x), unsigned((m + kSplitTile - 1) / kSplitTile),
+                  unsigned(p.splits));
+  float* part = static_cast<float*>(ws);
+  const SplitArgs sk{part};
+  constexpr int T = kSplitTile;
+  const bool pc = BITS == 8 && g == k;
+  if (pc)
+    hipLaunchKernelGGL((qlinear_gemm_kernel<BITS, T, T, BITS == 8, EDGERAG_GEMM_THREADS_64,
+                                            EDGERAG_GEMM_STAGES_64, true>),
+                       grid, dim3(EDGERAG_GEMM_THREADS_64), 0, s, x, xs, m, k, packed, scales,
+                       bias, n, g, y, ys, sk);
+  else
+    hipLaunchKernelGGL((qlinear_gemm_kernel<BITS, T, T, false, EDGERAG_GEMM_THREADS_64,
+                                            EDGERAG_GEMM_STAGES_64, true>),
+                       grid, dim3(EDGERAG_GEMM_THREADS_64), 0, s, x, xs, m, k, packed, scales,
+                       bias, n, g, y, ys, sk);
+  const unsigned rblocks = unsigned(int64_t(grid.x) * grid.y * (T * T / 4 / 256));
+  const float4* part4 = reinterpret_cast<const float4*>(part);
+  if (pc)
+    hipLaunchKernelGGL((qlinear_split_reduce_kernel<true>), dim3(rblocks), dim3(256), 0, s, part4,
+                       p.splits, tiles_x, m, n, scales, bias, y, ys);
+  else
+    hipLaunchKernelGGL((qlinear_split_reduce_kernel<false>), dim3(rblocks), dim3(256), 0, s,
+                       part4, p.splits, tiles_x, m, n, scales, bias, y, ys);
 }
 
 // The streaming kernel's shape: k-slices F and row tiles NT from N alone (two k-slices when
@@ -1243,6 +1363,72 @@ void dispatch(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* pac
 }
 
 }  // namespace
+
+// The workspace route of the tiled GEMM (edgerag_quant_linear_ws): batches of 17..64 tokens where
+// the streaming / skinny GEMV, which re-reads every activation row once per 16-row tile, is
+// slower (measured crossovers on MI355X, config-4 and config-5 shapes: from 17 tokens for
+// K >= 4096 or N >= 16384, from 40 tokens for layers of more than 4M codes, from 64 tokens for
+// 2M..4M codes, never for smaller ones), and larger M whose 64x64 tile grid leaves CUs idle. Its
+// time is modelled in 64-k steps of one workgroup:
+//   cost(s) = fixed(s) + (steps per split) x (rounds of workgroups over the 256 CUs),
+// fixed(1) = 0 and fixed(s > 1) = EDGERAG_SPLITK_FIXED_STEPS (the partial tiles' round trip and
+// the second launch); the plan takes the cheapest s of 1, 2, 4, .. EDGERAG_SPLITK_MAX (each split
+// at least EDGERAG_SPLITK_MIN_STEPS steps, all splits equal).
+SplitPlan qlinear_split_plan(int32_t m, int32_t k, int32_t n, int32_t bits, int32_t g) {
+  SplitPlan p{0, 0};
+  if (m < 17 || n <= 0 || k % kBK != 0) return p;
+  if ((bits != 8 && bits != 4) || g % 32 != 0) return p;
+  const int64_t tiles = int64_t((n + kSplitTile - 1) / kSplitTile) *
+                        ((m + kSplitTile - 1) / kSplitTile);
+  if (m > EDGERAG_SKINNY_MAX_M) {
+    // Larger M: only where the plain launch would also use 64x64 tiles.
+    const int64_t t128x64 = int64_t((n + 127) / 128) * ((m + 63) / 64);
+    if (t128x64 >= EDGERAG_GEMM_TARGET_WGS) return p;
+  } else if (m < 40) {
+    if (k < 4096 && n < 16384) return p;
+  } else {
+    const int64_t codes = int64_t(n) * k;
+    if (codes <= (int64_t(1) << 22) && (m < 64 || codes < (int64_t(1) << 21))) return p;
+  }
+  const int nk = k / kBK;
+  auto rounds = [&](int64_t wgs) {
+    return (wgs + EDGERAG_GEMM_TARGET_WGS - 1) / EDGERAG_GEMM_TARGET_WGS;
+  };
+  int best = 1;
+  int64_t best_cost = int64_t(nk) * rounds(tiles);
+  for (int sp = 2; sp <= EDGERAG_SPLITK_MAX; sp *= 2) {
+    if (nk % sp != 0 || nk / sp < EDGERAG_SPLITK_MIN_STEPS) break;
+    const int64_t cost = EDGERAG_SPLITK_FIXED_STEPS + int64_t(nk / sp) * rounds(tiles * sp);
+    if (cost < best_cost) {
+      best = sp;
+      best_cost = cost;
+    }
+  }
+  p.splits = best;
+  p.bytes = best > 1 ? tiles * best * kSplitTile * kSplitTile * 4 : 0;
+  return p;
+}
+
+bool launch_qlinear_split(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
+                          const f16* scales, const f16* bias, int32_t n, int32_t bits, int32_t g,
+                          f16* y, int64_t ys, void* ws, int64_t ws_bytes, hipStream_t s) {
+  const SplitPlan p = qlinear_split_plan(m, k, n, bits, g);
+  if (p.splits < 1 || (p.splits > 1 && (ws == nullptr || ws_bytes < p.bytes))) return false;
+  constexpr int T = kSplitTile;
+  if (p.splits == 1) {
+    if (bits == 8)
+      launch_gemm<8, T, T, EDGERAG_GEMM_THREADS_64, EDGERAG_GEMM_STAGES_64>(
+          x, xs, m, k, packed, scales, bias, n, g, y, ys, s);
+    else
+      launch_gemm<4, T, T, EDGERAG_GEMM_THREADS_64, EDGERAG_GEMM_STAGES_64>(
+          x, xs, m, k, packed, scales, bias, n, g, y, ys, s);
+  } else if (bits == 8) {
+    launch_gemm_split<8>(x, xs, m, k, packed, scales, bias, n, g, y, ys, p, ws, s);
+  } else {
+    launch_gemm_split<4>(x, xs, m, k, packed, scales, bias, n, g, y, ys, p, ws, s);
+  }
+  return true;
+}
 
 bool qlinear_mfma_supported(int32_t k, int32_t bits, int32_t g, const void* x, int64_t x_stride,
                             const void* packed) {

@@ -206,6 +206,28 @@ def attention_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return buf
 
 
+_QUANT_WORKSPACES: dict[torch.device, torch.Tensor] = {}
+
+
+def quant_workspace(device: torch.device) -> torch.Tensor:
+    """The per-device split-K workspace of the quant linears: the largest any shape uses,
+    allocated once and never replaced (a HIP graph that captured a launch keeps using the same
+    buffer). Launches that share it must be ordered on one stream."""
+    device = torch.device(device)
+    if device.type == "cuda" and device.index is None:
+        device = torch.device("cuda", torch.cuda.current_device())
+    buf = _QUANT_WORKSPACES.get(device)
+    if buf is None:
+        buf = torch.empty(_lib.QUANT_WORKSPACE_MAX, dtype=torch.uint8, device=device)
+        _QUANT_WORKSPACES[device] = buf
+    return buf
+
+
+def quant_workspace_bytes(m: int, k: int, n: int, bits: int, group_size: int) -> int:
+    """Workspace bytes the split-K quant linear uses for this shape (0: it does not split)."""
+    return int(_lib.load().edgerag_quant_linear_workspace_bytes(m, k, n, bits, group_size))
+
+
 def make_plan_host(
     query_start_loc: np.ndarray,
     context_lens: np.ndarray,
@@ -691,7 +713,8 @@ def quant_linear_rope_append(
     if norm is not None and not fused:
         raise ValueError("a normed input needs the one-launch path (decode batch, rope rows)")
     if not fused:
-        qkv = quant_linear(x2, packed, scales, bias, in_features, n, bits, group_size)
+        qkv = quant_linear(x2, packed, scales, bias, in_features, n, bits, group_size,
+                           split_k=False)
         return rope_append(qkv, positions, cos, sin, n_q_heads, n_kv_heads, head_dim, slots,
                            key_pool, value_pool, q_out=q_out)
     _check_pool(key_pool, "key_pool")
@@ -776,7 +799,8 @@ def quant_linear_swiglu(
     if norm is not None and not fused:
         raise ValueError("a normed input needs the one-launch path (decode batch)")
     if not fused:
-        gu = quant_linear(x2, packed, scales, bias, in_features, out_features, bits, group_size)
+        gu = quant_linear(x2, packed, scales, bias, in_features, out_features, bits, group_size,
+                          split_k=False)
         return silu_mul(gu, inter, out=out)
     y = out if out is not None else torch.empty((m, inter), dtype=x.dtype, device=x.device)
     if y.shape != (m, inter) or y.stride(1) != 1:
@@ -838,8 +862,13 @@ def quant_linear(
     bits: int,
     group_size: int,
     out: torch.Tensor | None = None,
+    split_k: bool = True,
 ) -> torch.Tensor:
-    """``x (..., K) -> (..., N)`` through the fused dequant + GEMV/GEMM kernels."""
+    """``x (..., K) -> (..., N)`` through the fused dequant + GEMV/GEMM kernels.
+
+    ``split_k``: shapes whose tile grid would leave CUs idle split K over the per-device
+    workspace (``edgerag_quant_linear_ws``); False runs ``edgerag_quant_linear``, whose bits the
+    fused-epilogue launches reproduce exactly."""
     require_device(x, packed, scales, bias)
     if x.shape[-1] != in_features:
         raise ValueError(f"input has {x.shape[-1]} features, layer expects {in_features}")
@@ -858,9 +887,12 @@ def quant_linear(
         scales = scales.to(torch.float16)
     if bias is not None and bias.dtype != torch.float16:
         bias = bias.to(torch.float16)
-    call(
-        "edgerag_quant_linear", x2.data_ptr(), dtype_code(x2.dtype), x2.stride(0), m,
-        in_features, packed.data_ptr(), scales.contiguous().data_ptr(), ptr(bias),
-        out_features, bits, group_size, y.data_ptr(), y.stride(0), stream_ptr(x.device),
-    )
+    args = (x2.data_ptr(), dtype_code(x2.dtype), x2.stride(0), m, in_features, packed.data_ptr(),
+            scales.contiguous().data_ptr(), ptr(bias), out_features, bits, group_size,
+            y.data_ptr(), y.stride(0))
+    if split_k:
+        ws = quant_workspace(x.device)
+        call("edgerag_quant_linear_ws", *args, ws.data_ptr(), ws.numel(), stream_ptr(x.device))
+    else:
+        call("edgerag_quant_linear", *args, stream_ptr(x.device))
     return y.view(*lead, out_features)

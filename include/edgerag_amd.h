@@ -257,6 +257,31 @@ int edgerag_quant_linear(const void* x, int32_t x_dtype, int64_t x_stride, int32
                          void* stream);
 
 /*
+ * edgerag_quant_linear with a workspace, for the shapes where the tiled GEMM beats the streaming
+ * GEMV (decode batches of 17..64 tokens on large layers, 40..64 tokens on most) or where the tiled
+ * GEMM's output tiles would not fill the GPU (larger M on narrow layers). There the 64x64-tile
+ * GEMM runs, with K cut into 2..16 equal ranges when a cost model says the GPU needs them: one
+ * launch writes each range's fp32 partial tiles to the workspace, a second adds them in range
+ * order and writes y (the same bits on every run). Results equal edgerag_quant_linear's to the
+ * linear tolerance (the fp32 sums are ordered differently), not bit for bit.
+ *
+ * workspace: at least edgerag_quant_linear_workspace_bytes(M, K, N, bits, group_size) bytes, any
+ * contents. Launches that share a workspace must be ordered (one stream). With a smaller or NULL
+ * workspace, or a shape that does not split, this is edgerag_quant_linear.
+ *
+ * Replaces QuantLinear.forward (edgerag/core/linear.py:194-196), as edgerag_quant_linear does.
+ */
+int edgerag_quant_linear_ws(const void* x, int32_t x_dtype, int64_t x_stride, int32_t m, int32_t k,
+                            const uint8_t* packed, const void* scales_f16, const void* bias_f16,
+                            int32_t n, int32_t bits, int32_t group_size, void* y, int64_t y_stride,
+                            void* workspace, int64_t workspace_bytes, void* stream);
+/* Workspace bytes edgerag_quant_linear_ws uses for this shape: 0 when it does not split K, and
+ * never more than EDGERAG_QUANT_WORKSPACE_MAX. */
+int64_t edgerag_quant_linear_workspace_bytes(int32_t m, int32_t k, int32_t n, int32_t bits,
+                                             int32_t group_size);
+#define EDGERAG_QUANT_WORKSPACE_MAX (8 * 1024 * 1024)
+
+/*
  * SwiGLU through one launch: W = [gate; up] is the packed INT8 per-channel weight of N = 2 I rows
  * (gate rows 0..I-1, up rows I..N-1), and
  *   y[t][j] = fp16(fp16(silu(g)) * u),  g = (x . W^T + bias)[t][j],  u = (...)[t][I + j]

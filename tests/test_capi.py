@@ -23,7 +23,8 @@ def declared_symbols() -> set[str]:
     names: set[str] = set()
     for header in HEADERS:
         text = header.read_text()
-        names |= set(re.findall(r"^(?:int|const char\*)\s+(edgerag_\w+)\s*\(", text, flags=re.M))
+        names |= set(re.findall(r"^(?:int64_t|int|const char\*)\s+(edgerag_\w+)\s*\(", text,
+                                flags=re.M))
     return names
 
 
@@ -54,6 +55,31 @@ def test_swiglu_support_query() -> None:
     assert q(F16, 8, 2048, 16384, 8, 128, 0) == 0  # grouped INT8
     assert q(F32, 8, 2048, 16384, 8, 2048, 0) == 0
     assert q(F16, 8, 200, 16384, 8, 200, 0) == 0  # K not a multiple of 64
+
+
+def test_quant_workspace_query() -> None:
+    """The workspace route is planned on the host. For decode batches past the streaming GEMV's
+    crossover, and for larger M whose 64x64 tile grid leaves CUs idle, the tiled GEMM splits K
+    where its cost model (a fixed 20 steps for the partials' round trip, plus 64-k steps per
+    split times rounds of workgroups over the 256 CUs) says so; the workspace holds the fp32
+    partial tiles."""
+    q = kernels.quant_workspace_bytes
+    tile = 64 * 64 * 4
+    assert q(64, 8192, 2048, 8, 8192) == 32 * 8 * tile  # 32 tiles x 8 splits: 20 + 16 steps
+    assert q(64, 2048, 2048, 8, 2048) == 32 * 8 * tile  # 20 + 4 steps, against 32
+    assert q(128, 2048, 2048, 8, 2048) == 64 * 4 * tile  # 64 tiles x 4
+    assert q(64, 2048, 8192, 8, 2048) == 0  # 128 tiles: 32 steps unsplit beat 20 + 16
+    assert q(40, 1152, 4608, 4, 128) == 0  # INT4: 18 steps, too few to pay for a split
+    assert q(24, 8192, 2048, 8, 8192) == 32 * 8 * tile  # K >= 4096: from 17 tokens
+    assert q(32, 2048, 2048, 8, 2048) == 0  # below 40 tokens on small layers: streaming GEMV
+    assert q(48, 2048, 2048, 8, 2048) == 0  # 4M codes: from 64 tokens
+    assert q(64, 1152, 1152, 4, 128) == 0  # 1.3M codes: the skinny GEMV at every batch size
+    assert q(16, 8192, 2048, 8, 8192) == 0
+    assert q(512, 2048, 8192, 8, 2048) == 0  # 128x64 tiles fill the GPU: the plain launch
+    assert q(64, 128, 2048, 8, 128) == 0  # two 64-k steps: nothing to split
+    assert q(64, 2048, 2048, 8, 48) == 0  # group not a multiple of 32
+    for args in [(64, 8192, 2048, 8, 8192), (40, 1152, 37, 4, 128), (300, 8192, 64, 8, 8192)]:
+        assert 0 <= q(*args) <= _lib.QUANT_WORKSPACE_MAX
 
 
 def test_rope_append_support_query() -> None:

@@ -183,7 +183,7 @@ def test_quant_linear_swiglu_fused(device, k, n, with_bias) -> None:
         xfull = torch.randn(m, k + 64, generator=seeded(m * 29 + k)).half()
         xd = xfull.to(device)[:, :k]
         fused = kernels.quant_linear_swiglu(xd, pd, sd, bd, k, n, 8, k)
-        gu = kernels.quant_linear(xd, pd, sd, bd, k, n, 8, k)
+        gu = kernels.quant_linear(xd, pd, sd, bd, k, n, 8, k, split_k=False)
         plain = kernels.silu_mul(gu, inter)
         assert fused.shape == (m, inter)
         assert torch.equal(fused, plain), f"M={m}: fused SwiGLU differs from projection + silu_mul"
@@ -260,7 +260,7 @@ def test_quant_linear_swiglu_falls_back_outside_its_shapes(device) -> None:
         x = torch.randn(m, k, generator=seeded(m + bits)).half().to(device)
         pd, sd = packed.to(device), scales.to(device)
         y = kernels.quant_linear_swiglu(x, pd, sd, None, k, n, bits, g)
-        gu = kernels.quant_linear(x, pd, sd, None, k, n, bits, g)
+        gu = kernels.quant_linear(x, pd, sd, None, k, n, bits, g, split_k=False)
         assert torch.equal(y, kernels.silu_mul(gu, n // 2))
     with pytest.raises(kernels._lib.EdgeragError, match="not covered"):
         kernels.call("edgerag_quant_linear_swiglu", x.data_ptr(), 1, k, 4, k, pd.data_ptr(),
@@ -288,7 +288,7 @@ def test_quant_linear_residual(device, k, n, with_bias) -> None:
         g = seeded(m + k + n)
         x = torch.randn(m, k, generator=g).half().to(device)
         hidden0 = (torch.randn(m, n, generator=g) * 4).half()
-        y = kernels.quant_linear(x, pd, sd, bd, k, n, 8, k).cpu()
+        y = kernels.quant_linear(x, pd, sd, bd, k, n, 8, k, split_k=False).cpu()
         expected = (hidden0.float() + y.float()).half()
         hidden = hidden0.to(device)
         partials = torch.full((m * parts,), float("nan"), dtype=torch.float32, device=device)
@@ -408,3 +408,93 @@ def test_quant_linear_int8_per_channel_streaming(device, k, n) -> None:
             y1 = kernels.quant_linear(xfull.to(device)[m - 1 : m, :k], packed.to(device),
                                       scales.to(device), bias.to(device), k, n, 8, k)
             assert torch.equal(y1[0], y[m - 1])
+
+
+SPLIT_SHAPES = [  # (K, N, bits, group): 64x64 tile grids below 256 workgroups (the workspace
+    # route: unsplit or split K by the cost model)
+    (8192, 2048, 8, 8192),
+    (2048, 2048, 8, 2048),
+    (2048, 8192, 8, 2048),
+    (1152, 4608, 4, 128),
+    (1152, 1152, 4, 128),
+    (512, 200, 8, 64),  # grouped INT8, N off the tile
+    (2048, 37, 4, 128),
+]
+
+
+def _split_case(k, n, bits, g, m, seed):
+    w = _weight(n, k, seed)
+    cfg = oq.QuantConfig(g, bits)
+    packed, scales = oq.quantize_for_layer(w, cfg)
+    bias = (torch.randn(n, generator=seeded(seed + 1)) * 0.1).half()
+    x = torch.randn(m, k, generator=seeded(seed + 2)).half()
+    return x, packed, scales, bias, cfg
+
+
+@pytest.mark.parametrize("k,n,bits,g", SPLIT_SHAPES)
+@pytest.mark.parametrize("m", [17, 32, 33, 64, 100, 130])
+def test_quant_linear_split_k(device, k, n, bits, g, m) -> None:
+    """The workspace route of the tiled GEMM (kernels.quant_linear passes its workspace; split K
+    or not) against the oracle's dequant-then-matmul. It is deterministic (partials are added in
+    k-range order: two runs give the same bits)."""
+    x, packed, scales, bias, cfg = _split_case(k, n, bits, g, m, k + n + m)
+    if m >= 33 and (k, n) == (8192, 2048):
+        assert kernels.quant_workspace_bytes(m, k, n, bits, g) > 0, "the down projection splits K"
+    expected = oq.quant_linear_reference(x, packed, scales, bias, k, cfg)
+    args = (packed.to(device), scales.to(device), bias.to(device), k, n, bits, g)
+    y1 = kernels.quant_linear(x.to(device), *args)
+    y2 = kernels.quant_linear(x.to(device), *args)
+    torch.testing.assert_close(y1.float().cpu(), expected, **LINEAR_TOL)
+    assert torch.equal(y1, y2)
+
+
+def test_quant_linear_ws_without_room_is_the_plain_launch(device) -> None:
+    """A workspace below the plan's size (or none) runs edgerag_quant_linear: the same bits."""
+    from edgerag_amd import _lib
+
+    k, n, bits, g, m = 8192, 2048, 8, 8192, 64
+    x, packed, scales, bias, _ = _split_case(k, n, bits, g, m, 3)
+    x, packed, scales, bias = (t.to(device) for t in (x, packed, scales, bias))
+    need = kernels.quant_workspace_bytes(m, k, n, bits, g)
+    assert need > 0
+    ws = torch.full((need,), 0xFF, dtype=torch.uint8, device=device)  # any contents
+    outs = []
+    for name, extra in [("edgerag_quant_linear", ()),
+                        ("edgerag_quant_linear_ws", (ws.data_ptr(), need - 1)),
+                        ("edgerag_quant_linear_ws", (0, 0)),
+                        ("edgerag_quant_linear_ws", (ws.data_ptr(), need))]:
+        y = torch.empty(m, n, dtype=torch.float16, device=device)
+        _lib.call(name, x.data_ptr(), 1, x.stride(0), m, k, packed.data_ptr(), scales.data_ptr(),
+                  bias.data_ptr(), n, bits, g, y.data_ptr(), y.stride(0), *extra,
+                  kernels.stream_ptr(device))
+        outs.append(y)
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+    torch.testing.assert_close(outs[3].float(), outs[0].float(), **LINEAR_TOL)
+
+
+def test_quant_linear_split_k_graph_replays(device) -> None:
+    """Captured in a HIP graph, the split-K launch replays to the eager bits every time, with
+    eager launches that share the workspace between the replays."""
+    k, n, bits, g, m = 8192, 2048, 8, 8192, 48
+    x, packed, scales, bias, _ = _split_case(k, n, bits, g, m, 5)
+    x, packed, scales, bias = (t.to(device) for t in (x, packed, scales, bias))
+    x2 = torch.randn(33, 2048, generator=seeded(6)).half().to(device)
+    p2, s2 = oq.quantize_for_layer(_weight(2048, 2048, 7), oq.QuantConfig(2048, 8))
+    p2, s2 = p2.to(device), s2.to(device)
+    eager = kernels.quant_linear(x, packed, scales, bias, k, n, bits, g)
+    eager2 = kernels.quant_linear(x2, p2, s2, None, 2048, 2048, 8, 2048)
+    out = torch.empty_like(eager)
+    stream = torch.cuda.Stream(device)
+    stream.wait_stream(torch.cuda.current_stream(device))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        kernels.quant_linear(x, packed, scales, bias, k, n, bits, g, out=out)
+        with torch.cuda.graph(graph, stream=stream):
+            kernels.quant_linear(x, packed, scales, bias, k, n, bits, g, out=out)
+    torch.cuda.current_stream(device).wait_stream(stream)
+    for _ in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        assert torch.equal(kernels.quant_linear(x2, p2, s2, None, 2048, 2048, 8, 2048), eager2)
