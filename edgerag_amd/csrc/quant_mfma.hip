@@ -66,7 +66,7 @@
 #define EDGERAG_SPLITK_MIN_STEPS 2  // fewest 64-k steps per split
 #endif
 #ifndef EDGERAG_SPLITK_FIXED_STEPS
-#define EDGERAG_SPLITK_FIXED_STEPS 20  // cost of a split launch's partials and second launch
+#define EDGERAG_SPLITK_FIXED_STEPS 12  // cost of a split launch's partials and second launch
 #endif
 #ifndef EDGERAG_GEMM_TARGET_WGS
 #define EDGERAG_GEMM_TARGET_WGS 256  // the tile is the largest whose grid reaches this many
@@ -1069,15 +1069,16 @@ void launch_gemm(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* 
 
 // Split-K launches use 64x64 tiles: the tile grid alone would leave CUs idle.
 constexpr int kSplitTile = 64;
+static_assert(EDGERAG_SPLITK_MAX <= 16, "the reduce launch is instantiated for 2, 4, 8, 16 splits");
 
 // Sums the split partials of the 64x64 tiles (as qlinear_gemm_kernel<..., SPLIT> wrote them, with
 // its 2 x 2 grid of 32x32 wave tiles) in split order and writes y = fp16(scale * sum + bias)
 // (PC) or fp16(sum + bias). Thread t of a tile owns float4 t: wave w = t / 256, register group
 // r = t / 64 % 4, lane l = t % 64, i.e. weight rows 32 (w % 2) + 8 r + 4 (l / 32) + 0..3 and token
 // row 32 (w / 2) + l % 32 of the tile: four consecutive outputs, one 8-byte store.
-template <bool PC>
+template <bool PC, int S>
 __global__ __launch_bounds__(256) void qlinear_split_reduce_kernel(
-    const float4* __restrict__ part, int32_t splits, int32_t tiles_x, int32_t m, int32_t n,
+    const float4* __restrict__ part, int32_t tiles_x, int32_t m, int32_t n,
     const f16* __restrict__ scales, const f16* __restrict__ bias, f16* __restrict__ y,
     int64_t ys) {
   constexpr int kTileF4 = kSplitTile * kSplitTile / 4;  // 1024 float4 per tile
@@ -1086,14 +1087,17 @@ __global__ __launch_bounds__(256) void qlinear_split_reduce_kernel(
   const int w = t / 256, r = (t / 64) % 4, l = t % 64;
   const int nrow = (tile % tiles_x) * kSplitTile + 32 * (w % 2) + 8 * r + 4 * (l / 32);
   const int mrow = (tile / tiles_x) * kSplitTile + 32 * (w / 2) + l % 32;
-  const float4* p = part + int64_t(tile) * splits * kTileF4 + t;
-  float4 sum = p[0];
-  for (int z = 1; z < splits; ++z) {
-    const float4 v = p[int64_t(z) * kTileF4];
-    sum.x += v.x;
-    sum.y += v.y;
-    sum.z += v.z;
-    sum.w += v.w;
+  const float4* p = part + int64_t(tile) * S * kTileF4 + t;
+  float4 pv[S];
+#pragma unroll
+  for (int z = 0; z < S; ++z) pv[z] = p[int64_t(z) * kTileF4];  // all loads in flight
+  float4 sum = pv[0];
+#pragma unroll
+  for (int z = 1; z < S; ++z) {
+    sum.x += pv[z].x;
+    sum.y += pv[z].y;
+    sum.z += pv[z].z;
+    sum.w += pv[z].w;
   }
   if (mrow >= m) return;
   const float s4[4] = {sum.x, sum.y, sum.z, sum.w};
@@ -1139,12 +1143,22 @@ void launch_gemm_split(const f16* x, int64_t xs, int32_t m, int32_t k, const uin
                        bias, n, g, y, ys, sk);
   const unsigned rblocks = unsigned(int64_t(grid.x) * grid.y * (T * T / 4 / 256));
   const float4* part4 = reinterpret_cast<const float4*>(part);
-  if (pc)
-    hipLaunchKernelGGL((qlinear_split_reduce_kernel<true>), dim3(rblocks), dim3(256), 0, s, part4,
-                       p.splits, tiles_x, m, n, scales, bias, y, ys);
-  else
-    hipLaunchKernelGGL((qlinear_split_reduce_kernel<false>), dim3(rblocks), dim3(256), 0, s,
-                       part4, p.splits, tiles_x, m, n, scales, bias, y, ys);
+#define EDGERAG_SPLIT_REDUCE(SPLITS)                                                              \
+  do {                                                                                            \
+    if (pc)                                                                                       \
+      hipLaunchKernelGGL((qlinear_split_reduce_kernel<true, SPLITS>), dim3(rblocks), dim3(256),   \
+                         0, s, part4, tiles_x, m, n, scales, bias, y, ys);                        \
+    else                                                                                          \
+      hipLaunchKernelGGL((qlinear_split_reduce_kernel<false, SPLITS>), dim3(rblocks), dim3(256),  \
+                         0, s, part4, tiles_x, m, n, scales, bias, y, ys);                        \
+  } while (0)
+  switch (p.splits) {
+    case 2: EDGERAG_SPLIT_REDUCE(2); break;
+    case 4: EDGERAG_SPLIT_REDUCE(4); break;
+    case 8: EDGERAG_SPLIT_REDUCE(8); break;
+    default: EDGERAG_SPLIT_REDUCE(16); break;
+  }
+#undef EDGERAG_SPLIT_REDUCE
 }
 
 // The streaming kernel's shape: k-slices F and row tiles NT from N alone (two k-slices when

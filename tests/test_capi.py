@@ -60,15 +60,15 @@ def test_swiglu_support_query() -> None:
 def test_quant_workspace_query() -> None:
     """The workspace route is planned on the host. For decode batches past the streaming GEMV's
     crossover, and for larger M whose 64x64 tile grid leaves CUs idle, the tiled GEMM splits K
-    where its cost model (a fixed 20 steps for the partials' round trip, plus 64-k steps per
+    where its cost model (a fixed 12 steps for the partials' round trip, plus 64-k steps per
     split times rounds of workgroups over the 256 CUs) says so; the workspace holds the fp32
     partial tiles."""
     q = kernels.quant_workspace_bytes
     tile = 64 * 64 * 4
-    assert q(64, 8192, 2048, 8, 8192) == 32 * 8 * tile  # 32 tiles x 8 splits: 20 + 16 steps
-    assert q(64, 2048, 2048, 8, 2048) == 32 * 8 * tile  # 20 + 4 steps, against 32
+    assert q(64, 8192, 2048, 8, 8192) == 32 * 8 * tile  # 32 tiles x 8 splits: 12 + 16 steps
+    assert q(64, 2048, 2048, 8, 2048) == 32 * 8 * tile  # 12 + 4 steps, against 32
     assert q(128, 2048, 2048, 8, 2048) == 64 * 4 * tile  # 64 tiles x 4
-    assert q(64, 2048, 8192, 8, 2048) == 0  # 128 tiles: 32 steps unsplit beat 20 + 16
+    assert q(64, 2048, 8192, 8, 2048) == 128 * 2 * tile  # 128 tiles: 12 + 16 steps beat 32
     assert q(40, 1152, 4608, 4, 128) == 0  # INT4: 18 steps, too few to pay for a split
     assert q(24, 8192, 2048, 8, 8192) == 32 * 8 * tile  # K >= 4096: from 17 tokens
     assert q(32, 2048, 2048, 8, 2048) == 0  # below 40 tokens on small layers: streaming GEMV
