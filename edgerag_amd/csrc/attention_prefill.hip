@@ -34,7 +34,13 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kD = 64;
-constexpr unsigned kSharedLdsPad = 48 * 1024;
+#ifndef EDGERAG_ATTN_SHARED_PAD_KB
+#define EDGERAG_ATTN_SHARED_PAD_KB 48  // dynamic LDS of a shared-mode tile workgroup
+#endif
+#ifndef EDGERAG_ATTN_SHARED_TILES_PER_CU
+#define EDGERAG_ATTN_SHARED_TILES_PER_CU 1  // tile workgroups per CU that the pad allows
+#endif
+constexpr unsigned kSharedLdsPad = EDGERAG_ATTN_SHARED_PAD_KB * 1024;
 constexpr int kKeys = 64;            // keys per LDS tile
 constexpr int kRow = 64;             // halves per LDS row (K: one key; V^T: one dim)
 constexpr float kRescaleLog2 = 8.f;  // lazy rescale: p may grow to 2^8 before the max moves
@@ -46,8 +52,10 @@ constexpr int kVPairs = (kKeys / 4) * (kD / 8);  // (key quad, dim chunk) pairs 
 constexpr int kVPerThread = (kVPairs + kThreads - 1) / kThreads;
 static_assert(kKChunks % kThreads == 0, "K staging split");
 constexpr unsigned kStaticLds = 2 * kKeys * kRow * 2 + 2 * kD * kRow * 2 + kMaxTileBlocks * 4;
-static_assert(2 * (kStaticLds + kSharedLdsPad) > 160 * 1024 && kStaticLds + kSharedLdsPad <= 160 * 1024,
-              "shared mode: exactly one tile workgroup per CU");
+constexpr unsigned kSharedTiles = EDGERAG_ATTN_SHARED_TILES_PER_CU;
+static_assert((kSharedTiles + 1) * (kStaticLds + kSharedLdsPad) > 160 * 1024 &&
+                  kSharedTiles * (kStaticLds + kSharedLdsPad) <= 160 * 1024,
+              "shared mode: the pad must leave room for exactly kSharedTiles tile workgroups per CU");
 
 // Byte offset handed to buffer loads for keys with no valid block: beyond num_records, so the
 // load returns zeros without a branch (the launcher keeps a head's pool slice below it).
