@@ -85,6 +85,7 @@ SIGNATURES: dict[str, tuple[list, object]] = {
         c_i32,
     ),
     "edgerag_silu_mul": ([c_vp, c_i64, c_i32, c_i32, c_vp, c_i64, c_i32, c_vp], c_i32),
+    "edgerag_argmax_rows": ([c_vp, c_i32, c_i32, c_i32, c_i64, c_vp, c_vp], c_i32),
     "edgerag_quantize": ([c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp, c_vp], c_i32),
     "edgerag_dequantize": ([c_vp, c_vp, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp], c_i32),
     "edgerag_quant_linear": (

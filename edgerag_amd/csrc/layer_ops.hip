@@ -274,6 +274,73 @@ int launch_rmsnorm(const void* x, const void* delta, const void* weight, void* h
   return check_launch("edgerag_rmsnorm");
 }
 
+// Greedy token choice: out[r] = argmax_j x[r][j], the first index of the maximum (torch.argmax's
+// choice; a NaN counts as larger than every number, and the first NaN wins). One 1024-thread
+// workgroup per row, 16-byte loads when the row allows them; lanes, then waves, reduce
+// (value, index) pairs with the same rule.
+__device__ __forceinline__ bool argmax_better(float v, int i, float bv, int bi) {
+  if (v != v) return bv == bv || i < bi;  // NaN
+  if (bv != bv) return false;
+  return v > bv || (v == bv && i < bi);
+}
+
+template <typename T>
+__global__ __launch_bounds__(1024) void argmax_rows_kernel(const T* __restrict__ x, int64_t stride,
+                                                           int32_t cols, bool vec,
+                                                           int32_t* __restrict__ out) {
+  constexpr int VEC = 16 / int(sizeof(T));
+  const T* row = x + int64_t(blockIdx.x) * stride;
+  float bv = -INFINITY;
+  int bi = INT32_MAX;
+  if (vec) {
+    for (int j = int(threadIdx.x) * VEC; j < cols; j += 1024 * VEC) {
+      const uint4 raw = *reinterpret_cast<const uint4*>(row + j);
+      const T* e = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+      for (int q = 0; q < VEC; ++q) {
+        const float v = to_f32<T>(e[q]);
+        if (argmax_better(v, j + q, bv, bi)) {
+          bv = v;
+          bi = j + q;
+        }
+      }
+    }
+  } else {
+    for (int j = int(threadIdx.x); j < cols; j += 1024) {
+      const float v = to_f32<T>(row[j]);
+      if (argmax_better(v, j, bv, bi)) {
+        bv = v;
+        bi = j;
+      }
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off /= 2) {
+    const float ov = __shfl_xor(bv, off);
+    const int oi = __shfl_xor(bi, off);
+    if (argmax_better(ov, oi, bv, bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  __shared__ float wv[16];
+  __shared__ int wi[16];
+  const int wave = int(threadIdx.x) / kWave;
+  if (threadIdx.x % kWave == 0) {
+    wv[wave] = bv;
+    wi[wave] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 16; ++w)
+      if (argmax_better(wv[w], wi[w], bv, bi)) {
+        bv = wv[w];
+        bi = wi[w];
+      }
+    out[blockIdx.x] = bi;
+  }
+}
+
 }  // namespace
 }  // namespace edgerag
 
@@ -367,4 +434,33 @@ extern "C" int edgerag_silu_mul(const void* gate_up, int64_t gate_up_stride, int
   }
 #undef EDGERAG_SILU
   return check_launch("edgerag_silu_mul");
+}
+
+extern "C" int edgerag_argmax_rows(const void* x, int32_t dtype, int32_t rows, int32_t cols,
+                                   int64_t row_stride, int32_t* out, void* stream) {
+  clear_error();
+  if (rows < 0 || cols <= 0 || row_stride < cols)
+    return fail(EDGERAG_EINVAL, "edgerag_argmax_rows: bad shape (%d x %d, stride %lld)", rows, cols,
+                (long long)row_stride);
+  if (rows == 0) return EDGERAG_OK;
+  if (x == nullptr || out == nullptr) return fail(EDGERAG_EINVAL, "edgerag_argmax_rows: NULL pointer");
+  const int es = dtype == EDGERAG_F32 ? 4 : 2;
+  const bool vec = (cols * es) % 16 == 0 && aligned_rows(x, row_stride, es);
+  auto s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case EDGERAG_F32:
+      hipLaunchKernelGGL((argmax_rows_kernel<float>), dim3(unsigned(rows)), dim3(1024), 0, s,
+                         static_cast<const float*>(x), row_stride, cols, vec, out);
+      break;
+    case EDGERAG_F16:
+      hipLaunchKernelGGL((argmax_rows_kernel<f16>), dim3(unsigned(rows)), dim3(1024), 0, s,
+                         static_cast<const f16*>(x), row_stride, cols, vec, out);
+      break;
+    case EDGERAG_BF16:
+      hipLaunchKernelGGL((argmax_rows_kernel<bf16>), dim3(unsigned(rows)), dim3(1024), 0, s,
+                         static_cast<const bf16*>(x), row_stride, cols, vec, out);
+      break;
+    default: return fail(EDGERAG_EINVAL, "edgerag_argmax_rows: dtype %d", dtype);
+  }
+  return check_launch("edgerag_argmax_rows");
 }

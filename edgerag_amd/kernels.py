@@ -838,6 +838,20 @@ def quantize(weight: torch.Tensor, bits: int, group_size: int) -> tuple[torch.Te
     return packed, scales
 
 
+def argmax_rows(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """int32 ``(rows,)``: the first index of each row's maximum (a NaN counts as the maximum),
+    like ``x.argmax(dim=-1)``; one launch (the executor's greedy token choice)."""
+    require_device(x, out)
+    if x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError("argmax_rows takes (rows, cols) with contiguous rows")
+    rows, cols = x.shape
+    if out is None:
+        out = torch.empty(rows, dtype=torch.int32, device=x.device)
+    call("edgerag_argmax_rows", x.data_ptr(), dtype_code(x.dtype), rows, cols, x.stride(0),
+         out.data_ptr(), stream_ptr(x.device))
+    return out
+
+
 def dequantize(packed: torch.Tensor, scales: torch.Tensor, in_features: int, bits: int,
                group_size: int) -> torch.Tensor:
     """fp16 ``(N, K)`` weight rebuilt from codes and scales, as the reference dequantizes."""

@@ -133,7 +133,7 @@ class ModelExecutor:
                 and self._stage_fixed(qsl, ctx, bt, extras)):
             logits = self._replay_decode(len(entries))
             self.last_logits = logits
-            tokens = logits.argmax(dim=-1).to(torch.int32).cpu().tolist()
+            tokens = kernels.argmax_rows(logits).cpu().tolist()
             for request, token in zip(emitting, tokens):
                 output.tokens[request.request_id] = int(token)
             self.graph_steps += 1
@@ -147,7 +147,7 @@ class ModelExecutor:
         if emitting:
             logits = self.decoder.logits(step, self.key_pool, self.value_pool)
             self.last_logits = logits
-            tokens = logits.argmax(dim=-1).to(torch.int32).cpu().tolist()
+            tokens = kernels.argmax_rows(logits).cpu().tolist()
             for request, token in zip(emitting, tokens):
                 output.tokens[request.request_id] = int(token)
         else:

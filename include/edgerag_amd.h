@@ -409,6 +409,15 @@ int edgerag_silu_mul(const void* gate_up, int64_t gate_up_stride, int32_t n_toke
                      int32_t intermediate, void* out, int64_t out_stride, int32_t dtype,
                      void* stream);
 
+/*
+ * Greedy token choice over each row of logits [rows, cols] (row stride row_stride elements):
+ * out[r] = the first index of the row's maximum, a NaN counting as the maximum (torch.argmax's
+ * choice). One workgroup per row. Replaces `int(logits[0, -1].argmax())` of the executor's
+ * greedy step (edgerag/serve/executor.py:136, :154) for all emitting requests at once.
+ */
+int edgerag_argmax_rows(const void* x, int32_t dtype, int32_t rows, int32_t cols,
+                        int64_t row_stride, int32_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -89,3 +89,26 @@ def test_silu_mul(device, dtype) -> None:
         torch.testing.assert_close(out, ref, rtol=1e-6, atol=1e-6)
     else:
         torch.testing.assert_close(out.float(), ref.float(), rtol=2e-3, atol=2e-3)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rows,cols", [(1, 49152), (8, 49152), (64, 49152), (5, 1000), (3, 7)])
+def test_argmax_rows_is_torch_argmax(device, dtype, rows, cols) -> None:
+    """The greedy choice over logit rows equals torch.argmax (the first index of the maximum),
+    including planted ties, -inf rows, NaN, a maximum in the last element, and strided rows."""
+    g = seeded(rows * 7 + cols)
+    x = torch.randn(rows, cols + 16, generator=g).to(dtype)
+    if cols > 10:
+        x[0, cols // 3] = x[0, cols // 2] = 50.0  # tie: the first index wins
+    if rows > 1:
+        x[1, :] = float("-inf")
+        x[1, cols - 1] = float("-inf")  # all -inf: index 0
+    if rows > 2:
+        x[2, cols - 1] = 60.0  # the last element
+    if rows > 3:
+        x[3, 5] = float("nan")
+        x[3, 2] = float("nan")  # NaN counts as the maximum; the first one wins
+    xd = x.to(device)
+    for view in (xd[:, :cols].contiguous(), xd[:, :cols]):  # contiguous, then strided rows
+        got = kernels.argmax_rows(view).cpu()
+        assert torch.equal(got, x[:, :cols].argmax(dim=-1).to(torch.int32))
