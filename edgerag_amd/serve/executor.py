@@ -73,7 +73,7 @@ class ModelExecutor:
         self.decode_graphs = decode_graphs and self.device.type == "cuda"
         self.max_decode_batch = max_decode_batch
         self._fixed: kernels.FixedAttention | None = None
-        self._graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor]] = {}
+        self._graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor, torch.Tensor]] = {}
         self.graph_steps = 0
 
     @property
@@ -131,9 +131,9 @@ class ModelExecutor:
                   np.asarray(ids, np.int32), np.asarray(rows, np.int32)]
         if (self.decode_graphs and not batch.prefill and len(entries) <= self.max_decode_batch
                 and self._stage_fixed(qsl, ctx, bt, extras)):
-            logits = self._replay_decode(len(entries))
+            logits, choice = self._replay_decode(len(entries))
             self.last_logits = logits
-            tokens = kernels.argmax_rows(logits).cpu().tolist()
+            tokens = choice.cpu().tolist()
             for request, token in zip(emitting, tokens):
                 output.tokens[request.request_id] = int(token)
             self.graph_steps += 1
@@ -170,8 +170,9 @@ class ModelExecutor:
         return self._fixed.update(np.asarray(qsl, np.int32), np.asarray(ctx, np.int32), bt,
                                   extras)
 
-    def _replay_decode(self, n: int) -> torch.Tensor:
-        """Logits ``(n, vocab)`` of a staged decode-only step of ``n`` requests."""
+    def _replay_decode(self, n: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """Logits ``(n, vocab)`` of a staged decode-only step of ``n`` requests and their greedy
+        tokens (int32 ``(n,)``), both computed inside the replayed graph."""
         entry = self._graphs.get(n)
         if entry is None:
             fx = self._fixed
@@ -187,11 +188,12 @@ class ModelExecutor:
                 self.decoder.logits(step, self.key_pool, self.value_pool)
                 with torch.cuda.graph(graph, stream=stream):
                     logits = self.decoder.logits(step, self.key_pool, self.value_pool)
+                    choice = kernels.argmax_rows(logits)
             torch.cuda.current_stream(self.device).wait_stream(stream)
-            entry = self._graphs[n] = (graph, logits)
-        graph, logits = entry
+            entry = self._graphs[n] = (graph, logits, choice)
+        graph, logits, choice = entry
         graph.replay()
-        return logits
+        return logits, choice
 
     def to_dict(self) -> dict[str, Any]:
         return {
