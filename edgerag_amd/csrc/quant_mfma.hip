@@ -59,6 +59,9 @@
 #ifndef EDGERAG_GEMM_STAGES_64
 #define EDGERAG_GEMM_STAGES_64 4
 #endif
+#ifndef EDGERAG_GEMM_READ_AHEAD
+#define EDGERAG_GEMM_READ_AHEAD 1  // 16-k steps whose LDS operands are read ahead of the MFMAs
+#endif
 #ifndef EDGERAG_SPLITK_MAX
 #define EDGERAG_SPLITK_MAX 16  // most k splits
 #endif
@@ -883,11 +886,13 @@ __global__ __launch_bounds__(NTH, EDGERAG_GEMM_MIN_WG) void qlinear_gemm_kernel(
   // overlaps this step's matrix-core work. The operands of 16-k step ks + 1 are read from LDS
   // before the MFMAs of step ks are issued, so their latency hides behind those MFMAs.
   auto step = [&](int p, const GemmStage<C>& stn) {
-    h8 a[2][C::TN], b[2][C::TM];
-    read_ops(sw[p], sx[p], 0, a[0], b[0]);
+    constexpr int KS = kBK / 16, RA = EDGERAG_GEMM_READ_AHEAD;  // 16-k steps read ahead
+    h8 a[RA + 1][C::TN], b[RA + 1][C::TM];
 #pragma unroll
-    for (int ks = 0; ks < kBK / 16; ++ks) {
-      if (ks + 1 < kBK / 16) read_ops(sw[p], sx[p], ks + 1, a[(ks + 1) & 1], b[(ks + 1) & 1]);
+    for (int ks = 0; ks < RA && ks < KS; ++ks) read_ops(sw[p], sx[p], ks, a[ks], b[ks]);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      if (ks + RA < KS) read_ops(sw[p], sx[p], ks + RA, a[(ks + RA) % (RA + 1)], b[(ks + RA) % (RA + 1)]);
 #pragma unroll
       for (int c = ks * NWC / 4; c < (ks + 1) * NWC / 4; ++c)
         gemm_store_w<C, PC>(stn, c, sw[p ^ 1], wr, wc0);
@@ -897,7 +902,8 @@ __global__ __launch_bounds__(NTH, EDGERAG_GEMM_MIN_WG) void qlinear_gemm_kernel(
 #pragma unroll
       for (int i = 0; i < C::TN; ++i)
 #pragma unroll
-        for (int j = 0; j < C::TM; ++j) acc[i][j] = mfma32(a[ks & 1][i], b[ks & 1][j], acc[i][j]);
+        for (int j = 0; j < C::TM; ++j)
+          acc[i][j] = mfma32(a[ks % (RA + 1)][i], b[ks % (RA + 1)][j], acc[i][j]);
     }
   };
   // One barrier per step: it orders this step's LDS writes (the next step's operands) before
@@ -1070,6 +1076,9 @@ void launch_gemm(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* 
 // Split-K launches use 64x64 tiles: the tile grid alone would leave CUs idle.
 constexpr int kSplitTile = 64;
 static_assert(EDGERAG_SPLITK_MAX <= 16, "the reduce launch is instantiated for 2, 4, 8, 16 splits");
+// Partial tiles a split may write: EDGERAG_QUANT_WORKSPACE_MAX / 16 KB.
+constexpr int64_t kSplitMaxPartials =
+    int64_t(EDGERAG_QUANT_WORKSPACE_MAX) / (kSplitTile * kSplitTile * 4);
 
 // Sums the split partials of the 64x64 tiles (as qlinear_gemm_kernel<..., SPLIT> wrote them, with
 // its 2 x 2 grid of 32x32 wave tiles) in split order and writes y = fp16(scale * sum + bias)
@@ -1412,6 +1421,7 @@ SplitPlan qlinear_split_plan(int32_t m, int32_t k, int32_t n, int32_t bits, int3
   int64_t best_cost = int64_t(nk) * rounds(tiles);
   for (int sp = 2; sp <= EDGERAG_SPLITK_MAX; sp *= 2) {
     if (nk % sp != 0 || nk / sp < EDGERAG_SPLITK_MIN_STEPS) break;
+    if (tiles * sp > kSplitMaxPartials) break;  // the workspace bound
     const int64_t cost = EDGERAG_SPLITK_FIXED_STEPS + int64_t(nk / sp) * rounds(tiles * sp);
     if (cost < best_cost) {
       best = sp;

@@ -78,8 +78,11 @@ def test_quant_workspace_query() -> None:
     assert q(512, 2048, 8192, 8, 2048) == 0  # 128x64 tiles fill the GPU: the plain launch
     assert q(64, 128, 2048, 8, 128) == 0  # two 64-k steps: nothing to split
     assert q(64, 2048, 2048, 8, 48) == 0  # group not a multiple of 32
-    for args in [(64, 8192, 2048, 8, 8192), (40, 1152, 37, 4, 128), (300, 8192, 64, 8, 8192)]:
-        assert 0 <= q(*args) <= _lib.QUANT_WORKSPACE_MAX
+    # 96 tiles: 8 splits would model cheaper but need 12 MiB of partials; the bound keeps 2.
+    assert q(64, 2048, 6144, 8, 2048) == 96 * 2 * tile
+    for m in (17, 24, 40, 64, 100, 200, 300):
+        for k, n in [(8192, 2048), (2048, 6144), (2048, 16384), (8192, 64), (1152, 37), (2048, 4100)]:
+            assert 0 <= q(m, k, n, 8, k) <= _lib.QUANT_WORKSPACE_MAX, (m, k, n)
 
 
 def test_rope_append_support_query() -> None:
