@@ -1437,7 +1437,9 @@ bool launch_qlinear_split(const f16* x, int64_t xs, int32_t m, int32_t k, const 
                           const f16* scales, const f16* bias, int32_t n, int32_t bits, int32_t g,
                           f16* y, int64_t ys, void* ws, int64_t ws_bytes, hipStream_t s) {
   const SplitPlan p = qlinear_split_plan(m, k, n, bits, g);
-  if (p.splits < 1 || (p.splits > 1 && (ws == nullptr || ws_bytes < p.bytes))) return false;
+  if (p.splits < 1 ||
+      (p.splits > 1 && (ws == nullptr || ws_bytes < p.bytes || !aligned16(ws))))  // float4 partials
+    return false;
   constexpr int T = kSplitTile;
   if (p.splits == 1) {
     if (bits == 8)

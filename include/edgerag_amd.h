@@ -265,9 +265,10 @@ int edgerag_quant_linear(const void* x, int32_t x_dtype, int64_t x_stride, int32
  * order and writes y (the same bits on every run). Results equal edgerag_quant_linear's to the
  * linear tolerance (the fp32 sums are ordered differently), not bit for bit.
  *
- * workspace: at least edgerag_quant_linear_workspace_bytes(M, K, N, bits, group_size) bytes, any
- * contents. Launches that share a workspace must be ordered (one stream). With a smaller or NULL
- * workspace, or a shape that does not split, this is edgerag_quant_linear.
+ * workspace: 16-byte aligned, at least edgerag_quant_linear_workspace_bytes(M, K, N, bits,
+ * group_size) bytes, any contents. Launches that share a workspace must be ordered (one stream).
+ * With a smaller, unaligned or NULL workspace, a shape that does not split K still takes the tiled
+ * GEMM when the route says so; one that would split runs edgerag_quant_linear.
  *
  * Replaces QuantLinear.forward (edgerag/core/linear.py:194-196), as edgerag_quant_linear does.
  */

@@ -449,7 +449,8 @@ def test_quant_linear_split_k(device, k, n, bits, g, m) -> None:
 
 
 def test_quant_linear_ws_without_room_is_the_plain_launch(device) -> None:
-    """A workspace below the plan's size (or none) runs edgerag_quant_linear: the same bits."""
+    """A workspace below the plan's size, unaligned, or none runs edgerag_quant_linear: the same
+    bits."""
     from edgerag_amd import _lib
 
     k, n, bits, g, m = 8192, 2048, 8, 8192, 64
@@ -457,11 +458,12 @@ def test_quant_linear_ws_without_room_is_the_plain_launch(device) -> None:
     x, packed, scales, bias = (t.to(device) for t in (x, packed, scales, bias))
     need = kernels.quant_workspace_bytes(m, k, n, bits, g)
     assert need > 0
-    ws = torch.full((need,), 0xFF, dtype=torch.uint8, device=device)  # any contents
+    ws = torch.full((need + 16,), 0xFF, dtype=torch.uint8, device=device)  # any contents
     outs = []
     for name, extra in [("edgerag_quant_linear", ()),
                         ("edgerag_quant_linear_ws", (ws.data_ptr(), need - 1)),
                         ("edgerag_quant_linear_ws", (0, 0)),
+                        ("edgerag_quant_linear_ws", (ws.data_ptr() + 4, need)),  # unaligned
                         ("edgerag_quant_linear_ws", (ws.data_ptr(), need))]:
         y = torch.empty(m, n, dtype=torch.float16, device=device)
         _lib.call(name, x.data_ptr(), 1, x.stride(0), m, k, packed.data_ptr(), scales.data_ptr(),
@@ -469,7 +471,8 @@ def test_quant_linear_ws_without_room_is_the_plain_launch(device) -> None:
                   kernels.stream_ptr(device))
         outs.append(y)
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
-    torch.testing.assert_close(outs[3].float(), outs[0].float(), **LINEAR_TOL)
+    assert torch.equal(outs[0], outs[3])
+    torch.testing.assert_close(outs[4].float(), outs[0].float(), **LINEAR_TOL)
 
 
 def test_quant_linear_split_k_graph_replays(device) -> None:
