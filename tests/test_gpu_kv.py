@@ -199,3 +199,33 @@ def test_copy_on_write_copies_contents_once_for_every_layer(device) -> None:
         keys, _ = child.gather(layer)
         assert (keys[0, :, :10] == 3.0).all()
         assert (keys[0, :, 10:12] == 9.0).all()
+
+
+def test_swap_out_in_on_device_pools(device) -> None:
+    """Swap-out gathers the victim's blocks into pinned host memory on the stream before the
+    blocks are freed: a kernel that reuses them right after (on the same stream) cannot change
+    the swapped copy; swap-in restores every layer bit for bit at the newly allocated blocks."""
+    from edgerag_amd.cache.allocator import BlockAllocator
+    from edgerag_amd.cache.preemption import Preemptor
+
+    g = torch.Generator(device=device).manual_seed(3)
+    layers, heads, nb, bs, d = 4, 8, 64, 16, 64
+    kp = [torch.randn(heads, nb, bs, d, generator=g, device=device).half() for _ in range(layers)]
+    vp = [torch.randn(heads, nb, bs, d, generator=g, device=device).half() for _ in range(layers)]
+    alloc = BlockAllocator(nb, bs)
+    blocks = alloc.allocate(9)
+    saved = [p[:, blocks].clone() for p in kp + vp]
+    pre = Preemptor(alloc)
+    rec = pre.swap_out("v", blocks, 130, kp, vp)
+    assert all(t.is_pinned() for t in rec.keys + rec.values)
+    other = alloc.allocate(nb)  # every block, the victim's included, is reused at once
+    for p in kp + vp:
+        p[:, other] = 0
+    rec.wait()
+    for host, ref in zip(rec.keys + rec.values, [s.cpu() for s in saved]):
+        assert torch.equal(host, ref)
+    alloc.free(other)
+    new_blocks, n = pre.swap_in("v", kp, vp)
+    assert n == 130 and len(new_blocks) == 9
+    for p, ref in zip(kp + vp, saved):
+        assert torch.equal(p[:, new_blocks], ref)
