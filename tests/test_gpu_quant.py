@@ -501,3 +501,37 @@ def test_quant_linear_split_k_graph_replays(device) -> None:
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
         assert torch.equal(kernels.quant_linear(x2, p2, s2, None, 2048, 2048, 8, 2048), eager2)
+
+
+@pytest.mark.parametrize("bits,g,with_bias", [(8, None, False), (4, 128, True), (8, 64, True)])
+def test_quant_state_dict_round_trips_through_safetensors(device, tmp_path, bits, g, with_bias):
+    """The on-disk quant format: a QuantLinear's state dict (`packed` / `scales` / `bias`, the
+    reference's buffers, edgerag/core/linear.py:152-164) saved with safetensors loads into a fresh
+    layer without re-quantising (buffers and outputs bit-identical), and a state dict written by
+    the oracle's quantiser in the reference layout loads the same way."""
+    from safetensors.torch import load_file, save_file
+
+    k, n = 512, 192
+    cfg = QuantConfig(g if g is not None else k, bits)
+    w = _weight(n, k, 11)
+    bias = (torch.randn(n, generator=seeded(12)) * 0.1).half() if with_bias else None
+    a = QuantLinear(k, n, bias=with_bias, config=cfg, device=device)
+    a.load_weight(w, bias)
+    path = tmp_path / "layer.safetensors"
+    save_file({key: t.contiguous().cpu() for key, t in a.state_dict().items()}, str(path))
+    b = QuantLinear(k, n, bias=with_bias, config=cfg, device=device)
+    b.load_state_dict({key: t.to(device) for key, t in load_file(str(path)).items()})
+    for key, t in a.state_dict().items():
+        assert torch.equal(b.state_dict()[key], t), key
+    x = torch.randn(7, k, generator=seeded(13)).half().to(device)
+    assert torch.equal(a(x), b(x))
+    # A checkpoint quantised elsewhere (the oracle restates the reference's quantiser).
+    packed, scales = oq.quantize_for_layer(w, oq.QuantConfig(cfg.group_size, bits))
+    ext = {"packed": packed, "scales": scales}
+    if with_bias:
+        ext["bias"] = bias
+    c = QuantLinear(k, n, bias=with_bias, config=cfg, device=device)
+    c.load_state_dict({key: t.to(device) for key, t in ext.items()})
+    assert torch.equal(c.packed, a.packed) and torch.equal(c.scales, a.scales)
+    expected = oq.quant_linear_reference(x.cpu(), packed, scales, bias, k, oq.QuantConfig(cfg.group_size, bits))
+    torch.testing.assert_close(c(x).float().cpu(), expected, **LINEAR_TOL)
