@@ -558,8 +558,10 @@ int pow2_at_least(int v) {
   return p;
 }
 
-struct PlanItem {
-  int32_t w[kItemWords];
+// One (request, query tile, KV split) of the plan: it becomes one work item per kv head. All
+// heads of a group cost the same, so the planner orders groups, not items.
+struct PlanGroup {
+  int32_t req, q_begin, q_count, kv_begin, kv_end, split;
   int64_t cost;
 };
 
@@ -743,9 +745,13 @@ extern "C" int edgerag_attn_plan(const int32_t* query_start_loc, const int32_t* 
           : round_up(std::max<int64_t>(kMinTileSplit,
                                        (tile_work + kTargetTiles - 1) / kTargetTiles), 64));
 
-  std::vector<PlanItem> rows, tiles;
-  std::vector<int32_t> reqs(size_t(num_reqs) * kReqWords, 0);
-  std::vector<int32_t> combine;
+  // Scratch reused across calls on a thread: the planner runs once per step on the host.
+  thread_local std::vector<PlanGroup> rows, tiles;
+  thread_local std::vector<int32_t> reqs, combine;
+  rows.clear();
+  tiles.clear();
+  combine.clear();
+  reqs.assign(size_t(num_reqs) * kReqWords, 0);
   int64_t n_partials = 0;
   int max_row_vecs = 0;
   for (int r = 0; r < num_reqs; ++r) {
@@ -772,6 +778,7 @@ extern "C" int edgerag_attn_plan(const int32_t* query_start_loc, const int32_t* 
       return fail(EDGERAG_EUNSUPPORTED, "edgerag_attn_plan: batch needs > 2^31 split partials");
     const int rows_per_item = row ? c : tile_rows;
     if (row) max_row_vecs = std::max(max_row_vecs, c * n_rep);
+    auto& groups = row ? rows : tiles;
     for (int tile = 0; tile < c; tile += rows_per_item) {
       const int qc = std::min(rows_per_item, c - tile);
       const int last_visible = L - c + tile + qc - 1;  // causal limit of the tile's last row
@@ -780,27 +787,19 @@ extern "C" int edgerag_attn_plan(const int32_t* query_start_loc, const int32_t* 
         if (kb > last_visible) break;
         const int ke = int(std::min<int64_t>(L, (s + 1) * slen));
         const int ke_eff = std::min(ke, last_visible + 1);
-        for (int h = 0; h < n_kv_heads; ++h) {
-          PlanItem p{};
-          p.w[I_REQ] = r;
-          p.w[I_HEAD] = h;
-          p.w[I_QBEGIN] = q0 + tile;
-          p.w[I_QCOUNT] = qc;
-          p.w[I_KVBEGIN] = kb;
-          p.w[I_KVEND] = ke_eff;
-          p.w[I_SPLIT] = s;
-          p.cost = int64_t(ke_eff - kb) * (row ? 1 : qc * n_rep);
-          (row ? rows : tiles).push_back(p);
-        }
+        groups.push_back(PlanGroup{r, q0 + tile, qc, kb, ke_eff, s,
+                                   int64_t(ke_eff - kb) * (row ? 1 : qc * n_rep)});
       }
     }
   }
   // Heaviest first: the dispatcher hands blocks out in index order, so this is LPT scheduling.
-  auto heavier = [](const PlanItem& a, const PlanItem& b) { return a.cost > b.cost; };
+  // Stable, so equal costs keep request order; a group's heads stay adjacent in head order.
+  auto heavier = [](const PlanGroup& a, const PlanGroup& b) { return a.cost > b.cost; };
   std::stable_sort(rows.begin(), rows.end(), heavier);
   std::stable_sort(tiles.begin(), tiles.end(), heavier);
 
-  const int64_t n_items = int64_t(rows.size() + tiles.size());
+  const int64_t n_row_items = int64_t(rows.size()) * n_kv_heads;
+  const int64_t n_items = n_row_items + int64_t(tiles.size()) * n_kv_heads;
   const int64_t item_off = kHeaderWords;
   const int64_t req_off = item_off + n_items * kItemWords;
   const int64_t combine_off = req_off + int64_t(num_reqs) * kReqWords;  // 16-byte aligned
@@ -826,7 +825,7 @@ extern "C" int edgerag_attn_plan(const int32_t* query_start_loc, const int32_t* 
   plan[H_BLOCK_SIZE] = block_size;
   plan[H_DTYPE] = dtype;
   plan[H_NUM_TOKENS_HINT] = num_reqs > 0 ? query_start_loc[num_reqs] : 0;
-  plan[H_N_ROW_ITEMS] = int32_t(rows.size());
+  plan[H_N_ROW_ITEMS] = int32_t(n_row_items);
   plan[H_MAX_ROW_VECS] = max_row_vecs;
   plan[H_MAX_SPLIT_BLOCKS] = split_blocks;
   plan[H_N_COMBINE] = int32_t(combine.size() / kCombineWords);
@@ -834,11 +833,18 @@ extern "C" int edgerag_attn_plan(const int32_t* query_start_loc, const int32_t* 
   plan[H_TILE_KIND] = mfma_tiles ? 1 : 0;
   std::copy(combine.begin(), combine.end(), plan + combine_off);
   int32_t* dst = plan + item_off;
-  for (const auto* group : {&rows, &tiles})
-    for (const PlanItem& p : *group) {
-      std::copy(p.w, p.w + kItemWords, dst);
-      dst += kItemWords;
-    }
+  for (const auto* groups : {&rows, &tiles})
+    for (const PlanGroup& g : *groups)
+      for (int h = 0; h < n_kv_heads; ++h, dst += kItemWords) {
+        dst[I_REQ] = g.req;
+        dst[I_HEAD] = h;
+        dst[I_QBEGIN] = g.q_begin;
+        dst[I_QCOUNT] = g.q_count;
+        dst[I_KVBEGIN] = g.kv_begin;
+        dst[I_KVEND] = g.kv_end;
+        dst[I_SPLIT] = g.split;
+        dst[I_PAD] = 0;
+      }
   std::copy(reqs.begin(), reqs.end(), plan + req_off);
   return EDGERAG_OK;
 }
@@ -1134,3 +1140,4 @@ extern "C" int edgerag_paged_attention_fixed(
   if (rc != EDGERAG_OK) return rc;
   return check_launch("edgerag_paged_attention_fixed(combine)");
 }
+

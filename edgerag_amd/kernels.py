@@ -228,6 +228,9 @@ def quant_workspace_bytes(m: int, k: int, n: int, bits: int, group_size: int) ->
     return int(_lib.load().edgerag_quant_linear_workspace_bytes(m, k, n, bits, group_size))
 
 
+_PLAN_WORDS_HINT = [1 << 14]  # largest plan seen so far: one planner call is usually enough
+
+
 def make_plan_host(
     query_start_loc: np.ndarray,
     context_lens: np.ndarray,
@@ -238,7 +241,10 @@ def make_plan_host(
     max_blocks_per_seq: int,
     dtype: torch.dtype,
 ) -> tuple[np.ndarray, int]:
-    """Run the native host planner. Returns ``(plan words, workspace bytes)``."""
+    """Run the native host planner. Returns ``(plan words, workspace bytes)``.
+
+    One planner call fills a buffer sized from the largest plan seen so far; only a plan larger
+    than every earlier one needs a second call (the first reports the size)."""
     lib = _lib.load()
     qsl = np.ascontiguousarray(query_start_loc, dtype=np.int32)
     ctx = np.ascontiguousarray(context_lens, dtype=np.int32)
@@ -250,14 +256,18 @@ def make_plan_host(
         qsl.ctypes.data, ctx.ctypes.data, num_reqs, n_q_heads, n_kv_heads, head_dim, block_size,
         max_blocks_per_seq, dtype_code(dtype),
     )
-    call("edgerag_attn_plan", *args, None, 0, ctypes.byref(words), ctypes.byref(ws))
-    plan = np.empty(words.value, dtype=np.int32)
-    call(
-        "edgerag_attn_plan", *args, plan.ctypes.data, plan.size, ctypes.byref(words),
-        ctypes.byref(ws),
-    )
-    del lib
-    return plan, int(ws.value)
+    plan = np.empty(_PLAN_WORDS_HINT[0], dtype=np.int32)
+    rc = lib.edgerag_attn_plan(*args, plan.ctypes.data, plan.size, ctypes.byref(words),
+                               ctypes.byref(ws))
+    if rc == _lib.EDGERAG_EWORKSPACE and words.value > plan.size:
+        plan = np.empty(words.value, dtype=np.int32)
+        rc = lib.edgerag_attn_plan(*args, plan.ctypes.data, plan.size, ctypes.byref(words),
+                                   ctypes.byref(ws))
+    if rc != _lib.EDGERAG_OK:
+        raise _lib.EdgeragError("edgerag_attn_plan", rc,
+                                lib.edgerag_last_error().decode(errors="replace"))
+    _PLAN_WORDS_HINT[0] = max(_PLAN_WORDS_HINT[0], int(words.value))
+    return plan[: words.value], int(ws.value)
 
 
 def plan_attention(
@@ -271,11 +281,13 @@ def plan_attention(
     dtype: torch.dtype,
     device: torch.device,
     extra_int32: list[np.ndarray] | None = None,
+    workspace: bool = True,
 ) -> tuple[AttentionPlan, list[torch.Tensor]]:
     """Plan a ragged step on the host and upload all of its metadata in one copy.
 
     ``extra_int32`` arrays (e.g. the step's slot mapping) ride along in the same copy; their
-    device views are returned second.
+    device views are returned second. ``workspace=False`` leaves the split-partial workspace out
+    (for a caller that brings its own).
     """
     block_tables = np.ascontiguousarray(block_tables, dtype=np.int32)
     if block_tables.ndim != 2:
@@ -290,11 +302,11 @@ def plan_attention(
          block_tables, *extra],
         device,
     )
-    workspace = attention_workspace(device, ws_bytes) if ws_bytes > 0 else None
+    ws = attention_workspace(device, ws_bytes) if ws_bytes > 0 and workspace else None
     num_reqs = int(np.asarray(context_lens).size)
     ap = AttentionPlan(
         plan_host=plan, plan_dev=views[0], query_start_loc=views[1], context_lens=views[2],
-        block_tables=views[3], workspace=workspace, workspace_bytes=ws_bytes, num_reqs=num_reqs,
+        block_tables=views[3], workspace=ws, workspace_bytes=ws_bytes, num_reqs=num_reqs,
         num_tokens=int(np.asarray(query_start_loc)[-1]) if num_reqs else 0,
         n_q_heads=n_q_heads, n_kv_heads=n_kv_heads, head_dim=head_dim, block_size=block_size,
         dtype=dtype,
@@ -302,19 +314,9 @@ def plan_attention(
     return ap, views[4:]
 
 
-def paged_attention(
-    query: torch.Tensor,
-    key_pool: torch.Tensor,
-    value_pool: torch.Tensor,
-    plan: AttentionPlan,
-    scale: float,
-    out: torch.Tensor | None = None,
-    overlap: bool = True,
-) -> torch.Tensor:
-    """Ragged paged attention. ``query``/``out``: ``(num_tokens, n_q_heads, head_dim)``.
-
-    With ``overlap`` and a batch holding both prefill tiles and decode rows, the two run on two
-    streams (joined before the split merge), so MFMA work overlaps the KV streaming."""
+def _attention_operands(query, key_pool, value_pool, plan, out):
+    """Validate one planned attention launch; returns ``(query, out, leading C-ABI arguments)``:
+    everything ``edgerag_paged_attention`` takes before its workspace."""
     require_device(query, key_pool, value_pool)
     _check_pool(key_pool, "key_pool")
     _check_pool(value_pool, "value_pool")
@@ -337,17 +339,35 @@ def paged_attention(
         out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
     elif out.shape != query.shape or out.dtype != query.dtype or out.stride(2) != 1:
         raise ValueError("out must match query in shape and dtype, head_dim contiguous")
-    ws = plan.workspace
-    args = (
+    return query, out, (
         plan.plan_host.ctypes.data, plan.plan_dev.data_ptr(), plan.plan_host.size,
         query.data_ptr(), query.stride(0), query.stride(1),
         key_pool.data_ptr(), value_pool.data_ptr(), dtype_code(key_pool.dtype),
         plan.block_tables.data_ptr(), plan.block_tables.stride(0),
         plan.query_start_loc.data_ptr(), plan.context_lens.data_ptr(),
         plan.num_reqs, query.shape[0], plan.n_q_heads, n_kv, head_dim, block_size, num_blocks,
-        float(scale), out.data_ptr(), out.stride(0), out.stride(1),
-        None if ws is None else ws.data_ptr(), plan.workspace_bytes,
     )
+
+
+def paged_attention(
+    query: torch.Tensor,
+    key_pool: torch.Tensor,
+    value_pool: torch.Tensor,
+    plan: AttentionPlan,
+    scale: float,
+    out: torch.Tensor | None = None,
+    overlap: bool = True,
+) -> torch.Tensor:
+    """Ragged paged attention. ``query``/``out``: ``(num_tokens, n_q_heads, head_dim)``.
+
+    With ``overlap`` and a batch holding both prefill tiles and decode rows, the two run on two
+    streams (joined before the split merge), so MFMA work overlaps the KV streaming."""
+    query, out, lead = _attention_operands(query, key_pool, value_pool, plan, out)
+    if plan.workspace_bytes > 0 and plan.workspace is None:
+        raise ValueError("this plan was built without a workspace")
+    ws = plan.workspace
+    args = (*lead, float(scale), out.data_ptr(), out.stride(0), out.stride(1),
+            None if ws is None else ws.data_ptr(), plan.workspace_bytes)
     device = query.device
     n_items, n_row = int(plan.plan_host[2]), int(plan.plan_host[13])
     if overlap and 0 < n_row < n_items:
