@@ -35,6 +35,7 @@ EDGERAG_EUNSUPPORTED = 4
 ATTN_TILES, ATTN_ROWS, ATTN_COMBINE, ATTN_ALL = 1, 2, 4, 7
 ATTN_TILES_SHARED = 8  # modifier of ATTN_TILES: one tile workgroup per CU, beside decode rows
 QUANT_WORKSPACE_MAX = 8 * 1024 * 1024  # bound of edgerag_quant_linear_workspace_bytes
+ATTN_SCRATCH_BYTES = 32 * 1024 * 1024  # static partials of edgerag_paged_attention_noalloc
 
 DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 
@@ -60,6 +61,11 @@ SIGNATURES: dict[str, tuple[list, object]] = {
         [c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_vp, c_vp, c_i32, c_vp, c_i64, c_vp, c_vp, c_i32,
          c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_f32, c_vp, c_i64, c_i64, c_vp, c_i64, c_i32,
          c_vp],
+        c_i32,
+    ),
+    "edgerag_paged_attention_noalloc": (
+        [c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_vp, c_vp, c_i32, c_vp, c_i64, c_vp, c_vp, c_i32,
+         c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_f32, c_vp, c_i64, c_i64, c_i32, c_vp],
         c_i32,
     ),
     "edgerag_paged_attention_append": (

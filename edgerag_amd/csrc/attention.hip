@@ -27,6 +27,7 @@
 // v_exp_f32.
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <vector>
 
 #include "attention_plan.h"
@@ -1141,3 +1142,88 @@ extern "C" int edgerag_paged_attention_fixed(
   return check_launch("edgerag_paged_attention_fixed(combine)");
 }
 
+// ---- edgerag_paged_attention_noalloc: split partials in a static device array -----------------
+//
+// The partials live in `scratch`, a file-scope device array (one copy per GPU, held until the
+// process ends). On the host the array's name is only a registration handle, never a device
+// address: its address on a device comes from hipGetSymbolAddress, looked up the first time the
+// entry point runs on that device (with the device current) and cached per device. Kernels get
+// that address as their workspace argument, exactly as they get a caller's workspace.
+namespace edgerag {
+namespace {
+
+static __device__ __align__(256) char scratch[EDGERAG_ATTN_SCRATCH_BYTES];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kMaxScratchDevices] = {};
+
+// The device address of `scratch` on the current device, which must be the stream's device.
+int scratch_address(hipStream_t stream, void** addr) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return fail(EDGERAG_EHIP, "edgerag_paged_attention_noalloc: hipGetDevice: %s",
+                hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(EDGERAG_EUNSUPPORTED, "edgerag_paged_attention_noalloc: device %d", dev);
+  if (stream != nullptr) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice(stream, &sdev);
+    if (e != hipSuccess)
+      return fail(EDGERAG_EHIP, "edgerag_paged_attention_noalloc: hipStreamGetDevice: %s",
+                  hipGetErrorString(e));
+    if (sdev != dev)
+      return fail(EDGERAG_EINVAL,
+                  "edgerag_paged_attention_noalloc: the stream belongs to device %d, device %d is "
+                  "current (make the stream's device current)",
+                  int(sdev), dev);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_addr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(EDGERAG_EHIP,
+                  "edgerag_paged_attention_noalloc: hipGetSymbolAddress(scratch) on device %d: %s",
+                  dev, hipGetErrorString(e));
+    g_scratch_addr[dev] = p;
+  }
+  *addr = g_scratch_addr[dev];
+  return EDGERAG_OK;
+}
+
+}  // namespace
+}  // namespace edgerag
+
+extern "C" int edgerag_paged_attention_noalloc(
+    const int32_t* plan_host, const int32_t* plan_dev, int64_t plan_words, const void* q,
+    int64_t q_stride_tok, int64_t q_stride_head, const void* key_pool, const void* value_pool,
+    int32_t dtype, const int32_t* block_tables, int64_t block_tables_stride,
+    const int32_t* query_start_loc, const int32_t* context_lens, int32_t num_reqs,
+    int32_t num_tokens, int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+    int32_t block_size, int32_t num_blocks, float scale, void* out, int64_t out_stride_tok,
+    int64_t out_stride_head, int32_t parts, void* stream) {
+  clear_error();
+  // Size check first, on the host: a plan whose partials do not fit is refused before any HIP call.
+  if (plan_host == nullptr || plan_words < kHeaderWords || plan_host[H_MAGIC] != kPlanMagic ||
+      plan_host[H_VERSION] != kPlanVersion)
+    return fail(EDGERAG_EINVAL, "edgerag_paged_attention_noalloc: not a plan from edgerag_attn_plan");
+  if (!head_dim_supported(head_dim) || plan_host[H_HEAD_DIM] != head_dim)
+    return fail(EDGERAG_EINVAL, "edgerag_paged_attention_noalloc: plan was made for a different shape");
+  const int64_t need = workspace_layout(plan_host[H_N_PARTIALS], head_dim).total;
+  if (need > EDGERAG_ATTN_SCRATCH_BYTES)
+    return fail(EDGERAG_EWORKSPACE,
+                "edgerag_paged_attention_noalloc: the plan's split partials need %lld bytes, the "
+                "static scratch holds %lld (use edgerag_paged_attention with a workspace)",
+                (long long)need, (long long)EDGERAG_ATTN_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (need > 0) {
+    if (int rc = scratch_address(static_cast<hipStream_t>(stream), &ws)) return rc;
+  }
+  return paged_attention_impl(plan_host, plan_dev, plan_words, q, q_stride_tok, q_stride_head,
+                              key_pool, value_pool, dtype, block_tables, block_tables_stride,
+                              query_start_loc, context_lens, num_reqs, num_tokens, n_q_heads,
+                              n_kv_heads, head_dim, block_size, num_blocks, scale, out,
+                              out_stride_tok, out_stride_head, ws, need, parts, stream, nullptr);
+}

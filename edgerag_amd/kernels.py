@@ -33,6 +33,7 @@ __all__ = [
     "kv_copy_blocks",
     "kv_gather",
     "paged_attention",
+    "paged_attention_noalloc",
     "plan_attention",
     "quant_linear",
     "quantize",
@@ -287,7 +288,7 @@ def plan_attention(
 
     ``extra_int32`` arrays (e.g. the step's slot mapping) ride along in the same copy; their
     device views are returned second. ``workspace=False`` leaves the split-partial workspace out
-    (for a caller that brings its own).
+    (for :func:`paged_attention_noalloc`, which keeps them in the library's static scratch).
     """
     block_tables = np.ascontiguousarray(block_tables, dtype=np.int32)
     if block_tables.ndim != 2:
@@ -364,7 +365,7 @@ def paged_attention(
     streams (joined before the split merge), so MFMA work overlaps the KV streaming."""
     query, out, lead = _attention_operands(query, key_pool, value_pool, plan, out)
     if plan.workspace_bytes > 0 and plan.workspace is None:
-        raise ValueError("this plan was built without a workspace")
+        raise ValueError("this plan was built without a workspace: use paged_attention_noalloc")
     ws = plan.workspace
     args = (*lead, float(scale), out.data_ptr(), out.stride(0), out.stride(1),
             None if ws is None else ws.data_ptr(), plan.workspace_bytes)
@@ -387,6 +388,27 @@ def paged_attention(
         call("edgerag_paged_attention", *args, _lib.ATTN_COMBINE, stream_ptr(device))
     else:
         call("edgerag_paged_attention", *args, _lib.ATTN_ALL, stream_ptr(device))
+    return out
+
+
+def paged_attention_noalloc(
+    query: torch.Tensor,
+    key_pool: torch.Tensor,
+    value_pool: torch.Tensor,
+    plan: AttentionPlan,
+    scale: float,
+    out: torch.Tensor,
+    parts: int = _lib.ATTN_ALL,
+) -> torch.Tensor:
+    """:func:`paged_attention` through ``edgerag_paged_attention_noalloc``: the split partials
+    live in the library's static per-GPU scratch (``_lib.ATTN_SCRATCH_BYTES``), so the call
+    allocates nothing, ``out`` included (the caller passes it). Calls that overlap in time on one
+    GPU share that scratch and must be ordered by the caller (one stream does it)."""
+    if out is None:
+        raise ValueError("paged_attention_noalloc writes into a caller-provided out")
+    query, out, lead = _attention_operands(query, key_pool, value_pool, plan, out)
+    call("edgerag_paged_attention_noalloc", *lead, float(scale), out.data_ptr(), out.stride(0),
+         out.stride(1), int(parts), stream_ptr(query.device))
     return out
 
 

@@ -12,7 +12,8 @@
  *     including the attention workspace sized by edgerag_attn_plan();
  *   - kernels are enqueued on `stream` and run asynchronously; the entry points are reentrant and
  *     keep no mutable global state, so calls from different host threads on different streams do
- *     not interact;
+ *     not interact -- except edgerag_paged_attention_noalloc, whose calls share one static
+ *     per-GPU scratch array (see there);
  *   - element types are EDGERAG_F32 / EDGERAG_F16 / EDGERAG_BF16 (see below).
  *
  * The reference (Tejas544/edgerag) is pure Python/PyTorch and has no FFI; each declaration cites
@@ -215,6 +216,36 @@ int edgerag_paged_attention_fixed(const int32_t* plan_dev, int32_t max_row_items
                                   int32_t block_size, int32_t num_blocks, float scale,
                                   void* out, int64_t out_stride_tok, int64_t out_stride_head,
                                   void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * edgerag_paged_attention without a workspace argument: the same plan, arguments, parts mask and
+ * results (bit for bit), with the split partials kept in a static device array of
+ * EDGERAG_ATTN_SCRATCH_BYTES that the library holds on each GPU it runs on until the process
+ * ends. It calls no hipMalloc / hipFree and no allocating routine. The first call on a device
+ * looks the array's address up (hipGetSymbolAddress) with that device current; the stream must
+ * belong to the current device. A plan whose partials need more than EDGERAG_ATTN_SCRATCH_BYTES
+ * (edgerag_attn_plan's *workspace_bytes) is refused with EDGERAG_EWORKSPACE before anything is
+ * enqueued. Every call on one GPU shares that GPU's array: calls that overlap in time on one GPU
+ * (other streams, other host threads) race on it and must be ordered by the caller; the parts of
+ * one step split over two streams (EDGERAG_ATTN_TILES / _ROWS, then _COMBINE) write disjoint
+ * partials and are one call in this sense. Partials are written before they are read in every
+ * call, so the array's leftover contents never matter.
+ *
+ * No counterpart in the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ */
+#define EDGERAG_ATTN_SCRATCH_BYTES (32 * 1024 * 1024)
+int edgerag_paged_attention_noalloc(const int32_t* plan_host, const int32_t* plan_dev,
+                                    int64_t plan_words, const void* q, int64_t q_stride_tok,
+                                    int64_t q_stride_head, const void* key_pool,
+                                    const void* value_pool, int32_t dtype,
+                                    const int32_t* block_tables, int64_t block_tables_stride,
+                                    const int32_t* query_start_loc, const int32_t* context_lens,
+                                    int32_t num_reqs, int32_t num_tokens, int32_t n_q_heads,
+                                    int32_t n_kv_heads, int32_t head_dim, int32_t block_size,
+                                    int32_t num_blocks, float scale, void* out,
+                                    int64_t out_stride_tok, int64_t out_stride_head,
+                                    int32_t parts, void* stream);
 
 /* ==== Weight-only INT8 / INT4 quantisation and linear ===================================== */
 
