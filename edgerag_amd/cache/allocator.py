@@ -1,202 +1,212 @@
-"""Physical block pool with reference counts -- host bookkeeping only, no tensors.
+"""Block pool accounting for the shared paged KV arena: which of the arena's blocks are taken,
+and by how many owners. Host-side only; the arena itself is the per-layer head-major pools in HBM.
 
-Same contract as the reference allocator (``edgerag/cache/allocator.py:76-254``):
+The state is two int32 arrays rather than Python lists, because what the device needs every step
+is arrays: block tables and slot mappings are assembled with numpy and uploaded in one copy.
 
-* a LIFO free list that hands out block 0 first and reuses the most recently freed block
-  (``:98-100``, ``:168``);
-* all-or-nothing :meth:`allocate` raising :class:`OutOfBlocksError` (``:150-174``);
-* reference counts for copy-on-write sharing, :class:`DoubleFreeError` on a second free
-  (``:176-196``), :meth:`copy_on_write` returning the block unchanged when it is private
-  (``:218-236``);
-* ``blocks_needed = ceil(n / block_size)`` (``:244-254``) and :meth:`check_invariants`
-  (``:120-146``).
+* ``_owners[b]`` -- how many holders (sequences, the prefix cache) reference block ``b``;
+  0 means free.
+* ``_stack[:_top]`` -- the free blocks, the next one to hand out on top. The stack starts as
+  ``[n-1, ..., 1, 0]``, so a fresh pool hands out 0, 1, 2, ... and a released block is the next
+  one reused (most recently released first).
 
-On MI355X the pool itself is one head-major tensor per layer in HBM; this object only decides
-which block ids a sequence owns. The executor turns those ids into device block tables and slot
-mappings once per step.
+Behaviour a caller of the reference allocator relies on (``edgerag/cache/allocator.py``):
+
+* ``allocate(n)`` is all or nothing and raises :class:`OutOfBlocksError` when short
+  (``:150-174``); the ids come out in the order above (``:98-100``, ``:168``);
+* ``blocks_needed(n) = ceil(n / block_size)``, so an exact multiple gets no spare block
+  (``:244-254``);
+* releasing a free block raises :class:`DoubleFreeError`; sharing (``incref``) refuses free
+  blocks; ``copy_on_write`` returns the block itself when it has one owner, otherwise a fresh
+  block, moving one ownership over (``:176-236``).
+
+Unlike the reference, a call that fails validation changes nothing: every id of a ``free`` or
+``incref`` call is checked before any count moves.
 """
 
 from __future__ import annotations
 
-from dataclasses import dataclass, field
-from typing import Any
+from dataclasses import dataclass
+from typing import Iterable
 
-#: Sentinel for "no physical block" in int32 block tables.
+import numpy as np
+
+#: Block-table entry for "no physical block" (int32 tables on the device).
 NO_BLOCK = -1
 
 
 class AllocatorError(RuntimeError):
-    """Misuse of the allocator: always a caller bug."""
+    """The pool was used incorrectly (a bug in the caller, never a capacity condition)."""
 
 
 class OutOfBlocksError(AllocatorError):
-    """The pool cannot satisfy a request. An expected runtime condition (admission, preemption)."""
+    """Not enough free blocks: an expected condition that admission or preemption handles."""
 
 
 class DoubleFreeError(AllocatorError):
-    """A block was released while already free; it would otherwise be handed out twice."""
+    """A block was released more times than it was owned."""
 
 
 @dataclass
-class AllocatorStats:
-    total_blocks: int
-    block_size: int
-    allocations: int = 0
-    frees: int = 0
-    forks: int = 0
-    copy_on_writes: int = 0
-    peak_used_blocks: int = 0
-    oom_events: int = 0
-    extra: dict[str, Any] = field(default_factory=dict)
+class PoolCounters:
+    """Monotone event counts of one pool (for logs and the serving report)."""
+
+    blocks_handed_out: int = 0
+    blocks_released: int = 0
+    shares: int = 0
+    private_copies: int = 0
+    refusals: int = 0
+    high_water: int = 0
+
+
+def _ids(blocks: Iterable[int] | np.ndarray) -> np.ndarray:
+    return np.asarray(blocks if isinstance(blocks, np.ndarray) else list(blocks), dtype=np.int64)
 
 
 class BlockAllocator:
-    """Fixed-size block pool with reference counting and a LIFO free list."""
+    """A fixed arena of ``num_blocks`` blocks of ``block_size`` tokens with owner counts."""
 
     def __init__(self, num_blocks: int, block_size: int) -> None:
-        if num_blocks <= 0:
-            raise ValueError(f"num_blocks must be positive, got {num_blocks}")
-        if block_size <= 0:
-            raise ValueError(f"block_size must be positive, got {block_size}")
-        self.num_blocks = num_blocks
-        self.block_size = block_size
-        self._refs = [0] * num_blocks
-        # Top of the stack is the end of the list: block 0 sits on top initially.
-        self._stack = list(reversed(range(num_blocks)))
-        self.stats = AllocatorStats(total_blocks=num_blocks, block_size=block_size)
+        if num_blocks < 1 or block_size < 1:
+            raise ValueError(
+                f"a block pool needs at least one block of at least one token "
+                f"(got {num_blocks} blocks of {block_size})"
+            )
+        self.num_blocks = int(num_blocks)
+        self.block_size = int(block_size)
+        self._owners = np.zeros(self.num_blocks, dtype=np.int32)
+        self._stack = np.arange(self.num_blocks - 1, -1, -1, dtype=np.int32)
+        self._top = self.num_blocks
+        self.counters = PoolCounters()
 
-    # --- inspection -----------------------------------------------------------------------------
+    # --- occupancy ------------------------------------------------------------------------------
 
     @property
     def num_free(self) -> int:
-        return len(self._stack)
+        return self._top
 
     @property
     def num_used(self) -> int:
-        return self.num_blocks - len(self._stack)
+        return self.num_blocks - self._top
 
     @property
     def utilization(self) -> float:
         return self.num_used / self.num_blocks
 
     def refcount(self, block: int) -> int:
-        return self._refs[block]
-
-    def check_invariants(self) -> None:
-        """Raise AllocatorError unless free list and reference counts agree exactly."""
-        on_stack = set(self._stack)
-        if len(on_stack) != len(self._stack):
-            raise AllocatorError(
-                f"free list holds duplicates ({len(self._stack)} entries, {len(on_stack)} distinct)"
-            )
-        for block, refs in enumerate(self._refs):
-            free = block in on_stack
-            if free and refs != 0:
-                raise AllocatorError(f"block {block} is free but has refcount {refs}")
-            if not free and refs <= 0:
-                raise AllocatorError(f"block {block} is allocated but has refcount {refs}")
-        if self.num_used + self.num_free != self.num_blocks:
-            raise AllocatorError("conservation violated")
-
-    # --- allocation -----------------------------------------------------------------------------
-
-    def allocate(self, n_blocks: int = 1) -> list[int]:
-        """Take ``n_blocks`` blocks at refcount 1, or none at all."""
-        if n_blocks < 0:
-            raise ValueError(f"cannot allocate {n_blocks} blocks")
-        if n_blocks == 0:
-            return []
-        if n_blocks > len(self._stack):
-            self.stats.oom_events += 1
-            raise OutOfBlocksError(
-                f"requested {n_blocks} blocks, only {self.num_free} free "
-                f"({self.num_used}/{self.num_blocks} in use)"
-            )
-        taken = self._stack[-n_blocks:][::-1]
-        del self._stack[-n_blocks:]
-        for block in taken:
-            self._refs[block] = 1
-        self.stats.allocations += n_blocks
-        self.stats.peak_used_blocks = max(self.stats.peak_used_blocks, self.num_used)
-        return taken
-
-    def free(self, blocks: list[int]) -> int:
-        """Drop one reference per block; return how many blocks went back to the pool."""
-        reclaimed = 0
-        for block in blocks:
-            self._validate(block)
-            if self._refs[block] == 0:
-                raise DoubleFreeError(
-                    f"block {block} freed while already free; it would be handed to two "
-                    "sequences at once"
-                )
-            self._refs[block] -= 1
-            if self._refs[block] == 0:
-                self._stack.append(block)
-                reclaimed += 1
-        self.stats.frees += len(blocks)
-        return reclaimed
-
-    def incref(self, blocks: list[int]) -> None:
-        """Share blocks (fork). Rejects free blocks rather than resurrecting them."""
-        for block in blocks:
-            self._validate(block)
-            if self._refs[block] == 0:
-                raise AllocatorError(f"cannot incref free block {block}")
-        for block in blocks:
-            self._refs[block] += 1
+        self._check_range(_ids([block]))
+        return int(self._owners[block])
 
     def is_shared(self, block: int) -> bool:
-        self._validate(block)
-        return self._refs[block] > 1
-
-    def copy_on_write(self, block: int) -> int:
-        """New private block replacing a shared one (caller copies contents); same id if private."""
-        self._validate(block)
-        if self._refs[block] == 0:
-            raise AllocatorError(f"cannot copy-on-write free block {block}")
-        if self._refs[block] == 1:
-            return block
-        fresh = self.allocate(1)[0]
-        self._refs[block] -= 1
-        self.stats.copy_on_writes += 1
-        return fresh
-
-    def _validate(self, block: int) -> None:
-        if not 0 <= block < self.num_blocks:
-            raise AllocatorError(f"block id {block} out of range [0, {self.num_blocks})")
-
-    # --- arithmetic -------------------------------------------------------------------------------
+        return self.refcount(block) > 1
 
     def blocks_needed(self, n_tokens: int) -> int:
-        """``ceil(n_tokens / block_size)``: exact multiples get no spare block."""
+        """Blocks that hold ``n_tokens`` tokens: ``ceil(n_tokens / block_size)``."""
         if n_tokens < 0:
-            raise ValueError(f"negative token count {n_tokens}")
-        return -(-n_tokens // self.block_size)
+            raise ValueError(f"token count must be >= 0, got {n_tokens}")
+        return (n_tokens + self.block_size - 1) // self.block_size
 
-    def internal_fragmentation(self, sequence_lengths: list[int]) -> dict[str, float]:
-        capacity = sum(self.blocks_needed(n) * self.block_size for n in sequence_lengths)
-        wasted = capacity - sum(sequence_lengths)
-        return {
-            "wasted_tokens": float(wasted),
-            "wasted_blocks_equiv": wasted / self.block_size,
-            "waste_fraction": wasted / capacity if capacity else 0.0,
-        }
+    # --- ownership changes ------------------------------------------------------------------------
 
-    def to_dict(self) -> dict[str, Any]:
-        s = self.stats
+    def allocate(self, n_blocks: int = 1) -> list[int]:
+        """Hand out ``n_blocks`` free blocks, each with one owner; raise without change if short."""
+        if n_blocks < 0:
+            raise ValueError(f"block count must be >= 0, got {n_blocks}")
+        if n_blocks > self._top:
+            self.counters.refusals += 1
+            raise OutOfBlocksError(
+                f"pool exhausted: {n_blocks} blocks wanted, {self._top} of {self.num_blocks} free"
+            )
+        if n_blocks == 0:
+            return []
+        out = self._stack[self._top - n_blocks : self._top][::-1].copy()
+        self._top -= n_blocks
+        self._owners[out] = 1
+        self.counters.blocks_handed_out += n_blocks
+        self.counters.high_water = max(self.counters.high_water, self.num_used)
+        return out.tolist()
+
+    def free(self, blocks: Iterable[int] | np.ndarray) -> int:
+        """Drop one ownership of each listed block (a block may be listed once per ownership);
+        blocks left with no owner go back on the stack in list order. Returns how many did."""
+        ids = _ids(blocks)
+        if ids.size == 0:
+            return 0
+        self._check_range(ids)
+        uniq, counts = np.unique(ids, return_counts=True)
+        short = uniq[self._owners[uniq] < counts]
+        if short.size:
+            raise DoubleFreeError(
+                f"release of block {int(short[0])} exceeds its {int(self._owners[short[0]])} "
+                "owner(s): the block would be handed out twice"
+            )
+        np.subtract.at(self._owners, ids, 1)
+        if uniq.size == ids.size:
+            back = ids[self._owners[ids] == 0]
+        else:  # a block listed several times goes back at its last listing
+            last = {int(b): i for i, b in enumerate(ids.tolist())}
+            back = np.array([b for b, i in sorted(last.items(), key=lambda kv: kv[1])
+                             if self._owners[b] == 0], dtype=np.int64)
+        self._stack[self._top : self._top + back.size] = back
+        self._top += back.size
+        self.counters.blocks_released += int(ids.size)
+        return int(back.size)
+
+    def incref(self, blocks: Iterable[int] | np.ndarray) -> None:
+        """Add one owner to each listed block (sharing); every block must already be owned."""
+        ids = _ids(blocks)
+        if ids.size == 0:
+            return
+        self._check_range(ids)
+        unowned = ids[self._owners[ids] == 0]
+        if unowned.size:
+            raise AllocatorError(
+                f"block {int(unowned[0])} is free: only owned blocks can be shared"
+            )
+        np.add.at(self._owners, ids, 1)
+        self.counters.shares += int(ids.size)
+
+    def copy_on_write(self, block: int) -> int:
+        """A block the caller may write: ``block`` itself if it has one owner, else a fresh block
+        that takes over the caller's ownership (the caller copies the contents)."""
+        self._check_range(_ids([block]))
+        owners = int(self._owners[block])
+        if owners == 0:
+            raise AllocatorError(f"block {block} is free: there is nothing to write into")
+        if owners == 1:
+            return int(block)
+        fresh = self.allocate(1)[0]
+        self._owners[block] -= 1
+        self.counters.private_copies += 1
+        return fresh
+
+    # --- checks -----------------------------------------------------------------------------------
+
+    def _check_range(self, ids: np.ndarray) -> None:
+        bad = ids[(ids < 0) | (ids >= self.num_blocks)]
+        if bad.size:
+            raise AllocatorError(f"block {int(bad[0])} is not in this pool of {self.num_blocks}")
+
+    def check_invariants(self) -> None:
+        """Raise :class:`AllocatorError` unless the stack and the owner counts agree: the stack
+        holds distinct blocks, exactly the ones with no owner."""
+        free = self._stack[: self._top]
+        if np.unique(free).size != free.size:
+            raise AllocatorError("free stack lists a block twice")
+        marked = np.zeros(self.num_blocks, dtype=bool)
+        marked[free] = True
+        if np.any(self._owners[marked] != 0):
+            raise AllocatorError("a block on the free stack still has owners")
+        if np.any(self._owners[~marked] <= 0):
+            raise AllocatorError("a block off the free stack has no owner")
+
+    def snapshot(self) -> dict:
+        """Occupancy and event counts, for logs and the serving report."""
+        c = self.counters
         return {
-            "num_blocks": self.num_blocks,
-            "block_size": self.block_size,
-            "num_free": self.num_free,
-            "num_used": self.num_used,
-            "utilization": round(self.utilization, 4),
-            "stats": {
-                "allocations": s.allocations,
-                "frees": s.frees,
-                "forks": s.forks,
-                "copy_on_writes": s.copy_on_writes,
-                "peak_used_blocks": s.peak_used_blocks,
-                "oom_events": s.oom_events,
-            },
+            "blocks": {"total": self.num_blocks, "free": self.num_free, "used": self.num_used,
+                       "block_size": self.block_size},
+            "events": {"handed_out": c.blocks_handed_out, "released": c.blocks_released,
+                       "shared": c.shares, "private_copies": c.private_copies,
+                       "refusals": c.refusals, "high_water": c.high_water},
         }

@@ -1,105 +1,181 @@
-"""Logical token positions -> physical block ids, for one sequence (host bookkeeping).
+"""One sequence's logical-to-physical block map, kept as a growable int32 array, plus the batch
+helpers that turn many maps into the step's device metadata in a few numpy operations.
 
-Same contract as the reference ``BlockTable`` (``edgerag/cache/block_table.py:27-129``):
-``blocks`` holds exactly ``ceil(num_tokens / block_size)`` ids; :meth:`append` grows capacity
-before the length so a failed allocation leaves the table untouched; :meth:`fork` shares blocks;
-:meth:`unshare` splits one shared block and leaves the content copy to the caller.
+A table holds ``len(blocks) == ceil(num_tokens / block_size)`` physical ids
+(``edgerag/cache/block_table.py:27-129`` keeps the same count): logical position ``p`` lives in
+block ``blocks[p // block_size]`` at offset ``p % block_size``, i.e. in pool slot
+``blocks[p // block_size] * block_size + p % block_size``.
 
-:meth:`slots` is the device-facing addition: the flat slot ids ``block * block_size + offset`` of
-a position range, which is what the ``edgerag_kv_append`` kernel consumes.
+* :meth:`grow` takes the blocks for ``n`` more tokens before it moves the length, so a refused
+  allocation leaves the table as it was (``block_table.py:71-79``);
+* :meth:`fork` shares every block with a new table (one more owner each);
+* :meth:`make_private` gives a shared block a private copy (the caller moves the contents);
+* :meth:`locate` refuses positions that were never written (they hold a previous tenant's data).
+
+:func:`pack_tables` and :func:`step_slots` build a whole batch's ``[R, width]`` block-table matrix
+and its slot mapping for the single per-step upload.
 """
 
 from __future__ import annotations
 
-from dataclasses import dataclass, field
-from typing import Any
+from typing import Sequence
 
 import numpy as np
 
-from edgerag_amd.cache.allocator import BlockAllocator
+from edgerag_amd.cache.allocator import NO_BLOCK, BlockAllocator
 
 
-@dataclass
 class BlockTable:
-    allocator: BlockAllocator
-    blocks: list[int] = field(default_factory=list)
-    num_tokens: int = 0
+    __slots__ = ("allocator", "_ids", "_n", "num_tokens")
+
+    def __init__(self, allocator: BlockAllocator, blocks: Sequence[int] | np.ndarray = (),
+                 num_tokens: int = 0) -> None:
+        self.allocator = allocator
+        ids = np.asarray(blocks, dtype=np.int32).reshape(-1)
+        self._ids = np.empty(max(8, ids.size), dtype=np.int32)
+        self._ids[: ids.size] = ids
+        self._n = int(ids.size)
+        self.num_tokens = int(num_tokens)
+
+    # --- shape ------------------------------------------------------------------------------------
 
     @property
     def block_size(self) -> int:
         return self.allocator.block_size
 
     @property
+    def blocks(self) -> np.ndarray:
+        """The physical ids, int32, logical order (a view: do not keep it across a change)."""
+        return self._ids[: self._n]
+
+    @property
+    def num_blocks(self) -> int:
+        return self._n
+
+    @property
     def capacity(self) -> int:
-        return len(self.blocks) * self.block_size
+        return self._n * self.block_size
 
     @property
     def slack(self) -> int:
         return self.capacity - self.num_tokens
 
-    def locate(self, position: int) -> tuple[int, int]:
-        """``(physical block, offset)`` of a written position; IndexError past the written region."""
-        if not 0 <= position < self.num_tokens:
-            raise IndexError(
-                f"position {position} outside the written region [0, {self.num_tokens}); "
-                "reading past it would return a previous tenant's data"
-            )
-        return self.blocks[position // self.block_size], position % self.block_size
+    # --- growth and release -------------------------------------------------------------------------
 
-    def ensure_capacity(self, n_tokens: int) -> list[int]:
-        """Grow so ``n_tokens`` fit; returns the freshly allocated blocks."""
-        needed = self.allocator.blocks_needed(n_tokens)
-        if needed <= len(self.blocks):
-            return []
-        fresh = self.allocator.allocate(needed - len(self.blocks))
-        self.blocks.extend(fresh)
+    def _push(self, fresh: list[int]) -> None:
+        need = self._n + len(fresh)
+        if need > self._ids.size:
+            bigger = np.empty(max(need, 2 * self._ids.size), dtype=np.int32)
+            bigger[: self._n] = self._ids[: self._n]
+            self._ids = bigger
+        self._ids[self._n : need] = fresh
+        self._n = need
+
+    def grow(self, n_new: int) -> list[int]:
+        """Make room for ``n_new`` more tokens and count them as written. Returns the fresh block
+        ids; raises :class:`OutOfBlocksError` with the table unchanged when the pool is short."""
+        if n_new < 0:
+            raise ValueError(f"a table grows by >= 0 tokens, got {n_new}")
+        missing = self.allocator.blocks_needed(self.num_tokens + n_new) - self._n
+        fresh = self.allocator.allocate(missing) if missing > 0 else []
+        self._push(fresh)
+        self.num_tokens += n_new
         return fresh
 
-    def append(self, n_tokens: int = 1) -> list[int]:
-        fresh = self.ensure_capacity(self.num_tokens + n_tokens)
-        self.num_tokens += n_tokens
-        return fresh
+    def shrink_to(self, n_tokens: int) -> int:
+        """Undo growth: keep the first ``n_tokens`` tokens and release blocks past them. Returns
+        the blocks released to the pool."""
+        if not 0 <= n_tokens <= self.num_tokens:
+            raise ValueError(f"cannot shrink {self.num_tokens} tokens to {n_tokens}")
+        keep = self.allocator.blocks_needed(n_tokens)
+        dropped = self._ids[keep : self._n].copy()
+        self._n = keep
+        self.num_tokens = n_tokens
+        return self.allocator.free(dropped) if dropped.size else 0
+
+    def release(self) -> int:
+        """Drop this table's ownership of all its blocks. Returns the blocks freed."""
+        freed = self.allocator.free(self.blocks.copy()) if self._n else 0
+        self._n = 0
+        self.num_tokens = 0
+        return freed
+
+    def detach(self) -> tuple[list[int], int]:
+        """Hand the blocks and token count over to a new owner (a swap-out record) and empty the
+        table without releasing anything."""
+        out = (self.blocks.tolist(), self.num_tokens)
+        self._n = 0
+        self.num_tokens = 0
+        return out
+
+    def adopt(self, blocks: Sequence[int], num_tokens: int) -> None:
+        """Take over already-owned ``blocks`` holding ``num_tokens`` tokens (a swap-in)."""
+        if self._n:
+            raise RuntimeError("only an empty table can adopt blocks")
+        if len(blocks) != self.allocator.blocks_needed(num_tokens):
+            raise ValueError(f"{len(blocks)} blocks cannot hold exactly {num_tokens} tokens")
+        self._push(list(blocks))
+        self.num_tokens = int(num_tokens)
+
+    # --- sharing ----------------------------------------------------------------------------------
 
     def fork(self) -> BlockTable:
+        """A second table over the same blocks (each gains an owner)."""
         self.allocator.incref(self.blocks)
-        self.allocator.stats.forks += 1
-        return BlockTable(self.allocator, list(self.blocks), self.num_tokens)
+        return BlockTable(self.allocator, self.blocks.copy(), self.num_tokens)
 
-    def unshare(self, logical_block: int) -> tuple[int, int] | None:
-        """Make ``logical_block`` private. ``(old, new)`` when a copy is needed, else None."""
-        old = self.blocks[logical_block]
+    def make_private(self, logical: int) -> tuple[int, int] | None:
+        """Ensure logical block ``logical`` has this table as its only owner. Returns
+        ``(shared id, private id)`` when a copy is needed, None when it already was private."""
+        if not 0 <= logical < self._n:
+            raise IndexError(f"logical block {logical} outside a table of {self._n}")
+        old = int(self._ids[logical])
         new = self.allocator.copy_on_write(old)
         if new == old:
             return None
-        self.blocks[logical_block] = new
+        self._ids[logical] = new
         return old, new
 
-    def writable_block_for(self, position: int) -> tuple[int, int, tuple[int, int] | None]:
-        logical = position // self.block_size
-        copied = self.unshare(logical)
-        return self.blocks[logical], position % self.block_size, copied
+    # --- addressing -------------------------------------------------------------------------------
+
+    def locate(self, position: int) -> tuple[int, int]:
+        """``(physical block, offset)`` of a written position."""
+        if not 0 <= position < self.num_tokens:
+            raise IndexError(
+                f"position {position} was never written (table holds {self.num_tokens} tokens); "
+                "its slot may hold another sequence's keys"
+            )
+        bs = self.block_size
+        return int(self._ids[position // bs]), position % bs
 
     def slots(self, start: int, n: int) -> np.ndarray:
-        """int32 slot ids of positions ``[start, start + n)``; they must be within capacity."""
-        if start < 0 or start + n > self.capacity:
-            raise IndexError(f"positions [{start}, {start + n}) exceed capacity {self.capacity}")
+        """int32 pool slots of positions ``[start, start + n)`` (within capacity)."""
+        if start < 0 or n < 0 or start + n > self.capacity:
+            raise IndexError(
+                f"positions [{start}, {start + n}) fall outside capacity {self.capacity}"
+            )
+        bs = self.block_size
         pos = np.arange(start, start + n, dtype=np.int64)
-        table = np.asarray(self.blocks, dtype=np.int64)
-        return (table[pos // self.block_size] * self.block_size + pos % self.block_size).astype(
-            np.int32
-        )
+        return (self._ids[pos // bs].astype(np.int64) * bs + pos % bs).astype(np.int32)
 
-    def free(self) -> int:
-        reclaimed = self.allocator.free(self.blocks)
-        self.blocks = []
-        self.num_tokens = 0
-        return reclaimed
+    def snapshot(self) -> dict:
+        return {"tokens": self.num_tokens, "blocks": self.blocks.tolist(),
+                "capacity": self.capacity}
 
-    def to_dict(self) -> dict[str, Any]:
-        return {
-            "num_tokens": self.num_tokens,
-            "num_blocks": len(self.blocks),
-            "capacity": self.capacity,
-            "slack": self.slack,
-            "blocks": list(self.blocks),
-        }
+
+def pack_tables(tables: Sequence[BlockTable], width: int | None = None) -> np.ndarray:
+    """``[len(tables), width]`` int32 block-table matrix, rows padded with ``NO_BLOCK``."""
+    width = max([t.num_blocks for t in tables] + [1]) if width is None else width
+    out = np.full((len(tables), width), NO_BLOCK, dtype=np.int32)
+    for r, t in enumerate(tables):
+        if t.num_blocks > width:
+            raise ValueError(f"table {r} has {t.num_blocks} blocks, wider than {width}")
+        out[r, : t.num_blocks] = t.blocks
+    return out
+
+
+def step_slots(tables: Sequence[BlockTable], counts: Sequence[int]) -> np.ndarray:
+    """Slot mapping of a packed step: for each table, its last ``counts[r]`` written positions
+    (the tokens this step appends), concatenated in table order."""
+    parts = [t.slots(t.num_tokens - c, c) for t, c in zip(tables, counts, strict=True)]
+    return np.concatenate(parts) if parts else np.zeros(0, dtype=np.int32)

@@ -76,10 +76,10 @@ class PagedKVCache:
     def nbytes(self) -> int:
         per_block = self.allocator.block_size * self.spec.n_kv_heads * self.spec.head_dim
         itemsize = torch.finfo(self.dtype).bits // 8
-        return 2 * len(self.table.blocks) * per_block * itemsize * len(self.key_pool)
+        return 2 * self.table.num_blocks * per_block * itemsize * len(self.key_pool)
 
     def used_bytes(self) -> int:
-        if not self.table.blocks:
+        if not self.table.num_blocks:
             return 0
         return self.nbytes * self.seq_len // self.table.capacity
 
@@ -94,14 +94,36 @@ class PagedKVCache:
         blocks = np.asarray(self.table.blocks, dtype=np.int32)
         self._slots, self._blocks = kernels.upload_int32([slots, blocks], self.device)
 
+    def blocks_to_reserve(self, n_new: int) -> int:
+        """Free blocks :meth:`reserve` would take for ``n_new`` more tokens: the fresh blocks past
+        the table's capacity plus a private copy of every shared block in the write range."""
+        table, bs = self.table, self.allocator.block_size
+        fresh = max(0, self.allocator.blocks_needed(self.seq_len + n_new) - table.num_blocks)
+        first, last = self.seq_len // bs, min(table.num_blocks, -(-(self.seq_len + n_new) // bs))
+        shared = sum(self.allocator.refcount(int(b)) > 1 for b in table.blocks[first:last])
+        return fresh + int(shared)
+
     def reserve(self, n_new: int) -> np.ndarray:
         """Grow the table by ``n_new`` tokens, copy-on-write any shared block in the write range
         (every layer), and return the int32 pool slots of positions ``[seq_len - n_new,
         seq_len)``. The host half of :meth:`begin_append`, for callers that upload several
         sequences' metadata at once (the ragged executor)."""
-        self.table.append(n_new)
-        self._unshare_write_range(self.seq_len - n_new, n_new)
+        self.table.grow(n_new)
+        try:
+            self._unshare_write_range(self.seq_len - n_new, n_new)
+        except Exception:
+            self.table.shrink_to(self.seq_len - n_new)
+            raise
         return self.table.slots(self.seq_len - n_new, n_new)
+
+    def unreserve(self, n_new: int) -> None:
+        """Take back the last :meth:`reserve` of ``n_new`` tokens (nothing was written yet)."""
+        self.table.shrink_to(self.seq_len - n_new)
+
+    def adopt_prefix(self, blocks: list[int], n_tokens: int) -> None:
+        """Start an empty sequence from ``blocks`` (already owned by the caller, e.g. a prefix
+        cache hit) holding its first ``n_tokens`` tokens."""
+        self.table.adopt(blocks, n_tokens)
 
     def append(self, key: torch.Tensor, value: torch.Tensor, layer_idx: int) -> None:
         """Write this step's post-RoPE K/V ``(1, kv_heads, n_new, head_dim)``; no gather."""
@@ -142,16 +164,21 @@ class PagedKVCache:
 
     def _unshare_write_range(self, start: int, n_new: int) -> None:
         """Copy-on-write every shared block in ``[start, start + n_new)``, in every layer's pool."""
-        if not self.table.blocks or n_new <= 0:
+        if not self.table.num_blocks or n_new <= 0:
             return
         bs = self.allocator.block_size
         pairs = []
-        for logical in range(start // bs, (start + n_new - 1) // bs + 1):
-            copied = self.table.unshare(logical)
-            if copied is not None:
-                pairs.append(copied)
-        if not pairs:
-            return
+        try:
+            for logical in range(start // bs, min(self.table.num_blocks,
+                                                   (start + n_new - 1) // bs + 1)):
+                copied = self.table.make_private(logical)
+                if copied is not None:
+                    pairs.append(copied)
+        finally:  # a block already switched to its private copy gets its contents either way
+            if pairs:
+                self._copy_blocks(pairs)
+
+    def _copy_blocks(self, pairs: list[tuple[int, int]]) -> None:
         src, dst = kernels.upload_int32(
             [np.array([p[0] for p in pairs], np.int32), np.array([p[1] for p in pairs], np.int32)],
             self.device,
@@ -187,7 +214,7 @@ class PagedKVCache:
 
     def gather(self, layer_idx: int) -> tuple[torch.Tensor, torch.Tensor]:
         """The sequence's K and V as contiguous ``(1, kv_heads, seq_len, head_dim)``."""
-        if not self.table.blocks or self.seq_len == 0:
+        if not self.table.num_blocks or self.seq_len == 0:
             empty = torch.zeros(
                 (1, self.spec.n_kv_heads, 0, self.spec.head_dim), dtype=self.dtype,
                 device=self.device,
@@ -211,7 +238,7 @@ class PagedKVCache:
 
     def free(self) -> int:
         self._slots = self._blocks = None
-        return self.table.free()
+        return self.table.release()
 
     def reset(self) -> None:
         self.free()

@@ -1,194 +1,214 @@
-"""Preemption of live sequences when the paged pool runs out: swap, recompute or reject.
+"""Taking pool blocks back from running requests: swap the KV to host memory, drop it for a
+recompute, or reject the request (policies of ``edgerag/cache/preemption.py:45-48``).
 
-Follows ``edgerag/cache/preemption.py`` (``Preemptor`` ``:91-233``): the same policies, records,
-statistics, victim order and ``to_dict`` keys. The pools here are head-major
-``(kv_heads, num_blocks, block_size, head_dim)`` device tensors, so a victim's KV is the block-axis
-slice ``pool[:, blocks]`` of every layer.
+A swap moves whole blocks of every layer with the library's own kernels, keeping the pools'
+head-major layout:
 
-* ``swap_out`` gathers the victim's blocks of every layer (one ``index_select`` per pool) and
-  copies them into host memory allocated pinned (never registered after the fact), all enqueued
-  on the current stream, *then* returns the blocks to the allocator: any later kernel that reuses
-  a block is enqueued behind the gather on that stream, so the reference's copy-before-free rule
-  (``:119-121``) holds without a host wait. An event marks the copies' end.
-* ``swap_in`` reallocates the blocks (``OutOfBlocksError`` when the pool cannot take the sequence
-  back: an admission decision, ``:145-149``), waits on the swap-out event, and scatters each layer
-  back with one ``index_copy_`` (``:142-171``).
+* out: ``edgerag_kv_gather`` reads the victim's blocks of each layer's K and V pool into one
+  device staging tensor ``[layers, 2, kv_heads, n_blocks * block_size, head_dim]`` (a block list
+  gathered for ``n_blocks * block_size`` positions is exactly ``pool[:, blocks]``), and one
+  asynchronous copy moves it to pinned host memory. The blocks go back to the allocator right
+  after the copies are *enqueued*: a kernel that later reuses a block is enqueued behind them on
+  the same stream, so it cannot overwrite data not yet read, and the host never waits.
+* in: the record is copied back to a device staging tensor and ``edgerag_kv_append`` scatters it
+  into freshly allocated blocks (slot ``new[p // bs] * bs + p % bs`` for position ``p``): bit for
+  bit what left, at new block ids.
 
-One deliberate difference: the reference reads the block count of a record from axis 0 of the
-head-major slice (``:157``, and ``preempt`` returns ``len(record.keys[0])``, ``:186``), which is
-the KV-head count; here it is the block axis, so a sequence comes back with as many blocks as it
-left with, and ``preempt`` returns the blocks it freed.
+A :class:`SwappedSequence` holds the host copy. Reading it (:meth:`SwappedSequence.layer`) first
+waits for the copy to land, so it never hands out memory the device is still writing.
 """
 
 from __future__ import annotations
 
-from dataclasses import dataclass, field
+from dataclasses import dataclass
 from enum import Enum
 from typing import Any
 
+import numpy as np
 import torch
 
 from edgerag_amd.cache.allocator import BlockAllocator
 
 
 class PreemptionPolicy(str, Enum):
-    """``edgerag/cache/preemption.py:45-48``."""
-
     SWAP = "swap"
     RECOMPUTE = "recompute"
     REJECT = "reject"
 
 
-@dataclass
 class SwappedSequence:
-    """A victim's KV in host memory: per layer ``(kv_heads, n_blocks, block_size, head_dim)``, the
-    pool's own layout, so restoring is one scatter per layer."""
+    """A victim's KV in pinned host memory, ``[layers, 2 (K, V), kv_heads, n_tokens_cap,
+    head_dim]`` with ``n_tokens_cap = num_blocks * block_size``."""
 
-    request_id: str
-    num_tokens: int
-    keys: list[torch.Tensor]
-    values: list[torch.Tensor]
-    ready: torch.cuda.Event | None = None  # recorded after the device-to-host copies
-
-    @property
-    def num_blocks(self) -> int:
-        return int(self.keys[0].shape[1])
+    def __init__(self, request_id: str, num_tokens: int, num_blocks: int, host: torch.Tensor,
+                 ready: torch.cuda.Event | None) -> None:
+        self.request_id = request_id
+        self.num_tokens = num_tokens
+        self.num_blocks = num_blocks
+        self._host = host
+        self._ready = ready
 
     @property
     def nbytes(self) -> int:
-        per = self.keys[0].numel() * self.keys[0].element_size()
-        return 2 * per * len(self.keys)
+        return self._host.numel() * self._host.element_size()
 
     def wait(self) -> None:
-        """Block the host until the copies have landed (before reading ``keys``/``values``)."""
-        if self.ready is not None:
-            self.ready.synchronize()
+        """Block until the device-to-host copy has completed."""
+        if self._ready is not None:
+            self._ready.synchronize()
+            self._ready = None
+
+    def layer(self, idx: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """Host K and V of layer ``idx`` as ``(kv_heads, num_blocks, block_size, head_dim)``,
+        the layout of ``pool[:, blocks]`` (waits for the copy first)."""
+        self.wait()
+        _, _, h, t, d = self._host.shape
+        bs = t // self.num_blocks
+        k, v = self._host[idx]
+        return k.view(h, self.num_blocks, bs, d), v.view(h, self.num_blocks, bs, d)
+
+    def staged(self, device: torch.device) -> torch.Tensor:
+        """The record on ``device`` (asynchronous on the current stream, after the swap-out)."""
+        if self._ready is not None:
+            torch.cuda.current_stream(device).wait_event(self._ready)
+        return self._host.to(device, non_blocking=True)
 
 
 @dataclass
-class PreemptionStats:
-    preemptions: int = 0
-    swaps_out: int = 0
-    swaps_in: int = 0
-    recomputes: int = 0
-    rejects: int = 0
-    bytes_swapped: int = 0
-    blocks_reclaimed: int = 0
-    extra: dict[str, Any] = field(default_factory=dict)
+class PreemptionCounters:
+    evicted: int = 0
+    swapped_out: int = 0
+    swapped_in: int = 0
+    recomputed: int = 0
+    rejected: int = 0
+    discarded: int = 0
+    bytes_moved: int = 0
+    blocks_returned: int = 0
+
+
+def _block_slots(blocks: list[int], block_size: int) -> np.ndarray:
+    ids = np.asarray(blocks, dtype=np.int64)[:, None] * block_size
+    return (ids + np.arange(block_size, dtype=np.int64)[None, :]).reshape(-1).astype(np.int32)
 
 
 class Preemptor:
-    """Frees pool capacity by evicting live sequences under the configured policy."""
-
     def __init__(self, allocator: BlockAllocator,
-                 policy: PreemptionPolicy = PreemptionPolicy.SWAP,
-                 pin_memory: bool = True) -> None:
+                 policy: PreemptionPolicy | str = PreemptionPolicy.SWAP) -> None:
         self.allocator = allocator
         self.policy = PreemptionPolicy(policy)
-        # Pinned host memory makes the copies DMA transfers; it is allocated pinned, and the
-        # scheduler bounds how many sequences sit swapped (pinned memory is not pageable).
-        self.pin_memory = pin_memory and torch.cuda.is_available()
         self.swapped: dict[str, SwappedSequence] = {}
-        self.stats = PreemptionStats()
+        self.counters = PreemptionCounters()
 
-    def _host(self, like: torch.Tensor) -> torch.Tensor:
-        return torch.empty(like.shape, dtype=like.dtype, device="cpu",
-                           pin_memory=self.pin_memory and like.is_cuda)
+    # --- block movement -----------------------------------------------------------------------
 
     def swap_out(self, request_id: str, blocks: list[int], num_tokens: int,
                  key_pool: list[torch.Tensor], value_pool: list[torch.Tensor]) -> SwappedSequence:
-        """Copy a victim's blocks of every layer to host memory, then release the blocks."""
+        """Copy ``blocks`` of every layer to pinned host memory, then return them to the pool."""
+        from edgerag_amd import kernels  # the HIP library: swapping runs on the device only
+
         if request_id in self.swapped:
-            raise KeyError(f"{request_id!r} is already swapped out")
+            raise KeyError(f"{request_id!r} already has a swapped-out record")
+        if not blocks:
+            raise ValueError(f"{request_id!r}: nothing to swap out")
+        kernels.require_device(*key_pool, *value_pool)
         device = key_pool[0].device
-        idx = torch.as_tensor(blocks, dtype=torch.long).to(device)
-        keys, values = [], []
-        for kp, vp in zip(key_pool, value_pool, strict=True):
-            for pool, out in ((kp, keys), (vp, values)):
-                staged = pool.index_select(1, idx)  # (kv_heads, n_blocks, bs, d), on the stream
-                host = self._host(staged)
-                host.copy_(staged, non_blocking=host.is_pinned())
-                out.append(host)
-        ready = None
-        if device.type == "cuda":
-            ready = torch.cuda.Event()
-            ready.record(torch.cuda.current_stream(device))
-        record = SwappedSequence(request_id, num_tokens, keys, values, ready)
+        h, _, bs, d = key_pool[0].shape
+        n = len(blocks)
+        (ids,) = kernels.upload_int32([np.asarray(blocks, dtype=np.int32)], device)
+        staging = torch.empty((len(key_pool), 2, h, n * bs, d), dtype=key_pool[0].dtype,
+                              device=device)
+        for layer, (kp, vp) in enumerate(zip(key_pool, value_pool, strict=True)):
+            kernels.kv_gather(kp, ids, n * bs, out=staging[layer, 0])
+            kernels.kv_gather(vp, ids, n * bs, out=staging[layer, 1])
+        host = torch.empty(staging.shape, dtype=staging.dtype, pin_memory=True)
+        host.copy_(staging, non_blocking=True)
+        ready = torch.cuda.Event()
+        ready.record(torch.cuda.current_stream(device))
+        record = SwappedSequence(request_id, num_tokens, n, host, ready)
         self.swapped[request_id] = record
-        reclaimed = self.allocator.free(blocks)
-        self.stats.preemptions += 1
-        self.stats.swaps_out += 1
-        self.stats.bytes_swapped += record.nbytes
-        self.stats.blocks_reclaimed += reclaimed
+        self.counters.blocks_returned += self.allocator.free(blocks)
+        self.counters.swapped_out += 1
+        self.counters.bytes_moved += record.nbytes
         return record
 
     def swap_in(self, request_id: str, key_pool: list[torch.Tensor],
                 value_pool: list[torch.Tensor]) -> tuple[list[int], int]:
-        """Reallocate blocks and restore a swapped sequence. Returns ``(blocks, num_tokens)``;
-        ``OutOfBlocksError`` (nothing changed) when the pool cannot take it back."""
+        """Allocate blocks for a swapped-out sequence and restore its KV into them. Returns
+        ``(blocks, num_tokens)``; raises ``OutOfBlocksError`` (record kept) if the pool is short."""
+        from edgerag_amd import kernels
+
         record = self.swapped.get(request_id)
         if record is None:
-            raise KeyError(f"no swapped sequence {request_id!r}")
+            raise KeyError(f"{request_id!r} has no swapped-out record")
         blocks = self.allocator.allocate(record.num_blocks)
         device = key_pool[0].device
-        if record.ready is not None and device.type == "cuda":
-            torch.cuda.current_stream(device).wait_event(record.ready)
-        idx = torch.as_tensor(blocks, dtype=torch.long).to(device)
+        _, _, bs, _ = key_pool[0].shape
+        staged = record.staged(device)
+        (slots,) = kernels.upload_int32([_block_slots(blocks, bs)], device)
         for layer, (kp, vp) in enumerate(zip(key_pool, value_pool, strict=True)):
-            for pool, host in ((kp, record.keys[layer]), (vp, record.values[layer])):
-                pool.index_copy_(1, idx, host.to(device, non_blocking=host.is_pinned()))
+            k = staged[layer, 0].transpose(0, 1)  # (tokens, kv_heads, head_dim) view
+            v = staged[layer, 1].transpose(0, 1)
+            kernels.kv_append(k, v, slots, kp, vp)
         del self.swapped[request_id]
-        self.stats.swaps_in += 1
-        self.stats.bytes_swapped += record.nbytes
+        self.counters.swapped_in += 1
+        self.counters.bytes_moved += record.nbytes
         return blocks, record.num_tokens
 
-    def preempt(self, request_id: str, blocks: list[int], num_tokens: int,
-                key_pool: list[torch.Tensor] | None = None,
-                value_pool: list[torch.Tensor] | None = None) -> int:
-        """Apply the configured policy. Returns the blocks returned to the pool."""
-        if self.policy is PreemptionPolicy.SWAP:
-            if key_pool is None or value_pool is None:
-                raise ValueError("SWAP requires the KV pools")
-            before = self.stats.blocks_reclaimed
-            self.swap_out(request_id, blocks, num_tokens, key_pool, value_pool)
-            return self.stats.blocks_reclaimed - before
-        reclaimed = self.allocator.free(blocks)
-        self.stats.preemptions += 1
-        self.stats.blocks_reclaimed += reclaimed
-        if self.policy is PreemptionPolicy.RECOMPUTE:
-            self.stats.recomputes += 1
-        else:
-            self.stats.rejects += 1
-        return reclaimed
+    # --- the scheduler's interface ------------------------------------------------------------
+
+    def evict(self, request: Any) -> str:
+        """Take ``request``'s blocks under the policy; returns the action taken ("swap",
+        "recompute" or "reject"). For a swap the request keeps its (now empty) cache object and
+        ``request.swap`` holds the record; otherwise the caller drops the cache."""
+        self.counters.evicted += 1
+        cache = request.cache
+        if self.policy is PreemptionPolicy.SWAP and cache is not None and cache.table.num_blocks:
+            blocks, n_tokens = cache.table.detach()
+            request.swap = self.swap_out(request.request_id, blocks, n_tokens, cache.key_pool,
+                                         cache.value_pool)
+            return "swap"
+        if self.policy is PreemptionPolicy.REJECT:
+            self.counters.rejected += 1
+            return "reject"
+        self.counters.recomputed += 1
+        return "recompute"
+
+    def restore(self, request: Any) -> None:
+        """Bring a swapped-out request's KV back into its cache (``OutOfBlocksError``: nothing
+        changed, the record is kept)."""
+        cache = request.cache
+        blocks, n_tokens = self.swap_in(request.request_id, cache.key_pool, cache.value_pool)
+        cache.table.adopt(blocks, n_tokens)
+        request.swap = None
+
+    def discard(self, request: Any) -> None:
+        """Drop a swapped-out record (the request will recompute, or is gone)."""
+        if self.swapped.pop(request.request_id, None) is not None:
+            self.counters.discarded += 1
+        request.swap = None
 
     @staticmethod
     def select_victims(candidates: list[tuple[str, int]], blocks_needed: int) -> list[str]:
-        """Newest first until ``blocks_needed`` is covered (``candidates`` in arrival order), as
-        ``edgerag/cache/preemption.py:198-217``."""
-        victims: list[str] = []
-        freed = 0
-        for request_id, held in reversed(candidates):
-            if freed >= blocks_needed:
+        """Victims among ``(request_id, blocks held)`` in admission order: the most recently
+        admitted first, until their blocks cover ``blocks_needed``."""
+        picked: list[str] = []
+        covered = 0
+        for rid, held in candidates[::-1]:
+            if covered >= blocks_needed:
                 break
-            victims.append(request_id)
-            freed += held
-        return victims
+            picked.append(rid)
+            covered += held
+        return picked
 
     @property
     def swapped_bytes(self) -> int:
-        return sum(record.nbytes for record in self.swapped.values())
+        return sum(r.nbytes for r in self.swapped.values())
 
-    def to_dict(self) -> dict[str, Any]:
-        return {
-            "policy": self.policy.value,
-            "pin_memory": self.pin_memory,
-            "num_swapped": len(self.swapped),
-            "swapped_bytes": self.swapped_bytes,
-            "preemptions": self.stats.preemptions,
-            "swaps_out": self.stats.swaps_out,
-            "swaps_in": self.stats.swaps_in,
-            "recomputes": self.stats.recomputes,
-            "rejects": self.stats.rejects,
-            "bytes_swapped": self.stats.bytes_swapped,
-            "blocks_reclaimed": self.stats.blocks_reclaimed,
-        }
+    def snapshot(self) -> dict[str, Any]:
+        c = self.counters
+        return {"policy": self.policy.value, "held": {"requests": len(self.swapped),
+                                                      "bytes": self.swapped_bytes},
+                "events": {"evicted": c.evicted, "swapped_out": c.swapped_out,
+                           "swapped_in": c.swapped_in, "recomputed": c.recomputed,
+                           "rejected": c.rejected, "discarded": c.discarded,
+                           "bytes_moved": c.bytes_moved, "blocks_returned": c.blocks_returned}}

@@ -44,6 +44,8 @@ class StepInputs:
     slots: torch.Tensor  # (T,) int32 pool slot of every new token
     logit_rows: torch.Tensor  # (R',) int32 rows of the packed batch whose logits are needed
     plan: kernels.AttentionPlan | kernels.FixedAttention  # eager plan, or graph-stable staging
+    #: (T, hidden) input rows replacing the embedding lookup (prompt embeddings), or None.
+    hidden: torch.Tensor | None = None
 
 
 def _config(bits: int, group_size: int | None, in_features: int) -> QuantConfig:
@@ -192,7 +194,9 @@ class EdgeRagDecoder(nn.Module):
         spec = self.spec
         T = step.token_ids.shape[0]
         d, eps = spec.head_dim, spec.rms_norm_eps
-        hidden = self.embed_tokens[step.token_ids.long()]
+        # The residual stream is updated in place, so it is always a fresh tensor of this step.
+        hidden = (self.embed_tokens[step.token_ids.long()] if step.hidden is None
+                  else step.hidden)
         x = kernels.rmsnorm(hidden, self.layers[0].input_layernorm.weight, eps)
         q = torch.empty((T, spec.n_q_heads, d), device=self.device, dtype=self.dtype)
         attn_out = torch.empty_like(q)

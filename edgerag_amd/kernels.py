@@ -118,12 +118,18 @@ def kv_append(
     )
 
 
-def kv_gather(pool: torch.Tensor, block_ids: torch.Tensor, seq_len: int) -> torch.Tensor:
-    """``(kv_heads, seq_len, head_dim)`` history of one sequence, copied out of the pool."""
-    require_device(pool, block_ids)
+def kv_gather(pool: torch.Tensor, block_ids: torch.Tensor, seq_len: int,
+              out: torch.Tensor | None = None) -> torch.Tensor:
+    """``(kv_heads, seq_len, head_dim)`` history of one sequence, copied out of the pool (into
+    ``out`` when given: contiguous, the pool's dtype)."""
+    require_device(pool, block_ids, out)
     _check_pool(pool, "pool")
     n_heads, num_blocks, block_size, head_dim = pool.shape
-    out = torch.empty((n_heads, seq_len, head_dim), dtype=pool.dtype, device=pool.device)
+    if out is None:
+        out = torch.empty((n_heads, seq_len, head_dim), dtype=pool.dtype, device=pool.device)
+    elif (out.shape != (n_heads, seq_len, head_dim) or out.dtype != pool.dtype
+          or not out.is_contiguous()):
+        raise ValueError(f"out must be contiguous ({n_heads}, {seq_len}, {head_dim}) {pool.dtype}")
     if seq_len == 0:
         return out
     if block_ids.dtype != torch.int32:

@@ -4,14 +4,23 @@ Contract of the reference ``ModelExecutor`` (``edgerag/serve/executor.py:57-156`
 ``execute(batch) -> StepOutput``, where each prefilling request advances by at most
 ``chunk_size`` prompt tokens (``:116-130``), the final prefill chunk emits the request's first
 generated token (``:131-136``), each decoding request feeds its last generated token and emits the
-next (``:138-154``), and one KV arena is allocated once and shared by every request's block
-table (``:76-83``, B-05). Greedy selection is ``argmax`` over the last position's logits.
+next (``:138-154``), a request's ``prompt_embeds`` replace the embedding lookup of its prompt
+(``:103-110``), and one KV arena is allocated once and shared by every request's block table
+(``:76-83``). Greedy selection is ``argmax`` over the last position's logits.
 
 What changes: the reference runs one decoder forward per request per iteration, each with its own
 host-to-device index uploads and a device-to-host argmax. Here the whole batch is one forward:
 the host builds the step's metadata (token ids, logical positions, pool slots, cu_seqlens,
 context lengths, block tables, the attention work plan, the rows whose logits are read) and
 uploads it in one pinned copy; the argmax of every emitting request comes back in one copy.
+
+A step either happens entirely or not at all on the host side: positions past the model's RoPE
+table are refused (``ValueError``) and the batch's block need (fresh blocks plus copy-on-write
+copies) is checked against the free pool (:class:`StepDoesNotFit`, an ``OutOfBlocksError``)
+before any table changes, so a refused step leaves every request as it was. With a
+:class:`~edgerag_amd.cache.prefix.PrefixCache`, a request's first chunk starts after the longest
+prefix of full prompt blocks already computed by an earlier request, and a finished prompt's full
+blocks are indexed for later ones.
 """
 
 from __future__ import annotations
@@ -23,7 +32,8 @@ import numpy as np
 import torch
 
 from edgerag_amd import kernels
-from edgerag_amd.cache.allocator import BlockAllocator
+from edgerag_amd.cache.allocator import BlockAllocator, OutOfBlocksError
+from edgerag_amd.cache.block_table import pack_tables
 from edgerag_amd.cache.paged import PagedKVCache
 from edgerag_amd.core.model import EdgeRagDecoder, StepInputs
 from edgerag_amd.core.spec import ModelSpec
@@ -41,6 +51,26 @@ class StepOutput:
     prefilled: dict[str, int] = field(default_factory=dict)
 
 
+class StepDoesNotFit(OutOfBlocksError):
+    """The batch needs more free blocks than the pool has; nothing was changed.
+    ``blocks_needed`` is the free count the step needs (pass it to ``Scheduler.preempt``)."""
+
+    def __init__(self, message: str, blocks_needed: int) -> None:
+        super().__init__(message)
+        self.blocks_needed = blocks_needed
+
+
+@dataclass
+class _Entry:
+    request: Request
+    cache: PagedKVCache
+    ids: list[int]
+    start: int  # first prefill position of the slice (prefill), or the decode position
+    consumed: int  # prefill positions this step accounts for (prefix reuse included)
+    emits: bool
+    prefill: bool
+
+
 class ModelExecutor:
     def __init__(
         self,
@@ -52,9 +82,11 @@ class ModelExecutor:
         chunk_size: int = DEFAULT_CHUNK_SIZE,
         decode_graphs: bool = True,
         max_decode_batch: int = 8,
+        prefix_cache: Any = None,
     ) -> None:
         """``decode_graphs``: replay decode-only iterations (up to ``max_decode_batch`` requests)
-        from HIP graphs captured per batch size; iterations with a prefill chunk run eagerly."""
+        from HIP graphs captured per batch size; iterations with a prefill chunk run eagerly.
+        ``prefix_cache``: reuse computed prompt blocks across requests (token-id prompts)."""
         if chunk_size <= 0:
             raise ValueError(f"chunk_size must be positive, got {chunk_size}")
         self.decoder = decoder
@@ -63,6 +95,8 @@ class ModelExecutor:
         self.device = torch.device(device)
         self.dtype = dtype
         self.chunk_size = chunk_size
+        self.prefix_cache = prefix_cache
+        self.max_positions = spec.max_position_embeddings
         shape = (spec.n_kv_heads, allocator.num_blocks, allocator.block_size, spec.head_dim)
         self.key_pool = [torch.zeros(shape, dtype=dtype, device=self.device)
                          for _ in range(spec.n_layers)]
@@ -87,45 +121,120 @@ class ModelExecutor:
                                          pool=self.key_pool, value_pool=self.value_pool)
         return request.cache
 
-    @torch.inference_mode()
-    def execute(self, batch: Batch) -> StepOutput:
-        output = StepOutput()
-        # (request, new tokens, emits a token, is a prefill chunk)
-        entries: list[tuple[Request, list[int], bool, bool]] = []
+    # --- host side of a step ------------------------------------------------------------------
+
+    def _entries(self, batch: Batch) -> list[_Entry]:
+        entries: list[_Entry] = []
         for request in batch.prefill:
+            cache = self._cache_for(request)
             start = request.prefill_offset
-            end = min(start + self.chunk_size, request.prompt_len)
-            if end - start <= 0:
-                continue
-            entries.append((request, request.prompt_token_ids[start:end],
-                            end >= request.prompt_len, True))
+            if cache.seq_len != start:
+                raise RuntimeError(
+                    f"{request.request_id}: cache holds {cache.seq_len} positions but the prompt "
+                    f"is read up to {start}"
+                )
+            end = min(start + self.chunk_size, request.prefill_len)
+            if end > start:
+                entries.append(_Entry(request, cache, request.prefill_ids(start, end), start,
+                                      end - start, end >= request.prefill_len, True))
         for request in batch.decode:
             if not request.generated_token_ids:
                 raise RuntimeError(
-                    f"{request.request_id} reached decode with no generated token: prefill "
-                    "completed without emitting one"
+                    f"{request.request_id} is decoding but has no generated token to feed: its "
+                    "prefill never emitted one"
                 )
-            entries.append((request, [request.generated_token_ids[-1]], True, False))
+            cache = self._cache_for(request)
+            entries.append(_Entry(request, cache, [request.generated_token_ids[-1]],
+                                  cache.seq_len, 0, True, False))
+        return entries
+
+    def _reuse_prefix(self, e: _Entry) -> int:
+        """Start a fresh token-id prompt after its longest cached prefix (at least one prompt
+        token is left to compute: the first generated token comes out of that forward)."""
+        r = e.request
+        if (self.prefix_cache is None or not e.prefill or e.start != 0 or r.refeed
+                or r.prompt_embeds is not None or e.cache.seq_len):
+            return 0
+        blocks, n = self.prefix_cache.lookup(r.prompt_token_ids, max_tokens=r.prompt_len - 1)
+        if n:
+            e.cache.adopt_prefix(blocks, n)
+            end = min(n + self.chunk_size, r.prefill_len)
+            e.ids, e.start = r.prefill_ids(n, end), n
+            e.consumed, e.emits = end, end >= r.prefill_len
+        return n
+
+    def _reserve(self, entries: list[_Entry]) -> list[np.ndarray]:
+        """All of the step's reservations or none (see the module docstring)."""
+        adopted = [e for e in entries if self._reuse_prefix(e)]
+
+        def undo_adoptions() -> None:
+            for e in adopted:
+                e.cache.free()
+                end = min(self.chunk_size, e.request.prefill_len)
+                e.ids, e.start = e.request.prefill_ids(0, end), 0
+                e.consumed, e.emits = end, end >= e.request.prefill_len
+
+        for e in entries:
+            top = e.cache.seq_len + len(e.ids)
+            if top > self.max_positions:
+                undo_adoptions()
+                raise ValueError(
+                    f"{e.request.request_id}: position {top - 1} is past the model's "
+                    f"{self.max_positions} positions (RoPE table)"
+                )
+        need = sum(e.cache.blocks_to_reserve(len(e.ids)) for e in entries)
+        if need > self.allocator.num_free:
+            undo_adoptions()
+            raise StepDoesNotFit(
+                f"step needs {need} free blocks, the pool has {self.allocator.num_free}", need)
+        done: list[_Entry] = []
+        slots = []
+        try:
+            for e in entries:
+                slots.append(e.cache.reserve(len(e.ids)))
+                done.append(e)
+        except Exception:
+            for e in reversed(done):
+                e.cache.unreserve(len(e.ids))
+            undo_adoptions()
+            raise
+        return slots
+
+    def _prompt_rows(self, entries: list[_Entry], qsl: list[int],
+                     ids_d: torch.Tensor) -> torch.Tensor | None:
+        """Packed input rows when a prefill slice comes with ``prompt_embeds`` (None: every row is
+        an embedding lookup)."""
+        with_embeds = [(i, e) for i, e in enumerate(entries)
+                       if e.prefill and e.request.prompt_embeds is not None]
+        if not with_embeds:
+            return None
+        hidden = self.decoder.embed_tokens[ids_d.long()]
+        for i, e in with_embeds:
+            pe = e.request.prompt_embeds
+            pe = pe[0] if pe.dim() == 3 else pe
+            lo, hi = e.start, min(e.start + len(e.ids), e.request.prompt_len)
+            if hi > lo:
+                hidden[qsl[i] : qsl[i] + hi - lo] = pe[lo:hi].to(self.device, self.dtype)
+        return hidden
+
+    @torch.inference_mode()
+    def execute(self, batch: Batch) -> StepOutput:
+        output = StepOutput()
+        entries = self._entries(batch)
         if not entries:
             return output
-
-        qsl, ctx, ids, pos, slots, tables, rows, emitting = [0], [], [], [], [], [], [], []
-        for request, toks, emits, _ in entries:
-            cache = self._cache_for(request)
-            n = len(toks)
-            slots.append(cache.reserve(n))
-            L = cache.seq_len
+        slots = self._reserve(entries)
+        qsl, ctx, pos, ids, rows, emitting = [0], [], [], [], [], []
+        for e in entries:
+            n, L = len(e.ids), e.cache.seq_len
+            qsl.append(qsl[-1] + n)
             ctx.append(L)
             pos.append(np.arange(L - n, L, dtype=np.int32))
-            ids.extend(toks)
-            qsl.append(qsl[-1] + n)
-            tables.append(cache.table.blocks)
-            if emits:
+            ids.extend(e.ids)
+            if e.emits:
                 rows.append(qsl[-1] - 1)
-                emitting.append(request)
-        bt = np.full((len(entries), max(len(t) for t in tables)), -1, np.int32)
-        for r, t in enumerate(tables):
-            bt[r, : len(t)] = t
+                emitting.append(e.request)
+        bt = pack_tables([e.cache.table for e in entries])
         spec = self.spec
         extras = [np.concatenate(slots).astype(np.int32), np.concatenate(pos),
                   np.asarray(ids, np.int32), np.asarray(rows, np.int32)]
@@ -134,27 +243,30 @@ class ModelExecutor:
             logits, choice = self._replay_decode(len(entries))
             self.last_logits = logits
             tokens = choice.cpu().tolist()
-            for request, token in zip(emitting, tokens):
-                output.tokens[request.request_id] = int(token)
             self.graph_steps += 1
-            return output
-        plan, (slot_d, pos_d, ids_d, rows_d) = kernels.plan_attention(
-            np.asarray(qsl, np.int32), np.asarray(ctx, np.int32), bt, spec.n_q_heads,
-            spec.n_kv_heads, spec.head_dim, self.allocator.block_size, self.dtype, self.device,
-            extras,
-        )
-        step = StepInputs(ids_d, pos_d, slot_d, rows_d, plan)
-        if emitting:
-            logits = self.decoder.logits(step, self.key_pool, self.value_pool)
-            self.last_logits = logits
-            tokens = kernels.argmax_rows(logits).cpu().tolist()
-            for request, token in zip(emitting, tokens):
-                output.tokens[request.request_id] = int(token)
         else:
-            self.decoder.forward_hidden(step, self.key_pool, self.value_pool)
-        for request, toks, _, is_prefill in entries:
-            if is_prefill:
-                output.prefilled[request.request_id] = len(toks)
+            plan, (slot_d, pos_d, ids_d, rows_d) = kernels.plan_attention(
+                np.asarray(qsl, np.int32), np.asarray(ctx, np.int32), bt, spec.n_q_heads,
+                spec.n_kv_heads, spec.head_dim, self.allocator.block_size, self.dtype,
+                self.device, extras,
+            )
+            step = StepInputs(ids_d, pos_d, slot_d, rows_d, plan,
+                              self._prompt_rows(entries, qsl, ids_d))
+            tokens = []
+            if emitting:
+                logits = self.decoder.logits(step, self.key_pool, self.value_pool)
+                self.last_logits = logits
+                tokens = kernels.argmax_rows(logits).cpu().tolist()
+            else:
+                self.decoder.forward_hidden(step, self.key_pool, self.value_pool)
+        for request, token in zip(emitting, tokens):
+            output.tokens[request.request_id] = int(token)
+        for e in entries:
+            if e.prefill:
+                output.prefilled[e.request.request_id] = e.consumed
+                if e.emits and self.prefix_cache is not None and not e.request.refeed \
+                        and e.request.prompt_embeds is None:
+                    self.prefix_cache.register(e.request.prompt_token_ids, e.cache.table.blocks)
         return output
 
     # --- decode iterations replayed from HIP graphs ------------------------------------------
@@ -213,7 +325,13 @@ def drive(scheduler, executor: ModelExecutor, max_steps: int = 100000, on_step=N
         batch = scheduler.schedule()
         if batch.is_empty:
             break
-        output = executor.execute(batch)
+        try:
+            output = executor.execute(batch)
+        except StepDoesNotFit as short:
+            # Nothing ran: free blocks by preemption and decide the iteration again.
+            if not scheduler.preempt(short.blocks_needed):
+                raise
+            continue
         apply_output(scheduler, batch, output)
         steps += 1
         if on_step is not None:

@@ -194,7 +194,7 @@ def test_copy_on_write_copies_contents_once_for_every_layer(device) -> None:
     fill(parent, 10, 3.0)
     child = parent.fork()
     fill(child, 2, 9.0)
-    assert allocator.stats.copy_on_writes == 1
+    assert allocator.counters.private_copies == 1
     for layer in range(6):
         keys, _ = child.gather(layer)
         assert (keys[0, :, :10] == 3.0).all()
@@ -202,9 +202,11 @@ def test_copy_on_write_copies_contents_once_for_every_layer(device) -> None:
 
 
 def test_swap_out_in_on_device_pools(device) -> None:
-    """Swap-out gathers the victim's blocks into pinned host memory on the stream before the
-    blocks are freed: a kernel that reuses them right after (on the same stream) cannot change
-    the swapped copy; swap-in restores every layer bit for bit at the newly allocated blocks."""
+    """Swap-out gathers the victim's blocks of every layer with edgerag_kv_gather into a device
+    staging buffer and copies it to pinned host memory on the stream, before the blocks are
+    freed: a kernel that reuses them right after (on the same stream) cannot change the swapped
+    copy. Swap-in scatters it back with edgerag_kv_append: every layer bit for bit at the newly
+    allocated blocks."""
     from edgerag_amd.cache.allocator import BlockAllocator
     from edgerag_amd.cache.preemption import Preemptor
 
@@ -214,18 +216,41 @@ def test_swap_out_in_on_device_pools(device) -> None:
     vp = [torch.randn(heads, nb, bs, d, generator=g, device=device).half() for _ in range(layers)]
     alloc = BlockAllocator(nb, bs)
     blocks = alloc.allocate(9)
-    saved = [p[:, blocks].clone() for p in kp + vp]
+    saved_k = [p[:, blocks].clone() for p in kp]
+    saved_v = [p[:, blocks].clone() for p in vp]
     pre = Preemptor(alloc)
     rec = pre.swap_out("v", blocks, 130, kp, vp)
-    assert all(t.is_pinned() for t in rec.keys + rec.values)
     other = alloc.allocate(nb)  # every block, the victim's included, is reused at once
     for p in kp + vp:
         p[:, other] = 0
-    rec.wait()
-    for host, ref in zip(rec.keys + rec.values, [s.cpu() for s in saved]):
-        assert torch.equal(host, ref)
+    for layer in range(layers):  # reading the record waits for the copy
+        k, v = rec.layer(layer)
+        assert k.is_pinned() and torch.equal(k, saved_k[layer].cpu())
+        assert torch.equal(v, saved_v[layer].cpu())
     alloc.free(other)
     new_blocks, n = pre.swap_in("v", kp, vp)
     assert n == 130 and len(new_blocks) == 9
-    for p, ref in zip(kp + vp, saved):
-        assert torch.equal(p[:, new_blocks], ref)
+    for layer in range(layers):
+        assert torch.equal(kp[layer][:, new_blocks], saved_k[layer])
+        assert torch.equal(vp[layer][:, new_blocks], saved_v[layer])
+    alloc.check_invariants()
+
+
+def test_swap_in_without_room_keeps_the_record(device) -> None:
+    from edgerag_amd.cache.allocator import BlockAllocator, OutOfBlocksError
+    from edgerag_amd.cache.preemption import Preemptor
+
+    kp = [torch.randn(2, 8, 16, 64, device=device).half()]
+    vp = [torch.randn(2, 8, 16, 64, device=device).half()]
+    alloc = BlockAllocator(8, 16)
+    pre = Preemptor(alloc)
+    pre.swap_out("a", alloc.allocate(6), 90, kp, vp)
+    hog = alloc.allocate(4)
+    with pytest.raises(OutOfBlocksError):
+        pre.swap_in("a", kp, vp)
+    assert "a" in pre.swapped and alloc.num_free == 4
+    alloc.free(hog)
+    blocks, n = pre.swap_in("a", kp, vp)
+    assert len(blocks) == 6 and n == 90
+    with pytest.raises(KeyError):
+        pre.swap_in("a", kp, vp)

@@ -131,3 +131,116 @@ def test_decode_graph_replays_equal_the_eager_path(device, dtype) -> None:
     assert ex_e.graph_steps == 0 and ex_g.graph_steps > 5 and len(ex_g._graphs) >= 2
     assert steps_g == steps_e
     assert graph == eager
+
+
+# --- prompt embeddings (edgerag/serve/executor.py:103-110; tests/test_executor.py:212-268) -------
+
+
+def _run_one(model, request, chunk, device, prefix_cache=None, num_blocks=128):
+    alloc = BlockAllocator(num_blocks, 16)
+    executor = ModelExecutor(model, TOY, alloc, device, model.dtype, chunk_size=chunk,
+                             prefix_cache=prefix_cache)
+    sched = Scheduler(alloc, SchedulerConfig())
+    sched.add_request(request)
+    firsts = []
+    drive(sched, executor, on_step=lambda b, o: firsts.append(executor.last_logits[0].clone())
+          if o.tokens else None)
+    return firsts, alloc
+
+
+def test_prompt_embeds_are_read_instead_of_the_token_ids(device) -> None:
+    """A request whose prompt_embeds are another token sequence's embeddings generates exactly
+    what that other sequence generates from its ids: the embeddings were read, the ids were not
+    (a rescaled copy of the same embeddings would prove nothing: every layer starts with RMSNorm)."""
+    model, _ = _model(device, seed=8)
+    ids, other = _prompt(16, 80), _prompt(16, 81)
+    plain = Request("plain", other, max_new_tokens=3)
+    plain_logits, _ = _run_one(model, plain, 64, device)
+    embedded = Request("emb", ids, max_new_tokens=3)
+    embedded.prompt_embeds = model.embed_tokens[torch.tensor(other, device=device)][None].clone()
+    emb_logits, _ = _run_one(model, embedded, 64, device)
+    by_ids, _ = _run_one(model, Request("ids", ids, max_new_tokens=3), 64, device)
+    assert embedded.generated_token_ids == plain.generated_token_ids
+    assert torch.equal(emb_logits[0], plain_logits[0])
+    assert float((emb_logits[0] - by_ids[0]).abs().max()) > 1e-2
+
+
+def test_prompt_embeds_of_the_ids_reproduce_the_id_path_exactly(device) -> None:
+    model, _ = _model(device, seed=9)
+    ids = _prompt(16, 90)
+    plain = Request("plain", ids, max_new_tokens=3)
+    plain_logits, _ = _run_one(model, plain, 8, device)
+    embedded = Request("emb", ids, max_new_tokens=3)
+    embedded.prompt_embeds = model.embed_tokens[torch.tensor(ids, device=device)][None].clone()
+    emb_logits, _ = _run_one(model, embedded, 8, device)
+    assert embedded.generated_token_ids == plain.generated_token_ids
+    assert all(torch.equal(a, b) for a, b in zip(emb_logits, plain_logits))
+
+
+# --- prefix reuse and preemption through the executor ------------------------------------------
+
+
+def test_prefix_reuse_skips_the_shared_prompt_blocks(device) -> None:
+    """Request B shares A's first 48 prompt tokens (3 full blocks). With a prefix cache, B's
+    first chunk starts at position 48 over A's blocks; its tokens match a run without reuse."""
+    from edgerag_amd.cache.prefix import PrefixCache
+
+    model, _ = _model(device, seed=10)
+    shared = _prompt(48, 100)
+    a_ids, b_ids = shared + _prompt(13, 101), shared + _prompt(21, 102)
+    b_alone = Request("b", b_ids, max_new_tokens=4)
+    ref_logits, _ = _run_one(model, b_alone, 64, device)
+
+    alloc = BlockAllocator(128, 16)
+    cache = PrefixCache(alloc)
+    executor = ModelExecutor(model, TOY, alloc, device, model.dtype, chunk_size=64,
+                             prefix_cache=cache)
+    sched = Scheduler(alloc, SchedulerConfig())
+    a, b = Request("a", a_ids, max_new_tokens=4), Request("b", b_ids, max_new_tokens=4)
+    sched.add_request(a)
+    drive(sched, executor)
+    assert cache.num_cached == 3  # A's three full prompt blocks (61 tokens)
+    firsts = []
+    sched.add_request(b)
+    drive(sched, executor, on_step=lambda bt, o: firsts.append(executor.last_logits[0].clone())
+          if o.tokens else None)
+    assert cache.counters.blocks_served == 3
+    assert b.generated_token_ids == b_alone.generated_token_ids
+    for got, ref in zip(firsts, ref_logits):
+        torch.testing.assert_close(got, ref, rtol=1e-4, atol=1e-4)
+    cache.clear()
+    assert alloc.num_free == alloc.num_blocks
+
+
+@pytest.mark.parametrize("policy", ["swap", "recompute"])
+def test_preemption_mid_decode_keeps_the_generated_tokens(device, policy) -> None:
+    """Three decoding requests; after a few iterations the two newest are preempted. Swapped
+    ones come back with their KV restored bit for bit; recomputed ones re-read prompt + generated
+    tokens. Either way every request generates what it generates without preemption."""
+    from edgerag_amd.cache.preemption import Preemptor
+
+    model, _ = _model(device, seed=11)
+    prompts = [_prompt(n, 110 + n) for n in (30, 45, 20)]
+    ref, _, _ = _generate(model, TOY, prompts, 10, 64, device)
+
+    alloc = BlockAllocator(64, 16)
+    executor = ModelExecutor(model, TOY, alloc, device, model.dtype, chunk_size=64)
+    pre = Preemptor(alloc, policy)
+    sched = Scheduler(alloc, SchedulerConfig(), preemptor=pre)
+    reqs = [Request(f"r{i}", p, max_new_tokens=10) for i, p in enumerate(prompts)]
+    for r in reqs:
+        sched.add_request(r)
+    fired = []
+
+    def on_step(batch, output):
+        if len(fired) == 0 and all(r.num_generated >= 3 for r in reqs):
+            held = sum(r.cache.table.num_blocks for r in reqs[1:])
+            fired.append(sched.preempt(alloc.num_free + held))
+
+    drive(sched, executor, on_step=on_step)
+    assert fired and fired[0] == reqs[1:]
+    assert [r.generated_token_ids for r in reqs] == ref
+    assert all(r.preemptions == (1 if i else 0) for i, r in enumerate(reqs))
+    if policy == "swap":
+        assert pre.counters.swapped_out == 2 and pre.counters.swapped_in == 2
+    assert alloc.num_free == alloc.num_blocks and not pre.swapped

@@ -28,10 +28,10 @@ class _FakeCache:
         self.table = BlockTable(allocator=allocator)
 
     def grow(self, n: int) -> None:
-        self.table.append(n)
+        self.table.grow(n)
 
     def free(self) -> int:
-        return self.table.free()
+        return self.table.release()
 
 
 def _run_step(s: Scheduler, alloc: BlockAllocator, chunk: int, rng: random.Random | None = None):
@@ -86,13 +86,14 @@ def test_chunked_prefill_progress_and_state_transitions() -> None:
 
 
 def test_admission_budgets_prompt_plus_generation_and_keeps_the_reserve() -> None:
-    alloc = BlockAllocator(20, 16)  # 20 free, reserve 4 -> 16 admissible
+    alloc = BlockAllocator(40, 16)
+    alloc.allocate(20)  # held by someone else: 20 free, reserve 4 -> 16 admissible now
     s = Scheduler(alloc, SchedulerConfig(cow_reserve_blocks=4))
     big = _req(0, prompt=200, new=57)  # ceil(257/16) = 17 > 16: blocked
     s.add_request(big)
     s.add_request(_req(1, prompt=10, new=2))
     b = s.schedule()
-    assert b.is_empty and s.stats.admission_blocked == 1  # FIFO: the small one waits behind
+    assert b.is_empty and s.counters.queue_held == 1  # FIFO: the small one waits behind
     assert s.blocks_required(big) == 17
     fits = _req(2, prompt=200, new=56)  # 16 blocks
     s2 = Scheduler(BlockAllocator(20, 16), SchedulerConfig(cow_reserve_blocks=4))
@@ -121,7 +122,7 @@ def test_randomized_soak_conserves_the_pool() -> None:
             break
         _run_step(s, alloc, chunk=rng.choice([8, 64, 512]), rng=rng)
         alloc.check_invariants()
-        held = sum(len(r.cache.table.blocks) for r in s.running if r.cache is not None)
+        held = sum(r.cache.table.num_blocks for r in s.running if r.cache is not None)
         assert held == alloc.num_used
     assert not s.has_work and len(s.finished) == 40
     assert alloc.num_free == alloc.num_blocks
@@ -138,3 +139,72 @@ def test_poisson_arrivals_and_trace_are_seeded_and_shaped() -> None:
     assert all(64 <= r.max_new_tokens <= 256 for r in reqs)
     with pytest.raises(ValueError):
         poisson_arrivals(3, 0.0, 1)
+
+
+def test_illegal_lifecycle_moves_are_refused() -> None:
+    from edgerag_amd.sched.request import TransitionError
+
+    r = _req(0)
+    with pytest.raises(TransitionError):
+        r.move_to(RequestState.DECODING)  # WAITING -> DECODING skips prefill
+    r.move_to(RequestState.PREFILLING)
+    r.move_to(RequestState.DECODING)
+    r.move_to(RequestState.FINISHED)
+    assert r.is_terminal
+    with pytest.raises(TransitionError):
+        r.move_to(RequestState.WAITING)
+
+
+def test_requests_that_can_never_fit_are_rejected_not_blocking() -> None:
+    alloc = BlockAllocator(20, 16)
+    s = Scheduler(alloc, SchedulerConfig(cow_reserve_blocks=4, max_model_len=300))
+    too_long = _req(0, prompt=280, new=40)  # 320 positions > 300
+    too_big = Request("r1", list(range(1, 200)), max_new_tokens=100)  # 19 blocks > 16 ever
+    ok = _req(2, prompt=30, new=5)
+    for r in (too_long, too_big, ok):
+        s.add_request(r)
+    b = s.schedule()
+    assert b.prefill == [ok]
+    assert too_long.state is RequestState.REJECTED and "positions" in too_long.reject_reason
+    assert too_big.state is RequestState.REJECTED and s.rejected == [too_long, too_big]
+
+
+def test_preempt_recompute_folds_generated_tokens_into_the_prefill() -> None:
+    """Newest admission first; victims wait at the queue front in their old order; after a
+    recompute preemption the request re-reads prompt + generated tokens, and its next token comes
+    from that prefill's last position."""
+    alloc = BlockAllocator(64, 16)
+    s = Scheduler(alloc, SchedulerConfig(max_batch_size=4, max_prefills_per_step=4))
+    reqs = [_req(i, prompt=20, new=8) for i in range(3)]
+    for r in reqs:
+        s.add_request(r)
+    for _ in range(3):
+        _run_step(s, alloc, chunk=512)
+    assert all(r.state is RequestState.DECODING for r in reqs)
+    held = [r.cache.table.num_blocks for r in reqs]
+    need = alloc.num_free + held[2] + held[1]
+    victims = s.preempt(need)
+    assert victims == [reqs[1], reqs[2]] and list(s.waiting)[:2] == victims
+    assert alloc.num_free == need and reqs[0].state is RequestState.DECODING
+    v = reqs[2]
+    gen = list(v.generated_token_ids)
+    assert v.state is RequestState.WAITING and v.cache is None and v.preemptions == 1
+    assert v.prefill_len == 20 + len(gen) and v.prefill_offset == 0
+    assert v.prefill_ids(0, v.prefill_len) == v.prompt_token_ids + gen
+    assert v.next_prefill_chunk(512) == v.prompt_token_ids + gen
+    alloc.check_invariants()
+
+
+def test_preempt_with_reject_policy_rejects_the_victims() -> None:
+    from edgerag_amd.cache.preemption import PreemptionPolicy, Preemptor
+
+    alloc = BlockAllocator(64, 16)
+    s = Scheduler(alloc, SchedulerConfig(max_batch_size=4, max_prefills_per_step=4),
+                  preemptor=Preemptor(alloc, PreemptionPolicy.REJECT))
+    reqs = [_req(i, prompt=40, new=8) for i in range(2)]
+    for r in reqs:
+        s.add_request(r)
+    _run_step(s, alloc, chunk=512)
+    assert s.preempt(alloc.num_blocks) == []
+    assert all(r.state is RequestState.REJECTED for r in reqs) and not s.running
+    assert alloc.num_free == alloc.num_blocks
