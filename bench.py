@@ -180,7 +180,29 @@ def cfg3_lens():
 # --- config 4: quant linears ---------------------------------------------------------------------
 
 
-# --- access-pattern ceilings (include/edgerag_probe.h) --------------------------------------------
+# --- access-pattern ceilings (edgerag_amd/csrc/probe/edgerag_probe.h) ----------------------------
+
+_PROBE = None
+
+
+def _probe_call(name: str, *args) -> None:
+    """Call an entry point of the bench-only probe library (built beside the product one)."""
+    global _PROBE
+    import ctypes
+
+    from edgerag_amd._build import PROBE_LIB_PATH
+
+    if _PROBE is None:
+        lib = ctypes.CDLL(str(PROBE_LIB_PATH))
+        vp, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+        lib.edgerag_probe_read.argtypes = [vp, i64, i32, i32, vp, vp]
+        lib.edgerag_probe_gather.argtypes = [vp, vp, i32, i32, i32, vp, vp]
+        lib.edgerag_last_error.restype = ctypes.c_char_p
+        _PROBE = lib
+    rc = getattr(_PROBE, name)(*args)
+    if rc != 0:
+        raise RuntimeError(f"{name} failed ({rc}): {_PROBE.edgerag_last_error().decode()}")
+
 
 
 def _stream() -> int:
@@ -197,7 +219,7 @@ def probe_read_us(buffers, nbytes, n_launch=256, shapes=((512, 2), (1024, 2), (2
     best = None
     for wgs, unroll in shapes:
         def launch(buf):
-            _lib.call("edgerag_probe_read", buf.data_ptr(), nbytes, wgs, unroll, sink.data_ptr(),
+            _probe_call("edgerag_probe_read", buf.data_ptr(), nbytes, wgs, unroll, sink.data_ptr(),
                       _stream())
 
         launch(buffers[0])
@@ -244,7 +266,7 @@ def measure_ceilings(device, gather_bytes):
     sink = torch.zeros(1, dtype=torch.int32, device=device)
 
     def launch():
-        _lib.call("edgerag_probe_gather", pool.data_ptr(), ids.data_ptr(), n_chunks // per_wave,
+        _probe_call("edgerag_probe_gather", pool.data_ptr(), ids.data_ptr(), n_chunks // per_wave,
                   per_wave, 2048, sink.data_ptr(), _stream())
 
     launch()

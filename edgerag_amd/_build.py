@@ -27,6 +27,9 @@ CSRC = PACKAGE_DIR / "csrc"
 BUILD_DIR = PACKAGE_DIR / "_build"
 LIB_NAME = "libedgerag_amd.so"
 LIB_PATH = PACKAGE_DIR / LIB_NAME
+# Bench-only measurement probes (access-pattern ceilings), kept out of the product library.
+PROBE_SOURCES = [CSRC / "probe" / "probe.hip", CSRC / "capi.cpp"]
+PROBE_LIB_PATH = PACKAGE_DIR / "libedgerag_probe.so"
 
 ARCH = "gfx950"
 COMMON_FLAGS = [
@@ -58,7 +61,8 @@ def sources() -> list[Path]:
 
 
 def _compile(src: Path, verbose: bool, build_dir: Path, defines: list[str]) -> Path:
-    obj = build_dir / (src.stem + ".o")
+    obj = build_dir / (src.parent.name + "_" + src.stem + ".o" if src.parent != CSRC
+                       else src.stem + ".o")
     lang = ["-x", "hip"] if src.suffix == ".hip" else []
     cmd = [hipcc(), *COMMON_FLAGS, *[f"-D{d}" for d in defines], *lang, "-c", str(src), "-o",
            str(obj)]
@@ -88,9 +92,20 @@ def build(
     build_dir = Path(build_dir) if build_dir is not None else BUILD_DIR
     build_dir.mkdir(parents=True, exist_ok=True)
     srcs = sources()
-    jobs = jobs or min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
+    with_probe = out == LIB_PATH
+    extra = [PROBE_SOURCES[0]] if with_probe else []
+    jobs = jobs or min(len(srcs) + len(extra), max(1, min(8, os.cpu_count() or 1)))
     with ThreadPoolExecutor(max_workers=jobs) as pool:
-        objs = list(pool.map(lambda s: _compile(s, verbose, build_dir, defines or []), srcs))
+        objs = list(pool.map(lambda s: _compile(s, verbose, build_dir, defines or []),
+                             srcs + extra))
+    _link(objs[: len(srcs)], out, verbose)
+    if with_probe:  # probe kernels + the error/version entry points, in their own library
+        capi = objs[srcs.index(CSRC / "capi.cpp")]
+        _link([objs[-1], capi], PROBE_LIB_PATH, verbose)
+    return out
+
+
+def _link(objs: list[Path], out: Path, verbose: bool) -> None:
     tmp = out.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     if verbose:
@@ -99,7 +114,6 @@ def build(
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stdout}\n{proc.stderr}")
     os.replace(tmp, out)
-    return out
 
 
 if __name__ == "__main__":

@@ -127,9 +127,6 @@ SIGNATURES: dict[str, tuple[list, object]] = {
         c_i32,
     ),
     "edgerag_quant_linear_residual_parts": ([c_i32, c_i32, c_i32, c_i32, c_i32, c_i32], c_i32),
-    # include/edgerag_probe.h: measurement probes for the rooflines bench.py reports.
-    "edgerag_probe_read": ([c_vp, c_i64, c_i32, c_i32, c_vp, c_vp], c_i32),
-    "edgerag_probe_gather": ([c_vp, c_vp, c_i32, c_i32, c_i32, c_vp, c_vp], c_i32),
 }
 
 

@@ -1,20 +1,14 @@
-"""Decoder-layer ops around the hot path, on packed token-major tensors ``(T, ...)``.
+"""Parameters and tables of a decoder layer's elementwise ops, on packed token-major tensors.
 
-The arithmetic follows the reference layer by layer (``edgerag/core/layers.py``):
-
-* :class:`RMSNorm` -- fp32 variance, ``x * rsqrt(var + eps)`` in fp32, cast back to the input
-  dtype *before* the weight multiply (``layers.py:40-47``);
-* :class:`RotaryTable` -- ``inv_freq = 1 / theta^(2i/d)`` in fp32, ``freqs = pos * inv_freq``,
-  ``emb = cat(freqs, freqs)``, cos/sin in fp32 cast to the activation dtype (``layers.py:64-90``);
-  positions are *logical* (P-03). The products ``pos * inv_freq`` are single fp32 multiplies, so a
-  table indexed by position holds exactly the values the reference recomputes per step;
-* :func:`apply_rope` -- the halves convention ``x * cos + rotate_half(x) * sin`` with
-  ``rotate_half(x) = [-x2, x1]`` (``layers.py:93-114``);
-* :func:`silu_mul` -- ``silu(gate) * up`` of SwiGLU (``layers.py:341``).
-
-The decoder's forward runs the fused HIP kernels (``edgerag_rmsnorm`` with the residual add,
-``edgerag_rope_append``, ``edgerag_silu_mul``); the modules here hold the parameters and tables
-those kernels read, and their ``forward`` methods state the same arithmetic in PyTorch.
+* :class:`RMSNorm` holds the norm weight; its ``forward`` runs ``edgerag_rmsnorm`` (fp32 variance,
+  ``x * rsqrt(var + eps)`` in fp32, cast to the input dtype *before* the weight multiply, as
+  ``edgerag/core/layers.py:40-47``).
+* :class:`RotaryTable` holds cos/sin for every logical position: ``inv_freq = 1 / theta^(2i/d)``
+  in fp32, ``freqs = pos * inv_freq``, ``emb = cat(freqs, freqs)``, cos/sin in fp32 cast to the
+  activation dtype (``layers.py:64-90``). The products ``pos * inv_freq`` are single fp32
+  multiplies, so a table indexed by position holds exactly the values the reference recomputes per
+  step. The decoder's RoPE (halves convention, ``layers.py:93-114``) runs in the HIP kernels that
+  read these tables.
 """
 
 from __future__ import annotations
@@ -31,11 +25,11 @@ class RMSNorm(nn.Module):
         self.eps = eps
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        input_dtype = x.dtype
-        xf = x.to(torch.float32)
-        variance = xf.pow(2).mean(-1, keepdim=True)
-        xf = xf * torch.rsqrt(variance + self.eps)
-        return self.weight * xf.to(input_dtype)
+        """RMSNorm over the last axis, on the device (``edgerag_rmsnorm``)."""
+        from edgerag_amd import kernels
+
+        flat = x.reshape(-1, x.shape[-1])
+        return kernels.rmsnorm(flat.contiguous(), self.weight, self.eps).view(x.shape)
 
 
 class RotaryTable(nn.Module):
@@ -55,18 +49,3 @@ class RotaryTable(nn.Module):
 
     def forward(self, positions: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         return self.cos[positions], self.sin[positions]
-
-
-def rotate_half(x: torch.Tensor) -> torch.Tensor:
-    half = x.shape[-1] // 2
-    return torch.cat((-x[..., half:], x[..., :half]), dim=-1)
-
-
-def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
-    """``x (T, H, d)``, ``cos``/``sin`` ``(T, d)`` broadcast over heads."""
-    return x * cos[:, None, :] + rotate_half(x) * sin[:, None, :]
-
-
-def silu_mul(gate_up: torch.Tensor, intermediate: int) -> torch.Tensor:
-    """``silu(gate) * up`` for the fused ``[gate | up]`` projection output ``(T, 2 I)``."""
-    return nn.functional.silu(gate_up[:, :intermediate]) * gate_up[:, intermediate:]

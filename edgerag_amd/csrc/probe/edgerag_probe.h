@@ -1,7 +1,7 @@
 /*
- * Measurement probes of libedgerag_amd.so (not part of the decoder step): HBM ceilings of the
- * access patterns the kernels use, for the rooflines bench.py reports. No counterpart in the
- * reference. Both launch on `stream`, allocate nothing, and return 0 or EDGERAG_EINVAL.
+ * Measurement probes of libedgerag_probe.so, a bench-only library (not part of the decoder
+ * step): HBM ceilings of the access patterns the kernels use, for the rooflines bench.py
+ * reports. No counterpart in the reference. Both launch on `stream`, allocate nothing, and return 0 or EDGERAG_EINVAL.
  */
 #ifndef EDGERAG_PROBE_H
 #define EDGERAG_PROBE_H

@@ -9,7 +9,8 @@
 //   read with 1 KiB wave-wide loads) sits at a random chunk-aligned offset -- the access pattern
 //   of the paged KV pool (one 2 KiB (head, block) row of K or V per 16 tokens).
 // Neither kernel writes anything but a sentinel that no real data produces.
-#include "common.h"
+#include "../common.h"
+#include "edgerag_probe.h"
 
 namespace edgerag {
 namespace {

@@ -38,6 +38,20 @@ def test_library_exports_every_declared_symbol() -> None:
     assert _lib.version().startswith("edgerag_amd")
 
 
+def test_measurement_probes_live_in_a_bench_only_library() -> None:
+    """The product library exports no probe; the probe library exports its header's symbols."""
+    from edgerag_amd._build import PROBE_LIB_PATH
+
+    lib = _lib.load()
+    assert not hasattr(lib, "edgerag_probe_read") and not hasattr(lib, "edgerag_probe_gather")
+    header = Path(__file__).resolve().parents[1] / "edgerag_amd/csrc/probe/edgerag_probe.h"
+    probe_names = set(re.findall(r"^int\s+(edgerag_probe_\w+)\s*\(", header.read_text(),
+                                 flags=re.M))
+    assert probe_names == {"edgerag_probe_read", "edgerag_probe_gather"}
+    probe = ctypes.CDLL(str(PROBE_LIB_PATH))
+    assert all(hasattr(probe, n) for n in probe_names)
+
+
 def test_swiglu_support_query() -> None:
     """The fused SwiGLU linear covers decode batches of wide INT8 per-channel [gate; up]
     weights (normed inputs up to 16 tokens); the query answers without touching a GPU."""
