@@ -16,9 +16,12 @@ events on the stream the kernels are launched on (torch's current stream). The s
 (block tables, slot mapping, attention plan) is built and uploaded before the timed region, like
 every other input; its host cost is reported separately as ``plan_us``.
 
-``cpu_baseline`` times this repository's CPU restatement of the reference path (oracle: gather +
-SDPA in fp32, ``edgerag/cache/paged.py:208-238`` + ``edgerag/core/layers.py:137-167``) on a
-bounded sample of the same workload, with all host cores.
+``cpu_baseline`` (on the line, and inside ``cfg3``, ``cfg4`` and ``cfg5``) times this repository's
+CPU restatement of the reference path (the oracle, fp32, the host's cores): the full config-2 and
+config-3 steps (gather + SDPA, ``edgerag/cache/paged.py:208-238`` +
+``edgerag/core/layers.py:137-167``), every config-4 shape and M (dequantise + ``F.linear``,
+``edgerag/core/linear.py:186-196``), and a truncated config-5 decode (one request through the
+24-layer decoder oracle), each labelled with what it ran.
 """
 
 from __future__ import annotations
@@ -73,14 +76,25 @@ def make_batch(lens, q_lens, num_blocks, seed, device):
     nk = torch.randn(T, H, D, generator=gd, device=device, dtype=torch.float16)
     nv = torch.randn(T, H, D, generator=gd, device=device, dtype=torch.float16)
     qsl = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
-    t0 = time.perf_counter()
-    plan, (slot_dev,) = kernels.plan_attention(
-        qsl, np.asarray(lens, np.int32), bt, H, H, D, BS, torch.float16, device, [slots]
-    )
-    plan_us = (time.perf_counter() - t0) * 1e6
+    ctx = np.asarray(lens, np.int32)
+    plan, (slot_dev,) = kernels.plan_attention(qsl, ctx, bt, H, H, D, BS, torch.float16, device,
+                                               [slots])
+    # The step's host cost, warm (median of repeated calls): the whole plan_attention (planner,
+    # packing, the pinned upload enqueued) and the native planner alone.
+    full, planner = [], []
+    for _ in range(30):
+        t0 = time.perf_counter()
+        kernels.plan_attention(qsl, ctx, bt, H, H, D, BS, torch.float16, device, [slots])
+        t1 = time.perf_counter()
+        kernels.make_plan_host(qsl, ctx, H, H, D, BS, bt.shape[1], torch.float16)
+        t2 = time.perf_counter()
+        full.append(t1 - t0)
+        planner.append(t2 - t1)
+    torch.cuda.synchronize()
     out = torch.empty_like(q)
     return dict(kp=kp, vp=vp, q=q, nk=nk, nv=nv, plan=plan, slots=slot_dev, out=out, bt=bt,
-                qsl=qsl, lens=lens, q_lens=q_lens, plan_us=plan_us)
+                qsl=qsl, lens=lens, q_lens=q_lens, plan_us=float(np.median(full)) * 1e6,
+                planner_us=float(np.median(planner)) * 1e6)
 
 
 def step_bytes(lens, q_lens, bt):
@@ -312,6 +326,26 @@ def vendor_gemm_us(x, packed, scales, k, bits, g, n_w=8, n_launch=64):
     return us
 
 
+CFG4_SHAPES = [(2048, 2048, 8, 2048), (2048, 8192, 8, 2048), (8192, 2048, 8, 8192),
+               (1152, 1152, 4, 128), (1152, 4608, 4, 128)]
+CFG4_MS = (1, 8, 32, 64, 512, 544)
+
+
+def run_cfg4(device, args):
+    res = {"rows": bench_quant(device)}
+    if not args.no_cpu:
+        rows = cpu_quant_rows(CFG4_SHAPES, CFG4_MS)
+        res["cpu_baseline"] = {
+            "unit": "us per call", "cores": cpu_threads(), "kind": "port", "rows": rows,
+            "sample": "every config-4 shape and M: dequantise + F.linear with fp32 activations "
+            "(oracle quant_linear_reference), median of >= 20 runs each",
+        }
+        gpu = {(r["k"], r["n"], r["m"]): r["us"] for r in res["rows"]}
+        for r in rows:
+            r["gpu_speedup"] = round(r["us"] / gpu[(r["k"], r["n"], r["m"])], 1)
+    return res
+
+
 def bench_quant(device, iters=None):
     """Config 4. Each timing replays a HIP graph of back-to-back launches, one per weight replica
     (>= 1 GiB of distinct packed weights in rotation, so the weights stream from HBM rather than
@@ -322,10 +356,8 @@ def bench_quant(device, iters=None):
     us for the HBM-bound rows). For the MFMA-bound rows, ``vendor_fp16_us`` is torch's fp16
     GEMM (hipBLASLt) on the dequantised weights of the same shape, timed the same way:
     what the vendor library needs for the matrix product alone, with no dequantisation."""
-    shapes = [(2048, 2048, 8, 2048), (2048, 8192, 8, 2048), (8192, 2048, 8, 8192),
-              (1152, 1152, 4, 128), (1152, 4608, 4, 128)]
     results = []
-    for k, n, bits, g in shapes:
+    for k, n, bits, g in CFG4_SHAPES:
         width = k // 2 if bits == 4 else k
         wbytes = n * width + n * (k // g) * 2
         reps = max(2, math.ceil((1 << 30) / wbytes))
@@ -334,7 +366,7 @@ def bench_quant(device, iters=None):
                                dtype=torch.uint8)
         scales = (torch.rand((reps, n, k // g), generator=gen, device=device) * 1e-3 + 1e-4).half()
         read_us = probe_read_us([packed[r] for r in range(reps)], n * width, min(reps, 512))
-        for m in (1, 8, 32, 64, 512, 544):
+        for m in CFG4_MS:
             x = torch.randn(m, k, generator=gen, device=device, dtype=torch.float16)
             y = torch.empty(m, n, device=device, dtype=torch.float16)
             n_launch = iters or min(reps, 512)
@@ -376,53 +408,119 @@ def bench_quant(device, iters=None):
     return results
 
 
-# --- CPU baseline ----------------------------------------------------------------------------------
+# --- CPU baselines ---------------------------------------------------------------------------------
+#
+# This repository's CPU restatement of the reference path (the oracle, PyTorch on the host's cores,
+# fp32 as the reference's own CPU tests run): gather + SDPA for attention
+# (edgerag/cache/paged.py:208-238, edgerag/core/layers.py:137-167), dequantise + F.linear for the
+# quant linears (edgerag/core/linear.py:186-196), the decoder forward one request at a time for
+# config 5 (edgerag/core/model.py:72-152, edgerag/serve/executor.py:113-156). Timing follows the
+# reference's rules (bench/metrics.py:1-12): warmup discarded, median of >= 20 runs.
 
 
-def cpu_baseline(lens, budget_s=15.0):
-    """The oracle's gather + SDPA (fp32) on a sample of the config-2 batch, all host cores."""
+def cpu_threads() -> int:
+    cores = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit() and int(env) > 0:
+        cores = min(cores, int(env))
+    torch.set_num_threads(cores)
+    return cores
+
+
+def _median_runs(fn, min_runs=20, budget_s=3.0):
+    fn()  # warmup, discarded
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < min_runs or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 200:
+            break
+    return float(np.median(times)), len(times)
+
+
+def cpu_attention_step(lens, q_lens, seed):
+    """One ragged step on the CPU oracle: slot writes of the new K/V, then per request gather +
+    causal SDPA (fp32). Returns (median s, runs, algorithmic bytes as on the GPU)."""
     from oracle import attention as oa
     from oracle import paged as op
 
-    cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
-    sample = lens[:8]
-    nbs = [math.ceil(L / BS) for L in sample]
-    nb_total = sum(nbs)
-    g = torch.Generator().manual_seed(7)
-    kp = torch.randn(H, nb_total, BS, D, generator=g)
-    vp = torch.randn(H, nb_total, BS, D, generator=g)
+    nbs = [math.ceil(L / BS) for L in lens]
+    g = torch.Generator().manual_seed(seed)
+    kp = torch.randn(H, sum(nbs), BS, D, generator=g)
+    vp = torch.randn(H, sum(nbs), BS, D, generator=g)
     tables, at = [], 0
     for nb in nbs:
         tables.append(list(range(at, at + nb)))
         at += nb
-    q = torch.randn(len(sample), H, D, generator=g)
-    qsl = list(range(len(sample) + 1))
+    qsl = [0]
+    for c in q_lens:
+        qsl.append(qsl[-1] + c)
+    q = torch.randn(qsl[-1], H, D, generator=g)
+    new = torch.randn(qsl[-1], H, D, generator=g)
 
     def once():
-        # one decode step per request: write the new token, gather, attend
-        for r, (L, t) in enumerate(zip(sample, tables)):
-            op.write_slots(kp, q[r][None, :, None], t, L - 1)
-            op.write_slots(vp, q[r][None, :, None], t, L - 1)
-        oa.ragged_reference(q, kp, vp, qsl, sample, tables, D**-0.5)
+        for r, (L, c, t) in enumerate(zip(lens, q_lens, tables)):
+            src = new[qsl[r] : qsl[r + 1]].transpose(0, 1)[None]  # (1, H, c, D)
+            op.write_slots(kp, src, t, L - c)
+            op.write_slots(vp, src, t, L - c)
+        oa.ragged_reference(q, kp, vp, qsl, lens, tables, D**-0.5)
 
-    once()
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 5:
-        t0 = time.perf_counter()
-        once()
-        times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
-    nbytes = sum(sample) * KV_BYTES_PER_TOKEN  # same algorithmic unit as the GPU (fp16 KV bytes)
+    med, runs = _median_runs(once)
+    kv, ap, qo, tb = step_bytes(lens, q_lens, np.zeros((len(lens), max(nbs)), np.int32))
+    return med, runs, kv + ap + qo + tb
+
+
+def cpu_quant_rows(shapes, ms):
+    """Dequantise + F.linear (fp32 activations, the oracle's quant_linear_reference) per cfg4
+    shape and M; microseconds per call."""
+    from oracle import quant as oq
+
+    rows = []
+    for k, n, bits, grp in shapes:
+        cfg = oq.QuantConfig(grp, bits)
+        g = torch.Generator().manual_seed(k + n)
+        packed, scales = oq.quantize_for_layer(torch.randn(n, k, generator=g) * 0.02, cfg)
+        for m in ms:
+            x = torch.randn(m, k, generator=g)
+            med, runs = _median_runs(
+                lambda: oq.quant_linear_reference(x, packed, scales, None, k, cfg), budget_s=0.3)
+            rows.append(dict(k=k, n=n, bits=bits, group=grp, m=m, us=round(med * 1e6, 1),
+                             runs=runs))
+    return rows
+
+
+def cpu_decoder_tok_s(model, prompt_len=512, new_tokens=16, seed=5):
+    """Config 5, truncated: one request of ``prompt_len`` random ids, greedy ``new_tokens``
+    through the 24-layer decoder oracle (the same quantised weights, dequantised to fp32), one
+    request per forward as the reference executor runs it. Output tokens / wall time."""
+    from oracle import model as om
+
+    t0 = time.perf_counter()
+    oracle = om.OracleDecoder(model, torch.float32)
+    build_s = time.perf_counter() - t0
+    g = torch.Generator().manual_seed(seed)
+    prompt = torch.randint(1, model.spec.vocab_size - 1, (prompt_len,), generator=g).tolist()
+    t0 = time.perf_counter()
+    oracle.reset()
+    logits = oracle.forward(prompt)[-1]
+    t_first = time.perf_counter() - t0
+    out = [int(logits.argmax())]
+    t1 = time.perf_counter()
+    while len(out) < new_tokens:
+        out.append(int(oracle.forward([out[-1]])[-1].argmax()))
+    t_dec = time.perf_counter() - t1
+    total = time.perf_counter() - t0
+    del oracle
     return {
-        "value": round(nbytes / med / 1e9, 3),
-        "unit": "GB/s",
-        "cores": cores,
-        "kind": "port",
-        "sample": f"8 of the 32 config-2 requests (contexts {sample}), one decode step each: "
-        f"slot write + gather + SDPA in fp32 (oracle), median of {len(times)} runs, "
-        f"{med * 1e3:.1f} ms per step",
+        "value": round(new_tokens / total, 3),
+        "unit": "output tok/s",
+        "decode_tok_s": round((new_tokens - 1) / t_dec, 3),
+        "prefill_s": round(t_first, 2),
+        "sample": f"truncated: 1 request, {prompt_len}-token prompt (one chunk), {new_tokens} "
+        "greedy tokens, 24-layer oracle decoder in fp32 (weights dequantised from the GPU "
+        f"model's INT8 codes; {build_s:.1f} s to build, not timed); one run",
     }
 
 
@@ -442,16 +540,25 @@ def run_cfg3(device, args):
         "attn_us": round(a3 * 1e3, 1),
         "prefill_gflop": 46.18,
         "attn_items": b3["plan"].n_items,
+        "plan_us": round(b3["plan_us"], 1),
     }
     del b3
     torch.cuda.empty_cache()
+    if not args.no_cpu:
+        med, runs, nbytes = cpu_attention_step(lens3, q3, 8)
+        res["cpu_baseline"] = {
+            "value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": cpu_threads(),
+            "kind": "port", "ms_per_step": round(med * 1e3, 2),
+            "sample": f"the full config-3 step (27 requests, 1560 tokens): slot writes + "
+            f"gather + causal SDPA per request in fp32 (oracle), median of {runs} runs",
+        }
     return res
 
 
 # --- config 5: end-to-end serving ---------------------------------------------------------------
 
 
-def run_cfg5(device, n_requests: int = 64):
+def run_cfg5(device, n_requests: int = 64, cpu: bool = True):
     """Config 5: the 24-layer SmolLM2-1.7B-shaped decoder (INT8 per-channel linears, fp16
     embeddings / norms / lm_head, random init) serving a seeded Poisson trace (12 req/min,
     lognormal prompts median 3000 clamped to [256, 7472], 64-256 greedy tokens) through the
@@ -482,7 +589,7 @@ def run_cfg5(device, n_requests: int = 64):
     offered = replay(Scheduler(alloc, SchedulerConfig()), executor, reqs, arrivals, "virtual")
     reqs = synthetic_requests(n_requests, spec.vocab_size, seed=5)
     saturated = replay(Scheduler(alloc, SchedulerConfig()), executor, reqs, None, "saturated")
-    return {
+    res = {
         "workload": f"{n_requests} requests, Poisson 12 req/min, prompts lognormal(3000, 0.6) "
         "in [256, 7472], 64-256 greedy tokens; 24-layer SmolLM2-1.7B shape, INT8 per-channel",
         "metric": "decoder output tok/s",
@@ -492,6 +599,11 @@ def run_cfg5(device, n_requests: int = 64):
         "kv_pool_bytes": executor.pool_bytes,
         "init_s": round(init_s, 2),
     }
+    if cpu:
+        del executor
+        torch.cuda.empty_cache()
+        res["cpu_baseline"] = dict(cpu_decoder_tok_s(model), cores=cpu_threads(), kind="port")
+    return res
 
 
 # --- main ------------------------------------------------------------------------------------------
@@ -519,10 +631,11 @@ def main() -> None:
         print(json.dumps({"cfg3": run_cfg3(device, args)}), flush=True)
         return
     if args.only == "cfg4":
-        print(json.dumps({"cfg4": bench_quant(device)}), flush=True)
+        print(json.dumps({"cfg4": run_cfg4(device, args)}), flush=True)
         return
     if args.only == "cfg5":
-        print(json.dumps({"cfg5": run_cfg5(device, args.cfg5_requests)}), flush=True)
+        print(json.dumps({"cfg5": run_cfg5(device, args.cfg5_requests, not args.no_cpu)}),
+              flush=True)
         return
 
     lens = cfg2_lens()
@@ -554,6 +667,9 @@ def main() -> None:
             "step_bytes": int(total),
             "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
             "plan_us": round(b["plan_us"], 1),
+            "planner_us": round(b["planner_us"], 1),
+            "plan_us_note": "host time per step, warm median of 30: plan_attention (native "
+            "planner + one pinned upload enqueued); planner_us is the planner alone",
             "attn_items": b["plan"].n_items,
         },
         "roofline": {
@@ -580,11 +696,17 @@ def main() -> None:
     torch.cuda.empty_cache()
     if not args.no_extra:
         line["cfg3"] = run_cfg3(device, args)
-        line["cfg4"] = bench_quant(device)
+        line["cfg4"] = run_cfg4(device, args)
         if not args.no_cfg5:
-            line["cfg5"] = run_cfg5(device, args.cfg5_requests)
+            line["cfg5"] = run_cfg5(device, args.cfg5_requests, not args.no_cpu)
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(lens)
+        med, runs, nbytes = cpu_attention_step(lens, [1] * 32, 7)
+        line["cpu_baseline"] = {
+            "value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": cpu_threads(),
+            "kind": "port", "ms_per_step": round(med * 1e3, 2),
+            "sample": f"the full config-2 step (all 32 requests, contexts {list(lens)}): slot "
+            f"write + gather + SDPA per request in fp32 (oracle), median of {runs} runs",
+        }
     print(json.dumps(line), flush=True)
 
 
