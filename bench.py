@@ -408,6 +408,60 @@ def bench_quant(device, iters=None):
     return results
 
 
+def bench_lm_head(device, vocab=49152, k=2048, ms=(1, 8, 16), reps=3):
+    """The output head of a decode step (config 5's lm_head: fp16 49152 x 2048, 201 MB): the
+    fused GEMV + greedy argmax (edgerag_lm_head_argmax) against torch's fp16 F.linear (hipBLASLt)
+    followed by edgerag_argmax_rows, both replayed from HIP graphs over ``reps`` weight replicas
+    (more bytes than the Infinity Cache holds); ``read_us`` is the streaming-read probe over the
+    same replicas."""
+    gen = torch.Generator(device=device).manual_seed(11)
+    ws = [(torch.randn(vocab, k, generator=gen, device=device) * 0.02).half() for _ in range(reps)]
+    wbytes = vocab * k * 2
+    read_us = probe_read_us(ws, wbytes, 4 * reps, shapes=((1024, 2), (2048, 1), (4096, 1)))
+    rows = []
+    for m in ms:
+        x = torch.randn(m, k, generator=gen, device=device).half()
+        logits = torch.empty(m, vocab, dtype=torch.float16, device=device)
+        tokens = torch.empty(m, dtype=torch.int32, device=device)
+
+        def fused(i):
+            kernels.lm_head_argmax(x, ws[i % reps], logits, tokens)
+
+        def vendor(i):
+            torch.mm(x, ws[i % reps].t(), out=logits)  # what F.linear(x, W) runs
+            kernels.argmax_rows(logits, out=tokens)
+
+        res = {}
+        for name, fn in (("fused", fused), ("vendor", vendor)):
+            for i in range(reps):
+                fn(i)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            n_launch = 24
+            with torch.cuda.graph(graph):
+                for i in range(n_launch):
+                    fn(i)
+            graph.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(5):
+                graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            res[name] = e0.elapsed_time(e1) * 1e3 / (5 * n_launch)
+            del graph
+        nbytes = wbytes + 2 * m * k + 2 * m * vocab
+        rows.append(dict(m=m, us=round(res["fused"], 2), vendor_us=round(res["vendor"], 2),
+                         gbs=round(nbytes / res["fused"] / 1e3, 1),
+                         frac=round(nbytes / res["fused"] / 1e3 / HBM_PEAK_GBS, 4),
+                         read_us=round(read_us, 2), read_frac=round(read_us / res["fused"], 4)))
+    del ws
+    torch.cuda.empty_cache()
+    return {"workload": f"lm_head fp16 {vocab} x {k} (201 MB) + greedy argmax, M rows",
+            "rows": rows}
+
+
 # --- CPU baselines ---------------------------------------------------------------------------------
 #
 # This repository's CPU restatement of the reference path (the oracle, PyTorch on the host's cores,
@@ -618,7 +672,7 @@ def main() -> None:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-cfg5", action="store_true", help="skip the end-to-end serving run")
     ap.add_argument("--cfg5-requests", type=int, default=64)
-    ap.add_argument("--only", choices=["cfg3", "cfg4", "cfg5"], default=None,
+    ap.add_argument("--only", choices=["cfg3", "cfg4", "cfg5", "lm_head"], default=None,
                     help="run just one secondary config (for profiling); prints its record")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -632,6 +686,9 @@ def main() -> None:
         return
     if args.only == "cfg4":
         print(json.dumps({"cfg4": run_cfg4(device, args)}), flush=True)
+        return
+    if args.only == "lm_head":
+        print(json.dumps({"lm_head": bench_lm_head(device)}), flush=True)
         return
     if args.only == "cfg5":
         print(json.dumps({"cfg5": run_cfg5(device, args.cfg5_requests, not args.no_cpu)}),
@@ -697,6 +754,7 @@ def main() -> None:
     if not args.no_extra:
         line["cfg3"] = run_cfg3(device, args)
         line["cfg4"] = run_cfg4(device, args)
+        line["lm_head"] = bench_lm_head(device)
         if not args.no_cfg5:
             line["cfg5"] = run_cfg5(device, args.cfg5_requests, not args.no_cpu)
     if not args.no_cpu:

@@ -92,6 +92,10 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     ),
     "edgerag_silu_mul": ([c_vp, c_i64, c_i32, c_i32, c_vp, c_i64, c_i32, c_vp], c_i32),
     "edgerag_argmax_rows": ([c_vp, c_i32, c_i32, c_i32, c_i64, c_vp, c_vp], c_i32),
+    "edgerag_lm_head_argmax": (
+        [c_vp, c_i64, c_i32, c_i32, c_vp, c_i32, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp], c_i32,
+    ),
+    "edgerag_lm_head_workspace_bytes": ([c_i32, c_i32], c_i64),
     "edgerag_quantize": ([c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp, c_vp], c_i32),
     "edgerag_dequantize": ([c_vp, c_vp, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp], c_i32),
     "edgerag_quant_linear": (

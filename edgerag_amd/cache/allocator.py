@@ -94,7 +94,7 @@ class BlockAllocator:
         return self.num_used / self.num_blocks
 
     def refcount(self, block: int) -> int:
-        self._check_range(_ids([block]))
+        self._check_id(block)
         return int(self._owners[block])
 
     def is_shared(self, block: int) -> bool:
@@ -169,7 +169,7 @@ class BlockAllocator:
     def copy_on_write(self, block: int) -> int:
         """A block the caller may write: ``block`` itself if it has one owner, else a fresh block
         that takes over the caller's ownership (the caller copies the contents)."""
-        self._check_range(_ids([block]))
+        self._check_id(block)
         owners = int(self._owners[block])
         if owners == 0:
             raise AllocatorError(f"block {block} is free: there is nothing to write into")
@@ -181,6 +181,14 @@ class BlockAllocator:
         return fresh
 
     # --- checks -----------------------------------------------------------------------------------
+
+    def _check_id(self, block: int) -> None:
+        if not 0 <= block < self.num_blocks:
+            raise AllocatorError(f"block {block} is not in this pool of {self.num_blocks}")
+
+    def shared_count(self, blocks: np.ndarray) -> int:
+        """How many of ``blocks`` (valid ids) have more than one owner."""
+        return int(np.count_nonzero(self._owners[blocks] > 1)) if len(blocks) else 0
 
     def _check_range(self, ids: np.ndarray) -> None:
         bad = ids[(ids < 0) | (ids >= self.num_blocks)]

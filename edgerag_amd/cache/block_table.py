@@ -155,6 +155,8 @@ class BlockTable:
                 f"positions [{start}, {start + n}) fall outside capacity {self.capacity}"
             )
         bs = self.block_size
+        if n == 1:  # the decode step: plain integer arithmetic
+            return np.array([int(self._ids[start // bs]) * bs + start % bs], dtype=np.int32)
         pos = np.arange(start, start + n, dtype=np.int64)
         return (self._ids[pos // bs].astype(np.int64) * bs + pos % bs).astype(np.int32)
 

@@ -100,8 +100,7 @@ class PagedKVCache:
         table, bs = self.table, self.allocator.block_size
         fresh = max(0, self.allocator.blocks_needed(self.seq_len + n_new) - table.num_blocks)
         first, last = self.seq_len // bs, min(table.num_blocks, -(-(self.seq_len + n_new) // bs))
-        shared = sum(self.allocator.refcount(int(b)) > 1 for b in table.blocks[first:last])
-        return fresh + int(shared)
+        return fresh + self.allocator.shared_count(table.blocks[first:last])
 
     def reserve(self, n_new: int) -> np.ndarray:
         """Grow the table by ``n_new`` tokens, copy-on-write any shared block in the write range
@@ -167,10 +166,12 @@ class PagedKVCache:
         if not self.table.num_blocks or n_new <= 0:
             return
         bs = self.allocator.block_size
+        first, last = start // bs, min(self.table.num_blocks, (start + n_new - 1) // bs + 1)
+        if not self.allocator.shared_count(self.table.blocks[first:last]):
+            return  # the usual case: nothing in the write range is shared
         pairs = []
         try:
-            for logical in range(start // bs, min(self.table.num_blocks,
-                                                   (start + n_new - 1) // bs + 1)):
+            for logical in range(first, last):
                 copied = self.table.make_private(logical)
                 if copied is not None:
                     pairs.append(copied)

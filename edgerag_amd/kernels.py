@@ -30,6 +30,7 @@ __all__ = [
     "silu_mul",
     "dequantize",
     "kv_append",
+    "lm_head_argmax",
     "kv_copy_blocks",
     "kv_gather",
     "paged_attention",
@@ -898,6 +899,41 @@ def argmax_rows(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tenso
     call("edgerag_argmax_rows", x.data_ptr(), dtype_code(x.dtype), rows, cols, x.stride(0),
          out.data_ptr(), stream_ptr(x.device))
     return out
+
+
+LM_HEAD_MAX_ROWS = 16
+_LM_WORKSPACES: dict[tuple[torch.device, int], torch.Tensor] = {}
+
+
+def lm_head_argmax(x: torch.Tensor, weight: torch.Tensor, logits: torch.Tensor | None = None,
+                   tokens: torch.Tensor | None = None) -> tuple[torch.Tensor | None, torch.Tensor]:
+    """``logits = x @ weight.T`` (fp16, written into ``logits`` when given) and each row's
+    greedy token (int32, ``tokens``), for up to 16 rows, in two launches; the weight streams from
+    HBM once. The candidate workspace is allocated once per (device, vocabulary) and reused, so a
+    graph that captured the call keeps a valid address."""
+    require_device(x, weight, logits, tokens)
+    m, k = x.shape
+    vocab = weight.shape[0]
+    if not 1 <= m <= LM_HEAD_MAX_ROWS:
+        raise ValueError(f"lm_head_argmax takes 1..{LM_HEAD_MAX_ROWS} rows, got {m}")
+    if x.dtype != torch.float16 or weight.dtype != torch.float16 or weight.shape[1] != k:
+        raise ValueError("lm_head_argmax takes fp16 x (m, k) and weight (vocab, k)")
+    if x.stride(1) != 1 or not weight.is_contiguous():
+        raise ValueError("x rows and the weight must be contiguous")
+    if tokens is None:
+        tokens = torch.empty(m, dtype=torch.int32, device=x.device)
+    if logits is not None and (logits.shape != (m, vocab) or logits.dtype != torch.float16
+                               or logits.stride(1) != 1):
+        raise ValueError(f"logits must be fp16 ({m}, {vocab}) with contiguous rows")
+    key = (x.device, vocab)
+    ws = _LM_WORKSPACES.get(key)
+    if ws is None:
+        nbytes = int(_lib.load().edgerag_lm_head_workspace_bytes(LM_HEAD_MAX_ROWS, vocab))
+        ws = _LM_WORKSPACES[key] = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+    call("edgerag_lm_head_argmax", x.data_ptr(), x.stride(0), m, k, weight.data_ptr(), vocab,
+         ptr(logits), 0 if logits is None else logits.stride(0), tokens.data_ptr(),
+         ws.data_ptr(), ws.numel(), stream_ptr(x.device))
+    return logits, tokens
 
 
 def dequantize(packed: torch.Tensor, scales: torch.Tensor, in_features: int, bits: int,

@@ -254,9 +254,9 @@ class ModelExecutor:
                               self._prompt_rows(entries, qsl, ids_d))
             tokens = []
             if emitting:
-                logits = self.decoder.logits(step, self.key_pool, self.value_pool)
+                logits, choice = self.decoder.greedy(step, self.key_pool, self.value_pool)
                 self.last_logits = logits
-                tokens = kernels.argmax_rows(logits).cpu().tolist()
+                tokens = choice.cpu().tolist()
             else:
                 self.decoder.forward_hidden(step, self.key_pool, self.value_pool)
         for request, token in zip(emitting, tokens):
@@ -297,10 +297,9 @@ class ModelExecutor:
                 # The staged metadata is already valid, so run once eagerly first (lets torch and
                 # hipBLASLt settle their workspaces outside the capture); it computes this step's
                 # logits, which the replay below recomputes identically.
-                self.decoder.logits(step, self.key_pool, self.value_pool)
+                self.decoder.greedy(step, self.key_pool, self.value_pool)
                 with torch.cuda.graph(graph, stream=stream):
-                    logits = self.decoder.logits(step, self.key_pool, self.value_pool)
-                    choice = kernels.argmax_rows(logits)
+                    logits, choice = self.decoder.greedy(step, self.key_pool, self.value_pool)
             torch.cuda.current_stream(self.device).wait_stream(stream)
             entry = self._graphs[n] = (graph, logits, choice)
         graph, logits, choice = entry

@@ -450,6 +450,28 @@ int edgerag_silu_mul(const void* gate_up, int64_t gate_up_stride, int32_t n_toke
 int edgerag_argmax_rows(const void* x, int32_t dtype, int32_t rows, int32_t cols,
                         int64_t row_stride, int32_t* out, void* stream);
 
+/*
+ * The output head of a decode step and its greedy choice in two launches: for the 1 <= m <= 16
+ * emitting rows x [m, k] (fp16, row stride x_stride elements, rows 16-byte aligned) and the fp16
+ * lm_head weight [vocab, k] (contiguous, 16-byte aligned; k a multiple of 32):
+ *   logits[t][j] = fp16(sum_k x[t][k] * weight[j][k])   (fp32 accumulation; skipped if logits
+ *                                                         is NULL; row stride logits_stride)
+ *   tokens[t]    = the first j of the maximum of logits[t][:] (a NaN counts as the maximum), the
+ *                  choice torch.argmax makes on the fp16 logits.
+ * The weight streams from HBM once. workspace (8-byte aligned, any contents) holds one candidate
+ * per (row, 64-row slice of the vocabulary): edgerag_lm_head_workspace_bytes(m, vocab) bytes;
+ * launches sharing it must be ordered. m > 16 returns EDGERAG_EUNSUPPORTED.
+ *
+ * Replaces `F.linear(hidden, lm_head)` on the last position (edgerag/core/model.py:150-152) and
+ * the greedy `int(logits[0, -1].argmax())` of ModelExecutor.execute
+ * (edgerag/serve/executor.py:136, :154) for every emitting request of a step.
+ */
+int edgerag_lm_head_argmax(const void* x, int64_t x_stride, int32_t m, int32_t k,
+                           const void* weight, int32_t vocab, void* logits,
+                           int64_t logits_stride, int32_t* tokens, void* workspace,
+                           int64_t workspace_bytes, void* stream);
+int64_t edgerag_lm_head_workspace_bytes(int32_t m, int32_t vocab);
+
 #ifdef __cplusplus
 }
 #endif
