@@ -5,7 +5,7 @@
 // (edgerag/core/model.py:150-152) and the executor's argmax (edgerag/serve/executor.py:136, :154).
 //
 // lm_head_kernel streams W once at HBM rate (201 MB for SmolLM2's 49152 x 2048):
-// * a workgroup owns 64 consecutive vocabulary rows, its four waves 16 rows each over all of K;
+// * a workgroup owns 16 consecutive vocabulary rows per wave, each wave over all of K;
 // * the M <= 16 activation rows are staged in LDS once per workgroup (row stride 2K + 16 bytes,
 //   so the 16-byte reads of 8 tokens hit distinct banks), not re-read from L2 per wave;
 // * per 32-k step a lane loads 16 bytes of its weight row (4 lanes cover 64 contiguous bytes) and
@@ -23,13 +23,13 @@ namespace {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kLmWaves = 4;
-constexpr int kLmRows = 16 * kLmWaves;  // vocabulary rows per workgroup
 constexpr int kLmMaxM = 16;
-#ifndef EDGERAG_LM_HEAD_U
-#define EDGERAG_LM_HEAD_U 8
-#endif
-constexpr int kLmU = EDGERAG_LM_HEAD_U;  // 32-k steps of weight loads in flight per lane
+// Launch shapes (waves per workgroup, 32-k steps of weight loads in flight per lane), measured on
+// the 49152 x 2048 head: up to 8 rows, 4-wave workgroups (3 per CU) 16 steps deep; 9..16 rows
+// stage twice the activations in LDS, and 12-wave workgroups (one per CU) 8 deep do better.
+constexpr int kLmSmallWaves = 4, kLmSmallU = 16;
+constexpr int kLmLargeWaves = 12, kLmLargeU = 8;
+constexpr int kLmSmallM = 8;
 
 __device__ __forceinline__ uint4 ldg16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 
@@ -49,16 +49,16 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int mask) {
   return (uint64_t(hi) << 32) | lo;
 }
 
-template <int U>
-__global__ __launch_bounds__(kLmWaves * kWave) void lm_head_kernel(
+template <int WAVES, int U>
+__global__ __launch_bounds__(WAVES * kWave) void lm_head_kernel(
     const f16* __restrict__ x, int64_t xs, int32_t m, int32_t k, const f16* __restrict__ w,
     int32_t v, f16* __restrict__ logits, int64_t ls, uint64_t* __restrict__ part) {
   extern __shared__ uint4 xt[];  // m rows of k fp16 each, row stride k / 8 + 1 uint4
-  __shared__ uint64_t best[kLmWaves][kLmMaxM];
+  __shared__ uint64_t best[WAVES][kLmMaxM];
   const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63;
   const int li = lane & 15, lg = lane >> 4;
-  const int row0 = int(blockIdx.x) * kLmRows + wave * 16;
+  const int row0 = int(blockIdx.x) * (16 * WAVES) + wave * 16;
   const int row = min(row0 + li, v - 1);  // rows past V re-read the last one (never written)
   const int steps = k / 32;
   const int xrow = (k >> 3) + 1;  // uint4 per staged activation row
@@ -69,7 +69,7 @@ __global__ __launch_bounds__(kLmWaves * kWave) void lm_head_kernel(
   uint4 wb[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) wb[u] = ldg16(wp + 4 * min(u, steps - 1));
-  for (int i = threadIdx.x; i < m * (k >> 3); i += kLmWaves * kWave) {
+  for (int i = threadIdx.x; i < m * (k >> 3); i += WAVES * kWave) {
     const int t = i / (k >> 3), c = i % (k >> 3);
     xt[t * xrow + c] = ldg16(x + int64_t(t) * xs + 8 * c);
   }
@@ -121,7 +121,7 @@ __global__ __launch_bounds__(kLmWaves * kWave) void lm_head_kernel(
   if (threadIdx.x < unsigned(m)) {
     uint64_t b = best[0][threadIdx.x];
 #pragma unroll
-    for (int wv = 1; wv < kLmWaves; ++wv) b = key_max(b, best[wv][threadIdx.x]);
+    for (int wv = 1; wv < WAVES; ++wv) b = key_max(b, best[wv][threadIdx.x]);
     part[int64_t(threadIdx.x) * gridDim.x + blockIdx.x] = b;
   }
 }
@@ -144,7 +144,9 @@ __global__ __launch_bounds__(256) void lm_head_pick_kernel(const uint64_t* __res
   }
 }
 
-int lm_head_workgroups(int32_t vocab) { return (vocab + kLmRows - 1) / kLmRows; }
+int lm_head_workgroups(int32_t vocab, int waves) {
+  return (vocab + 16 * waves - 1) / (16 * waves);
+}
 
 }  // namespace
 }  // namespace edgerag
@@ -153,7 +155,8 @@ using namespace edgerag;
 
 extern "C" int64_t edgerag_lm_head_workspace_bytes(int32_t m, int32_t vocab) {
   if (m < 1 || m > kLmMaxM || vocab < 1) return 0;
-  return int64_t(m) * lm_head_workgroups(vocab) * int64_t(sizeof(uint64_t));
+  // Sized for the launch shape with the most workgroups.
+  return int64_t(m) * lm_head_workgroups(vocab, kLmSmallWaves) * int64_t(sizeof(uint64_t));
 }
 
 extern "C" int edgerag_lm_head_argmax(const void* x, int64_t x_stride, int32_t m, int32_t k,
@@ -182,12 +185,21 @@ extern "C" int edgerag_lm_head_argmax(const void* x, int64_t x_stride, int32_t m
   if (lds > 128 * 1024)  // of the CU's 160 KiB
     return fail(EDGERAG_EUNSUPPORTED, "edgerag_lm_head_argmax: %d rows of %d exceed the staging "
                                       "space", m, k);
-  const int wgs = lm_head_workgroups(vocab);
+  const bool small = m <= kLmSmallM;
+  const int wgs = lm_head_workgroups(vocab, small ? kLmSmallWaves : kLmLargeWaves);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL((lm_head_kernel<kLmU>), dim3(wgs), dim3(kLmWaves * kWave), lds, s,
-                     static_cast<const f16*>(x), x_stride, m, k, static_cast<const f16*>(weight),
-                     vocab, static_cast<f16*>(logits), logits_stride,
-                     static_cast<uint64_t*>(workspace));
+  const f16* xh = static_cast<const f16*>(x);
+  const f16* wh = static_cast<const f16*>(weight);
+  f16* lh = static_cast<f16*>(logits);
+  uint64_t* part = static_cast<uint64_t*>(workspace);
+  if (small)
+    hipLaunchKernelGGL((lm_head_kernel<kLmSmallWaves, kLmSmallU>), dim3(wgs),
+                       dim3(kLmSmallWaves * kWave), lds, s, xh, x_stride, m, k, wh, vocab, lh,
+                       logits_stride, part);
+  else
+    hipLaunchKernelGGL((lm_head_kernel<kLmLargeWaves, kLmLargeU>), dim3(wgs),
+                       dim3(kLmLargeWaves * kWave), lds, s, xh, x_stride, m, k, wh, vocab, lh,
+                       logits_stride, part);
   hipLaunchKernelGGL(lm_head_pick_kernel, dim3(m), dim3(256), 0, s,
                      static_cast<const uint64_t*>(workspace), wgs, tokens);
   return check_launch("edgerag_lm_head_argmax");
