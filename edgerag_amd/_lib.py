@@ -34,6 +34,7 @@ EDGERAG_EUNSUPPORTED = 4
 
 ATTN_TILES, ATTN_ROWS, ATTN_COMBINE, ATTN_ALL = 1, 2, 4, 7
 ATTN_TILES_SHARED = 8  # modifier of ATTN_TILES: one tile workgroup per CU, beside decode rows
+PLAN_SPLIT_ROWS = 1  # edgerag_attn_plan_ex flag: decode rows as KV splits merged by a launch
 QUANT_WORKSPACE_MAX = 8 * 1024 * 1024  # bound of edgerag_quant_linear_workspace_bytes
 ATTN_SCRATCH_BYTES = 32 * 1024 * 1024  # static partials of edgerag_paged_attention_noalloc
 
@@ -57,6 +58,11 @@ SIGNATURES: dict[str, tuple[list, object]] = {
         [c_vp, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_i64, c_i64p, c_i64p],
         c_i32,
     ),
+    "edgerag_attn_plan_ex": (
+        [c_vp, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_i64, c_i64p,
+         c_i64p],
+        c_i32,
+    ),
     "edgerag_paged_attention": (
         [c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_vp, c_vp, c_i32, c_vp, c_i64, c_vp, c_vp, c_i32,
          c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_f32, c_vp, c_i64, c_i64, c_vp, c_i64, c_i32,
@@ -75,7 +81,8 @@ SIGNATURES: dict[str, tuple[list, object]] = {
         c_i32,
     ),
     "edgerag_paged_attention_fixed": (
-        [c_vp, c_i32, c_i32, c_i32, c_i64, c_vp, c_i64, c_i64, c_vp, c_vp, c_i32, c_vp, c_i64,
+        [c_vp, c_i32, c_i32, c_i32, c_i64, c_i32, c_vp, c_i64, c_i64, c_vp, c_vp, c_i32, c_vp,
+         c_i64,
          c_vp, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_f32, c_vp, c_i64, c_i64, c_vp, c_i64,
          c_vp],
         c_i32,

@@ -49,6 +49,12 @@ constexpr int32_t kPlanVersion = plan::kVersion;
 #ifndef EDGERAG_DECODE_U
 #define EDGERAG_DECODE_U 2
 #endif
+#ifndef EDGERAG_ROW_WG
+#define EDGERAG_ROW_WG 1  // decode rows as one workgroup per (request, kv head), merged in LDS
+#endif
+#ifndef EDGERAG_ROW_WG_PART
+#define EDGERAG_ROW_WG_PART 256  // longest part (tokens) a wave of a workgroup-split row takes
+#endif
 constexpr int kMaxRowVecs = 8;  // query vectors a decode item may carry (c * n_rep)
 constexpr int kQTile = 16;      // query rows per prefill tile item
 constexpr int kMinSplit = EDGERAG_MIN_SPLIT;  // tokens; shorter splits are not worth a partial
@@ -142,8 +148,11 @@ struct QReg {
 // APPEND: the step's own tokens (positions L - c .. L - 1 of each request) are read from the new
 // K/V rows instead of the pools, and the split that reads them also writes them to the pools at
 // their slots (kv_append fused in: no other wave reads those pool rows in this launch).
-template <typename T, int D, int QR, int U, bool APPEND>
-__global__ __launch_bounds__(kWave) void attn_decode_kernel(
+// WG: one workgroup per row item (blockDim / 64 waves); wave w takes the w-th of equal,
+// block-aligned parts of the item's keys, and the waves' (m, l, acc) merge in LDS before wave 0
+// writes the output (no partials, no merge launch). Otherwise one wave per item (a KV split).
+template <typename T, int D, int QR, int U, bool APPEND, bool WG>
+__global__ __launch_bounds__(WG ? kMaxRowWaves * kWave : kWave) void attn_decode_kernel(
     const T* __restrict__ q, int64_t q_st, int64_t q_sh, const T* __restrict__ kpool,
     const T* __restrict__ vpool, const int32_t* __restrict__ block_tables, int64_t bt_stride,
     const int32_t* __restrict__ qsl, const int32_t* __restrict__ ctx,
@@ -162,13 +171,25 @@ __global__ __launch_bounds__(kWave) void attn_decode_kernel(
   if (item_base + int(blockIdx.x) >= plan[limit_word]) return;
   const int32_t* it = plan + plan[H_ITEM_OFF] + int64_t(item_base + blockIdx.x) * kItemWords;
   const int r = it[I_REQ], h = it[I_HEAD], qb = it[I_QBEGIN], qc = it[I_QCOUNT];
-  const int kb = it[I_KVBEGIN], ke = it[I_KVEND], split = it[I_SPLIT];
+  const int split = it[I_SPLIT];
+  int kb = it[I_KVBEGIN], ke = it[I_KVEND];
+  const int wave = WG ? int(threadIdx.x >> 6) : 0;
+  if constexpr (WG) {
+    // This wave's part of the keys: equal parts of whole blocks (a part never straddles the
+    // wave's block-id registers), empty for waves past the end.
+    const int nw = int(blockDim.x >> 6);
+    const int per = (ke - kb + nw - 1) / nw;
+    const int part = (per + block_size - 1) / block_size * block_size;
+    const int b0 = min(ke, kb + wave * part);
+    ke = min(ke, b0 + part);
+    kb = b0;
+  }
   const int32_t* rq = plan + plan[H_REQ_OFF] + r * kReqWords;
   const int nsplit = rq[R_NSPLIT], part_off = rq[R_PARTOFF];
   const int q0 = qsl[r], c = qsl[r + 1] - q0, L = ctx[r];
   const int n_rep = n_q_heads / n_kv_heads;
 
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & (kWave - 1);
   const int sub = lane & (LPT - 1);
   const int tslot = lane >> LOG_LPT;
   const int64_t head_base = int64_t(h) * num_blocks;
@@ -266,6 +287,68 @@ __global__ __launch_bounds__(kWave) void attn_decode_kernel(
     }
 
     // Merge the TPW lane groups of each query vector, then write.
+    if constexpr (WG) {
+      // The waves' partials (log2-domain max, sum, acc) meet in LDS; wave 0 merges and writes.
+      __shared__ float wg_ml[kMaxRowWaves][QR][2];
+      __shared__ float wg_acc[kMaxRowWaves][QR][D];
+#pragma unroll
+      for (int j = 0; j < QR; ++j) {
+        float mm = m[j];
+#pragma unroll
+        for (int b = LOG_LPT; b < 6; ++b) mm = fmaxf(mm, __shfl_xor(mm, 1 << b, kWave));
+        const float w = m[j] == -INFINITY ? 0.f : exp2_fast(m[j] - mm);
+        float lsum = w * l[j];
+#pragma unroll
+        for (int b = LOG_LPT; b < 6; ++b) lsum += __shfl_xor(lsum, 1 << b, kWave);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          float a = w * acc[j][e];
+#pragma unroll
+          for (int b = LOG_LPT; b < 6; ++b) a += __shfl_xor(a, 1 << b, kWave);
+          if (tslot == 0) wg_acc[wave][j][sub * VEC + e] = a;
+        }
+        if (lane == 0) {
+          wg_ml[wave][j][0] = mm;
+          wg_ml[wave][j][1] = lsum;
+        }
+      }
+      __syncthreads();
+      if (wave == 0) {
+        const int nw = int(blockDim.x >> 6);
+#pragma unroll
+        for (int j = 0; j < QR; ++j) {
+          const int v = v0 + j;
+          if (v >= nvec) break;
+          float mx = -INFINITY;
+          for (int wv = 0; wv < nw; ++wv) mx = fmaxf(mx, wg_ml[wv][j][0]);
+          float lsum = 0.f;
+          float a[(D + kWave - 1) / kWave];
+#pragma unroll
+          for (int e = 0; e < (D + kWave - 1) / kWave; ++e) a[e] = 0.f;
+          for (int wv = 0; wv < nw; ++wv) {
+            const float mw = wg_ml[wv][j][0];
+            const float wgt = mw == -INFINITY ? 0.f : exp2_fast(mw - mx);
+            lsum = fmaf(wgt, wg_ml[wv][j][1], lsum);
+#pragma unroll
+            for (int e = 0; e < (D + kWave - 1) / kWave; ++e) {
+              const int d = lane + e * kWave;
+              if (d < D) a[e] = fmaf(wgt, wg_acc[wv][j][d], a[e]);
+            }
+          }
+          const float inv = 1.f / fmaxf(lsum, 1.17549435e-38f);
+          const int t = qb + v / n_rep;
+          const int hq = h * n_rep + (v % n_rep);
+          T* op = out + int64_t(t) * o_st + int64_t(hq) * o_sh;
+#pragma unroll
+          for (int e = 0; e < (D + kWave - 1) / kWave; ++e) {
+            const int d = lane + e * kWave;
+            if (d < D) op[d] = from_f32<T>(a[e] * inv);
+          }
+        }
+      }
+      __syncthreads();  // the LDS is rewritten by the next pass over query vectors
+      continue;
+    }
 #pragma unroll
     for (int j = 0; j < QR; ++j) {
       const int v = v0 + j;
@@ -580,10 +663,13 @@ WorkspaceLayout workspace_layout(int64_t n_partials, int64_t head_dim) {
 
 using Launch = AttnLaunch;
 
-template <typename T, int D, int QR, int U>
-void launch_decode(const Launch& a, int base, int count, int limit_word) {
+// waves > 0: workgroup-split rows (one workgroup of `waves` waves per item), else one wave per
+// item.
+template <typename T, int D, int QR, int U, bool WG>
+void launch_decode_mode(const Launch& a, int base, int count, int limit_word, int waves) {
+  const dim3 grid(count), block(WG ? waves * kWave : kWave);
   if (a.nk != nullptr)
-    hipLaunchKernelGGL((attn_decode_kernel<T, D, QR, U, true>), dim3(count), dim3(kWave), 0, a.s,
+    hipLaunchKernelGGL((attn_decode_kernel<T, D, QR, U, true, WG>), grid, block, 0, a.s,
                        static_cast<const T*>(a.q), a.q_st, a.q_sh, static_cast<const T*>(a.kp),
                        static_cast<const T*>(a.vp), a.bt, a.bt_stride, a.qsl, a.ctx, a.plan, base,
                        limit_word, a.hq, a.hkv, a.nb, a.bs, a.scale_log2,
@@ -592,12 +678,23 @@ void launch_decode(const Launch& a, int base, int count, int limit_word) {
                        a.slots, static_cast<T*>(const_cast<void*>(a.kp)),
                        static_cast<T*>(const_cast<void*>(a.vp)));
   else
-    hipLaunchKernelGGL((attn_decode_kernel<T, D, QR, U, false>), dim3(count), dim3(kWave), 0,
-                       a.s, static_cast<const T*>(a.q), a.q_st, a.q_sh,
+    hipLaunchKernelGGL((attn_decode_kernel<T, D, QR, U, false, WG>), grid, block, 0, a.s,
+                       static_cast<const T*>(a.q), a.q_st, a.q_sh,
                        static_cast<const T*>(a.kp), static_cast<const T*>(a.vp), a.bt,
                        a.bt_stride, a.qsl, a.ctx, a.plan, base, limit_word, a.hq, a.hkv, a.nb,
                        a.bs, a.scale_log2, static_cast<T*>(a.out), a.o_st, a.o_sh, a.ml, a.pacc,
                        nullptr, nullptr, 0, 0, nullptr, nullptr, nullptr);
+}
+
+template <typename T, int D, int QR, int U>
+void launch_decode(const Launch& a, int base, int count, int limit_word, int waves) {
+  if constexpr (D <= 128) {
+    if (waves > 0) {
+      launch_decode_mode<T, D, QR, U, true>(a, base, count, limit_word, waves);
+      return;
+    }
+  }
+  launch_decode_mode<T, D, QR, U, false>(a, base, count, limit_word, 0);
 }
 
 template <typename T, int D, int QR>
@@ -610,13 +707,14 @@ void launch_rows(const Launch& a, int base, int count, int limit_word) {
 }
 
 template <typename T, int D>
-void dispatch_decode_qr(const Launch& a, int qr, int base, int count, int limit_word) {
+void dispatch_decode_qr(const Launch& a, int qr, int base, int count, int limit_word,
+                        int waves) {
   constexpr int U = D >= 256 ? 2 : kDecodeU;
   switch (qr) {
-    case 1: launch_decode<T, D, 1, U>(a, base, count, limit_word); break;
-    case 2: launch_decode<T, D, 2, U>(a, base, count, limit_word); break;
-    case 4: launch_decode<T, D, 4, U>(a, base, count, limit_word); break;
-    default: launch_decode<T, D, 8, 2>(a, base, count, limit_word); break;
+    case 1: launch_decode<T, D, 1, U>(a, base, count, limit_word, waves); break;
+    case 2: launch_decode<T, D, 2, U>(a, base, count, limit_word, waves); break;
+    case 4: launch_decode<T, D, 4, U>(a, base, count, limit_word, waves); break;
+    default: launch_decode<T, D, 8, 2>(a, base, count, limit_word, waves); break;
   }
 }
 
@@ -653,8 +751,8 @@ int run_items(const Launch& a, const int32_t* ph, int parts) {
   const bool fast = a.bs % C::TPW == 0 && ph[H_MAX_SPLIT_BLOCKS] <= kMaxSplitBlocks;
   if ((parts & EDGERAG_ATTN_ROWS) && n_row > 0) {
     if (fast)
-      dispatch_decode_qr<T, D>(a, qr, 0, n_row, H_N_ROW_ITEMS);
-    else
+      dispatch_decode_qr<T, D>(a, qr, 0, n_row, H_N_ROW_ITEMS, ph[H_ROW_WAVES]);
+    else  // (workgroup-split rows are only planned for the fast kernel)
       dispatch_rows_qr<T, D>(a, qr, 0, n_row, H_N_ROW_ITEMS);
   }
   return check_launch("edgerag_paged_attention");
@@ -678,12 +776,15 @@ int run_dtype(const Launch& a, const int32_t* ph, int32_t D, int parts) {
 
 using namespace edgerag;
 
-extern "C" int edgerag_attn_plan(const int32_t* query_start_loc, const int32_t* context_lens,
-                                 int32_t num_reqs, int32_t n_q_heads, int32_t n_kv_heads,
-                                 int32_t head_dim, int32_t block_size, int32_t max_blocks_per_seq,
-                                 int32_t dtype, int32_t* plan, int64_t plan_capacity_words,
-                                 int64_t* plan_words, int64_t* workspace_bytes) {
+extern "C" int edgerag_attn_plan_ex(const int32_t* query_start_loc, const int32_t* context_lens,
+                                    int32_t num_reqs, int32_t n_q_heads, int32_t n_kv_heads,
+                                    int32_t head_dim, int32_t block_size,
+                                    int32_t max_blocks_per_seq, int32_t dtype, int32_t flags,
+                                    int32_t* plan, int64_t plan_capacity_words,
+                                    int64_t* plan_words, int64_t* workspace_bytes) {
   clear_error();
+  if ((flags & ~EDGERAG_PLAN_SPLIT_ROWS) != 0)
+    return fail(EDGERAG_EINVAL, "edgerag_attn_plan: flags %d", flags);
   if (plan_words == nullptr || workspace_bytes == nullptr)
     return fail(EDGERAG_EINVAL, "edgerag_attn_plan: plan_words/workspace_bytes are NULL");
   if (num_reqs < 0) return fail(EDGERAG_EINVAL, "edgerag_attn_plan: num_reqs < 0");
@@ -729,6 +830,32 @@ extern "C" int edgerag_attn_plan(const int32_t* query_start_loc, const int32_t* 
     }
     max_len = std::max(max_len, L);
   }
+  // Decode rows as one workgroup of kMaxRowWaves waves per (request, kv head) whose waves split
+  // the keys and merge in LDS, when the fast decode kernel takes them and every row's context
+  // fits kMaxRowWaves parts of at most EDGERAG_ROW_WG_PART tokens. Longer contexts would leave
+  // each wave a long, latency-bound stream while the chip idles (measured: cfg2 -2%, cfg5 with 8
+  // long requests -5%), so those batches (or any, when asked) keep one workgroup per KV split,
+  // merged by the combine launch through fp32 partials.
+  int64_t row_items = 0, max_row_len = 0;
+  for (int r = 0; r < num_reqs; ++r) {
+    const int64_t c = int64_t(query_start_loc[r + 1]) - query_start_loc[r];
+    if (c > 0 && c * n_rep <= kMaxRowVecs) {
+      row_items += n_kv_heads;
+      max_row_len = std::max<int64_t>(max_row_len, context_lens[r]);
+    }
+  }
+  const int es = elem_size(dtype);
+  const bool wg_rows =
+      EDGERAG_ROW_WG && !(flags & EDGERAG_PLAN_SPLIT_ROWS) && row_items > 0 && head_dim <= 128 &&
+      head_dim % (16 / es) == 0 && head_dim / (16 / es) <= kWave &&
+      block_size % (kWave / (head_dim / (16 / es))) == 0 &&
+      max_row_len <= int64_t(kMaxRowWaves) * EDGERAG_ROW_WG_PART &&
+      max_row_len <= int64_t(kMaxRowWaves) * kMaxSplitBlocks * block_size;
+  const int row_waves = wg_rows ? kMaxRowWaves : 0;
+  const int wg_split_blocks =
+      wg_rows ? int(((max_row_len + kMaxRowWaves - 1) / kMaxRowWaves + block_size - 1) /
+                    block_size)
+              : 0;
   int64_t split_len = std::max<int64_t>(kMinSplit, (work + kTargetItems - 1) / kTargetItems);
   split_len = round_up(split_len, block_size);
   split_len = std::min<int64_t>(split_len, int64_t(kMaxSplitBlocks) * block_size);
@@ -761,7 +888,8 @@ extern "C" int edgerag_attn_plan(const int32_t* query_start_loc, const int32_t* 
     const int L = context_lens[r];
     int32_t* rq = reqs.data() + size_t(r) * kReqWords;
     const bool row = c * n_rep <= kMaxRowVecs;
-    const int64_t slen = row ? split_len : tile_split_len;
+    // Workgroup-split rows are one item over the whole context (the waves split it).
+    const int64_t slen = row ? (wg_rows ? std::max<int64_t>(L, 1) : split_len) : tile_split_len;
     const int nsplit = c == 0 ? 0 : int((L + slen - 1) / slen);
     rq[R_NSPLIT] = nsplit;
     rq[R_SPLITLEN] = int32_t(slen);
@@ -828,10 +956,11 @@ extern "C" int edgerag_attn_plan(const int32_t* query_start_loc, const int32_t* 
   plan[H_NUM_TOKENS_HINT] = num_reqs > 0 ? query_start_loc[num_reqs] : 0;
   plan[H_N_ROW_ITEMS] = int32_t(n_row_items);
   plan[H_MAX_ROW_VECS] = max_row_vecs;
-  plan[H_MAX_SPLIT_BLOCKS] = split_blocks;
+  plan[H_MAX_SPLIT_BLOCKS] = wg_rows ? wg_split_blocks : split_blocks;
   plan[H_N_COMBINE] = int32_t(combine.size() / kCombineWords);
   plan[H_COMBINE_OFF] = int32_t(combine_off);
   plan[H_TILE_KIND] = mfma_tiles ? 1 : 0;
+  plan[H_ROW_WAVES] = row_waves;
   std::copy(combine.begin(), combine.end(), plan + combine_off);
   int32_t* dst = plan + item_off;
   for (const auto* groups : {&rows, &tiles})
@@ -848,6 +977,16 @@ extern "C" int edgerag_attn_plan(const int32_t* query_start_loc, const int32_t* 
       }
   std::copy(reqs.begin(), reqs.end(), plan + req_off);
   return EDGERAG_OK;
+}
+
+extern "C" int edgerag_attn_plan(const int32_t* query_start_loc, const int32_t* context_lens,
+                                 int32_t num_reqs, int32_t n_q_heads, int32_t n_kv_heads,
+                                 int32_t head_dim, int32_t block_size, int32_t max_blocks_per_seq,
+                                 int32_t dtype, int32_t* plan, int64_t plan_capacity_words,
+                                 int64_t* plan_words, int64_t* workspace_bytes) {
+  return edgerag_attn_plan_ex(query_start_loc, context_lens, num_reqs, n_q_heads, n_kv_heads,
+                              head_dim, block_size, max_blocks_per_seq, dtype, 0, plan,
+                              plan_capacity_words, plan_words, workspace_bytes);
 }
 
 namespace edgerag {
@@ -1035,23 +1174,23 @@ namespace {
 // Decode-row items of a fixed-capacity launch: the fast decode kernel when every load group of a
 // split stays inside one block, the general row kernel otherwise (both bound-checked on device).
 template <typename T, int D>
-void run_rows_fixed(const Launch& a, int qr, int max_items) {
+void run_rows_fixed(const Launch& a, int qr, int max_items, int row_waves) {
   using C = RowCfg<T, D>;
   if (a.bs % C::TPW == 0)
-    dispatch_decode_qr<T, D>(a, qr, 0, max_items, H_N_ROW_ITEMS);
+    dispatch_decode_qr<T, D>(a, qr, 0, max_items, H_N_ROW_ITEMS, row_waves);
   else
     dispatch_rows_qr<T, D>(a, qr, 0, max_items, H_N_ROW_ITEMS);
 }
 
 template <typename T>
-int run_fixed_dtype(const Launch& a, int32_t D, int qr, int max_items) {
+int run_fixed_dtype(const Launch& a, int32_t D, int qr, int max_items, int row_waves) {
   switch (D) {
-    case 8: run_rows_fixed<T, 8>(a, qr, max_items); break;
-    case 16: run_rows_fixed<T, 16>(a, qr, max_items); break;
-    case 32: run_rows_fixed<T, 32>(a, qr, max_items); break;
-    case 64: run_rows_fixed<T, 64>(a, qr, max_items); break;
-    case 128: run_rows_fixed<T, 128>(a, qr, max_items); break;
-    case 256: run_rows_fixed<T, 256>(a, qr, max_items); break;
+    case 8: run_rows_fixed<T, 8>(a, qr, max_items, row_waves); break;
+    case 16: run_rows_fixed<T, 16>(a, qr, max_items, row_waves); break;
+    case 32: run_rows_fixed<T, 32>(a, qr, max_items, row_waves); break;
+    case 64: run_rows_fixed<T, 64>(a, qr, max_items, row_waves); break;
+    case 128: run_rows_fixed<T, 128>(a, qr, max_items, row_waves); break;
+    case 256: run_rows_fixed<T, 256>(a, qr, max_items, row_waves); break;
     default: return fail(EDGERAG_EUNSUPPORTED, "edgerag_paged_attention_fixed: head_dim %d", D);
   }
   return check_launch("edgerag_paged_attention_fixed");
@@ -1062,7 +1201,8 @@ int run_fixed_dtype(const Launch& a, int32_t D, int qr, int max_items) {
 
 extern "C" int edgerag_paged_attention_fixed(
     const int32_t* plan_dev, int32_t max_row_items, int32_t max_combine_rows,
-    int32_t max_row_vecs, int64_t max_partials, const void* q, int64_t q_stride_tok,
+    int32_t max_row_vecs, int64_t max_partials, int32_t row_waves, const void* q,
+    int64_t q_stride_tok,
     int64_t q_stride_head, const void* key_pool, const void* value_pool, int32_t dtype,
     const int32_t* block_tables, int64_t block_tables_stride, const int32_t* query_start_loc,
     const int32_t* context_lens, int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
@@ -1082,6 +1222,13 @@ extern "C" int edgerag_paged_attention_fixed(
   if (n_q_heads <= 0 || n_kv_heads <= 0 || n_q_heads % n_kv_heads != 0 ||
       !head_dim_supported(head_dim) || block_size <= 0 || num_blocks <= 0)
     return fail(EDGERAG_EINVAL, "edgerag_paged_attention_fixed: bad shape");
+  if (row_waves < 0 || row_waves > kMaxRowWaves ||
+      (row_waves > 0 && (head_dim > 128 || max_combine_rows != 0 ||
+                         block_size % (kWave / (head_dim / (16 / elem_size(dtype)))) != 0)))
+    return fail(EDGERAG_EINVAL,
+                "edgerag_paged_attention_fixed: row_waves %d (1..%d workgroup-split rows need "
+                "head_dim <= 128, the fast decode kernel's block sizes and no combine rows)",
+                row_waves, kMaxRowWaves);
   if (!(scale > 0.f) || !std::isfinite(scale))
     return fail(EDGERAG_EINVAL, "edgerag_paged_attention_fixed: scale must be positive");
   const int es = elem_size(dtype);
@@ -1122,9 +1269,12 @@ extern "C" int edgerag_paged_attention_fixed(
   int rc = EDGERAG_OK;
   if (max_row_items > 0) {
     switch (dtype) {
-      case EDGERAG_F32: rc = run_fixed_dtype<float>(a, head_dim, qr, max_row_items); break;
-      case EDGERAG_F16: rc = run_fixed_dtype<f16>(a, head_dim, qr, max_row_items); break;
-      case EDGERAG_BF16: rc = run_fixed_dtype<bf16>(a, head_dim, qr, max_row_items); break;
+      case EDGERAG_F32: rc = run_fixed_dtype<float>(a, head_dim, qr, max_row_items, row_waves);
+        break;
+      case EDGERAG_F16: rc = run_fixed_dtype<f16>(a, head_dim, qr, max_row_items, row_waves);
+        break;
+      case EDGERAG_BF16: rc = run_fixed_dtype<bf16>(a, head_dim, qr, max_row_items, row_waves);
+        break;
     }
   }
   if (rc != EDGERAG_OK || max_combine_rows == 0) return rc;

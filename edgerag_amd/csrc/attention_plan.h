@@ -8,7 +8,7 @@ namespace edgerag {
 namespace plan {
 
 constexpr int32_t kMagic = 0x47415245;  // "ERAG"
-constexpr int32_t kVersion = 4;
+constexpr int32_t kVersion = 5;
 constexpr int kHeaderWords = 24;
 constexpr int kItemWords = 8;
 constexpr int kReqWords = 4;
@@ -34,7 +34,12 @@ enum Header {
   H_N_COMBINE,         // rows (query tokens of split requests) attn_combine_kernel merges
   H_COMBINE_OFF,       // word offset of the combine list
   H_TILE_KIND,         // 0: prefill tiles run on the row kernel, 1: on the MFMA tile kernel
+  H_ROW_WAVES,         // 0: decode rows split across workgroups (partials + combine list);
+                       // W > 0: one workgroup per row item, its W waves split the keys and
+                       // merge in LDS (no partials)
 };
+// Waves a workgroup-split row item may use (the kernel's LDS merge is sized for this many).
+constexpr int kMaxRowWaves = 16;
 enum Item { I_REQ = 0, I_HEAD, I_QBEGIN, I_QCOUNT, I_KVBEGIN, I_KVEND, I_SPLIT, I_PAD };
 enum Req { R_NSPLIT = 0, R_SPLITLEN, R_PARTOFF, R_PAD };
 // Combine-list entry: everything one merge needs in a single 32-byte load.

@@ -248,11 +248,14 @@ def make_plan_host(
     block_size: int,
     max_blocks_per_seq: int,
     dtype: torch.dtype,
+    split_rows: bool = False,
 ) -> tuple[np.ndarray, int]:
     """Run the native host planner. Returns ``(plan words, workspace bytes)``.
 
     One planner call fills a buffer sized from the largest plan seen so far; only a plan larger
-    than every earlier one needs a second call (the first reports the size)."""
+    than every earlier one needs a second call (the first reports the size). ``split_rows``
+    plans decode rows as KV splits merged by a launch (``EDGERAG_PLAN_SPLIT_ROWS``) instead of
+    workgroups whose waves merge in LDS."""
     lib = _lib.load()
     qsl = np.ascontiguousarray(query_start_loc, dtype=np.int32)
     ctx = np.ascontiguousarray(context_lens, dtype=np.int32)
@@ -262,15 +265,15 @@ def make_plan_host(
     words, ws = ctypes.c_int64(0), ctypes.c_int64(0)
     args = (
         qsl.ctypes.data, ctx.ctypes.data, num_reqs, n_q_heads, n_kv_heads, head_dim, block_size,
-        max_blocks_per_seq, dtype_code(dtype),
+        max_blocks_per_seq, dtype_code(dtype), _lib.PLAN_SPLIT_ROWS if split_rows else 0,
     )
     plan = np.empty(_PLAN_WORDS_HINT[0], dtype=np.int32)
-    rc = lib.edgerag_attn_plan(*args, plan.ctypes.data, plan.size, ctypes.byref(words),
-                               ctypes.byref(ws))
+    rc = lib.edgerag_attn_plan_ex(*args, plan.ctypes.data, plan.size, ctypes.byref(words),
+                                  ctypes.byref(ws))
     if rc == _lib.EDGERAG_EWORKSPACE and words.value > plan.size:
         plan = np.empty(words.value, dtype=np.int32)
-        rc = lib.edgerag_attn_plan(*args, plan.ctypes.data, plan.size, ctypes.byref(words),
-                                   ctypes.byref(ws))
+        rc = lib.edgerag_attn_plan_ex(*args, plan.ctypes.data, plan.size, ctypes.byref(words),
+                                      ctypes.byref(ws))
     if rc != _lib.EDGERAG_OK:
         raise _lib.EdgeragError("edgerag_attn_plan", rc,
                                 lib.edgerag_last_error().decode(errors="replace"))
@@ -290,6 +293,7 @@ def plan_attention(
     device: torch.device,
     extra_int32: list[np.ndarray] | None = None,
     workspace: bool = True,
+    split_rows: bool = False,
 ) -> tuple[AttentionPlan, list[torch.Tensor]]:
     """Plan a ragged step on the host and upload all of its metadata in one copy.
 
@@ -302,7 +306,7 @@ def plan_attention(
         raise ValueError("block_tables must be (num_reqs, max_blocks)")
     plan, ws_bytes = make_plan_host(
         query_start_loc, context_lens, n_q_heads, n_kv_heads, head_dim, block_size,
-        block_tables.shape[1], dtype,
+        block_tables.shape[1], dtype, split_rows,
     )
     extra = list(extra_int32 or [])
     views = upload_int32(
@@ -498,7 +502,10 @@ class FixedAttention:
     by :meth:`update` (one pinned H2D copy): cu_seqlens, context lengths, block tables with a
     fixed row stride, caller-defined extra int32 arrays (token ids, positions, slots, ...) and the
     plan. :meth:`launch` calls ``edgerag_paged_attention_fixed``, whose grid depends only on the
-    capacities, so a graph that captured it stays valid for every plan :meth:`update` accepts.
+    capacities and on :attr:`row_waves`, the launch mode of the staged plan: 0 for KV splits
+    merged by a combine launch, > 0 for workgroup-split rows (the planner takes these when every
+    context is short). A captured graph stays valid for every plan :meth:`update` accepts in the
+    mode it was captured in, so callers key their graphs by :attr:`row_waves` as well.
     The pinned host staging buffer is reused: the caller must have synchronised with the previous
     step (the executor does, when it reads the tokens back) before calling :meth:`update` again.
     """
@@ -506,16 +513,23 @@ class FixedAttention:
     def __init__(self, device, n_q_heads: int, n_kv_heads: int, head_dim: int, block_size: int,
                  dtype: torch.dtype, max_reqs: int, max_blocks_per_seq: int,
                  extra_capacities: list[int], max_items: int = 16384,
-                 min_split: int = 256) -> None:
+                 min_split: int = 256, split_rows: bool = False) -> None:
+        """``split_rows``: always plan decode rows as KV splits merged by a launch, never as
+        workgroup-split rows."""
         self.device = torch.device(device)
+        self.split_rows = split_rows
         self.n_q_heads, self.n_kv_heads, self.head_dim = n_q_heads, n_kv_heads, head_dim
         self.block_size, self.dtype = block_size, dtype
         self.max_reqs, self.max_blocks = max_reqs, max_blocks_per_seq
         self.max_row_vecs = min(8, max(1, n_q_heads // n_kv_heads))
-        self.max_items = max_items
+        # Capacities of both launch modes: KV splits (items, merge rows, partials) and
+        # workgroup-split rows (one workgroup per request and kv head).
         self.max_combine = max_reqs
         max_splits = -(-max_blocks_per_seq * block_size // min_split)
         self.max_partials = max_reqs * n_q_heads * max_splits
+        self.max_items = max_items
+        self.wg_items = max_reqs * n_kv_heads
+        self.row_waves = 0
         self.plan_words = 24 + 8 * max_items + 4 * max_reqs + 8 * self.max_combine + 64
 
         def pad(n: int) -> int:
@@ -555,9 +569,12 @@ class FixedAttention:
         if any(int(e.size) > c for e, c in zip(extras, self._caps)):
             return False
         plan, _ = make_plan_host(query_start_loc, context_lens, self.n_q_heads, self.n_kv_heads,
-                                 self.head_dim, self.block_size, self.max_blocks, self.dtype)
+                                 self.head_dim, self.block_size, self.max_blocks, self.dtype,
+                                 self.split_rows)
         n_items, n_row, n_partials = int(plan[2]), int(plan[13]), int(plan[6])
-        if (n_items != n_row or n_row > self.max_items or int(plan[16]) > self.max_combine
+        row_waves = int(plan[19])
+        if (n_items != n_row or n_row > (self.wg_items if row_waves else self.max_items)
+                or int(plan[16]) > (0 if row_waves else self.max_combine)
                 or int(plan[14]) > self.max_row_vecs or n_partials > self.max_partials
                 or plan.size > self.plan_words):
             return False
@@ -575,6 +592,7 @@ class FixedAttention:
         used = self._plan_off + plan.size
         self.buf[:used].copy_(self.host[:used], non_blocking=True)
         self.num_reqs = R
+        self.row_waves = row_waves
         return True
 
     def launch(self, query: torch.Tensor, key_pool: torch.Tensor, value_pool: torch.Tensor,
@@ -582,9 +600,13 @@ class FixedAttention:
         n_kv, num_blocks, block_size, head_dim = key_pool.shape
         if query.stride(2) != 1 or out.stride(2) != 1:
             raise ValueError("query and out need a contiguous head_dim axis")
+        if self.row_waves:
+            items, combine, partials = self.wg_items, 0, 0
+        else:
+            items, combine, partials = self.max_items, self.max_combine, self.max_partials
         call(
-            "edgerag_paged_attention_fixed", self.plan.data_ptr(), self.max_items,
-            self.max_combine, self.max_row_vecs, self.max_partials, query.data_ptr(),
+            "edgerag_paged_attention_fixed", self.plan.data_ptr(), items, combine,
+            self.max_row_vecs, partials, self.row_waves, query.data_ptr(),
             query.stride(0), query.stride(1), key_pool.data_ptr(), value_pool.data_ptr(),
             dtype_code(key_pool.dtype), self.block_tables.data_ptr(), self.max_blocks,
             self.qsl.data_ptr(), self.ctx.data_ptr(), self.n_q_heads, n_kv, head_dim, block_size,

@@ -107,7 +107,9 @@ class ModelExecutor:
         self.decode_graphs = decode_graphs and self.device.type == "cuda"
         self.max_decode_batch = max_decode_batch
         self._fixed: kernels.FixedAttention | None = None
-        self._graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor, torch.Tensor]] = {}
+        # Decode graphs by (requests, attention launch mode of the staged plan).
+        self._graphs: dict[tuple[int, int],
+                           tuple[torch.cuda.CUDAGraph, torch.Tensor, torch.Tensor]] = {}
         self.graph_steps = 0
 
     @property
@@ -285,9 +287,10 @@ class ModelExecutor:
     def _replay_decode(self, n: int) -> tuple[torch.Tensor, torch.Tensor]:
         """Logits ``(n, vocab)`` of a staged decode-only step of ``n`` requests and their greedy
         tokens (int32 ``(n,)``), both computed inside the replayed graph."""
-        entry = self._graphs.get(n)
+        fx = self._fixed
+        key = (n, fx.row_waves)
+        entry = self._graphs.get(key)
         if entry is None:
-            fx = self._fixed
             slots, pos, ids, rows = (e[:n] for e in fx.extras)
             step = StepInputs(ids, pos, slots, rows, fx)
             stream = torch.cuda.Stream(self.device)
@@ -301,7 +304,7 @@ class ModelExecutor:
                 with torch.cuda.graph(graph, stream=stream):
                     logits, choice = self.decoder.greedy(step, self.key_pool, self.value_pool)
             torch.cuda.current_stream(self.device).wait_stream(stream)
-            entry = self._graphs[n] = (graph, logits, choice)
+            entry = self._graphs[key] = (graph, logits, choice)
         graph, logits, choice = entry
         graph.replay()
         return logits, choice

@@ -130,6 +130,21 @@ int edgerag_attn_plan(const int32_t* query_start_loc, const int32_t* context_len
                       int64_t* workspace_bytes);
 
 /*
+ * edgerag_attn_plan with planning flags. Decode rows (requests with c * n_q_heads / n_kv_heads
+ * <= 8 query vectors) are by default planned as one workgroup per (request, kv head) whose waves
+ * split the context and merge in LDS (no split partials, no merge launch), whenever the fast
+ * decode kernel takes the shape and every such context fits 16 waves of 64 blocks; otherwise,
+ * or with EDGERAG_PLAN_SPLIT_ROWS, as one workgroup per KV split merged through fp32 partials
+ * in the workspace. Results agree to fp32 rounding either way.
+ */
+#define EDGERAG_PLAN_SPLIT_ROWS 1
+int edgerag_attn_plan_ex(const int32_t* query_start_loc, const int32_t* context_lens,
+                         int32_t num_reqs, int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                         int32_t block_size, int32_t max_blocks_per_seq, int32_t dtype,
+                         int32_t flags, int32_t* plan, int64_t plan_capacity_words,
+                         int64_t* plan_words, int64_t* workspace_bytes);
+
+/*
  * Run the planned attention. plan_host is the plan edgerag_attn_plan wrote (read on the host for
  * the launch configuration) and plan_dev its device copy (read by the kernels). q:
  * [num_tokens, n_q_heads, head_dim] at q + t*q_stride_tok + h*q_stride_head; out likewise. Pools
@@ -201,13 +216,18 @@ int edgerag_paged_attention_append(
  * partials and no request with more than max_row_vecs query vectors. The workspace holds
  * max_partials partials: (m, l) pairs at offset 0, accumulators at round_up(8 * max_partials,
  * 256); size it with that formula. Semantics are those of edgerag_paged_attention.
+ * row_waves > 0 runs workgroup-split rows instead (one workgroup of row_waves waves per row item,
+ * merged in LDS; plans with a nonzero EDGERAG plan word H_ROW_WAVES, i.e. planned without
+ * EDGERAG_PLAN_SPLIT_ROWS, contexts up to row_waves * 64 blocks): then max_combine_rows must be
+ * 0 and no workspace is needed.
  *
  * No counterpart in the reference: it exists so that the decode step of the serving loop
  * (edgerag/serve/executor.py:138-154 replaced by one packed forward) can be replayed from a graph.
  */
 int edgerag_paged_attention_fixed(const int32_t* plan_dev, int32_t max_row_items,
                                   int32_t max_combine_rows, int32_t max_row_vecs,
-                                  int64_t max_partials, const void* q, int64_t q_stride_tok,
+                                  int64_t max_partials, int32_t row_waves, const void* q,
+                                  int64_t q_stride_tok,
                                   int64_t q_stride_head, const void* key_pool,
                                   const void* value_pool, int32_t dtype,
                                   const int32_t* block_tables, int64_t block_tables_stride,

@@ -156,8 +156,11 @@ def test_validation_errors_come_back_as_messages() -> None:
             _lib.call("edgerag_paged_attention", None, None, 0, None, 0, 0, None, None, 1, None,
                       0, None, None, 0, 0, 4, 4, 64, 16, 1, 1.0, None, 0, 0, None, 0, parts, None)
     with pytest.raises(_lib.EdgeragError, match="capacities"):
-        _lib.call("edgerag_paged_attention_fixed", 16, -1, 0, 1, 0, 16, 0, 0, 16, 16, 1, 16, 0,
-                  16, 16, 4, 4, 64, 16, 1, 1.0, 16, 0, 0, None, 0, None)
+        _lib.call("edgerag_paged_attention_fixed", 16, -1, 0, 1, 0, 0, 16, 0, 0, 16, 16, 1, 16,
+                  0, 16, 16, 4, 4, 64, 16, 1, 1.0, 16, 0, 0, None, 0, None)
+    with pytest.raises(_lib.EdgeragError, match="row_waves"):
+        _lib.call("edgerag_paged_attention_fixed", 16, 4, 4, 1, 0, 16, 16, 0, 0, 16, 16, 1, 16,
+                  0, 16, 16, 4, 4, 64, 16, 1, 1.0, 16, 0, 0, None, 0, None)
     with pytest.raises(_lib.EdgeragError, match="width"):
         _lib.call("edgerag_rmsnorm", None, 0, None, 0, None, None, 0, None, 0, 1, 0, 1e-5, 1,
                   None)
@@ -263,11 +266,48 @@ def test_plan_rejects_bad_batches() -> None:
 def test_plan_size_query_without_buffer() -> None:
     words, ws = ctypes.c_int64(0), ctypes.c_int64(0)
     qsl = np.array([0, 1], np.int32)
+    ctx = np.array([4000], np.int32)
+    _lib.call("edgerag_attn_plan", qsl.ctypes.data, ctx.ctypes.data, 1, 32, 32, 64, 16, 400, 1,
+              None, 0, ctypes.byref(words), ctypes.byref(ws))
+    assert words.value > 16 and ws.value == 0  # workgroup-split rows: no partials
+    _lib.call("edgerag_attn_plan_ex", qsl.ctypes.data, ctx.ctypes.data, 1, 32, 32, 64, 16, 400, 1,
+              _lib.PLAN_SPLIT_ROWS, None, 0, ctypes.byref(words), ctypes.byref(ws))
+    assert words.value > 16 and ws.value > 0  # KV splits: fp32 partials
     ctx = np.array([5000], np.int32)
     _lib.call("edgerag_attn_plan", qsl.ctypes.data, ctx.ctypes.data, 1, 32, 32, 64, 16, 400, 1,
               None, 0, ctypes.byref(words), ctypes.byref(ws))
-    assert words.value > 16 and ws.value > 0
+    assert ws.value > 0  # a long context keeps KV splits
     small = np.empty(4, np.int32)
     with pytest.raises(_lib.EdgeragError, match="capacity"):
         _lib.call("edgerag_attn_plan", qsl.ctypes.data, ctx.ctypes.data, 1, 32, 32, 64, 16, 400,
                   1, small.ctypes.data, 4, ctypes.byref(words), ctypes.byref(ws))
+
+
+@pytest.mark.parametrize(
+    "ctx,d,bs,split_rows,row_waves",
+    [
+        ([4096, 1, 300], 64, 16, False, 16),  # every decode context short: workgroup-split rows
+        ([4097, 1, 300], 64, 16, False, 0),  # one longer than 16 waves x 256 tokens: KV splits
+        ([4096, 1, 300], 64, 16, True, 0),  # asked for KV splits
+        ([2000], 256, 16, False, 0),  # head_dim past the workgroup kernel's 128
+        ([2000], 128, 8, False, 16),
+        ([2000], 64, 32, False, 16),
+    ],
+)
+def test_plan_row_mode_selection(ctx, d, bs, split_rows, row_waves) -> None:
+    """Decode rows become one workgroup per (request, kv head) only when every decode context is
+    at most 4096 tokens and the fast decode kernel takes the shape; a prefill slice beside them
+    does not change the rows' mode."""
+    n = len(ctx)
+    plan, ws = kernels.make_plan_host(np.arange(n + 1, dtype=np.int32), np.array(ctx, np.int32),
+                                      8, 8, d, bs, -(-max(ctx) // bs), torch.float16, split_rows)
+    assert int(plan[19]) == row_waves
+    items, reqs = decode_plan(plan)
+    if row_waves:
+        assert ws == 0 and int(plan[16]) == 0
+        assert items.shape[0] == n * 8 and all(int(nsplit) == 1 for nsplit in reqs[:, 0])
+    # With a prefill slice of 600 tokens at offset 3000 in the batch.
+    qsl = np.array([0, *range(1, n + 1), n + 600], np.int32)
+    plan2, _ = kernels.make_plan_host(qsl, np.array([*ctx, 3600], np.int32), 8, 8, d, bs,
+                                      -(-max(*ctx, 3600) // bs), torch.float16, split_rows)
+    assert int(plan2[19]) == row_waves

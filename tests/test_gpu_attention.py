@@ -279,10 +279,10 @@ def test_repeated_launches_with_a_shared_workspace_agree(device) -> None:
     kp, vp, tables, qsl, q, bt = _ragged_case(lens, [1] * 4, 8, 4, 64, torch.float16, 12)
     kd, vd, qd = kp.to(device), vp.to(device), q.to(device)
     plan, _ = kernels.plan_attention(qsl, np.asarray(lens, np.int32), bt, 8, 4, 64, BLOCK_SIZE,
-                                     torch.float16, device)
+                                     torch.float16, device, split_rows=True)
     assert int(plan.plan_host[6]) > 0, "the case must exercise split merging (partials)"
     other, _ = kernels.plan_attention(qsl[:3], np.asarray(lens[:2], np.int32), bt[:2], 8, 4, 64,
-                                      BLOCK_SIZE, torch.float16, device)
+                                      BLOCK_SIZE, torch.float16, device, split_rows=True)
     outs = []
     for _ in range(3):
         outs.append(kernels.paged_attention(qd, kd, vd, plan, 0.125).clone())
@@ -300,7 +300,7 @@ def test_graph_replays_match_eager_with_split_merge(device) -> None:
     kp, vp, tables, qsl, q, bt = _ragged_case(lens, [1] * 6, 8, 8, 64, torch.float16, 21)
     kd, vd, qd = kp.to(device), vp.to(device), q.to(device)
     plan, _ = kernels.plan_attention(qsl, np.asarray(lens, np.int32), bt, 8, 8, 64, BLOCK_SIZE,
-                                     torch.float16, device)
+                                     torch.float16, device, split_rows=True)
     assert int(plan.plan_host[6]) > 0 and int(plan.plan_host[16]) > 0
     eager = kernels.paged_attention(qd, kd, vd, plan, 0.125).clone()
     out = torch.empty_like(qd)
@@ -329,7 +329,7 @@ def test_plans_of_different_sizes_share_one_workspace(device) -> None:
         kp, vp, tables, qsl, q, bt = _ragged_case(lens, [1] * len(lens), 8, 8, 64, torch.float16,
                                                   seed)
         plan, _ = kernels.plan_attention(qsl, np.asarray(lens, np.int32), bt, 8, 8, 64,
-                                         BLOCK_SIZE, torch.float16, device)
+                                         BLOCK_SIZE, torch.float16, device, split_rows=True)
         assert int(plan.plan_host[6]) > 0
         expected = oa.ragged_reference(q, kp, vp, qsl.tolist(), lens, tables, 0.125)
         cases.append((kp.to(device), vp.to(device), q.to(device), plan, expected))

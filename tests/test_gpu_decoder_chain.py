@@ -58,7 +58,12 @@ def _tables(lens, bs, num_blocks, g):
 # --- fixed-capacity attention (graph replay) at long contexts -----------------------------------
 
 
-def test_fixed_attention_long_contexts_split_merge_and_graph_replays(device) -> None:
+@pytest.mark.parametrize("split_rows", [False, True])
+def test_fixed_attention_long_contexts_split_merge_and_graph_replays(device, split_rows) -> None:
+    """Both row modes of the fixed launch, switching from step to step as the planner picks
+    them: KV splits merged by the combine launch (which reads its row count from the device
+    plan header) for long contexts, workgroup-split rows (16 waves per (request, head), merged in
+    LDS) when every context is short. One graph per mode replays every plan of that mode."""
     n_q = n_kv = 32
     d, bs, cap = 64, 16, 8
     max_blocks = math.ceil(7472 / bs)
@@ -66,13 +71,16 @@ def test_fixed_attention_long_contexts_split_merge_and_graph_replays(device) -> 
     gd = torch.Generator(device=device).manual_seed(41)
     kp = torch.randn((n_kv, NB, bs, d), generator=gd, device=device, dtype=torch.float16)
     vp = torch.randn((n_kv, NB, bs, d), generator=gd, device=device, dtype=torch.float16)
-    fx = kernels.FixedAttention(device, n_q, n_kv, d, bs, torch.float16, cap, max_blocks, [])
+    fx = kernels.FixedAttention(device, n_q, n_kv, d, bs, torch.float16, cap, max_blocks, [],
+                                split_rows=split_rows)
     q_static = torch.zeros((cap, n_q, d), device=device, dtype=torch.float16)
     out = torch.zeros_like(q_static)
     plans = {
         "A": [7472, 6000, 300, 4100, 257, 5000, 7000, 1024],
         "B": [7472, 2000, 100],
         "C": [256, 3000, 7471, 90, 1800],
+        "D": [4096, 17, 1000, 2500, 1, 4000, 33, 700],  # every context short
+        "E": [300, 16, 4095],
     }
     g = seeded(41)
     cases = {}
@@ -81,22 +89,28 @@ def test_fixed_attention_long_contexts_split_merge_and_graph_replays(device) -> 
         qsl = np.arange(len(lens) + 1, dtype=np.int32)
         q = torch.randn((len(lens), n_q, d), generator=g).half()
         plan_host, _ = kernels.make_plan_host(qsl, np.asarray(lens, np.int32), n_q, n_kv, d, bs,
-                                              max_blocks, torch.float16)
+                                              max_blocks, torch.float16, split_rows)
         cases[name] = (lens, tables, bt, qsl, q, plan_host)
-    splits = {n: int(c[5][16]) for n, c in cases.items()}  # combine rows per plan
-    assert all(v > 0 for v in splits.values())
-    assert len({int(c[5][6]) for c in cases.values()}) == 3  # partial counts all differ
+    for name in "ABC":  # long contexts: KV splits, with merge rows and differing partial counts
+        assert int(cases[name][5][19]) == 0 and int(cases[name][5][16]) > 0
+    assert len({int(cases[n][5][6]) for n in "ABC"}) == 3
+    for name in "DE":
+        if split_rows:
+            assert int(cases[name][5][19]) == 0
+        else:
+            assert int(cases[name][5][19]) == 16 and int(cases[name][5][6]) == 0
 
     kp_cpu, vp_cpu = kp.cpu(), vp.cpu()
-    graph = None
-    for name in ["A", "B", "C", "A", "C", "B"]:
+    graphs = {}
+    for name in ["A", "D", "B", "C", "E", "A", "D", "C", "B", "E"]:
         lens, tables, bt, qsl, q, _ = cases[name]
         torch.cuda.synchronize()  # update() reuses its pinned staging buffer
         assert fx.update(qsl, np.asarray(lens, np.int32), bt, [])
+        assert fx.row_waves == int(cases[name][5][19])
         q_static.zero_()
         q_static[: len(lens)].copy_(q.to(device))
         out.fill_(float("nan"))
-        if graph is None:
+        if fx.row_waves not in graphs:
             side = torch.cuda.Stream(device)
             side.wait_stream(torch.cuda.current_stream(device))
             graph = torch.cuda.CUDAGraph()
@@ -105,14 +119,18 @@ def test_fixed_attention_long_contexts_split_merge_and_graph_replays(device) -> 
                 with torch.cuda.graph(graph, stream=side):
                     fx.launch(q_static, kp, vp, 0.125, out)
             torch.cuda.current_stream(device).wait_stream(side)
+            graphs[fx.row_waves] = graph
             out.fill_(float("nan"))
-        print(f"fixed attention replay, plan {name}: {len(lens)} requests", flush=True)
-        graph.replay()
+        print(f"fixed attention replay, plan {name}: {len(lens)} requests, row_waves "
+              f"{fx.row_waves}", flush=True)
+        graphs[fx.row_waves].replay()
         torch.cuda.synchronize()
         got = out[: len(lens)].clone()
-        eager = ragged_paged_attention(q.to(device), kp, vp, qsl, np.asarray(lens, np.int32), bt,
-                                       0.125)
+        eager_plan, _ = kernels.plan_attention(qsl, np.asarray(lens, np.int32), bt, n_q, n_kv, d,
+                                               bs, torch.float16, device, split_rows=split_rows)
+        eager = kernels.paged_attention(q.to(device), kp, vp, eager_plan, 0.125)
         torch.cuda.synchronize()
+        # The same kernels over the same items.
         assert torch.equal(got, eager), f"plan {name}: replay differs from the eager launch"
         expected = oa.ragged_reference(q, kp_cpu, vp_cpu, qsl.tolist(), lens, tables, 0.125)
         torch.testing.assert_close(got.float().cpu(), expected, **FP16_TOL)

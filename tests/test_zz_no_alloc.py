@@ -44,10 +44,12 @@ def _batch(lens, q_lens, n_q, n_kv, seed, device):
 
 
 def _both(kp, vp, q, qsl, lens, bt, n_q, n_kv, device):
-    """The same plan through edgerag_paged_attention (workspace) and the no-alloc entry."""
-    plan_ws, _ = kernels.plan_attention(qsl, lens, bt, n_q, n_kv, 64, BS, torch.float16, device)
+    """The same plan through edgerag_paged_attention (workspace) and the no-alloc entry. Decode
+    rows are planned as KV splits, so they too leave partials in the scratch."""
+    plan_ws, _ = kernels.plan_attention(qsl, lens, bt, n_q, n_kv, 64, BS, torch.float16, device,
+                                        split_rows=True)
     plan_na, _ = kernels.plan_attention(qsl, lens, bt, n_q, n_kv, 64, BS, torch.float16, device,
-                                        workspace=False)
+                                        workspace=False, split_rows=True)
     assert plan_na.workspace is None and plan_na.workspace_bytes == plan_ws.workspace_bytes
     assert 0 < plan_na.workspace_bytes <= _lib.ATTN_SCRATCH_BYTES
     ref = kernels.paged_attention(q, kp, vp, plan_ws, 0.125, overlap=False)
@@ -113,7 +115,8 @@ def test_noalloc_refuses_plans_beyond_the_scratch() -> None:
     n_q = n_kv = 128
     lens = np.full(128, 7472, np.int32)  # 128 decodes x 128 heads x 8 splits: 34.6 MB
     qsl = np.arange(129, dtype=np.int32)
-    plan, ws = kernels.make_plan_host(qsl, lens, n_q, n_kv, 64, BS, 467, torch.float16)
+    plan, ws = kernels.make_plan_host(qsl, lens, n_q, n_kv, 64, BS, 467, torch.float16,
+                                      split_rows=True)
     assert ws > _lib.ATTN_SCRATCH_BYTES
     lib = _lib.load()
     rc = lib.edgerag_paged_attention_noalloc(
