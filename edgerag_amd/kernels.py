@@ -535,24 +535,27 @@ class FixedAttention:
         def pad(n: int) -> int:
             return (n + 15) // 16 * 16
 
-        sizes = [pad(max_reqs + 1), pad(max_reqs), max_reqs * max_blocks_per_seq,
-                 *[pad(c) for c in extra_capacities]]
+        # Layout: cu_seqlens, context lengths, extras, the plan, then the block tables last, so
+        # that a step uploads [0, end of its plan) and only the table rows of its requests.
+        sizes = [pad(max_reqs + 1), pad(max_reqs), *[pad(c) for c in extra_capacities]]
         offs, at = [], 0
         for n in sizes:
             offs.append(at)
             at += pad(n)
         self._plan_off = at
-        total = at + self.plan_words
+        self._tables_off = pad(at + self.plan_words)
+        total = self._tables_off + max_reqs * max_blocks_per_seq
         self.buf = torch.zeros(total, dtype=torch.int32, device=self.device)
         self.host = torch.zeros(total, dtype=torch.int32, pin_memory=True)
         self._host_np = self.host.numpy()
         self.qsl = self.buf[offs[0] : offs[0] + max_reqs + 1]
         self.ctx = self.buf[offs[1] : offs[1] + max_reqs]
-        self.block_tables = self.buf[offs[2] : offs[2] + max_reqs * max_blocks_per_seq].view(
+        tables = self._tables_off
+        self.block_tables = self.buf[tables : tables + max_reqs * max_blocks_per_seq].view(
             max_reqs, max_blocks_per_seq)
-        self.extras = [self.buf[o : o + c] for o, c in zip(offs[3:], extra_capacities)]
+        self.extras = [self.buf[o : o + c] for o, c in zip(offs[2:], extra_capacities)]
         self._offs, self._caps = offs, extra_capacities
-        self.plan = self.buf[self._plan_off :]
+        self.plan = self.buf[self._plan_off : self._tables_off]
         acc_off = (self.max_partials * 8 + 255) // 256 * 256
         ws = acc_off + (self.max_partials * head_dim * 4 + 255) // 256 * 256
         self.workspace = torch.empty(ws, dtype=torch.uint8, device=self.device)
@@ -582,15 +585,17 @@ class FixedAttention:
         o = self._offs
         h[o[0] : o[0] + R + 1] = query_start_loc
         h[o[1] : o[1] + R] = context_lens
-        tbl = h[o[2] : o[2] + self.max_reqs * self.max_blocks].reshape(self.max_reqs,
-                                                                        self.max_blocks)
-        tbl[:R] = -1
-        tbl[:R, : bt.shape[1]] = bt
-        for e, off in zip(extras, o[3:]):
+        t0 = self._tables_off
+        tbl = h[t0 : t0 + R * self.max_blocks].reshape(R, self.max_blocks)
+        tbl[:] = -1
+        tbl[:, : bt.shape[1]] = bt
+        for e, off in zip(extras, o[2:]):
             h[off : off + e.size] = e.reshape(-1)
         h[self._plan_off : self._plan_off + plan.size] = plan
         used = self._plan_off + plan.size
         self.buf[:used].copy_(self.host[:used], non_blocking=True)
+        t1 = t0 + R * self.max_blocks
+        self.buf[t0:t1].copy_(self.host[t0:t1], non_blocking=True)
         self.num_reqs = R
         self.row_waves = row_waves
         return True
