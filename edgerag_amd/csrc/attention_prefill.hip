@@ -40,6 +40,13 @@ constexpr int kD = 64;
 #ifndef EDGERAG_ATTN_SHARED_TILES_PER_CU
 #define EDGERAG_ATTN_SHARED_TILES_PER_CU 1  // tile workgroups per CU that the pad allows
 #endif
+#ifndef EDGERAG_TILE_PRIO
+// Issue priority (s_setprio) of the tile waves. Beside the decode rows (shared mode) the VALU-
+// bound tiles then win the SIMDs' issue slots and the memory-bound row waves fill the gaps:
+// config 3 227-229 -> 220-221 us (priority 1: 221-224, 3: 221-223; two tile workgroups per CU
+// instead of one, at priority 2: 253 us).
+#define EDGERAG_TILE_PRIO 2
+#endif
 constexpr unsigned kSharedLdsPad = EDGERAG_ATTN_SHARED_PAD_KB * 1024;
 constexpr int kKeys = 64;            // keys per LDS tile
 constexpr int kRow = 64;             // halves per LDS row (K: one key; V^T: one dim)
@@ -166,6 +173,7 @@ void attn_prefill_mfma_kernel(
   __shared__ __align__(16) _Float16 svt[2][kD * kRow];
   __shared__ int sblk[kMaxTileBlocks];
 
+  if (EDGERAG_TILE_PRIO > 0) __builtin_amdgcn_s_setprio(EDGERAG_TILE_PRIO);
   const int32_t* it = plan + plan[H_ITEM_OFF] + int64_t(item_base + blockIdx.x) * kItemWords;
   const int r = it[I_REQ], h = it[I_HEAD], qb = it[I_QBEGIN], qc = it[I_QCOUNT];
   const int kb = it[I_KVBEGIN], ke = it[I_KVEND], split = it[I_SPLIT];
