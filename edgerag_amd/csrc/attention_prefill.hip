@@ -13,10 +13,12 @@
 //     MFMA operand reads and the staging writes are bank-conflict free.
 //   * each wave computes S^T = K Q^T with v_mfma_f32_32x32x16_f16: A = 32 keys x 16 dims from
 //     LDS, B = Q^T from registers (loaded once per item): per lane, 16 keys of one query.
-//   * online softmax in the log2 domain: the running max is kept on raw scores, the scale is
-//     folded into the exponent's FMA, and the max is only raised when a score beats it by 2^8
-//     (lazy rescale; p <= 256 stays exact in fp16). Masks (causal k <= L - c + i, split end,
-//     invalid blocks) are applied only on tiles that need them.
+//   * online softmax in the log2 domain: Q is scaled by softmax_scale * log2(e) once per item
+//     (rounded to fp16, as torch's SDPA scales q before the product), and the S accumulators start
+//     at -m, so the MFMA leaves s - m and every probability is one v_exp_f32 with no FMA. The max
+//     m is only raised when a score beats it by 2^8 (lazy rescale; p <= 256 stays exact in fp16).
+//     Masks (causal k <= L - c + i, split end, invalid blocks) are applied only on tiles that need
+//     them.
 //   * O^T += V^T P^T with the same MFMA: the probabilities, packed to fp16, are already in the
 //     B-operand layout once the contraction index is permuted; V^T is stored in that permuted key
 //     order, so each A operand is one 16-byte LDS read. l accumulates the same fp16 p (v_dot2).
@@ -219,16 +221,20 @@ void attn_prefill_mfma_kernel(
   }
   const bool item_has_bad = __syncthreads_or(any_bad) != 0;
 
-  // Q^T as the B operand: k-step ks covers dims 16*ks + 8*g .. +7 of this lane's query.
+  // Q^T as the B operand: k-step ks covers dims 16*ks + 8*g .. +7 of this lane's query, scaled
+  // by scale_log2 (so S is in the log2 domain).
   h8 qop[4];
   {
     const _Float16* qp = q + int64_t(t) * q_st + int64_t(hq) * q_sh;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-      qop[ks] = active ? *reinterpret_cast<const h8*>(qp + 16 * ks + 8 * g) : h8{};
+    for (int ks = 0; ks < 4; ++ks) {
+      const h8 raw = active ? *reinterpret_cast<const h8*>(qp + 16 * ks + 8 * g) : h8{};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qop[ks][e] = _Float16(float(raw[e]) * scale_log2);
+    }
   }
   f32x16 o0 = {}, o1 = {};  // O^T dims 0-31 and 32-63 of this lane's query
-  float m = -INFINITY;      // reference max of raw (unscaled) scores
+  float m = -INFINITY;      // reference max of the log2-domain scores
   float l = 0.f;
   const h2 ones = {_Float16(1.f), _Float16(1.f)};
 
@@ -240,8 +246,15 @@ void attn_prefill_mfma_kernel(
 
   // One 64-key tile on staged LDS buffers (skb, svb).
   auto tile = [&](int k0, const _Float16* skb, const _Float16* svb) {
-    // S^T = K Q^T: two 32-key tiles, 4 k-steps of 16 dims (dim chunk 2ks + g).
-    f32x16 s[2] = {{}, {}};
+    // S^T = K Q^T - m: two 32-key tiles, 4 k-steps of 16 dims (dim chunk 2ks + g), accumulated
+    // onto -m (0 before the first visible score).
+    const float c0 = m == -INFINITY ? 0.f : -m;
+    f32x16 s[2];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      s[0][i] = c0;
+      s[1][i] = c0;
+    }
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
@@ -283,19 +296,25 @@ void attn_prefill_mfma_kernel(
 #pragma unroll
       for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, s[kt][i]);
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));  // the other 16 keys of each 32-key tile
-    // Lazy rescale: the reference max m only moves when a score beats it by 2^kRescaleLog2.
-    const bool up = m == -INFINITY ? tmax != -INFINITY : (tmax - m) * scale_log2 > kRescaleLog2;
+    // Lazy rescale: the reference max m only moves when a score beats it by 2^kRescaleLog2 (the
+    // scores are s - m here; before the first visible score, m is -inf and s is absolute).
+    const bool first = m == -INFINITY;
+    const bool up = first ? tmax != -INFINITY : tmax > kRescaleLog2;
     if (__any(up)) {
-      const float m_new = up ? tmax : m;
-      const float alpha = m == -INFINITY ? (up ? 0.f : 1.f) : exp2_fast((m - m_new) * scale_log2);
-      m = m_new;
+      const float shift = up ? tmax : 0.f;
+      const float alpha = first ? (up ? 0.f : 1.f) : exp2_fast(-shift);
+      if (up) m = first ? tmax : m + tmax;
       l *= alpha;
       o0 *= alpha;
       o1 *= alpha;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        s[0][i] -= shift;
+        s[1][i] -= shift;
+      }
     }
-    const float bias = m == -INFINITY ? 0.f : -m * scale_log2;
 
-    // P = exp2(s * scale - m * scale), packed to fp16 in the B-operand order of each k-step.
+    // P = exp2(s - m), packed to fp16 in the B-operand order of each k-step.
     float lsum = 0.f;
 #pragma unroll
     for (int st4 = 0; st4 < 4; ++st4) {
@@ -303,8 +322,8 @@ void attn_prefill_mfma_kernel(
       h8 pb;
 #pragma unroll
       for (int j = 0; j < 8; j += 2) {
-        const float p0 = exp2_fast(fmaf(s[kt][8 * half + j], scale_log2, bias));
-        const float p1 = exp2_fast(fmaf(s[kt][8 * half + j + 1], scale_log2, bias));
+        const float p0 = exp2_fast(s[kt][8 * half + j]);
+        const float p1 = exp2_fast(s[kt][8 * half + j + 1]);
         const h2 pp = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(p0, p1));
         pb[j] = pp[0];
         pb[j + 1] = pp[1];
@@ -354,9 +373,9 @@ void attn_prefill_mfma_kernel(
              _Float16(o1[4 * qd + 2] * inv), _Float16(o1[4 * qd + 3] * inv)};
     }
   } else {
-    // Partials carry the max in the same log2 domain as the decode kernels: m * scale_log2.
+    // Partials carry the max in the log2 domain, like the decode kernels'.
     const int64_t idx = int64_t(part_off) + (int64_t(t - q0) * n_q_heads + hq) * nsplit + split;
-    if (g == 0) part_ml[idx] = make_float2(m == -INFINITY ? m : m * scale_log2, l);
+    if (g == 0) part_ml[idx] = make_float2(m, l);
     float* pa = part_acc + idx * kD;
 #pragma unroll
     for (int qd = 0; qd < 4; ++qd) {
