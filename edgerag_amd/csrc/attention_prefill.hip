@@ -236,6 +236,9 @@ void attn_prefill_mfma_kernel(
   f32x16 o0 = {}, o1 = {};  // O^T dims 0-31 and 32-63 of this lane's query
   float m = -INFINITY;      // reference max of the log2-domain scores
   float l = 0.f;
+  // -m in every register (0 while m is -inf): the C operand of each tile's first S MFMA, rewritten
+  // only when m moves, so no tile spends instructions on initialising its accumulators.
+  f32x16 neg_m = {};
   const h2 ones = {_Float16(1.f), _Float16(1.f)};
 
   const uint32_t head_bytes = uint32_t(int64_t(num_blocks) * block_size * kD * 2);
@@ -246,21 +249,15 @@ void attn_prefill_mfma_kernel(
 
   // One 64-key tile on staged LDS buffers (skb, svb).
   auto tile = [&](int k0, const _Float16* skb, const _Float16* svb) {
-    // S^T = K Q^T - m: two 32-key tiles, 4 k-steps of 16 dims (dim chunk 2ks + g), accumulated
-    // onto -m (0 before the first visible score).
-    const float c0 = m == -INFINITY ? 0.f : -m;
+    // S^T = K Q^T - m: two 32-key tiles, 4 k-steps of 16 dims (dim chunk 2ks + g), the first
+    // one accumulating onto -m (0 before the first visible score).
     f32x16 s[2];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      s[0][i] = c0;
-      s[1][i] = c0;
-    }
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) {
         const h8 ka = *reinterpret_cast<const h8*>(skb + lds_chunk(32 * kt + col, 2 * ks + g));
-        s[kt] = mfma32(ka, qop[ks], s[kt]);
+        s[kt] = mfma32(ka, qop[ks], ks == 0 ? neg_m : s[kt]);
       }
     }
     // Register i of tile kt holds key 32kt + (i%4) + 8(i/4) + 4g.
@@ -304,6 +301,9 @@ void attn_prefill_mfma_kernel(
       const float shift = up ? tmax : 0.f;
       const float alpha = first ? (up ? 0.f : 1.f) : exp2_fast(-shift);
       if (up) m = first ? tmax : m + tmax;
+      const float nm = m == -INFINITY ? 0.f : -m;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) neg_m[i] = nm;
       l *= alpha;
       o0 *= alpha;
       o1 *= alpha;
