@@ -106,15 +106,12 @@ def step_bytes(lens, q_lens, bt):
 
 
 def run_step(b):
-    """The KV append and the attention of one step: one launch for a decode-only batch (the
-    append fused into the decode rows), otherwise kv_append, then the attention (prefill tiles and
-    decode rows overlapped on two streams)."""
-    if b["plan"].decode_only:
-        kernels.paged_attention_append(b["nk"], b["nv"], b["slots"], b["q"], b["kp"], b["vp"],
-                                       b["plan"], D**-0.5, out=b["out"])
-        return
-    kernels.kv_append(b["nk"], b["nv"], b["slots"], b["kp"], b["vp"])
-    kernels.paged_attention(b["q"], b["kp"], b["vp"], b["plan"], D**-0.5, out=b["out"])
+    """The KV append and the attention of one step, through paged_attention_append: one launch
+    for a decode-only batch (the append fused into the decode rows); with prefill tiles, the tiles
+    after the append of the new rows on the current stream and the decode rows, appending their
+    own positions, on a second one."""
+    kernels.paged_attention_append(b["nk"], b["nv"], b["slots"], b["q"], b["kp"], b["vp"],
+                                   b["plan"], D**-0.5, out=b["out"])
 
 
 def time_step(b, steps, warmup):
@@ -125,17 +122,10 @@ def time_step(b, steps, warmup):
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
            torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     torch.cuda.synchronize()
-    fused = b["plan"].decode_only
     for e0, e1, e2 in ev:
         e0.record()
-        if not fused:
-            kernels.kv_append(b["nk"], b["nv"], b["slots"], b["kp"], b["vp"])
-        e1.record()  # fused: the attention launch carries the append
-        if fused:
-            kernels.paged_attention_append(b["nk"], b["nv"], b["slots"], b["q"], b["kp"],
-                                           b["vp"], b["plan"], D**-0.5, out=b["out"])
-        else:
-            kernels.paged_attention(b["q"], b["kp"], b["vp"], b["plan"], D**-0.5, out=b["out"])
+        e1.record()  # the attention launch carries the append
+        run_step(b)
         e2.record()
     torch.cuda.synchronize()
     step_ms = sum(e0.elapsed_time(e2) for e0, _, e2 in ev) / steps
@@ -591,7 +581,7 @@ def run_cfg3(device, args):
         "step_bytes": int(step_bytes_total),
         "step_gbs": round(step_bytes_total / (s3 * 1e-3) / 1e9, 1),
         "hbm_frac": round(step_bytes_total / (s3 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-        "attn_us": round(a3 * 1e3, 1),
+        "attn_us": round(a3 * 1e3, 1),  # the append + attention launches (one call)
         "prefill_gflop": 46.18,
         "attn_items": b3["plan"].n_items,
         "plan_us": round(b3["plan_us"], 1),

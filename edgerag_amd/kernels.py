@@ -433,10 +433,13 @@ def paged_attention_append(
     plan: AttentionPlan,
     scale: float,
     out: torch.Tensor | None = None,
+    overlap: bool = True,
 ) -> torch.Tensor:
     """``kv_append(key, value, slot_mapping, pools)`` then ``paged_attention(query, ...)``, with the
     same results; one launch for decode batches (the waves reaching a request's new positions read
-    them from ``key``/``value`` and write them to the pools)."""
+    them from ``key``/``value`` and write them to the pools). With ``overlap`` and a batch holding
+    prefill tiles, the attention after the append overlaps tiles and decode rows as
+    ``paged_attention`` does."""
     require_device(key, value, slot_mapping, query, key_pool, value_pool)
     _check_pool(key_pool, "key_pool")
     _check_pool(value_pool, "value_pool")
@@ -467,6 +470,14 @@ def paged_attention_append(
         out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
     elif out.shape != query.shape or out.dtype != query.dtype or out.stride(2) != 1:
         raise ValueError("out must match query in shape and dtype, head_dim contiguous")
+    n_items, n_row = int(plan.plan_host[2]), int(plan.plan_host[13])
+    if overlap and 0 < n_row < n_items:
+        # A batch with prefill tiles: the append, then the tiles and the decode rows overlapped
+        # on two streams (paged_attention). Appending only the tiles' rows first and letting the
+        # rows append their own positions beside them measured slower (config 3: 0.242-0.26
+        # against 0.221 ms per step): the rows then take the CUs before the tiles are resident.
+        kv_append(key, value, slot_mapping, key_pool, value_pool)
+        return paged_attention(query, key_pool, value_pool, plan, scale, out=out, overlap=True)
     ws = plan.workspace
     call(
         "edgerag_paged_attention_append", key.data_ptr(), value.data_ptr(),
