@@ -1021,11 +1021,11 @@ void launch_skinny(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t
                    const f16* scales, const f16* bias, int32_t n, int32_t g, f16* y, int64_t ys,
                    hipStream_t s) {
   constexpr int U = skinny_u<BITS, MT>();
-  // Waves per workgroup split K, chosen from K alone (so a row's summation order, and so its
-  // bits, does not depend on N or on the other rows of the launch): enough waves that each
-  // holds about one batch of U chunks, at most kMaxSkinnyWaves -- or 16 for one-tile,
-  // one-m-tile launches over a long K (the down projection), where 1024-thread workgroups still
-  // fit the register file and halve the round trips per wave.
+  // Waves per workgroup split K: enough that each holds about one batch of U chunks, at most
+  // kMaxSkinnyWaves -- or 16 for one-tile, one-m-tile launches over a long K (the down
+  // projection), where 1024-thread workgroups still fit the register file and halve the round
+  // trips per wave. The split depends on K, the row tiles (N) and the m-tiles (M), never on the
+  // values, so a launch shape always sums a row in the same order.
   const int nkb = k / SkinnyCfg<BITS>::KB;
   const int kw_max = (NT == 1 && MT == 1 && nkb > kMaxSkinnyWaves * U) ? 16 : kMaxSkinnyWaves;
   int kw = 1;
@@ -1195,11 +1195,12 @@ void launch_stream(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t
 
 // Waves per workgroup and steps per batch of the streaming kernel for F k-slices, NT row tiles
 // and MT m-tiles: one batch of at most 8 steps per wave; at least 4 waves (one per SIMD), or 8
-// for two row tiles (one output per thread); at most 16, or 8 for two row or m tiles, whose
-// registers would not fit 16 waves. They depend on K, F, NT and MT only (so a row's summation
-// order, and so its bits, on the shape alone), except that 16-wave workgroups (K > 64 F steps)
-// drop to 8 where their registers would not fit (F = 2 with two m-tiles, four m-tiles); several
-// m-tiles take batches of 4 steps to bound their activation registers.
+// for two row tiles (one output per thread); at most 16 for one k-slice with one row tile and
+// up to two m-tiles, else 8 (the registers of 16 such waves would not fit; two k-slices stop at
+// 8 for one m-tile too, so that their one- and two-m-tile launches split K alike). The waves
+// depend on K, F, NT and MT; for up to 16 tokens MT does not change them, so a decode token's
+// summation order, and so its bits, depend on K and N alone. Several m-tiles take batches of 4
+// steps to bound their activation registers.
 struct StreamWaves {
   int kw;
   bool u8;
@@ -1207,7 +1208,7 @@ struct StreamWaves {
 StreamWaves stream_waves(int f, int nt, int mt, int k) {
   const int nc = k / (64 * f);
   const int kw_min = nt == 1 ? 4 : 8;
-  const int kw_max = nt == 1 && mt < 4 && !(f == 2 && mt == 2) ? 16 : 8;
+  const int kw_max = nt == 1 && mt < 4 && f == 1 ? 16 : 8;
   int kw = kw_min;
   while (kw < kw_max && kw * 8 < nc) kw *= 2;
   return {kw, mt == 1 && (nc + kw - 1) / kw > 4 && nc >= 8};
@@ -1236,7 +1237,7 @@ void launch_stream_w(StreamWaves sw, const f16* x, int64_t xs, int32_t m, int32_
   if constexpr (NT == 1 || EPI == kEpiRope) {
     if (sw.kw == 4) EDGERAG_STREAM(4);
   }
-  if constexpr (NT == 1 && MT < 4 && !(F == 2 && MT == 2)) {
+  if constexpr (NT == 1 && MT < 4 && F == 1) {
     if (sw.kw == 16) EDGERAG_STREAM(16);
   }
   EDGERAG_STREAM(8);

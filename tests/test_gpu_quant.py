@@ -410,6 +410,27 @@ def test_quant_linear_int8_per_channel_streaming(device, k, n) -> None:
             assert torch.equal(y1[0], y[m - 1])
 
 
+def test_streaming_long_k_rows_independent_of_batch(device) -> None:
+    """Two k-slices (N < 4096) over a K long enough that one m-tile alone could take 16 waves:
+    the launches of 1..8 and 9..16 tokens split K alike, so every row of a decode batch has the
+    bits it has alone, and all match the reference at the linear tolerance."""
+    k, n = 16384, 2048
+    w = _weight(n, k, 91)
+    cfg = oq.QuantConfig(k, 8)
+    packed, scales = oq.quantize_for_layer(w, cfg)
+    pd, sd = packed.to(device), scales.to(device)
+    for m in (8, 9, 16):
+        x = torch.randn(m, k, generator=seeded(m + 5)).half()
+        xd = x.to(device)
+        y = kernels.quant_linear(xd, pd, sd, None, k, n, 8, k)
+        torch.testing.assert_close(y.float().cpu(),
+                                   oq.quant_linear_reference(x, packed, scales, None, k, cfg),
+                                   **LINEAR_TOL)
+        for r in (0, m - 1):
+            y1 = kernels.quant_linear(xd[r : r + 1], pd, sd, None, k, n, 8, k)
+            assert torch.equal(y1[0], y[r])
+
+
 SPLIT_SHAPES = [  # (K, N, bits, group): 64x64 tile grids below 256 workgroups (the workspace
     # route: unsplit or split K by the cost model)
     (8192, 2048, 8, 8192),
