@@ -239,6 +239,30 @@ def test_mixed_prefill_chunks_and_decodes(device, dtype) -> None:
         k_: v_ * 2 for k_, v_ in tol.items()})
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("d", [16, 32, 256])
+def test_mixed_batch_other_head_dims(device, dtype, d) -> None:
+    """The same mixed batch at the other head dims the kernels instantiate (the row kernels take
+    the prefill slices there), in fp16 and bf16; one head of the offset chunk against the float64
+    textbook softmax as well."""
+    lens = [40, 64 + 37, 300, 17, 1000, 5]
+    q_lens = [40, 37, 1, 1, 129, 5]
+    scale = d**-0.5
+    # bf16 rounds q, K, V and the output to 8 significant bits.
+    tol = FP16_TOL if dtype == torch.float16 else dict(rtol=2e-2, atol=1e-2)
+    kp, vp, tables, qsl, q, bt = _ragged_case(lens, q_lens, 8, 4, d, dtype, 91 + d)
+    expected = oa.ragged_reference(q, kp, vp, qsl.tolist(), lens, tables, scale)
+    got = _run_ragged(device, kp, vp, qsl, lens, bt, q, scale)
+    assert got.dtype == dtype
+    torch.testing.assert_close(got.float(), expected, **tol)
+    r, h = 1, 5
+    k = op.gather_pool(kp.float(), tables[r], lens[r])[h // 2]
+    v = op.gather_pool(vp.float(), tables[r], lens[r])[h // 2]
+    ref64 = oa.attention_f64(q[qsl[r] : qsl[r + 1], h].float(), k, v, lens[r] - q_lens[r], scale)
+    torch.testing.assert_close(got[qsl[r] : qsl[r + 1], h].double(), ref64,
+                               **{k_: v_ * 2 for k_, v_ in tol.items()})
+
+
 def test_chunked_prefill_equals_single_shot(device) -> None:
     """test_batched.py:80-119 restated: 3 chunks over the same pool == 1 chunk."""
     L, d = 300, 64
