@@ -61,14 +61,12 @@ def _both(kp, vp, q, qsl, lens, bt, n_q, n_kv, device):
 
 @pytest.mark.gpu
 def test_noalloc_equals_the_workspace_entry_on_two_calls(device) -> None:
-    """Call 1: the config-3 batch (3 prefill slices of 512 at offsets 0 / 3584 / 6656 beside 24
-    decodes, 32/32 heads): MFMA tiles and decode rows, 22.7 MB of partials. Call 2: a smaller
-    decode batch with split contexts. Each equals edgerag_paged_attention bit for bit."""
-    g = seeded(303)
-    dec = torch.randint(512, 7473, (24,), generator=g).tolist()
-    lens1 = [512, 3584 + 512, 6656 + 512] + dec
-    q1 = [512, 512, 512] + [1] * 24
-    print("noalloc call 1: cfg3 batch, 27 requests, 1560 tokens", flush=True)
+    """Call 1: the config-3 prefill slices alone (3 slices of 512 at offsets 0 / 3584 / 6656,
+    32/32 heads): MFMA tiles split over the keys, 21.6 MB of partials. Call 2: a smaller decode
+    batch with split contexts. Each equals edgerag_paged_attention bit for bit."""
+    lens1 = [512, 3584 + 512, 6656 + 512]
+    q1 = [512, 512, 512]
+    print("noalloc call 1: 3 prefill slices, 1536 tokens", flush=True)
     kp, vp, q, qsl, lens, bt, tables = _batch(lens1, q1, 32, 32, 303, device)
     ref1, got1, plan1 = _both(kp, vp, q, qsl, lens, bt, 32, 32, device)
     assert plan1.workspace_bytes > 16 << 20
