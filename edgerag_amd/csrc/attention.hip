@@ -55,6 +55,9 @@ constexpr int32_t kPlanVersion = plan::kVersion;
 #ifndef EDGERAG_ROW_WG_PART
 #define EDGERAG_ROW_WG_PART 256  // longest part (tokens) a wave of a workgroup-split row takes
 #endif
+#ifndef EDGERAG_ROW_WG_PART_TILES
+#define EDGERAG_ROW_WG_PART_TILES 512  // the same, in a batch with prefill tiles beside the rows
+#endif
 constexpr int kMaxRowVecs = 8;  // query vectors a decode item may carry (c * n_rep)
 constexpr int kQTile = 16;      // query rows per prefill tile item
 constexpr int kMinSplit = EDGERAG_MIN_SPLIT;  // tokens; shorter splits are not worth a partial
@@ -69,6 +72,7 @@ constexpr int kMaxSplitBlocks = 64;  // one block id per lane in the decode kern
 #endif
 constexpr int kMinTileSplit = EDGERAG_MIN_TILE_SPLIT;  // keys: tiles split no finer than this
 constexpr int kTargetTiles = EDGERAG_TARGET_TILES;  // prefill tile items a batch aims for
+constexpr int kPlanCUs = 256;  // compute units the planner fills (MI355X)
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -835,7 +839,12 @@ extern "C" int edgerag_attn_plan_ex(const int32_t* query_start_loc, const int32_
   // fits kMaxRowWaves parts of at most EDGERAG_ROW_WG_PART tokens. Longer contexts would leave
   // each wave a long, latency-bound stream while the chip idles (measured: cfg2 -2%, cfg5 with 8
   // long requests -5%), so those batches (or any, when asked) keep one workgroup per KV split,
-  // merged by the combine launch through fp32 partials.
+  // merged by the combine launch through fp32 partials. Beside prefill tiles, when the rows'
+  // workgroups cover every CU, the chip does not idle (the tiles take the slack), so parts of up
+  // to EDGERAG_ROW_WG_PART_TILES tokens stay workgroup-split and the step saves the merge launch
+  // (three 512-token slices beside 24 decodes of up to 7,472 tokens, 768 row workgroups: 0.213
+  // -> 0.207 ms per step). Fewer row workgroups than CUs (a 512-token chunk beside 7 decodes,
+  // 224 of them) left a few CUs with long streams: -2.5% output tokens/s end to end.
   int64_t row_items = 0, max_row_len = 0;
   for (int r = 0; r < num_reqs; ++r) {
     const int64_t c = int64_t(query_start_loc[r + 1]) - query_start_loc[r];
@@ -849,7 +858,9 @@ extern "C" int edgerag_attn_plan_ex(const int32_t* query_start_loc, const int32_
       EDGERAG_ROW_WG && !(flags & EDGERAG_PLAN_SPLIT_ROWS) && row_items > 0 && head_dim <= 128 &&
       head_dim % (16 / es) == 0 && head_dim / (16 / es) <= kWave &&
       block_size % (kWave / (head_dim / (16 / es))) == 0 &&
-      max_row_len <= int64_t(kMaxRowWaves) * EDGERAG_ROW_WG_PART &&
+      max_row_len <= int64_t(kMaxRowWaves) * (n_tiles > 0 && row_items >= kPlanCUs
+                                                  ? EDGERAG_ROW_WG_PART_TILES
+                                                  : EDGERAG_ROW_WG_PART) &&
       max_row_len <= int64_t(kMaxRowWaves) * kMaxSplitBlocks * block_size;
   const int row_waves = wg_rows ? kMaxRowWaves : 0;
   const int wg_split_blocks =

@@ -284,30 +284,35 @@ def test_plan_size_query_without_buffer() -> None:
 
 
 @pytest.mark.parametrize(
-    "ctx,d,bs,split_rows,row_waves",
+    "ctx,d,bs,split_rows,row_waves,row_waves_tiles",
     [
-        ([4096, 1, 300], 64, 16, False, 16),  # every decode context short: workgroup-split rows
-        ([4097, 1, 300], 64, 16, False, 0),  # one longer than 16 waves x 256 tokens: KV splits
-        ([4096, 1, 300], 64, 16, True, 0),  # asked for KV splits
-        ([2000], 256, 16, False, 0),  # head_dim past the workgroup kernel's 128
-        ([2000], 128, 8, False, 16),
-        ([2000], 64, 32, False, 16),
+        ([4096, 1, 300], 64, 16, False, 16, 16),  # every decode context short: workgroup rows
+        # One longer than 16 waves x 256 tokens: KV splits; beside prefill tiles workgroup rows
+        # (parts of up to 512 tokens) once their 32 kv heads x 8 requests cover the 256 CUs.
+        ([4097, 1, 300], 64, 16, False, 0, 0),
+        ([4097] + [300] * 7, 64, 16, False, 0, 16),
+        ([8193] + [300] * 7, 64, 16, False, 0, 0),  # past 16 waves x 512 tokens: KV splits
+        ([4096, 1, 300], 64, 16, True, 0, 0),  # asked for KV splits
+        ([2000], 256, 16, False, 0, 0),  # head_dim past the workgroup kernel's 128
+        ([2000], 128, 8, False, 16, 16),
+        ([2000], 64, 32, False, 16, 16),
     ],
 )
-def test_plan_row_mode_selection(ctx, d, bs, split_rows, row_waves) -> None:
-    """Decode rows become one workgroup per (request, kv head) only when every decode context is
-    at most 4096 tokens and the fast decode kernel takes the shape; a prefill slice beside them
-    does not change the rows' mode."""
-    n = len(ctx)
+def test_plan_row_mode_selection(ctx, d, bs, split_rows, row_waves, row_waves_tiles) -> None:
+    """Decode rows become one workgroup per (request, kv head) when the fast decode kernel takes
+    the shape and every decode context fits 16 waves of at most 256 tokens -- 512 tokens when a
+    prefill slice in the batch keeps the chip busy beside them and the rows' workgroups cover
+    every CU."""
+    n, h = len(ctx), 32
     plan, ws = kernels.make_plan_host(np.arange(n + 1, dtype=np.int32), np.array(ctx, np.int32),
-                                      8, 8, d, bs, -(-max(ctx) // bs), torch.float16, split_rows)
+                                      h, h, d, bs, -(-max(ctx) // bs), torch.float16, split_rows)
     assert int(plan[19]) == row_waves
     items, reqs = decode_plan(plan)
     if row_waves:
         assert ws == 0 and int(plan[16]) == 0
-        assert items.shape[0] == n * 8 and all(int(nsplit) == 1 for nsplit in reqs[:, 0])
+        assert items.shape[0] == n * h and all(int(nsplit) == 1 for nsplit in reqs[:, 0])
     # With a prefill slice of 600 tokens at offset 3000 in the batch.
     qsl = np.array([0, *range(1, n + 1), n + 600], np.int32)
-    plan2, _ = kernels.make_plan_host(qsl, np.array([*ctx, 3600], np.int32), 8, 8, d, bs,
+    plan2, _ = kernels.make_plan_host(qsl, np.array([*ctx, 3600], np.int32), h, h, d, bs,
                                       -(-max(*ctx, 3600) // bs), torch.float16, split_rows)
-    assert int(plan2[19]) == row_waves
+    assert int(plan2[19]) == row_waves_tiles
