@@ -200,7 +200,7 @@ def _probe_call(name: str, *args) -> None:
         lib = ctypes.CDLL(str(PROBE_LIB_PATH))
         vp, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
         lib.edgerag_probe_read.argtypes = [vp, i64, i32, i32, vp, vp]
-        lib.edgerag_probe_gather.argtypes = [vp, vp, i32, i32, i32, vp, vp]
+        lib.edgerag_probe_gather.argtypes = [vp, vp, i32, i32, i32, i32, vp, vp]
         lib.edgerag_last_error.restype = ctypes.c_char_p
         _PROBE = lib
     rc = getattr(_PROBE, name)(*args)
@@ -250,7 +250,8 @@ def measure_ceilings(device, gather_bytes):
     """HBM ceilings of the two access patterns on this GPU (rooflines read against them as well as
     against the datasheet 8 TB/s): a 1 GiB contiguous stream, and `gather_bytes` read as random
     2 KiB chunks of a 2 GiB buffer (the paged pool's (head, block) rows) -- the cfg2 decode
-    launch's pattern and byte count."""
+    launch's pattern and byte count -- with plain loads and with non-temporal ones (the load
+    policy of the decode rows)."""
     from edgerag_amd import _lib
 
     out = {}
@@ -269,20 +270,26 @@ def measure_ceilings(device, gather_bytes):
                         dtype=torch.int32)
     sink = torch.zeros(1, dtype=torch.int32, device=device)
 
-    def launch():
-        _probe_call("edgerag_probe_gather", pool.data_ptr(), ids.data_ptr(), n_chunks // per_wave,
-                  per_wave, 2048, sink.data_ptr(), _stream())
+    def gather_gbs(nontemporal):
+        def launch():
+            _probe_call("edgerag_probe_gather", pool.data_ptr(), ids.data_ptr(),
+                        n_chunks // per_wave, per_wave, 2048, nontemporal, sink.data_ptr(),
+                        _stream())
 
-    launch()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(10):
         launch()
-    e1.record()
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / 10
-    out["gather_2KiB_gbs"] = round(n_chunks * 2048 / us / 1e3, 1)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(10):
+            launch()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / 10
+        return round(n_chunks * 2048 / us / 1e3, 1)
+
+    out["gather_2KiB_gbs"] = gather_gbs(0)
+    # Non-temporal loads, as the decode rows read the pools: the ceiling of their pattern.
+    out["gather_2KiB_nt_gbs"] = gather_gbs(1)
     out["source"] = "bench.py measure_ceilings: edgerag_probe_read / edgerag_probe_gather"
     del pool, ids
     torch.cuda.empty_cache()
@@ -739,7 +746,7 @@ def main() -> None:
     line["config"]["copy_gbs_1gib"] = copy_bandwidth(device)
     ceilings = measure_ceilings(device, attn_bytes)
     line["ceilings"] = ceilings
-    line["roofline"]["frac_of_gather_ceiling"] = round(attn_gbs / ceilings["gather_2KiB_gbs"], 4)
+    line["roofline"]["frac_of_gather_ceiling"] = round(attn_gbs / ceilings["gather_2KiB_nt_gbs"], 4)
     torch.cuda.empty_cache()
     if not args.no_extra:
         line["cfg3"] = run_cfg3(device, args)

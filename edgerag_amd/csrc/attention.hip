@@ -49,6 +49,9 @@ constexpr int32_t kPlanVersion = plan::kVersion;
 #ifndef EDGERAG_DECODE_U
 #define EDGERAG_DECODE_U 2
 #endif
+#ifndef EDGERAG_DECODE_NT
+#define EDGERAG_DECODE_NT 1  // decode rows read the pools with non-temporal loads
+#endif
 #ifndef EDGERAG_ROW_WG
 #define EDGERAG_ROW_WG 1  // decode rows as one workgroup per (request, kv head), merged in LDS
 #endif
@@ -254,8 +257,16 @@ __global__ __launch_bounds__(WG ? kMaxRowWaves * kWave : kWave) void attn_decode
         } else if (valid[u]) {
           const int64_t off =
               ((head_base + blk) * block_size + (tok[u] % block_size)) * D + sub * VEC;
-          kr[u] = load16(kpool + off);
-          vr[u] = load16(vpool + off);
+          // A launch reads each pool byte of a decode row once: non-temporal loads stream it
+          // without evicting reused lines (prefill tiles' K/V beside the rows). Measured on a
+          // 32-request decode step: 5.69 -> 6.40 TB/s; on the mixed step: 0.212 -> 0.199 ms.
+          if constexpr (EDGERAG_DECODE_NT) {
+            kr[u] = load16_stream(kpool + off);
+            vr[u] = load16_stream(vpool + off);
+          } else {
+            kr[u] = load16(kpool + off);
+            vr[u] = load16(vpool + off);
+          }
         } else {
           kr[u] = Vec16{};
           vr[u] = Vec16{};

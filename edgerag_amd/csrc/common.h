@@ -48,6 +48,16 @@ template <typename T>
 __device__ __forceinline__ Vec16 load16(const T* p) {
   return *reinterpret_cast<const Vec16*>(p);
 }
+
+// A 16-byte load marked non-temporal (its cache lines are the first to be evicted): for data a
+// launch reads exactly once, so that streaming it does not push reused lines out of L2.
+template <typename T>
+__device__ __forceinline__ Vec16 load16_stream(const T* p) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return Vec16{{v.x, v.y, v.z, v.w}};
+}
+
 template <typename T>
 __device__ __forceinline__ void store16(T* p, const Vec16& v) {
   *reinterpret_cast<Vec16*>(p) = v;

@@ -21,9 +21,11 @@ int edgerag_probe_read(const void* src, int64_t bytes, int32_t workgroups, int32
 
 /* Random gather: `waves` wavefronts, wave w reading the `per_wave` chunks
  * chunk_ids[w * per_wave ...] of `chunk_bytes` (1024, 2048 or 4096) at base + id * chunk_bytes,
- * with wave-wide 1 KiB loads, two chunks in flight. */
+ * with wave-wide 1 KiB loads, two chunks in flight; non-temporal loads when `nontemporal` != 0
+ * (the decode rows' loads). */
 int edgerag_probe_gather(const void* base, const int32_t* chunk_ids, int32_t waves,
-                         int32_t per_wave, int32_t chunk_bytes, void* sink, void* stream);
+                         int32_t per_wave, int32_t chunk_bytes, int32_t nontemporal, void* sink,
+                         void* stream);
 
 #ifdef __cplusplus
 }

@@ -7,7 +7,8 @@
 //   stream of the same size.
 // * probe_gather_kernel: one wavefront per list of chunk ids; each chunk (a multiple of 1 KiB,
 //   read with 1 KiB wave-wide loads) sits at a random chunk-aligned offset -- the access pattern
-//   of the paged KV pool (one 2 KiB (head, block) row of K or V per 16 tokens).
+//   of the paged KV pool (one 2 KiB (head, block) row of K or V per 16 tokens). With NT the loads
+//   are non-temporal, as the decode rows read the pools.
 // Neither kernel writes anything but a sentinel that no real data produces.
 #include "../common.h"
 #include "edgerag_probe.h"
@@ -37,7 +38,7 @@ __global__ __launch_bounds__(kProbeThreads) void probe_read_kernel(const uint4* 
   if (acc == 0x9E3779B9u) sink[0] = acc;
 }
 
-template <int LOADS>
+template <int LOADS, bool NT>
 __global__ __launch_bounds__(kWave) void probe_gather_kernel(const uint8_t* __restrict__ base,
                                                              const int32_t* __restrict__ ids,
                                                              int32_t per_wave,
@@ -52,7 +53,15 @@ __global__ __launch_bounds__(kWave) void probe_gather_kernel(const uint8_t* __re
       const int64_t c = my[min(i + u, per_wave - 1)];
 #pragma unroll
       for (int l = 0; l < LOADS; ++l)
-        v[u][l] = *reinterpret_cast<const uint4*>(base + c * (LOADS * 1024) + l * 1024 + lane * 16);
+      {
+        const uint8_t* a = base + c * (LOADS * 1024) + l * 1024 + lane * 16;
+        if constexpr (NT) {
+          const Vec16 w = load16_stream(a);
+          v[u][l] = uint4{w.w[0], w.w[1], w.w[2], w.w[3]};
+        } else {
+          v[u][l] = *reinterpret_cast<const uint4*>(a);
+        }
+      }
     }
 #pragma unroll
     for (int u = 0; u < 2; ++u)
@@ -86,8 +95,8 @@ extern "C" int edgerag_probe_read(const void* src, int64_t bytes, int32_t workgr
 }
 
 extern "C" int edgerag_probe_gather(const void* base, const int32_t* chunk_ids, int32_t waves,
-                                    int32_t per_wave, int32_t chunk_bytes, void* sink,
-                                    void* stream) {
+                                    int32_t per_wave, int32_t chunk_bytes, int32_t nontemporal,
+                                    void* sink, void* stream) {
   clear_error();
   if (base == nullptr || chunk_ids == nullptr || sink == nullptr || waves <= 0 || per_wave <= 0 ||
       !aligned16(base))
@@ -95,11 +104,21 @@ extern "C" int edgerag_probe_gather(const void* base, const int32_t* chunk_ids, 
   auto s = static_cast<hipStream_t>(stream);
   const auto* b = static_cast<const uint8_t*>(base);
   auto* out = static_cast<uint32_t*>(sink);
+#define EDGERAG_GATHER(L)                                                                       \
+  do {                                                                                         \
+    if (nontemporal)                                                                           \
+      hipLaunchKernelGGL((probe_gather_kernel<L, true>), dim3(waves), dim3(kWave), 0, s, b,    \
+                         chunk_ids, per_wave, out);                                            \
+    else                                                                                       \
+      hipLaunchKernelGGL((probe_gather_kernel<L, false>), dim3(waves), dim3(kWave), 0, s, b,   \
+                         chunk_ids, per_wave, out);                                            \
+  } while (0)
   switch (chunk_bytes) {
-    case 1024: hipLaunchKernelGGL(probe_gather_kernel<1>, dim3(waves), dim3(kWave), 0, s, b, chunk_ids, per_wave, out); break;
-    case 2048: hipLaunchKernelGGL(probe_gather_kernel<2>, dim3(waves), dim3(kWave), 0, s, b, chunk_ids, per_wave, out); break;
-    case 4096: hipLaunchKernelGGL(probe_gather_kernel<4>, dim3(waves), dim3(kWave), 0, s, b, chunk_ids, per_wave, out); break;
+    case 1024: EDGERAG_GATHER(1); break;
+    case 2048: EDGERAG_GATHER(2); break;
+    case 4096: EDGERAG_GATHER(4); break;
     default: return fail(EDGERAG_EINVAL, "edgerag_probe_gather: chunk_bytes %d (1, 2 or 4 KiB)", chunk_bytes);
   }
+#undef EDGERAG_GATHER
   return check_launch("edgerag_probe_gather");
 }
