@@ -72,6 +72,20 @@ constexpr uint32_t kOutOfRange = 0xFFFFFFF0u;
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// max / sum of v and its value in lane (lane ^ 32) in every lane: v_permlane32_swap exchanges
+// the wave's halves in a VALU op, where a shuffle goes through LDS (ds_bpermute, a round trip).
+// The swap leaves lane i with (v[i], v[i + 32]) and lane i + 32 with (v[i], v[i + 32]).
+__device__ __forceinline__ float halves_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float halves_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 __device__ __forceinline__ f32x16 mfma32(h8 a, h8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
@@ -101,25 +115,47 @@ struct Geometry {
   int kb, ke, blk0, bs_shift, bs_mask;
 };
 
-// Byte offset of (pos, 16-byte dim chunk dc) in one kv head's pool slice, or kOutOfRange.
-__device__ __forceinline__ uint32_t pool_offset(const Geometry& geo, const int* __restrict__ sblk,
-                                                int pos, int dc) {
+// Block id of key position pos (-1 past the split or for an invalid table entry).
+__device__ __forceinline__ int block_of(const Geometry& geo, const int* __restrict__ sblk,
+                                        int pos) {
   const int i = (pos >> geo.bs_shift) - geo.blk0;
-  const int blk = (pos < geo.ke && i < kMaxTileBlocks) ? sblk[i] : -1;
+  return (pos < geo.ke && i < kMaxTileBlocks) ? sblk[i] : -1;
+}
+
+// Byte offset of (pos, 16-byte dim chunk dc) in one kv head's pool slice, or kOutOfRange.
+__device__ __forceinline__ uint32_t pool_offset(const Geometry& geo, int blk, int pos, int dc) {
   return blk >= 0 ? ((uint32_t(blk) << geo.bs_shift) + uint32_t(pos & geo.bs_mask)) *
                             uint32_t(kD * 2) + uint32_t(16 * dc)
                   : kOutOfRange;
 }
 
+// The block ids one thread's staging loads of a 64-key tile need, looked up in LDS a tile before
+// the loads are issued (so issuing them waits on no LDS round trip).
+struct StageIds {
+  int k[kKPerThread];
+  int v[kVPerThread];
+};
+
 // K: chunk c = tid + kThreads * j is key c / 8, dim chunk c % 8 (8 lanes fill one key row).
 // V: pair p = tid + kThreads * j is key quad p % 16, dim chunk p / 16 (16 lanes fill one V^T row).
-__device__ __forceinline__ void stage_load(StageRegs& st, int tid, int k0, const Geometry& geo,
-                                           const int* __restrict__ sblk,
-                                           __amdgpu_buffer_rsrc_t krs, __amdgpu_buffer_rsrc_t vrs) {
+__device__ __forceinline__ void stage_ids(StageIds& ids, int tid, int k0, const Geometry& geo,
+                                          const int* __restrict__ sblk) {
+#pragma unroll
+  for (int j = 0; j < kKPerThread; ++j) ids.k[j] = block_of(geo, sblk, k0 + (tid + kThreads * j) / 8);
+#pragma unroll
+  for (int j = 0; j < kVPerThread; ++j) {
+    const int p = tid + kThreads * j;
+    ids.v[j] = (kVPairs % kThreads != 0 && p >= kVPairs) ? -1 : block_of(geo, sblk, k0 + 4 * (p % 16));
+  }
+}
+
+__device__ __forceinline__ void stage_load(StageRegs& st, const StageIds& ids, int tid, int k0,
+                                           const Geometry& geo, __amdgpu_buffer_rsrc_t krs,
+                                           __amdgpu_buffer_rsrc_t vrs) {
 #pragma unroll
   for (int j = 0; j < kKPerThread; ++j) {
     const int c = tid + kThreads * j;
-    st.k[j] = buffer_load16(krs, pool_offset(geo, sblk, k0 + c / 8, c % 8));
+    st.k[j] = buffer_load16(krs, pool_offset(geo, ids.k[j], k0 + c / 8, c % 8));
   }
 #pragma unroll
   for (int j = 0; j < kVPerThread; ++j) {
@@ -129,7 +165,7 @@ __device__ __forceinline__ void stage_load(StageRegs& st, int tid, int k0, const
     // The 4 keys of a quad share one block (blocks hold a multiple of 4 keys): one lookup, then
     // consecutive rows; keys past the split still get the out-of-range offset.
     const int pos = k0 + 4 * a;
-    const uint32_t base = pool_offset(geo, sblk, pos, b);
+    const uint32_t base = pool_offset(geo, ids.v[j], pos, b);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
       st.v[4 * j + kk] = buffer_load16(
@@ -292,7 +328,7 @@ void attn_prefill_mfma_kernel(
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, s[kt][i]);
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));  // the other 16 keys of each 32-key tile
+    tmax = halves_max(tmax);  // the other 16 keys of each 32-key tile
     // Lazy rescale: the reference max m only moves when a score beats it by 2^kRescaleLog2 (the
     // scores are s - m here; before the first visible score, m is -inf and s is absolute).
     const bool first = m == -INFINITY;
@@ -333,29 +369,37 @@ void attn_prefill_mfma_kernel(
       o0 = mfma32(*reinterpret_cast<const h8*>(svb + lds_chunk(col, vchunk)), pb, o0);
       o1 = mfma32(*reinterpret_cast<const h8*>(svb + lds_chunk(32 + col, vchunk)), pb, o1);
     }
-    lsum += __shfl_xor(lsum, 32, kWave);
-    l += lsum;
+    l += lsum;  // this half's keys only: the halves are added once, after the last tile
   };
 
   // Register stages st0 / st1 alternate, so a tile's loads are issued two tiles before it is
   // staged to LDS and have two tiles of matrix work to land. Loads past the split need no branch:
   // their positions get out-of-range offsets and load zeros. One barrier per tile: it orders the
   // tile's LDS writes before its reads, and every wave's reads of a buffer before its rewrite.
+  // The block ids of each stage's next loads are read from LDS one tile ahead (id0 / id1).
   StageRegs st0, st1;
-  stage_load(st0, tid, kb, geo, sblk, krs, vrs);
-  stage_load(st1, tid, kb + kKeys, geo, sblk, krs, vrs);
+  StageIds id0, id1;
+  stage_ids(id0, tid, kb, geo, sblk);
+  stage_ids(id1, tid, kb + kKeys, geo, sblk);
+  stage_load(st0, id0, tid, kb, geo, krs, vrs);
+  stage_load(st1, id1, tid, kb + kKeys, geo, krs, vrs);
+  stage_ids(id0, tid, kb + 2 * kKeys, geo, sblk);
+  stage_ids(id1, tid, kb + 3 * kKeys, geo, sblk);
   for (int k0 = kb; k0 < ke; k0 += 2 * kKeys) {
     stage_store(st0, tid, sk[0], svt[0]);
     __syncthreads();
-    stage_load(st0, tid, k0 + 2 * kKeys, geo, sblk, krs, vrs);
+    stage_load(st0, id0, tid, k0 + 2 * kKeys, geo, krs, vrs);
+    stage_ids(id0, tid, k0 + 4 * kKeys, geo, sblk);
     if (wave_live) tile(k0, sk[0], svt[0]);
     if (k0 + kKeys < ke) {
       stage_store(st1, tid, sk[1], svt[1]);
       __syncthreads();
-      stage_load(st1, tid, k0 + 3 * kKeys, geo, sblk, krs, vrs);
+      stage_load(st1, id1, tid, k0 + 3 * kKeys, geo, krs, vrs);
+      stage_ids(id1, tid, k0 + 5 * kKeys, geo, sblk);
       if (wave_live) tile(k0 + kKeys, sk[1], svt[1]);
     }
   }
+  l = halves_sum(l);
 
   if (!active) return;
   // O^T register i of dim tile dt holds dim 32dt + (i%4) + 8(i/4) + 4g of this lane's query.
