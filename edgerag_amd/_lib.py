@@ -35,6 +35,8 @@ EDGERAG_EUNSUPPORTED = 4
 ATTN_TILES, ATTN_ROWS, ATTN_COMBINE, ATTN_ALL = 1, 2, 4, 7
 ATTN_TILES_SHARED = 8  # modifier of ATTN_TILES: one tile workgroup per CU, beside decode rows
 PLAN_SPLIT_ROWS = 1  # edgerag_attn_plan_ex flag: decode rows as KV splits merged by a launch
+PLAN_OVERLAP = 2  # edgerag_attn_plan_ex flag: plan tiles beside rows (two streams) whenever both
+PLAN_WORD_OVERLAP = 20  # plan word: 1 when the plan is for tiles and rows on two streams
 QUANT_WORKSPACE_MAX = 8 * 1024 * 1024  # bound of edgerag_quant_linear_workspace_bytes
 ATTN_SCRATCH_BYTES = 32 * 1024 * 1024  # static partials of edgerag_paged_attention_noalloc
 
@@ -176,12 +178,17 @@ def load() -> ctypes.CDLL:
     return lib
 
 
+_FNS: dict = {}  # entry point name -> its bound ctypes function
+
+
 def call(name: str, *args) -> None:
     """Invoke an entry point and raise EdgeragError on a non-zero status."""
-    lib = load()
-    rc = getattr(lib, name)(*args)
+    fn = _FNS.get(name)
+    if fn is None:
+        fn = _FNS[name] = getattr(load(), name)
+    rc = fn(*args)
     if rc != EDGERAG_OK:
-        message = lib.edgerag_last_error().decode(errors="replace")
+        message = load().edgerag_last_error().decode(errors="replace")
         raise EdgeragError(name, rc, message)
 
 
@@ -206,8 +213,18 @@ def require_device(*tensors: torch.Tensor | None) -> None:
             )
 
 
+# torch's raw current-stream query: one C call where torch.cuda.current_stream builds a Stream
+# object (a few microseconds of host time per launch).
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_ptr(device: torch.device | None = None) -> int:
     """The current torch stream on ``device`` as a raw hipStream_t."""
+    if _RAW_STREAM is not None:
+        if isinstance(device, str):
+            device = torch.device(device)
+        index = device.index if isinstance(device, torch.device) else device
+        return _RAW_STREAM(torch.cuda.current_device() if index is None else index)
     return torch.cuda.current_stream(device).cuda_stream
 
 

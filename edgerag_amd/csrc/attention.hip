@@ -76,6 +76,8 @@ constexpr int kMaxSplitBlocks = 64;  // one block id per lane in the decode kern
 constexpr int kMinTileSplit = EDGERAG_MIN_TILE_SPLIT;  // keys: tiles split no finer than this
 constexpr int kTargetTiles = EDGERAG_TARGET_TILES;  // prefill tile items a batch aims for
 constexpr int kPlanCUs = 256;  // compute units the planner fills (MI355X)
+// K/V bytes decode rows must read for the planner to put them beside prefill tiles.
+constexpr int64_t kOverlapRowBytes = int64_t(256) << 20;
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -798,7 +800,7 @@ extern "C" int edgerag_attn_plan_ex(const int32_t* query_start_loc, const int32_
                                     int32_t* plan, int64_t plan_capacity_words,
                                     int64_t* plan_words, int64_t* workspace_bytes) {
   clear_error();
-  if ((flags & ~EDGERAG_PLAN_SPLIT_ROWS) != 0)
+  if ((flags & ~(EDGERAG_PLAN_SPLIT_ROWS | EDGERAG_PLAN_OVERLAP)) != 0)
     return fail(EDGERAG_EINVAL, "edgerag_attn_plan: flags %d", flags);
   if (plan_words == nullptr || workspace_bytes == nullptr)
     return fail(EDGERAG_EINVAL, "edgerag_attn_plan: plan_words/workspace_bytes are NULL");
@@ -865,11 +867,21 @@ extern "C" int edgerag_attn_plan_ex(const int32_t* query_start_loc, const int32_
     }
   }
   const int es = elem_size(dtype);
+  // Tiles and rows on two streams (the tiles at one workgroup per CU, the rows in the rest of
+  // each CU) pay only when both sides are heavy: the tiles fill every CU and the rows stream at
+  // least kOverlapRowBytes of K/V. Otherwise one stream runs the tiles at full occupancy and then
+  // the rows, which also saves the host the fork and join of the streams. (Three 512-token
+  // slices beside 24 decodes of up to 7,472 tokens, 707 MB of rows: 0.175 against 0.258 ms on
+  // one stream. One 512-token chunk, 128 tiles, beside 7 decodes of 32-256 MB: every prefill
+  // iteration of the config-5 serving trace was faster on one stream.)
+  const bool overlap = n_tiles > 0 && row_items > 0 &&
+                       ((flags & EDGERAG_PLAN_OVERLAP) ||
+                        (n_tiles >= kPlanCUs && work * head_dim * 2 * es >= kOverlapRowBytes));
   const bool wg_rows =
       EDGERAG_ROW_WG && !(flags & EDGERAG_PLAN_SPLIT_ROWS) && row_items > 0 && head_dim <= 128 &&
       head_dim % (16 / es) == 0 && head_dim / (16 / es) <= kWave &&
       block_size % (kWave / (head_dim / (16 / es))) == 0 &&
-      max_row_len <= int64_t(kMaxRowWaves) * (n_tiles > 0 && row_items >= kPlanCUs
+      max_row_len <= int64_t(kMaxRowWaves) * (overlap && row_items >= kPlanCUs
                                                   ? EDGERAG_ROW_WG_PART_TILES
                                                   : EDGERAG_ROW_WG_PART) &&
       max_row_len <= int64_t(kMaxRowWaves) * kMaxSplitBlocks * block_size;
@@ -884,12 +896,12 @@ extern "C" int edgerag_attn_plan_ex(const int32_t* query_start_loc, const int32_
   const int split_blocks = int((split_len + block_size - 1) / block_size);
   // Prefill tiles: split the keys only when there are too few tiles to fill the GPU's tile slots,
   // and then only as far as needed for about that many items, in whole 64-key LDS tiles; every
-  // extra split costs a partial write and a merge. Beside decode rows the tiles run at one
-  // workgroup per CU (the rows take the rest of each CU), alone at two: kTargetTiles / 2 or
-  // kTargetTiles items. (Three 512-token slices, 384 tiles, beside 24 decodes: splitting them to
+  // extra split costs a partial write and a merge. Beside decode rows (overlap) the tiles run at
+  // one workgroup per CU (the rows take the rest of each CU), otherwise at two: kTargetTiles / 2
+  // or kTargetTiles items. (Three 512-token slices, 384 tiles, beside 24 decodes: splitting them to
   // 768 items for the larger target measured 0.225 against 0.215 ms per step.)
   // A split may span at most kMaxTileBlocks blocks (the MFMA tile kernel stages its block ids).
-  const int64_t target_tiles = row_items > 0 ? kTargetTiles / 2 : kTargetTiles;
+  const int64_t target_tiles = overlap ? kTargetTiles / 2 : kTargetTiles;
   const int64_t tile_split_cap =
       std::max<int64_t>(64, int64_t(kMaxTileBlocks - 1) * block_size / 64 * 64);
   const int64_t tile_split_len = std::min(
@@ -987,6 +999,7 @@ extern "C" int edgerag_attn_plan_ex(const int32_t* query_start_loc, const int32_
   plan[H_COMBINE_OFF] = int32_t(combine_off);
   plan[H_TILE_KIND] = mfma_tiles ? 1 : 0;
   plan[H_ROW_WAVES] = row_waves;
+  plan[H_OVERLAP] = overlap ? 1 : 0;
   std::copy(combine.begin(), combine.end(), plan + combine_off);
   int32_t* dst = plan + item_off;
   for (const auto* groups : {&rows, &tiles})

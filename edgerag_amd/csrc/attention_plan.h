@@ -37,6 +37,7 @@ enum Header {
   H_ROW_WAVES,         // 0: decode rows split across workgroups (partials + combine list);
                        // W > 0: one workgroup per row item, its W waves split the keys and
                        // merge in LDS (no partials)
+  H_OVERLAP,           // 1: planned for tiles and rows on two streams (tiles shared), 0: one
 };
 // Waves a workgroup-split row item may use (the kernel's LDS merge is sized for this many).
 constexpr int kMaxRowWaves = 16;

@@ -197,6 +197,12 @@ class AttentionPlan:
         """Every work item is a decode row (no prefill tiles): the append can fuse in."""
         return int(self.plan_host[2]) == int(self.plan_host[13])
 
+    @property
+    def overlap_rows(self) -> bool:
+        """The planner sized this batch's prefill tiles to run beside its decode rows on a second
+        stream (both are heavy, or ``force_overlap`` asked for it); else one stream runs all."""
+        return int(self.plan_host[_lib.PLAN_WORD_OVERLAP]) == 1
+
 
 _WORKSPACES: dict[torch.device, torch.Tensor] = {}
 
@@ -249,13 +255,16 @@ def make_plan_host(
     max_blocks_per_seq: int,
     dtype: torch.dtype,
     split_rows: bool = False,
+    force_overlap: bool = False,
 ) -> tuple[np.ndarray, int]:
     """Run the native host planner. Returns ``(plan words, workspace bytes)``.
 
     One planner call fills a buffer sized from the largest plan seen so far; only a plan larger
     than every earlier one needs a second call (the first reports the size). ``split_rows``
     plans decode rows as KV splits merged by a launch (``EDGERAG_PLAN_SPLIT_ROWS``) instead of
-    workgroups whose waves merge in LDS."""
+    workgroups whose waves merge in LDS. ``force_overlap`` plans any batch with both prefill
+    tiles and decode rows for the two-stream run (``EDGERAG_PLAN_OVERLAP``), which the planner
+    otherwise picks only when both are heavy."""
     lib = _lib.load()
     qsl = np.ascontiguousarray(query_start_loc, dtype=np.int32)
     ctx = np.ascontiguousarray(context_lens, dtype=np.int32)
@@ -265,7 +274,8 @@ def make_plan_host(
     words, ws = ctypes.c_int64(0), ctypes.c_int64(0)
     args = (
         qsl.ctypes.data, ctx.ctypes.data, num_reqs, n_q_heads, n_kv_heads, head_dim, block_size,
-        max_blocks_per_seq, dtype_code(dtype), _lib.PLAN_SPLIT_ROWS if split_rows else 0,
+        max_blocks_per_seq, dtype_code(dtype),
+        (_lib.PLAN_SPLIT_ROWS if split_rows else 0) | (_lib.PLAN_OVERLAP if force_overlap else 0),
     )
     plan = np.empty(_PLAN_WORDS_HINT[0], dtype=np.int32)
     rc = lib.edgerag_attn_plan_ex(*args, plan.ctypes.data, plan.size, ctypes.byref(words),
@@ -294,6 +304,7 @@ def plan_attention(
     extra_int32: list[np.ndarray] | None = None,
     workspace: bool = True,
     split_rows: bool = False,
+    force_overlap: bool = False,
 ) -> tuple[AttentionPlan, list[torch.Tensor]]:
     """Plan a ragged step on the host and upload all of its metadata in one copy.
 
@@ -306,7 +317,7 @@ def plan_attention(
         raise ValueError("block_tables must be (num_reqs, max_blocks)")
     plan, ws_bytes = make_plan_host(
         query_start_loc, context_lens, n_q_heads, n_kv_heads, head_dim, block_size,
-        block_tables.shape[1], dtype, split_rows,
+        block_tables.shape[1], dtype, split_rows, force_overlap,
     )
     extra = list(extra_int32 or [])
     views = upload_int32(
@@ -372,8 +383,9 @@ def paged_attention(
 ) -> torch.Tensor:
     """Ragged paged attention. ``query``/``out``: ``(num_tokens, n_q_heads, head_dim)``.
 
-    With ``overlap`` and a batch holding both prefill tiles and decode rows, the two run on two
-    streams (joined before the split merge), so MFMA work overlaps the KV streaming."""
+    With ``overlap`` and a plan made for it (:attr:`AttentionPlan.overlap_rows`: heavy prefill
+    tiles beside heavy decode rows), the two run on two streams (joined before the split merge),
+    so MFMA work overlaps the KV streaming."""
     query, out, lead = _attention_operands(query, key_pool, value_pool, plan, out)
     if plan.workspace_bytes > 0 and plan.workspace is None:
         raise ValueError("this plan was built without a workspace: use paged_attention_noalloc")
@@ -381,8 +393,7 @@ def paged_attention(
     args = (*lead, float(scale), out.data_ptr(), out.stride(0), out.stride(1),
             None if ws is None else ws.data_ptr(), plan.workspace_bytes)
     device = query.device
-    n_items, n_row = int(plan.plan_host[2]), int(plan.plan_host[13])
-    if overlap and 0 < n_row < n_items:
+    if overlap and plan.overlap_rows:
         # Prefill tiles (MFMA-bound) beside the decode rows (HBM-bound) on a side stream; the
         # merge of split partials waits for both. The tiles go first, on the current stream (the
         # side stream starts a few microseconds later, after its event wait), at one workgroup per
@@ -390,13 +401,15 @@ def paged_attention(
         # waves and ran mostly after the rows.
         main = torch.cuda.current_stream(device)
         side = _side_stream(device)
-        side.wait_stream(main)
+        fork, join = _overlap_events(device)
+        fork.record(main)
+        side.wait_event(fork)
         call("edgerag_paged_attention", *args, _lib.ATTN_TILES | _lib.ATTN_TILES_SHARED,
-             stream_ptr(device))
-        with torch.cuda.stream(side):
-            call("edgerag_paged_attention", *args, _lib.ATTN_ROWS, stream_ptr(device))
-        main.wait_stream(side)
-        call("edgerag_paged_attention", *args, _lib.ATTN_COMBINE, stream_ptr(device))
+             main.cuda_stream)
+        call("edgerag_paged_attention", *args, _lib.ATTN_ROWS, side.cuda_stream)
+        join.record(side)
+        main.wait_event(join)
+        call("edgerag_paged_attention", *args, _lib.ATTN_COMBINE, main.cuda_stream)
     else:
         call("edgerag_paged_attention", *args, _lib.ATTN_ALL, stream_ptr(device))
     return out
@@ -437,8 +450,8 @@ def paged_attention_append(
 ) -> torch.Tensor:
     """``kv_append(key, value, slot_mapping, pools)`` then ``paged_attention(query, ...)``, with the
     same results; one launch for decode batches (the waves reaching a request's new positions read
-    them from ``key``/``value`` and write them to the pools). With ``overlap`` and a batch holding
-    prefill tiles, the attention after the append overlaps tiles and decode rows as
+    them from ``key``/``value`` and write them to the pools). With ``overlap`` and a plan made for
+    the two-stream run, the attention after the append overlaps tiles and rows as
     ``paged_attention`` does."""
     require_device(key, value, slot_mapping, query, key_pool, value_pool)
     _check_pool(key_pool, "key_pool")
@@ -470,8 +483,7 @@ def paged_attention_append(
         out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
     elif out.shape != query.shape or out.dtype != query.dtype or out.stride(2) != 1:
         raise ValueError("out must match query in shape and dtype, head_dim contiguous")
-    n_items, n_row = int(plan.plan_host[2]), int(plan.plan_host[13])
-    if overlap and 0 < n_row < n_items:
+    if overlap and plan.overlap_rows:
         # A batch with prefill tiles: the append, then the tiles and the decode rows overlapped
         # on two streams (paged_attention). Appending only the tiles' rows first and letting the
         # rows append their own positions beside them measured slower (config 3: 0.242-0.26
@@ -494,7 +506,20 @@ def paged_attention_append(
     return out
 
 
+_OVERLAP_EVENTS: dict = {}
 _SIDE_STREAMS: dict[torch.device, torch.cuda.Stream] = {}
+
+
+def _overlap_events(device: torch.device) -> tuple[torch.cuda.Event, torch.cuda.Event]:
+    """Two events per device, made once, that order the side stream after the current one (fork)
+    and the current one after the side stream (join). A wait binds to the event's latest record
+    when it is enqueued, so recording the same event again for the next call is safe, and no
+    event is created per call (torch's wait_stream makes one each time)."""
+    device = torch.device(device)
+    events = _OVERLAP_EVENTS.get(device)
+    if events is None:
+        events = _OVERLAP_EVENTS[device] = (torch.cuda.Event(), torch.cuda.Event())
+    return events
 
 
 def _side_stream(device: torch.device) -> torch.cuda.Stream:

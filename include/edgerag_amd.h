@@ -136,8 +136,17 @@ int edgerag_attn_plan(const int32_t* query_start_loc, const int32_t* context_len
  * decode kernel takes the shape and every such context fits 16 waves of 64 blocks; otherwise,
  * or with EDGERAG_PLAN_SPLIT_ROWS, as one workgroup per KV split merged through fp32 partials
  * in the workspace. Results agree to fp32 rounding either way.
+ *
+ * A batch with both prefill tiles and decode rows is planned for one of two runs, recorded in
+ * plan word 20 (1: two streams, 0: one): the tiles (EDGERAG_ATTN_TILES | EDGERAG_ATTN_TILES_SHARED)
+ * on one stream beside the rows (EDGERAG_ATTN_ROWS) on another, joined before
+ * EDGERAG_ATTN_COMBINE; or EDGERAG_ATTN_ALL on one stream. The planner picks two streams when the
+ * tiles fill every CU at one workgroup each and the rows read at least 256 MiB of K/V;
+ * EDGERAG_PLAN_OVERLAP asks for it whenever the batch holds both. Either run of either plan gives
+ * the same results; the plan only sizes the work items for the run it names.
  */
 #define EDGERAG_PLAN_SPLIT_ROWS 1
+#define EDGERAG_PLAN_OVERLAP 2
 int edgerag_attn_plan_ex(const int32_t* query_start_loc, const int32_t* context_lens,
                          int32_t num_reqs, int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
                          int32_t block_size, int32_t max_blocks_per_seq, int32_t dtype,

@@ -300,9 +300,9 @@ def test_plan_size_query_without_buffer() -> None:
 )
 def test_plan_row_mode_selection(ctx, d, bs, split_rows, row_waves, row_waves_tiles) -> None:
     """Decode rows become one workgroup per (request, kv head) when the fast decode kernel takes
-    the shape and every decode context fits 16 waves of at most 256 tokens -- 512 tokens when a
-    prefill slice in the batch keeps the chip busy beside them and the rows' workgroups cover
-    every CU."""
+    the shape and every decode context fits 16 waves of at most 256 tokens -- 512 tokens when
+    the plan puts prefill tiles on a second stream beside them (keeping the chip busy) and the
+    rows' workgroups cover every CU."""
     n, h = len(ctx), 32
     plan, ws = kernels.make_plan_host(np.arange(n + 1, dtype=np.int32), np.array(ctx, np.int32),
                                       h, h, d, bs, -(-max(ctx) // bs), torch.float16, split_rows)
@@ -314,5 +314,46 @@ def test_plan_row_mode_selection(ctx, d, bs, split_rows, row_waves, row_waves_ti
     # With a prefill slice of 600 tokens at offset 3000 in the batch.
     qsl = np.array([0, *range(1, n + 1), n + 600], np.int32)
     plan2, _ = kernels.make_plan_host(qsl, np.array([*ctx, 3600], np.int32), h, h, d, bs,
+                                      -(-max(*ctx, 3600) // bs), torch.float16, split_rows,
+                                      force_overlap=True)
+    assert int(plan2[19]) == row_waves_tiles and int(plan2[20]) == 1
+    # Planned for one stream (160 tiles do not fill the CUs), the rows run alone after the tiles.
+    plan3, _ = kernels.make_plan_host(qsl, np.array([*ctx, 3600], np.int32), h, h, d, bs,
                                       -(-max(*ctx, 3600) // bs), torch.float16, split_rows)
-    assert int(plan2[19]) == row_waves_tiles
+    assert int(plan3[19]) == row_waves and int(plan3[20]) == 0
+
+
+def _mixed(slices, decodes):
+    """query_start_loc / context_lens of prefill slices (tokens, prefix) followed by decodes."""
+    q = [c for c, _ in slices] + [1] * len(decodes)
+    ctx = [c + p for c, p in slices] + list(decodes)
+    return np.concatenate([[0], np.cumsum(q)]).astype(np.int32), np.array(ctx, np.int32)
+
+
+@pytest.mark.parametrize("slices,decodes,force,overlap", [
+    # config 3: 384 tiles (every CU at one workgroup) beside 24 decodes reading 707 MB
+    ([(512, 0), (512, 3584), (512, 6656)], "cfg3", False, 1),
+    ([(512, 3000)], [3000] * 7, False, 0),  # a serving chunk: 128 tiles
+    ([(512, 3000)], [3000] * 7, True, 1),
+    ([(512, 0), (512, 3584), (512, 6656)], [100] * 24, False, 0),  # light rows (20 MB)
+    ([], [3000] * 7, True, 0),  # no tiles
+    ([(512, 3000)], [], True, 0),  # no rows
+])
+def test_plan_overlap_choice(slices, decodes, force, overlap) -> None:
+    """Plan word 20 records whether the batch is planned for tiles beside rows on two streams:
+    only when the tiles fill every CU and the rows read at least 256 MiB (or when asked), and
+    never without both. The tile split follows the run: unsplit at the 256 slots of one
+    workgroup per CU beside the rows, split toward 512 items for the one-stream run."""
+    if decodes == "cfg3":
+        decodes = torch.randint(512, 7473, (24,), generator=torch.Generator().manual_seed(3))
+        decodes = [int(x) for x in decodes]
+    qsl, ctx = _mixed(slices, decodes)
+    plan, _ = kernels.make_plan_host(qsl, ctx, 32, 32, 64, 16, -(-int(ctx.max()) // 16),
+                                     torch.float16, force_overlap=force)
+    assert int(plan[20]) == overlap
+    n_tiles = int(plan[2]) - int(plan[13])
+    unsplit = sum(-(-c // 128) for c, _ in slices) * 32
+    if overlap:
+        assert n_tiles == unsplit if unsplit >= 256 else 256 <= n_tiles < 512
+    elif slices:
+        assert n_tiles >= 512

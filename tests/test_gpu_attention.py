@@ -497,3 +497,51 @@ def test_append_fused_into_attention_equals_append_then_attention(device, dtype,
     ref64 = oa.attention_f64(q[qsl[r] : qsl[r + 1], 0], kh, vh, lens[r] - q_lens[r], scale)
     tol = FP32_TOL if dtype == torch.float32 else {k_: v_ * 4 for k_, v_ in FP16_TOL.items()}
     torch.testing.assert_close(got[qsl[r] : qsl[r + 1], 0].cpu().double(), ref64, **tol)
+
+
+@pytest.mark.parametrize("dtype,n_q,n_kv,d,dec", [
+    (torch.float16, 8, 4, 64, [300, 17, 1000, 5]),  # MFMA tiles beside decode rows
+    (torch.float16, 9, 3, 64, None),                 # config 3 lengths, GQA
+    (torch.float32, 8, 4, 64, [300, 17, 1000, 5]),  # tiles on the row kernel
+    (torch.bfloat16, 4, 2, 128, [900, 33]),
+])
+def test_two_stream_overlap_equals_one_stream(device, dtype, n_q, n_kv, d, dec) -> None:
+    """Decode rows on a second stream beside the prefill tiles (planned when both are heavy;
+    forced here with EDGERAG_PLAN_OVERLAP) give the one-stream results of the same plan bit for
+    bit, through paged_attention and paged_attention_append alike."""
+    g = seeded(d + n_q + len(dec or []))
+    if dec is None:
+        dec = torch.randint(512, 7473, (24,), generator=g).tolist()
+        lens, q_lens = [512, 3584 + 512, 6656 + 512] + dec, [512, 512, 512] + [1] * len(dec)
+    else:
+        lens, q_lens = [40, 64 + 37, 129 + 200] + dec, [40, 37, 129] + [1] * len(dec)
+    kp, vp, tables, qsl, q, bt = _ragged_case(lens, q_lens, n_q, n_kv, d, dtype, 53,
+                                              poison=False)
+    T = int(qsl[-1])
+    nk = torch.randn(T, n_kv, d, generator=g).to(dtype)
+    nv = torch.randn(T, n_kv, d, generator=g).to(dtype)
+    slots = np.array([tables[r][p // BLOCK_SIZE] * BLOCK_SIZE + p % BLOCK_SIZE
+                      for r, (L, c) in enumerate(zip(lens, q_lens)) for p in range(L - c, L)],
+                     np.int32)
+    plan, (slots_d,) = kernels.plan_attention(qsl, np.asarray(lens, np.int32), bt, n_q, n_kv, d,
+                                              BLOCK_SIZE, dtype, device, [slots],
+                                              force_overlap=True)
+    assert plan.overlap_rows
+    scale = d ** -0.5
+    qd, kpd, vpd = q.to(device), kp.to(device), vp.to(device)
+    one = kernels.paged_attention(qd, kpd, vpd, plan, scale, overlap=False)
+    two = kernels.paged_attention(qd, kpd, vpd, plan, scale, overlap=True)
+    torch.cuda.synchronize()
+    assert torch.equal(two, one)
+    tol = FP32_TOL if dtype == torch.float32 else dict(rtol=2e-2, atol=1e-2)
+    expected = oa.ragged_reference(q, kp, vp, qsl.tolist(), lens, tables, scale)
+    torch.testing.assert_close(two.cpu().float(), expected, **tol)
+    nkd, nvd = nk.to(device), nv.to(device)
+    kp1, vp1 = kp.to(device), vp.to(device)
+    kernels.kv_append(nkd, nvd, slots_d, kp1, vp1)
+    ref = kernels.paged_attention(qd, kp1, vp1, plan, scale, overlap=False)
+    got = kernels.paged_attention_append(nkd, nvd, slots_d, qd, kpd, vpd, plan, scale,
+                                         overlap=True)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+    assert torch.equal(kpd, kp1) and torch.equal(vpd, vp1)
