@@ -545,3 +545,26 @@ def test_two_stream_overlap_equals_one_stream(device, dtype, n_q, n_kv, d, dec) 
     torch.cuda.synchronize()
     assert torch.equal(got, ref)
     assert torch.equal(kpd, kp1) and torch.equal(vpd, vp1)
+
+
+def test_one_and_two_stream_plans_agree(device) -> None:
+    """A serving-shaped batch (a 512-token chunk after a 3,000-token prefix beside 7 decodes) is
+    planned for one stream by default (128 tiles split toward 512 items, rows sized to run
+    alone) and for two with EDGERAG_PLAN_OVERLAP (256 tile items, tiles at one workgroup per
+    CU). Both plans give the oracle's attention; they differ only in summation order."""
+    dec = [3000, 2500, 4000, 1200, 3300, 700, 3900]
+    lens, q_lens = [3512] + dec, [512] + [1] * len(dec)
+    kp, vp, tables, qsl, q, bt = _ragged_case(lens, q_lens, 32, 32, 64, torch.float16, 61)
+    ctx = np.asarray(lens, np.int32)
+    one, _ = kernels.plan_attention(qsl, ctx, bt, 32, 32, 64, BLOCK_SIZE, torch.float16, device)
+    two, _ = kernels.plan_attention(qsl, ctx, bt, 32, 32, 64, BLOCK_SIZE, torch.float16, device,
+                                    force_overlap=True)
+    assert not one.overlap_rows and two.overlap_rows
+    assert one.n_items - int(one.plan_host[13]) >= 512 > two.n_items - int(two.plan_host[13])
+    qd, kpd, vpd = q.to(device), kp.to(device), vp.to(device)
+    got1 = kernels.paged_attention(qd, kpd, vpd, one, 0.125).cpu()
+    got2 = kernels.paged_attention(qd, kpd, vpd, two, 0.125).cpu()
+    expected = oa.ragged_reference(q, kp, vp, qsl.tolist(), lens, tables, 0.125)
+    torch.testing.assert_close(got1.float(), expected, **FP16_TOL)
+    torch.testing.assert_close(got2.float(), expected, **FP16_TOL)
+    torch.testing.assert_close(got1, got2, **FP16_TOL)
