@@ -49,7 +49,7 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int mask) {
   return (uint64_t(hi) << 32) | lo;
 }
 
-template <int WAVES, int U>
+template <int WAVES, int U, int R>
 __global__ __launch_bounds__(WAVES * kWave) void lm_head_kernel(
     const f16* __restrict__ x, int64_t xs, int32_t m, int32_t k, const f16* __restrict__ w,
     int32_t v, f16* __restrict__ logits, int64_t ls, uint64_t* __restrict__ part) {
@@ -65,13 +65,35 @@ __global__ __launch_bounds__(WAVES * kWave) void lm_head_kernel(
 
   // Weight row `row`, k chunk (step, lg): 16 bytes at element 32 step + 8 lg.
   const uint4* wp = reinterpret_cast<const uint4*>(w + int64_t(row) * k) + lg;
-  // The first batch of weight loads is issued before the activations are staged.
+  // Staging the m x k/8 16-byte activation chunks. With R > 0 (at most R rows), thread c loads
+  // chunk c of every row, then issues the first batch of weight loads, then stores the chunks to
+  // LDS: the stores wait only for the activation loads (L2 hits, issued first) while the weight
+  // loads stay in flight. Up to 8 rows this took the launch from 44.3 / 47.0 to 43.0-43.9 /
+  // 44.8-44.9 us (1 / 8 rows), where a loop of load -> store per chunk waited out a round trip
+  // per chunk, the first behind the weights. The 12-wave launch for 9..16 rows keeps that loop
+  // (R = 0): staging 16 rows at once cost it its second workgroup per CU (108 VGPRs), and smaller
+  // batches measured 48.9-49.9 against 47.7 us.
+  const int chunks = k >> 3, nth = WAVES * kWave;
   uint4 wb[U];
+  if constexpr (R == 0) {
 #pragma unroll
-  for (int u = 0; u < U; ++u) wb[u] = ldg16(wp + 4 * min(u, steps - 1));
-  for (int i = threadIdx.x; i < m * (k >> 3); i += WAVES * kWave) {
-    const int t = i / (k >> 3), c = i % (k >> 3);
-    xt[t * xrow + c] = ldg16(x + int64_t(t) * xs + 8 * c);
+    for (int u = 0; u < U; ++u) wb[u] = ldg16(wp + 4 * min(u, steps - 1));
+    for (int i = threadIdx.x; i < m * chunks; i += nth)
+      xt[(i / chunks) * xrow + i % chunks] = ldg16(x + int64_t(i / chunks) * xs + 8 * (i % chunks));
+  } else {
+    // Loads without branches: rows past m re-read row m - 1 and chunks past the row re-read its
+    // last chunk (L2 hits); only the stores are guarded.
+    const int c = threadIdx.x, cc = min(c, chunks - 1);
+    uint4 xr[R];
+#pragma unroll
+    for (int t = 0; t < R; ++t) xr[t] = ldg16(x + int64_t(min(t, m - 1)) * xs + 8 * cc);
+#pragma unroll
+    for (int u = 0; u < U; ++u) wb[u] = ldg16(wp + 4 * min(u, steps - 1));
+#pragma unroll
+    for (int t = 0; t < R; ++t)
+      if (t < m && c < chunks) xt[t * xrow + c] = xr[t];
+    for (int i = c + nth; i < chunks; i += nth)  // K past 8 x threads
+      for (int t = 0; t < m; ++t) xt[t * xrow + i] = ldg16(x + int64_t(t) * xs + 8 * i);
   }
   __syncthreads();
 
@@ -193,11 +215,11 @@ extern "C" int edgerag_lm_head_argmax(const void* x, int64_t x_stride, int32_t m
   f16* lh = static_cast<f16*>(logits);
   uint64_t* part = static_cast<uint64_t*>(workspace);
   if (small)
-    hipLaunchKernelGGL((lm_head_kernel<kLmSmallWaves, kLmSmallU>), dim3(wgs),
+    hipLaunchKernelGGL((lm_head_kernel<kLmSmallWaves, kLmSmallU, kLmSmallM>), dim3(wgs),
                        dim3(kLmSmallWaves * kWave), lds, s, xh, x_stride, m, k, wh, vocab, lh,
                        logits_stride, part);
   else
-    hipLaunchKernelGGL((lm_head_kernel<kLmLargeWaves, kLmLargeU>), dim3(wgs),
+    hipLaunchKernelGGL((lm_head_kernel<kLmLargeWaves, kLmLargeU, 0>), dim3(wgs),
                        dim3(kLmLargeWaves * kWave), lds, s, xh, x_stride, m, k, wh, vocab, lh,
                        logits_stride, part);
   hipLaunchKernelGGL(lm_head_pick_kernel, dim3(m), dim3(256), 0, s,
