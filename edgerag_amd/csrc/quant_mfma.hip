@@ -1341,6 +1341,14 @@ void dispatch_stream_swiglu(const f16* x, int64_t xs, int32_t m, int32_t k, cons
     launch_stream_k<1, 2, 4, kEpiSwiglu>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
 }
 
+// The tiled GEMM's tile for M x N: the largest whose grid still covers the 256 CUs, 128x128,
+// else 128x64 (this test), else 64x64.
+inline bool gemm_tiles_128x64(int32_t m, int32_t n) {
+  const int64_t tn = (n + 127) / 128;
+  return tn * ((m + 127) / 128) < EDGERAG_GEMM_TARGET_WGS &&
+         tn * ((m + 63) / 64) >= EDGERAG_GEMM_TARGET_WGS;
+}
+
 template <int BITS>
 void dispatch(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
               const f16* scales, const f16* bias, int32_t n, int32_t g, f16* y, int64_t ys,
@@ -1363,10 +1371,12 @@ void dispatch(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* pac
     return;
   }
   // A remainder of at most 16 rows past a whole number of 64-row tiles (the decode tokens packed
-  // after a prefill chunk) would cost a mostly empty extra row of workgroups: it runs on the
-  // streaming (or skinny) path as a second launch instead.
+  // after a prefill chunk) runs on the streaming (or skinny) path as a second launch, where an
+  // extra row of 128x128 or 64x64 tiles would be mostly empty. 128x64 tiles (up to three
+  // workgroups per CU) take the extra row at almost no cost, less than a second pass over the
+  // weights (2048->6144, M = 519: 28.1 against 33.5 us; M = 512: 28.2).
   const int rem = m % 64;
-  if (rem > 0 && rem <= 16 && m - rem >= 128) {
+  if (rem > 0 && rem <= 16 && m - rem >= 128 && !gemm_tiles_128x64(m, n)) {
     dispatch<BITS>(x, xs, m - rem, k, packed, scales, bias, n, g, y, ys, s);
     dispatch<BITS>(x + int64_t(m - rem) * xs, xs, rem, k, packed, scales, bias, n, g,
                    y + int64_t(m - rem) * ys, ys, s);
@@ -1374,11 +1384,10 @@ void dispatch(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* pac
   }
   // Tiles: the largest whose grid still covers the 256 CUs.
   const int64_t t128 = int64_t((n + 127) / 128) * ((m + 127) / 128);
-  const int64_t t128x64 = int64_t((n + 127) / 128) * ((m + 63) / 64);
   if (t128 >= EDGERAG_GEMM_TARGET_WGS)
     launch_gemm<BITS, 128, 128, EDGERAG_GEMM_THREADS_128, EDGERAG_GEMM_STAGES_128>(
         x, xs, m, k, packed, scales, bias, n, g, y, ys, s);
-  else if (t128x64 >= EDGERAG_GEMM_TARGET_WGS)
+  else if (gemm_tiles_128x64(m, n))
     launch_gemm<BITS, 128, 64, EDGERAG_GEMM_THREADS_128x64, EDGERAG_GEMM_STAGES_128x64>(
         x, xs, m, k, packed, scales, bias, n, g, y, ys, s);
   else
@@ -1400,6 +1409,9 @@ void dispatch(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* pac
 // at least EDGERAG_SPLITK_MIN_STEPS steps, all splits equal).
 SplitPlan qlinear_split_plan(int32_t m, int32_t k, int32_t n, int32_t bits, int32_t g) {
   SplitPlan p{0, 0};
+  // At most 16 rows past whole 64-row tiles go to the streaming path (launch_qlinear_split): the
+  // plan covers the tiles.
+  if (m > EDGERAG_SKINNY_MAX_M && m % 64 > 0 && m % 64 <= 16 && m - m % 64 >= 128) m -= m % 64;
   if (m < 17 || n <= 0 || k % kBK != 0) return p;
   if ((bits != 8 && bits != 4) || g % 32 != 0) return p;
   const int64_t tiles = int64_t((n + kSplitTile - 1) / kSplitTile) *
@@ -1437,6 +1449,21 @@ SplitPlan qlinear_split_plan(int32_t m, int32_t k, int32_t n, int32_t bits, int3
 bool launch_qlinear_split(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
                           const f16* scales, const f16* bias, int32_t n, int32_t bits, int32_t g,
                           f16* y, int64_t ys, void* ws, int64_t ws_bytes, hipStream_t s) {
+  // As in dispatch: at most 16 rows past whole 64-row tiles run on the streaming path, the tiles
+  // on this route (8192->2048, M = 519: 47 against 53 us as one launch with a ninth tile row).
+  const int rem = m % 64;
+  if (m > EDGERAG_SKINNY_MAX_M && rem > 0 && rem <= 16 && m - rem >= 128) {
+    if (!launch_qlinear_split(x, xs, m - rem, k, packed, scales, bias, n, bits, g, y, ys, ws,
+                              ws_bytes, s))
+      return false;  // nothing launched: the caller runs the whole product on the plain path
+    if (bits == 8)
+      dispatch<8>(x + int64_t(m - rem) * xs, xs, rem, k, packed, scales, bias, n, g,
+                  y + int64_t(m - rem) * ys, ys, s);
+    else
+      dispatch<4>(x + int64_t(m - rem) * xs, xs, rem, k, packed, scales, bias, n, g,
+                  y + int64_t(m - rem) * ys, ys, s);
+    return true;
+  }
   const SplitPlan p = qlinear_split_plan(m, k, n, bits, g);
   if (p.splits < 1 ||
       (p.splits > 1 && (ws == nullptr || ws_bytes < p.bytes || !aligned16(ws))))  // float4 partials
