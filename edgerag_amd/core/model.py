@@ -215,6 +215,13 @@ class EdgeRagDecoder(nn.Module):
         partials = (torch.empty(T * 256, dtype=torch.float32, device=self.device) if fused
                     else None)
         xw = torch.empty_like(hidden) if fused else None  # fp16(norm weight * hidden)
+        # Larger batches run SiLU * up in the tiled GEMM's epilogue where the library covers the
+        # shape (the same bits as the projection and silu_mul apart).
+        gu0 = self.layers[0].gate_up
+        gemm_swiglu = (not stream_epi and isinstance(gu0, QuantLinear)
+                       and self.dtype == torch.float16
+                       and kernels.quant_swiglu_fused(T, gu0.in_features, gu0.out_features,
+                                                      gu0.config.bits, gu0.config.group_size))
         norm = None  # the normed input of the next q/k/v projection (None: x is normalised)
         for idx, layer in enumerate(self.layers):
             rope_append = layer.qkv.rope_append if stream_epi else partial(
@@ -244,7 +251,7 @@ class EdgeRagDecoder(nn.Module):
             o = layer.o_proj(attn_out.view(T, layer.q_out))
             x = kernels.rmsnorm(hidden, layer.post_attention_layernorm.weight, eps, delta=o,
                                 h_out=hidden)
-            act = (layer.gate_up.swiglu(x) if stream_epi
+            act = (layer.gate_up.swiglu(x) if stream_epi or gemm_swiglu
                    else LinearBase.swiglu(layer.gate_up, x))
             down = layer.down_proj(act)
             x = kernels.rmsnorm(hidden, next_norm, eps, delta=down, h_out=hidden)

@@ -834,7 +834,12 @@ struct SplitArgs {
   float* part;  // [tiles][splits][BN * BM] fp32 partial tiles
 };
 
-template <int BITS, int BN, int BM, bool PC, int NTH, int NS, bool SPLIT = false>
+// SWIGLU: the weight is [gate; up] (N = 2 I rows) and y is I wide: each wave's two 32-row tiles
+// hold 32 gate rows and the matching 32 up rows, and the epilogue writes fp16(silu(gate) * up)
+// with the roundings of the projection followed by silu_mul (one fp16 rounding of each
+// projection, of the SiLU, of the product).
+template <int BITS, int BN, int BM, bool PC, int NTH, int NS, bool SPLIT = false,
+          bool SWIGLU = false>
 __global__ __launch_bounds__(NTH, EDGERAG_GEMM_MIN_WG) void qlinear_gemm_kernel(
     const f16* __restrict__ x, int64_t xs, int32_t m, int32_t k,
     const uint8_t* __restrict__ packed, const f16* __restrict__ scales,
@@ -855,7 +860,19 @@ __global__ __launch_bounds__(NTH, EDGERAG_GEMM_MIN_WG) void qlinear_gemm_kernel(
   // of one row are adjacent lanes, so each global load instruction touches few cache lines.
   const int wr = tid / C::W_TPR, wseg = tid % C::W_TPR;
   const int xr = tid / C::X_TPR, xseg = tid % C::X_TPR;
-  const int wrow_g = min(nb + wr, n - 1);
+  // Weight row of tile row lr. SWIGLU: wave wn's rows 64 wn .. + 31 are gate rows (output
+  // columns nb2 + 32 wn ..) and 64 wn + 32 .. + 63 the matching up rows.
+  static_assert(!SWIGLU || (C::TN == 2 && !SPLIT), "SwiGLU pairs a wave's two 32-row tiles");
+  const int inter = n / 2, nb2 = int(blockIdx.x) * (BN / 2);
+  auto weight_row = [&](int lr) {
+    if constexpr (SWIGLU) {
+      const int c = min(nb2 + 32 * (lr / 64) + lr % 32, inter - 1);
+      return (lr / 32) % 2 == 0 ? c : inter + c;
+    } else {
+      return min(nb + lr, n - 1);
+    }
+  };
+  const int wrow_g = weight_row(wr);
   const uint8_t* wrow = packed + int64_t(wrow_g) * row_bytes + wseg * C::W_BPT;
   const f16* srow = scales + int64_t(wrow_g) * groups;
   const int wk_off = wseg * C::W_K;  // k offset of this thread's weight segment in a stage
@@ -917,7 +934,7 @@ __global__ __launch_bounds__(NTH, EDGERAG_GEMM_MIN_WG) void qlinear_gemm_kernel(
   __shared__ uint32_t ep_lds[BN];  // scale bits | bias bits << 16
   const uint16_t* scales16 = reinterpret_cast<const uint16_t*>(scales);
   const uint16_t* bias16 = reinterpret_cast<const uint16_t*>(bias);
-  const int ep_row = min(nb + (tid < BN ? tid : 0), n - 1);
+  const int ep_row = weight_row(tid < BN ? tid : 0);
   uint32_t ep_s = PC ? scales16[ep_row] : 0u;
   uint32_t ep_b = bias != nullptr ? bias16[ep_row] : 0u;
 
@@ -975,6 +992,49 @@ __global__ __launch_bounds__(NTH, EDGERAG_GEMM_MIN_WG) void qlinear_gemm_kernel(
   if (tid < BN) ep_lds[tid] = ep_s | (ep_b << 16);
   __syncthreads();
   const bool vec_out = (ys % 4) == 0 && (reinterpret_cast<uintptr_t>(y) & 7) == 0;
+  if constexpr (SWIGLU) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int lrow = wn * 64 + 8 * q + 4 * half;  // gate row in the tile
+      const int ncol = nb2 + wn * 32 + 8 * q + 4 * half;  // output column
+      float sg[4], bg[4], su[4], bu[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint32_t eg = ep_lds[lrow + r], eu = ep_lds[lrow + 32 + r];
+        sg[r] = float(__builtin_bit_cast(_Float16, uint16_t(eg & 0xFFFFu)));
+        bg[r] = float(__builtin_bit_cast(_Float16, uint16_t(eg >> 16)));
+        su[r] = float(__builtin_bit_cast(_Float16, uint16_t(eu & 0xFFFFu)));
+        bu[r] = float(__builtin_bit_cast(_Float16, uint16_t(eu >> 16)));
+      }
+#pragma unroll
+      for (int j = 0; j < C::TM; ++j) {
+        const int mrow = mb + wm * (32 * C::TM) + 32 * j + col;
+        if (mrow >= m) continue;
+        f16* yr = y + int64_t(mrow) * ys;
+        _Float16 o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float vg = PC ? sg[r] * acc[0][j][4 * q + r] + bg[r] : acc[0][j][4 * q + r] + bg[r];
+          float vu = PC ? su[r] * acc[1][j][4 * q + r] + bu[r] : acc[1][j][4 * q + r] + bu[r];
+          // The fp32 results first, then fp16, as the plain epilogue rounds them (left alone, the
+          // compiler fuses each into one v_fma_mixlo_f16, which rounds once and can differ).
+          asm volatile("" : "+v"(vg), "+v"(vu));
+          const float gr = __half2float(__float2half_rn(vg));
+          const float ur = __half2float(__float2half_rn(vu));
+          o[r] = __builtin_bit_cast(_Float16, __float2half_rn(silu_rounded_f16(gr) * ur));
+        }
+        if (vec_out && ncol + 3 < inter) {
+          const h2 lo = {o[0], o[1]}, hi = {o[2], o[3]};
+          *reinterpret_cast<uint2*>(yr + ncol) = uint2{as_u32(lo), as_u32(hi)};
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (ncol + r < inter) yr[ncol + r] = __builtin_bit_cast(f16, o[r]);
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < C::TN; ++i) {
 #pragma unroll
@@ -1071,6 +1131,19 @@ void launch_gemm(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* 
   else
     hipLaunchKernelGGL((qlinear_gemm_kernel<BITS, BN, BM, false, NTH, NS>), grid, dim3(NTH), 0, s,
                        x, xs, m, k, packed, scales, bias, n, g, y, ys, none);
+}
+
+// SwiGLU GEMM: 128 weight rows per tile (64 gate + 64 up), so the grid covers I = N / 2 output
+// columns 64 at a time: the same workgroups and k order as the plain launch of the [gate; up]
+// weight with BN = 128.
+template <int BM, int NTH, int NS>
+void launch_gemm_swiglu(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
+                        const f16* scales, const f16* bias, int32_t n, f16* y, int64_t ys,
+                        hipStream_t s) {
+  const dim3 grid(unsigned((n / 2 + 63) / 64), unsigned((m + BM - 1) / BM));
+  const SplitArgs none{nullptr};
+  hipLaunchKernelGGL((qlinear_gemm_kernel<8, 128, BM, true, NTH, NS, false, true>), grid,
+                     dim3(NTH), 0, s, x, xs, m, k, packed, scales, bias, n, k, y, ys, none);
 }
 
 // Split-K launches use 64x64 tiles: the tile grid alone would leave CUs idle.
@@ -1323,9 +1396,52 @@ void dispatch_stream_residual(const f16* x, int64_t xs, int32_t m, int32_t k,
 // The streaming shapes with two row tiles of one k-slice: the only ones the SwiGLU form covers.
 // dispatch_stream picks exactly these for the same (M, K, N), so the fused launch computes the
 // same gate and up bits as the plain one.
+// The tiled GEMM's tile for M x N: the largest whose grid still covers the 256 CUs, 128x128,
+// else 128x64 (this test), else 64x64.
+inline bool gemm_tiles_128x64(int32_t m, int32_t n) {
+  const int64_t tn = (n + 127) / 128;
+  return tn * ((m + 127) / 128) < EDGERAG_GEMM_TARGET_WGS &&
+         tn * ((m + 63) / 64) >= EDGERAG_GEMM_TARGET_WGS;
+}
+
 bool stream_swiglu_shape(int32_t m, int32_t k, int32_t n) {
   return m <= EDGERAG_STREAM_MAX_M && stream_slices(m, k, n) == 1 && n % 2 == 0 &&
          (int64_t(n) + 15) / 16 >= EDGERAG_STREAM_NT2_TILES;
+}
+
+// The tiled GEMM with the SwiGLU epilogue (per-channel INT8, M > 64) where the plain launch of
+// the [gate; up] weight uses 128-row weight tiles (128x128 or 128x64), so that the fused launch
+// sums every output in the plain launch's order; a remainder the plain launch hands to the
+// streaming path goes to the streaming SwiGLU kernel.
+bool gemm_swiglu_shape(int32_t m, int32_t k, int32_t n) {
+  if (m <= EDGERAG_SKINNY_MAX_M || n % 2 != 0 || k % kBK != 0) return false;
+  const int rem = m % 64;
+  if (rem > 0 && rem <= 16 && m - rem >= 128 && !gemm_tiles_128x64(m, n))
+    return gemm_swiglu_shape(m - rem, k, n) && stream_swiglu_shape(rem, k, n);
+  return int64_t((n + 127) / 128) * ((m + 127) / 128) >= EDGERAG_GEMM_TARGET_WGS ||
+         gemm_tiles_128x64(m, n);
+}
+
+void dispatch_stream_swiglu(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
+                            const f16* scales, const f16* bias, int32_t n, f16* y, int64_t ys,
+                            const EpiArgs& ea, hipStream_t s);
+
+void dispatch_gemm_swiglu(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
+                          const f16* scales, const f16* bias, int32_t n, f16* y, int64_t ys,
+                          hipStream_t s) {
+  const int rem = m % 64;
+  if (rem > 0 && rem <= 16 && m - rem >= 128 && !gemm_tiles_128x64(m, n)) {
+    dispatch_gemm_swiglu(x, xs, m - rem, k, packed, scales, bias, n, y, ys, s);
+    dispatch_stream_swiglu(x + int64_t(m - rem) * xs, xs, rem, k, packed, scales, bias, n,
+                           y + int64_t(m - rem) * ys, ys, EpiArgs{}, s);
+    return;
+  }
+  if (int64_t((n + 127) / 128) * ((m + 127) / 128) >= EDGERAG_GEMM_TARGET_WGS)
+    launch_gemm_swiglu<128, EDGERAG_GEMM_THREADS_128, EDGERAG_GEMM_STAGES_128>(
+        x, xs, m, k, packed, scales, bias, n, y, ys, s);
+  else
+    launch_gemm_swiglu<64, EDGERAG_GEMM_THREADS_128x64, EDGERAG_GEMM_STAGES_128x64>(
+        x, xs, m, k, packed, scales, bias, n, y, ys, s);
 }
 
 void dispatch_stream_swiglu(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
@@ -1339,14 +1455,6 @@ void dispatch_stream_swiglu(const f16* x, int64_t xs, int32_t m, int32_t k, cons
     launch_stream_k<1, 2, 2, kEpiSwiglu>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
   else
     launch_stream_k<1, 2, 4, kEpiSwiglu>(x, xs, m, k, packed, scales, bias, n, y, ys, s);
-}
-
-// The tiled GEMM's tile for M x N: the largest whose grid still covers the 256 CUs, 128x128,
-// else 128x64 (this test), else 64x64.
-inline bool gemm_tiles_128x64(int32_t m, int32_t n) {
-  const int64_t tn = (n + 127) / 128;
-  return tn * ((m + 127) / 128) < EDGERAG_GEMM_TARGET_WGS &&
-         tn * ((m + 63) / 64) >= EDGERAG_GEMM_TARGET_WGS;
 }
 
 template <int BITS>
@@ -1535,13 +1643,16 @@ void launch_qlinear_rope(const f16* x, int64_t xs, int32_t m, int32_t k, const u
 bool qlinear_swiglu_supported(int32_t m, int32_t k, int32_t n, int32_t bits, int32_t g,
                               const void* x, int64_t x_stride, const void* packed) {
   return bits == 8 && g == k && qlinear_mfma_supported(k, bits, g, x, x_stride, packed) &&
-         stream_swiglu_shape(m, k, n);
+         (stream_swiglu_shape(m, k, n) || gemm_swiglu_shape(m, k, n));
 }
 
 void launch_qlinear_swiglu(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
                            const f16* scales, const f16* bias, int32_t n, f16* y, int64_t ys,
                            const EpiArgs& ea, hipStream_t s) {
-  dispatch_stream_swiglu(x, xs, m, k, packed, scales, bias, n, y, ys, ea, s);
+  if (stream_swiglu_shape(m, k, n))
+    dispatch_stream_swiglu(x, xs, m, k, packed, scales, bias, n, y, ys, ea, s);
+  else
+    dispatch_gemm_swiglu(x, xs, m, k, packed, scales, bias, n, y, ys, s);
 }
 
 int qlinear_residual_parts(int32_t m, int32_t k, int32_t n, int32_t bits, int32_t g,

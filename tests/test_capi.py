@@ -54,14 +54,18 @@ def test_measurement_probes_live_in_a_bench_only_library() -> None:
 
 def test_swiglu_support_query() -> None:
     """The fused SwiGLU linear covers decode batches of wide INT8 per-channel [gate; up]
-    weights (normed inputs up to 16 tokens); the query answers without touching a GPU."""
+    weights (normed inputs up to 16 tokens) and prefill slices whose plain launch takes 128-row
+    weight tiles; the query answers without touching a GPU."""
     q = _lib.load().edgerag_quant_linear_swiglu_supported
     F16, F32 = 1, 0
     assert q(F16, 8, 2048, 16384, 8, 2048, 0) == 1  # config 5's gate/up, a decode batch
     assert q(F16, 8, 2048, 16384, 8, 2048, 1) == 1  # ... with the RMSNorm folded in
     assert q(F16, 64, 2048, 16384, 8, 2048, 0) == 1
     assert q(F16, 17, 2048, 16384, 8, 2048, 1) == 0  # normed: at most 16 tokens
-    assert q(F16, 65, 2048, 16384, 8, 2048, 0) == 0  # prefill-sized M
+    assert q(F16, 65, 2048, 16384, 8, 2048, 0) == 1  # prefill slices: the tiled GEMM
+    assert q(F16, 519, 2048, 16384, 8, 2048, 0) == 1  # a chunk + 7 decode rows
+    assert q(F16, 65, 2048, 16384, 8, 2048, 1) == 0  # normed: at most 16 tokens
+    assert q(F16, 80, 1024, 2048, 8, 1024, 0) == 0  # 64x64 tiles: gate and up in other waves
     assert q(F16, 0, 2048, 16384, 8, 2048, 0) == 0
     assert q(F16, 8, 2048, 4096, 8, 2048, 0) == 0  # one 16-row tile per workgroup
     assert q(F16, 8, 2048, 16383, 8, 2048, 0) == 0  # odd N: no [gate; up] split

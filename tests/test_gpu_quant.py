@@ -248,9 +248,42 @@ def test_quant_linear_rope_append_fused(device, n_q, n_kv, d, k, with_bias) -> N
         assert torch.all(kc.reshape(n_kv, nb * bs, d)[:, untouched] == 7.0)
 
 
+@pytest.mark.parametrize("k,n,ms", [
+    (2048, 16384, (65, 128, 200, 512, 519, 544)),
+    (2048, 6144, (384, 512, 519, 544)),   # 128x64 tiles from 6 tile rows (M > 320) on
+    (1152, 8192, (320, 512, 519, 544)),
+])
+def test_quant_linear_swiglu_tiled_gemm(device, k, n, ms) -> None:
+    """SwiGLU in the tiled GEMM's epilogue (prefill slices, M > 64, weights whose plain launch
+    takes 128-row tiles: 128x128 for 2048 -> 16384 and 1152 -> 8192 at M = 512, 128x64 for
+    2048 -> 6144): bit-identical to the projection followed by silu_mul, including M = 519
+    (512 chunk tokens + 7 decode rows: the remainder on the streaming SwiGLU kernel where the
+    plain launch streams it too) and M = 544; within the linear tolerance of the oracle."""
+    w = _weight(n, k, n + 5 * k)
+    cfg = oq.QuantConfig(k, 8)
+    packed, scales = oq.quantize_for_layer(w, cfg)
+    bias = (torch.randn(n, generator=seeded(n + k)) * 0.1).half()
+    inter = n // 2
+    pd, sd, bd = packed.to(device), scales.to(device), bias.to(device)
+    for m in ms:
+        assert kernels.quant_swiglu_fused(m, k, n, 8, k)
+        x = torch.randn(m, k, generator=seeded(m * 31 + k)).half()
+        xd = x.to(device)
+        fused = kernels.quant_linear_swiglu(xd, pd, sd, bd, k, n, 8, k)
+        gu = kernels.quant_linear(xd, pd, sd, bd, k, n, 8, k, split_k=False)
+        plain = kernels.silu_mul(gu, inter)
+        assert fused.shape == (m, inter)
+        assert torch.equal(fused, plain), f"M={m}: fused SwiGLU differs from projection + silu_mul"
+        if m == ms[0]:
+            ref_gu = oq.quant_linear_reference(x, packed, scales, bias, k, cfg)
+            ref = torch.nn.functional.silu(ref_gu[:, :inter]) * ref_gu[:, inter:]
+            torch.testing.assert_close(fused.float().cpu(), ref, **LINEAR_TOL)
+
+
 def test_quant_linear_swiglu_falls_back_outside_its_shapes(device) -> None:
-    """Shapes the fused launch does not cover (M > 64, N below two tiles per workgroup, INT4)
-    run as projection + silu_mul through the same entry, and the C entry point says why."""
+    """Shapes the fused launch does not cover (M > 64 on a weight whose plain launch takes
+    64x64 tiles, N below two tiles per workgroup, INT4) run as projection + silu_mul through the
+    same entry, and the C entry point says why."""
     k, n = 1024, 2048
     w = _weight(n, k, 77)
     for bits, g, m in ((8, k, 4), (8, k, 80), (4, 128, 4)):
