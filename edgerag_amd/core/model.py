@@ -81,6 +81,8 @@ class DecoderLayer(nn.Module):
 class EdgeRagDecoder(nn.Module):
     # Largest batch whose q/k/v and gate/up projections use the fused streaming epilogues.
     STREAM_EPILOGUE_MAX_TOKENS = 32
+    # Smallest batch whose q/k/v and gate/up projections use the tiled GEMM's fused epilogues.
+    TILED_EPILOGUE_MIN_TOKENS = 65
 
     def __init__(
         self,
@@ -206,8 +208,12 @@ class EdgeRagDecoder(nn.Module):
         # The fused streaming epilogues (q/k/v + RoPE + append, gate/up + SiLU * up) serve batches
         # of up to 32 tokens; larger batches run the tiled GEMM and the elementwise launch apart,
         # which is faster there.
+        # Batches past 64 tokens run the tiled GEMM, whose epilogues take RoPE + append and
+        # SiLU * up where the library covers the shape (the same bits as the elementwise launches
+        # apart); batches of 33-64 tokens run the projection and the elementwise launch apart.
         stream_epi = T <= self.STREAM_EPILOGUE_MAX_TOKENS
-        if stream_epi and isinstance(qkv0, QuantLinear) and kernels.quant_rope_fused(
+        tiled_epi = T >= self.TILED_EPILOGUE_MIN_TOKENS
+        if (stream_epi or tiled_epi) and isinstance(qkv0, QuantLinear) and kernels.quant_rope_fused(
                 T, qkv0.in_features, qkv0.config.bits, qkv0.config.group_size, spec.n_q_heads,
                 spec.n_kv_heads, d, self.dtype):
             rows = kernels.rope_rows(step.positions, self.rotary.cos, self.rotary.sin)
@@ -215,16 +221,15 @@ class EdgeRagDecoder(nn.Module):
         partials = (torch.empty(T * 256, dtype=torch.float32, device=self.device) if fused
                     else None)
         xw = torch.empty_like(hidden) if fused else None  # fp16(norm weight * hidden)
-        # Larger batches run SiLU * up in the tiled GEMM's epilogue where the library covers the
-        # shape (the same bits as the projection and silu_mul apart).
         gu0 = self.layers[0].gate_up
-        gemm_swiglu = (not stream_epi and isinstance(gu0, QuantLinear)
+        gemm_swiglu = (tiled_epi and isinstance(gu0, QuantLinear)
                        and self.dtype == torch.float16
                        and kernels.quant_swiglu_fused(T, gu0.in_features, gu0.out_features,
                                                       gu0.config.bits, gu0.config.group_size))
+        gemm_rope = tiled_epi and rows is not None
         norm = None  # the normed input of the next q/k/v projection (None: x is normalised)
         for idx, layer in enumerate(self.layers):
-            rope_append = layer.qkv.rope_append if stream_epi else partial(
+            rope_append = layer.qkv.rope_append if stream_epi or gemm_rope else partial(
                 LinearBase.rope_append, layer.qkv)
             rope_append(xw if norm is not None else x, step.positions, self.rotary.cos,
                         self.rotary.sin, spec.n_q_heads, spec.n_kv_heads, d, step.slots,

@@ -830,21 +830,31 @@ __device__ __forceinline__ void gemm_store_x(const GemmStage<C>& st, int i, _Flo
 // SPLIT: blockIdx.z is one of gridDim.z equal k ranges (split K). The workgroup writes its fp32
 // partial tile to sk.part and stops; qlinear_split_reduce_kernel, the next launch on the stream,
 // adds the partials in split order and applies the epilogue.
-struct SplitArgs {
+// By value to every tiled-GEMM launch: the split partials, or the RoPE epilogue's operands.
+struct GemmArgs {
   float* part;  // [tiles][splits][BN * BM] fp32 partial tiles
+  EpiArgs ea;
 };
+// Epilogues of the tiled GEMM: y = the projection; SiLU(gate) * up; or q / k with RoPE and k / v
+// appended to the pools (the RoPE epilogue writes no y).
+constexpr int kGemmPlain = 0, kGemmSwiglu = 1, kGemmRope = 2;
 
-// SWIGLU: the weight is [gate; up] (N = 2 I rows) and y is I wide: each wave's two 32-row tiles
-// hold 32 gate rows and the matching 32 up rows, and the epilogue writes fp16(silu(gate) * up)
-// with the roundings of the projection followed by silu_mul (one fp16 rounding of each
-// projection, of the SiLU, of the product).
+// GEPI kGemmSwiglu: the weight is [gate; up] (N = 2 I rows) and y is I wide: each wave's two
+// 32-row tiles hold 32 gate rows and the matching 32 up rows, and the epilogue writes
+// fp16(silu(gate) * up) with the roundings of the projection followed by silu_mul (one fp16
+// rounding of each projection, of the SiLU, of the product).
+// GEPI kGemmRope: the weight is [q; k; v] with head_dim 64, so each wave's 64 rows are one head,
+// dims 0..31 in its first tile and 32..63 in its second: the rotate_half partner of every value
+// is in the same lane. The epilogue rounds the projection to fp16 as the plain launch does, then
+// writes q with RoPE to ea.q_out and k with RoPE / v to the pools at each token's slot, with the
+// arithmetic of rope_append.
 template <int BITS, int BN, int BM, bool PC, int NTH, int NS, bool SPLIT = false,
-          bool SWIGLU = false>
+          int GEPI = kGemmPlain>
 __global__ __launch_bounds__(NTH, EDGERAG_GEMM_MIN_WG) void qlinear_gemm_kernel(
     const f16* __restrict__ x, int64_t xs, int32_t m, int32_t k,
     const uint8_t* __restrict__ packed, const f16* __restrict__ scales,
     const f16* __restrict__ bias, int32_t n, int32_t g, f16* __restrict__ y, int64_t ys,
-    SplitArgs sk) {
+    GemmArgs sk) {
   using C = GemmCfg<BITS, BN, BM, NTH>;
   static_assert(NS % 2 == 0, "the register ring must keep the LDS buffer parity of a step");
   constexpr int NWC = C::W_K / 8, NXC = C::X_BPT / 16;  // LDS chunks this thread stages per step
@@ -860,12 +870,13 @@ __global__ __launch_bounds__(NTH, EDGERAG_GEMM_MIN_WG) void qlinear_gemm_kernel(
   // of one row are adjacent lanes, so each global load instruction touches few cache lines.
   const int wr = tid / C::W_TPR, wseg = tid % C::W_TPR;
   const int xr = tid / C::X_TPR, xseg = tid % C::X_TPR;
-  // Weight row of tile row lr. SWIGLU: wave wn's rows 64 wn .. + 31 are gate rows (output
+  // Weight row of tile row lr. kGemmSwiglu: wave wn's rows 64 wn .. + 31 are gate rows (output
   // columns nb2 + 32 wn ..) and 64 wn + 32 .. + 63 the matching up rows.
-  static_assert(!SWIGLU || (C::TN == 2 && !SPLIT), "SwiGLU pairs a wave's two 32-row tiles");
+  static_assert(GEPI == kGemmPlain || (C::TN == 2 && !SPLIT),
+                "the SwiGLU / RoPE epilogues pair a wave's two 32-row tiles");
   const int inter = n / 2, nb2 = int(blockIdx.x) * (BN / 2);
   auto weight_row = [&](int lr) {
-    if constexpr (SWIGLU) {
+    if constexpr (GEPI == kGemmSwiglu) {
       const int c = min(nb2 + 32 * (lr / 64) + lr % 32, inter - 1);
       return (lr / 32) % 2 == 0 ? c : inter + c;
     } else {
@@ -992,7 +1003,7 @@ __global__ __launch_bounds__(NTH, EDGERAG_GEMM_MIN_WG) void qlinear_gemm_kernel(
   if (tid < BN) ep_lds[tid] = ep_s | (ep_b << 16);
   __syncthreads();
   const bool vec_out = (ys % 4) == 0 && (reinterpret_cast<uintptr_t>(y) & 7) == 0;
-  if constexpr (SWIGLU) {
+  if constexpr (GEPI == kGemmSwiglu) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int lrow = wn * 64 + 8 * q + 4 * half;  // gate row in the tile
@@ -1030,6 +1041,88 @@ __global__ __launch_bounds__(NTH, EDGERAG_GEMM_MIN_WG) void qlinear_gemm_kernel(
 #pragma unroll
           for (int r = 0; r < 4; ++r)
             if (ncol + r < inter) yr[ncol + r] = __builtin_bit_cast(f16, o[r]);
+        }
+      }
+    }
+    return;
+  }
+  if constexpr (GEPI == kGemmRope) {
+    const EpiArgs& ea = sk.ea;
+    const int head = nb / 64 + wn;  // 64 rows per wave: one head
+    const int heads = n / 64, nq = ea.n_q_heads, nkv = ea.n_kv_heads;
+    const int64_t pool_rows = int64_t(ea.num_blocks) * ea.block_size;
+    if (head >= heads) return;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int d0 = 8 * q + 4 * half;  // dims d0 .. d0 + 3 (first tile), + 32 (second tile)
+      float sc[2][4], bv[2][4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t e = ep_lds[wn * 64 + 32 * i + d0 + r];
+          sc[i][r] = float(__builtin_bit_cast(_Float16, uint16_t(e & 0xFFFFu)));
+          bv[i][r] = float(__builtin_bit_cast(_Float16, uint16_t(e >> 16)));
+        }
+#pragma unroll
+      for (int j = 0; j < C::TM; ++j) {
+        const int mrow = mb + wm * (32 * C::TM) + 32 * j + col;
+        if (mrow >= m) continue;
+        // The projection rounded to fp16 as the plain epilogue rounds it (fp32 first).
+        float v[2][4];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float t = PC ? sc[i][r] * acc[i][j][4 * q + r] + bv[i][r] : acc[i][j][4 * q + r] + bv[i][r];
+            asm volatile("" : "+v"(t));
+            v[i][r] = __half2float(__float2half_rn(t));
+          }
+        f16 o[2][4];
+        if (head < nq + nkv) {  // q or k: RoPE
+          const f16* ct = ea.cos_tok + int64_t(mrow) * 64;
+          const f16* st = ea.sin_tok + int64_t(mrow) * 64;
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int d = 32 * i + d0 + r;
+              // One element at a time: paired across the two tiles, the vectoriser forms
+              // two-float vector negations this target cannot select without packed fp32 ops.
+              float own = v[i][r], partner = v[1 - i][r];
+              asm volatile("" : "+v"(own), "+v"(partner));
+              o[i][r] = rope_elem(own, partner, i == 1, __half2float(ct[d]), __half2float(st[d]));
+            }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[i][r] = __float2half_rn(v[i][r]);
+        }
+        f16* dst;
+        if (head < nq) {
+          dst = ea.q_out + int64_t(mrow) * ea.q_st + int64_t(head) * 64;
+        } else {
+          const int64_t slot = ea.slots[mrow];
+          if (slot < 0 || slot >= pool_rows) continue;
+          const int kvh = head < nq + nkv ? head - nq : head - nq - nkv;
+          dst = (head < nq + nkv ? ea.kpool : ea.vpool) +
+                ((int64_t(kvh) * ea.num_blocks + slot / ea.block_size) * ea.block_size +
+                 slot % ea.block_size) * 64;
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          f16* p = dst + 32 * i + d0;
+          if ((reinterpret_cast<uintptr_t>(p) & 7) == 0) {
+            const h2 lo = {__builtin_bit_cast(_Float16, o[i][0]),
+                           __builtin_bit_cast(_Float16, o[i][1])};
+            const h2 hi = {__builtin_bit_cast(_Float16, o[i][2]),
+                           __builtin_bit_cast(_Float16, o[i][3])};
+            *reinterpret_cast<uint2*>(p) = uint2{as_u32(lo), as_u32(hi)};
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) p[r] = o[i][r];
+          }
         }
       }
     }
@@ -1124,7 +1217,7 @@ void launch_gemm(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* 
                  const f16* scales, const f16* bias, int32_t n, int32_t g, f16* y, int64_t ys,
                  hipStream_t s) {
   const dim3 grid(unsigned((n + BN - 1) / BN), unsigned((m + BM - 1) / BM));
-  const SplitArgs none{nullptr};
+  const GemmArgs none{nullptr};
   if (BITS == 8 && g == k)
     hipLaunchKernelGGL((qlinear_gemm_kernel<BITS, BN, BM, BITS == 8, NTH, NS>), grid, dim3(NTH),
                        0, s, x, xs, m, k, packed, scales, bias, n, g, y, ys, none);
@@ -1141,9 +1234,21 @@ void launch_gemm_swiglu(const f16* x, int64_t xs, int32_t m, int32_t k, const ui
                         const f16* scales, const f16* bias, int32_t n, f16* y, int64_t ys,
                         hipStream_t s) {
   const dim3 grid(unsigned((n / 2 + 63) / 64), unsigned((m + BM - 1) / BM));
-  const SplitArgs none{nullptr};
-  hipLaunchKernelGGL((qlinear_gemm_kernel<8, 128, BM, true, NTH, NS, false, true>), grid,
+  const GemmArgs none{nullptr};
+  hipLaunchKernelGGL((qlinear_gemm_kernel<8, 128, BM, true, NTH, NS, false, kGemmSwiglu>), grid,
                      dim3(NTH), 0, s, x, xs, m, k, packed, scales, bias, n, k, y, ys, none);
+}
+
+// RoPE GEMM: the plain launch's 128-row weight tiles (two 64-dim heads per workgroup); writes q
+// to ea.q_out and k / v to the pools, no y.
+template <int BM, int NTH, int NS>
+void launch_gemm_rope(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
+                      const f16* scales, const f16* bias, int32_t n, const EpiArgs& ea,
+                      hipStream_t s) {
+  const dim3 grid(unsigned((n + 127) / 128), unsigned((m + BM - 1) / BM));
+  const GemmArgs ga{nullptr, ea};
+  hipLaunchKernelGGL((qlinear_gemm_kernel<8, 128, BM, true, NTH, NS, false, kGemmRope>), grid,
+                     dim3(NTH), 0, s, x, xs, m, k, packed, scales, bias, n, k, nullptr, 0, ga);
 }
 
 // Split-K launches use 64x64 tiles: the tile grid alone would leave CUs idle.
@@ -1210,7 +1315,7 @@ void launch_gemm_split(const f16* x, int64_t xs, int32_t m, int32_t k, const uin
   const dim3 grid(unsigned(tiles_x), unsigned((m + kSplitTile - 1) / kSplitTile),
                   unsigned(p.splits));
   float* part = static_cast<float*>(ws);
-  const SplitArgs sk{part};
+  const GemmArgs sk{part};
   constexpr int T = kSplitTile;
   const bool pc = BITS == 8 && g == k;
   if (pc)
@@ -1611,6 +1716,21 @@ bool stream_rope_shape(int32_t m, int32_t k, int32_t n, int32_t heads, int32_t h
   return stream_waves(1, nt, mt, k).kw <= 8;
 }
 
+// The tiled GEMM with the RoPE epilogue (per-channel INT8, M > 64, head_dim 64) where the plain
+// launch of the [q; k; v] weight uses 128-row weight tiles; a remainder the plain launch hands
+// to the streaming path goes to the streaming RoPE kernel.
+bool gemm_rope_shape(int32_t m, int32_t k, int32_t n, int32_t heads, int32_t head_dim) {
+  if (head_dim != 64 || int64_t(heads) * head_dim != n || m <= EDGERAG_SKINNY_MAX_M ||
+      k % kBK != 0)
+    return false;
+  const int rem = m % 64;
+  if (rem > 0 && rem <= 16 && m - rem >= 128 && !gemm_tiles_128x64(m, n))
+    return gemm_rope_shape(m - rem, k, n, heads, head_dim) &&
+           stream_rope_shape(rem, k, n, heads, head_dim);
+  return int64_t((n + 127) / 128) * ((m + 127) / 128) >= EDGERAG_GEMM_TARGET_WGS ||
+         gemm_tiles_128x64(m, n);
+}
+
 template <int MT, bool NORM = false>
 void launch_rope(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
                  const f16* scales, const f16* bias, int32_t n, const EpiArgs& ea,
@@ -1624,12 +1744,33 @@ bool qlinear_rope_supported(int32_t m, int32_t k, int32_t n, int32_t bits, int32
                             int32_t heads, int32_t head_dim, const void* x, int64_t x_stride,
                             const void* packed) {
   return bits == 8 && g == k && qlinear_mfma_supported(k, bits, g, x, x_stride, packed) &&
-         stream_rope_shape(m, k, n, heads, head_dim);
+         (stream_rope_shape(m, k, n, heads, head_dim) ||
+          gemm_rope_shape(m, k, n, heads, head_dim));
 }
 
 void launch_qlinear_rope(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
                          const f16* scales, const f16* bias, int32_t n, const EpiArgs& ea,
                          hipStream_t s) {
+  if (!stream_rope_shape(m, k, n, ea.n_q_heads + 2 * ea.n_kv_heads, ea.head_dim)) {
+    const int rem = m % 64;
+    if (rem > 0 && rem <= 16 && m - rem >= 128 && !gemm_tiles_128x64(m, n)) {
+      launch_qlinear_rope(x, xs, m - rem, k, packed, scales, bias, n, ea, s);
+      const int t0 = m - rem;
+      EpiArgs er = ea;
+      er.cos_tok += int64_t(t0) * ea.head_dim;
+      er.sin_tok += int64_t(t0) * ea.head_dim;
+      er.slots += t0;
+      er.q_out += int64_t(t0) * ea.q_st;
+      launch_qlinear_rope(x + int64_t(t0) * xs, xs, rem, k, packed, scales, bias, n, er, s);
+    } else if (int64_t((n + 127) / 128) * ((m + 127) / 128) >= EDGERAG_GEMM_TARGET_WGS) {
+      launch_gemm_rope<128, EDGERAG_GEMM_THREADS_128, EDGERAG_GEMM_STAGES_128>(
+          x, xs, m, k, packed, scales, bias, n, ea, s);
+    } else {
+      launch_gemm_rope<64, EDGERAG_GEMM_THREADS_128x64, EDGERAG_GEMM_STAGES_128x64>(
+          x, xs, m, k, packed, scales, bias, n, ea, s);
+    }
+    return;
+  }
   if (ea.norm_part != nullptr)  // normed input: decode batches of up to 16 tokens
     launch_rope<1, true>(x, xs, m, k, packed, scales, bias, n, ea, s);
   else if (m <= 16)

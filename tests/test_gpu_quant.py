@@ -248,6 +248,56 @@ def test_quant_linear_rope_append_fused(device, n_q, n_kv, d, k, with_bias) -> N
         assert torch.all(kc.reshape(n_kv, nb * bs, d)[:, untouched] == 7.0)
 
 
+@pytest.mark.parametrize("n_q,n_kv,k,ms", [
+    (32, 32, 2048, (384, 512, 519, 544)),  # config 5's q/k/v: 128x64 tiles
+    (48, 16, 2048, (512, 519)),            # GQA: q / k / v boundaries between workgroups' heads
+    (64, 64, 1024, (200, 512, 519, 544)),  # 128x128 tiles from M = 257; M = 519 streams 7 rows
+])
+def test_quant_linear_rope_append_tiled_gemm(device, n_q, n_kv, k, ms) -> None:
+    """q/k/v projection + RoPE + KV append in the tiled GEMM's epilogue (prefill slices, M > 64,
+    head_dim 64, weights whose plain launch takes 128-row tiles): each wave's 64 rows are one
+    head, so every rotate_half partner is in the same lane. q_out and both pools bit-identical to
+    quant_linear followed by rope_append; padding and out-of-pool slots leave the pools alone."""
+    from edgerag_amd.core.layers import RotaryTable
+
+    d = 64
+    n = (n_q + 2 * n_kv) * d
+    w = _weight(n, k, n + 3 * k)
+    cfg = oq.QuantConfig(k, 8)
+    packed, scales = oq.quantize_for_layer(w, cfg)
+    bias = (torch.randn(n, generator=seeded(n + 3)) * 0.1).half()
+    pd, sd, bd = packed.to(device), scales.to(device), bias.to(device)
+    bs, nb = 16, 64
+    table = RotaryTable(d, 130000.0, 8192, device, torch.float16)
+    for m in ms:
+        assert kernels.quant_rope_fused(m, k, 8, k, n_q, n_kv, d), f"M={m}"
+        g = seeded(m * 11 + n_q)
+        x = torch.randn(m, k, generator=g).half().to(device)
+        positions = torch.randint(0, 8192, (m,), generator=g, dtype=torch.int32)
+        slots = torch.randperm(nb * bs, generator=g)[:m].to(torch.int32)
+        slots[0] = -1
+        slots[m - 1] = nb * bs + 5  # past the pool (a remainder row at M = 519)
+        pos_d, slots_d = positions.to(device), slots.to(device)
+        rows = kernels.rope_rows(pos_d, table.cos, table.sin)
+        pools, qs = [], []
+        for use_rows in (rows, None):  # fused launch, then the two-launch path
+            kp = torch.full((n_kv, nb, bs, d), 7.0, dtype=torch.float16, device=device)
+            vp = torch.full_like(kp, -3.0)
+            q = kernels.quant_linear_rope_append(
+                x, pd, sd, bd, k, 8, k, pos_d, table.cos, table.sin, n_q, n_kv, d, slots_d, kp, vp,
+                rows=use_rows)
+            qs.append(q)
+            pools.append((kp, vp))
+        assert torch.equal(qs[0], qs[1]), f"M={m}: q differs from the two-launch path"
+        assert torch.equal(pools[0][0], pools[1][0]), f"M={m}: key pool differs"
+        assert torch.equal(pools[0][1], pools[1][1]), f"M={m}: value pool differs"
+        vc = pools[0][1].cpu()
+        valid = [int(s_) for s_ in slots if 0 <= int(s_) < nb * bs]
+        untouched = torch.ones(nb * bs, dtype=torch.bool)
+        untouched[valid] = False
+        assert torch.all(vc.reshape(n_kv, nb * bs, d)[:, untouched] == -3.0)
+
+
 @pytest.mark.parametrize("k,n,ms", [
     (2048, 16384, (65, 128, 200, 512, 519, 544)),
     (2048, 6144, (384, 512, 519, 544)),   # 128x64 tiles from 6 tile rows (M > 320) on
