@@ -1052,63 +1052,69 @@ __global__ __launch_bounds__(NTH, EDGERAG_GEMM_MIN_WG) void qlinear_gemm_kernel(
     const int heads = n / 64, nq = ea.n_q_heads, nkv = ea.n_kv_heads;
     const int64_t pool_rows = int64_t(ea.num_blocks) * ea.block_size;
     if (head >= heads) return;
+    const bool rotate = head < nq + nkv;  // q or k; v is copied
+    // The lane's dims: d0(q) .. + 3 in the first tile and 32 + d0(q) .. + 3 in the second.
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int d0 = 8 * q + 4 * half;  // dims d0 .. d0 + 3 (first tile), + 32 (second tile)
-      float sc[2][4], bv[2][4];
+    for (int j = 0; j < C::TM; ++j) {
+      const int mrow = mb + wm * (32 * C::TM) + 32 * j + col;
+      if (mrow >= m) continue;
+      // Everything this row reads, before any store: its slot and the 8-byte runs of cos / sin
+      // at its 16 dims (the stores could alias them as far as the compiler knows).
+      const int64_t slot = head >= nq ? int64_t(ea.slots[mrow]) : 0;
+      uint2 cv[4][2], sv[4][2];
+      if (rotate) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+        for (int q = 0; q < 4; ++q)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const uint32_t e = ep_lds[wn * 64 + 32 * i + d0 + r];
-          sc[i][r] = float(__builtin_bit_cast(_Float16, uint16_t(e & 0xFFFFu)));
-          bv[i][r] = float(__builtin_bit_cast(_Float16, uint16_t(e >> 16)));
-        }
+          for (int i = 0; i < 2; ++i) {
+            const int64_t off = int64_t(mrow) * 64 + 32 * i + 8 * q + 4 * half;
+            cv[q][i] = *reinterpret_cast<const uint2*>(ea.cos_tok + off);
+            sv[q][i] = *reinterpret_cast<const uint2*>(ea.sin_tok + off);
+          }
+      }
+      f16* dst;
+      if (head < nq) {
+        dst = ea.q_out + int64_t(mrow) * ea.q_st + int64_t(head) * 64;
+      } else {
+        if (slot < 0 || slot >= pool_rows) continue;
+        const int kvh = rotate ? head - nq : head - nq - nkv;
+        dst = (rotate ? ea.kpool : ea.vpool) +
+              ((int64_t(kvh) * ea.num_blocks + slot / ea.block_size) * ea.block_size +
+               slot % ea.block_size) * 64;
+      }
 #pragma unroll
-      for (int j = 0; j < C::TM; ++j) {
-        const int mrow = mb + wm * (32 * C::TM) + 32 * j + col;
-        if (mrow >= m) continue;
+      for (int q = 0; q < 4; ++q) {
+        const int d0 = 8 * q + 4 * half;
         // The projection rounded to fp16 as the plain epilogue rounds it (fp32 first).
         float v[2][4];
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            float t = PC ? sc[i][r] * acc[i][j][4 * q + r] + bv[i][r] : acc[i][j][4 * q + r] + bv[i][r];
+            const uint32_t e = ep_lds[wn * 64 + 32 * i + d0 + r];
+            const float sc = float(__builtin_bit_cast(_Float16, uint16_t(e & 0xFFFFu)));
+            const float bv = float(__builtin_bit_cast(_Float16, uint16_t(e >> 16)));
+            float t = PC ? sc * acc[i][j][4 * q + r] + bv : acc[i][j][4 * q + r] + bv;
             asm volatile("" : "+v"(t));
             v[i][r] = __half2float(__float2half_rn(t));
           }
         f16 o[2][4];
-        if (head < nq + nkv) {  // q or k: RoPE
-          const f16* ct = ea.cos_tok + int64_t(mrow) * 64;
-          const f16* st = ea.sin_tok + int64_t(mrow) * 64;
 #pragma unroll
-          for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < 2; ++i) {
+          const _Float16* cw = reinterpret_cast<const _Float16*>(&cv[q][i]);
+          const _Float16* sw = reinterpret_cast<const _Float16*>(&sv[q][i]);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int d = 32 * i + d0 + r;
+          for (int r = 0; r < 4; ++r) {
+            if (rotate) {
               // One element at a time: paired across the two tiles, the vectoriser forms
               // two-float vector negations this target cannot select without packed fp32 ops.
               float own = v[i][r], partner = v[1 - i][r];
               asm volatile("" : "+v"(own), "+v"(partner));
-              o[i][r] = rope_elem(own, partner, i == 1, __half2float(ct[d]), __half2float(st[d]));
+              o[i][r] = rope_elem(own, partner, i == 1, float(cw[r]), float(sw[r]));
+            } else {
+              o[i][r] = __float2half_rn(v[i][r]);
             }
-        } else {
-#pragma unroll
-          for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) o[i][r] = __float2half_rn(v[i][r]);
-        }
-        f16* dst;
-        if (head < nq) {
-          dst = ea.q_out + int64_t(mrow) * ea.q_st + int64_t(head) * 64;
-        } else {
-          const int64_t slot = ea.slots[mrow];
-          if (slot < 0 || slot >= pool_rows) continue;
-          const int kvh = head < nq + nkv ? head - nq : head - nq - nkv;
-          dst = (head < nq + nkv ? ea.kpool : ea.vpool) +
-                ((int64_t(kvh) * ea.num_blocks + slot / ea.block_size) * ea.block_size +
-                 slot % ea.block_size) * 64;
+          }
         }
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
