@@ -491,6 +491,11 @@ extern "C" int edgerag_quant_linear_rope_append(
                 "edgerag_quant_linear_rope_append: shape not covered (dtype %d, M %d, K %d, N %d, "
                 "bits %d, group %d, head_dim %d); use edgerag_quant_linear + edgerag_rope_append",
                 x_dtype, m, k, n, bits, group_size, head_dim);
+  if (!stream_rope_shape(m, k, n, int32_t(heads), head_dim) &&
+      ((reinterpret_cast<uintptr_t>(cos_tok) | reinterpret_cast<uintptr_t>(sin_tok)) & 7) != 0)
+    return fail(EDGERAG_EINVAL,
+                "edgerag_quant_linear_rope_append: cos_tok / sin_tok must be 8-byte aligned for "
+                "M %d (the tiled GEMM reads them in 8-byte runs)", m);
   EpiArgs ea{};
   if (int rc = set_norm("edgerag_quant_linear_rope_append", m, norm_partials, norm_parts, eps,
                         ea))

@@ -73,6 +73,9 @@ constexpr int kNormMaxParts = 256;
 bool qlinear_rope_supported(int32_t m, int32_t k, int32_t n, int32_t bits, int32_t g,
                             int32_t heads, int32_t head_dim, const void* x, int64_t x_stride,
                             const void* packed);
+// True when launch_qlinear_rope takes the shape on the streaming GEMV alone; otherwise the tiled
+// GEMM's epilogue reads cos / sin in 8-byte runs, so their rows must be 8-byte aligned.
+bool stream_rope_shape(int32_t m, int32_t k, int32_t n, int32_t heads, int32_t head_dim);
 void launch_qlinear_rope(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
                          const f16* scales, const f16* bias, int32_t n, const EpiArgs& ea,
                          hipStream_t s);

@@ -347,10 +347,13 @@ int64_t edgerag_quant_linear_workspace_bytes(int32_t m, int32_t k, int32_t n, in
  * (gate rows 0..I-1, up rows I..N-1), and
  *   y[t][j] = fp16(fp16(silu(g)) * u),  g = (x . W^T + bias)[t][j],  u = (...)[t][I + j]
  * with g and u exactly the fp16 values edgerag_quant_linear would write for the same arguments.
- * y: [M, I] fp16, row stride y_stride. Covered: fp16 x, bits 8 with group_size == K, 1 <= M <= 64,
- * K a multiple of 64 (at least 256), N even and at least 8192, 16-byte aligned x rows and W.
- * Anything else returns EDGERAG_EUNSUPPORTED (edgerag_quant_linear_swiglu_supported says so
- * beforehand); the caller then runs edgerag_quant_linear and edgerag_silu_mul.
+ * y: [M, I] fp16, row stride y_stride. Covered: fp16 x, bits 8 with group_size == K, 16-byte
+ * aligned x rows and W, K a multiple of 64 (at least 256), N even, and either 1 <= M <= 64 with
+ * N at least 8192 (the streaming GEMV's epilogue), or M > 64 where edgerag_quant_linear's tiled
+ * GEMM takes 128-row weight tiles (its epilogue; at most 16 rows past whole 64-row tiles go to
+ * the streaming form). Anything else returns EDGERAG_EUNSUPPORTED
+ * (edgerag_quant_linear_swiglu_supported says so beforehand); the caller then runs
+ * edgerag_quant_linear and edgerag_silu_mul.
  *
  * Replaces `down_proj(F.silu(gate_proj(x)) * up_proj(x))`'s first half (edgerag/core/layers.py:341)
  * for decode batches: the [M, N] projection never goes through HBM, and one launch goes away.
@@ -373,9 +376,12 @@ int edgerag_quant_linear_swiglu_supported(int32_t x_dtype, int32_t m, int32_t k,
  * row per token: cos_tok / sin_tok are [M, head_dim] (row t = the table row at token t's
  * position, already clamped), fp16. q heads go to q_out (row stride q_stride_tok, head stride
  * head_dim), rotated k and raw v heads to the pools at slots[t] (skipped when negative or
- * outside the pool). Covered: fp16 x, bits 8 with group_size == K, 1 <= M <= 64, K a multiple of
- * 64 (at least 256) handled by at most 8 waves, head_dim a multiple of 32, and N at least 4096
- * when M <= 16; edgerag_quant_linear_rope_append_supported says so beforehand. Anything else
+ * outside the pool). Covered: fp16 x, bits 8 with group_size == K, and either 1 <= M <= 64 with
+ * K a multiple of 64 (at least 256) handled by at most 8 waves, head_dim a multiple of 32 and N
+ * at least 4096 when M <= 16 (the streaming GEMV's epilogue), or M > 64 with head_dim 64 where
+ * edgerag_quant_linear's tiled GEMM takes 128-row weight tiles (its epilogue; at most 16 rows
+ * past whole 64-row tiles go to the streaming form; cos_tok and sin_tok 8-byte aligned, else
+ * EDGERAG_EINVAL). edgerag_quant_linear_rope_append_supported says so beforehand. Anything else
  * returns EDGERAG_EUNSUPPORTED (then run edgerag_quant_linear and edgerag_rope_append).
  *
  * Replaces the decode iteration's q/k/v projections + apply_rope + cache.update's write

@@ -173,6 +173,13 @@ def test_validation_errors_come_back_as_messages() -> None:
                   None, None, 1, 16, 1, None)
     with pytest.raises(_lib.EdgeragError, match="bad shape"):
         _lib.call("edgerag_silu_mul", None, 0, 1, 0, None, 0, 1, None)
+    # The tiled q/k/v + RoPE launch (M = 512, 32 + 2 x 32 heads of 64) reads cos / sin rows in
+    # 8-byte runs: a table 2 bytes off is refused before anything is launched.
+    base = 1 << 20
+    with pytest.raises(_lib.EdgeragError, match="8-byte aligned"):
+        _lib.call("edgerag_quant_linear_rope_append", base, 1, 2048, 512, 2048, base, base, None,
+                  8, 2048, base + 2, base, 32, 32, 64, base, 2048, base, base, base, 16, 16,
+                  None, 0, 1e-5, None)
 
 
 def test_device_guard_refuses_cpu_tensors() -> None:
