@@ -302,6 +302,7 @@ def test_quant_linear_rope_append_tiled_gemm(device, n_q, n_kv, k, ms) -> None:
     (2048, 16384, (65, 128, 200, 512, 519, 544)),
     (2048, 6144, (384, 512, 519, 544)),   # 128x64 tiles from 6 tile rows (M > 320) on
     (1152, 8192, (320, 512, 519, 544)),
+    (1024, 8200, (512, 519)),  # I = 4100: the last 64-column block holds 4 outputs
 ])
 def test_quant_linear_swiglu_tiled_gemm(device, k, n, ms) -> None:
     """SwiGLU in the tiled GEMM's epilogue (prefill slices, M > 64, weights whose plain launch
