@@ -92,7 +92,8 @@ def test_silu_mul(device, dtype) -> None:
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("rows,cols", [(1, 49152), (8, 49152), (64, 49152), (5, 1000), (3, 7)])
+@pytest.mark.parametrize("rows,cols", [(1, 49152), (8, 49152), (64, 49152), (5, 1000), (3, 7),
+                                       (4, 70000)])
 def test_argmax_rows_is_torch_argmax(device, dtype, rows, cols) -> None:
     """The greedy choice over logit rows equals torch.argmax (the first index of the maximum),
     including planted ties, -inf rows, NaN, a maximum in the last element, and strided rows."""
