@@ -54,9 +54,32 @@ class PoolCounters:
     blocks_handed_out: int = 0
     blocks_released: int = 0
     shares: int = 0
+    forks: int = 0
     private_copies: int = 0
     refusals: int = 0
     high_water: int = 0
+
+    # The reference's ``AllocatorStats`` names for the same counts (``allocator.py:58-73``), read
+    # by its tests and reports.
+    @property
+    def allocations(self) -> int:
+        return self.blocks_handed_out
+
+    @property
+    def frees(self) -> int:
+        return self.blocks_released
+
+    @property
+    def copy_on_writes(self) -> int:
+        return self.private_copies
+
+    @property
+    def peak_used_blocks(self) -> int:
+        return self.high_water
+
+    @property
+    def oom_events(self) -> int:
+        return self.refusals
 
 
 def _ids(blocks: Iterable[int] | np.ndarray) -> np.ndarray:
@@ -78,6 +101,11 @@ class BlockAllocator:
         self._stack = np.arange(self.num_blocks - 1, -1, -1, dtype=np.int32)
         self._top = self.num_blocks
         self.counters = PoolCounters()
+
+    @property
+    def stats(self) -> PoolCounters:
+        """The event counts under the reference's attribute name (``allocator.py:104``)."""
+        return self.counters
 
     # --- occupancy ------------------------------------------------------------------------------
 
@@ -208,6 +236,28 @@ class BlockAllocator:
         if np.any(self._owners[~marked] <= 0):
             raise AllocatorError("a block off the free stack has no owner")
 
+    def internal_fragmentation(self, sequence_lengths: Iterable[int]) -> dict[str, float]:
+        """Slack of sequences of the given lengths: the unused tail of each one's last block
+        (``allocator.py:256-274``)."""
+        lengths = np.asarray(list(sequence_lengths), dtype=np.int64)
+        held = (lengths + self.block_size - 1) // self.block_size * self.block_size
+        wasted, capacity = float((held - lengths).sum()), float(held.sum())
+        return {"wasted_tokens": wasted, "wasted_blocks_equiv": wasted / self.block_size,
+                "waste_fraction": wasted / capacity if capacity else 0.0}
+
+    def to_dict(self) -> dict:
+        """Occupancy and event counts under the reference report's keys
+        (``allocator.py:276-291``)."""
+        c = self.counters
+        return {
+            "num_blocks": self.num_blocks, "block_size": self.block_size,
+            "num_free": self.num_free, "num_used": self.num_used,
+            "utilization": round(self.utilization, 4),
+            "stats": {"allocations": c.allocations, "frees": c.frees, "forks": c.forks,
+                      "copy_on_writes": c.copy_on_writes,
+                      "peak_used_blocks": c.peak_used_blocks, "oom_events": c.oom_events},
+        }
+
     def snapshot(self) -> dict:
         """Occupancy and event counts, for logs and the serving report."""
         c = self.counters
@@ -215,6 +265,7 @@ class BlockAllocator:
             "blocks": {"total": self.num_blocks, "free": self.num_free, "used": self.num_used,
                        "block_size": self.block_size},
             "events": {"handed_out": c.blocks_handed_out, "released": c.blocks_released,
-                       "shared": c.shares, "private_copies": c.private_copies,
+                       "shared": c.shares, "forks": c.forks,
+                       "private_copies": c.private_copies,
                        "refusals": c.refusals, "high_water": c.high_water},
         }

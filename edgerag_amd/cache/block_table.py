@@ -6,11 +6,20 @@ A table holds ``len(blocks) == ceil(num_tokens / block_size)`` physical ids
 block ``blocks[p // block_size]`` at offset ``p % block_size``, i.e. in pool slot
 ``blocks[p // block_size] * block_size + p % block_size``.
 
-* :meth:`grow` takes the blocks for ``n`` more tokens before it moves the length, so a refused
-  allocation leaves the table as it was (``block_table.py:71-79``);
+The methods keep the reference's names and contracts, so its executor and scheduler drive this
+table unchanged:
+
+* :meth:`ensure_capacity` takes blocks for a length without moving it; :meth:`append` takes the
+  blocks for ``n`` more tokens before it moves the length, so a refused allocation leaves the
+  table as it was (``block_table.py:62-79``);
 * :meth:`fork` shares every block with a new table (one more owner each);
-* :meth:`make_private` gives a shared block a private copy (the caller moves the contents);
-* :meth:`locate` refuses positions that were never written (they hold a previous tenant's data).
+* :meth:`unshare` / :meth:`writable_block_for` give a shared block a private copy (the caller
+  moves the contents); :meth:`free` drops every ownership;
+* :meth:`locate` refuses positions that were never written (they hold a previous tenant's data);
+* ``blocks`` reads as a list of ints and may be assigned; ``num_tokens`` is a plain attribute.
+
+The ids live in a growable int32 array (:attr:`ids` is a view of it), which is what the batch
+helpers read.
 
 :func:`pack_tables` and :func:`step_slots` build a whole batch's ``[R, width]`` block-table matrix
 and its slot mapping for the single per-step upload.
@@ -31,10 +40,9 @@ class BlockTable:
     def __init__(self, allocator: BlockAllocator, blocks: Sequence[int] | np.ndarray = (),
                  num_tokens: int = 0) -> None:
         self.allocator = allocator
-        ids = np.asarray(blocks, dtype=np.int32).reshape(-1)
-        self._ids = np.empty(max(8, ids.size), dtype=np.int32)
-        self._ids[: ids.size] = ids
-        self._n = int(ids.size)
+        self._ids = np.empty(8, dtype=np.int32)
+        self._n = 0
+        self.blocks = blocks
         self.num_tokens = int(num_tokens)
 
     # --- shape ------------------------------------------------------------------------------------
@@ -44,9 +52,26 @@ class BlockTable:
         return self.allocator.block_size
 
     @property
-    def blocks(self) -> np.ndarray:
+    def ids(self) -> np.ndarray:
         """The physical ids, int32, logical order (a view: do not keep it across a change)."""
         return self._ids[: self._n]
+
+    @property
+    def blocks(self) -> list[int]:
+        """The physical ids as a list of ints (a copy), the reference's field
+        (``block_table.py:31``)."""
+        return self._ids[: self._n].tolist()
+
+    @blocks.setter
+    def blocks(self, ids: Sequence[int] | np.ndarray) -> None:
+        """Replace the mapping without touching owner counts, as assigning the reference's field
+        does: its scheduler hands a preempted table's blocks to the swapper this way
+        (``sched/scheduler.py:244-245``)."""
+        arr = np.asarray(ids, dtype=np.int32).reshape(-1)
+        if arr.size > self._ids.size:
+            self._ids = np.empty(max(8, arr.size), dtype=np.int32)
+        self._ids[: arr.size] = arr
+        self._n = int(arr.size)
 
     @property
     def num_blocks(self) -> int:
@@ -71,15 +96,24 @@ class BlockTable:
         self._ids[self._n : need] = fresh
         self._n = need
 
-    def grow(self, n_new: int) -> list[int]:
-        """Make room for ``n_new`` more tokens and count them as written. Returns the fresh block
-        ids; raises :class:`OutOfBlocksError` with the table unchanged when the pool is short."""
-        if n_new < 0:
-            raise ValueError(f"a table grows by >= 0 tokens, got {n_new}")
-        missing = self.allocator.blocks_needed(self.num_tokens + n_new) - self._n
-        fresh = self.allocator.allocate(missing) if missing > 0 else []
+    def ensure_capacity(self, n_tokens: int) -> list[int]:
+        """Hold enough blocks for ``n_tokens`` tokens without moving the length. Returns the
+        fresh ids (none when the table is already big enough); a refused allocation raises
+        :class:`OutOfBlocksError` and leaves the table as it was (``block_table.py:62-69``)."""
+        missing = self.allocator.blocks_needed(n_tokens) - self._n
+        if missing <= 0:
+            return []
+        fresh = self.allocator.allocate(missing)
         self._push(fresh)
-        self.num_tokens += n_new
+        return fresh
+
+    def append(self, n_tokens: int = 1) -> list[int]:
+        """Count ``n_tokens`` more tokens as written, taking blocks first, so a refusal leaves
+        the length unchanged (``block_table.py:71-79``). Returns the fresh ids."""
+        if n_tokens < 0:
+            raise ValueError(f"a table grows by >= 0 tokens, got {n_tokens}")
+        fresh = self.ensure_capacity(self.num_tokens + n_tokens)
+        self.num_tokens += n_tokens
         return fresh
 
     def shrink_to(self, n_tokens: int) -> int:
@@ -93,9 +127,11 @@ class BlockTable:
         self.num_tokens = n_tokens
         return self.allocator.free(dropped) if dropped.size else 0
 
-    def release(self) -> int:
-        """Drop this table's ownership of all its blocks. Returns the blocks freed."""
-        freed = self.allocator.free(self.blocks.copy()) if self._n else 0
+    def free(self) -> int:
+        """Drop this table's ownership of all its blocks and empty it. Returns how many blocks
+        went back to the pool: fewer than the table held while another table shares some
+        (``block_table.py:120-129``)."""
+        freed = self.allocator.free(self.ids.copy()) if self._n else 0
         self._n = 0
         self.num_tokens = 0
         return freed
@@ -103,7 +139,7 @@ class BlockTable:
     def detach(self) -> tuple[list[int], int]:
         """Hand the blocks and token count over to a new owner (a swap-out record) and empty the
         table without releasing anything."""
-        out = (self.blocks.tolist(), self.num_tokens)
+        out = (self.blocks, self.num_tokens)
         self._n = 0
         self.num_tokens = 0
         return out
@@ -120,21 +156,30 @@ class BlockTable:
     # --- sharing ----------------------------------------------------------------------------------
 
     def fork(self) -> BlockTable:
-        """A second table over the same blocks (each gains an owner)."""
-        self.allocator.incref(self.blocks)
-        return BlockTable(self.allocator, self.blocks.copy(), self.num_tokens)
+        """A second table over the same blocks (each gains an owner; no contents move)."""
+        self.allocator.incref(self.ids)
+        self.allocator.counters.forks += 1
+        return BlockTable(self.allocator, self.ids.copy(), self.num_tokens)
 
-    def make_private(self, logical: int) -> tuple[int, int] | None:
-        """Ensure logical block ``logical`` has this table as its only owner. Returns
-        ``(shared id, private id)`` when a copy is needed, None when it already was private."""
-        if not 0 <= logical < self._n:
-            raise IndexError(f"logical block {logical} outside a table of {self._n}")
-        old = int(self._ids[logical])
+    def unshare(self, logical_block: int) -> tuple[int, int] | None:
+        """Make logical block ``logical_block`` owned by this table alone. Returns
+        ``(shared id, private id)`` when a fresh block replaced it -- the caller then copies the
+        contents -- and None when it already was private (``block_table.py:95-107``)."""
+        if not 0 <= logical_block < self._n:
+            raise IndexError(f"logical block {logical_block} outside a table of {self._n}")
+        old = int(self._ids[logical_block])
         new = self.allocator.copy_on_write(old)
         if new == old:
             return None
-        self._ids[logical] = new
+        self._ids[logical_block] = new
         return old, new
+
+    def writable_block_for(self, position: int) -> tuple[int, int, tuple[int, int] | None]:
+        """``(physical block, offset, copied)`` for a write at ``position``, after making its
+        block private (``copied`` as :meth:`unshare` returns it) (``block_table.py:109-118``)."""
+        bs = self.block_size
+        copied = self.unshare(position // bs)
+        return int(self._ids[position // bs]), position % bs, copied
 
     # --- addressing -------------------------------------------------------------------------------
 
@@ -142,8 +187,8 @@ class BlockTable:
         """``(physical block, offset)`` of a written position."""
         if not 0 <= position < self.num_tokens:
             raise IndexError(
-                f"position {position} was never written (table holds {self.num_tokens} tokens); "
-                "its slot may hold another sequence's keys"
+                f"position {position} outside the written region [0, {self.num_tokens}); its "
+                "slot may hold another sequence's keys"
             )
         bs = self.block_size
         return int(self._ids[position // bs]), position % bs
@@ -160,9 +205,10 @@ class BlockTable:
         pos = np.arange(start, start + n, dtype=np.int64)
         return (self._ids[pos // bs].astype(np.int64) * bs + pos % bs).astype(np.int32)
 
-    def snapshot(self) -> dict:
-        return {"tokens": self.num_tokens, "blocks": self.blocks.tolist(),
-                "capacity": self.capacity}
+    def to_dict(self) -> dict:
+        """The reference report's keys (``block_table.py:131-138``)."""
+        return {"num_tokens": self.num_tokens, "num_blocks": self._n,
+                "capacity": self.capacity, "slack": self.slack, "blocks": self.blocks}
 
 
 def pack_tables(tables: Sequence[BlockTable], width: int | None = None) -> np.ndarray:
@@ -172,7 +218,7 @@ def pack_tables(tables: Sequence[BlockTable], width: int | None = None) -> np.nd
     for r, t in enumerate(tables):
         if t.num_blocks > width:
             raise ValueError(f"table {r} has {t.num_blocks} blocks, wider than {width}")
-        out[r, : t.num_blocks] = t.blocks
+        out[r, : t.num_blocks] = t.ids
     return out
 
 

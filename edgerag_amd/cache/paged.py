@@ -91,7 +91,7 @@ class PagedKVCache:
         """
         self._pending_tokens = n_new
         slots = self.reserve(n_new)
-        blocks = np.asarray(self.table.blocks, dtype=np.int32)
+        blocks = self.table.ids
         self._slots, self._blocks = kernels.upload_int32([slots, blocks], self.device)
 
     def blocks_to_reserve(self, n_new: int) -> int:
@@ -100,14 +100,14 @@ class PagedKVCache:
         table, bs = self.table, self.allocator.block_size
         fresh = max(0, self.allocator.blocks_needed(self.seq_len + n_new) - table.num_blocks)
         first, last = self.seq_len // bs, min(table.num_blocks, -(-(self.seq_len + n_new) // bs))
-        return fresh + self.allocator.shared_count(table.blocks[first:last])
+        return fresh + self.allocator.shared_count(table.ids[first:last])
 
     def reserve(self, n_new: int) -> np.ndarray:
         """Grow the table by ``n_new`` tokens, copy-on-write any shared block in the write range
         (every layer), and return the int32 pool slots of positions ``[seq_len - n_new,
         seq_len)``. The host half of :meth:`begin_append`, for callers that upload several
         sequences' metadata at once (the ragged executor)."""
-        self.table.grow(n_new)
+        self.table.append(n_new)
         try:
             self._unshare_write_range(self.seq_len - n_new, n_new)
         except Exception:
@@ -167,12 +167,12 @@ class PagedKVCache:
             return
         bs = self.allocator.block_size
         first, last = start // bs, min(self.table.num_blocks, (start + n_new - 1) // bs + 1)
-        if not self.allocator.shared_count(self.table.blocks[first:last]):
+        if not self.allocator.shared_count(self.table.ids[first:last]):
             return  # the usual case: nothing in the write range is shared
         pairs = []
         try:
             for logical in range(first, last):
-                copied = self.table.make_private(logical)
+                copied = self.table.unshare(logical)
                 if copied is not None:
                     pairs.append(copied)
         finally:  # a block already switched to its private copy gets its contents either way
@@ -209,7 +209,7 @@ class PagedKVCache:
 
     def _device_blocks(self) -> torch.Tensor:
         (blocks,) = kernels.upload_int32(
-            [np.asarray(self.table.blocks, dtype=np.int32)], self.device
+            [self.table.ids], self.device
         )
         return blocks
 
@@ -239,7 +239,7 @@ class PagedKVCache:
 
     def free(self) -> int:
         self._slots = self._blocks = None
-        return self.table.release()
+        return self.table.free()
 
     def reset(self) -> None:
         self.free()

@@ -271,11 +271,11 @@ class EdgeRagDecoder(nn.Module):
     def greedy(self, step: StepInputs, key_pool, value_pool) -> tuple[torch.Tensor, torch.Tensor]:
         """Logits ``(R', vocab)`` of the rows in ``step.logit_rows`` and their greedy tokens
         (int32 ``(R',)``). fp16 batches of up to 16 rows run the fused lm_head GEMV + argmax
-        (the 201 MB weight streamed once, no separate argmax pass); others the vendor GEMM and
-        ``edgerag_argmax_rows``."""
+        (the 201 MB weight streamed once, no separate argmax pass) where the kernel takes the
+        width; others the vendor GEMM and ``edgerag_argmax_rows``."""
         h = self.forward_hidden(step, key_pool, value_pool)
         rows = h.shape[0]
-        if self.dtype == torch.float16 and 1 <= rows <= kernels.LM_HEAD_MAX_ROWS:
+        if self.dtype == torch.float16 and rows >= 1 and kernels.lm_head_fused(h):
             logits = torch.empty((rows, self.spec.vocab_size), dtype=self.dtype,
                                  device=self.device)
             return kernels.lm_head_argmax(h, self.lm_head, logits)

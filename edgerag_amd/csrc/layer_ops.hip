@@ -135,6 +135,22 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_vec_kernel(
   }
 }
 
+// out[p] = x1 cos[p] + (-x2) sin[p]; out[p + half] = x2 cos[p + half] + x1 sin[p + half].
+// No contraction: each product is rounded before the add, like the reference's separate tensor
+// ops, also on the fp32 path.
+template <typename T>
+__device__ __forceinline__ void rotate_pair(float x1, float x2, const T* __restrict__ cr,
+                                            const T* __restrict__ sr, int p, int half, T& o1,
+                                            T& o2) {
+#pragma clang fp contract(off)
+  const float a1 = to_f32<T>(round_to<T>(x1 * to_f32<T>(cr[p])));
+  const float b1 = to_f32<T>(round_to<T>(-x2 * to_f32<T>(sr[p])));
+  const float a2 = to_f32<T>(round_to<T>(x2 * to_f32<T>(cr[p + half])));
+  const float b2 = to_f32<T>(round_to<T>(x1 * to_f32<T>(sr[p + half])));
+  o1 = round_to<T>(a1 + b1);
+  o2 = round_to<T>(a2 + b2);
+}
+
 // One thread per (token, head, pair i in [0, d/2)) of the q, k and v heads of the fused
 // projection row [q heads | k heads | v heads].
 template <typename T>
@@ -165,18 +181,16 @@ __global__ __launch_bounds__(256) void rope_append_kernel(
     dst[p + half] = src[p + half];
     return;
   }
-  int pos = positions[t];
-  pos = pos < 0 ? 0 : (pos >= max_pos ? max_pos - 1 : pos);
-  const T* cr = cos_t + int64_t(pos) * head_dim;
-  const T* sr = sin_t + int64_t(pos) * head_dim;
-  // out[p] = x1 cos[p] + (-x2) sin[p]; out[p + half] = x2 cos[p + half] + x1 sin[p + half]
-  // No contraction (pragma above): each product is rounded before the add, like the
-  // reference's separate tensor ops, also on the fp32 path.
-  const float a1 = to_f32<T>(round_to<T>(x1 * to_f32<T>(cr[p])));
-  const float b1 = to_f32<T>(round_to<T>(-x2 * to_f32<T>(sr[p])));
-  const float a2 = to_f32<T>(round_to<T>(x2 * to_f32<T>(cr[p + half])));
-  const float b2 = to_f32<T>(round_to<T>(x1 * to_f32<T>(sr[p + half])));
-  const T o1 = round_to<T>(a1 + b1), o2 = round_to<T>(a2 + b2);
+  const int pos = positions[t];
+  T o1, o2;
+  if (pos < 0 || pos >= max_pos) {
+    // No table row: the token's q and k become NaN, so a caller whose table is too short sees
+    // it in the logits instead of getting another position's rotation.
+    o1 = o2 = round_to<T>(__builtin_nanf(""));
+  } else {
+    rotate_pair<T>(x1, x2, cos_t + int64_t(pos) * head_dim, sin_t + int64_t(pos) * head_dim, p,
+                   half, o1, o2);
+  }
   if (hd < n_q_heads) {
     T* dst = q_out + int64_t(t) * q_stride_tok + int64_t(hd) * head_dim;
     dst[p] = o1;

@@ -181,6 +181,17 @@ extern "C" int64_t edgerag_lm_head_workspace_bytes(int32_t m, int32_t vocab) {
   return int64_t(m) * lm_head_workgroups(vocab, kLmSmallWaves) * int64_t(sizeof(uint64_t));
 }
 
+// Rows of k fp16 values staged in LDS, one 16-byte chunk of padding per row.
+static size_t lm_head_stage_bytes(int32_t m, int32_t k) {
+  return size_t(m) * (size_t(k / 8) + 1) * sizeof(uint4);
+}
+static constexpr size_t kLmStageMax = 128 * 1024;  // of the CU's 160 KiB
+
+extern "C" int edgerag_lm_head_argmax_supported(int32_t m, int32_t k) {
+  return m >= 1 && m <= kLmMaxM && k >= 32 && k % 32 == 0 &&
+         lm_head_stage_bytes(m, k) <= kLmStageMax;
+}
+
 extern "C" int edgerag_lm_head_argmax(const void* x, int64_t x_stride, int32_t m, int32_t k,
                                       const void* weight, int32_t vocab, void* logits,
                                       int64_t logits_stride, int32_t* tokens, void* workspace,
@@ -203,8 +214,8 @@ extern "C" int edgerag_lm_head_argmax(const void* x, int64_t x_stride, int32_t m
     return fail(EDGERAG_EWORKSPACE, "edgerag_lm_head_argmax: workspace %lld bytes, need %lld "
                                     "(8-byte aligned)",
                 (long long)workspace_bytes, (long long)need);
-  const size_t lds = size_t(m) * (size_t(k / 8) + 1) * sizeof(uint4);
-  if (lds > 128 * 1024)  // of the CU's 160 KiB
+  const size_t lds = lm_head_stage_bytes(m, k);
+  if (lds > kLmStageMax)
     return fail(EDGERAG_EUNSUPPORTED, "edgerag_lm_head_argmax: %d rows of %d exceed the staging "
                                       "space", m, k);
   const bool small = m <= kLmSmallM;

@@ -713,10 +713,15 @@ def rope_append(qkv: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor, s
 
 def rope_rows(positions: torch.Tensor, cos: torch.Tensor,
               sin: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """The rotary table rows at each token's position (clamped to the table), ``(T, head_dim)``
-    each: what ``quant_linear_rope_append`` reads. Gathered once per forward, shared by layers."""
-    idx = positions.long().clamp(0, cos.shape[0] - 1)
-    return cos.index_select(0, idx), sin.index_select(0, idx)
+    """The rotary table rows at each token's position, ``(T, head_dim)`` each: what
+    ``quant_linear_rope_append`` reads. Gathered once per forward, shared by layers. A position
+    outside the table gets a NaN row (its q and k come out NaN), as ``rope_append`` does."""
+    idx = positions.long()
+    bad = (idx < 0) | (idx >= cos.shape[0])
+    idx = idx.clamp(0, cos.shape[0] - 1)
+    c, s = cos.index_select(0, idx), sin.index_select(0, idx)
+    nan = bad.unsqueeze(1)
+    return c.masked_fill_(nan, float("nan")), s.masked_fill_(nan, float("nan"))
 
 
 def quant_rope_fused(m: int, k: int, bits: int, group_size: int, n_q_heads: int,
@@ -966,6 +971,15 @@ def argmax_rows(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tenso
 
 LM_HEAD_MAX_ROWS = 16
 _LM_WORKSPACES: dict[tuple[torch.device, int], torch.Tensor] = {}
+
+
+def lm_head_fused(x: torch.Tensor) -> bool:
+    """Whether ``lm_head_argmax`` takes the hidden rows ``x (m, k)``: fp16, 1..16 rows of a width
+    the kernel stages, 16-byte aligned rows."""
+    m, k = x.shape
+    return (x.dtype == torch.float16 and x.stride(1) == 1 and (x.stride(0) * 2) % 16 == 0
+            and x.data_ptr() % 16 == 0
+            and bool(_lib.load().edgerag_lm_head_argmax_supported(m, k)))
 
 
 def lm_head_argmax(x: torch.Tensor, weight: torch.Tensor, logits: torch.Tensor | None = None,

@@ -14,6 +14,11 @@ the host builds the step's metadata (token ids, logical positions, pool slots, c
 context lengths, block tables, the attention work plan, the rows whose logits are read) and
 uploads it in one pinned copy; the argmax of every emitting request comes back in one copy.
 
+Requests are duck-typed: this package's :class:`~edgerag_amd.sched.request.Request` (which can
+re-feed generated tokens after a recompute preemption) or the reference's own ``Request``
+(``edgerag/sched/request.py:37-172``: ``request_id``, ``prompt_token_ids``, ``prompt_embeds``,
+``prefill_offset``, ``generated_token_ids``, ``cache``), whose prefill is just its prompt.
+
 A step either happens entirely or not at all on the host side: positions past the model's RoPE
 table are refused (``ValueError``) and the batch's block need (fresh blocks plus copy-on-write
 copies) is checked against the free pool (:class:`StepDoesNotFit`, an ``OutOfBlocksError``)
@@ -58,6 +63,24 @@ class StepDoesNotFit(OutOfBlocksError):
     def __init__(self, message: str, blocks_needed: int) -> None:
         super().__init__(message)
         self.blocks_needed = blocks_needed
+
+
+def _prefill_len(request) -> int:
+    """Positions a request prefills: its prompt, plus any generated tokens it re-feeds."""
+    n = getattr(request, "prefill_len", None)
+    return len(request.prompt_token_ids) if n is None else n
+
+
+def _prefill_ids(request, start: int, end: int) -> list[int]:
+    """Token ids of prefill positions ``[start, end)``."""
+    take = getattr(request, "prefill_ids", None)
+    if take is not None:
+        return take(start, end)
+    return [int(t) for t in request.prompt_token_ids[start:end]]
+
+
+def _refeeds(request) -> bool:
+    return bool(getattr(request, "refeed", 0))
 
 
 @dataclass
@@ -135,10 +158,11 @@ class ModelExecutor:
                     f"{request.request_id}: cache holds {cache.seq_len} positions but the prompt "
                     f"is read up to {start}"
                 )
-            end = min(start + self.chunk_size, request.prefill_len)
+            total = _prefill_len(request)
+            end = min(start + self.chunk_size, total)
             if end > start:
-                entries.append(_Entry(request, cache, request.prefill_ids(start, end), start,
-                                      end - start, end >= request.prefill_len, True))
+                entries.append(_Entry(request, cache, _prefill_ids(request, start, end), start,
+                                      end - start, end >= total, True))
         for request in batch.decode:
             if not request.generated_token_ids:
                 raise RuntimeError(
@@ -154,15 +178,17 @@ class ModelExecutor:
         """Start a fresh token-id prompt after its longest cached prefix (at least one prompt
         token is left to compute: the first generated token comes out of that forward)."""
         r = e.request
-        if (self.prefix_cache is None or not e.prefill or e.start != 0 or r.refeed
+        if (self.prefix_cache is None or not e.prefill or e.start != 0 or _refeeds(r)
                 or r.prompt_embeds is not None or e.cache.seq_len):
             return 0
-        blocks, n = self.prefix_cache.lookup(r.prompt_token_ids, max_tokens=r.prompt_len - 1)
+        prompt_len = len(r.prompt_token_ids)
+        blocks, n = self.prefix_cache.lookup(r.prompt_token_ids, max_tokens=prompt_len - 1)
         if n:
             e.cache.adopt_prefix(blocks, n)
-            end = min(n + self.chunk_size, r.prefill_len)
-            e.ids, e.start = r.prefill_ids(n, end), n
-            e.consumed, e.emits = end, end >= r.prefill_len
+            total = _prefill_len(r)
+            end = min(n + self.chunk_size, total)
+            e.ids, e.start = _prefill_ids(r, n, end), n
+            e.consumed, e.emits = end, end >= total
         return n
 
     def _reserve(self, entries: list[_Entry]) -> list[np.ndarray]:
@@ -172,9 +198,10 @@ class ModelExecutor:
         def undo_adoptions() -> None:
             for e in adopted:
                 e.cache.free()
-                end = min(self.chunk_size, e.request.prefill_len)
-                e.ids, e.start = e.request.prefill_ids(0, end), 0
-                e.consumed, e.emits = end, end >= e.request.prefill_len
+                total = _prefill_len(e.request)
+                end = min(self.chunk_size, total)
+                e.ids, e.start = _prefill_ids(e.request, 0, end), 0
+                e.consumed, e.emits = end, end >= total
 
         for e in entries:
             top = e.cache.seq_len + len(e.ids)
@@ -214,7 +241,7 @@ class ModelExecutor:
         for i, e in with_embeds:
             pe = e.request.prompt_embeds
             pe = pe[0] if pe.dim() == 3 else pe
-            lo, hi = e.start, min(e.start + len(e.ids), e.request.prompt_len)
+            lo, hi = e.start, min(e.start + len(e.ids), len(e.request.prompt_token_ids))
             if hi > lo:
                 hidden[qsl[i] : qsl[i] + hi - lo] = pe[lo:hi].to(self.device, self.dtype)
         return hidden
@@ -266,7 +293,7 @@ class ModelExecutor:
         for e in entries:
             if e.prefill:
                 output.prefilled[e.request.request_id] = e.consumed
-                if e.emits and self.prefix_cache is not None and not e.request.refeed \
+                if e.emits and self.prefix_cache is not None and not _refeeds(e.request) \
                         and e.request.prompt_embeds is None:
                     self.prefix_cache.register(e.request.prompt_token_ids, e.cache.table.blocks)
         return output

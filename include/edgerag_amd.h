@@ -374,7 +374,7 @@ int edgerag_quant_linear_swiglu_supported(int32_t x_dtype, int32_t m, int32_t k,
  * head_dim rows). Each projection value is exactly what edgerag_quant_linear writes for the same
  * arguments; the rest is edgerag_rope_append on those values, except that the tables come as one
  * row per token: cos_tok / sin_tok are [M, head_dim] (row t = the table row at token t's
- * position, already clamped), fp16. q heads go to q_out (row stride q_stride_tok, head stride
+ * position; the caller gathers them, and a NaN row gives that token NaN q and k), fp16. q heads go to q_out (row stride q_stride_tok, head stride
  * head_dim), rotated k and raw v heads to the pools at slots[t] (skipped when negative or
  * outside the pool). Covered: fp16 x, bits 8 with group_size == K, and either 1 <= M <= 64 with
  * K a multiple of 64 (at least 256) handled by at most 8 waves, head_dim a multiple of 32 and N
@@ -452,11 +452,15 @@ int edgerag_rmsnorm(const void* x, int64_t x_stride, const void* delta, int64_t 
 /*
  * RoPE on the fused q/k/v projection output and the KV append, in one launch. Row t of qkv holds
  * [n_q_heads | n_kv_heads | n_kv_heads] heads of head_dim elements. For position p =
- * positions[t] (clamped to the table), q and k heads become dtype(dtype(x * cos[p]) +
+ * positions[t] in [0, max_pos), q and k heads become dtype(dtype(x * cos[p]) +
  * dtype(rotate_half(x) * sin[p])) with rotate_half(x) = [-x2, x1] (the halves convention); q is
  * written to q_out[t, h, :] (row stride q_stride_tok, head stride head_dim), k and the raw v to
  * key_pool / value_pool [n_kv_heads, num_blocks, block_size, head_dim] at slot slots[t] (skipped
- * when negative or outside the pool). cos/sin tables are [max_pos, head_dim] in dtype.
+ * when negative or outside the pool). cos/sin tables are [max_pos, head_dim] in dtype. A
+ * position outside [0, max_pos) has no table row: that token's q and k are written as NaN (v is
+ * still appended), never another position's rotation. The reference computes cos/sin for any
+ * position (edgerag/core/layers.py:64-90), so a caller sizes the table for every position it
+ * feeds; the positions are on the device, so the check cannot fail the launch itself.
  * Replaces apply_rope + cache.update's write (edgerag/core/layers.py:93-114, :301-306;
  * edgerag/cache/paged.py:186-206).
  */
@@ -506,6 +510,10 @@ int edgerag_lm_head_argmax(const void* x, int64_t x_stride, int32_t m, int32_t k
                            int64_t logits_stride, int32_t* tokens, void* workspace,
                            int64_t workspace_bytes, void* stream);
 int64_t edgerag_lm_head_workspace_bytes(int32_t m, int32_t vocab);
+/* 1 when edgerag_lm_head_argmax takes m rows of width k (1 <= m <= 16, k a multiple of 32 and
+ * the m rows staged in 128 KiB of LDS: m * (k / 8 + 1) * 16 bytes), else 0; with 16-byte aligned
+ * rows and weight it then accepts the call. */
+int edgerag_lm_head_argmax_supported(int32_t m, int32_t k);
 
 #ifdef __cplusplus
 }

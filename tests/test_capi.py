@@ -121,6 +121,17 @@ def test_rope_append_support_query() -> None:
     assert q(F16, 8, 16384, 8, 16384, 32, 32, 64, 0) == 0  # K needing 16 waves
 
 
+def test_lm_head_support_query() -> None:
+    """The fused lm_head + argmax stages m rows of width k in 128 KiB of LDS; wider batches (such
+    as 16 rows of a 4,096-wide model: 131,328 bytes) are declined beforehand, so the decoder takes
+    the vendor GEMM + argmax path instead of failing the step."""
+    q = _lib.load().edgerag_lm_head_argmax_supported
+    assert q(1, 2048) == 1 and q(16, 2048) == 1  # config 5
+    assert q(16, 4096) == 0 and q(15, 4096) == 1  # 15 * 513 * 16 = 123,120 bytes
+    assert q(1, 8160) == 1 and q(17, 2048) == 0 and q(0, 2048) == 0
+    assert q(4, 2000) == 0 and q(4, 16) == 0  # k a multiple of 32, at least 32
+
+
 def test_residual_parts_query() -> None:
     """The residual-add producer covers decode batches (up to 16 tokens) of the streaming
     shapes and reports how many partial sums per token it writes: one per workgroup."""

@@ -254,3 +254,24 @@ def test_swap_in_without_room_keeps_the_record(device) -> None:
     assert len(blocks) == 6 and n == 90
     with pytest.raises(KeyError):
         pre.swap_in("a", kp, vp)
+
+
+def test_reference_executor_call_sequence(device) -> None:
+    """The reference executor's order (``edgerag/serve/executor.py:124-128``, ``:151-153``):
+    ``table.ensure_capacity(seq_len + n)`` first, then ``update(k, v, layer)`` for every layer.
+    The pre-grown table takes no further block, and each layer's history is exact."""
+    allocator = BlockAllocator(16, BLOCK)
+    cache = make_cache(allocator, device)
+    g = seeded(4)
+    chunks = [torch.randn(1, 2, n, 8, generator=g) for n in (21, 1, 16, 1, 3)]
+    for c in chunks:
+        cache.table.ensure_capacity(cache.seq_len + c.shape[2])
+        used = allocator.num_used
+        for layer in range(2):
+            keys, values = cache.update(c.to(device), (c * 3).to(device), layer)
+        assert allocator.num_used == used
+    history = torch.cat(chunks, dim=2)
+    assert cache.seq_len == history.shape[2]
+    assert torch.equal(keys.cpu(), history) and torch.equal(values.cpu(), history * 3)
+    assert len(cache.table.blocks) == op.blocks_needed(cache.seq_len, BLOCK)
+    allocator.check_invariants()

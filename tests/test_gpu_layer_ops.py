@@ -113,3 +113,31 @@ def test_argmax_rows_is_torch_argmax(device, dtype, rows, cols) -> None:
     for view in (xd[:, :cols].contiguous(), xd[:, :cols]):  # contiguous, then strided rows
         got = kernels.argmax_rows(view).cpu()
         assert torch.equal(got, x[:, :cols].argmax(dim=-1).to(torch.int32))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_positions_outside_the_rope_table_give_nan_not_a_clamp(device, dtype) -> None:
+    """A position outside the caller's cos/sin table has no rotation to give: the token's q and k
+    come out NaN in both the launch and the per-token rows of the fused projection, while the
+    in-table tokens keep their exact values and v is still appended."""
+    d, n_q, n_kv, bs, nb, max_pos = 64, 4, 2, 16, 4, 64
+    g = seeded(77)
+    T = 4
+    qkv = torch.randn(T, (n_q + 2 * n_kv) * d, generator=g).to(dtype)
+    positions = torch.tensor([3, 64, -1, 63], dtype=torch.int32)  # 64 and -1: no row
+    slots = torch.tensor([0, 1, 2, 3], dtype=torch.int32)
+    table = RotaryTable(d, 10000.0, max_pos, device, dtype)
+    kp = torch.zeros(n_kv, nb, bs, d, dtype=dtype, device=device)
+    vp = torch.zeros_like(kp)
+    q = kernels.rope_append(qkv.to(device), positions.to(device), table.cos, table.sin, n_q, n_kv,
+                            d, slots.to(device), kp, vp).cpu()
+    kc, vc = kp.cpu(), vp.cpu()
+    heads = qkv.view(T, n_q + 2 * n_kv, d)
+    for t, bad in enumerate([False, True, True, False]):
+        assert bool(q[t].isnan().all()) == bad and bool(q[t].isnan().any()) == bad
+        assert bool(kc[:, 0, t].isnan().all()) == bad and bool(kc[:, 0, t].isnan().any()) == bad
+        assert torch.equal(vc[:, 0, t], heads[t, n_q + n_kv :])
+    cos_rows, sin_rows = kernels.rope_rows(positions.to(device), table.cos, table.sin)
+    assert cos_rows[[1, 2]].isnan().all() and sin_rows[[1, 2]].isnan().all()
+    assert torch.equal(cos_rows[[0, 3]], table.cos[[3, 63]])
+    assert torch.equal(sin_rows[[0, 3]], table.sin[[3, 63]])

@@ -244,3 +244,55 @@ def test_preemption_mid_decode_keeps_the_generated_tokens(device, policy) -> Non
     if policy == "swap":
         assert pre.counters.swapped_out == 2 and pre.counters.swapped_in == 2
     assert alloc.num_free == alloc.num_blocks and not pre.swapped
+
+
+class _ReferenceShapedRequest:
+    """Only the fields of the reference ``Request`` (``edgerag/sched/request.py:37-96``): no
+    ``prefill_len``, ``prefill_ids`` or ``refeed``."""
+
+    def __init__(self, request_id: str, prompt_token_ids: list[int], max_new_tokens: int) -> None:
+        self.request_id = request_id
+        self.prompt_token_ids = prompt_token_ids
+        self.max_new_tokens = max_new_tokens
+        self.prefill_offset = 0
+        self.generated_token_ids: list[int] = []
+        self.cache = None
+        self.prompt_embeds = None
+
+    @property
+    def prompt_len(self) -> int:
+        return len(self.prompt_token_ids)
+
+
+def test_execute_runs_reference_shaped_requests(device) -> None:
+    """The reference engine's loop (``serve/engine.py:191-214``) over reference-shaped requests:
+    the scheduler's growth through ``cache.table.ensure_capacity`` before each forward, then
+    ``execute``; prefill offsets and tokens advanced by the caller. Tokens equal the oracle's."""
+    from edgerag_amd.sched.scheduler import Batch
+
+    model, weights = _model(device, seed=6)
+    oracle = om.OracleDecoder(weights, torch.float32)
+    alloc = BlockAllocator(64, 16)
+    executor = ModelExecutor(model, TOY, alloc, device, model.dtype, chunk_size=16)
+    reqs = [_ReferenceShapedRequest("a", _prompt(37, 20), 5),
+            _ReferenceShapedRequest("b", _prompt(9, 21), 4)]
+    step = 0
+    while any(len(r.generated_token_ids) < r.max_new_tokens for r in reqs):
+        live = [r for r in reqs if len(r.generated_token_ids) < r.max_new_tokens]
+        prefill = [r for r in live if r.prefill_offset < r.prompt_len][:1]
+        decode = [r for r in live if r.prefill_offset >= r.prompt_len]
+        for r in prefill + decode:  # what the reference scheduler's try_allocate does
+            if r.cache is not None:
+                n = min(16, r.prompt_len - r.prefill_offset) if r in prefill else 1
+                r.cache.table.ensure_capacity(r.cache.seq_len + n)
+        out = executor.execute(Batch(step, prefill=prefill, decode=decode))
+        for r in live:
+            r.prefill_offset += out.prefilled.get(r.request_id, 0)
+            if r.request_id in out.tokens:
+                r.generated_token_ids.append(out.tokens[r.request_id])
+        step += 1
+    for r in reqs:
+        assert r.generated_token_ids == oracle.generate(r.prompt_token_ids, r.max_new_tokens)
+        assert r.cache.seq_len == r.prompt_len + r.max_new_tokens - 1
+        r.cache.free()
+    assert alloc.num_free == alloc.num_blocks

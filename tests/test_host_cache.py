@@ -124,33 +124,33 @@ def test_randomized_against_a_list_model() -> None:
 def test_table_growth_is_all_or_nothing_and_counts_blocks() -> None:
     a = BlockAllocator(4, 16)
     t = BlockTable(a)
-    assert t.grow(16) == [0] and t.num_blocks == 1  # exact multiple: no spare block
-    assert t.grow(1) == [1]
+    assert t.append(16) == [0] and t.num_blocks == 1  # exact multiple: no spare block
+    assert t.append(1) == [1]
     other = BlockTable(a)
-    other.grow(32)
+    other.append(32)
     with pytest.raises(OutOfBlocksError):
-        t.grow(40)
+        t.append(40)
     assert t.num_tokens == 17 and t.num_blocks == 2  # unchanged
     assert t.locate(16) == (1, 0)
     with pytest.raises(IndexError):
         t.locate(17)  # never written
     assert t.shrink_to(10) == 1 and t.num_blocks == 1
-    assert t.release() == 1 and a.num_free == 2
+    assert t.free() == 1 and a.num_free == 2
 
 
 def test_slots_pack_and_step_helpers() -> None:
     a = BlockAllocator(16, 4)
     a.allocate(5)  # offset the ids
     t1, t2 = BlockTable(a), BlockTable(a)
-    t1.grow(6)
-    t2.grow(9)
+    t1.append(6)
+    t2.append(9)
     assert t1.slots(0, 6).tolist() == [20, 21, 22, 23, 24, 25]
     bt = pack_tables([t1, t2])
     assert bt.shape == (2, 3) and bt[0].tolist() == [5, 6, -1] and bt[1].tolist() == [7, 8, 9]
     assert step_slots([t1, t2], [1, 2]).tolist() == [25, 35, 36]
     fork = t2.fork()
-    assert a.is_shared(7) and fork.make_private(2) == (9, 10)
-    assert fork.blocks.tolist() == [7, 8, 10] and t2.blocks.tolist() == [7, 8, 9]
+    assert a.is_shared(7) and fork.unshare(2) == (9, 10)
+    assert fork.blocks == [7, 8, 10] and t2.blocks == [7, 8, 9]
 
 
 # --- the executor's step reservation ----------------------------------------------------------
@@ -197,8 +197,8 @@ def test_positions_past_the_rope_table_are_refused() -> None:
     r.move_to(r.state.__class__.PREFILLING)
     r.prefill_offset = 64
     r.cache = ex._cache_for(r)
-    r.cache.table.grow(64)
+    r.cache.table.append(64)
     with pytest.raises(ValueError, match="past the model's 100 positions"):
         ex.execute(Batch(0, prefill=[r]))
     assert r.cache.seq_len == 64 and alloc.num_used == 4
-    assert np.array_equal(r.cache.table.blocks, np.arange(4))
+    assert r.cache.table.blocks == [0, 1, 2, 3]

@@ -14,7 +14,7 @@ from edgerag_amd.cache.preemption import PreemptionPolicy, Preemptor
 
 def _request(alloc, n_tokens):
     table = BlockTable(alloc)
-    table.grow(n_tokens)
+    table.append(n_tokens)
     cache = types.SimpleNamespace(table=table, key_pool=None, value_pool=None)
     return types.SimpleNamespace(request_id="r", cache=cache, swap=None)
 

@@ -28,10 +28,10 @@ class _FakeCache:
         self.table = BlockTable(allocator=allocator)
 
     def grow(self, n: int) -> None:
-        self.table.grow(n)
+        self.table.append(n)
 
     def free(self) -> int:
-        return self.table.release()
+        return self.table.free()
 
 
 def _run_step(s: Scheduler, alloc: BlockAllocator, chunk: int, rng: random.Random | None = None):
