@@ -606,6 +606,67 @@ def run_cfg3(device, args):
     return res
 
 
+# --- single-sequence fused decode attention (the reference's published shape) --------------------
+
+SINGLE_SEQ_LENS = (128, 512, 1024, 2048, 4096, 6758, 7992)
+
+
+def bench_single_seq(device, lens=SINGLE_SEQ_LENS, batch=1, num_blocks=16384):
+    """``fused_paged_attention`` at the reference's published shape (``CONTEXT.md:1584-1592``):
+    one (or ``batch``) decode query, 32/32 heads of 64, fp16, 16-token blocks, at each context
+    length. Every launch of a replayed HIP graph attends a different sequence (disjoint shuffled
+    block tables over a 16,384-block pool, 2 GiB of K + V), so the K/V stream from HBM, not the
+    Infinity Cache. ``us`` is the launch-to-launch time (the merge launch included where the plan
+    cuts contexts into parts); bytes = K/V read + q/out + block table."""
+    gd = torch.Generator(device=device).manual_seed(17)
+    shape = (H, num_blocks, BS, D)
+    kp = torch.randn(shape, generator=gd, device=device, dtype=torch.float16)
+    vp = torch.randn(shape, generator=gd, device=device, dtype=torch.float16)
+    g = torch.Generator().manual_seed(17)
+    rows = []
+    for L in lens:
+        nb = math.ceil(L / BS)
+        # >= 1.2 GB of distinct K/V per replay, or the whole pool.
+        n_seq = min(num_blocks // (nb * batch),
+                    max(64, math.ceil(1.2e9 / (batch * L * KV_BYTES_PER_TOKEN))))
+        n_launch = max(64, n_seq)
+        perm = torch.randperm(num_blocks, generator=g).numpy().astype(np.int32)
+        plans, qs, outs = [], [], []
+        for i in range(n_seq):
+            bt = perm[i * nb * batch : (i + 1) * nb * batch].reshape(batch, nb)
+            qsl = np.arange(batch + 1, dtype=np.int32)
+            plan, _ = kernels.plan_attention(qsl, np.full(batch, L, np.int32), bt, H, H, D, BS,
+                                             torch.float16, device)
+            plans.append(plan)
+            qs.append(torch.randn(batch, H, D, generator=gd, device=device, dtype=torch.float16))
+            outs.append(torch.empty(batch, H, D, device=device, dtype=torch.float16))
+        for i in range(n_seq):
+            kernels.paged_attention(qs[i], kp, vp, plans[i], D**-0.5, out=outs[i])
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(n_launch):
+                j = i % n_seq
+                kernels.paged_attention(qs[j], kp, vp, plans[j], D**-0.5, out=outs[j])
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(5):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (5 * n_launch)
+        del graph
+        nbytes = batch * (L * KV_BYTES_PER_TOKEN + 2 * H * D * 2 + nb * 4)
+        ph = plans[0].plan_host
+        rows.append([L, round(us, 2), round(nbytes / us / 1e3, 1),
+                     round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), int(ph[2]), int(ph[16] > 0)])
+    del kp, vp
+    torch.cuda.empty_cache()
+    return {"batch": batch, "cols": ["L", "us", "gbs", "frac", "items", "merge"], "rows": rows}
+
+
 # --- config 5: end-to-end serving ---------------------------------------------------------------
 
 
@@ -669,7 +730,8 @@ def main() -> None:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-cfg5", action="store_true", help="skip the end-to-end serving run")
     ap.add_argument("--cfg5-requests", type=int, default=64)
-    ap.add_argument("--only", choices=["cfg3", "cfg4", "cfg5", "lm_head"], default=None,
+    ap.add_argument("--only", choices=["cfg3", "cfg4", "cfg5", "lm_head", "single_seq"],
+                    default=None,
                     help="run just one secondary config (for profiling); prints its record")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -686,6 +748,10 @@ def main() -> None:
         return
     if args.only == "lm_head":
         print(json.dumps({"lm_head": bench_lm_head(device)}), flush=True)
+        return
+    if args.only == "single_seq":
+        print(json.dumps({"single_seq": bench_single_seq(device),
+                          "batch2": bench_single_seq(device, batch=2)}), flush=True)
         return
     if args.only == "cfg5":
         print(json.dumps({"cfg5": run_cfg5(device, args.cfg5_requests, not args.no_cpu)}),

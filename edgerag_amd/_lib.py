@@ -105,6 +105,7 @@ SIGNATURES: dict[str, tuple[list, object]] = {
         [c_vp, c_i64, c_i32, c_i32, c_vp, c_i32, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp], c_i32,
     ),
     "edgerag_lm_head_workspace_bytes": ([c_i32, c_i32], c_i64),
+    "edgerag_attn_fixed_row_items": ([c_i32, c_i32, c_i32, c_i32], c_i64),
     "edgerag_lm_head_argmax_supported": ([c_i32, c_i32], c_i32),
     "edgerag_quantize": ([c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp, c_vp], c_i32),
     "edgerag_dequantize": ([c_vp, c_vp, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp], c_i32),

@@ -61,6 +61,25 @@ constexpr int32_t kPlanVersion = plan::kVersion;
 #ifndef EDGERAG_ROW_WG_PART_TILES
 #define EDGERAG_ROW_WG_PART_TILES 512  // the same, in a batch with prefill tiles beside the rows
 #endif
+#ifndef EDGERAG_ROW_WG_WAVES
+#define EDGERAG_ROW_WG_WAVES 16  // waves of a workgroup over a whole context
+#endif
+#ifndef EDGERAG_ROW_PART_WAVES
+#define EDGERAG_ROW_PART_WAVES 8  // waves of a workgroup over a part of a context
+#endif
+#ifndef EDGERAG_ROW_TARGET_WGS
+#define EDGERAG_ROW_TARGET_WGS 512  // row workgroups a batch of few decodes is cut into
+#endif
+#ifndef EDGERAG_ROW_MIN_WAVE_TOKENS
+#define EDGERAG_ROW_MIN_WAVE_TOKENS 32  // shortest stream a wave of a context part takes
+#endif
+#ifndef EDGERAG_ROW_WG_LONG
+#define EDGERAG_ROW_WG_LONG 0  // 1: contexts past the per-wave cap in part workgroups too
+#endif
+constexpr int kRowWgWaves = EDGERAG_ROW_WG_WAVES;
+constexpr int kRowPartWaves = EDGERAG_ROW_PART_WAVES;
+constexpr int kRowTargetWgs = EDGERAG_ROW_TARGET_WGS;
+constexpr int kRowMinWaveTokens = EDGERAG_ROW_MIN_WAVE_TOKENS;
 constexpr int kMaxRowVecs = 8;  // query vectors a decode item may carry (c * n_rep)
 constexpr int kQTile = 16;      // query rows per prefill tile item
 constexpr int kMinSplit = EDGERAG_MIN_SPLIT;  // tokens; shorter splits are not worth a partial
@@ -159,7 +178,8 @@ struct QReg {
 // their slots (kv_append fused in: no other wave reads those pool rows in this launch).
 // WG: one workgroup per row item (blockDim / 64 waves); wave w takes the w-th of equal,
 // block-aligned parts of the item's keys, and the waves' (m, l, acc) merge in LDS before wave 0
-// writes the output (no partials, no merge launch). Otherwise one wave per item (a KV split).
+// writes the output, or, when the item is one of several parts of a context, the part's fp32
+// partial for the merge launch. Otherwise one wave per item (a KV split).
 template <typename T, int D, int QR, int U, bool APPEND, bool WG>
 __global__ __launch_bounds__(WG ? kMaxRowWaves * kWave : kWave) void attn_decode_kernel(
     const T* __restrict__ q, int64_t q_st, int64_t q_sh, const T* __restrict__ kpool,
@@ -176,12 +196,16 @@ __global__ __launch_bounds__(WG ? kMaxRowWaves * kWave : kWave) void attn_decode
   constexpr int STEP = TPW * U;
 
   // The grid may exceed the work list (fixed-size launches replayed from a graph): the item
-  // count of this launch's kind is read from the device plan.
-  if (item_base + int(blockIdx.x) >= plan[limit_word]) return;
-  const int32_t* it = plan + plan[H_ITEM_OFF] + int64_t(item_base + blockIdx.x) * kItemWords;
-  const int r = it[I_REQ], h = it[I_HEAD], qb = it[I_QBEGIN], qc = it[I_QCOUNT];
-  const int split = it[I_SPLIT];
-  int kb = it[I_KVBEGIN], ke = it[I_KVEND];
+  // count of this launch's kind is read from the device plan. The item is read in the same
+  // round trip (items follow the header, and a fixed-capacity plan buffer holds every slot the
+  // grid covers), not after it.
+  const int64_t idx = int64_t(item_base) + blockIdx.x;
+  const int32_t* it = plan + kHeaderWords + idx * kItemWords;
+  const int4 ia = reinterpret_cast<const int4*>(it)[0], ib = reinterpret_cast<const int4*>(it)[1];
+  if (idx >= plan[limit_word]) return;
+  const int r = ia.x, h = ia.y, qb = ia.z, qc = ia.w;  // I_REQ, I_HEAD, I_QBEGIN, I_QCOUNT
+  int kb = ib.x, ke = ib.y;                             // I_KVBEGIN, I_KVEND
+  const int split = ib.z;                               // I_SPLIT
   const int wave = WG ? int(threadIdx.x >> 6) : 0;
   if constexpr (WG) {
     // This wave's part of the keys: equal parts of whole blocks (a part never straddles the
@@ -352,14 +376,26 @@ __global__ __launch_bounds__(WG ? kMaxRowWaves * kWave : kWave) void attn_decode
               if (d < D) a[e] = fmaf(wgt, wg_acc[wv][j][d], a[e]);
             }
           }
-          const float inv = 1.f / fmaxf(lsum, 1.17549435e-38f);
           const int t = qb + v / n_rep;
           const int hq = h * n_rep + (v % n_rep);
-          T* op = out + int64_t(t) * o_st + int64_t(hq) * o_sh;
+          if (nsplit == 1) {
+            const float inv = 1.f / fmaxf(lsum, 1.17549435e-38f);
+            T* op = out + int64_t(t) * o_st + int64_t(hq) * o_sh;
 #pragma unroll
-          for (int e = 0; e < (D + kWave - 1) / kWave; ++e) {
-            const int d = lane + e * kWave;
-            if (d < D) op[d] = from_f32<T>(a[e] * inv);
+            for (int e = 0; e < (D + kWave - 1) / kWave; ++e) {
+              const int d = lane + e * kWave;
+              if (d < D) op[d] = from_f32<T>(a[e] * inv);
+            }
+          } else {  // one of several parts of the context: a partial for the merge launch
+            const int64_t idx =
+                int64_t(part_off) + (int64_t(t - q0) * n_q_heads + hq) * nsplit + split;
+            if (lane == 0) part_ml[idx] = make_float2(mx, lsum);
+            float* pa = part_acc + idx * D;
+#pragma unroll
+            for (int e = 0; e < (D + kWave - 1) / kWave; ++e) {
+              const int d = lane + e * kWave;
+              if (d < D) pa[d] = a[e];
+            }
           }
         }
       }
@@ -727,6 +763,12 @@ template <typename T, int D>
 void dispatch_decode_qr(const Launch& a, int qr, int base, int count, int limit_word,
                         int waves) {
   constexpr int U = D >= 256 ? 2 : kDecodeU;
+#ifdef EDGERAG_WG_U
+  if (waves > 0 && waves < kMaxRowWaves && qr == 1) {
+    launch_decode<T, D, 1, (D >= 256 ? 2 : EDGERAG_WG_U)>(a, base, count, limit_word, waves);
+    return;
+  }
+#endif
   switch (qr) {
     case 1: launch_decode<T, D, 1, U>(a, base, count, limit_word, waves); break;
     case 2: launch_decode<T, D, 2, U>(a, base, count, limit_word, waves); break;
@@ -847,9 +889,9 @@ extern "C" int edgerag_attn_plan_ex(const int32_t* query_start_loc, const int32_
     }
     max_len = std::max(max_len, L);
   }
-  // Decode rows as one workgroup of kMaxRowWaves waves per (request, kv head) whose waves split
+  // Decode rows as one workgroup of kRowWgWaves waves per (request, kv head) whose waves split
   // the keys and merge in LDS, when the fast decode kernel takes them and every row's context
-  // fits kMaxRowWaves parts of at most EDGERAG_ROW_WG_PART tokens. Longer contexts would leave
+  // fits kRowWgWaves parts of at most EDGERAG_ROW_WG_PART tokens. Longer contexts would leave
   // each wave a long, latency-bound stream while the chip idles (measured: cfg2 -2%, cfg5 with 8
   // long requests -5%), so those batches (or any, when asked) keep one workgroup per KV split,
   // merged by the combine launch through fp32 partials. Beside prefill tiles, when the rows'
@@ -858,6 +900,8 @@ extern "C" int edgerag_attn_plan_ex(const int32_t* query_start_loc, const int32_
   // (three 512-token slices beside 24 decodes of up to 7,472 tokens, 768 row workgroups: 0.213
   // -> 0.207 ms per step). Fewer row workgroups than CUs (a 512-token chunk beside 7 decodes,
   // 224 of them) left a few CUs with long streams: -2.5% output tokens/s end to end.
+  static_assert(kRowWgWaves >= 1 && kRowWgWaves <= kMaxRowWaves, "row workgroup size");
+  static_assert(kRowPartWaves >= 1 && kRowPartWaves <= kMaxRowWaves, "part workgroup size");
   int64_t row_items = 0, max_row_len = 0;
   for (int r = 0; r < num_reqs; ++r) {
     const int64_t c = int64_t(query_start_loc[r + 1]) - query_start_loc[r];
@@ -877,18 +921,51 @@ extern "C" int edgerag_attn_plan_ex(const int32_t* query_start_loc, const int32_
   const bool overlap = n_tiles > 0 && row_items > 0 &&
                        ((flags & EDGERAG_PLAN_OVERLAP) ||
                         (n_tiles >= kPlanCUs && work * head_dim * 2 * es >= kOverlapRowBytes));
-  const bool wg_rows =
+  // Batches with fewer row workgroups than CUs (one or a few long decodes: 32 workgroups for a
+  // single request of 32 kv heads) instead cut every context into parts, one workgroup each, so
+  // that about kRowTargetWgs workgroups cover the chip; a context's parts write fp32 partials
+  // that the merge launch combines. Parts are whole blocks, at least kRowMinWaveTokens tokens per
+  // wave (shorter streams are all fixed cost) and at most the per-wave cap above.
+  const bool wg_capable =
       EDGERAG_ROW_WG && !(flags & EDGERAG_PLAN_SPLIT_ROWS) && row_items > 0 && head_dim <= 128 &&
       head_dim % (16 / es) == 0 && head_dim / (16 / es) <= kWave &&
-      block_size % (kWave / (head_dim / (16 / es))) == 0 &&
-      max_row_len <= int64_t(kMaxRowWaves) * (overlap && row_items >= kPlanCUs
-                                                  ? EDGERAG_ROW_WG_PART_TILES
-                                                  : EDGERAG_ROW_WG_PART) &&
-      max_row_len <= int64_t(kMaxRowWaves) * kMaxSplitBlocks * block_size;
-  const int row_waves = wg_rows ? kMaxRowWaves : 0;
+      block_size % (kWave / (head_dim / (16 / es))) == 0;
+  const int64_t wave_cap = std::min<int64_t>(
+      overlap && row_items >= kPlanCUs ? EDGERAG_ROW_WG_PART_TILES : EDGERAG_ROW_WG_PART,
+      int64_t(kMaxSplitBlocks) * block_size);
+  const int64_t part_cap = int64_t(kRowWgWaves) * round_up(wave_cap, block_size);
+  bool wg_rows = false;
+  int row_waves = 0;
+  int64_t wg_part = 0;  // longest part of a context one row workgroup takes (0: whole contexts)
+  if (wg_capable && kRowTargetWgs > 0 && row_items < kPlanCUs) {
+    // Parts take kRowPartWaves waves: single-sequence attention over 6,758 tokens measured
+    // 17.7 us at 8 waves against 21.5 us at 16 and 19.4 us at 4 (with the merge launch).
+    // At most kRowTargetWgs workgroups plus one per (request, kv head) for the rounding: the
+    // parts are never shorter than work / kRowTargetWgs (the waves' block-id registers bound
+    // them only for contexts far past any BASELINE shape).
+    const int64_t min_part = int64_t(kRowPartWaves) * round_up(kRowMinWaveTokens, block_size);
+    const int64_t want = (work + kRowTargetWgs - 1) / kRowTargetWgs;
+    const int64_t cap = int64_t(kRowPartWaves) * kMaxSplitBlocks * block_size;
+    wg_part = std::min(cap, std::max(min_part, round_up(want, block_size)));
+    wg_rows = true;
+    row_waves = kRowPartWaves;
+  } else if (wg_capable && max_row_len <= part_cap) {
+    wg_rows = true;
+    row_waves = kRowWgWaves;
+  } else if (wg_capable && EDGERAG_ROW_WG_LONG) {
+    wg_part = part_cap;
+    wg_rows = true;
+    row_waves = kRowWgWaves;
+  }
+  // Tokens of a row request's parts: equal whole-block parts of at most wg_part tokens.
+  auto wg_split_len = [&](int64_t L) -> int64_t {
+    if (wg_part == 0 || L <= wg_part) return std::max<int64_t>(L, 1);
+    const int64_t n = (L + wg_part - 1) / wg_part;
+    return round_up((L + n - 1) / n, block_size);
+  };
+  const int64_t longest_part = wg_rows ? wg_split_len(max_row_len) : 0;
   const int wg_split_blocks =
-      wg_rows ? int(((max_row_len + kMaxRowWaves - 1) / kMaxRowWaves + block_size - 1) /
-                    block_size)
+      wg_rows ? int(((longest_part + row_waves - 1) / row_waves + block_size - 1) / block_size)
               : 0;
   int64_t split_len = std::max<int64_t>(kMinSplit, (work + kTargetItems - 1) / kTargetItems);
   split_len = round_up(split_len, block_size);
@@ -926,8 +1003,8 @@ extern "C" int edgerag_attn_plan_ex(const int32_t* query_start_loc, const int32_
     const int L = context_lens[r];
     int32_t* rq = reqs.data() + size_t(r) * kReqWords;
     const bool row = c * n_rep <= kMaxRowVecs;
-    // Workgroup-split rows are one item over the whole context (the waves split it).
-    const int64_t slen = row ? (wg_rows ? std::max<int64_t>(L, 1) : split_len) : tile_split_len;
+    // Workgroup-split rows: one item per part of the context (the waves split the part).
+    const int64_t slen = row ? (wg_rows ? wg_split_len(L) : split_len) : tile_split_len;
     const int nsplit = c == 0 ? 0 : int((L + slen - 1) / slen);
     rq[R_NSPLIT] = nsplit;
     rq[R_SPLITLEN] = int32_t(slen);
@@ -967,7 +1044,7 @@ extern "C" int edgerag_attn_plan_ex(const int32_t* query_start_loc, const int32_
 
   const int64_t n_row_items = int64_t(rows.size()) * n_kv_heads;
   const int64_t n_items = n_row_items + int64_t(tiles.size()) * n_kv_heads;
-  const int64_t item_off = kHeaderWords;
+  const int64_t item_off = kHeaderWords;  // the decode kernel reads items at this offset
   const int64_t req_off = item_off + n_items * kItemWords;
   const int64_t combine_off = req_off + int64_t(num_reqs) * kReqWords;  // 16-byte aligned
   const int64_t words = combine_off + int64_t(combine.size());
@@ -1016,6 +1093,27 @@ extern "C" int edgerag_attn_plan_ex(const int32_t* query_start_loc, const int32_
       }
   std::copy(reqs.begin(), reqs.end(), plan + req_off);
   return EDGERAG_OK;
+}
+
+extern "C" int64_t edgerag_attn_fixed_row_items(int32_t max_reqs, int32_t n_kv_heads,
+                                                int32_t max_context, int32_t block_size) {
+  if (max_reqs < 0 || n_kv_heads <= 0 || max_context < 0 || block_size <= 0) return -1;
+  // The planner's row workgroups for decode-only batches (no tiles beside them): whole contexts,
+  // one per (request, kv head); a batch of fewer such workgroups than CUs cut into parts of at
+  // least ceil(work / kRowTargetWgs) tokens (at most kRowTargetWgs plus one per (request, kv
+  // head) for the rounding) or of the per-wave cap, whichever is longer; contexts past the cap
+  // in parts of the cap.
+  const int64_t rh = int64_t(max_reqs) * n_kv_heads;
+  const int64_t wave_cap =
+      std::min<int64_t>(EDGERAG_ROW_WG_PART, int64_t(kMaxSplitBlocks) * block_size);
+  const int64_t part_cap = int64_t(kRowWgWaves) * round_up(wave_cap, block_size);
+  const int64_t per_req = std::max<int64_t>(1, (int64_t(max_context) + part_cap - 1) / part_cap);
+  // Few-row parts: at most kRowTargetWgs + rh, or parts of the block-id cap when that binds.
+  const int64_t small_cap = int64_t(kRowPartWaves) * kMaxSplitBlocks * block_size;
+  const int64_t per_req_small =
+      std::max<int64_t>(1, (int64_t(max_context) + small_cap - 1) / small_cap);
+  return std::max<int64_t>(
+      {kRowTargetWgs + rh, rh * per_req, std::min<int64_t>(rh, kPlanCUs - 1) * per_req_small});
 }
 
 extern "C" int edgerag_attn_plan(const int32_t* query_start_loc, const int32_t* context_lens,
@@ -1262,11 +1360,12 @@ extern "C" int edgerag_paged_attention_fixed(
       !head_dim_supported(head_dim) || block_size <= 0 || num_blocks <= 0)
     return fail(EDGERAG_EINVAL, "edgerag_paged_attention_fixed: bad shape");
   if (row_waves < 0 || row_waves > kMaxRowWaves ||
-      (row_waves > 0 && (head_dim > 128 || max_combine_rows != 0 ||
+      (row_waves > 0 && (head_dim > 128 || elem_size(dtype) == 0 ||
+                         head_dim % (16 / elem_size(dtype)) != 0 ||
                          block_size % (kWave / (head_dim / (16 / elem_size(dtype)))) != 0)))
     return fail(EDGERAG_EINVAL,
                 "edgerag_paged_attention_fixed: row_waves %d (1..%d workgroup-split rows need "
-                "head_dim <= 128, the fast decode kernel's block sizes and no combine rows)",
+                "head_dim <= 128 and the fast decode kernel's block sizes)",
                 row_waves, kMaxRowWaves);
   if (!(scale > 0.f) || !std::isfinite(scale))
     return fail(EDGERAG_EINVAL, "edgerag_paged_attention_fixed: scale must be positive");
@@ -1275,10 +1374,8 @@ extern "C" int edgerag_paged_attention_fixed(
   if (!aligned16(key_pool) || !aligned16(value_pool) || !aligned16(q) ||
       (q_stride_tok * es) % 16 != 0 || (q_stride_head * es) % 16 != 0)
     return fail(EDGERAG_EINVAL, "edgerag_paged_attention_fixed: q and pools must be 16-byte aligned");
-  const int64_t acc_off = round_up(max_partials * int64_t(sizeof(float2)), 256);
-  const int64_t need = max_partials > 0
-                           ? acc_off + round_up(max_partials * head_dim * int64_t(sizeof(float)), 256)
-                           : 0;
+  const WorkspaceLayout ws = workspace_layout(max_partials, head_dim);
+  const int64_t need = ws.total;
   if (workspace_bytes < need || (need > 0 && workspace == nullptr))
     return fail(EDGERAG_EWORKSPACE, "edgerag_paged_attention_fixed: workspace %lld bytes, need %lld",
                 (long long)workspace_bytes, (long long)need);
@@ -1302,8 +1399,9 @@ extern "C" int edgerag_paged_attention_fixed(
   a.out = out;
   a.o_st = out_stride_tok;
   a.o_sh = out_stride_head;
-  a.ml = reinterpret_cast<float2*>(workspace);
-  a.pacc = reinterpret_cast<float*>(static_cast<char*>(workspace) + acc_off);
+  char* wsp = static_cast<char*>(workspace);
+  a.ml = reinterpret_cast<float2*>(wsp);
+  a.pacc = reinterpret_cast<float*>(wsp + ws.acc_off);
   const int qr = std::min(8, pow2_at_least(max_row_vecs));
   int rc = EDGERAG_OK;
   if (max_row_items > 0) {

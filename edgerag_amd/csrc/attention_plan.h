@@ -36,12 +36,14 @@ enum Header {
   H_TILE_KIND,         // 0: prefill tiles run on the row kernel, 1: on the MFMA tile kernel
   H_ROW_WAVES,         // 0: decode rows split across workgroups (partials + combine list);
                        // W > 0: one workgroup per row item, its W waves split the keys and
-                       // merge in LDS (no partials)
+                       // merge in LDS (partials only where a context is cut into parts)
   H_OVERLAP,           // 1: planned for tiles and rows on two streams (tiles shared), 0: one
 };
 // Waves a workgroup-split row item may use (the kernel's LDS merge is sized for this many).
 constexpr int kMaxRowWaves = 16;
 enum Item { I_REQ = 0, I_HEAD, I_QBEGIN, I_QCOUNT, I_KVBEGIN, I_KVEND, I_SPLIT, I_PAD };
+static_assert(kItemWords == 8 && I_KVBEGIN == 4 && I_PAD == 7,
+              "the decode kernel reads an item as two int4 words");
 enum Req { R_NSPLIT = 0, R_SPLITLEN, R_PARTOFF, R_PAD };
 // Combine-list entry: everything one merge needs in a single 32-byte load.
 enum Combine { C_TOK = 0, C_Q0, C_C, C_L, C_NSPLIT, C_SPLITLEN, C_PARTOFF, C_PAD };

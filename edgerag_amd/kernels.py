@@ -559,13 +559,16 @@ class FixedAttention:
         self.max_reqs, self.max_blocks = max_reqs, max_blocks_per_seq
         self.max_row_vecs = min(8, max(1, n_q_heads // n_kv_heads))
         # Capacities of both launch modes: KV splits (items, merge rows, partials) and
-        # workgroup-split rows (one workgroup per request and kv head).
+        # workgroup-split rows (one workgroup per request and kv head, or per part of a context
+        # when the batch has few requests), the latter bounded by the planner itself.
         self.max_combine = max_reqs
-        max_splits = -(-max_blocks_per_seq * block_size // min_split)
+        max_splits = -(-max_blocks_per_seq * block_size // min(min_split, 128))
         self.max_partials = max_reqs * n_q_heads * max_splits
         self.max_items = max_items
-        self.wg_items = max_reqs * n_kv_heads
+        self.wg_items = int(_lib.load().edgerag_attn_fixed_row_items(
+            max_reqs, n_kv_heads, max_blocks_per_seq * block_size, block_size))
         self.row_waves = 0
+        self.combine = False
         self.plan_words = 24 + 8 * max_items + 4 * max_reqs + 8 * self.max_combine + 64
 
         def pad(n: int) -> int:
@@ -611,9 +614,9 @@ class FixedAttention:
                                  self.head_dim, self.block_size, self.max_blocks, self.dtype,
                                  self.split_rows)
         n_items, n_row, n_partials = int(plan[2]), int(plan[13]), int(plan[6])
-        row_waves = int(plan[19])
+        row_waves, n_combine = int(plan[19]), int(plan[16])
         if (n_items != n_row or n_row > (self.wg_items if row_waves else self.max_items)
-                or int(plan[16]) > (0 if row_waves else self.max_combine)
+                or n_combine > self.max_combine
                 or int(plan[14]) > self.max_row_vecs or n_partials > self.max_partials
                 or plan.size > self.plan_words):
             return False
@@ -634,17 +637,22 @@ class FixedAttention:
         self.buf[t0:t1].copy_(self.host[t0:t1], non_blocking=True)
         self.num_reqs = R
         self.row_waves = row_waves
+        self.combine = n_combine > 0
         return True
+
+    @property
+    def mode(self) -> tuple[int, bool]:
+        """The launch shape the staged plan needs: (row waves, merge launch). A graph captured
+        in one mode replays every plan staged in that mode."""
+        return self.row_waves, self.combine
 
     def launch(self, query: torch.Tensor, key_pool: torch.Tensor, value_pool: torch.Tensor,
                scale: float, out: torch.Tensor) -> torch.Tensor:
         n_kv, num_blocks, block_size, head_dim = key_pool.shape
         if query.stride(2) != 1 or out.stride(2) != 1:
             raise ValueError("query and out need a contiguous head_dim axis")
-        if self.row_waves:
-            items, combine, partials = self.wg_items, 0, 0
-        else:
-            items, combine, partials = self.max_items, self.max_combine, self.max_partials
+        items = self.wg_items if self.row_waves else self.max_items
+        combine, partials = (self.max_combine, self.max_partials) if self.combine else (0, 0)
         call(
             "edgerag_paged_attention_fixed", self.plan.data_ptr(), items, combine,
             self.max_row_vecs, partials, self.row_waves, query.data_ptr(),

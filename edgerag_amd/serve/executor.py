@@ -315,7 +315,7 @@ class ModelExecutor:
         """Logits ``(n, vocab)`` of a staged decode-only step of ``n`` requests and their greedy
         tokens (int32 ``(n,)``), both computed inside the replayed graph."""
         fx = self._fixed
-        key = (n, fx.row_waves)
+        key = (n, *fx.mode)
         entry = self._graphs.get(key)
         if entry is None:
             slots, pos, ids, rows = (e[:n] for e in fx.extras)

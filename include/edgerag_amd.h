@@ -226,13 +226,21 @@ int edgerag_paged_attention_append(
  * max_partials partials: (m, l) pairs at offset 0, accumulators at round_up(8 * max_partials,
  * 256); size it with that formula. Semantics are those of edgerag_paged_attention.
  * row_waves > 0 runs workgroup-split rows instead (one workgroup of row_waves waves per row item,
- * merged in LDS; plans with a nonzero EDGERAG plan word H_ROW_WAVES, i.e. planned without
- * EDGERAG_PLAN_SPLIT_ROWS, contexts up to row_waves * 64 blocks): then max_combine_rows must be
- * 0 and no workspace is needed.
+ * merged in LDS; plans whose word 19, the row-wave count, is nonzero, i.e. planned without
+ * EDGERAG_PLAN_SPLIT_ROWS). Such a plan may still cut a context into parts (one row item each,
+ * merged by the combine launch through partials: batches of few decodes); pass
+ * max_combine_rows = 0 only for plans without combine rows (word 16 zero), which then need no
+ * workspace.
  *
  * No counterpart in the reference: it exists so that the decode step of the serving loop
  * (edgerag/serve/executor.py:138-154 replaced by one packed forward) can be replayed from a graph.
  */
+/* Upper bound on the row items of any decode-only plan with a nonzero row-wave count that
+ * edgerag_attn_plan makes for at most max_reqs requests of contexts up to max_context tokens:
+ * the max_row_items to pass edgerag_paged_attention_fixed with row_waves > 0. -1 for bad
+ * arguments. */
+int64_t edgerag_attn_fixed_row_items(int32_t max_reqs, int32_t n_kv_heads, int32_t max_context,
+                                     int32_t block_size);
 int edgerag_paged_attention_fixed(const int32_t* plan_dev, int32_t max_row_items,
                                   int32_t max_combine_rows, int32_t max_row_vecs,
                                   int64_t max_partials, int32_t row_waves, const void* q,

@@ -173,9 +173,12 @@ def test_validation_errors_come_back_as_messages() -> None:
     with pytest.raises(_lib.EdgeragError, match="capacities"):
         _lib.call("edgerag_paged_attention_fixed", 16, -1, 0, 1, 0, 0, 16, 0, 0, 16, 16, 1, 16,
                   0, 16, 16, 4, 4, 64, 16, 1, 1.0, 16, 0, 0, None, 0, None)
-    with pytest.raises(_lib.EdgeragError, match="row_waves"):
-        _lib.call("edgerag_paged_attention_fixed", 16, 4, 4, 1, 0, 16, 16, 0, 0, 16, 16, 1, 16,
+    with pytest.raises(_lib.EdgeragError, match="row_waves"):  # past the 16-wave merge space
+        _lib.call("edgerag_paged_attention_fixed", 16, 4, 0, 1, 0, 17, 16, 0, 0, 16, 16, 1, 16,
                   0, 16, 16, 4, 4, 64, 16, 1, 1.0, 16, 0, 0, None, 0, None)
+    with pytest.raises(_lib.EdgeragError, match="row_waves"):  # head_dim past 128
+        _lib.call("edgerag_paged_attention_fixed", 16, 4, 0, 1, 0, 16, 16, 0, 0, 16, 16, 1, 16,
+                  0, 16, 16, 4, 4, 256, 16, 1, 1.0, 16, 0, 0, None, 0, None)
     with pytest.raises(_lib.EdgeragError, match="width"):
         _lib.call("edgerag_rmsnorm", None, 0, None, 0, None, None, 0, None, 0, 1, 0, 1e-5, 1,
                   None)
@@ -245,6 +248,38 @@ def check_coverage(qsl, ctx, n_q, n_kv, bs=16):
     return items
 
 
+def check_parts(ctx, h, bs, items, reqs, plan) -> None:
+    """A batch of fewer row workgroups than CUs: each context in equal whole-block parts of at
+    least 8 waves x 32 tokens, about 512 workgroups in all (never more than 512 plus one per
+    request and head), one combine row per request cut into several parts."""
+    work = sum(ctx) * h
+    part = min(8 * 64 * bs, max(8 * 32, -(-(-(-work // 512)) // bs) * bs))
+    for r, L in enumerate(ctx):
+        n = -(-L // part) if L > part else 1
+        slen = max(L, 1) if n == 1 else -(-(-(-L // n)) // bs) * bs
+        assert (int(reqs[r][0]), int(reqs[r][1])) == (-(-L // slen) if L else 0, slen), r
+    assert items.shape[0] <= 512 + len(ctx) * h
+    assert int(plan[16]) == sum(1 for r in range(len(ctx)) if int(reqs[r][0]) > 1)
+
+
+def test_fixed_capacity_bounds_the_planner() -> None:
+    """edgerag_attn_fixed_row_items bounds the row items of every decode-only plan with
+    workgroup rows, across batch sizes and context lengths."""
+    q = _lib.load().edgerag_attn_fixed_row_items
+    rng = np.random.default_rng(5)
+    for cap in (1, 2, 4, 8):
+        bound = q(cap, 32, 8192, 16)
+        assert bound >= 512
+        for _ in range(60):
+            n = int(rng.integers(1, cap + 1))
+            ctx = rng.integers(1, 8193, n).astype(np.int32)
+            plan, _ = kernels.make_plan_host(np.arange(n + 1, dtype=np.int32), ctx, 32, 32, 64,
+                                             16, 512, torch.float16)
+            if int(plan[19]):
+                assert int(plan[13]) <= bound, (cap, ctx.tolist())
+    assert q(-1, 32, 8192, 16) == -1
+
+
 @given(
     reqs=st.lists(
         st.tuples(st.integers(0, 3000), st.integers(0, 600)), min_size=1, max_size=12
@@ -287,14 +322,19 @@ def test_plan_rejects_bad_batches() -> None:
 
 def test_plan_size_query_without_buffer() -> None:
     words, ws = ctypes.c_int64(0), ctypes.c_int64(0)
+    qsl = np.arange(9, dtype=np.int32)
+    ctx = np.full(8, 4000, np.int32)
+    _lib.call("edgerag_attn_plan", qsl.ctypes.data, ctx.ctypes.data, 8, 32, 32, 64, 16, 400, 1,
+              None, 0, ctypes.byref(words), ctypes.byref(ws))
+    assert words.value > 16 and ws.value == 0  # a workgroup per (request, head): no partials
+    _lib.call("edgerag_attn_plan_ex", qsl.ctypes.data, ctx.ctypes.data, 8, 32, 32, 64, 16, 400, 1,
+              _lib.PLAN_SPLIT_ROWS, None, 0, ctypes.byref(words), ctypes.byref(ws))
+    assert words.value > 16 and ws.value > 0  # KV splits: fp32 partials
     qsl = np.array([0, 1], np.int32)
     ctx = np.array([4000], np.int32)
     _lib.call("edgerag_attn_plan", qsl.ctypes.data, ctx.ctypes.data, 1, 32, 32, 64, 16, 400, 1,
               None, 0, ctypes.byref(words), ctypes.byref(ws))
-    assert words.value > 16 and ws.value == 0  # workgroup-split rows: no partials
-    _lib.call("edgerag_attn_plan_ex", qsl.ctypes.data, ctx.ctypes.data, 1, 32, 32, 64, 16, 400, 1,
-              _lib.PLAN_SPLIT_ROWS, None, 0, ctypes.byref(words), ctypes.byref(ws))
-    assert words.value > 16 and ws.value > 0  # KV splits: fp32 partials
+    assert ws.value > 0  # one request: its context cut into parts, merged through partials
     ctx = np.array([5000], np.int32)
     _lib.call("edgerag_attn_plan", qsl.ctypes.data, ctx.ctypes.data, 1, 32, 32, 64, 16, 400, 1,
               None, 0, ctypes.byref(words), ctypes.byref(ws))
@@ -308,31 +348,41 @@ def test_plan_size_query_without_buffer() -> None:
 @pytest.mark.parametrize(
     "ctx,d,bs,split_rows,row_waves,row_waves_tiles",
     [
-        ([4096, 1, 300], 64, 16, False, 16, 16),  # every decode context short: workgroup rows
-        # One longer than 16 waves x 256 tokens: KV splits; beside prefill tiles workgroup rows
-        # (parts of up to 512 tokens) once their 32 kv heads x 8 requests cover the 256 CUs.
-        ([4097, 1, 300], 64, 16, False, 0, 0),
+        # Fewer than 256 row workgroups (32 kv heads x 3 requests): workgroups of 8 waves over
+        # parts of the contexts, whatever their length.
+        ([4096, 1, 300], 64, 16, False, 8, 8),
+        ([4097, 1, 300], 64, 16, False, 8, 8),
+        ([8000], 64, 16, False, 8, 8),
+        # 256 row workgroups: one per (request, head) when every context fits 16 waves x 256
+        # tokens; else KV splits, but beside prefill tiles workgroup rows (parts of up to 512
+        # tokens per wave) once their 32 kv heads x 8 requests cover the 256 CUs.
+        ([4096] + [300] * 7, 64, 16, False, 16, 16),
         ([4097] + [300] * 7, 64, 16, False, 0, 16),
         ([8193] + [300] * 7, 64, 16, False, 0, 0),  # past 16 waves x 512 tokens: KV splits
         ([4096, 1, 300], 64, 16, True, 0, 0),  # asked for KV splits
         ([2000], 256, 16, False, 0, 0),  # head_dim past the workgroup kernel's 128
-        ([2000], 128, 8, False, 16, 16),
-        ([2000], 64, 32, False, 16, 16),
+        ([2000], 128, 8, False, 8, 8),
+        ([2000], 64, 32, False, 8, 8),
     ],
 )
 def test_plan_row_mode_selection(ctx, d, bs, split_rows, row_waves, row_waves_tiles) -> None:
-    """Decode rows become one workgroup per (request, kv head) when the fast decode kernel takes
-    the shape and every decode context fits 16 waves of at most 256 tokens -- 512 tokens when
-    the plan puts prefill tiles on a second stream beside them (keeping the chip busy) and the
-    rows' workgroups cover every CU."""
+    """Decode rows become workgroups whose waves split the keys and merge in LDS when the fast
+    decode kernel takes the shape: one of 16 waves per (request, kv head) when they cover the
+    256 CUs and every decode context fits 16 waves of at most 256 tokens (512 when the plan puts
+    prefill tiles on a second stream beside them), one of 8 waves per part of a context when
+    they would not cover the CUs."""
     n, h = len(ctx), 32
     plan, ws = kernels.make_plan_host(np.arange(n + 1, dtype=np.int32), np.array(ctx, np.int32),
                                       h, h, d, bs, -(-max(ctx) // bs), torch.float16, split_rows)
     assert int(plan[19]) == row_waves
     items, reqs = decode_plan(plan)
-    if row_waves:
+    if row_waves and n * h >= 256:
         assert ws == 0 and int(plan[16]) == 0
         assert items.shape[0] == n * h and all(int(nsplit) == 1 for nsplit in reqs[:, 0])
+    if row_waves and n * h < 256:
+        check_parts(ctx, h, bs, items, reqs, plan)
+    if row_waves and d == 64 and bs == 16:
+        check_coverage(list(range(n + 1)), ctx, h, h)
     # With a prefill slice of 600 tokens at offset 3000 in the batch.
     qsl = np.array([0, *range(1, n + 1), n + 600], np.int32)
     plan2, _ = kernels.make_plan_host(qsl, np.array([*ctx, 3600], np.int32), h, h, d, bs,

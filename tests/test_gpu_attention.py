@@ -568,3 +568,42 @@ def test_one_and_two_stream_plans_agree(device) -> None:
     torch.testing.assert_close(got1.float(), expected, **FP16_TOL)
     torch.testing.assert_close(got2.float(), expected, **FP16_TOL)
     torch.testing.assert_close(got1, got2, **FP16_TOL)
+
+
+@pytest.mark.parametrize("lens,n_q,n_kv", [
+    ([256], 32, 32), ([1000], 32, 32), ([3000], 32, 32), ([4097], 32, 32), ([6758], 32, 32),
+    ([7472], 32, 32), ([256, 7472], 32, 32), ([3000, 4100], 32, 32), ([7472, 7000], 32, 32),
+    ([5000], 9, 3), ([2500, 700], 8, 1),
+])
+def test_few_decodes_as_context_parts_fp16(device, lens, n_q, n_kv) -> None:
+    """Batches of one or two decodes (fewer row workgroups than CUs): every context cut into
+    parts of 8-wave workgroups merged by the combine launch, slack poisoned with 1e4; against
+    the oracle at the fp16 gate tolerance. The append fused into the same launch writes the pools
+    exactly as kv_append does."""
+    d = 64
+    q_lens = [1] * len(lens)
+    kp, vp, tables, qsl, q, bt = _ragged_case(lens, q_lens, n_q, n_kv, d, torch.float16,
+                                              sum(lens) + n_q)
+    plan_host, _ = kernels.make_plan_host(qsl, np.asarray(lens, np.int32), n_q, n_kv, d,
+                                          BLOCK_SIZE, bt.shape[1], torch.float16)
+    assert int(plan_host[19]) == 8, "expected workgroups over parts of the contexts"
+    assert (int(plan_host[16]) > 0) == any(L > 256 for L in lens)  # parts of >= 8 x 32 tokens
+    got = _run_ragged(device, kp, vp, qsl, lens, bt, q, d**-0.5)
+    expected = oa.ragged_reference(q, kp, vp, qsl.tolist(), lens, tables, d**-0.5)
+    torch.testing.assert_close(got.float(), expected, **FP16_TOL)
+    # The append fused into the parts' launch: the step's own token read from the new rows.
+    g = seeded(len(lens) + 7)
+    nk = torch.randn(len(lens), n_kv, d, generator=g).half()
+    nv = torch.randn(len(lens), n_kv, d, generator=g).half()
+    slots = torch.tensor([tables[r][(L - 1) // BLOCK_SIZE] * BLOCK_SIZE + (L - 1) % BLOCK_SIZE
+                          for r, L in enumerate(lens)], dtype=torch.int32)
+    plan, (slots_d,) = kernels.plan_attention(qsl, np.asarray(lens, np.int32), bt, n_q, n_kv, d,
+                                              BLOCK_SIZE, torch.float16, device, [slots.numpy()])
+    qd, nkd, nvd = q.to(device), nk.to(device), nv.to(device)
+    kp1, vp1 = kp.to(device), vp.to(device)
+    kernels.kv_append(nkd, nvd, slots_d, kp1, vp1)
+    ref = kernels.paged_attention(qd, kp1, vp1, plan, d**-0.5)
+    kp2, vp2 = kp.to(device), vp.to(device)
+    fused = kernels.paged_attention_append(nkd, nvd, slots_d, qd, kp2, vp2, plan, d**-0.5)
+    assert torch.equal(fused, ref)
+    assert torch.equal(kp2, kp1) and torch.equal(vp2, vp1)

@@ -60,10 +60,12 @@ def _tables(lens, bs, num_blocks, g):
 
 @pytest.mark.parametrize("split_rows", [False, True])
 def test_fixed_attention_long_contexts_split_merge_and_graph_replays(device, split_rows) -> None:
-    """Both row modes of the fixed launch, switching from step to step as the planner picks
+    """Every row mode of the fixed launch, switching from step to step as the planner picks
     them: KV splits merged by the combine launch (which reads its row count from the device
     plan header) for long contexts, workgroup-split rows (16 waves per (request, head), merged in
-    LDS) when every context is short. One graph per mode replays every plan of that mode."""
+    LDS) when every context is short, and workgroups over parts of the contexts merged by the
+    combine launch when the batch is small. One graph per mode replays every plan of that
+    mode."""
     n_q = n_kv = 32
     d, bs, cap = 64, 16, 8
     max_blocks = math.ceil(7472 / bs)
@@ -80,7 +82,7 @@ def test_fixed_attention_long_contexts_split_merge_and_graph_replays(device, spl
         "B": [7472, 2000, 100],
         "C": [256, 3000, 7471, 90, 1800],
         "D": [4096, 17, 1000, 2500, 1, 4000, 33, 700],  # every context short
-        "E": [300, 16, 4095],
+        "E": [300, 16, 3000],
     }
     g = seeded(41)
     cases = {}
@@ -91,14 +93,22 @@ def test_fixed_attention_long_contexts_split_merge_and_graph_replays(device, spl
         plan_host, _ = kernels.make_plan_host(qsl, np.asarray(lens, np.int32), n_q, n_kv, d, bs,
                                               max_blocks, torch.float16, split_rows)
         cases[name] = (lens, tables, bt, qsl, q, plan_host)
-    for name in "ABC":  # long contexts: KV splits, with merge rows and differing partial counts
-        assert int(cases[name][5][19]) == 0 and int(cases[name][5][16]) > 0
-    assert len({int(cases[n][5][6]) for n in "ABC"}) == 3
-    for name in "DE":
-        if split_rows:
-            assert int(cases[name][5][19]) == 0
+    # A: 8 requests with a context past 16 waves x 256 tokens: KV splits and merge rows. B, C,
+    # E: 3-5 requests, fewer workgroups than CUs: workgroups of 8 waves over parts of the
+    # contexts, merged by the combine launch. D: 8 short contexts: a workgroup of 16 waves per
+    # (request, head), no merge.
+    for name in "ABCDE":
+        plan = cases[name][5]
+        if split_rows or name == "A":
+            assert int(plan[19]) == 0 and int(plan[16]) > 0
+        elif name == "D":
+            assert int(plan[19]) == 16 and int(plan[6]) == 0
         else:
-            assert int(cases[name][5][19]) == 16 and int(cases[name][5][6]) == 0
+            assert int(plan[19]) == 8 and int(plan[16]) > 0
+    # B, C, E share one launch mode; their items, merge rows and partials (read on the device)
+    # differ.
+    assert len({(int(cases[n][5][6]), int(cases[n][5][13]), int(cases[n][5][16]))
+                for n in "BCE"}) == 3
 
     kp_cpu, vp_cpu = kp.cpu(), vp.cpu()
     graphs = {}
@@ -106,11 +116,11 @@ def test_fixed_attention_long_contexts_split_merge_and_graph_replays(device, spl
         lens, tables, bt, qsl, q, _ = cases[name]
         torch.cuda.synchronize()  # update() reuses its pinned staging buffer
         assert fx.update(qsl, np.asarray(lens, np.int32), bt, [])
-        assert fx.row_waves == int(cases[name][5][19])
+        assert fx.mode == (int(cases[name][5][19]), int(cases[name][5][16]) > 0)
         q_static.zero_()
         q_static[: len(lens)].copy_(q.to(device))
         out.fill_(float("nan"))
-        if fx.row_waves not in graphs:
+        if fx.mode not in graphs:
             side = torch.cuda.Stream(device)
             side.wait_stream(torch.cuda.current_stream(device))
             graph = torch.cuda.CUDAGraph()
@@ -119,11 +129,11 @@ def test_fixed_attention_long_contexts_split_merge_and_graph_replays(device, spl
                 with torch.cuda.graph(graph, stream=side):
                     fx.launch(q_static, kp, vp, 0.125, out)
             torch.cuda.current_stream(device).wait_stream(side)
-            graphs[fx.row_waves] = graph
+            graphs[fx.mode] = graph
             out.fill_(float("nan"))
-        print(f"fixed attention replay, plan {name}: {len(lens)} requests, row_waves "
-              f"{fx.row_waves}", flush=True)
-        graphs[fx.row_waves].replay()
+        print(f"fixed attention replay, plan {name}: {len(lens)} requests, mode {fx.mode}",
+              flush=True)
+        graphs[fx.mode].replay()
         torch.cuda.synchronize()
         got = out[: len(lens)].clone()
         eager_plan, _ = kernels.plan_attention(qsl, np.asarray(lens, np.int32), bt, n_q, n_kv, d,
@@ -162,10 +172,12 @@ def _run_recording(model, spec, prompts, max_new, chunk, device, num_blocks, gra
 
 
 def _check_against_oracle(oracle, prompt, steps, tag):
-    """Teacher-forced: prefill the prompt, then feed the GPU's own tokens, comparing every
-    step's logits (the GPU's greedy choices may differ from the oracle's only at near-ties)."""
+    """Teacher-forced: prefill the prompt (in 512-token chunks, which keeps the oracle's logits
+    and masks small), then feed the GPU's own tokens, comparing every step's logits (the GPU's
+    greedy choices may differ from the oracle's only at near-ties)."""
     oracle.reset()
-    ref = oracle.forward(prompt)[-1]
+    for start in range(0, len(prompt), 512):
+        ref = oracle.forward(prompt[start : start + 512])[-1]
     worst = 0.0
     for i, (token, got) in enumerate(steps):
         err = float((got - ref).abs().max())
@@ -227,6 +239,59 @@ def test_smollm2_24_layers_matches_the_oracle(device) -> None:
     reqs2, record2, _, _ = _run_recording(model, spec, prompts[:1], [1], 128, device, 128)
     a, b = record[reqs[0].request_id][0][1], record2[reqs2[0].request_id][0][1]
     assert float((a - b).abs().max()) <= 2e-2 * float(a.abs().max()) + 2e-2
+
+
+def test_decoder_at_cfg5_lengths_through_every_decode_attention_mode(device) -> None:
+    """Config 5's own lengths on two layers of the 1.7B shape (INT8 per-channel, fp16) through
+    the executor with decode graphs. A 4,080-token prompt runs as eight 512-token chunks, the
+    later ones over a cached prefix of up to 3,584 tokens (MFMA prefill tiles), beside seven
+    shorter requests; then eight requests decode together, the long context crossing 4,096
+    tokens mid-way, and the batch shrinks as requests finish. The decode graphs therefore replay
+    all three attention modes: a 16-wave workgroup per (request, head), KV splits + the merge
+    launch, and 8-wave workgroups over parts of each context + the merge launch. Every emitted
+    token's logits are checked against OracleDecoder (fp32, teacher-forced); a 384-token chunk
+    size gives the same first-token logits within tolerance (tests/test_executor.py:114-130)."""
+    spec = ModelSpec("smol2", "llama", 2, 2048, 32, 32, 64, 49152, 8192, 130000.0,
+                     intermediate_size=8192)
+    weights = om.random_weights(spec, 13, 8, None)
+    model = EdgeRagDecoder(spec, 8, None, device, torch.float16)
+    model.load_quantized(weights)
+    g = seeded(13)
+    lens = [4080, 300, 1100, 512, 700, 256, 900, 450]
+    max_new = [26, 18, 19, 20, 21, 22, 23, 24]
+    prompts = [torch.randint(1, 49151, (n,), generator=g).tolist() for n in lens]
+    modes: list[tuple[int, bool]] = []
+    alloc = BlockAllocator(1024, 16)
+    executor = ModelExecutor(model, spec, alloc, device, model.dtype, chunk_size=512)
+    sched = Scheduler(alloc, SchedulerConfig(max_batch_size=8))
+    reqs = [Request(f"r{i}", p, max_new_tokens=n) for i, (p, n) in enumerate(zip(prompts, max_new))]
+    for r in reqs:
+        sched.add_request(r)
+    record: dict[str, list[tuple[int, torch.Tensor]]] = {r.request_id: [] for r in reqs}
+
+    def on_step(batch, output):
+        if not batch.prefill:
+            modes.append(executor._fixed.mode)
+        if output.tokens:
+            logits = executor.last_logits.float().cpu()
+            for row, (rid, token) in enumerate(output.tokens.items()):
+                record[rid].append((token, logits[row]))
+
+    print("cfg5 lengths: 8 requests, a 4,080-token prompt", flush=True)
+    drive(sched, executor, on_step=on_step)
+    assert alloc.num_free == alloc.num_blocks
+    assert {(16, False), (0, True), (8, True)} <= set(modes), modes
+    oracle = om.OracleDecoder(weights, torch.float32)
+    for r, p in zip(reqs, prompts):
+        steps = record[r.request_id]
+        assert [t for t, _ in steps] == r.generated_token_ids and len(steps) == r.max_new_tokens
+        print(f"oracle check {r.request_id} ({len(p)} prompt tokens)", flush=True)
+        _check_against_oracle(oracle, p, steps, "cfg5 " + r.request_id)
+    first = {rid: steps[0][1] for rid, steps in record.items()}
+    reqs2, record2, _, _ = _run_recording(model, spec, prompts[:2], [1, 1], 384, device, 512)
+    for r2 in reqs2:
+        a, b = first[r2.request_id], record2[r2.request_id][0][1]
+        assert float((a - b).abs().max()) <= 2e-2 * float(a.abs().max()) + 2e-2
 
 
 # --- the timed config-2 launch at full shape ----------------------------------------------------
