@@ -7,9 +7,12 @@ the decoder-step hot path on that batch: slot-mapped append of the 32 new K/V to
 ragged paged attention over every context. ``value`` is the step's algorithmic KV bytes
 (context reads + appended K/V + q/out + block tables) divided by the step time, in GB/s.
 
-Extra fields (same line) cover config 3 (3 prefill slices of 512 + 24 decodes, one launch) and
-config 4 (INT8 / INT4 quant linears over M in {1, 8, 32, 64, 512, 544}, weight replicas rotated
-through >= 1 GiB so the timings are HBM, not Infinity Cache).
+Extra fields (same line, tables as ``cols`` + ``rows`` arrays so the whole line stays a few KB):
+``cfg3`` (3 prefill slices of 512 + 24 decodes, one step), ``single_seq`` (the reference's
+published fused-attention shape: batch 1 and 2 decodes at L in {128 ... 7992}), ``cfg4`` (INT8 /
+INT4 quant linears over M in {1, 8, 32, 64, 512, 544}, weight replicas rotated through >= 1 GiB so
+the timings are HBM, not Infinity Cache), ``lm_head`` (the fused output head + greedy argmax)
+and ``cfg5`` (the 24-layer decoder serving the synthetic Poisson trace).
 
 Timing: W untimed warmup steps, then K steps bracketed by ``torch.cuda.synchronize()`` and HIP
 events on the stream the kernels are launched on (torch's current stream). The step's metadata
@@ -290,7 +293,6 @@ def measure_ceilings(device, gather_bytes):
     out["gather_2KiB_gbs"] = gather_gbs(0)
     # Non-temporal loads, as the decode rows read the pools: the ceiling of their pattern.
     out["gather_2KiB_nt_gbs"] = gather_gbs(1)
-    out["source"] = "bench.py measure_ceilings: edgerag_probe_read / edgerag_probe_gather"
     del pool, ids
     torch.cuda.empty_cache()
     return out
@@ -329,17 +331,24 @@ CFG4_MS = (1, 8, 32, 64, 512, 544)
 
 
 def run_cfg4(device, args):
-    res = {"rows": bench_quant(device)}
+    """Config 4 as compact rows: [K, N, bits, M, us, frac, ref_us, cpu_us]. ``frac`` is of the
+    row's roofline (HBM 8 TB/s for M <= 64, dense fp16 MFMA 2.5 PFLOP/s above); ``ref_us`` is the
+    streaming-read probe over the same weight bytes for the HBM rows and torch's fp16 GEMM
+    (hipBLASLt) on the dequantised weights for the MFMA rows; ``cpu_us`` the CPU baseline."""
+    rows = bench_quant(device)
+    cpu = {}
     if not args.no_cpu:
-        rows = cpu_quant_rows(CFG4_SHAPES, CFG4_MS)
-        res["cpu_baseline"] = {
-            "unit": "us per call", "cores": cpu_threads(), "kind": "port", "rows": rows,
-            "sample": "every config-4 shape and M: dequantise + F.linear with fp32 activations "
-            "(oracle quant_linear_reference), median of >= 20 runs each",
-        }
-        gpu = {(r["k"], r["n"], r["m"]): r["us"] for r in res["rows"]}
-        for r in rows:
-            r["gpu_speedup"] = round(r["us"] / gpu[(r["k"], r["n"], r["m"])], 1)
+        for r in cpu_quant_rows(CFG4_SHAPES, CFG4_MS):
+            cpu[(r["k"], r["n"], r["m"])] = r["us"]
+    out = []
+    for r in rows:
+        ref = r["read_us"] if r["bound"] == "hbm" else r["vendor_fp16_us"]
+        out.append([r["k"], r["n"], r["bits"], r["m"], r["us"], r["frac"], ref,
+                    cpu.get((r["k"], r["n"], r["m"]))])
+    res = {"cols": ["k", "n", "bits", "m", "us", "frac", "ref_us", "cpu_us"], "rows": out}
+    if cpu:
+        res["cpu_baseline"] = {"unit": "us per call", "cores": cpu_threads(), "kind": "port",
+                               "sample": "oracle dequantise + F.linear, fp32, median of >= 20"}
     return res
 
 
@@ -449,14 +458,11 @@ def bench_lm_head(device, vocab=49152, k=2048, ms=(1, 8, 16), reps=3):
             res[name] = e0.elapsed_time(e1) * 1e3 / (5 * n_launch)
             del graph
         nbytes = wbytes + 2 * m * k + 2 * m * vocab
-        rows.append(dict(m=m, us=round(res["fused"], 2), vendor_us=round(res["vendor"], 2),
-                         gbs=round(nbytes / res["fused"] / 1e3, 1),
-                         frac=round(nbytes / res["fused"] / 1e3 / HBM_PEAK_GBS, 4),
-                         read_us=round(read_us, 2), read_frac=round(read_us / res["fused"], 4)))
+        rows.append([m, round(res["fused"], 2), round(res["vendor"], 2), round(read_us, 2),
+                     round(nbytes / res["fused"] / 1e3 / HBM_PEAK_GBS, 4)])
     del ws
     torch.cuda.empty_cache()
-    return {"workload": f"lm_head fp16 {vocab} x {k} (201 MB) + greedy argmax, M rows",
-            "rows": rows}
+    return {"cols": ["m", "us", "vendor_us", "read_us", "frac"], "rows": rows}
 
 
 # --- CPU baselines ---------------------------------------------------------------------------------
@@ -548,31 +554,29 @@ def cpu_decoder_tok_s(model, prompt_len=512, new_tokens=16, seed=5):
     request per forward as the reference executor runs it. Output tokens / wall time."""
     from oracle import model as om
 
-    t0 = time.perf_counter()
-    oracle = om.OracleDecoder(model, torch.float32)
-    build_s = time.perf_counter() - t0
+    oracle = om.OracleDecoder(model, torch.float32)  # dequantised once, not timed
     g = torch.Generator().manual_seed(seed)
     prompt = torch.randint(1, model.spec.vocab_size - 1, (prompt_len,), generator=g).tolist()
-    t0 = time.perf_counter()
-    oracle.reset()
-    logits = oracle.forward(prompt)[-1]
-    t_first = time.perf_counter() - t0
-    out = [int(logits.argmax())]
-    t1 = time.perf_counter()
-    while len(out) < new_tokens:
-        out.append(int(oracle.forward([out[-1]])[-1].argmax()))
-    t_dec = time.perf_counter() - t1
-    total = time.perf_counter() - t0
+
+    def once(n_prompt, n_new):
+        t0 = time.perf_counter()
+        oracle.reset()
+        out = [int(oracle.forward(prompt[:n_prompt])[-1].argmax())]
+        t1 = time.perf_counter()
+        while len(out) < n_new:
+            out.append(int(oracle.forward([out[-1]])[-1].argmax()))
+        t2 = time.perf_counter()
+        return t2 - t0, t2 - t1
+
+    once(64, 2)  # warmup, discarded (bench/metrics.py:1-12)
+    runs = [once(prompt_len, new_tokens) for _ in range(3)]
+    total = float(np.median([r[0] for r in runs]))
+    dec = float(np.median([r[1] for r in runs]))
     del oracle
-    return {
-        "value": round(new_tokens / total, 3),
-        "unit": "output tok/s",
-        "decode_tok_s": round((new_tokens - 1) / t_dec, 3),
-        "prefill_s": round(t_first, 2),
-        "sample": f"truncated: 1 request, {prompt_len}-token prompt (one chunk), {new_tokens} "
-        "greedy tokens, 24-layer oracle decoder in fp32 (weights dequantised from the GPU "
-        f"model's INT8 codes; {build_s:.1f} s to build, not timed); one run",
-    }
+    return {"value": round(new_tokens / total, 3), "unit": "output tok/s",
+            "decode_tok_s": round((new_tokens - 1) / dec, 3), "runs": 3,
+            "sample": f"1 request, {prompt_len}-token prompt, {new_tokens} tokens, 24-layer "
+            "fp32 oracle, median of 3 after a warmup"}
 
 
 def run_cfg3(device, args):
@@ -583,26 +587,19 @@ def run_cfg3(device, args):
     kv3, ap3, qo3, tb3 = step_bytes(lens3, q3, b3["bt"])
     step_bytes_total = kv3 + ap3 + qo3 + tb3
     res = {
-        "workload": "3 prefill slices (512 at offsets 0/3584/6656) + 24 decodes, 1560 tokens",
         "ms_per_step": round(s3, 4),
         "step_bytes": int(step_bytes_total),
-        "step_gbs": round(step_bytes_total / (s3 * 1e-3) / 1e9, 1),
+        "gbs": round(step_bytes_total / (s3 * 1e-3) / 1e9, 1),
         "hbm_frac": round(step_bytes_total / (s3 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "attn_us": round(a3 * 1e3, 1),  # the append + attention launches (one call)
-        "prefill_gflop": 46.18,
-        "attn_items": b3["plan"].n_items,
-        "plan_us": round(b3["plan_us"], 1),
+        "items": b3["plan"].n_items,
     }
     del b3
     torch.cuda.empty_cache()
     if not args.no_cpu:
         med, runs, nbytes = cpu_attention_step(lens3, q3, 8)
-        res["cpu_baseline"] = {
-            "value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": cpu_threads(),
-            "kind": "port", "ms_per_step": round(med * 1e3, 2),
-            "sample": f"the full config-3 step (27 requests, 1560 tokens): slot writes + "
-            f"gather + causal SDPA per request in fp32 (oracle), median of {runs} runs",
-        }
+        res["cpu_baseline"] = {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s",
+                               "cores": cpu_threads(), "kind": "port", "runs": runs}
     return res
 
 
@@ -664,7 +661,15 @@ def bench_single_seq(device, lens=SINGLE_SEQ_LENS, batch=1, num_blocks=16384):
                      round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), int(ph[2]), int(ph[16] > 0)])
     del kp, vp
     torch.cuda.empty_cache()
-    return {"batch": batch, "cols": ["L", "us", "gbs", "frac", "items", "merge"], "rows": rows}
+    return rows
+
+
+SINGLE_SEQ_COLS = ["L", "us", "gbs", "frac", "items", "merge"]
+
+
+def run_single_seq(device):
+    return {"cols": SINGLE_SEQ_COLS, "b1": bench_single_seq(device),
+            "b2": bench_single_seq(device, batch=2)}
 
 
 # --- config 5: end-to-end serving ---------------------------------------------------------------
@@ -685,11 +690,9 @@ def run_cfg5(device, n_requests: int = 64, cpu: bool = True):
     from edgerag_amd.serve.replay import poisson_arrivals, replay, synthetic_requests
 
     spec = SMOLLM2_1_7B
-    t0 = time.perf_counter()
     model = EdgeRagDecoder(spec, bits=8, group_size=None, device=device, dtype=torch.float16)
     model.init_random(seed=5)
     torch.cuda.synchronize()
-    init_s = time.perf_counter() - t0
     num_blocks = 8 * math.ceil((7472 + 256) / BS) + 64
     alloc = BlockAllocator(num_blocks, BS)
     executor = ModelExecutor(model, spec, alloc, device, torch.float16, chunk_size=512)
@@ -701,16 +704,13 @@ def run_cfg5(device, n_requests: int = 64, cpu: bool = True):
     offered = replay(Scheduler(alloc, SchedulerConfig()), executor, reqs, arrivals, "virtual")
     reqs = synthetic_requests(n_requests, spec.vocab_size, seed=5)
     saturated = replay(Scheduler(alloc, SchedulerConfig()), executor, reqs, None, "saturated")
-    res = {
-        "workload": f"{n_requests} requests, Poisson 12 req/min, prompts lognormal(3000, 0.6) "
-        "in [256, 7472], 64-256 greedy tokens; 24-layer SmolLM2-1.7B shape, INT8 per-channel",
-        "metric": "decoder output tok/s",
-        "offered_load": offered.summary(),
-        "saturated": saturated.summary(),
-        "weight_bytes": model.weight_bytes(),
-        "kv_pool_bytes": executor.pool_bytes,
-        "init_s": round(init_s, 2),
-    }
+    def brief(summary):
+        keep = ("output_tok_per_s", "iterations", "iteration_ms_p50", "iteration_ms_p99",
+                "ttft_s_p50", "ttft_s_p99", "gpu_busy_s")
+        return {k: summary[k] for k in keep}
+
+    res = {"requests": n_requests, "offered_load": brief(offered.summary()),
+           "saturated": brief(saturated.summary()), "weight_bytes": model.weight_bytes()}
     if cpu:
         del executor
         torch.cuda.empty_cache()
@@ -750,8 +750,7 @@ def main() -> None:
         print(json.dumps({"lm_head": bench_lm_head(device)}), flush=True)
         return
     if args.only == "single_seq":
-        print(json.dumps({"single_seq": bench_single_seq(device),
-                          "batch2": bench_single_seq(device, batch=2)}), flush=True)
+        print(json.dumps({"single_seq": run_single_seq(device)}), flush=True)
         return
     if args.only == "cfg5":
         print(json.dumps({"cfg5": run_cfg5(device, args.cfg5_requests, not args.no_cpu)}),
@@ -781,28 +780,23 @@ def main() -> None:
         "dtype": "f16",
         "data": "synthetic (seeded N(0,1) pools/queries, seeded-shuffled block tables)",
         "config": {
-            "workload": "cfg2: ragged decode step (KV append + fused paged attention), 32 seqs, "
-            "L~U[256,7472], 32/32 heads, d64, bs16, 16384-block pool",
+            "workload": "cfg2: KV append + ragged paged attention, 32 decodes, L~U[256,7472], "
+            "32/32 heads, d64, bs16, 16384-block pool",
             "context_tokens": int(sum(lens)),
             "step_bytes": int(total),
             "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
             "plan_us": round(b["plan_us"], 1),
             "planner_us": round(b["planner_us"], 1),
-            "plan_us_note": "host time per step, warm median of 30: plan_attention (native "
-            "planner + one pinned upload enqueued); planner_us is the planner alone",
             "attn_items": b["plan"].n_items,
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "paged attention launch with the KV append fused in: attn_decode_kernel "
-            "(APPEND) + attn_combine_kernel",
+            "kernel": "attn_decode_kernel (append fused) + attn_combine_kernel",
             "achieved": round(attn_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic("attn_decode_cfg2.md"),
-            "traffic_source": "profiles/attn_decode_cfg2.md (rocprofv3 --pmc FETCH_SIZE / "
-            "WRITE_SIZE, scaled by a 1 GiB copy)",
             "algorithmic_bytes": int(attn_bytes),
             "launch_us": round(attn_ms * 1e3, 2),
         },
@@ -814,21 +808,22 @@ def main() -> None:
     line["ceilings"] = ceilings
     line["roofline"]["frac_of_gather_ceiling"] = round(attn_gbs / ceilings["gather_2KiB_nt_gbs"], 4)
     torch.cuda.empty_cache()
-    if not args.no_extra:
-        line["cfg3"] = run_cfg3(device, args)
-        line["cfg4"] = run_cfg4(device, args)
-        line["lm_head"] = bench_lm_head(device)
-        if not args.no_cfg5:
-            line["cfg5"] = run_cfg5(device, args.cfg5_requests, not args.no_cpu)
     if not args.no_cpu:
         med, runs, nbytes = cpu_attention_step(lens, [1] * 32, 7)
         line["cpu_baseline"] = {
             "value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": cpu_threads(),
             "kind": "port", "ms_per_step": round(med * 1e3, 2),
-            "sample": f"the full config-2 step (all 32 requests, contexts {list(lens)}): slot "
-            f"write + gather + SDPA per request in fp32 (oracle), median of {runs} runs",
+            "sample": f"the full cfg2 step (32 requests): slot writes + gather + SDPA per "
+            f"request, fp32 oracle, median of {runs} runs",
         }
-    print(json.dumps(line), flush=True)
+    if not args.no_extra:
+        line["cfg3"] = run_cfg3(device, args)
+        line["single_seq"] = run_single_seq(device)
+        line["cfg4"] = run_cfg4(device, args)
+        line["lm_head"] = bench_lm_head(device)
+        if not args.no_cfg5:
+            line["cfg5"] = run_cfg5(device, args.cfg5_requests, not args.no_cpu)
+    print(json.dumps(line, separators=(",", ":")), flush=True)
 
 
 if __name__ == "__main__":
