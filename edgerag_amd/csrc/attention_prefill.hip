@@ -257,24 +257,22 @@ void attn_prefill_mfma_kernel(
   }
   const bool item_has_bad = __syncthreads_or(any_bad) != 0;
 
-  // Q^T as the B operand: k-step ks covers dims 16*ks + 8*g .. +7 of this lane's query, scaled
-  // by scale_log2 (so S is in the log2 domain).
+  // Q^T as the B operand: k-step ks covers dims 16*ks + 8*g .. +7 of this lane's query, as
+  // given. The scale (times log2 e) multiplies the fp32 dot products afterwards, like the decode
+  // rows: scaling q first would round every q * scale to fp16, a score error that grows with the
+  // score (scores of tens of nats, as with attention sinks, moved outputs by 3e-2).
   h8 qop[4];
   {
     const _Float16* qp = q + int64_t(t) * q_st + int64_t(hq) * q_sh;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const h8 raw = active ? *reinterpret_cast<const h8*>(qp + 16 * ks + 8 * g) : h8{};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qop[ks][e] = _Float16(float(raw[e]) * scale_log2);
-    }
+    for (int ks = 0; ks < 4; ++ks)
+      qop[ks] = active ? *reinterpret_cast<const h8*>(qp + 16 * ks + 8 * g) : h8{};
   }
   f32x16 o0 = {}, o1 = {};  // O^T dims 0-31 and 32-63 of this lane's query
   float m = -INFINITY;      // reference max of the log2-domain scores
   float l = 0.f;
-  // -m in every register (0 while m is -inf): the C operand of each tile's first S MFMA, rewritten
-  // only when m moves, so no tile spends instructions on initialising its accumulators.
-  f32x16 neg_m = {};
+  float nm = 0.f;           // -m (0 while m is -inf)
+  const f32x16 zero16 = {};
   const h2 ones = {_Float16(1.f), _Float16(1.f)};
 
   const uint32_t head_bytes = uint32_t(int64_t(num_blocks) * block_size * kD * 2);
@@ -285,17 +283,21 @@ void attn_prefill_mfma_kernel(
 
   // One 64-key tile on staged LDS buffers (skb, svb).
   auto tile = [&](int k0, const _Float16* skb, const _Float16* svb) {
-    // S^T = K Q^T - m: two 32-key tiles, 4 k-steps of 16 dims (dim chunk 2ks + g), the first
-    // one accumulating onto -m (0 before the first visible score).
+    // S^T = K Q^T: two 32-key tiles, 4 k-steps of 16 dims (dim chunk 2ks + g).
     f32x16 s[2];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) {
         const h8 ka = *reinterpret_cast<const h8*>(skb + lds_chunk(32 * kt + col, 2 * ks + g));
-        s[kt] = mfma32(ka, qop[ks], ks == 0 ? neg_m : s[kt]);
+        s[kt] = mfma32(ka, qop[ks], ks == 0 ? zero16 : s[kt]);
       }
     }
+    // log2-domain scores relative to the reference max: q.k * scale * log2(e) - m.
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[kt][i] = __builtin_fmaf(s[kt][i], scale_log2, nm);
     // Register i of tile kt holds key 32kt + (i%4) + 8(i/4) + 4g.
     const int key_end = min(ke - k0, kKeys);  // keys of this tile inside the split
     if (k0 + kKeys - 1 > wave_min_lim || key_end < kKeys) {
@@ -337,9 +339,7 @@ void attn_prefill_mfma_kernel(
       const float shift = up ? tmax : 0.f;
       const float alpha = first ? (up ? 0.f : 1.f) : exp2_fast(-shift);
       if (up) m = first ? tmax : m + tmax;
-      const float nm = m == -INFINITY ? 0.f : -m;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) neg_m[i] = nm;
+      nm = m == -INFINITY ? 0.f : -m;
       l *= alpha;
       o0 *= alpha;
       o1 *= alpha;

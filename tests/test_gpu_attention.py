@@ -607,3 +607,29 @@ def test_few_decodes_as_context_parts_fp16(device, lens, n_q, n_kv) -> None:
     fused = kernels.paged_attention_append(nkd, nvd, slots_d, qd, kp2, vp2, plan, d**-0.5)
     assert torch.equal(fused, ref)
     assert torch.equal(kp2, kp1) and torch.equal(vp2, vp1)
+
+
+@pytest.mark.parametrize("c,past,q_lens_kind", [(512, 3584, "prefill"), (200, 900, "prefill"),
+                                                (1, 4000, "decode")])
+def test_large_scores_and_attention_sinks_fp16(device, c, past, q_lens_kind) -> None:
+    """Scores far from the unit-variance regime: Q and K scaled 8x (scores of tens of nats) and
+    four attention-sink keys aligned with every query; prefill MFMA tiles and decode rows both
+    at the fp16 gate tolerance against the float64 head over the same fp16 inputs."""
+    n_q = n_kv = 4
+    d = 64
+    L = past + c
+    kp, vp, tables, qsl, q, bt = _ragged_case([L], [c], n_q, n_kv, d, torch.float16, L + c,
+                                              poison=False)
+    g = seeded(L)
+    q = (8 * torch.randn(c, n_q, d, generator=g)).half()
+    kp = (8 * kp.float()).half()
+    sink_dir = q.float().mean(dim=0)  # (n_q, d): the queries' common direction per head
+    for pos in range(4):
+        blk, off = tables[0][pos // BLOCK_SIZE], pos % BLOCK_SIZE
+        kp[:, blk, off] = (0.6 * sink_dir / sink_dir.norm(dim=-1, keepdim=True) * 64).half()
+    got = _run_ragged(device, kp, vp, qsl, [L], bt, q, d**-0.5)
+    for h in range(n_q):
+        kh = op.gather_pool(kp.double(), tables[0], L)[h]
+        vh = op.gather_pool(vp.double(), tables[0], L)[h]
+        ref = oa.attention_f64(q[:, h], kh, vh, past, d**-0.5)
+        torch.testing.assert_close(got[:, h].double(), ref, **FP16_TOL)
