@@ -33,6 +33,9 @@
 #ifndef EDGERAG_STREAM_NARROW_F2
 #define EDGERAG_STREAM_NARROW_F2 1  // 17..32 tokens on narrow N: two k-slices (see dispatch_stream)
 #endif
+#ifndef EDGERAG_STREAM_F2_TILES
+#define EDGERAG_STREAM_F2_TILES 256  // 16-row tiles below which decode launches take two k-slices
+#endif
 #ifndef EDGERAG_STREAM_NT2_TILES
 #define EDGERAG_STREAM_NT2_TILES 512  // 16-row tiles from which a workgroup takes two
 #endif
@@ -408,11 +411,16 @@ __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlin
   constexpr int OUTS = NT * MT * R * R;    // outputs (token, row) of a workgroup
   constexpr int NO = (OUTS + KW * kWave - 1) / (KW * kWave);  // outputs per thread
   static_assert((KW * kWave) % (NT * R) == 0, "a thread's outputs share one weight row");
-  static_assert(EPI == kEpiPlain || EPI == kEpiResidual || (NT == 2 && kWave % (NT * R) == 0),
+  static_assert(EPI == kEpiPlain || EPI == kEpiResidual || (NT == 2 && kWave % (NT * R) == 0) ||
+                    (EPI == kEpiRope && NT == 1 && F == 2),
                 "paired epilogues pair tile 0 with tile 1 inside one wave");
-  static_assert(EPI != kEpiRope || F == 1, "RoPE pairs 16-row tiles");
+  static_assert(EPI != kEpiRope || (F == 1 && NT == 2) || (F == 2 && NT == 1),
+                "RoPE pairs two 16-row tiles, or the rows of one 8-row tile");
   static_assert(EPI != kEpiResidual || kWave % (NT * R) == 0, "a token's rows share one wave");
-  static_assert(!NORM || ((EPI == kEpiSwiglu || EPI == kEpiRope) && F == 1), "normed inputs");
+  static_assert(!NORM || (EPI == kEpiSwiglu && F == 1) || EPI == kEpiRope, "normed inputs");
+  // kEpiRope with one 8-row tile: lane row rr is element rr / 2 of the workgroup's run of a
+  // head's first half (rr even) or its rotate_half partner in the second half (rr odd).
+  constexpr bool ROPE8 = EPI == kEpiRope && NT == 1;
   constexpr int NPQ = kNormMaxParts / kWave;           // partials per lane and token
   constexpr int TOKW = NORM ? (MT * R + KW - 1) / KW : 1;  // tokens whose factor a wave sums
   __shared__ float red[KW * NT * MT * 4 * kWave];
@@ -423,9 +431,10 @@ __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlin
   const int f = li / R, r = li % R;
   // kEpiSwiglu: gate rows [0, half), up rows [half, n). kEpiRope: head_dim / 2.
   const int half = EPI == kEpiRope ? ea.head_dim >> 1 : n >> 1;
-  const int per_head = half / 16;  // kEpiRope: workgroups per head
+  constexpr int PAIRS = NT * R / 2;  // kEpiRope: rotate_half pairs of a workgroup
+  const int per_head = half / PAIRS;  // kEpiRope: workgroups per head
   const int rope_head = EPI == kEpiRope ? int(blockIdx.x) / per_head : 0;
-  const int rope_j = EPI == kEpiRope ? (int(blockIdx.x) % per_head) * 16 : 0;
+  const int rope_j = EPI == kEpiRope ? (int(blockIdx.x) % per_head) * PAIRS : 0;
   const int n0 = EPI == kEpiRope ? rope_head * ea.head_dim + rope_j
                                  : int(blockIdx.x) * (EPI == kEpiSwiglu ? R : NT * R);
   const int nc = k / CB;  // chunk steps: >= U, and a multiple of KW * U when EXACT
@@ -436,6 +445,7 @@ __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlin
   auto wrow = [&](int tn, int rr) {
     if constexpr (EPI == kEpiPlain || EPI == kEpiResidual) return min(n0 + tn * R + rr, n - 1);
     else if constexpr (EPI == kEpiSwiglu) return min(n0 + rr, half - 1) + tn * half;
+    else if constexpr (ROPE8) return n0 + (rr & 1) * half + (rr >> 1);
     else return n0 + tn * half + rr;
   };
 
@@ -464,7 +474,8 @@ __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlin
   uint32_t b_bits = reinterpret_cast<const uint32_t*>(b_src - b_mis)[b_idx >> 1];
   // kEpiRope: every output of this thread is element e_d of its head for token e / (NT R); the
   // token's cos / sin at e_d and its slot are loaded now as well (tokens past M re-read the last).
-  const int e_d = (e_in / R) * half + rope_j + e_in % R;
+  const int e_d = ROPE8 ? (e_in & 1) * half + rope_j + (e_in >> 1)
+                        : (e_in / R) * half + rope_j + e_in % R;
   // (Raw loads only, nothing computed on them before the pins, like the scale and bias words.)
   int32_t rope_slot[EPI == kEpiRope ? NO : 1];
   uint32_t rope_c[EPI == kEpiRope ? NO : 1], rope_s[EPI == kEpiRope ? NO : 1];
@@ -673,8 +684,10 @@ __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlin
         y[int64_t(tok) * ys + n0 + rr] = __float2half_rn(silu_rounded_f16(v) * u);
     }
   } else {
-    // Element d of a head sits in lane l and its rotate_half partner d +- D/2 in lane l ^ 16.
+    // Element d of a head sits in lane l and its rotate_half partner d +- D/2 in lane l ^ 16
+    // (two 16-row tiles) or l ^ 1 (one 8-row tile).
     const int tn = e_in / R;
+    const bool second = ROPE8 ? (e_in & 1) != 0 : tn == 1;
     const int nq = ea.n_q_heads, nkv = ea.n_kv_heads;
     const int64_t pool_rows = int64_t(ea.num_blocks) * ea.block_size;
 #pragma unroll
@@ -683,14 +696,14 @@ __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlin
       if (e >= OUTS) break;  // uniform per wave
       const int tok = e / (NT * R);
       const float v = __half2float(out_sum(tok, tn, e_in % R));
-      const float partner = __shfl_xor(v, 16, kWave);
+      const float partner = __shfl_xor(v, ROPE8 ? 1 : 16, kWave);
       if (tok >= m) continue;
       const float c = __half2float(__builtin_bit_cast(f16, uint16_t(rope_c[o])));
       const float sn = __half2float(__builtin_bit_cast(f16, uint16_t(rope_s[o])));
       const int head = rope_head;
       if (head < nq) {
         ea.q_out[int64_t(tok) * ea.q_st + int64_t(head) * ea.head_dim + e_d] =
-            rope_elem(v, partner, tn == 1, c, sn);
+            rope_elem(v, partner, second, c, sn);
         continue;
       }
       const int64_t slot = rope_slot[o];
@@ -700,7 +713,7 @@ __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlin
           ((int64_t(kvh) * ea.num_blocks + slot / ea.block_size) * ea.block_size +
            slot % ea.block_size) * ea.head_dim + e_d;
       if (head < nq + nkv)
-        ea.kpool[off] = rope_elem(v, partner, tn == 1, c, sn);
+        ea.kpool[off] = rope_elem(v, partner, second, c, sn);
       else
         ea.vpool[off] = __float2half_rn(v);
     }
@@ -1365,9 +1378,9 @@ void launch_stream(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t
                    const EpiArgs& ea, hipStream_t s) {
   constexpr int rows = NT * 16 / F;
   // SwiGLU: one workgroup per 16 / F activation columns (a gate tile and its up twin); RoPE: one
-  // per 16 elements of a head's first half (that tile and its rotate_half twin).
+  // per NT 16 / F rows, half of them elements of a head's first half and half their rotate_half
+  // twins.
   const unsigned blocks = EPI == kEpiSwiglu ? unsigned((n / 2 + 16 / F - 1) / (16 / F))
-                          : EPI == kEpiRope ? unsigned(n / 32)
                                             : unsigned((n + rows - 1) / rows);
   if ((k / (64 * F)) % (KW * U) == 0)
     hipLaunchKernelGGL((qlinear_stream_kernel<F, NT, MT, KW, U, true, EPI, NORM>), dim3(blocks),
@@ -1439,14 +1452,24 @@ void launch_stream_k(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8
 // The k-slices (1 or 2) dispatch_stream uses for (M, K, N), 0 when it does not take the shape:
 // two (8-row tiles) when 16-row tiles would leave CUs idle (N < 4096) for up to 16 tokens, and for
 // 17..32 tokens (M = 32, K 8192 -> N 2048: 21.4 -> 18.8 us; for 33..64 tokens two such launches
-// measured slower than one k-slice).
+// measured slower than one k-slice). Also when the one-slice workgroups (one per 16 rows, fewer
+// than 512) would give some CUs two and others one while the 8-row ones are spread more evenly:
+// N = 6144 (the q/k/v projection) 384 -> 768 workgroups, 6.41 -> 4.80 us at M = 1, 7.58 -> 6.53
+// us at M = 8; N = 4096 (256 workgroups either way) gained nothing. The rule holds for all of
+// 1..16 tokens so that a decode token's bits stay independent of the batch, although at 16 tokens
+// the two 8-token m-tiles cost more than they gain (8.9 -> 11.4 us).
 int stream_slices(int32_t m, int32_t k, int32_t n) {
   const int64_t tiles16 = (int64_t(n) + 15) / 16;
   const bool one = k % 64 == 0 && k / 64 >= 4, two = k % 128 == 0 && k / 128 >= 4;
   if (m < 1 || m > 64) return 0;
   if (EDGERAG_STREAM_NARROW_F2 && m > 16 && m <= 32 && tiles16 < 256 && two) return 2;
   if (m > 16) return one ? 1 : 0;
-  if (tiles16 < 256) return two ? 2 : 0;
+  if (tiles16 < EDGERAG_STREAM_F2_TILES) return two ? 2 : 0;
+  if (tiles16 < EDGERAG_STREAM_NT2_TILES && two) {
+    // Rounds of workgroups over the 256 CUs, against a perfectly even spread.
+    auto imbalance = [](int64_t wgs) { return double((wgs + 255) / 256) * 256.0 / double(wgs); };
+    if (imbalance(2 * tiles16) < imbalance(tiles16) - 1e-9) return 2;
+  }
   return one ? 1 : 0;
 }
 
@@ -1713,9 +1736,13 @@ bool qlinear_mfma_supported(int32_t k, int32_t bits, int32_t g, const void* x, i
 // The fused RoPE launch takes the waves and batch of the plain launch of the same (M, K, N), which
 // must itself be a one-k-slice streaming launch: then every q / k / v value it rotates or copies
 // has the plain launch's bits.
+// With two k-slices the RoPE launch takes 8-row tiles whose rows pair every element with its
+// rotate_half twin, the plain launch's waves and k-slices; with one, two 16-row tiles per
+// workgroup (a run of a head's first half and its twin), the plain launch's waves.
 bool stream_rope_shape(int32_t m, int32_t k, int32_t n, int32_t heads, int32_t head_dim) {
-  if (m > EDGERAG_STREAM_MAX_M || stream_slices(m, k, n) != 1) return false;
-  if (head_dim % 32 != 0 || int64_t(heads) * head_dim != n) return false;
+  const int slices = m > EDGERAG_STREAM_MAX_M ? 0 : stream_slices(m, k, n);
+  if (slices == 0 || head_dim % 32 != 0 || int64_t(heads) * head_dim != n) return false;
+  if (slices == 2) return m <= 32;
   const int64_t tiles16 = (int64_t(n) + 15) / 16;
   const int nt = tiles16 >= EDGERAG_STREAM_NT2_TILES ? 2 : 1;
   const int mt = m <= 16 ? 1 : m <= 32 ? 2 : 4;
@@ -1744,6 +1771,20 @@ void launch_rope(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* 
   const int nt = (int64_t(n) + 15) / 16 >= EDGERAG_STREAM_NT2_TILES ? 2 : 1;
   launch_stream_w<1, 2, MT, kEpiRope, NORM>(stream_waves(1, nt, MT, k), x, xs, m, k, packed,
                                             scales, bias, n, nullptr, 0, ea, s);
+}
+
+// Two k-slices: 8-row tiles with 8-token m-tiles, the plain launch's shape for M <= 32.
+template <bool NORM = false>
+void launch_rope8(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
+                  const f16* scales, const f16* bias, int32_t n, const EpiArgs& ea,
+                  hipStream_t s) {
+#define EDGERAG_ROPE8(MT)                                                                        \
+  launch_stream_w<2, 1, MT, kEpiRope, NORM>(stream_waves(2, 1, MT, k), x, xs, m, k, packed,      \
+                                            scales, bias, n, nullptr, 0, ea, s)
+  if (m <= 8) EDGERAG_ROPE8(1);
+  else if (m <= 16) EDGERAG_ROPE8(2);
+  else EDGERAG_ROPE8(4);
+#undef EDGERAG_ROPE8
 }
 
 bool qlinear_rope_supported(int32_t m, int32_t k, int32_t n, int32_t bits, int32_t g,
@@ -1777,7 +1818,12 @@ void launch_qlinear_rope(const f16* x, int64_t xs, int32_t m, int32_t k, const u
     }
     return;
   }
-  if (ea.norm_part != nullptr)  // normed input: decode batches of up to 16 tokens
+  if (stream_slices(m, k, n) == 2) {
+    if (ea.norm_part != nullptr)
+      launch_rope8<true>(x, xs, m, k, packed, scales, bias, n, ea, s);
+    else
+      launch_rope8(x, xs, m, k, packed, scales, bias, n, ea, s);
+  } else if (ea.norm_part != nullptr)  // normed input: decode batches of up to 16 tokens
     launch_rope<1, true>(x, xs, m, k, packed, scales, bias, n, ea, s);
   else if (m <= 16)
     launch_rope<1>(x, xs, m, k, packed, scales, bias, n, ea, s);

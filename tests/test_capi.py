@@ -112,13 +112,16 @@ def test_rope_append_support_query() -> None:
     assert q(F16, 8, 2048, 8, 2048, 32, 32, 64, 1) == 1  # ... with the RMSNorm folded in
     assert q(F16, 20, 2048, 8, 2048, 32, 32, 64, 1) == 0  # normed: at most 16 tokens
     assert q(F16, 64, 2048, 8, 2048, 32, 8, 64, 0) == 1  # GQA, N 3072: one k-slice from M > 32
-    assert q(F16, 8, 2048, 8, 2048, 32, 8, 64, 0) == 0  # N 3072 at M <= 32: two k-slices
-    assert q(F16, 24, 2048, 8, 2048, 32, 8, 64, 0) == 0
+    # Two k-slices (N 3072 at M <= 32; N 6144 at M <= 8): 8-row tiles pairing rotate_half twins.
+    assert q(F16, 8, 2048, 8, 2048, 32, 8, 64, 0) == 1
+    assert q(F16, 24, 2048, 8, 2048, 32, 8, 64, 0) == 1
+    assert q(F16, 8, 16384, 8, 16384, 32, 32, 64, 0) == 1
+    # N 4096 (256 one-slice workgroups, evenly spread): one k-slice, 16 waves at K 16384.
+    assert q(F16, 8, 16384, 8, 16384, 32, 16, 64, 0) == 0
     assert q(F16, 65, 2048, 8, 2048, 32, 32, 64, 0) == 0
     assert q(F16, 8, 2048, 8, 2048, 32, 32, 48, 0) == 0  # head_dim not a multiple of 32
     assert q(F16, 8, 2048, 4, 128, 32, 32, 64, 0) == 0  # INT4
     assert q(0, 8, 2048, 8, 2048, 32, 32, 64, 0) == 0  # fp32 activations
-    assert q(F16, 8, 16384, 8, 16384, 32, 32, 64, 0) == 0  # K needing 16 waves
 
 
 def test_lm_head_support_query() -> None:
