@@ -89,6 +89,9 @@ constexpr int kMaxSplitBlocks = 64;  // one block id per lane in the decode kern
 #ifndef EDGERAG_TARGET_TILES
 #define EDGERAG_TARGET_TILES 512
 #endif
+#ifndef EDGERAG_TILE_BALANCE
+#define EDGERAG_TILE_BALANCE 1  // split the longest tile items however many tile items there are
+#endif
 #ifndef EDGERAG_MIN_TILE_SPLIT
 #define EDGERAG_MIN_TILE_SPLIT 1024
 #endif
@@ -981,12 +984,17 @@ extern "C" int edgerag_attn_plan_ex(const int32_t* query_start_loc, const int32_
   const int64_t target_tiles = overlap ? kTargetTiles / 2 : kTargetTiles;
   const int64_t tile_split_cap =
       std::max<int64_t>(64, int64_t(kMaxTileBlocks - 1) * block_size / 64 * 64);
-  const int64_t tile_split_len = std::min(
-      tile_split_cap,
-      n_tiles >= target_tiles
-          ? round_up(std::max<int64_t>(max_len, 1), 64)
-          : round_up(std::max<int64_t>(kMinTileSplit,
-                                       (tile_work + target_tiles - 1) / target_tiles), 64));
+  const int64_t tile_share = round_up(
+      std::max<int64_t>(kMinTileSplit, (tile_work + target_tiles - 1) / target_tiles), 64);
+  const int64_t tile_part = std::min(
+      tile_split_cap, (EDGERAG_TILE_BALANCE || n_tiles < target_tiles)
+                          ? tile_share
+                          : round_up(std::max<int64_t>(max_len, 1), 64));
+  // Keys of a tile request's splits: equal 64-key multiples of at most tile_part.
+  auto tile_split_len = [&](int64_t L) -> int64_t {
+    const int64_t n = std::max<int64_t>(1, (L + tile_part - 1) / tile_part);
+    return std::min(tile_split_cap, round_up((std::max<int64_t>(L, 1) + n - 1) / n, 64));
+  };
 
   // Scratch reused across calls on a thread: the planner runs once per step on the host.
   thread_local std::vector<PlanGroup> rows, tiles;
@@ -1004,7 +1012,7 @@ extern "C" int edgerag_attn_plan_ex(const int32_t* query_start_loc, const int32_
     int32_t* rq = reqs.data() + size_t(r) * kReqWords;
     const bool row = c * n_rep <= kMaxRowVecs;
     // Workgroup-split rows: one item per part of the context (the waves split the part).
-    const int64_t slen = row ? (wg_rows ? wg_split_len(L) : split_len) : tile_split_len;
+    const int64_t slen = row ? (wg_rows ? wg_split_len(L) : split_len) : tile_split_len(L);
     const int nsplit = c == 0 ? 0 : int((L + slen - 1) / slen);
     rq[R_NSPLIT] = nsplit;
     rq[R_SPLITLEN] = int32_t(slen);

@@ -417,8 +417,9 @@ def _mixed(slices, decodes):
 def test_plan_overlap_choice(slices, decodes, force, overlap) -> None:
     """Plan word 20 records whether the batch is planned for tiles beside rows on two streams:
     only when the tiles fill every CU and the rows read at least 256 MiB (or when asked), and
-    never without both. The tile split follows the run: unsplit at the 256 slots of one
-    workgroup per CU beside the rows, split toward 512 items for the one-stream run."""
+    never without both. The tile split follows the run: toward the 256 slots of one workgroup
+    per CU beside the rows, 512 for the one-stream run; no tile item spans more keys than its
+    share of the tile work (at least 1,024), and a request's splits are equal 64-key multiples."""
     if decodes == "cfg3":
         decodes = torch.randint(512, 7473, (24,), generator=torch.Generator().manual_seed(3))
         decodes = [int(x) for x in decodes]
@@ -427,8 +428,21 @@ def test_plan_overlap_choice(slices, decodes, force, overlap) -> None:
                                      torch.float16, force_overlap=force)
     assert int(plan[20]) == overlap
     n_tiles = int(plan[2]) - int(plan[13])
-    unsplit = sum(-(-c // 128) for c, _ in slices) * 32
-    if overlap:
-        assert n_tiles == unsplit if unsplit >= 256 else 256 <= n_tiles < 512
-    elif slices:
-        assert n_tiles >= 512
+    if not slices:
+        assert n_tiles == 0
+        return
+    target = 256 if overlap else 512
+    work = sum(-(-c // 128) * 32 * (c + p) for c, p in slices)
+    part = -(-max(1024, -(-work // target)) // 64) * 64
+    items, reqs = decode_plan(plan)
+    expected = 0
+    for r, (c, p) in enumerate(slices):
+        L = c + p
+        n = -(-L // part)
+        slen = -(-(-(-L // n)) // 64) * 64
+        assert int(reqs[r][1]) == slen and int(reqs[r][0]) == -(-L // slen)
+        for t in range(-(-c // 128)):  # splits past a tile's causal limit are skipped
+            expected += 32 * min(-(-L // slen), (p + 128 * t + min(128, c - 128 * t) - 1) // slen + 1)
+    assert n_tiles == expected
+    assert all(int(ke) - int(kb) <= part for _r, _h, _qb, _qc, kb, ke, *_ in
+               items[int(plan[13]):].tolist())
