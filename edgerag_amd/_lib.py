@@ -99,6 +99,8 @@ SIGNATURES: dict[str, tuple[list, object]] = {
          c_vp, c_vp, c_i32, c_i32, c_i32, c_vp],
         c_i32,
     ),
+    "edgerag_rope_rows": ([c_vp, c_i32, c_vp, c_vp, c_i32, c_i32, c_i32, c_vp, c_vp, c_vp],
+                          c_i32),
     "edgerag_silu_mul": ([c_vp, c_i64, c_i32, c_i32, c_vp, c_i64, c_i32, c_vp], c_i32),
     "edgerag_argmax_rows": ([c_vp, c_i32, c_i32, c_i32, c_i64, c_vp, c_vp], c_i32),
     "edgerag_lm_head_argmax": (

@@ -197,7 +197,8 @@ class EdgeRagDecoder(nn.Module):
         T = step.token_ids.shape[0]
         d, eps = spec.head_dim, spec.rms_norm_eps
         # The residual stream is updated in place, so it is always a fresh tensor of this step.
-        hidden = (self.embed_tokens[step.token_ids.long()] if step.hidden is None
+        # index_select takes the int32 ids as they are (no widening launch).
+        hidden = (self.embed_tokens.index_select(0, step.token_ids) if step.hidden is None
                   else step.hidden)
         x = kernels.rmsnorm(hidden, self.layers[0].input_layernorm.weight, eps)
         q = torch.empty((T, spec.n_q_heads, d), device=self.device, dtype=self.dtype)
@@ -260,7 +261,7 @@ class EdgeRagDecoder(nn.Module):
                    else LinearBase.swiglu(layer.gate_up, x))
             down = layer.down_proj(act)
             x = kernels.rmsnorm(hidden, next_norm, eps, delta=down, h_out=hidden)
-        return x[step.logit_rows.long()]
+        return x.index_select(0, step.logit_rows)
 
     @torch.inference_mode()
     def logits(self, step: StepInputs, key_pool, value_pool) -> torch.Tensor:

@@ -416,6 +416,59 @@ extern "C" int edgerag_rope_append(const void* qkv, int64_t qkv_stride, const in
   return check_launch("edgerag_rope_append");
 }
 
+// One thread per (token, 2-byte element) of the per-token cos / sin rows: the table row at the
+// token's position, or NaN where the position has no row.
+template <typename T>
+__global__ __launch_bounds__(256) void rope_rows_kernel(const int32_t* __restrict__ positions,
+                                                        int32_t n_tokens,
+                                                        const T* __restrict__ cos_t,
+                                                        const T* __restrict__ sin_t,
+                                                        int32_t max_pos, int32_t head_dim,
+                                                        T* __restrict__ cos_out,
+                                                        T* __restrict__ sin_out) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= int64_t(n_tokens) * head_dim) return;
+  const int t = int(i / head_dim), d = int(i % head_dim);
+  const int pos = positions[t];
+  T c, s;
+  if (pos < 0 || pos >= max_pos) {
+    c = s = round_to<T>(__builtin_nanf(""));
+  } else {
+    c = cos_t[int64_t(pos) * head_dim + d];
+    s = sin_t[int64_t(pos) * head_dim + d];
+  }
+  cos_out[i] = c;
+  sin_out[i] = s;
+}
+
+extern "C" int edgerag_rope_rows(const int32_t* positions, int32_t n_tokens,
+                                 const void* cos_table, const void* sin_table, int32_t max_pos,
+                                 int32_t head_dim, int32_t dtype, void* cos_out, void* sin_out,
+                                 void* stream) {
+  clear_error();
+  if (n_tokens < 0 || max_pos <= 0 || head_dim <= 0)
+    return fail(EDGERAG_EINVAL, "edgerag_rope_rows: bad shape");
+  if (n_tokens == 0) return EDGERAG_OK;
+  if (positions == nullptr || cos_table == nullptr || sin_table == nullptr ||
+      cos_out == nullptr || sin_out == nullptr)
+    return fail(EDGERAG_EINVAL, "edgerag_rope_rows: NULL pointer");
+  const int64_t total = int64_t(n_tokens) * head_dim;
+  const dim3 grid(unsigned((total + 255) / 256)), block(256);
+  auto s = static_cast<hipStream_t>(stream);
+#define EDGERAG_ROPE_ROWS(TYPE)                                                                  \
+  hipLaunchKernelGGL((rope_rows_kernel<TYPE>), grid, block, 0, s, positions, n_tokens,          \
+                     static_cast<const TYPE*>(cos_table), static_cast<const TYPE*>(sin_table), \
+                     max_pos, head_dim, static_cast<TYPE*>(cos_out), static_cast<TYPE*>(sin_out))
+  switch (dtype) {
+    case EDGERAG_F32: EDGERAG_ROPE_ROWS(float); break;
+    case EDGERAG_F16: EDGERAG_ROPE_ROWS(f16); break;
+    case EDGERAG_BF16: EDGERAG_ROPE_ROWS(bf16); break;
+    default: return fail(EDGERAG_EINVAL, "edgerag_rope_rows: dtype %d", dtype);
+  }
+#undef EDGERAG_ROPE_ROWS
+  return check_launch("edgerag_rope_rows");
+}
+
 extern "C" int edgerag_silu_mul(const void* gate_up, int64_t gate_up_stride, int32_t n_tokens,
                                 int32_t intermediate, void* out, int64_t out_stride,
                                 int32_t dtype, void* stream) {

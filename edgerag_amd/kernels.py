@@ -722,14 +722,22 @@ def rope_append(qkv: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor, s
 def rope_rows(positions: torch.Tensor, cos: torch.Tensor,
               sin: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """The rotary table rows at each token's position, ``(T, head_dim)`` each: what
-    ``quant_linear_rope_append`` reads. Gathered once per forward, shared by layers. A position
-    outside the table gets a NaN row (its q and k come out NaN), as ``rope_append`` does."""
-    idx = positions.long()
-    bad = (idx < 0) | (idx >= cos.shape[0])
-    idx = idx.clamp(0, cos.shape[0] - 1)
-    c, s = cos.index_select(0, idx), sin.index_select(0, idx)
-    nan = bad.unsqueeze(1)
-    return c.masked_fill_(nan, float("nan")), s.masked_fill_(nan, float("nan"))
+    ``quant_linear_rope_append`` reads. Gathered once per forward (one ``edgerag_rope_rows``
+    launch), shared by layers. A position outside the table gets a NaN row (its q and k come
+    out NaN), as ``rope_append`` does."""
+    require_device(positions, cos, sin)
+    if positions.dtype != torch.int32 or not positions.is_contiguous():
+        raise ValueError("positions must be a contiguous int32 tensor")
+    if cos.shape != sin.shape or cos.dim() != 2 or not cos.is_contiguous() or \
+            not sin.is_contiguous() or cos.dtype != sin.dtype:
+        raise ValueError("cos and sin must be matching contiguous (max_pos, head_dim) tables")
+    T = positions.numel()
+    c = torch.empty((T, cos.shape[1]), dtype=cos.dtype, device=cos.device)
+    s = torch.empty_like(c)
+    call("edgerag_rope_rows", positions.data_ptr(), T, cos.data_ptr(), sin.data_ptr(),
+         cos.shape[0], cos.shape[1], dtype_code(cos.dtype), c.data_ptr(), s.data_ptr(),
+         stream_ptr(positions.device))
+    return c, s
 
 
 def quant_rope_fused(m: int, k: int, bits: int, group_size: int, n_q_heads: int,

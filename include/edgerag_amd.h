@@ -480,6 +480,17 @@ int edgerag_rope_append(const void* qkv, int64_t qkv_stride, const int32_t* posi
                         void* stream);
 
 /*
+ * The per-token RoPE rows edgerag_quant_linear_rope_append reads: cos_out[t, :] =
+ * cos_table[positions[t], :] and likewise sin, for the n_tokens positions (device int32); a
+ * position outside [0, max_pos) gets a row of NaN (that token's q and k then come out NaN). One
+ * launch; tables [max_pos, head_dim] and outputs [n_tokens, head_dim] contiguous, in dtype.
+ * Replaces the per-call cos/sin of apply_rope (edgerag/core/layers.py:64-90) for one forward.
+ */
+int edgerag_rope_rows(const int32_t* positions, int32_t n_tokens, const void* cos_table,
+                      const void* sin_table, int32_t max_pos, int32_t head_dim, int32_t dtype,
+                      void* cos_out, void* sin_out, void* stream);
+
+/*
  * SwiGLU activation of the fused [gate | up] projection: out[t, c] = dtype(dtype(silu(g)) * u),
  * g = gate_up[t, c], u = gate_up[t, intermediate + c]. Replaces silu(gate_proj(x)) * up_proj(x)
  * (edgerag/core/layers.py:341).
