@@ -83,8 +83,8 @@ SIGNATURES: dict[str, tuple[list, object]] = {
         c_i32,
     ),
     "edgerag_paged_attention_fixed": (
-        [c_vp, c_i32, c_i32, c_i32, c_i64, c_i32, c_vp, c_i64, c_i64, c_vp, c_vp, c_i32, c_vp,
-         c_i64,
+        [c_vp, c_i32, c_i32, c_i32, c_i64, c_i32, c_i32, c_vp, c_i64, c_i64, c_vp, c_vp, c_i32,
+         c_vp, c_i64,
          c_vp, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_f32, c_vp, c_i64, c_i64, c_vp, c_i64,
          c_vp],
         c_i32,

@@ -221,7 +221,7 @@ __global__ __launch_bounds__(WG ? kMaxRowWaves * kWave : kWave) void attn_decode
     kb = b0;
   }
   const int32_t* rq = plan + plan[H_REQ_OFF] + r * kReqWords;
-  const int nsplit = rq[R_NSPLIT], part_off = rq[R_PARTOFF];
+  const int nsplit = rq[R_NSPLIT], part_off = rq[R_PARTOFF], pstride = rq[R_PSTRIDE];
   const int q0 = qsl[r], c = qsl[r + 1] - q0, L = ctx[r];
   const int n_rep = n_q_heads / n_kv_heads;
 
@@ -381,7 +381,7 @@ __global__ __launch_bounds__(WG ? kMaxRowWaves * kWave : kWave) void attn_decode
           }
           const int t = qb + v / n_rep;
           const int hq = h * n_rep + (v % n_rep);
-          if (nsplit == 1) {
+          if (pstride == 1) {
             const float inv = 1.f / fmaxf(lsum, 1.17549435e-38f);
             T* op = out + int64_t(t) * o_st + int64_t(hq) * o_sh;
 #pragma unroll
@@ -389,10 +389,14 @@ __global__ __launch_bounds__(WG ? kMaxRowWaves * kWave : kWave) void attn_decode
               const int d = lane + e * kWave;
               if (d < D) op[d] = from_f32<T>(a[e] * inv);
             }
-          } else {  // one of several parts of the context: a partial for the merge launch
-            const int64_t idx =
-                int64_t(part_off) + (int64_t(t - q0) * n_q_heads + hq) * nsplit + split;
+          } else {  // one of several parts of the context (or a slot): a partial for the merge
+            const int64_t row0 = int64_t(part_off) + (int64_t(t - q0) * n_q_heads + hq) * pstride;
+            const int64_t idx = row0 + split;
             if (lane == 0) part_ml[idx] = make_float2(mx, lsum);
+            // Slotted plans: the last part also marks the row's unused slots empty, so that a
+            // merge reading all of them gives them weight 0.
+            if (split == nsplit - 1 && nsplit + lane < pstride)
+              part_ml[row0 + nsplit + lane] = make_float2(-INFINITY, 0.f);
             float* pa = part_acc + idx * D;
 #pragma unroll
             for (int e = 0; e < (D + kWave - 1) / kWave; ++e) {
@@ -433,7 +437,7 @@ __global__ __launch_bounds__(WG ? kMaxRowWaves * kWave : kWave) void attn_decode
         for (int e = 0; e < VEC; ++e) op[e] = from_f32<T>(a[e] * inv);
       } else {
         const int64_t idx =
-            int64_t(part_off) + (int64_t(t - q0) * n_q_heads + hq) * nsplit + split;
+            int64_t(part_off) + (int64_t(t - q0) * n_q_heads + hq) * pstride + split;
         if (sub == 0) part_ml[idx] = make_float2(mm, lsum);
         float* pa = part_acc + idx * D + sub * VEC;
 #pragma unroll
@@ -464,7 +468,7 @@ __global__ __launch_bounds__(kWave) void attn_rows_kernel(
   const int r = it[I_REQ], h = it[I_HEAD], qb = it[I_QBEGIN], qc = it[I_QCOUNT];
   const int kb = it[I_KVBEGIN], ke = it[I_KVEND], split = it[I_SPLIT];
   const int32_t* rq = plan + plan[H_REQ_OFF] + r * kReqWords;
-  const int nsplit = rq[R_NSPLIT], part_off = rq[R_PARTOFF];
+  const int nsplit = rq[R_NSPLIT], part_off = rq[R_PARTOFF], pstride = rq[R_PSTRIDE];
   const int q0 = qsl[r], c = qsl[r + 1] - q0, L = ctx[r];
   const int n_rep = n_q_heads / n_kv_heads;
 
@@ -557,7 +561,7 @@ __global__ __launch_bounds__(kWave) void attn_rows_kernel(
         for (int e = 0; e < VEC; ++e) op[e] = from_f32<T>(a[e] * inv);
       } else {
         const int64_t idx =
-            int64_t(part_off) + (int64_t(t - q0) * n_q_heads + hq) * nsplit + split;
+            int64_t(part_off) + (int64_t(t - q0) * n_q_heads + hq) * pstride + split;
         if (sub == 0) part_ml[idx] = make_float2(mm, lsum);
         float* pa = part_acc + idx * D + sub * VEC;
 #pragma unroll
@@ -568,72 +572,56 @@ __global__ __launch_bounds__(kWave) void attn_rows_kernel(
 }
 
 // ---- combine -----------------------------------------------------------------------------------
-// Merges split partials (m, l, acc[D]) into the output: one thread per (combine-list row, query
-// head, 4 consecutive output elements), so a (row, head) pair takes D / 4 adjacent lanes and every
-// partial load is one 16-byte access. A thread issues the (m, l) and acc loads of up to
-// kCombineBatch splits together (the acc loads do not depend on (m, l)), so the chain of dependent
-// loads is entry -> {(m, l), acc}; more splits are merged batch by batch with a running maximum.
-// n_rows < 0 / combine_off < 0: read the list's length / offset from the device plan header
-// (fixed-capacity launches).
-constexpr int kCombineBatch = 8;
+// Merges split partials (m, l, acc[D]) into the output: one thread per (row, query head, 4
+// consecutive output elements), so a (row, head) pair takes D / 4 adjacent lanes and every partial
+// load is one 16-byte access. A thread issues the (m, l) and acc loads of up to kCombineBatch
+// splits together (the acc loads do not depend on (m, l)); more splits are merged batch by batch
+// with a running maximum.
+// * attn_combine_kernel reads each row's combine-list entry first: the chain of dependent loads
+//   is entry -> {(m, l), acc}. n_rows < 0 / combine_off < 0: the list's length / offset are read
+//   from the device plan header (fixed-capacity launches).
+// * attn_combine_slots_kernel serves slotted plans with row requests only: row t's partials sit in
+//   the H_SLOTS slots (t * n_q_heads + hq) * S + [0, S), the unused ones marked empty by the
+//   decode kernel, so every load address follows from the thread index alone and the merge takes
+//   one round trip.
+// Both fold the partials with merge_partials in slot order, so a row merges to the same values.
+constexpr int kCombineBatch = 16;
+
+// Folds one batch of partial records into the running (m, l, acc): weight exp2(m_k - max) for the
+// records that hold keys (take[k] and m_k > -inf); the others are skipped whatever their acc
+// holds (a slot never written this step may hold any bits).
+__device__ __forceinline__ void merge_partials(const float2 (&ml)[kCombineBatch],
+                                               const float4 (&v)[kCombineBatch],
+                                               const bool (&take)[kCombineBatch], float& m,
+                                               float& l, float4& acc) {
+  float mb = m;
+#pragma unroll
+  for (int k = 0; k < kCombineBatch; ++k)
+    if (take[k]) mb = fmaxf(mb, ml[k].x);
+  // No branch on mb == -inf (no record so far has seen a key): every weight below is then 0, and
+  // a branch here would make the compiler sink the acc loads behind the (m, l) wait.
+  const float r = m == -INFINITY ? 0.f : exp2_fast(m - mb);
+  l *= r;
+  acc.x *= r;
+  acc.y *= r;
+  acc.z *= r;
+  acc.w *= r;
+#pragma unroll
+  for (int k = 0; k < kCombineBatch; ++k) {
+    const bool on = take[k] && ml[k].x != -INFINITY;
+    const float w = on ? exp2_fast(ml[k].x - mb) : 0.f;
+    l = on ? fmaf(w, ml[k].y, l) : l;
+    acc.x = on ? fmaf(w, v[k].x, acc.x) : acc.x;
+    acc.y = on ? fmaf(w, v[k].y, acc.y) : acc.y;
+    acc.z = on ? fmaf(w, v[k].z, acc.z) : acc.z;
+    acc.w = on ? fmaf(w, v[k].w, acc.w) : acc.w;
+  }
+  m = mb;
+}
 
 template <typename T, bool VEC_OUT>
-__global__ __launch_bounds__(256) void attn_combine_kernel(
-    const int32_t* __restrict__ plan, int32_t n_rows, int32_t combine_off, int32_t n_q_heads,
-    int32_t ch_log2, const float2* __restrict__ part_ml, const float4* __restrict__ part_acc,
-    T* __restrict__ out, int64_t o_st, int64_t o_sh) {
-  const int gid = int(blockIdx.x) * int(blockDim.x) + int(threadIdx.x);
-  const int ch = gid & ((1 << ch_log2) - 1);
-  const int pair = gid >> ch_log2;
-  const int row = pair / n_q_heads;
-  const int hq = pair - row * n_q_heads;
-  if (row >= (n_rows >= 0 ? n_rows : plan[H_N_COMBINE])) return;
-  const int off = combine_off >= 0 ? combine_off : plan[H_COMBINE_OFF];
-  const int4* e4 = reinterpret_cast<const int4*>(plan + off + int64_t(row) * kCombineWords);
-  const int4 ea = e4[0], eb = e4[1];  // {tok, q0, c, L}, {nsplit, split_len, part_off, pad}
-  const int t = ea.x, q0 = ea.y, c = ea.z, L = ea.w;
-  const int nsplit = eb.x, split_len = eb.y, part_off = eb.z;
-  // Splits that start past this row's causal limit were never computed (lim >= 0 for every row
-  // the planner writes, since c <= L; the clamp keeps the arithmetic branch-free).
-  const int lim = max(L - c + (t - q0), 0);
-  const int n_valid = min(nsplit, lim / split_len + 1);
-  const int64_t base = int64_t(part_off) + (int64_t(t - q0) * n_q_heads + hq) * nsplit;
-  float m = -INFINITY, l = 0.f;
-  float4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int s0 = 0; s0 < n_valid; s0 += kCombineBatch) {
-    float2 ml[kCombineBatch];
-    float4 v[kCombineBatch];
-#pragma unroll
-    for (int k = 0; k < kCombineBatch; ++k) {
-      const int64_t p = base + min(s0 + k, n_valid - 1);  // clamped: extra splits weigh 0
-      ml[k] = part_ml[p];
-      v[k] = part_acc[(p << ch_log2) + ch];
-    }
-    float mb = m;
-#pragma unroll
-    for (int k = 0; k < kCombineBatch; ++k)
-      if (s0 + k < n_valid) mb = fmaxf(mb, ml[k].x);
-    // No branch on mb == -inf (no split so far has seen a key): every weight below is then 0, and
-    // a branch here would make the compiler sink the acc loads behind the (m, l) wait.
-    const float r = m == -INFINITY ? 0.f : exp2_fast(m - mb);
-    l *= r;
-    acc.x *= r;
-    acc.y *= r;
-    acc.z *= r;
-    acc.w *= r;
-#pragma unroll
-    for (int k = 0; k < kCombineBatch; ++k) {
-      const float w = (s0 + k < n_valid && ml[k].x != -INFINITY) ? exp2_fast(ml[k].x - mb) : 0.f;
-      l = fmaf(w, ml[k].y, l);
-      acc.x = fmaf(w, v[k].x, acc.x);
-      acc.y = fmaf(w, v[k].y, acc.y);
-      acc.z = fmaf(w, v[k].z, acc.z);
-      acc.w = fmaf(w, v[k].w, acc.w);
-    }
-    m = mb;
-  }
+__device__ __forceinline__ void store_merged(T* op, float4 acc, float l) {
   const float inv = 1.f / fmaxf(l, 1.17549435e-38f);
-  T* op = out + int64_t(t) * o_st + int64_t(hq) * o_sh + ch * 4;
   const T o0 = from_f32<T>(acc.x * inv), o1 = from_f32<T>(acc.y * inv),
           o2 = from_f32<T>(acc.z * inv), o3 = from_f32<T>(acc.w * inv);
   if constexpr (VEC_OUT) {
@@ -649,12 +637,89 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(
   }
 }
 
-// Enqueues the merge of n_rows combine-list rows (n_rows < 0: capacity `cap_rows`, length read
-// on the device).
+template <typename T, bool VEC_OUT>
+__global__ __launch_bounds__(256) void attn_combine_kernel(
+    const int32_t* __restrict__ plan, int32_t n_rows, int32_t combine_off, int32_t n_q_heads,
+    int32_t ch_log2, const float2* __restrict__ part_ml, const float4* __restrict__ part_acc,
+    T* __restrict__ out, int64_t o_st, int64_t o_sh) {
+  const int gid = int(blockIdx.x) * int(blockDim.x) + int(threadIdx.x);
+  const int ch = gid & ((1 << ch_log2) - 1);
+  const int pair = gid >> ch_log2;
+  const int row = pair / n_q_heads;
+  const int hq = pair - row * n_q_heads;
+  if (row >= (n_rows >= 0 ? n_rows : plan[H_N_COMBINE])) return;
+  const int off = combine_off >= 0 ? combine_off : plan[H_COMBINE_OFF];
+  const int4* e4 = reinterpret_cast<const int4*>(plan + off + int64_t(row) * kCombineWords);
+  const int4 ea = e4[0], eb = e4[1];  // {tok, q0, c, L}, {nsplit, split_len, part_off, pstride}
+  const int t = ea.x, q0 = ea.y, c = ea.z, L = ea.w;
+  const int nsplit = eb.x, split_len = eb.y, part_off = eb.z, pstride = eb.w;
+  // Splits that start past this row's causal limit were never computed (lim >= 0 for every row
+  // the planner writes, since c <= L; the clamp keeps the arithmetic branch-free).
+  const int lim = max(L - c + (t - q0), 0);
+  const int n_valid = min(nsplit, lim / split_len + 1);
+  const int64_t base = int64_t(part_off) + (int64_t(t - q0) * n_q_heads + hq) * pstride;
+  float m = -INFINITY, l = 0.f;
+  float4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < n_valid; s0 += kCombineBatch) {
+    float2 ml[kCombineBatch];
+    float4 v[kCombineBatch];
+    bool take[kCombineBatch];
+#pragma unroll
+    for (int k = 0; k < kCombineBatch; ++k) {
+      const int64_t p = base + min(s0 + k, n_valid - 1);  // clamped: extra splits weigh 0
+      ml[k] = part_ml[p];
+      v[k] = part_acc[(p << ch_log2) + ch];
+      take[k] = s0 + k < n_valid;
+    }
+    merge_partials(ml, v, take, m, l, acc);
+  }
+  store_merged<T, VEC_OUT>(out + int64_t(t) * o_st + int64_t(hq) * o_sh + ch * 4, acc, l);
+}
+
+// n_rows < 0: the token count is read from the device plan header (fixed-capacity launches), in
+// the same round trip as the partials (rows past it load in-bounds slots and store nothing). A
+// plan whose H_SLOTS differs from `slots` gets NaN rows: a launch shape that does not match the
+// staged plan fails loudly.
+template <typename T, bool VEC_OUT>
+__global__ __launch_bounds__(256) void attn_combine_slots_kernel(
+    const int32_t* __restrict__ plan, int32_t n_rows, int32_t slots, int32_t n_q_heads,
+    int32_t ch_log2, const float2* __restrict__ part_ml, const float4* __restrict__ part_acc,
+    T* __restrict__ out, int64_t o_st, int64_t o_sh) {
+  const int gid = int(blockIdx.x) * int(blockDim.x) + int(threadIdx.x);
+  const int ch = gid & ((1 << ch_log2) - 1);
+  const int pair = gid >> ch_log2;
+  const int t = pair / n_q_heads;
+  const int hq = pair - t * n_q_heads;
+  const int rows = n_rows >= 0 ? n_rows : plan[H_NUM_TOKENS_HINT];
+  const int plan_slots = plan[H_SLOTS];
+  const int64_t base = (int64_t(t) * n_q_heads + hq) * slots;
+  float m = -INFINITY, l = 0.f;
+  float4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < slots; s0 += kCombineBatch) {
+    float2 ml[kCombineBatch];
+    float4 v[kCombineBatch];
+    bool take[kCombineBatch];
+#pragma unroll
+    for (int k = 0; k < kCombineBatch; ++k) {
+      const int64_t p = base + min(s0 + k, slots - 1);
+      ml[k] = part_ml[p];
+      v[k] = part_acc[(p << ch_log2) + ch];
+      take[k] = s0 + k < slots;
+    }
+    issue_fence();  // every load of the batch is in flight before the row bound is looked at
+    merge_partials(ml, v, take, m, l, acc);
+  }
+  if (t >= rows) return;
+  if (plan_slots != slots) acc.x = acc.y = acc.z = acc.w = l = __builtin_nanf("");
+  store_merged<T, VEC_OUT>(out + int64_t(t) * o_st + int64_t(hq) * o_sh + ch * 4, acc, l);
+}
+
+// Enqueues the merge of n_rows rows (n_rows < 0: capacity `cap_rows`, the count read on the
+// device): combine-list rows, or with slots > 0 the tokens of a slotted plan.
 template <typename T>
 int launch_combine(hipStream_t s, const int32_t* plan_dev, int32_t n_rows, int32_t cap_rows,
-                   int32_t combine_off, int32_t n_q_heads, int32_t head_dim, const float2* ml,
-                   const float* pacc, void* out, int64_t o_st, int64_t o_sh) {
+                   int32_t combine_off, int32_t slots, int32_t n_q_heads, int32_t head_dim,
+                   const float2* ml, const float* pacc, void* out, int64_t o_st, int64_t o_sh) {
   const int rows = n_rows >= 0 ? n_rows : cap_rows;
   const int ch_log2 = log2_exact(head_dim / 4);
   const int64_t threads = (int64_t(rows) * n_q_heads) << ch_log2;
@@ -663,17 +728,26 @@ int launch_combine(hipStream_t s, const int32_t* plan_dev, int32_t n_rows, int32
   if (threads > INT32_MAX - 256)
     return fail(EDGERAG_EUNSUPPORTED, "attention combine: %d rows x %d heads too many", rows,
                 n_q_heads);
+  if (threads == 0) return EDGERAG_OK;
   const dim3 block(256), grid(unsigned((threads + 255) / 256));
   const auto* acc4 = reinterpret_cast<const float4*>(pacc);
   T* o = static_cast<T*>(out);
   const bool vec = reinterpret_cast<uintptr_t>(out) % (4 * sizeof(T)) == 0 && o_st % 4 == 0 &&
                    o_sh % 4 == 0;
-  if (vec)
+  if (slots > 0) {
+    if (vec)
+      hipLaunchKernelGGL((attn_combine_slots_kernel<T, true>), grid, block, 0, s, plan_dev, n_rows,
+                         slots, n_q_heads, ch_log2, ml, acc4, o, o_st, o_sh);
+    else
+      hipLaunchKernelGGL((attn_combine_slots_kernel<T, false>), grid, block, 0, s, plan_dev,
+                         n_rows, slots, n_q_heads, ch_log2, ml, acc4, o, o_st, o_sh);
+  } else if (vec) {
     hipLaunchKernelGGL((attn_combine_kernel<T, true>), grid, block, 0, s, plan_dev, n_rows,
                        combine_off, n_q_heads, ch_log2, ml, acc4, o, o_st, o_sh);
-  else
+  } else {
     hipLaunchKernelGGL((attn_combine_kernel<T, false>), grid, block, 0, s, plan_dev, n_rows,
                        combine_off, n_q_heads, ch_log2, ml, acc4, o, o_st, o_sh);
+  }
   return EDGERAG_OK;
 }
 
@@ -939,6 +1013,7 @@ extern "C" int edgerag_attn_plan_ex(const int32_t* query_start_loc, const int32_
   const int64_t part_cap = int64_t(kRowWgWaves) * round_up(wave_cap, block_size);
   bool wg_rows = false;
   int row_waves = 0;
+  int slots = 0;        // partial slots per (token, q head) of the row requests (0: nsplit)
   int64_t wg_part = 0;  // longest part of a context one row workgroup takes (0: whole contexts)
   if (wg_capable && kRowTargetWgs > 0 && row_items < kPlanCUs) {
     // Parts take kRowPartWaves waves: single-sequence attention over 6,758 tokens measured
@@ -952,6 +1027,19 @@ extern "C" int edgerag_attn_plan_ex(const int32_t* query_start_loc, const int32_
     wg_part = std::min(cap, std::max(min_part, round_up(want, block_size)));
     wg_rows = true;
     row_waves = kRowPartWaves;
+    // The parts write their partials to S fixed slots per (token, q head), the unused ones
+    // marked empty, so that a merge addresses every partial from its thread index alone and
+    // needs one round trip (attn_combine_slots_kernel). S (a power of two) covers the parts
+    // kRowTargetWgs workgroups give one request; contexts that would need more take longer parts.
+    // A batch whose contexts all fit one part has nothing to merge and stays unslotted.
+    const int64_t want_slots = (kRowTargetWgs + n_kv_heads - 1) / n_kv_heads;
+    int s = 2;
+    while (s < want_slots && s < kMaxPartSlots) s *= 2;
+    const int64_t slot_part = round_up((max_row_len + s - 1) / s, block_size);
+    if (slot_part <= cap && max_row_len > std::max(wg_part, slot_part)) {
+      wg_part = std::max(wg_part, slot_part);
+      slots = s;
+    }
   } else if (wg_capable && max_row_len <= part_cap) {
     wg_rows = true;
     row_waves = kRowWgWaves;
@@ -1014,17 +1102,21 @@ extern "C" int edgerag_attn_plan_ex(const int32_t* query_start_loc, const int32_
     // Workgroup-split rows: one item per part of the context (the waves split the part).
     const int64_t slen = row ? (wg_rows ? wg_split_len(L) : split_len) : tile_split_len(L);
     const int nsplit = c == 0 ? 0 : int((L + slen - 1) / slen);
+    // Slotted row requests write partials (and get merge rows) even when not split.
+    const bool slotted = slots > 0 && row;
+    const int pstride = slotted ? slots : nsplit;
     rq[R_NSPLIT] = nsplit;
     rq[R_SPLITLEN] = int32_t(slen);
     rq[R_PARTOFF] = int32_t(n_partials);
+    rq[R_PSTRIDE] = pstride;
     if (c == 0) continue;
-    if (nsplit > 1) {
+    if (nsplit > 1 || slotted) {
       for (int t = q0; t < q0 + c; ++t) {
         const int32_t e[kCombineWords] = {t, q0, c, L, nsplit, int32_t(slen),
-                                          int32_t(n_partials), 0};
+                                          int32_t(n_partials), pstride};
         combine.insert(combine.end(), e, e + kCombineWords);
       }
-      n_partials += int64_t(c) * n_q_heads * nsplit;
+      n_partials += int64_t(c) * n_q_heads * pstride;
     }
     if (n_partials > INT32_MAX)
       return fail(EDGERAG_EUNSUPPORTED, "edgerag_attn_plan: batch needs > 2^31 split partials");
@@ -1085,6 +1177,7 @@ extern "C" int edgerag_attn_plan_ex(const int32_t* query_start_loc, const int32_
   plan[H_TILE_KIND] = mfma_tiles ? 1 : 0;
   plan[H_ROW_WAVES] = row_waves;
   plan[H_OVERLAP] = overlap ? 1 : 0;
+  plan[H_SLOTS] = slots;
   std::copy(combine.begin(), combine.end(), plan + combine_off);
   int32_t* dst = plan + item_off;
   for (const auto* groups : {&rows, &tiles})
@@ -1233,10 +1326,13 @@ int paged_attention_impl(
   }
   const int n_combine = plan_host[H_N_COMBINE];
   if (rc != EDGERAG_OK || n_combine == 0 || !(parts & EDGERAG_ATTN_COMBINE)) return rc;
+  // A slotted plan of row requests only lists every token, in order: the one-round-trip merge.
+  const int slots =
+      plan_host[H_N_ITEMS] == plan_host[H_N_ROW_ITEMS] ? std::max(plan_host[H_SLOTS], 0) : 0;
 
   switch (dtype) {
 #define EDGERAG_COMBINE(TYPE)                                                                     \
-  rc = launch_combine<TYPE>(a.s, plan_dev, n_combine, n_combine, plan_host[H_COMBINE_OFF],          \
+  rc = launch_combine<TYPE>(a.s, plan_dev, n_combine, n_combine, plan_host[H_COMBINE_OFF], slots, \
                             n_q_heads, head_dim, a.ml, a.pacc, out, out_stride_tok,               \
                             out_stride_head)
     case EDGERAG_F32: EDGERAG_COMBINE(float); break;
@@ -1346,7 +1442,7 @@ int run_fixed_dtype(const Launch& a, int32_t D, int qr, int max_items, int row_w
 
 extern "C" int edgerag_paged_attention_fixed(
     const int32_t* plan_dev, int32_t max_row_items, int32_t max_combine_rows,
-    int32_t max_row_vecs, int64_t max_partials, int32_t row_waves, const void* q,
+    int32_t max_row_vecs, int64_t max_partials, int32_t row_waves, int32_t slots, const void* q,
     int64_t q_stride_tok,
     int64_t q_stride_head, const void* key_pool, const void* value_pool, int32_t dtype,
     const int32_t* block_tables, int64_t block_tables_stride, const int32_t* query_start_loc,
@@ -1375,6 +1471,12 @@ extern "C" int edgerag_paged_attention_fixed(
                 "edgerag_paged_attention_fixed: row_waves %d (1..%d workgroup-split rows need "
                 "head_dim <= 128 and the fast decode kernel's block sizes)",
                 row_waves, kMaxRowWaves);
+  if (slots < 0 || slots > kMaxPartSlots || (slots > 0 && row_waves == 0) ||
+      (slots > 0 && max_partials < int64_t(max_combine_rows) * n_q_heads * slots))
+    return fail(EDGERAG_EINVAL,
+                "edgerag_paged_attention_fixed: slots %d (0, or 1..%d with row_waves > 0 and "
+                "partials for every slot of %d rows x %d heads)",
+                slots, kMaxPartSlots, max_combine_rows, n_q_heads);
   if (!(scale > 0.f) || !std::isfinite(scale))
     return fail(EDGERAG_EINVAL, "edgerag_paged_attention_fixed: scale must be positive");
   const int es = elem_size(dtype);
@@ -1423,11 +1525,11 @@ extern "C" int edgerag_paged_attention_fixed(
     }
   }
   if (rc != EDGERAG_OK || max_combine_rows == 0) return rc;
-  // No host plan here: the kernel reads the list's length and offset from the device header.
+  // No host plan here: the kernel reads the list's length (and offset) from the device header.
   switch (dtype) {
 #define EDGERAG_COMBINE_FIXED(TYPE)                                                               \
-  rc = launch_combine<TYPE>(a.s, plan_dev, -1, max_combine_rows, -1, n_q_heads, head_dim, a.ml,  \
-                            a.pacc, out, out_stride_tok, out_stride_head)
+  rc = launch_combine<TYPE>(a.s, plan_dev, -1, max_combine_rows, -1, slots, n_q_heads, head_dim, \
+                            a.ml, a.pacc, out, out_stride_tok, out_stride_head)
     case EDGERAG_F32: EDGERAG_COMBINE_FIXED(float); break;
     case EDGERAG_F16: EDGERAG_COMBINE_FIXED(f16); break;
     case EDGERAG_BF16: EDGERAG_COMBINE_FIXED(bf16); break;

@@ -8,7 +8,7 @@ namespace edgerag {
 namespace plan {
 
 constexpr int32_t kMagic = 0x47415245;  // "ERAG"
-constexpr int32_t kVersion = 5;
+constexpr int32_t kVersion = 6;
 constexpr int kHeaderWords = 24;
 constexpr int kItemWords = 8;
 constexpr int kReqWords = 4;
@@ -38,15 +38,22 @@ enum Header {
                        // W > 0: one workgroup per row item, its W waves split the keys and
                        // merge in LDS (partials only where a context is cut into parts)
   H_OVERLAP,           // 1: planned for tiles and rows on two streams (tiles shared), 0: one
+  H_SLOTS,             // S > 0: the row requests' partials sit in S slots per (token, q head)
+                       // (rows cut into parts); 0: nsplit slots per (token, q head)
 };
 // Waves a workgroup-split row item may use (the kernel's LDS merge is sized for this many).
 constexpr int kMaxRowWaves = 16;
 enum Item { I_REQ = 0, I_HEAD, I_QBEGIN, I_QCOUNT, I_KVBEGIN, I_KVEND, I_SPLIT, I_PAD };
 static_assert(kItemWords == 8 && I_KVBEGIN == 4 && I_PAD == 7,
               "the decode kernel reads an item as two int4 words");
-enum Req { R_NSPLIT = 0, R_SPLITLEN, R_PARTOFF, R_PAD };
+// R_PSTRIDE: partial slots per (token, q head): nsplit, or H_SLOTS for slotted row requests,
+// whose splits past nsplit hold empty records (m = -inf). Partial (t, hq, s) of request r sits at
+// R_PARTOFF + ((t - q0) * n_q_heads + hq) * R_PSTRIDE + s.
+enum Req { R_NSPLIT = 0, R_SPLITLEN, R_PARTOFF, R_PSTRIDE };
 // Combine-list entry: everything one merge needs in a single 32-byte load.
-enum Combine { C_TOK = 0, C_Q0, C_C, C_L, C_NSPLIT, C_SPLITLEN, C_PARTOFF, C_PAD };
+enum Combine { C_TOK = 0, C_Q0, C_C, C_L, C_NSPLIT, C_SPLITLEN, C_PARTOFF, C_PSTRIDE };
+// Largest slot count of a slotted plan (the slotted merge launch reads every slot of a row).
+constexpr int kMaxPartSlots = 32;
 
 }  // namespace plan
 

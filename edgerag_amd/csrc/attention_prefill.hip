@@ -216,7 +216,7 @@ void attn_prefill_mfma_kernel(
   const int r = it[I_REQ], h = it[I_HEAD], qb = it[I_QBEGIN], qc = it[I_QCOUNT];
   const int kb = it[I_KVBEGIN], ke = it[I_KVEND], split = it[I_SPLIT];
   const int32_t* rq = plan + plan[H_REQ_OFF] + r * kReqWords;
-  const int nsplit = rq[R_NSPLIT], part_off = rq[R_PARTOFF];
+  const int nsplit = rq[R_NSPLIT], part_off = rq[R_PARTOFF], pstride = rq[R_PSTRIDE];
   const int q0 = qsl[r], c = qsl[r + 1] - q0, L = ctx[r];
   const int n_rep = n_q_heads / n_kv_heads;
   const int32_t* table = block_tables + int64_t(r) * bt_stride;
@@ -418,7 +418,7 @@ void attn_prefill_mfma_kernel(
     }
   } else {
     // Partials carry the max in the log2 domain, like the decode kernels'.
-    const int64_t idx = int64_t(part_off) + (int64_t(t - q0) * n_q_heads + hq) * nsplit + split;
+    const int64_t idx = int64_t(part_off) + (int64_t(t - q0) * n_q_heads + hq) * pstride + split;
     if (g == 0) part_ml[idx] = make_float2(m, l);
     float* pa = part_acc + idx * kD;
 #pragma unroll

@@ -39,6 +39,15 @@ template <> __device__ __forceinline__ bf16 from_f32<bf16>(float v) { return __f
 
 template <typename T> struct Same { static constexpr bool value = false; };
 
+// Compiler-only fence: keeps the loads issued above it from being sunk below it (next to their
+// first use), which would serialise memory latency with the compute they are meant to overlap.
+// The memory clobber stops IR-level code motion; the scheduling barrier stops the machine
+// scheduler, which otherwise moves each load next to its first use to save registers.
+__device__ __forceinline__ void issue_fence() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // A plain 16-byte register payload. Loads/stores through it compile to dwordx4 accesses.
 struct alignas(16) Vec16 {
   uint32_t w[4];

@@ -146,15 +146,6 @@ __device__ __forceinline__ uint4 ldg16(const void* p) {
   return *reinterpret_cast<const uint4*>(p);
 }
 
-// Compiler-only fence: keeps the loads issued above it from being sunk below it (next to their
-// first use), which would serialise memory latency with the compute they are meant to overlap.
-// The memory clobber stops IR-level code motion; the scheduling barrier stops the machine
-// scheduler, which otherwise moves each load next to its first use to save registers.
-__device__ __forceinline__ void issue_fence() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_sched_barrier(0);
-}
-
 // ---- skinny kernel (M <= 64) ----------------------------------------------------------------
 constexpr int kMaxSkinnyWaves = 8;
 

@@ -538,10 +538,13 @@ class FixedAttention:
     by :meth:`update` (one pinned H2D copy): cu_seqlens, context lengths, block tables with a
     fixed row stride, caller-defined extra int32 arrays (token ids, positions, slots, ...) and the
     plan. :meth:`launch` calls ``edgerag_paged_attention_fixed``, whose grid depends only on the
-    capacities and on :attr:`row_waves`, the launch mode of the staged plan: 0 for KV splits
+    capacities and on :attr:`mode`, the launch mode of the staged plan: row waves 0 for KV splits
     merged by a combine launch, > 0 for workgroup-split rows (the planner takes these when every
-    context is short). A captured graph stays valid for every plan :meth:`update` accepts in the
-    mode it was captured in, so callers key their graphs by :attr:`row_waves` as well.
+    context is short, or cuts the contexts into parts when the batch has few requests); whether
+    a merge launch follows; and the plan's partial slots (parts in fixed slots take the merge
+    launch that reads no plan entry first). A captured graph stays valid for every plan
+    :meth:`update` accepts in the mode it was captured in, so callers key their graphs by
+    :attr:`mode` as well.
     The pinned host staging buffer is reused: the caller must have synchronised with the previous
     step (the executor does, when it reads the tokens back) before calling :meth:`update` again.
     """
@@ -562,13 +565,15 @@ class FixedAttention:
         # workgroup-split rows (one workgroup per request and kv head, or per part of a context
         # when the batch has few requests), the latter bounded by the planner itself.
         self.max_combine = max_reqs
-        max_splits = -(-max_blocks_per_seq * block_size // min(min_split, 128))
+        # Every slot of a slotted plan (at most 32 per token and head) or every split.
+        max_splits = max(-(-max_blocks_per_seq * block_size // min(min_split, 128)), 32)
         self.max_partials = max_reqs * n_q_heads * max_splits
         self.max_items = max_items
         self.wg_items = int(_lib.load().edgerag_attn_fixed_row_items(
             max_reqs, n_kv_heads, max_blocks_per_seq * block_size, block_size))
         self.row_waves = 0
         self.combine = False
+        self.slots = 0
         self.plan_words = 24 + 8 * max_items + 4 * max_reqs + 8 * self.max_combine + 64
 
         def pad(n: int) -> int:
@@ -614,7 +619,7 @@ class FixedAttention:
                                  self.head_dim, self.block_size, self.max_blocks, self.dtype,
                                  self.split_rows)
         n_items, n_row, n_partials = int(plan[2]), int(plan[13]), int(plan[6])
-        row_waves, n_combine = int(plan[19]), int(plan[16])
+        row_waves, n_combine, slots = int(plan[19]), int(plan[16]), int(plan[21])
         if (n_items != n_row or n_row > (self.wg_items if row_waves else self.max_items)
                 or n_combine > self.max_combine
                 or int(plan[14]) > self.max_row_vecs or n_partials > self.max_partials
@@ -638,13 +643,14 @@ class FixedAttention:
         self.num_reqs = R
         self.row_waves = row_waves
         self.combine = n_combine > 0
+        self.slots = slots if self.combine else 0
         return True
 
     @property
-    def mode(self) -> tuple[int, bool]:
-        """The launch shape the staged plan needs: (row waves, merge launch). A graph captured
-        in one mode replays every plan staged in that mode."""
-        return self.row_waves, self.combine
+    def mode(self) -> tuple[int, bool, int]:
+        """The launch shape the staged plan needs: (row waves, merge launch, partial slots). A
+        graph captured in one mode replays every plan staged in that mode."""
+        return self.row_waves, self.combine, self.slots
 
     def launch(self, query: torch.Tensor, key_pool: torch.Tensor, value_pool: torch.Tensor,
                scale: float, out: torch.Tensor) -> torch.Tensor:
@@ -655,7 +661,7 @@ class FixedAttention:
         combine, partials = (self.max_combine, self.max_partials) if self.combine else (0, 0)
         call(
             "edgerag_paged_attention_fixed", self.plan.data_ptr(), items, combine,
-            self.max_row_vecs, partials, self.row_waves, query.data_ptr(),
+            self.max_row_vecs, partials, self.row_waves, self.slots, query.data_ptr(),
             query.stride(0), query.stride(1), key_pool.data_ptr(), value_pool.data_ptr(),
             dtype_code(key_pool.dtype), self.block_tables.data_ptr(), self.max_blocks,
             self.qsl.data_ptr(), self.ctx.data_ptr(), self.n_q_heads, n_kv, head_dim, block_size,

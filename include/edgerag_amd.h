@@ -135,7 +135,10 @@ int edgerag_attn_plan(const int32_t* query_start_loc, const int32_t* context_len
  * split the context and merge in LDS (no split partials, no merge launch), whenever the fast
  * decode kernel takes the shape and every such context fits 16 waves of 64 blocks; otherwise,
  * or with EDGERAG_PLAN_SPLIT_ROWS, as one workgroup per KV split merged through fp32 partials
- * in the workspace. Results agree to fp32 rounding either way.
+ * in the workspace. Results agree to fp32 rounding either way. A batch with fewer such
+ * workgroups than CUs (few decodes) instead cuts every row context into parts of 8 waves, one
+ * workgroup each, whose partials sit in S fixed slots per (token, query head): plan word 21
+ * holds S (0 when the rows are not slotted), and every row token then has a merge row.
  *
  * A batch with both prefill tiles and decode rows is planned for one of two runs, recorded in
  * plan word 20 (1: two streams, 0: one): the tiles (EDGERAG_ATTN_TILES | EDGERAG_ATTN_TILES_SHARED)
@@ -230,7 +233,11 @@ int edgerag_paged_attention_append(
  * EDGERAG_PLAN_SPLIT_ROWS). Such a plan may still cut a context into parts (one row item each,
  * merged by the combine launch through partials: batches of few decodes); pass
  * max_combine_rows = 0 only for plans without combine rows (word 16 zero), which then need no
- * workspace.
+ * workspace. slots: the plan's word 21. With slots > 0 (parts in fixed slots, row_waves > 0) the
+ * merge launch addresses every partial from its thread index, reads the token count from the
+ * plan and takes one round trip; max_combine_rows is then the token capacity and max_partials
+ * must hold max_combine_rows * n_q_heads * slots partials. A replayed plan whose word 21 differs
+ * from `slots` gets NaN outputs instead of a wrong merge.
  *
  * No counterpart in the reference: it exists so that the decode step of the serving loop
  * (edgerag/serve/executor.py:138-154 replaced by one packed forward) can be replayed from a graph.
@@ -243,8 +250,8 @@ int64_t edgerag_attn_fixed_row_items(int32_t max_reqs, int32_t n_kv_heads, int32
                                      int32_t block_size);
 int edgerag_paged_attention_fixed(const int32_t* plan_dev, int32_t max_row_items,
                                   int32_t max_combine_rows, int32_t max_row_vecs,
-                                  int64_t max_partials, int32_t row_waves, const void* q,
-                                  int64_t q_stride_tok,
+                                  int64_t max_partials, int32_t row_waves, int32_t slots,
+                                  const void* q, int64_t q_stride_tok,
                                   int64_t q_stride_head, const void* key_pool,
                                   const void* value_pool, int32_t dtype,
                                   const int32_t* block_tables, int64_t block_tables_stride,

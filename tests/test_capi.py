@@ -174,14 +174,22 @@ def test_validation_errors_come_back_as_messages() -> None:
             _lib.call("edgerag_paged_attention", None, None, 0, None, 0, 0, None, None, 1, None,
                       0, None, None, 0, 0, 4, 4, 64, 16, 1, 1.0, None, 0, 0, None, 0, parts, None)
     with pytest.raises(_lib.EdgeragError, match="capacities"):
-        _lib.call("edgerag_paged_attention_fixed", 16, -1, 0, 1, 0, 0, 16, 0, 0, 16, 16, 1, 16,
-                  0, 16, 16, 4, 4, 64, 16, 1, 1.0, 16, 0, 0, None, 0, None)
+        _lib.call("edgerag_paged_attention_fixed", 16, -1, 0, 1, 0, 0, 0, 16, 0, 0, 16, 16, 1,
+                  16, 0, 16, 16, 4, 4, 64, 16, 1, 1.0, 16, 0, 0, None, 0, None)
     with pytest.raises(_lib.EdgeragError, match="row_waves"):  # past the 16-wave merge space
-        _lib.call("edgerag_paged_attention_fixed", 16, 4, 0, 1, 0, 17, 16, 0, 0, 16, 16, 1, 16,
-                  0, 16, 16, 4, 4, 64, 16, 1, 1.0, 16, 0, 0, None, 0, None)
+        _lib.call("edgerag_paged_attention_fixed", 16, 4, 0, 1, 0, 17, 0, 16, 0, 0, 16, 16, 1,
+                  16, 0, 16, 16, 4, 4, 64, 16, 1, 1.0, 16, 0, 0, None, 0, None)
     with pytest.raises(_lib.EdgeragError, match="row_waves"):  # head_dim past 128
-        _lib.call("edgerag_paged_attention_fixed", 16, 4, 0, 1, 0, 16, 16, 0, 0, 16, 16, 1, 16,
-                  0, 16, 16, 4, 4, 256, 16, 1, 1.0, 16, 0, 0, None, 0, None)
+        _lib.call("edgerag_paged_attention_fixed", 16, 4, 0, 1, 0, 16, 0, 16, 0, 0, 16, 16, 1,
+                  16, 0, 16, 16, 4, 4, 256, 16, 1, 1.0, 16, 0, 0, None, 0, None)
+    # Slots: past 32, without workgroup rows, or more than the partials hold (2 rows x 4 heads x
+    # 16 slots = 128 > 100).
+    for rows, partials, row_waves, slots in ((2, 4096, 8, 64), (2, 4096, 0, 16),
+                                             (2, 100, 8, 16)):
+        with pytest.raises(_lib.EdgeragError, match="slots"):
+            _lib.call("edgerag_paged_attention_fixed", 16, 4, rows, 1, partials, row_waves,
+                      slots, 16, 0, 0, 16, 16, 1, 16, 0, 16, 16, 4, 4, 64, 16, 1, 1.0, 16, 0, 0,
+                      16, 1 << 20, None)
     with pytest.raises(_lib.EdgeragError, match="width"):
         _lib.call("edgerag_rmsnorm", None, 0, None, 0, None, None, 0, None, 0, 1, 0, 1e-5, 1,
                   None)
@@ -235,11 +243,17 @@ def check_coverage(qsl, ctx, n_q, n_kv, bs=16):
                 assert key not in seen
                 seen[key] = min(ke, lim + 1) - kb
     n_partials = 0
+    slots = int(plan[21])
     for r in range(len(ctx)):
         q0, c, L = qsl[r], qsl[r + 1] - qsl[r], ctx[r]
-        nsplit, split_len = int(reqs[r][0]), int(reqs[r][1])
-        if c and nsplit > 1:
-            n_partials += c * n_q * nsplit
+        nsplit, split_len, part_off, pstride = (int(w) for w in reqs[r])
+        row = c * n_rep <= 8
+        # Slotted row requests: S slots per (token, head), even when not split.
+        assert pstride == (slots if slots and row else nsplit), r
+        assert nsplit <= pstride
+        assert part_off == n_partials, r
+        if c and (nsplit > 1 or (slots and row)):
+            n_partials += c * n_q * pstride
         for t in range(q0, q0 + c):
             lim = L - c + (t - q0)
             for hq in range(n_q):
@@ -254,15 +268,28 @@ def check_coverage(qsl, ctx, n_q, n_kv, bs=16):
 def check_parts(ctx, h, bs, items, reqs, plan) -> None:
     """A batch of fewer row workgroups than CUs: each context in equal whole-block parts of at
     least 8 waves x 32 tokens, about 512 workgroups in all (never more than 512 plus one per
-    request and head), one combine row per request cut into several parts."""
+    request and head), their partials in fixed slots: every token has a merge row."""
     work = sum(ctx) * h
     part = min(8 * 64 * bs, max(8 * 32, -(-(-(-work // 512)) // bs) * bs))
+    slots = int(plan[21])
+    if max(ctx) <= part:  # no context cut: nothing to merge, no slots
+        assert slots == 0 and int(plan[16]) == 0
+        return
+    part = max(part, -(-(-(-max(ctx) // slots)) // bs) * bs)  # at most `slots` parts
     for r, L in enumerate(ctx):
         n = -(-L // part) if L > part else 1
         slen = max(L, 1) if n == 1 else -(-(-(-L // n)) // bs) * bs
         assert (int(reqs[r][0]), int(reqs[r][1])) == (-(-L // slen) if L else 0, slen), r
     assert items.shape[0] <= 512 + len(ctx) * h
-    assert int(plan[16]) == sum(1 for r in range(len(ctx)) if int(reqs[r][0]) > 1)
+    # Parts in fixed slots: a power of two covering 512 / h parts (at most 32); every token of the
+    # batch has a merge row, in token order, naming its slots.
+    assert slots == min(32, 1 << max(1, (-(-512 // h) - 1).bit_length()))
+    assert all(int(reqs[r][0]) <= slots for r in range(len(ctx)))
+    n_tok = len(ctx)
+    assert int(plan[16]) == n_tok
+    comb = plan[int(plan[17]) : int(plan[17]) + 8 * n_tok].reshape(n_tok, 8)
+    for t, e in enumerate(comb.tolist()):
+        assert e[0] == t and e[6] == t * h * slots and e[7] == slots, e
 
 
 def test_fixed_capacity_bounds_the_planner() -> None:

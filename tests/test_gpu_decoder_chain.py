@@ -116,7 +116,10 @@ def test_fixed_attention_long_contexts_split_merge_and_graph_replays(device, spl
         lens, tables, bt, qsl, q, _ = cases[name]
         torch.cuda.synchronize()  # update() reuses its pinned staging buffer
         assert fx.update(qsl, np.asarray(lens, np.int32), bt, [])
-        assert fx.mode == (int(cases[name][5][19]), int(cases[name][5][16]) > 0)
+        plan = cases[name][5]
+        assert fx.mode == (int(plan[19]), int(plan[16]) > 0, int(plan[21]))
+        # Parts of few contexts sit in 16 fixed slots per (token, head) (32 kv heads).
+        assert int(plan[21]) == (16 if fx.mode[0] == 8 else 0)
         q_static.zero_()
         q_static[: len(lens)].copy_(q.to(device))
         out.fill_(float("nan"))
@@ -144,6 +147,33 @@ def test_fixed_attention_long_contexts_split_merge_and_graph_replays(device, spl
         assert torch.equal(got, eager), f"plan {name}: replay differs from the eager launch"
         expected = oa.ragged_reference(q, kp_cpu, vp_cpu, qsl.tolist(), lens, tables, 0.125)
         torch.testing.assert_close(got.float().cpu(), expected, **FP16_TOL)
+
+
+def test_fixed_slotted_merge_fails_loudly_on_a_mismatched_plan(device) -> None:
+    """The slotted merge launch reads no plan entry: a staged plan whose slot count (word 21)
+    differs from the launch's gives NaN rows instead of a merge over the wrong slots."""
+    n_q = n_kv = 32
+    d, bs, cap = 64, 16, 2
+    max_blocks = math.ceil(3000 / bs)
+    NB = cap * max_blocks + 16
+    gd = torch.Generator(device=device).manual_seed(43)
+    kp = torch.randn((n_kv, NB, bs, d), generator=gd, device=device, dtype=torch.float16)
+    vp = torch.randn((n_kv, NB, bs, d), generator=gd, device=device, dtype=torch.float16)
+    fx = kernels.FixedAttention(device, n_q, n_kv, d, bs, torch.float16, cap, max_blocks, [])
+    _, bt = _tables([3000], bs, NB, seeded(43))
+    qsl = np.array([0, 1], np.int32)
+    assert fx.update(qsl, np.array([3000], np.int32), bt, [])
+    assert fx.mode == (8, True, 16)
+    q = torch.randn((cap, n_q, d), generator=gd, device=device, dtype=torch.float16)
+    out = torch.full_like(q, float("nan"))
+    fx.launch(q, kp, vp, 0.125, out)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out[:1]).all())
+    fx.plan[21] = 0  # the staged plan now claims unslotted partials
+    out.fill_(0.0)
+    fx.launch(q, kp, vp, 0.125, out)
+    torch.cuda.synchronize()
+    assert bool(torch.isnan(out[:1]).all())
 
 
 # --- the decoder's fused decode chain at full width ---------------------------------------------
@@ -260,7 +290,7 @@ def test_decoder_at_cfg5_lengths_through_every_decode_attention_mode(device) -> 
     lens = [4080, 300, 1100, 512, 700, 256, 900, 450]
     max_new = [26, 18, 19, 20, 21, 22, 23, 24]
     prompts = [torch.randint(1, 49151, (n,), generator=g).tolist() for n in lens]
-    modes: list[tuple[int, bool]] = []
+    modes: list[tuple[int, bool, int]] = []
     alloc = BlockAllocator(1024, 16)
     executor = ModelExecutor(model, spec, alloc, device, model.dtype, chunk_size=512)
     sched = Scheduler(alloc, SchedulerConfig(max_batch_size=8))
@@ -280,7 +310,7 @@ def test_decoder_at_cfg5_lengths_through_every_decode_attention_mode(device) -> 
     print("cfg5 lengths: 8 requests, a 4,080-token prompt", flush=True)
     drive(sched, executor, on_step=on_step)
     assert alloc.num_free == alloc.num_blocks
-    assert {(16, False), (0, True), (8, True)} <= set(modes), modes
+    assert {(16, False, 0), (0, True, 0), (8, True, 16)} <= set(modes), modes
     oracle = om.OracleDecoder(weights, torch.float32)
     for r, p in zip(reqs, prompts):
         steps = record[r.request_id]
