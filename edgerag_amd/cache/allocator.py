@@ -98,6 +98,9 @@ class BlockAllocator:
         self.num_blocks = int(num_blocks)
         self.block_size = int(block_size)
         self._owners = np.zeros(self.num_blocks, dtype=np.int32)
+        # Owners past the first, summed over blocks: 0 when nothing is shared, which lets the
+        # per-step copy-on-write checks skip the owner array.
+        self._extra_owners = 0
         self._stack = np.arange(self.num_blocks - 1, -1, -1, dtype=np.int32)
         self._top = self.num_blocks
         self.counters = PoolCounters()
@@ -177,6 +180,8 @@ class BlockAllocator:
                              if self._owners[b] == 0], dtype=np.int64)
         self._stack[self._top : self._top + back.size] = back
         self._top += back.size
+        # Every listing but a block's last (the one that frees it) dropped an extra owner.
+        self._extra_owners -= int(ids.size - back.size)
         self.counters.blocks_released += int(ids.size)
         return int(back.size)
 
@@ -192,6 +197,7 @@ class BlockAllocator:
                 f"block {int(unowned[0])} is free: only owned blocks can be shared"
             )
         np.add.at(self._owners, ids, 1)
+        self._extra_owners += int(ids.size)
         self.counters.shares += int(ids.size)
 
     def copy_on_write(self, block: int) -> int:
@@ -205,6 +211,7 @@ class BlockAllocator:
             return int(block)
         fresh = self.allocate(1)[0]
         self._owners[block] -= 1
+        self._extra_owners -= 1
         self.counters.private_copies += 1
         return fresh
 
@@ -216,7 +223,9 @@ class BlockAllocator:
 
     def shared_count(self, blocks: np.ndarray) -> int:
         """How many of ``blocks`` (valid ids) have more than one owner."""
-        return int(np.count_nonzero(self._owners[blocks] > 1)) if len(blocks) else 0
+        if not self._extra_owners or not len(blocks):
+            return 0
+        return int(np.count_nonzero(self._owners[blocks] > 1))
 
     def _check_range(self, ids: np.ndarray) -> None:
         bad = ids[(ids < 0) | (ids >= self.num_blocks)]
@@ -225,7 +234,8 @@ class BlockAllocator:
 
     def check_invariants(self) -> None:
         """Raise :class:`AllocatorError` unless the stack and the owner counts agree: the stack
-        holds distinct blocks, exactly the ones with no owner."""
+        holds distinct blocks, exactly the ones with no owner, and the running count of shared
+        ownerships matches the owner counts."""
         free = self._stack[: self._top]
         if np.unique(free).size != free.size:
             raise AllocatorError("free stack lists a block twice")
@@ -235,6 +245,10 @@ class BlockAllocator:
             raise AllocatorError("a block on the free stack still has owners")
         if np.any(self._owners[~marked] <= 0):
             raise AllocatorError("a block off the free stack has no owner")
+        extra = int(np.maximum(self._owners - 1, 0).sum())
+        if extra != self._extra_owners:
+            raise AllocatorError(f"{extra} owners past the first, the count says "
+                                 f"{self._extra_owners}")
 
     def internal_fragmentation(self, sequence_lengths: Iterable[int]) -> dict[str, float]:
         """Slack of sequences of the given lengths: the unused tail of each one's last block

@@ -579,67 +579,95 @@ class FixedAttention:
         def pad(n: int) -> int:
             return (n + 15) // 16 * 16
 
-        # Layout: cu_seqlens, context lengths, extras, the plan, then the block tables last, so
-        # that a step uploads [0, end of its plan) and only the table rows of its requests.
-        sizes = [pad(max_reqs + 1), pad(max_reqs), *[pad(c) for c in extra_capacities]]
+        # Layout: cu_seqlens, context lengths, extras, the block tables, then the plan last, so
+        # that a step uploads [0, end of its plan) in one copy.
+        sizes = [pad(max_reqs + 1), pad(max_reqs), *[pad(c) for c in extra_capacities],
+                 pad(max_reqs * max_blocks_per_seq)]
         offs, at = [], 0
         for n in sizes:
             offs.append(at)
             at += pad(n)
+        self._tables_off = offs[-1]
         self._plan_off = at
-        self._tables_off = pad(at + self.plan_words)
-        total = self._tables_off + max_reqs * max_blocks_per_seq
+        total = self._plan_off + self.plan_words
         self.buf = torch.zeros(total, dtype=torch.int32, device=self.device)
         self.host = torch.zeros(total, dtype=torch.int32, pin_memory=True)
         self._host_np = self.host.numpy()
+        self._host_np[self._tables_off : self._plan_off] = -1
         self.qsl = self.buf[offs[0] : offs[0] + max_reqs + 1]
         self.ctx = self.buf[offs[1] : offs[1] + max_reqs]
         tables = self._tables_off
         self.block_tables = self.buf[tables : tables + max_reqs * max_blocks_per_seq].view(
             max_reqs, max_blocks_per_seq)
-        self.extras = [self.buf[o : o + c] for o, c in zip(offs[2:], extra_capacities)]
-        self._offs, self._caps = offs, extra_capacities
-        self.plan = self.buf[self._plan_off : self._tables_off]
+        self.extras = [self.buf[o : o + c] for o, c in zip(offs[2:-1], extra_capacities)]
+        self._offs, self._caps = offs[:-1], extra_capacities
+        self.plan = self.buf[self._plan_off :]
         acc_off = (self.max_partials * 8 + 255) // 256 * 256
         ws = acc_off + (self.max_partials * head_dim * 4 + 255) // 256 * 256
         self.workspace = torch.empty(ws, dtype=torch.uint8, device=self.device)
         self.num_reqs = 0
+        self._table_rows = [0] * max_reqs  # entries written per table row (the rest hold -1)
+        # The planner reads cu_seqlens / context lengths from the staging buffer and writes the
+        # plan into it: no host array is built or copied per step.
+        base = self.host.data_ptr()
+        self._plan_fn = _lib.load().edgerag_attn_plan_ex
+        self._plan_args = (base + 4 * offs[0], base + 4 * offs[1])
+        self._plan_flags = _lib.PLAN_SPLIT_ROWS if split_rows else 0
+        self._plan_dst = base + 4 * self._plan_off
+        self._words, self._ws = ctypes.c_int64(0), ctypes.c_int64(0)
+        self._words_p, self._ws_p = ctypes.byref(self._words), ctypes.byref(self._ws)
+        self._arange = np.arange(max_reqs + 1, dtype=np.int32)
 
-    def update(self, query_start_loc: np.ndarray, context_lens: np.ndarray,
-               block_tables: np.ndarray, extras: list[np.ndarray]) -> bool:
-        """Plan the step and stage it; False (nothing written) if it exceeds a capacity or has
-        prefill tiles -- the caller then runs the eager path."""
-        R = int(np.asarray(context_lens).size)
-        bt = np.asarray(block_tables, np.int32)
-        if R > self.max_reqs or bt.shape[1] > self.max_blocks:
+    def update(self, query_start_loc: np.ndarray | None, context_lens,
+               block_tables, extras: list) -> bool:
+        """Plan the step and stage it; False (nothing uploaded) if it exceeds a capacity or has
+        prefill tiles -- the caller then runs the eager path. ``query_start_loc`` None: one
+        query token per request. ``block_tables``: a ``[R, width]`` int32 array, or one int32
+        row per request (each as long as that request's table)."""
+        R = len(context_lens)
+        if R > self.max_reqs:
             return False
-        if any(int(e.size) > c for e, c in zip(extras, self._caps)):
-            return False
-        plan, _ = make_plan_host(query_start_loc, context_lens, self.n_q_heads, self.n_kv_heads,
-                                 self.head_dim, self.block_size, self.max_blocks, self.dtype,
-                                 self.split_rows)
-        n_items, n_row, n_partials = int(plan[2]), int(plan[13]), int(plan[6])
-        row_waves, n_combine, slots = int(plan[19]), int(plan[16]), int(plan[21])
-        if (n_items != n_row or n_row > (self.wg_items if row_waves else self.max_items)
-                or n_combine > self.max_combine
-                or int(plan[14]) > self.max_row_vecs or n_partials > self.max_partials
-                or plan.size > self.plan_words):
-            return False
+        for e, c in zip(extras, self._caps):
+            if len(e) > c:
+                return False
         h = self._host_np
         o = self._offs
-        h[o[0] : o[0] + R + 1] = query_start_loc
+        h[o[0] : o[0] + R + 1] = self._arange[: R + 1] if query_start_loc is None \
+            else query_start_loc
         h[o[1] : o[1] + R] = context_lens
-        t0 = self._tables_off
-        tbl = h[t0 : t0 + R * self.max_blocks].reshape(R, self.max_blocks)
-        tbl[:] = -1
-        tbl[:, : bt.shape[1]] = bt
+        # Table rows: this step's entries, -1 past them where an earlier step wrote more.
+        t0, mb, rows = self._tables_off, self.max_blocks, self._table_rows
+        for r in range(R):
+            row = block_tables[r]
+            n = len(row)
+            if n > mb:
+                return False
+            at = t0 + r * mb
+            h[at : at + n] = row
+            if rows[r] > n:
+                h[at + n : at + rows[r]] = -1
+            rows[r] = n
         for e, off in zip(extras, o[2:]):
-            h[off : off + e.size] = e.reshape(-1)
-        h[self._plan_off : self._plan_off + plan.size] = plan
-        used = self._plan_off + plan.size
+            h[off : off + len(e)] = e
+        rc = self._plan_fn(*self._plan_args, R, self.n_q_heads, self.n_kv_heads, self.head_dim,
+                           self.block_size, self.max_blocks, dtype_code(self.dtype),
+                           self._plan_flags, self._plan_dst, self.plan_words, self._words_p,
+                           self._ws_p)
+        if rc == _lib.EDGERAG_EWORKSPACE:
+            return False  # the plan does not fit the staging capacity
+        if rc != _lib.EDGERAG_OK:
+            raise _lib.EdgeragError("edgerag_attn_plan", rc,
+                                    _lib.load().edgerag_last_error().decode(errors="replace"))
+        po = self._plan_off
+        hdr = h[po : po + 22].tolist()
+        n_items, n_row, n_partials = hdr[2], hdr[13], hdr[6]
+        row_waves, n_combine, slots = hdr[19], hdr[16], hdr[21]
+        if (n_items != n_row or n_row > (self.wg_items if row_waves else self.max_items)
+                or n_combine > self.max_combine or hdr[14] > self.max_row_vecs
+                or n_partials > self.max_partials):
+            return False
+        used = po + int(self._words.value)
         self.buf[:used].copy_(self.host[:used], non_blocking=True)
-        t1 = t0 + R * self.max_blocks
-        self.buf[t0:t1].copy_(self.host[t0:t1], non_blocking=True)
         self.num_reqs = R
         self.row_waves = row_waves
         self.combine = n_combine > 0

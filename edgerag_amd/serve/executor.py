@@ -193,7 +193,8 @@ class ModelExecutor:
 
     def _reserve(self, entries: list[_Entry]) -> list[np.ndarray]:
         """All of the step's reservations or none (see the module docstring)."""
-        adopted = [e for e in entries if self._reuse_prefix(e)]
+        adopted = ([e for e in entries if e.prefill and self._reuse_prefix(e)]
+                   if self.prefix_cache is not None else [])
 
         def undo_adoptions() -> None:
             for e in adopted:
@@ -253,6 +254,16 @@ class ModelExecutor:
         if not entries:
             return output
         slots = self._reserve(entries)
+        if (self.decode_graphs and not batch.prefill and len(entries) <= self.max_decode_batch
+                and self._stage_decode(entries, slots)):
+            # One token per request, each emitting: the staging buffer takes the step's lists
+            # as they are (no packed arrays are built on the host).
+            logits, choice = self._replay_decode(len(entries))
+            self.last_logits = logits
+            self.graph_steps += 1
+            for e, token in zip(entries, choice.cpu().tolist()):
+                output.tokens[e.request.request_id] = int(token)
+            return output
         qsl, ctx, pos, ids, rows, emitting = [0], [], [], [], [], []
         for e in entries:
             n, L = len(e.ids), e.cache.seq_len
@@ -267,27 +278,20 @@ class ModelExecutor:
         spec = self.spec
         extras = [np.concatenate(slots).astype(np.int32), np.concatenate(pos),
                   np.asarray(ids, np.int32), np.asarray(rows, np.int32)]
-        if (self.decode_graphs and not batch.prefill and len(entries) <= self.max_decode_batch
-                and self._stage_fixed(qsl, ctx, bt, extras)):
-            logits, choice = self._replay_decode(len(entries))
+        plan, (slot_d, pos_d, ids_d, rows_d) = kernels.plan_attention(
+            np.asarray(qsl, np.int32), np.asarray(ctx, np.int32), bt, spec.n_q_heads,
+            spec.n_kv_heads, spec.head_dim, self.allocator.block_size, self.dtype,
+            self.device, extras,
+        )
+        step = StepInputs(ids_d, pos_d, slot_d, rows_d, plan,
+                          self._prompt_rows(entries, qsl, ids_d))
+        tokens = []
+        if emitting:
+            logits, choice = self.decoder.greedy(step, self.key_pool, self.value_pool)
             self.last_logits = logits
             tokens = choice.cpu().tolist()
-            self.graph_steps += 1
         else:
-            plan, (slot_d, pos_d, ids_d, rows_d) = kernels.plan_attention(
-                np.asarray(qsl, np.int32), np.asarray(ctx, np.int32), bt, spec.n_q_heads,
-                spec.n_kv_heads, spec.head_dim, self.allocator.block_size, self.dtype,
-                self.device, extras,
-            )
-            step = StepInputs(ids_d, pos_d, slot_d, rows_d, plan,
-                              self._prompt_rows(entries, qsl, ids_d))
-            tokens = []
-            if emitting:
-                logits, choice = self.decoder.greedy(step, self.key_pool, self.value_pool)
-                self.last_logits = logits
-                tokens = choice.cpu().tolist()
-            else:
-                self.decoder.forward_hidden(step, self.key_pool, self.value_pool)
+            self.decoder.forward_hidden(step, self.key_pool, self.value_pool)
         for request, token in zip(emitting, tokens):
             output.tokens[request.request_id] = int(token)
         for e in entries:
@@ -300,16 +304,22 @@ class ModelExecutor:
 
     # --- decode iterations replayed from HIP graphs ------------------------------------------
 
-    def _stage_fixed(self, qsl, ctx, bt, extras) -> bool:
-        if self._fixed is None:
+    def _stage_decode(self, entries: list[_Entry], slots: list[np.ndarray]) -> bool:
+        """Stage a decode-only step (one token per request) for graph replay; False if it
+        does not fit the fixed capacities (the step then runs eagerly)."""
+        fx = self._fixed
+        if fx is None:
             spec = self.spec
             max_blocks = -(-spec.max_position_embeddings // self.allocator.block_size)
             cap = self.max_decode_batch
-            self._fixed = kernels.FixedAttention(
+            fx = self._fixed = kernels.FixedAttention(
                 self.device, spec.n_q_heads, spec.n_kv_heads, spec.head_dim,
                 self.allocator.block_size, self.dtype, cap, max_blocks, [cap, cap, cap, cap])
-        return self._fixed.update(np.asarray(qsl, np.int32), np.asarray(ctx, np.int32), bt,
-                                  extras)
+        ctx = [e.cache.seq_len for e in entries]
+        n = len(entries)
+        extras = [[int(s[0]) for s in slots], [L - 1 for L in ctx], [e.ids[0] for e in entries],
+                  fx._arange[:n]]
+        return fx.update(None, ctx, [e.cache.table.ids for e in entries], extras)
 
     def _replay_decode(self, n: int) -> tuple[torch.Tensor, torch.Tensor]:
         """Logits ``(n, vocab)`` of a staged decode-only step of ``n`` requests and their greedy

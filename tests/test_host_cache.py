@@ -107,6 +107,20 @@ def test_randomized_against_a_list_model() -> None:
             refs[b] += 1
             owned.append(b)
             a.incref([b])
+        elif op < 0.7 and owned:
+            b = rng.choice(owned)
+            if refs[b] == 1:
+                assert a.copy_on_write(b) == b
+            elif not stack:
+                with pytest.raises(OutOfBlocksError):
+                    a.copy_on_write(b)
+            else:  # a private copy takes over one ownership
+                fresh = stack.pop()
+                refs[b] -= 1
+                refs[fresh] = 1
+                owned.remove(b)
+                owned.append(fresh)
+                assert a.copy_on_write(b) == fresh
         elif owned:
             picks = rng.sample(owned, min(len(owned), rng.randint(1, 3)))
             back = 0
@@ -118,6 +132,8 @@ def test_randomized_against_a_list_model() -> None:
                     back += 1
             assert a.free(picks) == back
         assert a.num_free == len(stack)
+        ids = np.arange(24)
+        assert a.shared_count(ids) == sum(1 for r in refs if r > 1)
         a.check_invariants()
 
 
