@@ -46,6 +46,8 @@ class StepInputs:
     plan: kernels.AttentionPlan | kernels.FixedAttention  # eager plan, or graph-stable staging
     #: (T, hidden) input rows replacing the embedding lookup (prompt embeddings), or None.
     hidden: torch.Tensor | None = None
+    #: Every row of the batch emits, in order (``logit_rows`` is then 0..T-1): no row gather.
+    all_rows: bool = False
 
 
 def _config(bits: int, group_size: int | None, in_features: int) -> QuantConfig:
@@ -261,7 +263,7 @@ class EdgeRagDecoder(nn.Module):
                    else LinearBase.swiglu(layer.gate_up, x))
             down = layer.down_proj(act)
             x = kernels.rmsnorm(hidden, next_norm, eps, delta=down, h_out=hidden)
-        return x.index_select(0, step.logit_rows)
+        return x if step.all_rows else x.index_select(0, step.logit_rows)
 
     @torch.inference_mode()
     def logits(self, step: StepInputs, key_pool, value_pool) -> torch.Tensor:

@@ -391,7 +391,7 @@ __device__ __forceinline__ f16 rope_elem(float own, float partner, bool second, 
   return __float2half_rn(a + b);
 }
 
-template <int F, int NT, int MT, int KW, int U, bool EXACT, int EPI, bool NORM>
+template <int F, int NT, int MT, int KW, int U, bool EXACT, int EPI, bool NORM, bool X1>
 __global__ __launch_bounds__(KW * kWave)
 __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlinear_stream_kernel(
     const f16* __restrict__ x, int64_t xs, int32_t m, int32_t k,
@@ -416,6 +416,13 @@ __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlin
   constexpr int TOKW = NORM ? (MT * R + KW - 1) / KW : 1;  // tokens whose factor a wave sums
   __shared__ float red[KW * NT * MT * 4 * kWave];
   __shared__ float rnorm[NORM ? MT * R : 1];
+  // X1 (one token): a wave loads the token's activations of a batch once, each lane a distinct
+  // 16 bytes, and the lanes read their B operands from this LDS copy. Loading them straight
+  // from global memory costs a 64-lane load instruction per operand and step although the lane
+  // rows of one token all want the same bytes (the address unit's time goes by instructions,
+  // not by distinct bytes: measured 0.8 us of a 6.2 us 8192->2048 launch).
+  constexpr int XV = U * CB / 8;  // 16-byte chunks of one token's activations per batch
+  __shared__ uint4 xlds[X1 ? KW : 1][X1 ? XV : 1];
   const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63;
   const int li = lane & 15, lg = lane >> 4;
@@ -522,18 +529,43 @@ __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlin
     // [cb, c1) (already done, or another wave's) keep the accumulators unchanged.
     const int cs = min(cb, nc - U);
     uint4 w[U][NT], xa[U][MT], xc[U][MT];
+    constexpr int XL = (XV + kWave - 1) / kWave;  // X1: activation loads per lane and batch
+    uint4 xr[X1 ? XL : 1];
+    if constexpr (X1) {  // issued first: the LDS copy waits for these, not for the weights
+#pragma unroll
+      for (int i = 0; i < XL; ++i)
+        xr[i] = ldg16(x + int64_t(cs) * CB + int64_t(min(lane + kWave * i, XV - 1)) * 8);
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {  // in step order, so step u waits only for its own loads
 #pragma unroll
       for (int tn = 0; tn < NT; ++tn) w[u][tn] = ldg16(wp[tn] + int64_t(cs) * CB + u * CB);
+      if constexpr (!X1) {
 #pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        const f16* xb = xp[t] + int64_t(cs) * CB + u * CB;
-        xa[u][t] = ldg16(xb);
-        xc[u][t] = ldg16(xb + 8);
+        for (int t = 0; t < MT; ++t) {
+          const f16* xb = xp[t] + int64_t(cs) * CB + u * CB;
+          xa[u][t] = ldg16(xb);
+          xc[u][t] = ldg16(xb + 8);
+        }
       }
     }
     issue_fence();
+    if constexpr (X1) {
+      // The wave's own LDS rows: a wavefront barrier orders the writes before the reads (and
+      // the reads of the previous batch before these writes).
+#pragma unroll
+      for (int i = 0; i < XL; ++i)
+        if (lane + kWave * i < XV) xlds[wave][lane + kWave * i] = xr[i];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = (u * CB + f * 64 + 16 * lg) / 8;
+        xa[u][0] = xlds[wave][c];
+        xc[u][0] = xlds[wave][c + 1];
+      }
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const bool on = EXACT || (cs + u >= cb && cs + u < c1);
@@ -1373,12 +1405,20 @@ void launch_stream(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t
   // twins.
   const unsigned blocks = EPI == kEpiSwiglu ? unsigned((n / 2 + 16 / F - 1) / (16 / F))
                                             : unsigned((n + rows - 1) / rows);
-  if ((k / (64 * F)) % (KW * U) == 0)
-    hipLaunchKernelGGL((qlinear_stream_kernel<F, NT, MT, KW, U, true, EPI, NORM>), dim3(blocks),
-                       dim3(KW * kWave), 0, s, x, xs, m, k, packed, scales, bias, n, y, ys, ea);
-  else
-    hipLaunchKernelGGL((qlinear_stream_kernel<F, NT, MT, KW, U, false, EPI, NORM>), dim3(blocks),
-                       dim3(KW * kWave), 0, s, x, xs, m, k, packed, scales, bias, n, y, ys, ea);
+  // One token on two k-slices: its activations go through LDS (X1), the same values in the same
+  // operands. (With one k-slice, 16 lane rows share each operand load and a batch holds half
+  // the steps: measured 8.16 -> 8.41 us on 2048->16384, so those keep the direct loads.)
+  constexpr bool kX1 = MT == 1 && F == 2;
+#define EDGERAG_STREAM_X(EX, X1)                                                                 \
+  hipLaunchKernelGGL((qlinear_stream_kernel<F, NT, MT, KW, U, EX, EPI, NORM, X1>), dim3(blocks),  \
+                     dim3(KW * kWave), 0, s, x, xs, m, k, packed, scales, bias, n, y, ys, ea)
+  const bool exact = (k / (64 * F)) % (KW * U) == 0;
+  if (kX1 && m == 1) {
+    if (exact) EDGERAG_STREAM_X(true, kX1); else EDGERAG_STREAM_X(false, kX1);
+  } else {
+    if (exact) EDGERAG_STREAM_X(true, false); else EDGERAG_STREAM_X(false, false);
+  }
+#undef EDGERAG_STREAM_X
 }
 
 // Waves per workgroup and steps per batch of the streaming kernel for F k-slices, NT row tiles

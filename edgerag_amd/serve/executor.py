@@ -329,7 +329,7 @@ class ModelExecutor:
         entry = self._graphs.get(key)
         if entry is None:
             slots, pos, ids, rows = (e[:n] for e in fx.extras)
-            step = StepInputs(ids, pos, slots, rows, fx)
+            step = StepInputs(ids, pos, slots, rows, fx, all_rows=True)
             stream = torch.cuda.Stream(self.device)
             stream.wait_stream(torch.cuda.current_stream(self.device))
             graph = torch.cuda.CUDAGraph()
