@@ -30,6 +30,7 @@
 #include <mutex>
 #include <vector>
 
+#include "attention_merge.h"
 #include "attention_plan.h"
 
 namespace edgerag {
@@ -100,8 +101,6 @@ constexpr int kTargetTiles = EDGERAG_TARGET_TILES;  // prefill tile items a batc
 constexpr int kPlanCUs = 256;  // compute units the planner fills (MI355X)
 // K/V bytes decode rows must read for the planner to put them beside prefill tiles.
 constexpr int64_t kOverlapRowBytes = int64_t(256) << 20;
-
-__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Cross-lane moves inside a 16-lane row via DPP (plain VALU instructions, no LDS crossbar).
 template <int CTRL>
@@ -585,43 +584,9 @@ __global__ __launch_bounds__(kWave) void attn_rows_kernel(
 //   decode kernel, so every load address follows from the thread index alone and the merge takes
 //   one round trip.
 // Both fold the partials with merge_partials in slot order, so a row merges to the same values.
-constexpr int kCombineBatch = 16;
-
-// Folds one batch of partial records into the running (m, l, acc): weight exp2(m_k - max) for the
-// records that hold keys (take[k] and m_k > -inf); the others are skipped whatever their acc
-// holds (a slot never written this step may hold any bits).
-__device__ __forceinline__ void merge_partials(const float2 (&ml)[kCombineBatch],
-                                               const float4 (&v)[kCombineBatch],
-                                               const bool (&take)[kCombineBatch], float& m,
-                                               float& l, float4& acc) {
-  float mb = m;
-#pragma unroll
-  for (int k = 0; k < kCombineBatch; ++k)
-    if (take[k]) mb = fmaxf(mb, ml[k].x);
-  // No branch on mb == -inf (no record so far has seen a key): every weight below is then 0, and
-  // a branch here would make the compiler sink the acc loads behind the (m, l) wait.
-  const float r = m == -INFINITY ? 0.f : exp2_fast(m - mb);
-  l *= r;
-  acc.x *= r;
-  acc.y *= r;
-  acc.z *= r;
-  acc.w *= r;
-#pragma unroll
-  for (int k = 0; k < kCombineBatch; ++k) {
-    const bool on = take[k] && ml[k].x != -INFINITY;
-    const float w = on ? exp2_fast(ml[k].x - mb) : 0.f;
-    l = on ? fmaf(w, ml[k].y, l) : l;
-    acc.x = on ? fmaf(w, v[k].x, acc.x) : acc.x;
-    acc.y = on ? fmaf(w, v[k].y, acc.y) : acc.y;
-    acc.z = on ? fmaf(w, v[k].z, acc.z) : acc.z;
-    acc.w = on ? fmaf(w, v[k].w, acc.w) : acc.w;
-  }
-  m = mb;
-}
-
 template <typename T, bool VEC_OUT>
 __device__ __forceinline__ void store_merged(T* op, float4 acc, float l) {
-  const float inv = 1.f / fmaxf(l, 1.17549435e-38f);
+  const float inv = merge_inv(l);
   const T o0 = from_f32<T>(acc.x * inv), o1 = from_f32<T>(acc.y * inv),
           o2 = from_f32<T>(acc.z * inv), o3 = from_f32<T>(acc.w * inv);
   if constexpr (VEC_OUT) {
