@@ -718,6 +718,42 @@ def run_cfg5(device, n_requests: int = 64, cpu: bool = True):
     return res
 
 
+def run_decode_b1(device, prompt: int = 3000, steps: int = 300):
+    """The config-5 decoder decoding one request: a ``prompt``-token prompt prefilled in 512-token
+    chunks, then ``steps`` greedy decode iterations replayed from graphs (the offered-load case:
+    almost every iteration of the config-5 trace has one running request). Reports the
+    iteration time as ``replay`` measures it (execute + sync)."""
+    from edgerag_amd.cache.allocator import BlockAllocator
+    from edgerag_amd.core.model import EdgeRagDecoder
+    from edgerag_amd.core.spec import SMOLLM2_1_7B
+    from edgerag_amd.sched.request import Request
+    from edgerag_amd.sched.scheduler import Scheduler, SchedulerConfig
+    from edgerag_amd.serve.executor import ModelExecutor, apply_output
+
+    spec = SMOLLM2_1_7B
+    model = EdgeRagDecoder(spec, bits=8, group_size=None, device=device, dtype=torch.float16)
+    model.init_random(seed=5)
+    alloc = BlockAllocator(math.ceil((prompt + steps) / BS) + 64, BS)
+    executor = ModelExecutor(model, spec, alloc, device, torch.float16, chunk_size=512)
+    sched = Scheduler(alloc, SchedulerConfig(max_batch_size=1))
+    g = torch.Generator().manual_seed(1)
+    sched.add_request(Request("r0", torch.randint(1, spec.vocab_size - 1, (prompt,),
+                                                  generator=g).tolist(), max_new_tokens=steps))
+    times = []
+    while sched.has_work:
+        batch = sched.schedule()
+        t0 = time.perf_counter()
+        out = executor.execute(batch)
+        torch.cuda.synchronize()
+        if not batch.prefill:
+            times.append((time.perf_counter() - t0) * 1e3)
+        apply_output(sched, batch, out)
+    t = np.array(times[20:])
+    return {"prompt": prompt, "steps": len(times), "graph_steps": executor.graph_steps,
+            "iteration_ms_p50": round(float(np.median(t)), 3),
+            "iteration_ms_p99": round(float(np.percentile(t, 99)), 3)}
+
+
 # --- main ------------------------------------------------------------------------------------------
 
 
@@ -730,7 +766,8 @@ def main() -> None:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-cfg5", action="store_true", help="skip the end-to-end serving run")
     ap.add_argument("--cfg5-requests", type=int, default=64)
-    ap.add_argument("--only", choices=["cfg3", "cfg4", "cfg5", "lm_head", "single_seq"],
+    ap.add_argument("--only", choices=["cfg3", "cfg4", "cfg5", "lm_head", "single_seq",
+                                       "decode_b1"],
                     default=None,
                     help="run just one secondary config (for profiling); prints its record")
     args = ap.parse_args()
@@ -755,6 +792,9 @@ def main() -> None:
     if args.only == "cfg5":
         print(json.dumps({"cfg5": run_cfg5(device, args.cfg5_requests, not args.no_cpu)}),
               flush=True)
+        return
+    if args.only == "decode_b1":
+        print(json.dumps({"decode_b1": run_decode_b1(device)}), flush=True)
         return
 
     lens = cfg2_lens()
