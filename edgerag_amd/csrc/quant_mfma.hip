@@ -507,13 +507,20 @@ __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlin
     nw_pre = nw_u[e_row];
   }
   if constexpr (NORM) {
+    // Only the batch's tokens and the partials the producer wrote are loaded (wave-uniform
+    // branches): at one token one wave of the workgroup loads its 256 sums, where every wave
+    // loaded a clamped copy, 8 instructions per wave through the address unit (one token:
+    // 2048->16384 gate/up 9.71 -> 9.58 us, q/k/v + RoPE 5.84 -> 5.64 us).
 #pragma unroll
     for (int j = 0; j < TOKW; ++j) {
-      const int tok = min(wave + KW * j, m - 1);
+      const int tok = wave + KW * j;
 #pragma unroll
-      for (int q = 0; q < NPQ; ++q)
-        norm_pre[j * NPQ + q] =
-            ea.norm_part[int64_t(tok) * ea.norm_parts + min(lane + kWave * q, ea.norm_parts - 1)];
+      for (int q = 0; q < NPQ; ++q) {
+        norm_pre[j * NPQ + q] = 0.f;
+        if (tok < m && kWave * q < ea.norm_parts)
+          norm_pre[j * NPQ + q] = ea.norm_part[int64_t(tok) * ea.norm_parts +
+                                               min(lane + kWave * q, ea.norm_parts - 1)];
+      }
     }
   }
 
