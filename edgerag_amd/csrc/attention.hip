@@ -47,6 +47,12 @@ constexpr int32_t kPlanVersion = plan::kVersion;
 #ifndef EDGERAG_TARGET_ITEMS
 #define EDGERAG_TARGET_ITEMS 4096
 #endif
+#ifndef EDGERAG_COMBINE_THREADS
+// Threads of a merge workgroup. The merges of small batches are a few hundred threads (batch 1:
+// 32 heads x 16 channels): one-wave workgroups spread them over as many CUs, where 256-thread
+// workgroups would put all of them on two.
+#define EDGERAG_COMBINE_THREADS 64
+#endif
 #ifndef EDGERAG_DECODE_U
 #define EDGERAG_DECODE_U 2
 #endif
@@ -694,7 +700,8 @@ int launch_combine(hipStream_t s, const int32_t* plan_dev, int32_t n_rows, int32
     return fail(EDGERAG_EUNSUPPORTED, "attention combine: %d rows x %d heads too many", rows,
                 n_q_heads);
   if (threads == 0) return EDGERAG_OK;
-  const dim3 block(256), grid(unsigned((threads + 255) / 256));
+  constexpr int kThreads = EDGERAG_COMBINE_THREADS;
+  const dim3 block(kThreads), grid(unsigned((threads + kThreads - 1) / kThreads));
   const auto* acc4 = reinterpret_cast<const float4*>(pacc);
   T* o = static_cast<T*>(out);
   const bool vec = reinterpret_cast<uintptr_t>(out) % (4 * sizeof(T)) == 0 && o_st % 4 == 0 &&
