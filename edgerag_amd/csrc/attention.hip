@@ -47,6 +47,12 @@ constexpr int32_t kPlanVersion = plan::kVersion;
 #ifndef EDGERAG_TARGET_ITEMS
 #define EDGERAG_TARGET_ITEMS 4096
 #endif
+#ifndef EDGERAG_WG_QR_MAX
+#define EDGERAG_WG_QR_MAX 4  // query vectors per pass of a workgroup row (fp16 / fp32)
+#endif
+#ifndef EDGERAG_WG_QR_MAX_BF16
+#define EDGERAG_WG_QR_MAX_BF16 4  // ... bf16
+#endif
 #ifndef EDGERAG_COMBINE_THREADS
 // Threads of a merge workgroup. The merges of small batches are a few hundred threads (batch 1:
 // 32 heads x 16 channels): one-wave workgroups spread them over as many CUs, where 256-thread
@@ -812,6 +818,11 @@ template <typename T, int D>
 void dispatch_decode_qr(const Launch& a, int qr, int base, int count, int limit_word,
                         int waves) {
   constexpr int U = D >= 256 ? 2 : kDecodeU;
+  // Workgroup rows (up to 16 waves, 128 registers per lane) take at most 4 query vectors per
+  // pass: a pass of 8 spills 236-264 B per lane to scratch (fp16; ~430 B for bf16, whose query
+  // vectors are fp32). GQA groups of 8 then take two passes over the keys, the second mostly from
+  // L2: 32 q / 4 kv heads, 64 decodes of 4,000 tokens, 309.6 -> 116.5 us (fp16), 291 -> 138 (bf16).
+  if (waves > 0) qr = min(qr, __is_same(T, bf16) ? EDGERAG_WG_QR_MAX_BF16 : EDGERAG_WG_QR_MAX);
 #ifdef EDGERAG_WG_U
   if (waves > 0 && waves < kMaxRowWaves && qr == 1) {
     launch_decode<T, D, 1, (D >= 256 ? 2 : EDGERAG_WG_U)>(a, base, count, limit_word, waves);
