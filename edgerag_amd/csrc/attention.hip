@@ -796,7 +796,9 @@ void launch_decode_mode(const Launch& a, int base, int count, int limit_word, in
 
 template <typename T, int D, int QR, int U>
 void launch_decode(const Launch& a, int base, int count, int limit_word, int waves) {
-  if constexpr (D <= 128) {
+  // Workgroup rows never get more query vectors per pass than dispatch_decode_qr allows them.
+  constexpr int kWgQr = __is_same(T, bf16) ? EDGERAG_WG_QR_MAX_BF16 : EDGERAG_WG_QR_MAX;
+  if constexpr (D <= 128 && QR <= kWgQr) {
     if (waves > 0) {
       launch_decode_mode<T, D, QR, U, true>(a, base, count, limit_word, waves);
       return;

@@ -1819,9 +1819,14 @@ void launch_rope8(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t*
 #define EDGERAG_ROPE8(MT)                                                                        \
   launch_stream_w<2, 1, MT, kEpiRope, NORM>(stream_waves(2, 1, MT, k), x, xs, m, k, packed,      \
                                             scales, bias, n, nullptr, 0, ea, s)
-  if (m <= 8) EDGERAG_ROPE8(1);
-  else if (m <= 16) EDGERAG_ROPE8(2);
-  else EDGERAG_ROPE8(4);
+  if (m <= 8) {
+    EDGERAG_ROPE8(1);
+  } else if constexpr (NORM) {
+    EDGERAG_ROPE8(2);  // normed inputs come with at most 16 tokens (set_norm refuses more)
+  } else {
+    if (m <= 16) EDGERAG_ROPE8(2);
+    else EDGERAG_ROPE8(4);
+  }
 #undef EDGERAG_ROPE8
 }
 
