@@ -863,7 +863,74 @@ def main() -> None:
         line["lm_head"] = bench_lm_head(device)
         if not args.no_cfg5:
             line["cfg5"] = run_cfg5(device, args.cfg5_requests, not args.no_cpu)
-    print(json.dumps(line, separators=(",", ":")), flush=True)
+    print(json.dumps(compact_line(line), separators=(",", ":")), flush=True)
+
+
+def _sig3(v: float) -> float:
+    """v to 3 significant digits (timings in the compact record)."""
+    return float(f"{v:.3g}")
+
+
+def compact_line(line: dict) -> dict:
+    """The record printed by a full run, small enough (about 1.8 KB) that the last 2,000
+    characters of the run's output hold all of it: the contract fields, the cfg2 roofline and CPU
+    baseline, and every secondary table as column lists (``--only <config>`` prints a config's
+    full record)."""
+    out = {k: line[k] for k in ("metric", "value", "unit", "n_gpus", "steps", "warmup",
+                                "ms_per_step", "higher_is_better", "scaling", "vs_baseline",
+                                "dtype")}
+    out["data"] = "synthetic (seeded N(0,1), shuffled block tables)"
+    c = line["config"]
+    out["config"] = {"workload": "cfg2: append+paged attn, 32 decodes L~U[256,7472], 32/32h d64 "
+                     "bs16", "context_tokens": c["context_tokens"],
+                     "step_bytes": c["step_bytes"], "hbm_frac": c["hbm_frac"]}
+    r = line["roofline"]
+    out["roofline"] = {k: r[k] for k in ("bound", "achieved", "peak", "unit", "frac", "traffic")}
+    out["roofline"]["launch_us"] = r["launch_us"]
+    if "frac_of_gather_ceiling" in r:
+        out["roofline"]["gather_frac"] = r["frac_of_gather_ceiling"]
+    if "cpu_baseline" in line:
+        cb = line["cpu_baseline"]
+        out["cpu_baseline"] = {"value": cb["value"], "unit": cb["unit"], "cores": cb["cores"],
+                               "kind": cb["kind"], "sample": "cfg2 step, fp32 oracle, median"}
+    if "cfg3" in line:
+        c3 = line["cfg3"]
+        out["cfg3"] = {"ms_per_step": c3["ms_per_step"], "hbm_frac": c3["hbm_frac"]}
+        if "cpu_baseline" in c3:
+            out["cfg3"]["cpu_gbs"] = c3["cpu_baseline"]["value"]
+    if "single_seq" in line:
+        b1 = line["single_seq"]["b1"]
+        out["single_seq"] = {"L": [row[0] for row in b1], "us": [_sig3(row[1]) for row in b1],
+                             "frac": [round(row[3], 3) for row in b1]}
+    if "cfg4" in line:
+        # Per shape "KxN/bits": us at each M, then the read probe (M <= 64) and hipBLASLt fp16 at
+        # each M >= 512 as "ref".
+        ms = sorted({row[3] for row in line["cfg4"]["rows"]})
+        us, ref, cpu = {}, {}, {}
+        for k, n, bits, m, t, _frac, rf, cu in line["cfg4"]["rows"]:
+            key = f"{k}x{n}/{bits}"
+            us.setdefault(key, []).append(_sig3(t))
+            refs = ref.setdefault(key, [])
+            if m > 64 or not refs:  # the read probe is the same bytes at every M <= 64
+                refs.append(_sig3(rf))
+            if m == 1 and cu is not None:
+                cpu[key] = round(cu)
+        out["cfg4"] = {"m": ms, "us": us, "ref": ref}
+        if cpu:
+            out["cfg4"]["cpu_us_m1"] = cpu
+    if "lm_head" in line:
+        rows = line["lm_head"]["rows"]
+        out["lm_head"] = {"m": [row[0] for row in rows], "us": [row[1] for row in rows],
+                          "vendor_us": [row[2] for row in rows], "read_us": rows[0][3]}
+    if "cfg5" in line:
+        c5 = line["cfg5"]
+        def brief(s):
+            return {"tok_s": round(s["output_tok_per_s"], 1), "p50_ms": s["iteration_ms_p50"],
+                    "p99_ms": s["iteration_ms_p99"], "ttft_p50_s": s["ttft_s_p50"]}
+        out["cfg5"] = {"offered": brief(c5["offered_load"]), "saturated": brief(c5["saturated"])}
+        if "cpu_baseline" in c5:
+            out["cfg5"]["cpu_tok_s"] = c5["cpu_baseline"]["value"]
+    return out
 
 
 if __name__ == "__main__":
