@@ -637,3 +637,30 @@ def test_large_scores_and_attention_sinks_fp16(device, c, past, q_lens_kind) -> 
         vh = op.gather_pool(vp.double(), tables[0], L)[h]
         ref = oa.attention_f64(q[:, h], kh, vh, past, d**-0.5)
         torch.testing.assert_close(got[:, h].double(), ref, **FP16_TOL)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("n_req", [2, 64])
+def test_gqa8_workgroup_rows_take_query_vectors_in_passes(device, dtype, n_req) -> None:
+    """Groups of 8 query heads per kv head (32 / 4) in workgroup rows: 64 decodes of at most
+    4,096 tokens make one 16-wave workgroup per (request, kv head), 2 decodes are cut into parts
+    of 8-wave workgroups, and both take their 8 query vectors in passes of 4. Against the oracle,
+    slack poisoned."""
+    n_q, n_kv, d = 32, 4, 64
+    g = seeded(300 + n_req)
+    lens = [int(x) for x in torch.randint(300, 4097, (n_req,), generator=g)]
+    kp, vp, tables, qsl, q, bt = _ragged_case(lens, [1] * n_req, n_q, n_kv, d, dtype,
+                                              90 + n_req)
+    plan_host, _ = kernels.make_plan_host(qsl, np.asarray(lens, np.int32), n_q, n_kv, d,
+                                          BLOCK_SIZE, bt.shape[1], dtype)
+    assert int(plan_host[19]) == (16 if n_req == 64 else 8)  # workgroup rows / context parts
+    assert int(plan_host[14]) == 8  # query vectors per row item
+    got = _run_ragged(device, kp, vp, qsl, lens, bt, q, d**-0.5)
+    expected = oa.ragged_reference(q, kp, vp, qsl.tolist(), lens, tables, d**-0.5)
+    if dtype == torch.float32:
+        tol = FP32_TOL
+    elif dtype == torch.float16:
+        tol = FP16_TOL
+    else:  # bf16 keeps 8 bits of mantissa where fp16 keeps 11
+        tol = {k_: v_ * 8 for k_, v_ in FP16_TOL.items()}
+    torch.testing.assert_close(got.float(), expected, **tol)
