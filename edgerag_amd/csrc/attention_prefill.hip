@@ -57,7 +57,16 @@ constexpr int kWaves = kMfmaTileRows / 32;
 constexpr int kThreads = kWaves * kWave;
 constexpr int kKChunks = kKeys * kD * 2 / 16;  // 16-byte chunks of a K tile (512)
 constexpr int kKPerThread = kKChunks / kThreads;
-constexpr int kVPairs = (kKeys / 4) * (kD / 8);  // (key quad, dim chunk) pairs of a V tile (128)
+#ifndef EDGERAG_TILE_VKEYS
+// Consecutive keys of one dim chunk a thread stages into V^T (2 or 4). With 2, the 256 (key pair,
+// dim chunk) units of a V tile give every thread of a 4-wave workgroup one, so no wave carries
+// the whole transpose (with 4 half the threads staged V and the other half waited at the barrier).
+#define EDGERAG_TILE_VKEYS 2
+#endif
+constexpr int kVKeys = EDGERAG_TILE_VKEYS;
+static_assert(kVKeys == 2 || kVKeys == 4, "V^T staging units of 2 or 4 keys");
+constexpr int kVGroups = kKeys / kVKeys;             // key groups of a V tile
+constexpr int kVPairs = kVGroups * (kD / 8);         // (key group, dim chunk) units of a V tile
 constexpr int kVPerThread = (kVPairs + kThreads - 1) / kThreads;
 static_assert(kKChunks % kThreads == 0, "K staging split");
 constexpr unsigned kStaticLds = 2 * kKeys * kRow * 2 + 2 * kD * kRow * 2 + kMaxTileBlocks * 4;
@@ -108,7 +117,7 @@ __device__ __forceinline__ int vt_slot(int key) {
 
 struct StageRegs {
   h8 k[kKPerThread];
-  h8 v[4 * kVPerThread];
+  h8 v[kVKeys * kVPerThread];
 };
 
 struct Geometry {
@@ -137,7 +146,8 @@ struct StageIds {
 };
 
 // K: chunk c = tid + kThreads * j is key c / 8, dim chunk c % 8 (8 lanes fill one key row).
-// V: pair p = tid + kThreads * j is key quad p % 16, dim chunk p / 16 (16 lanes fill one V^T row).
+// V: unit p = tid + kThreads * j is key group p % kVGroups (kVKeys keys), dim chunk p / kVGroups
+// (kVGroups lanes fill one V^T row).
 __device__ __forceinline__ void stage_ids(StageIds& ids, int tid, int k0, const Geometry& geo,
                                           const int* __restrict__ sblk) {
 #pragma unroll
@@ -145,7 +155,9 @@ __device__ __forceinline__ void stage_ids(StageIds& ids, int tid, int k0, const 
 #pragma unroll
   for (int j = 0; j < kVPerThread; ++j) {
     const int p = tid + kThreads * j;
-    ids.v[j] = (kVPairs % kThreads != 0 && p >= kVPairs) ? -1 : block_of(geo, sblk, k0 + 4 * (p % 16));
+    ids.v[j] = (kVPairs % kThreads != 0 && p >= kVPairs)
+                   ? -1
+                   : block_of(geo, sblk, k0 + kVKeys * (p % kVGroups));
   }
 }
 
@@ -161,14 +173,14 @@ __device__ __forceinline__ void stage_load(StageRegs& st, const StageIds& ids, i
   for (int j = 0; j < kVPerThread; ++j) {
     const int p = tid + kThreads * j;
     if (kVPairs % kThreads != 0 && p >= kVPairs) break;
-    const int a = p % 16, b = p / 16;
-    // The 4 keys of a quad share one block (blocks hold a multiple of 4 keys): one lookup, then
+    const int a = p % kVGroups, b = p / kVGroups;
+    // The keys of a group share one block (blocks hold a multiple of 4 keys): one lookup, then
     // consecutive rows; keys past the split still get the out-of-range offset.
-    const int pos = k0 + 4 * a;
+    const int pos = k0 + kVKeys * a;
     const uint32_t base = pool_offset(geo, ids.v[j], pos, b);
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
-      st.v[4 * j + kk] = buffer_load16(
+    for (int kk = 0; kk < kVKeys; ++kk)
+      st.v[kVKeys * j + kk] = buffer_load16(
           vrs, (base != kOutOfRange && pos + kk < geo.ke) ? base + uint32_t(kk * kD * 2)
                                                           : kOutOfRange);
   }
@@ -185,14 +197,17 @@ __device__ __forceinline__ void stage_store(const StageRegs& st, int tid,
   for (int j = 0; j < kVPerThread; ++j) {
     const int p = tid + kThreads * j;
     if (kVPairs % kThreads != 0 && p >= kVPairs) break;
-    const int a = p % 16, b = p / 16;
-    const int slot = vt_slot(4 * a);  // 4-aligned: the 4 keys stay contiguous
+    const int a = p % kVGroups, b = p / kVGroups;
+    const int slot = vt_slot(kVKeys * a);  // kVKeys-aligned: the group's keys stay contiguous
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
-      const int row = 8 * b + d;
-      const h4 col4 = {st.v[4 * j][d], st.v[4 * j + 1][d], st.v[4 * j + 2][d],
-                       st.v[4 * j + 3][d]};
-      *reinterpret_cast<h4*>(svt + lds_chunk(row, slot >> 3) + (slot & 7)) = col4;
+      _Float16* dst = svt + lds_chunk(8 * b + d, slot >> 3) + (slot & 7);
+      if constexpr (kVKeys == 4) {
+        *reinterpret_cast<h4*>(dst) = h4{st.v[4 * j][d], st.v[4 * j + 1][d], st.v[4 * j + 2][d],
+                                         st.v[4 * j + 3][d]};
+      } else {
+        *reinterpret_cast<h2*>(dst) = h2{st.v[2 * j][d], st.v[2 * j + 1][d]};
+      }
     }
   }
 }
