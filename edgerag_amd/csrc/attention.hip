@@ -74,6 +74,21 @@ constexpr int32_t kPlanVersion = plan::kVersion;
 #ifndef EDGERAG_ROW_WG_PART_TILES
 #define EDGERAG_ROW_WG_PART_TILES 512  // the same, in a batch with prefill tiles beside the rows
 #endif
+#ifndef EDGERAG_ROW_WG_MAX_ITEMS
+// On one stream, a decode batch takes (request, kv head) workgroup rows when they make one round
+// over the CUs, or up to EDGERAG_ROW_WG_MAX_ITEMS of them when no context passes
+// EDGERAG_ROW_WG_SHORT tokens; otherwise KV splits. A 16-wave row workgroup holds a CU alone, so
+// past one round the splits' one-wave workgroups, more of them in flight per CU, win despite
+// their merge launch, except on short contexts (32/32 heads, fp16, contexts of 1,000 / 2,000 /
+// 4,000 tokens, rows against splits: 8 requests 15.7 / 26.3 / 46.2 against 29.8 / 38.8 / 48.3
+// us; 12: 27.8 / 43.7 / 77.2 against 34.7 / 39.3 / 65.3; 16: 27.9 / 48.3 / 86.0 against
+// 34.6 / 46.4 / 85.5; 24: 41.4 / 71.1 / 127.2 against 38.7 / 65.8 / 124.0; 64: 107.6 / 182.4 /
+// 334.9 against 83.0 / 158.8 / 315.5).
+#define EDGERAG_ROW_WG_MAX_ITEMS 512
+#endif
+#ifndef EDGERAG_ROW_WG_SHORT
+#define EDGERAG_ROW_WG_SHORT 1536
+#endif
 #ifndef EDGERAG_ROW_WG_WAVES
 #define EDGERAG_ROW_WG_WAVES 16  // waves of a workgroup over a whole context
 #endif
@@ -1025,7 +1040,9 @@ extern "C" int edgerag_attn_plan_ex(const int32_t* query_start_loc, const int32_
       wg_part = std::max(wg_part, slot_part);
       slots = s;
     }
-  } else if (wg_capable && max_row_len <= part_cap) {
+  } else if (wg_capable && max_row_len <= part_cap &&
+             (overlap || row_items <= kPlanCUs ||
+              (row_items <= EDGERAG_ROW_WG_MAX_ITEMS && max_row_len <= EDGERAG_ROW_WG_SHORT))) {
     wg_rows = true;
     row_waves = kRowWgWaves;
   } else if (wg_capable && EDGERAG_ROW_WG_LONG) {
