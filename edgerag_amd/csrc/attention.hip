@@ -75,15 +75,16 @@ constexpr int32_t kPlanVersion = plan::kVersion;
 #define EDGERAG_ROW_WG_PART_TILES 512  // the same, in a batch with prefill tiles beside the rows
 #endif
 #ifndef EDGERAG_ROW_WG_MAX_ITEMS
-// On one stream, a decode batch takes (request, kv head) workgroup rows when they make one round
-// over the CUs, or up to EDGERAG_ROW_WG_MAX_ITEMS of them when no context passes
-// EDGERAG_ROW_WG_SHORT tokens; otherwise KV splits. A 16-wave row workgroup holds a CU alone, so
-// past one round the splits' one-wave workgroups, more of them in flight per CU, win despite
-// their merge launch, except on short contexts (32/32 heads, fp16, contexts of 1,000 / 2,000 /
+// A decode batch takes (request, kv head) workgroup rows when they make one round over the CUs,
+// or up to EDGERAG_ROW_WG_MAX_ITEMS of them when no context passes EDGERAG_ROW_WG_SHORT tokens;
+// otherwise KV splits. A 16-wave row workgroup holds a CU alone, so past one round the splits'
+// one-wave workgroups, more of them in flight per CU, win despite their merge launch, except on
+// short contexts, on one stream (32/32 heads, fp16, contexts of 1,000 / 2,000 /
 // 4,000 tokens, rows against splits: 8 requests 15.7 / 26.3 / 46.2 against 29.8 / 38.8 / 48.3
 // us; 12: 27.8 / 43.7 / 77.2 against 34.7 / 39.3 / 65.3; 16: 27.9 / 48.3 / 86.0 against
 // 34.6 / 46.4 / 85.5; 24: 41.4 / 71.1 / 127.2 against 38.7 / 65.8 / 124.0; 64: 107.6 / 182.4 /
-// 334.9 against 83.0 / 158.8 / 315.5).
+// 334.9 against 83.0 / 158.8 / 315.5) and beside prefill tiles on a second stream (config 3:
+// 768 row workgroups, step 181-189 against 176-177 us with KV splits).
 #define EDGERAG_ROW_WG_MAX_ITEMS 512
 #endif
 #ifndef EDGERAG_ROW_WG_SHORT
@@ -973,10 +974,9 @@ extern "C" int edgerag_attn_plan_ex(const int32_t* query_start_loc, const int32_
   // long requests -5%), so those batches (or any, when asked) keep one workgroup per KV split,
   // merged by the combine launch through fp32 partials. Beside prefill tiles, when the rows'
   // workgroups cover every CU, the chip does not idle (the tiles take the slack), so parts of up
-  // to EDGERAG_ROW_WG_PART_TILES tokens stay workgroup-split and the step saves the merge launch
-  // (three 512-token slices beside 24 decodes of up to 7,472 tokens, 768 row workgroups: 0.213
-  // -> 0.207 ms per step). Fewer row workgroups than CUs (a 512-token chunk beside 7 decodes,
-  // 224 of them) left a few CUs with long streams: -2.5% output tokens/s end to end.
+  // to EDGERAG_ROW_WG_PART_TILES tokens stay workgroup-split (as long as the rows are few enough
+  // for EDGERAG_ROW_WG_MAX_ITEMS). Fewer row workgroups than CUs (a 512-token chunk beside 7
+  // decodes, 224 of them) left a few CUs with long streams: -2.5% output tokens/s end to end.
   static_assert(kRowWgWaves >= 1 && kRowWgWaves <= kMaxRowWaves, "row workgroup size");
   static_assert(kRowPartWaves >= 1 && kRowPartWaves <= kMaxRowWaves, "part workgroup size");
   int64_t row_items = 0, max_row_len = 0;
@@ -1041,7 +1041,7 @@ extern "C" int edgerag_attn_plan_ex(const int32_t* query_start_loc, const int32_
       slots = s;
     }
   } else if (wg_capable && max_row_len <= part_cap &&
-             (overlap || row_items <= kPlanCUs ||
+             (row_items <= kPlanCUs ||
               (row_items <= EDGERAG_ROW_WG_MAX_ITEMS && max_row_len <= EDGERAG_ROW_WG_SHORT))) {
     wg_rows = true;
     row_waves = kRowWgWaves;

@@ -390,11 +390,10 @@ def test_plan_size_query_without_buffer() -> None:
         ([4097] + [300] * 7, 64, 16, False, 0, 16),
         ([8193] + [300] * 7, 64, 16, False, 0, 0),  # past 16 waves x 512 tokens: KV splits
         # More than one round of row workgroups: 12 requests of short contexts stay rows, longer
-        # ones and more than 512 workgroups (24 requests) take KV splits on one stream, and
-        # workgroup rows beside prefill tiles on a second.
+        # ones and more than 512 workgroups (24 requests) take KV splits, beside prefill tiles too.
         ([1000] * 12, 64, 16, False, 16, 16),
-        ([2000] * 12, 64, 16, False, 0, 16),
-        ([1000] * 24, 64, 16, False, 0, 16),
+        ([2000] * 12, 64, 16, False, 0, 0),
+        ([1000] * 24, 64, 16, False, 0, 0),
         ([4096, 1, 300], 64, 16, True, 0, 0),  # asked for KV splits
         ([2000], 256, 16, False, 0, 0),  # head_dim past the workgroup kernel's 128
         ([2000], 128, 8, False, 8, 8),
@@ -405,9 +404,8 @@ def test_plan_row_mode_selection(ctx, d, bs, split_rows, row_waves, row_waves_ti
     """Decode rows become workgroups whose waves split the keys and merge in LDS when the fast
     decode kernel takes the shape: one of 16 waves per (request, kv head) when they cover the
     256 CUs in one round (or in two, on contexts of at most 1,536 tokens) and every decode context
-    fits 16 waves of at most 256 tokens (any number, and 512 tokens, when the plan puts prefill
-    tiles on a second stream beside them), one of 8 waves per part of a context when they would
-    not cover the CUs."""
+    fits 16 waves of at most 256 tokens (512 when the plan puts prefill tiles on a second stream
+    beside them), one of 8 waves per part of a context when they would not cover the CUs."""
     n, h = len(ctx), 32
     plan, ws = kernels.make_plan_host(np.arange(n + 1, dtype=np.int32), np.array(ctx, np.int32),
                                       h, h, d, bs, -(-max(ctx) // bs), torch.float16, split_rows)
