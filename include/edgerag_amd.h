@@ -133,9 +133,10 @@ int edgerag_attn_plan(const int32_t* query_start_loc, const int32_t* context_len
  * edgerag_attn_plan with planning flags. Decode rows (requests with c * n_q_heads / n_kv_heads
  * <= 8 query vectors) are by default planned as one workgroup per (request, kv head) whose waves
  * split the context and merge in LDS (no split partials, no merge launch), whenever the fast
- * decode kernel takes the shape and every such context fits 16 waves of 64 blocks; otherwise,
- * or with EDGERAG_PLAN_SPLIT_ROWS, as one workgroup per KV split merged through fp32 partials
- * in the workspace. Results agree to fp32 rounding either way. A batch with fewer such
+ * decode kernel takes the shape, every such context fits 16 waves of 64 blocks and those
+ * workgroups make at most one round over the CUs (two when no context passes 1,536 tokens);
+ * otherwise, or with EDGERAG_PLAN_SPLIT_ROWS, as one workgroup per KV split merged through fp32
+ * partials in the workspace. Results agree to fp32 rounding either way. A batch with fewer such
  * workgroups than CUs (few decodes) instead cuts every row context into parts of 8 waves, one
  * workgroup each, whose partials sit in S fixed slots per (token, query head): plan word 21
  * holds S (0 when the rows are not slotted), and every row token then has a merge row.
