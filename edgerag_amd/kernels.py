@@ -540,7 +540,8 @@ class FixedAttention:
     plan. :meth:`launch` calls ``edgerag_paged_attention_fixed``, whose grid depends only on the
     capacities and on :attr:`mode`, the launch mode of the staged plan: row waves 0 for KV splits
     merged by a combine launch, > 0 for workgroup-split rows (the planner takes these when every
-    context is short, or cuts the contexts into parts when the batch has few requests); whether
+    context is short and the rows are few, or cuts the contexts into parts when the batch has few
+    requests); whether
     a merge launch follows; and the plan's partial slots (parts in fixed slots take the merge
     launch that reads no plan entry first). A captured graph stays valid for every plan
     :meth:`update` accepts in the mode it was captured in, so callers key their graphs by
