@@ -11,6 +11,11 @@ Flags that matter:
   ROCm 7.2.
 * ``-Xclang -target-feature -Xclang -packed-fp32-ops``: keep the compiler from emitting packed
   fp32 VALU instructions (v_pk_fma_f32 and friends), which are not used in this library.
+* ``-mllvm -amdgpu-kernarg-preload-count=16``: the leading kernel arguments (13-14 dwords, as
+  many as the free user SGPRs hold) arrive in SGPRs at wave launch instead of through a scalar
+  load from the kernel-argument buffer, a memory round trip before a kernel's first load can be
+  addressed. The kernels put the arguments of their first loads first. The few-microsecond
+  launches gain most (INT8 GEMV at one token, 2048 x 2048: 3.19 -> 2.85 us).
 """
 
 from __future__ import annotations
@@ -42,6 +47,8 @@ COMMON_FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    "-mllvm",
+    "-amdgpu-kernarg-preload-count=16",
     "-Wall",
     "-Wno-unused-function",
     "-Wno-unused-command-line-argument",

@@ -56,7 +56,8 @@ constexpr int32_t kPlanVersion = plan::kVersion;
 #ifndef EDGERAG_COMBINE_THREADS
 // Threads of a merge workgroup. The merges of small batches are a few hundred threads (batch 1:
 // 32 heads x 16 channels): one-wave workgroups spread them over as many CUs, where 256-thread
-// workgroups would put all of them on two.
+// workgroups would put all of them on two. The kernels take it as a constant (not blockDim), so
+// no thread index waits for a load of the workgroup size from the hidden kernel arguments.
 #define EDGERAG_COMBINE_THREADS 64
 #endif
 #ifndef EDGERAG_DECODE_U
@@ -210,14 +211,17 @@ struct QReg {
 // block-aligned parts of the item's keys, and the waves' (m, l, acc) merge in LDS before wave 0
 // writes the output, or, when the item is one of several parts of a context, the part's fp32
 // partial for the merge launch. Otherwise one wave per item (a KV split).
+// The arguments of the first loads (plan, request arrays, block table) lead the list: the library
+// is built to preload the leading kernel arguments into SGPRs at wave launch, so the work item's
+// load does not wait for a kernel-argument fetch from memory.
 template <typename T, int D, int QR, int U, bool APPEND, bool WG>
 __global__ __launch_bounds__(WG ? kMaxRowWaves * kWave : kWave) void attn_decode_kernel(
-    const T* __restrict__ q, int64_t q_st, int64_t q_sh, const T* __restrict__ kpool,
-    const T* __restrict__ vpool, const int32_t* __restrict__ block_tables, int64_t bt_stride,
+    const int32_t* __restrict__ plan, int32_t item_base, int32_t limit_word,
     const int32_t* __restrict__ qsl, const int32_t* __restrict__ ctx,
-    const int32_t* __restrict__ plan, int32_t item_base, int32_t limit_word, int32_t n_q_heads,
-    int32_t n_kv_heads, int32_t num_blocks, int32_t block_size, float scale_log2,
-    T* __restrict__ out, int64_t o_st, int64_t o_sh, float2* __restrict__ part_ml,
+    const int32_t* __restrict__ block_tables, int64_t bt_stride, int32_t num_blocks,
+    int32_t block_size, const T* __restrict__ q, int64_t q_st, int64_t q_sh,
+    const T* __restrict__ kpool, const T* __restrict__ vpool, int32_t n_q_heads,
+    int32_t n_kv_heads, float scale_log2, T* __restrict__ out, int64_t o_st, int64_t o_sh, float2* __restrict__ part_ml,
     float* __restrict__ part_acc, const T* __restrict__ nk, const T* __restrict__ nv,
     int64_t n_st, int64_t n_sh, const int32_t* __restrict__ slots, T* __restrict__ kdst,
     T* __restrict__ vdst) {
@@ -478,12 +482,12 @@ __global__ __launch_bounds__(WG ? kMaxRowWaves * kWave : kWave) void attn_decode
 // Any block size and split length; per-lane block lookups; QR query vectors per pass.
 template <typename T, int D, int QR>
 __global__ __launch_bounds__(kWave) void attn_rows_kernel(
-    const T* __restrict__ q, int64_t q_st, int64_t q_sh, const T* __restrict__ kpool,
-    const T* __restrict__ vpool, const int32_t* __restrict__ block_tables, int64_t bt_stride,
+    const int32_t* __restrict__ plan, int32_t item_base, int32_t limit_word,
     const int32_t* __restrict__ qsl, const int32_t* __restrict__ ctx,
-    const int32_t* __restrict__ plan, int32_t item_base, int32_t limit_word, int32_t n_q_heads,
-    int32_t n_kv_heads, int32_t num_blocks, int32_t block_size, float scale_log2,
-    T* __restrict__ out, int64_t o_st, int64_t o_sh, float2* __restrict__ part_ml,
+    const int32_t* __restrict__ block_tables, int64_t bt_stride, int32_t num_blocks,
+    int32_t block_size, const T* __restrict__ q, int64_t q_st, int64_t q_sh,
+    const T* __restrict__ kpool, const T* __restrict__ vpool, int32_t n_q_heads,
+    int32_t n_kv_heads, float scale_log2, T* __restrict__ out, int64_t o_st, int64_t o_sh, float2* __restrict__ part_ml,
     float* __restrict__ part_acc) {
   using C = RowCfg<T, D>;
   constexpr int VEC = C::VEC, LPT = C::LPT, TPW = C::TPW, LOG_LPT = C::LOG_LPT;
@@ -631,11 +635,11 @@ __device__ __forceinline__ void store_merged(T* op, float4 acc, float l) {
 }
 
 template <typename T, bool VEC_OUT>
-__global__ __launch_bounds__(256) void attn_combine_kernel(
+__global__ __launch_bounds__(EDGERAG_COMBINE_THREADS) void attn_combine_kernel(
     const int32_t* __restrict__ plan, int32_t n_rows, int32_t combine_off, int32_t n_q_heads,
     int32_t ch_log2, const float2* __restrict__ part_ml, const float4* __restrict__ part_acc,
     T* __restrict__ out, int64_t o_st, int64_t o_sh) {
-  const int gid = int(blockIdx.x) * int(blockDim.x) + int(threadIdx.x);
+  const int gid = int(blockIdx.x) * EDGERAG_COMBINE_THREADS + int(threadIdx.x);
   const int ch = gid & ((1 << ch_log2) - 1);
   const int pair = gid >> ch_log2;
   const int row = pair / n_q_heads;
@@ -674,11 +678,11 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(
 // plan whose H_SLOTS differs from `slots` gets NaN rows: a launch shape that does not match the
 // staged plan fails loudly.
 template <typename T, bool VEC_OUT>
-__global__ __launch_bounds__(256) void attn_combine_slots_kernel(
+__global__ __launch_bounds__(EDGERAG_COMBINE_THREADS) void attn_combine_slots_kernel(
     const int32_t* __restrict__ plan, int32_t n_rows, int32_t slots, int32_t n_q_heads,
     int32_t ch_log2, const float2* __restrict__ part_ml, const float4* __restrict__ part_acc,
     T* __restrict__ out, int64_t o_st, int64_t o_sh) {
-  const int gid = int(blockIdx.x) * int(blockDim.x) + int(threadIdx.x);
+  const int gid = int(blockIdx.x) * EDGERAG_COMBINE_THREADS + int(threadIdx.x);
   const int ch = gid & ((1 << ch_log2) - 1);
   const int pair = gid >> ch_log2;
   const int t = pair / n_q_heads;
@@ -794,19 +798,19 @@ void launch_decode_mode(const Launch& a, int base, int count, int limit_word, in
   const dim3 grid(count), block(WG ? waves * kWave : kWave);
   if (a.nk != nullptr)
     hipLaunchKernelGGL((attn_decode_kernel<T, D, QR, U, true, WG>), grid, block, 0, a.s,
+                       a.plan, base, limit_word, a.qsl, a.ctx, a.bt, a.bt_stride, a.nb, a.bs,
                        static_cast<const T*>(a.q), a.q_st, a.q_sh, static_cast<const T*>(a.kp),
-                       static_cast<const T*>(a.vp), a.bt, a.bt_stride, a.qsl, a.ctx, a.plan, base,
-                       limit_word, a.hq, a.hkv, a.nb, a.bs, a.scale_log2,
+                       static_cast<const T*>(a.vp), a.hq, a.hkv, a.scale_log2,
                        static_cast<T*>(a.out), a.o_st, a.o_sh, a.ml, a.pacc,
                        static_cast<const T*>(a.nk), static_cast<const T*>(a.nv), a.n_st, a.n_sh,
                        a.slots, static_cast<T*>(const_cast<void*>(a.kp)),
                        static_cast<T*>(const_cast<void*>(a.vp)));
   else
     hipLaunchKernelGGL((attn_decode_kernel<T, D, QR, U, false, WG>), grid, block, 0, a.s,
-                       static_cast<const T*>(a.q), a.q_st, a.q_sh,
-                       static_cast<const T*>(a.kp), static_cast<const T*>(a.vp), a.bt,
-                       a.bt_stride, a.qsl, a.ctx, a.plan, base, limit_word, a.hq, a.hkv, a.nb,
-                       a.bs, a.scale_log2, static_cast<T*>(a.out), a.o_st, a.o_sh, a.ml, a.pacc,
+                       a.plan, base, limit_word, a.qsl, a.ctx, a.bt, a.bt_stride, a.nb, a.bs,
+                       static_cast<const T*>(a.q), a.q_st, a.q_sh, static_cast<const T*>(a.kp),
+                       static_cast<const T*>(a.vp), a.hq, a.hkv, a.scale_log2,
+                       static_cast<T*>(a.out), a.o_st, a.o_sh, a.ml, a.pacc,
                        nullptr, nullptr, 0, 0, nullptr, nullptr, nullptr);
 }
 
@@ -825,11 +829,11 @@ void launch_decode(const Launch& a, int base, int count, int limit_word, int wav
 
 template <typename T, int D, int QR>
 void launch_rows(const Launch& a, int base, int count, int limit_word) {
-  hipLaunchKernelGGL((attn_rows_kernel<T, D, QR>), dim3(count), dim3(kWave), 0, a.s,
+  hipLaunchKernelGGL((attn_rows_kernel<T, D, QR>), dim3(count), dim3(kWave), 0, a.s, a.plan,
+                     base, limit_word, a.qsl, a.ctx, a.bt, a.bt_stride, a.nb, a.bs,
                      static_cast<const T*>(a.q), a.q_st, a.q_sh, static_cast<const T*>(a.kp),
-                     static_cast<const T*>(a.vp), a.bt, a.bt_stride, a.qsl, a.ctx, a.plan, base,
-                     limit_word, a.hq, a.hkv, a.nb, a.bs, a.scale_log2, static_cast<T*>(a.out),
-                     a.o_st, a.o_sh, a.ml, a.pacc);
+                     static_cast<const T*>(a.vp), a.hq, a.hkv, a.scale_log2,
+                     static_cast<T*>(a.out), a.o_st, a.o_sh, a.ml, a.pacc);
 }
 
 template <typename T, int D>

@@ -215,12 +215,12 @@ __device__ __forceinline__ void stage_store(const StageRegs& st, int tid,
 // Two waves per SIMD: the register budget (256 per lane) keeps S, O and the staged tile in VGPRs.
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_prefill_mfma_kernel(
-    const _Float16* __restrict__ q, int64_t q_st, int64_t q_sh,
-    const _Float16* __restrict__ kpool, const _Float16* __restrict__ vpool,
-    const int32_t* __restrict__ block_tables, int64_t bt_stride,
+    const int32_t* __restrict__ plan, int32_t item_base, int32_t bs_shift,
     const int32_t* __restrict__ qsl, const int32_t* __restrict__ ctx,
-    const int32_t* __restrict__ plan, int32_t item_base, int32_t n_q_heads, int32_t n_kv_heads,
-    int32_t num_blocks, int32_t bs_shift, float scale_log2, _Float16* __restrict__ out,
+    const int32_t* __restrict__ block_tables, int64_t bt_stride, int32_t num_blocks,
+    int32_t n_q_heads, const _Float16* __restrict__ q, int64_t q_st, int64_t q_sh,
+    const _Float16* __restrict__ kpool, const _Float16* __restrict__ vpool, int32_t n_kv_heads,
+    float scale_log2, _Float16* __restrict__ out,
     int64_t o_st, int64_t o_sh, float2* __restrict__ part_ml, float* __restrict__ part_acc) {
   __shared__ __align__(16) _Float16 sk[2][kKeys * kRow];
   __shared__ __align__(16) _Float16 svt[2][kD * kRow];
@@ -461,11 +461,11 @@ void launch_prefill_tiles_f16_d64(const AttnLaunch& a, int item_base, int count,
   // 160 KiB (the static arrays take ~34 KiB): the tiles then hold one of each SIMD's two register
   // halves and decode waves keep the other.
   const unsigned pad = shared ? kSharedLdsPad : 0;
-  hipLaunchKernelGGL(attn_prefill_mfma_kernel, dim3(count), dim3(kThreads), pad, a.s,
+  hipLaunchKernelGGL(attn_prefill_mfma_kernel, dim3(count), dim3(kThreads), pad, a.s, a.plan,
+                     item_base, log2_exact(a.bs), a.qsl, a.ctx, a.bt, a.bt_stride, a.nb, a.hq,
                      static_cast<const _Float16*>(a.q), a.q_st, a.q_sh,
-                     static_cast<const _Float16*>(a.kp), static_cast<const _Float16*>(a.vp), a.bt,
-                     a.bt_stride, a.qsl, a.ctx, a.plan, item_base, a.hq, a.hkv, a.nb,
-                     log2_exact(a.bs), a.scale_log2, static_cast<_Float16*>(a.out), a.o_st,
+                     static_cast<const _Float16*>(a.kp), static_cast<const _Float16*>(a.vp),
+                     a.hkv, a.scale_log2, static_cast<_Float16*>(a.out), a.o_st,
                      a.o_sh, a.ml, a.pacc);
 }
 

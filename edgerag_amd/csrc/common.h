@@ -48,6 +48,22 @@ __device__ __forceinline__ void issue_fence() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
+// v, made opaque to the optimiser at this point of the program (a wave-uniform value kept in
+// SGPRs): computations on it cannot be hoisted above the statement that uses pin_s.
+template <class V>
+__device__ __forceinline__ V pin_s(V v) {
+  asm volatile("" : "+s"(v));
+  return v;
+}
+
+// p as a global-memory pointer: loads through it are global_load instructions (a pointer that
+// went through pin_s is a generic one, whose loads would be flat loads, which also count against
+// lgkmcnt and make every later wait a full one).
+template <class T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T* as_global(const T* p) {
+  return (const __attribute__((address_space(1))) T*)p;
+}
+
 // A plain 16-byte register payload. Loads/stores through it compile to dwordx4 accesses.
 struct alignas(16) Vec16 {
   uint32_t w[4];

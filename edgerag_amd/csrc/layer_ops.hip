@@ -27,8 +27,8 @@ __device__ __forceinline__ T round_to(float v) {
 template <typename T, int kPer>
 __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(
     const T* __restrict__ x, const T* __restrict__ delta, const T* __restrict__ weight,
-    T* __restrict__ h_out, T* __restrict__ y, int32_t width, int64_t x_stride, int64_t d_stride,
-    int64_t h_stride, int64_t y_stride, float eps) {
+    int64_t x_stride, int64_t d_stride, int32_t width, float eps, T* __restrict__ h_out,
+    T* __restrict__ y, int64_t h_stride, int64_t y_stride) {
 #pragma clang fp contract(off)
   const int64_t row = blockIdx.x;
   const T* xr = x + row * x_stride;
@@ -74,8 +74,8 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(
 template <typename T, int NV>
 __global__ __launch_bounds__(kNormThreads) void rmsnorm_vec_kernel(
     const T* __restrict__ x, const T* __restrict__ delta, const T* __restrict__ weight,
-    T* __restrict__ h_out, T* __restrict__ y, int32_t width, int64_t x_stride, int64_t d_stride,
-    int64_t h_stride, int64_t y_stride, float eps) {
+    int64_t x_stride, int64_t d_stride, int32_t width, float eps, T* __restrict__ h_out,
+    T* __restrict__ y, int64_t h_stride, int64_t y_stride) {
 #pragma clang fp contract(off)
   constexpr int E = 16 / sizeof(T);
   const int64_t row = blockIdx.x;
@@ -264,8 +264,8 @@ int launch_rmsnorm(const void* x, const void* delta, const void* weight, void* h
 #define EDGERAG_NORMV(NV)                                                                       \
   hipLaunchKernelGGL((rmsnorm_vec_kernel<T, NV>), dim3(rows), dim3(kNormThreads), 0, s,         \
                      static_cast<const T*>(x), static_cast<const T*>(delta),                    \
-                     static_cast<const T*>(weight), static_cast<T*>(h_out), static_cast<T*>(y), \
-                     width, xs, ds, hs, ys, eps)
+                     static_cast<const T*>(weight), xs, ds, width, eps,                         \
+                     static_cast<T*>(h_out), static_cast<T*>(y), hs, ys)
     if (nv <= 1) EDGERAG_NORMV(1);
     else if (nv <= 2) EDGERAG_NORMV(2);
     else if (nv <= 4) EDGERAG_NORMV(4);
@@ -277,8 +277,8 @@ int launch_rmsnorm(const void* x, const void* delta, const void* weight, void* h
 #define EDGERAG_NORM(P)                                                                         \
   hipLaunchKernelGGL((rmsnorm_kernel<T, P>), dim3(rows), dim3(kNormThreads), 0, s,              \
                      static_cast<const T*>(x), static_cast<const T*>(delta),                    \
-                     static_cast<const T*>(weight), static_cast<T*>(h_out), static_cast<T*>(y), \
-                     width, xs, ds, hs, ys, eps)
+                     static_cast<const T*>(weight), xs, ds, width, eps,                         \
+                     static_cast<T*>(h_out), static_cast<T*>(y), hs, ys)
   if (per <= 4) EDGERAG_NORM(4);
   else if (per <= 8) EDGERAG_NORM(8);
   else if (per <= 16) EDGERAG_NORM(16);

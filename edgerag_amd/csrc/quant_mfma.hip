@@ -249,15 +249,17 @@ __device__ __forceinline__ void skinny_compute(const SkinnyBatch<BITS, NT, MT, U
 // (blockDim.x / 64 of them). Lane l feeds row l % 16 of a tile (A operand) and activation row
 // l % 16 of an m-tile (B operand); lane group l / 16 owns bytes [16 (l/16), +16) of every 64-byte
 // row chunk.
+// kw: the launch's waves per workgroup (blockDim.x / 64), passed among the leading arguments, which
+// the library preloads into SGPRs, so the K split does not wait for a load of the workgroup size
+// from the hidden kernel arguments.
 template <int BITS, int NT, int MT, int U, int NB, bool PG, int KWMAX>
 __global__ __launch_bounds__(KWMAX * kWave) void qlinear_skinny_kernel(
-    const f16* __restrict__ x, int64_t xs, int32_t m, int32_t k,
-    const uint8_t* __restrict__ packed, const f16* __restrict__ scales,
-    const f16* __restrict__ bias, int32_t n, int32_t g, f16* __restrict__ y, int64_t ys) {
+    const f16* __restrict__ x, int64_t xs, const uint8_t* __restrict__ packed,
+    const f16* __restrict__ scales, int32_t m, int32_t k, int32_t n, int32_t g, int32_t kw,
+    const f16* __restrict__ bias, f16* __restrict__ y, int64_t ys) {
   using C = SkinnyCfg<BITS>;
   __shared__ float red[KWMAX * NT * MT * 4 * kWave];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int kw = blockDim.x >> 6;
   const int li = lane & 15, lg = lane >> 4;
   const int nkb = k / C::KB;
   const int per = (nkb + kw - 1) / kw;
@@ -475,54 +477,68 @@ __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlin
   const int e_d = ROPE8 ? (e_in & 1) * half + rope_j + (e_in >> 1)
                         : (e_in / R) * half + rope_j + e_in % R;
   // (Raw loads only, nothing computed on them before the pins, like the scale and bias words.)
+  // These loads take their pointers from the epilogue arguments, which are not among the
+  // leading kernel arguments preloaded into SGPRs: they are issued right after the first batch's
+  // weight loads (epi_loads), so that the batch does not wait for the argument fetch.
   int32_t rope_slot[EPI == kEpiRope ? NO : 1];
   uint32_t rope_c[EPI == kEpiRope ? NO : 1], rope_s[EPI == kEpiRope ? NO : 1];
-  if constexpr (EPI == kEpiRope) {
-    const uint16_t* cos_u = reinterpret_cast<const uint16_t*>(ea.cos_tok);
-    const uint16_t* sin_u = reinterpret_cast<const uint16_t*>(ea.sin_tok);
-#pragma unroll
-    for (int o = 0; o < NO; ++o) {
-      const int tok = min((int(threadIdx.x) + o * KW * kWave) / (NT * R), m - 1);
-      rope_slot[o] = ea.slots[tok];
-      rope_c[o] = cos_u[int64_t(tok) * ea.head_dim + e_d];
-      rope_s[o] = sin_u[int64_t(tok) * ea.head_dim + e_d];
-    }
-  }
-  // kEpiResidual: the residual-stream value of each output. NORM: wave w sums the partials of
-  // tokens w, w + KW, ..., lane l those with index l + 64 q (clamped; masked when summed).
   uint32_t hid_pre[EPI == kEpiResidual ? NO : 1];
   uint32_t nw_pre = 0;  // kEpiResidual with xw: the next norm's weight at this thread's row
   float norm_pre[NORM ? TOKW * NPQ : 1];
-  if constexpr (EPI == kEpiResidual) {
-    const uint16_t* hid_u = reinterpret_cast<const uint16_t*>(ea.hidden);
+  // The argument values pass through pin_s where they are used, so that no address computation
+  // (and no wait for the argument fetch) is hoisted above the batch loads.
+  auto epi_loads = [&]() {
+    if constexpr (EPI == kEpiRope) {
+      const auto* cos_u = as_global(reinterpret_cast<const uint16_t*>(pin_s(ea.cos_tok)));
+      const auto* sin_u = as_global(reinterpret_cast<const uint16_t*>(pin_s(ea.sin_tok)));
+      const auto* slots = as_global(pin_s(ea.slots));
+      const int hd = pin_s(ea.head_dim);
 #pragma unroll
-    for (int o = 0; o < NO; ++o) {
-      const int tok = min((int(threadIdx.x) + o * KW * kWave) / (NT * R), m - 1);
-      hid_pre[o] = hid_u[int64_t(tok) * ea.hid_st + e_row];
-    }
-    // Loaded unconditionally (from the hidden row when there is no xw) so no branch sits
-    // between these loads and the batch loads.
-    const uint16_t* nw_u = reinterpret_cast<const uint16_t*>(ea.next_w != nullptr ? ea.next_w
-                                                                                  : ea.hidden);
-    nw_pre = nw_u[e_row];
-  }
-  if constexpr (NORM) {
-    // Only the batch's tokens and the partials the producer wrote are loaded (wave-uniform
-    // branches): at one token one wave of the workgroup loads its 256 sums, where every wave
-    // loaded a clamped copy, 8 instructions per wave through the address unit (one token:
-    // 2048->16384 gate/up 9.71 -> 9.58 us, q/k/v + RoPE 5.84 -> 5.64 us).
-#pragma unroll
-    for (int j = 0; j < TOKW; ++j) {
-      const int tok = wave + KW * j;
-#pragma unroll
-      for (int q = 0; q < NPQ; ++q) {
-        norm_pre[j * NPQ + q] = 0.f;
-        if (tok < m && kWave * q < ea.norm_parts)
-          norm_pre[j * NPQ + q] = ea.norm_part[int64_t(tok) * ea.norm_parts +
-                                               min(lane + kWave * q, ea.norm_parts - 1)];
+      for (int o = 0; o < NO; ++o) {
+        const int tok = min((int(threadIdx.x) + o * KW * kWave) / (NT * R), m - 1);
+        rope_slot[o] = slots[tok];
+        rope_c[o] = cos_u[int64_t(tok) * hd + e_d];
+        rope_s[o] = sin_u[int64_t(tok) * hd + e_d];
       }
     }
-  }
+    // kEpiResidual: the residual-stream value of each output. NORM: wave w sums the partials of
+    // tokens w, w + KW, ..., lane l those with index l + 64 q (clamped; masked when summed).
+    if constexpr (EPI == kEpiResidual) {
+      const f16* hidden = pin_s(ea.hidden);
+      const f16* next_w = pin_s(ea.next_w);
+      const int64_t hid_st = pin_s(ea.hid_st);
+      const auto* hid_u = as_global(reinterpret_cast<const uint16_t*>(hidden));
+#pragma unroll
+      for (int o = 0; o < NO; ++o) {
+        const int tok = min((int(threadIdx.x) + o * KW * kWave) / (NT * R), m - 1);
+        hid_pre[o] = hid_u[int64_t(tok) * hid_st + e_row];
+      }
+      // Loaded unconditionally (from the hidden row when there is no xw): no branch between
+      // these loads.
+      const auto* nw_u =
+          as_global(reinterpret_cast<const uint16_t*>(next_w != nullptr ? next_w : hidden));
+      nw_pre = nw_u[e_row];
+    }
+    if constexpr (NORM) {
+      // Only the batch's tokens and the partials the producer wrote are loaded (wave-uniform
+      // branches): at one token one wave of the workgroup loads its 256 sums, where every wave
+      // loaded a clamped copy, 8 instructions per wave through the address unit (one token:
+      // 2048->16384 gate/up 9.71 -> 9.58 us, q/k/v + RoPE 5.84 -> 5.64 us).
+      const auto* norm_part = as_global(pin_s(ea.norm_part));
+      const int parts = pin_s(ea.norm_parts);
+#pragma unroll
+      for (int j = 0; j < TOKW; ++j) {
+        const int tok = wave + KW * j;
+#pragma unroll
+        for (int q = 0; q < NPQ; ++q) {
+          norm_pre[j * NPQ + q] = 0.f;
+          if (tok < m && kWave * q < parts)
+            norm_pre[j * NPQ + q] =
+                norm_part[int64_t(tok) * parts + min(lane + kWave * q, parts - 1)];
+        }
+      }
+    }
+  };
 
   f32x4 acc[NT][MT];
 #pragma unroll
@@ -554,6 +570,12 @@ __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlin
           xa[u][t] = ldg16(xb);
           xc[u][t] = ldg16(xb + 8);
         }
+      }
+    }
+    if constexpr (EPI == kEpiRope || EPI == kEpiResidual || NORM) {
+      if (cb == c0) {
+        issue_fence();  // the batch's loads go out before the epilogue's wait for its arguments
+        epi_loads();
       }
     }
     issue_fence();
@@ -617,6 +639,8 @@ __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlin
       }
     }
   }
+  if (c0 >= c1) epi_loads();  // a wave with no K range still writes outputs (none for kEpiPlain,
+                              // kEpiSwiglu without NORM: their epi_loads is empty)
 
   // Sum slices and waves in a fixed order, then y[m][n] = scale[n] * sum (+ bias[n]).
   // Accumulator register i of lane l holds D row 4 (l / 16) + i, column l % 16.
@@ -1244,7 +1268,7 @@ void launch_skinny(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t
   const bool pg = k / g > 1;
 #define EDGERAG_SKINNY(NB, PG, KWM)                                                            \
   hipLaunchKernelGGL((qlinear_skinny_kernel<BITS, NT, MT, U, NB, PG, KWM>), dim3(blocks),      \
-                     dim3(kw * kWave), 0, s, x, xs, m, k, packed, scales, bias, n, g, y, ys)
+                     dim3(kw * kWave), 0, s, x, xs, packed, scales, m, k, n, g, kw, bias, y, ys)
   if (kw > kMaxSkinnyWaves) {
     if constexpr (NT == 1 && MT == 1) {
       if (per_wave <= U) {
