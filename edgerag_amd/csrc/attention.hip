@@ -236,39 +236,56 @@ __global__ __launch_bounds__(WG ? kMaxRowWaves * kWave : kWave) void attn_decode
   const int64_t idx = int64_t(item_base) + blockIdx.x;
   const int32_t* it = plan + kHeaderWords + idx * kItemWords;
   const int4 ia = reinterpret_cast<const int4*>(it)[0], ib = reinterpret_cast<const int4*>(it)[1];
-  if (idx >= plan[limit_word]) return;
-  const int r = ia.x, h = ia.y, qb = ia.z, qc = ia.w;  // I_REQ, I_HEAD, I_QBEGIN, I_QCOUNT
-  int kb = ib.x, ke = ib.y;                             // I_KVBEGIN, I_KVEND
-  const int split = ib.z;                               // I_SPLIT
-  const int wave = WG ? int(threadIdx.x >> 6) : 0;
+  int r = ia.x, h = ia.y, qb = ia.z, qc = ia.w;  // I_REQ, I_HEAD, I_QBEGIN, I_QCOUNT
+  int kb = ib.x, ke = ib.y;                       // I_KVBEGIN, I_KVEND
+  int split = ib.z;                               // I_SPLIT
+  int limit = plan[limit_word], req_off = plan[H_REQ_OFF];
+  const int nw = WG ? int(blockDim.x >> 6) : 1;
+  // The prologue's dependent loads take three round trips: (1) the item, the count, the request
+  // table's offset and the kernel arguments that are not preloaded; (2) the request's entries
+  // and the split's block ids; (3) q and the first K/V rows. Used here, the first group is loaded
+  // together, not each after the exit test or where first needed (the compiler would sink them).
+  // (The item's unused last word is used too: left dead, its register is handed to another load
+  // of the group, which then has to wait for the item's load to land.)
+  asm volatile("" : "+s"(limit), "+s"(req_off), "+s"(r), "+s"(h), "+s"(qb), "+s"(qc), "+s"(kb),
+               "+s"(ke), "+s"(split)
+               : "s"(ib.w), "s"(nw), "s"(n_q_heads), "s"(n_kv_heads), "s"(q), "s"(q_st),
+                 "s"(q_sh), "s"(kpool), "s"(vpool), "s"(scale_log2), "s"(out), "s"(o_st),
+                 "s"(o_sh), "s"(part_ml), "s"(part_acc));
+  if constexpr (APPEND)
+    asm volatile("" ::"s"(nk), "s"(nv), "s"(n_st), "s"(n_sh), "s"(slots), "s"(kdst), "s"(vdst));
+  if (idx >= limit) return;
+  const int wave = WG ? __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6)) : 0;
   if constexpr (WG) {
     // This wave's part of the keys: equal parts of whole blocks (a part never straddles the
     // wave's block-id registers), empty for waves past the end.
-    const int nw = int(blockDim.x >> 6);
     const int per = (ke - kb + nw - 1) / nw;
     const int part = (per + block_size - 1) / block_size * block_size;
     const int b0 = min(ke, kb + wave * part);
     ke = min(ke, b0 + part);
     kb = b0;
   }
-  const int32_t* rq = plan + plan[H_REQ_OFF] + r * kReqWords;
-  const int nsplit = rq[R_NSPLIT], part_off = rq[R_PARTOFF], pstride = rq[R_PSTRIDE];
-  const int q0 = qsl[r], c = qsl[r + 1] - q0, L = ctx[r];
+  const int lane = threadIdx.x & (kWave - 1);
+  // Block ids of this split, one per lane; broadcast per load with v_readlane. The load is
+  // unconditional (lanes past the split re-read its last entry, always inside the table row) and
+  // the ids are checked only after the request's entries are loaded as well: one round trip.
+  const int blk0 = kb / block_size;
+  const int nblk = (ke - kb + block_size - 1) / block_size;
+  int32_t b_raw = -1;
+  if (nblk > 0)  // wave-uniform
+    b_raw = block_tables[int64_t(r) * bt_stride + blk0 + min(lane, nblk - 1)];
+  const int32_t* rq = plan + req_off + r * kReqWords;
+  int nsplit = rq[R_NSPLIT], part_off = rq[R_PARTOFF], pstride = rq[R_PSTRIDE];
+  int q0 = qsl[r], q1 = qsl[r + 1], L = ctx[r];
+  asm volatile("" : "+s"(nsplit), "+s"(part_off), "+s"(pstride), "+s"(q0), "+s"(q1), "+s"(L));
+  const int c = q1 - q0;
+  issue_fence();
+  const int my_blk = (lane < nblk && b_raw >= 0 && b_raw < num_blocks) ? b_raw : -1;
   const int n_rep = n_q_heads / n_kv_heads;
 
-  const int lane = threadIdx.x & (kWave - 1);
   const int sub = lane & (LPT - 1);
   const int tslot = lane >> LOG_LPT;
   const int64_t head_base = int64_t(h) * num_blocks;
-
-  // Block ids of this split, one per lane; broadcast per load with v_readlane.
-  const int blk0 = kb / block_size;
-  const int nblk = (ke - kb + block_size - 1) / block_size;
-  int my_blk = -1;
-  if (lane < nblk) {
-    const int32_t b = block_tables[int64_t(r) * bt_stride + blk0 + lane];
-    my_blk = (b >= 0 && b < num_blocks) ? b : -1;
-  }
 
   const int nvec = qc * n_rep;
   for (int v0 = 0; v0 < nvec; v0 += QR) {
