@@ -267,10 +267,12 @@ def check_coverage(qsl, ctx, n_q, n_kv, bs=16):
 
 def check_parts(ctx, h, bs, items, reqs, plan) -> None:
     """A batch of fewer row workgroups than CUs: each context in equal whole-block parts of at
-    least 8 waves x 32 tokens, about 512 workgroups in all (never more than 512 plus one per
-    request and head), their partials in fixed slots: every token has a merge row."""
+    least 8 waves x 32 tokens (x 16 when no context passes 2,048 tokens), about 512 workgroups in
+    all (never more than 512 plus one per request and head), their partials in fixed slots: every
+    token has a merge row."""
     work = sum(ctx) * h
-    part = min(8 * 64 * bs, max(8 * 32, -(-(-(-work // 512)) // bs) * bs))
+    wave_tokens = -(-(16 if max(ctx) <= 2048 else 32) // bs) * bs
+    part = min(8 * 64 * bs, max(8 * wave_tokens, -(-(-(-work // 512)) // bs) * bs))
     slots = int(plan[21])
     if max(ctx) <= part:  # no context cut: nothing to merge, no slots
         assert slots == 0 and int(plan[16]) == 0

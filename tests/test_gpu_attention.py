@@ -587,9 +587,10 @@ def test_few_decodes_as_context_parts_fp16(device, lens, n_q, n_kv) -> None:
     plan_host, _ = kernels.make_plan_host(qsl, np.asarray(lens, np.int32), n_q, n_kv, d,
                                           BLOCK_SIZE, bt.shape[1], torch.float16)
     assert int(plan_host[19]) == 8, "expected workgroups over parts of the contexts"
-    # Parts (of >= 8 x 32 tokens) in fixed slots: every token has a merge row, split or not;
-    # nothing to merge when no context is cut.
-    split = any(L > 256 for L in lens)
+    # Parts (of >= 8 x 32 tokens, 8 x 16 when no context passes 2,048) in fixed slots: every
+    # token has a merge row, split or not; nothing to merge when no context is cut.
+    min_part = 128 if max(lens) <= 2048 else 256
+    split = any(L > min_part for L in lens)
     assert int(plan_host[21]) == ((16 if n_kv == 32 else 32) if split else 0)
     assert int(plan_host[16]) == (len(lens) if split else 0)
     got = _run_ragged(device, kp, vp, qsl, lens, bt, q, d**-0.5)
