@@ -393,7 +393,11 @@ __device__ __forceinline__ f16 rope_elem(float own, float partner, bool second, 
   return __float2half_rn(a + b);
 }
 
-template <int F, int NT, int MT, int KW, int U, bool EXACT, int EPI, bool NORM, bool X1>
+// RH (kEpiRope): half the head dimension when known at compile time (0: ea.head_dim / 2). The
+// weight rows of a RoPE workgroup follow from it, and ea is not among the leading kernel
+// arguments preloaded into SGPRs: a run-time value makes the first loads wait for its fetch.
+template <int F, int NT, int MT, int KW, int U, bool EXACT, int EPI, bool NORM, bool X1,
+          int RH = 0>
 __global__ __launch_bounds__(KW * kWave)
 __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlinear_stream_kernel(
     const f16* __restrict__ x, int64_t xs, int32_t m, int32_t k,
@@ -430,12 +434,12 @@ __attribute__((amdgpu_waves_per_eu(1, U * MT * NT >= 8 ? KW / 4 : 8))) void qlin
   const int li = lane & 15, lg = lane >> 4;
   const int f = li / R, r = li % R;
   // kEpiSwiglu: gate rows [0, half), up rows [half, n). kEpiRope: head_dim / 2.
-  const int half = EPI == kEpiRope ? ea.head_dim >> 1 : n >> 1;
+  const int half = EPI == kEpiRope ? (RH > 0 ? RH : ea.head_dim >> 1) : n >> 1;
   constexpr int PAIRS = NT * R / 2;  // kEpiRope: rotate_half pairs of a workgroup
   const int per_head = half / PAIRS;  // kEpiRope: workgroups per head
   const int rope_head = EPI == kEpiRope ? int(blockIdx.x) / per_head : 0;
   const int rope_j = EPI == kEpiRope ? (int(blockIdx.x) % per_head) * PAIRS : 0;
-  const int n0 = EPI == kEpiRope ? rope_head * ea.head_dim + rope_j
+  const int n0 = EPI == kEpiRope ? rope_head * 2 * half + rope_j
                                  : int(blockIdx.x) * (EPI == kEpiSwiglu ? R : NT * R);
   const int nc = k / CB;  // chunk steps: >= U, and a multiple of KW * U when EXACT
   const int per = (nc + KW - 1) / KW;
@@ -1426,7 +1430,7 @@ void launch_gemm_split(const f16* x, int64_t xs, int32_t m, int32_t k, const uin
 // steps per batch U from K alone, so that a row's summation order, and so its bits, do not depend
 // on M or on the other rows of the launch. Returns false when the shape does not fit (the caller
 // then uses the skinny kernel).
-template <int F, int NT, int MT, int KW, int U, int EPI, bool NORM>
+template <int F, int NT, int MT, int KW, int U, int EPI, bool NORM, int RH = 0>
 void launch_stream(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* packed,
                    const f16* scales, const f16* bias, int32_t n, f16* y, int64_t ys,
                    const EpiArgs& ea, hipStream_t s) {
@@ -1441,8 +1445,9 @@ void launch_stream(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t
   // the steps: measured 8.16 -> 8.41 us on 2048->16384, so those keep the direct loads.)
   constexpr bool kX1 = MT == 1 && F == 2;
 #define EDGERAG_STREAM_X(EX, X1)                                                                 \
-  hipLaunchKernelGGL((qlinear_stream_kernel<F, NT, MT, KW, U, EX, EPI, NORM, X1>), dim3(blocks),  \
-                     dim3(KW * kWave), 0, s, x, xs, m, k, packed, scales, bias, n, y, ys, ea)
+  hipLaunchKernelGGL((qlinear_stream_kernel<F, NT, MT, KW, U, EX, EPI, NORM, X1, RH>),            \
+                     dim3(blocks), dim3(KW * kWave), 0, s, x, xs, m, k, packed, scales, bias, n, y, \
+                     ys, ea)
   const bool exact = (k / (64 * F)) % (KW * U) == 0;
   if (kX1 && m == 1) {
     if (exact) EDGERAG_STREAM_X(true, kX1); else EDGERAG_STREAM_X(false, kX1);
@@ -1474,7 +1479,7 @@ StreamWaves stream_waves(int f, int nt, int mt, int k) {
 }
 
 // Launches the shape with the given waves (KW in {4, 8, 16}) and batch (U in {4, 8}).
-template <int F, int NT, int MT, int EPI, bool NORM = false>
+template <int F, int NT, int MT, int EPI, bool NORM = false, int RH = 0>
 void launch_stream_w(StreamWaves sw, const f16* x, int64_t xs, int32_t m, int32_t k,
                      const uint8_t* packed, const f16* scales, const f16* bias, int32_t n, f16* y,
                      int64_t ys, const EpiArgs& ea, hipStream_t s) {
@@ -1482,13 +1487,13 @@ void launch_stream_w(StreamWaves sw, const f16* x, int64_t xs, int32_t m, int32_
   do {                                                                                         \
     if constexpr (MT == 1) {                                                                   \
       if (sw.u8) {                                                                             \
-        launch_stream<F, NT, MT, KW, 8, EPI, NORM>(x, xs, m, k, packed, scales, bias, n, y, ys, \
-                                                   ea, s);                                     \
+        launch_stream<F, NT, MT, KW, 8, EPI, NORM, RH>(x, xs, m, k, packed, scales, bias, n, y, \
+                                                       ys, ea, s);                             \
         return;                                                                                \
       }                                                                                        \
     }                                                                                          \
-    launch_stream<F, NT, MT, KW, 4, EPI, NORM>(x, xs, m, k, packed, scales, bias, n, y, ys, ea,  \
-                                               s);                                             \
+    launch_stream<F, NT, MT, KW, 4, EPI, NORM, RH>(x, xs, m, k, packed, scales, bias, n, y, ys,  \
+                                                   ea, s);                                     \
     return;                                                                                    \
   } while (0)
   // Only the combinations stream_waves can pick are instantiated: 4 waves for one row tile (and
@@ -1831,8 +1836,12 @@ void launch_rope(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t* 
                  const f16* scales, const f16* bias, int32_t n, const EpiArgs& ea,
                  hipStream_t s) {
   const int nt = (int64_t(n) + 15) / 16 >= EDGERAG_STREAM_NT2_TILES ? 2 : 1;
-  launch_stream_w<1, 2, MT, kEpiRope, NORM>(stream_waves(1, nt, MT, k), x, xs, m, k, packed,
-                                            scales, bias, n, nullptr, 0, ea, s);
+  if (ea.head_dim == 64)
+    launch_stream_w<1, 2, MT, kEpiRope, NORM, 32>(stream_waves(1, nt, MT, k), x, xs, m, k, packed,
+                                                  scales, bias, n, nullptr, 0, ea, s);
+  else
+    launch_stream_w<1, 2, MT, kEpiRope, NORM>(stream_waves(1, nt, MT, k), x, xs, m, k, packed,
+                                              scales, bias, n, nullptr, 0, ea, s);
 }
 
 // Two k-slices: 8-row tiles with 8-token m-tiles, the plain launch's shape for M <= 32.
@@ -1841,8 +1850,14 @@ void launch_rope8(const f16* x, int64_t xs, int32_t m, int32_t k, const uint8_t*
                   const f16* scales, const f16* bias, int32_t n, const EpiArgs& ea,
                   hipStream_t s) {
 #define EDGERAG_ROPE8(MT)                                                                        \
-  launch_stream_w<2, 1, MT, kEpiRope, NORM>(stream_waves(2, 1, MT, k), x, xs, m, k, packed,      \
-                                            scales, bias, n, nullptr, 0, ea, s)
+  do {                                                                                           \
+    if (ea.head_dim == 64)                                                                       \
+      launch_stream_w<2, 1, MT, kEpiRope, NORM, 32>(stream_waves(2, 1, MT, k), x, xs, m, k,      \
+                                                    packed, scales, bias, n, nullptr, 0, ea, s); \
+    else                                                                                         \
+      launch_stream_w<2, 1, MT, kEpiRope, NORM>(stream_waves(2, 1, MT, k), x, xs, m, k, packed,  \
+                                                scales, bias, n, nullptr, 0, ea, s);             \
+  } while (0)
   if (m <= 8) {
     EDGERAG_ROPE8(1);
   } else if constexpr (NORM) {
