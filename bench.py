@@ -766,6 +766,8 @@ def main() -> None:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-cfg5", action="store_true", help="skip the end-to-end serving run")
     ap.add_argument("--cfg5-requests", type=int, default=64)
+    ap.add_argument("--record", default=None,
+                    help="also write the full (uncompacted) record of the run to this JSON file")
     ap.add_argument("--only", choices=["cfg3", "cfg4", "cfg5", "lm_head", "single_seq",
                                        "decode_b1"],
                     default=None,
@@ -863,6 +865,9 @@ def main() -> None:
         line["lm_head"] = bench_lm_head(device)
         if not args.no_cfg5:
             line["cfg5"] = run_cfg5(device, args.cfg5_requests, not args.no_cpu)
+    if args.record:
+        with open(args.record, "w") as f:
+            json.dump(line, f, indent=1)
     print(json.dumps(compact_line(line), separators=(",", ":")), flush=True)
 
 
