@@ -199,10 +199,15 @@ class EdgeRagDecoder(nn.Module):
         T = step.token_ids.shape[0]
         d, eps = spec.head_dim, spec.rms_norm_eps
         # The residual stream is updated in place, so it is always a fresh tensor of this step.
-        # index_select takes the int32 ids as they are (no widening launch).
-        hidden = (self.embed_tokens.index_select(0, step.token_ids) if step.hidden is None
-                  else step.hidden)
-        x = kernels.rmsnorm(hidden, self.layers[0].input_layernorm.weight, eps)
+        # Token ids: the embedding rows and the first RMSNorm in one launch (the same bits as
+        # index_select + rmsnorm).
+        w0 = self.layers[0].input_layernorm.weight
+        if step.hidden is None and kernels.embed_rmsnorm_fits(self.embed_tokens):
+            hidden, x = kernels.embed_rmsnorm(step.token_ids, self.embed_tokens, w0, eps)
+        else:
+            hidden = (self.embed_tokens.index_select(0, step.token_ids) if step.hidden is None
+                      else step.hidden)
+            x = kernels.rmsnorm(hidden, w0, eps)
         q = torch.empty((T, spec.n_q_heads, d), device=self.device, dtype=self.dtype)
         attn_out = torch.empty_like(q)
         n_layers = len(self.layers)

@@ -71,16 +71,26 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(
 // chunks t, t + 256, ... of the row. Every load of the row (x, delta and weight) is issued before
 // any is used, so a row costs one memory round trip; chunks past the row re-read its last chunk
 // and are masked.
+// ids != NULL (embedding lookup + the first RMSNorm): row r of x is table row ids[r], copied to
+// h_out; an id outside [0, n_table) has no row: its h and y are written as NaN.
 template <typename T, int NV>
 __global__ __launch_bounds__(kNormThreads) void rmsnorm_vec_kernel(
-    const T* __restrict__ x, const T* __restrict__ delta, const T* __restrict__ weight,
-    int64_t x_stride, int64_t d_stride, int32_t width, float eps, T* __restrict__ h_out,
-    T* __restrict__ y, int64_t h_stride, int64_t y_stride) {
+    const T* __restrict__ x, const int32_t* __restrict__ ids, int32_t n_table,
+    const T* __restrict__ delta, const T* __restrict__ weight, int64_t x_stride,
+    int64_t d_stride, int32_t width, float eps, T* __restrict__ h_out, T* __restrict__ y,
+    int64_t h_stride, int64_t y_stride) {
 #pragma clang fp contract(off)
   constexpr int E = 16 / sizeof(T);
   const int64_t row = blockIdx.x;
   const int nch = width / E;
-  const T* xr = x + row * x_stride;
+  int64_t src = row;
+  bool bad = false;
+  if (ids != nullptr) {
+    const int32_t id = ids[row];
+    bad = id < 0 || id >= n_table;
+    src = bad ? 0 : id;
+  }
+  const T* xr = x + src * x_stride;
   const T* dr = delta != nullptr ? delta + row * d_stride : nullptr;
   Vec16 xv[NV], dv[NV], wv[NV];
 #pragma unroll
@@ -126,9 +136,9 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_vec_kernel(
     T ho[E], yo[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-      ho[e] = round_to<T>(h[j][e]);
+      ho[e] = round_to<T>(bad ? __builtin_nanf("") : h[j][e]);
       const float nv = to_f32<T>(round_to<T>(h[j][e] * r));
-      yo[e] = round_to<T>(vec_elem<T>(wv[j], e) * nv);
+      yo[e] = round_to<T>(bad ? __builtin_nanf("") : vec_elem<T>(wv[j], e) * nv);
     }
     if (hr != nullptr) store16(hr + ch * E, *reinterpret_cast<const Vec16*>(ho));
     store16(yr + ch * E, *reinterpret_cast<const Vec16*>(yo));
@@ -254,7 +264,7 @@ inline bool aligned_rows(const void* p, int64_t stride_elems, int elem_size) {
 template <typename T>
 int launch_rmsnorm(const void* x, const void* delta, const void* weight, void* h_out, void* y,
                    int32_t rows, int32_t width, int64_t xs, int64_t ds, int64_t hs, int64_t ys,
-                   float eps, hipStream_t s) {
+                   float eps, hipStream_t s, const int32_t* ids = nullptr, int32_t n_table = 0) {
   constexpr int E = 16 / sizeof(T);
   const int nch = width / E;
   if (width % E == 0 && aligned_rows(x, xs, sizeof(T)) && aligned_rows(delta, ds, sizeof(T)) &&
@@ -263,7 +273,7 @@ int launch_rmsnorm(const void* x, const void* delta, const void* weight, void* h
     const int nv = (nch + kNormThreads - 1) / kNormThreads;
 #define EDGERAG_NORMV(NV)                                                                       \
   hipLaunchKernelGGL((rmsnorm_vec_kernel<T, NV>), dim3(rows), dim3(kNormThreads), 0, s,         \
-                     static_cast<const T*>(x), static_cast<const T*>(delta),                    \
+                     static_cast<const T*>(x), ids, n_table, static_cast<const T*>(delta),      \
                      static_cast<const T*>(weight), xs, ds, width, eps,                         \
                      static_cast<T*>(h_out), static_cast<T*>(y), hs, ys)
     if (nv <= 1) EDGERAG_NORMV(1);
@@ -273,6 +283,9 @@ int launch_rmsnorm(const void* x, const void* delta, const void* weight, void* h
 #undef EDGERAG_NORMV
     return check_launch("edgerag_rmsnorm");
   }
+  if (ids != nullptr)
+    return fail(EDGERAG_EUNSUPPORTED, "edgerag_embed_rmsnorm: rows of %d elements not in "
+                "16-byte chunks (or above 8 x %d chunks)", width, kNormThreads);
   const int per = (width + kNormThreads - 1) / kNormThreads;
 #define EDGERAG_NORM(P)                                                                         \
   hipLaunchKernelGGL((rmsnorm_kernel<T, P>), dim3(rows), dim3(kNormThreads), 0, s,              \
@@ -378,6 +391,26 @@ extern "C" int edgerag_rmsnorm(const void* x, int64_t x_stride, const void* delt
     case EDGERAG_BF16: return launch_rmsnorm<bf16>(x, delta, weight, h_out, y, rows, width, x_stride, delta_stride, h_stride, y_stride, eps, s);
   }
   return fail(EDGERAG_EINVAL, "edgerag_rmsnorm: dtype %d", dtype);
+}
+
+extern "C" int edgerag_embed_rmsnorm(const int32_t* ids, int32_t rows, const void* table,
+                                     int64_t table_stride, int32_t vocab, const void* weight,
+                                     void* h_out, int64_t h_stride, void* y, int64_t y_stride,
+                                     int32_t width, float eps, int32_t dtype, void* stream) {
+  clear_error();
+  if (rows < 0 || width <= 0 || vocab <= 0)
+    return fail(EDGERAG_EINVAL, "edgerag_embed_rmsnorm: rows %d width %d vocab %d", rows, width,
+                vocab);
+  if (rows == 0) return EDGERAG_OK;
+  if (ids == nullptr || table == nullptr || weight == nullptr || h_out == nullptr || y == nullptr)
+    return fail(EDGERAG_EINVAL, "edgerag_embed_rmsnorm: NULL pointer");
+  auto s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case EDGERAG_F32: return launch_rmsnorm<float>(table, nullptr, weight, h_out, y, rows, width, table_stride, 0, h_stride, y_stride, eps, s, ids, vocab);
+    case EDGERAG_F16: return launch_rmsnorm<f16>(table, nullptr, weight, h_out, y, rows, width, table_stride, 0, h_stride, y_stride, eps, s, ids, vocab);
+    case EDGERAG_BF16: return launch_rmsnorm<bf16>(table, nullptr, weight, h_out, y, rows, width, table_stride, 0, h_stride, y_stride, eps, s, ids, vocab);
+  }
+  return fail(EDGERAG_EINVAL, "edgerag_embed_rmsnorm: dtype %d", dtype);
 }
 
 extern "C" int edgerag_rope_append(const void* qkv, int64_t qkv_stride, const int32_t* positions,

@@ -725,6 +725,41 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, delta: torch.Tens
     return out
 
 
+def embed_rmsnorm_fits(table: torch.Tensor) -> bool:
+    """Whether :func:`embed_rmsnorm` takes rows of this table: whole 16-byte chunks, at most
+    8 x 256 of them, rows 16-byte aligned."""
+    width = table.shape[1]
+    es = table.element_size()
+    return (table.dim() == 2 and table.stride(1) == 1 and (width * es) % 16 == 0
+            and width * es // 16 <= 8 * 256 and (table.stride(0) * es) % 16 == 0
+            and table.data_ptr() % 16 == 0)
+
+
+def embed_rmsnorm(ids: torch.Tensor, table: torch.Tensor, weight: torch.Tensor, eps: float,
+                  h_out: torch.Tensor | None = None,
+                  out: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """The embedding rows of the int32 ``ids`` (``h``, a copy of ``table[ids]``) and their
+    RMSNorm (``out``), in one launch; returns ``(h, out)``. An id outside the table gives a row
+    of NaN in both."""
+    require_device(ids, table, weight, h_out, out)
+    if ids.dtype != torch.int32 or ids.dim() != 1 or (ids.numel() > 1 and ids.stride(0) != 1):
+        raise ValueError("ids must be a contiguous int32 vector")
+    if not embed_rmsnorm_fits(table):
+        raise ValueError("embed_rmsnorm takes tables with 16-byte aligned rows of whole 16-byte "
+                         "chunks (at most 2,048 of them)")
+    rows, (vocab, width) = ids.numel(), table.shape
+    if h_out is None:
+        h_out = torch.empty((rows, width), device=table.device, dtype=table.dtype)
+    if out is None:
+        out = torch.empty_like(h_out)
+    call(
+        "edgerag_embed_rmsnorm", ids.data_ptr(), rows, table.data_ptr(), table.stride(0), vocab,
+        weight.data_ptr(), h_out.data_ptr(), h_out.stride(0), out.data_ptr(), out.stride(0),
+        width, float(eps), dtype_code(table.dtype), stream_ptr(table.device),
+    )
+    return h_out, out
+
+
 def rope_append(qkv: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
                 n_q_heads: int, n_kv_heads: int, head_dim: int, slots: torch.Tensor,
                 key_pool: torch.Tensor, value_pool: torch.Tensor,

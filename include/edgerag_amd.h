@@ -466,6 +466,21 @@ int edgerag_rmsnorm(const void* x, int64_t x_stride, const void* delta, int64_t 
                     int32_t rows, int32_t width, float eps, int32_t dtype, void* stream);
 
 /*
+ * Embedding lookup + the first layer's RMSNorm, one launch: for t < rows,
+ *   h_out[t] = table[ids[t]]            (a copy of the embedding row)
+ *   y[t]     = weight * dtype(h * rsqrt(mean(h^2) + eps))   as edgerag_rmsnorm computes it
+ * An id outside [0, vocab) has no table row: that row's h and y are written as NaN (the
+ * reference's nn.Embedding raises on such an id). Rows must be whole 16-byte chunks, at most
+ * 8 x 256 of them (EDGERAG_EUNSUPPORTED otherwise). Replaces `embed_tokens(input_ids)`
+ * (edgerag/core/model.py:109) followed by the first layer's input RMSNorm
+ * (edgerag/core/layers.py:27-47).
+ */
+int edgerag_embed_rmsnorm(const int32_t* ids, int32_t rows, const void* table,
+                          int64_t table_stride, int32_t vocab, const void* weight, void* h_out,
+                          int64_t h_stride, void* y, int64_t y_stride, int32_t width, float eps,
+                          int32_t dtype, void* stream);
+
+/*
  * RoPE on the fused q/k/v projection output and the KV append, in one launch. Row t of qkv holds
  * [n_q_heads | n_kv_heads | n_kv_heads] heads of head_dim elements. For position p =
  * positions[t] in [0, max_pos), q and k heads become dtype(dtype(x * cos[p]) +

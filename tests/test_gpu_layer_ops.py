@@ -38,6 +38,31 @@ def test_add_rmsnorm(device, dtype, width) -> None:
                                rtol=2e-3, atol=2e-3)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("width", [64, 2048, 8192])
+def test_embed_rmsnorm_equals_lookup_then_rmsnorm(device, dtype, width) -> None:
+    """The embedding lookup fused into the first RMSNorm: bit for bit the rows of index_select
+    (nn.Embedding, edgerag/core/model.py:109) and the RMSNorm of the same launch shape; ids
+    outside the table give rows of NaN; widths that are not whole 16-byte chunks are refused."""
+    g = seeded(width + 3)
+    vocab = 500
+    table = torch.randn(vocab, width, generator=g).to(dtype).to(device)
+    w = (1 + 0.1 * torch.randn(width, generator=g)).to(dtype).to(device)
+    ids = torch.tensor([3, 499, 0, 17, 3, 250, 1, 498], dtype=torch.int32)
+    h, y = kernels.embed_rmsnorm(ids.to(device), table, w, 1e-5)
+    h_ref = table.index_select(0, ids.to(device))
+    assert torch.equal(h, h_ref)
+    assert torch.equal(y, kernels.rmsnorm(h_ref, w, 1e-5))
+    tol = {torch.float32: 1e-5, torch.float16: 2e-3, torch.bfloat16: 1.6e-2}[dtype]
+    torch.testing.assert_close(y.cpu().float(), om.rms_norm(h_ref.cpu(), w.cpu(), 1e-5).float(),
+                               rtol=tol, atol=tol)
+    bad = torch.tensor([5, -1, vocab, 7], dtype=torch.int32)
+    h2, y2 = kernels.embed_rmsnorm(bad.to(device), table, w, 1e-5)
+    assert h2[[1, 2]].isnan().all() and y2[[1, 2]].isnan().all()
+    assert torch.equal(h2[[0, 3]], table[[5, 7]]) and not y2[[0, 3]].isnan().any()
+    assert not kernels.embed_rmsnorm_fits(torch.zeros(4, 13, device=device, dtype=torch.float16))
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
 @pytest.mark.parametrize("n_q,n_kv", [(32, 32), (9, 3)])
 def test_rope_append_matches_reference_rope_and_slot_write(device, dtype, n_q, n_kv) -> None:
