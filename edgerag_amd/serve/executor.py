@@ -134,6 +134,12 @@ class ModelExecutor:
         self._graphs: dict[tuple[int, int],
                            tuple[torch.cuda.CUDAGraph, torch.Tensor, torch.Tensor]] = {}
         self.graph_steps = 0
+        # Tokens come back through a pinned buffer: a direct DMA copy, where a pageable
+        # destination goes through a staging copy (batch-1 decode iteration 0.960-0.966 ->
+        # 0.934-0.948 ms).
+        self._tokens_host = (torch.empty(max(max_decode_batch, 64), dtype=torch.int32,
+                                         pin_memory=True)
+                             if self.device.type == "cuda" else None)
 
     @property
     def pool_bytes(self) -> int:
@@ -261,7 +267,7 @@ class ModelExecutor:
             logits, choice = self._replay_decode(len(entries))
             self.last_logits = logits
             self.graph_steps += 1
-            for e, token in zip(entries, choice.cpu().tolist()):
+            for e, token in zip(entries, self._read_tokens(choice)):
                 output.tokens[e.request.request_id] = int(token)
             return output
         qsl, ctx, pos, ids, rows, emitting = [0], [], [], [], [], []
@@ -289,7 +295,7 @@ class ModelExecutor:
         if emitting:
             logits, choice = self.decoder.greedy(step, self.key_pool, self.value_pool)
             self.last_logits = logits
-            tokens = choice.cpu().tolist()
+            tokens = self._read_tokens(choice)
         else:
             self.decoder.forward_hidden(step, self.key_pool, self.value_pool)
         for request, token in zip(emitting, tokens):
@@ -301,6 +307,18 @@ class ModelExecutor:
                         and e.request.prompt_embeds is None:
                     self.prefix_cache.register(e.request.prompt_token_ids, e.cache.table.blocks)
         return output
+
+    def _read_tokens(self, choice: torch.Tensor) -> list[int]:
+        """The step's greedy tokens on the host (waits for the step)."""
+        if self._tokens_host is None or choice.dtype != torch.int32:
+            return choice.cpu().tolist()
+        n = choice.numel()
+        if n > self._tokens_host.numel():
+            self._tokens_host = torch.empty(n, dtype=torch.int32, pin_memory=True)
+        host = self._tokens_host[:n]
+        host.copy_(choice, non_blocking=True)
+        torch.cuda.current_stream(self.device).synchronize()
+        return host.tolist()
 
     # --- decode iterations replayed from HIP graphs ------------------------------------------
 
