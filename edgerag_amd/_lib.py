@@ -95,8 +95,8 @@ SIGNATURES: dict[str, tuple[list, object]] = {
         c_i32,
     ),
     "edgerag_embed_rmsnorm": (
-        [c_vp, c_i32, c_vp, c_i64, c_i32, c_vp, c_vp, c_i64, c_vp, c_i64, c_i32, c_f32, c_i32,
-         c_vp],
+        [c_vp, c_i32, c_vp, c_i64, c_i32, c_vp, c_vp, c_i64, c_vp, c_i64, c_i32, c_f32,
+         c_vp, c_vp, c_vp, c_i32, c_i32, c_vp, c_vp, c_i32, c_vp],
         c_i32,
     ),
     "edgerag_rope_append": (

@@ -198,21 +198,8 @@ class EdgeRagDecoder(nn.Module):
         spec = self.spec
         T = step.token_ids.shape[0]
         d, eps = spec.head_dim, spec.rms_norm_eps
-        # The residual stream is updated in place, so it is always a fresh tensor of this step.
-        # Token ids: the embedding rows and the first RMSNorm in one launch (the same bits as
-        # index_select + rmsnorm).
-        w0 = self.layers[0].input_layernorm.weight
-        if step.hidden is None and kernels.embed_rmsnorm_fits(self.embed_tokens):
-            hidden, x = kernels.embed_rmsnorm(step.token_ids, self.embed_tokens, w0, eps)
-        else:
-            hidden = (self.embed_tokens.index_select(0, step.token_ids) if step.hidden is None
-                      else step.hidden)
-            x = kernels.rmsnorm(hidden, w0, eps)
-        q = torch.empty((T, spec.n_q_heads, d), device=self.device, dtype=self.dtype)
-        attn_out = torch.empty_like(q)
         n_layers = len(self.layers)
         qkv0 = self.layers[0].qkv
-        rows = None
         # The fused streaming epilogues (q/k/v + RoPE + append, gate/up + SiLU * up) serve batches
         # of up to 32 tokens; larger batches run the tiled GEMM and the elementwise launch apart,
         # which is faster there.
@@ -221,10 +208,27 @@ class EdgeRagDecoder(nn.Module):
         # apart); batches of 33-64 tokens run the projection and the elementwise launch apart.
         stream_epi = T <= self.STREAM_EPILOGUE_MAX_TOKENS
         tiled_epi = T >= self.TILED_EPILOGUE_MIN_TOKENS
-        if (stream_epi or tiled_epi) and isinstance(qkv0, QuantLinear) and kernels.quant_rope_fused(
-                T, qkv0.in_features, qkv0.config.bits, qkv0.config.group_size, spec.n_q_heads,
-                spec.n_kv_heads, d, self.dtype):
-            rows = kernels.rope_rows(step.positions, self.rotary.cos, self.rotary.sin)
+        want_rows = ((stream_epi or tiled_epi) and isinstance(qkv0, QuantLinear)
+                     and kernels.quant_rope_fused(T, qkv0.in_features, qkv0.config.bits,
+                                                  qkv0.config.group_size, spec.n_q_heads,
+                                                  spec.n_kv_heads, d, self.dtype))
+        rows = None
+        w0 = self.layers[0].input_layernorm.weight
+        # The residual stream is updated in place, so it is always a fresh tensor of this step.
+        if step.hidden is None and kernels.embed_rmsnorm_fits(self.embed_tokens):
+            # Token ids: the embedding rows, the first RMSNorm and the step's rotary rows in one
+            # launch (the same bits as index_select, rmsnorm and rope_rows).
+            hidden, x, rows = kernels.embed_rmsnorm(
+                step.token_ids, self.embed_tokens, w0, eps,
+                rope=(step.positions, self.rotary.cos, self.rotary.sin) if want_rows else None)
+        else:
+            hidden = (self.embed_tokens.index_select(0, step.token_ids) if step.hidden is None
+                      else step.hidden)
+            x = kernels.rmsnorm(hidden, w0, eps)
+            if want_rows:
+                rows = kernels.rope_rows(step.positions, self.rotary.cos, self.rotary.sin)
+        q = torch.empty((T, spec.n_q_heads, d), device=self.device, dtype=self.dtype)
+        attn_out = torch.empty_like(q)
         fused = rows is not None and self._norm_fused(T)
         partials = (torch.empty(T * 256, dtype=torch.float32, device=self.device) if fused
                     else None)

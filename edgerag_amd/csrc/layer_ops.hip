@@ -71,18 +71,41 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(
 // chunks t, t + 256, ... of the row. Every load of the row (x, delta and weight) is issued before
 // any is used, so a row costs one memory round trip; chunks past the row re-read its last chunk
 // and are masked.
+// The rotary table rows at each token's position (what edgerag_rope_rows writes), gathered by the
+// embedding launch of a step: positions == NULL for none.
+struct RopeRowsArgs {
+  const int32_t* positions;
+  const void* cos_t;
+  const void* sin_t;
+  int32_t max_pos, head_dim;
+  void* cos_out;
+  void* sin_out;
+};
+
 // ids != NULL (embedding lookup + the first RMSNorm): row r of x is table row ids[r], copied to
-// h_out; an id outside [0, n_table) has no row: its h and y are written as NaN.
+// h_out; an id outside [0, n_table) has no row: its h and y are written as NaN. rr.positions !=
+// NULL: the workgroup of row r also writes row r of the rotary rows (a position outside the
+// table gets a NaN row).
 template <typename T, int NV>
 __global__ __launch_bounds__(kNormThreads) void rmsnorm_vec_kernel(
     const T* __restrict__ x, const int32_t* __restrict__ ids, int32_t n_table,
     const T* __restrict__ delta, const T* __restrict__ weight, int64_t x_stride,
     int64_t d_stride, int32_t width, float eps, T* __restrict__ h_out, T* __restrict__ y,
-    int64_t h_stride, int64_t y_stride) {
+    int64_t h_stride, int64_t y_stride, const RopeRowsArgs rr) {
 #pragma clang fp contract(off)
   constexpr int E = 16 / sizeof(T);
   const int64_t row = blockIdx.x;
   const int nch = width / E;
+  if (rr.positions != nullptr && int(threadIdx.x) < rr.head_dim) {  // wave-uniform pointer test
+    const int pos = rr.positions[row];
+    const int dd = threadIdx.x;
+    const bool ok = pos >= 0 && pos < rr.max_pos;
+    const int64_t src = int64_t(ok ? pos : 0) * rr.head_dim + dd;
+    const T c = ok ? static_cast<const T*>(rr.cos_t)[src] : round_to<T>(__builtin_nanf(""));
+    const T sn = ok ? static_cast<const T*>(rr.sin_t)[src] : round_to<T>(__builtin_nanf(""));
+    static_cast<T*>(rr.cos_out)[row * rr.head_dim + dd] = c;
+    static_cast<T*>(rr.sin_out)[row * rr.head_dim + dd] = sn;
+  }
   int64_t src = row;
   bool bad = false;
   if (ids != nullptr) {
@@ -264,7 +287,8 @@ inline bool aligned_rows(const void* p, int64_t stride_elems, int elem_size) {
 template <typename T>
 int launch_rmsnorm(const void* x, const void* delta, const void* weight, void* h_out, void* y,
                    int32_t rows, int32_t width, int64_t xs, int64_t ds, int64_t hs, int64_t ys,
-                   float eps, hipStream_t s, const int32_t* ids = nullptr, int32_t n_table = 0) {
+                   float eps, hipStream_t s, const int32_t* ids = nullptr, int32_t n_table = 0,
+                   const RopeRowsArgs& rr = RopeRowsArgs{}) {
   constexpr int E = 16 / sizeof(T);
   const int nch = width / E;
   if (width % E == 0 && aligned_rows(x, xs, sizeof(T)) && aligned_rows(delta, ds, sizeof(T)) &&
@@ -275,7 +299,7 @@ int launch_rmsnorm(const void* x, const void* delta, const void* weight, void* h
   hipLaunchKernelGGL((rmsnorm_vec_kernel<T, NV>), dim3(rows), dim3(kNormThreads), 0, s,         \
                      static_cast<const T*>(x), ids, n_table, static_cast<const T*>(delta),      \
                      static_cast<const T*>(weight), xs, ds, width, eps,                         \
-                     static_cast<T*>(h_out), static_cast<T*>(y), hs, ys)
+                     static_cast<T*>(h_out), static_cast<T*>(y), hs, ys, rr)
     if (nv <= 1) EDGERAG_NORMV(1);
     else if (nv <= 2) EDGERAG_NORMV(2);
     else if (nv <= 4) EDGERAG_NORMV(4);
@@ -283,7 +307,7 @@ int launch_rmsnorm(const void* x, const void* delta, const void* weight, void* h
 #undef EDGERAG_NORMV
     return check_launch("edgerag_rmsnorm");
   }
-  if (ids != nullptr)
+  if (ids != nullptr || rr.positions != nullptr)
     return fail(EDGERAG_EUNSUPPORTED, "edgerag_embed_rmsnorm: rows of %d elements not in "
                 "16-byte chunks (or above 8 x %d chunks)", width, kNormThreads);
   const int per = (width + kNormThreads - 1) / kNormThreads;
@@ -396,7 +420,10 @@ extern "C" int edgerag_rmsnorm(const void* x, int64_t x_stride, const void* delt
 extern "C" int edgerag_embed_rmsnorm(const int32_t* ids, int32_t rows, const void* table,
                                      int64_t table_stride, int32_t vocab, const void* weight,
                                      void* h_out, int64_t h_stride, void* y, int64_t y_stride,
-                                     int32_t width, float eps, int32_t dtype, void* stream) {
+                                     int32_t width, float eps, const int32_t* positions,
+                                     const void* cos_table, const void* sin_table,
+                                     int32_t max_pos, int32_t head_dim, void* cos_out,
+                                     void* sin_out, int32_t dtype, void* stream) {
   clear_error();
   if (rows < 0 || width <= 0 || vocab <= 0)
     return fail(EDGERAG_EINVAL, "edgerag_embed_rmsnorm: rows %d width %d vocab %d", rows, width,
@@ -404,11 +431,17 @@ extern "C" int edgerag_embed_rmsnorm(const int32_t* ids, int32_t rows, const voi
   if (rows == 0) return EDGERAG_OK;
   if (ids == nullptr || table == nullptr || weight == nullptr || h_out == nullptr || y == nullptr)
     return fail(EDGERAG_EINVAL, "edgerag_embed_rmsnorm: NULL pointer");
+  const RopeRowsArgs rr{positions, cos_table, sin_table, max_pos, head_dim, cos_out, sin_out};
+  if (positions != nullptr &&
+      (cos_table == nullptr || sin_table == nullptr || cos_out == nullptr || sin_out == nullptr ||
+       max_pos <= 0 || head_dim <= 0 || head_dim > kNormThreads))
+    return fail(EDGERAG_EINVAL, "edgerag_embed_rmsnorm: rotary rows need both tables, both "
+                "outputs, max_pos > 0 and 0 < head_dim <= %d", kNormThreads);
   auto s = static_cast<hipStream_t>(stream);
   switch (dtype) {
-    case EDGERAG_F32: return launch_rmsnorm<float>(table, nullptr, weight, h_out, y, rows, width, table_stride, 0, h_stride, y_stride, eps, s, ids, vocab);
-    case EDGERAG_F16: return launch_rmsnorm<f16>(table, nullptr, weight, h_out, y, rows, width, table_stride, 0, h_stride, y_stride, eps, s, ids, vocab);
-    case EDGERAG_BF16: return launch_rmsnorm<bf16>(table, nullptr, weight, h_out, y, rows, width, table_stride, 0, h_stride, y_stride, eps, s, ids, vocab);
+    case EDGERAG_F32: return launch_rmsnorm<float>(table, nullptr, weight, h_out, y, rows, width, table_stride, 0, h_stride, y_stride, eps, s, ids, vocab, rr);
+    case EDGERAG_F16: return launch_rmsnorm<f16>(table, nullptr, weight, h_out, y, rows, width, table_stride, 0, h_stride, y_stride, eps, s, ids, vocab, rr);
+    case EDGERAG_BF16: return launch_rmsnorm<bf16>(table, nullptr, weight, h_out, y, rows, width, table_stride, 0, h_stride, y_stride, eps, s, ids, vocab, rr);
   }
   return fail(EDGERAG_EINVAL, "edgerag_embed_rmsnorm: dtype %d", dtype);
 }

@@ -736,11 +736,13 @@ def embed_rmsnorm_fits(table: torch.Tensor) -> bool:
 
 
 def embed_rmsnorm(ids: torch.Tensor, table: torch.Tensor, weight: torch.Tensor, eps: float,
-                  h_out: torch.Tensor | None = None,
-                  out: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+                  h_out: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                  rope: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
+                  ) -> tuple[torch.Tensor, torch.Tensor, tuple[torch.Tensor, torch.Tensor] | None]:
     """The embedding rows of the int32 ``ids`` (``h``, a copy of ``table[ids]``) and their
-    RMSNorm (``out``), in one launch; returns ``(h, out)``. An id outside the table gives a row
-    of NaN in both."""
+    RMSNorm (``out``), in one launch; returns ``(h, out, rows)``. An id outside the table gives a
+    row of NaN in both. ``rope = (positions, cos, sin)``: the same launch also gathers what
+    :func:`rope_rows` returns (``rows``; None without ``rope``)."""
     require_device(ids, table, weight, h_out, out)
     if ids.dtype != torch.int32 or ids.dim() != 1 or (ids.numel() > 1 and ids.stride(0) != 1):
         raise ValueError("ids must be a contiguous int32 vector")
@@ -752,12 +754,29 @@ def embed_rmsnorm(ids: torch.Tensor, table: torch.Tensor, weight: torch.Tensor, 
         h_out = torch.empty((rows, width), device=table.device, dtype=table.dtype)
     if out is None:
         out = torch.empty_like(h_out)
+    rope_args, rows_out = (None, None, None, 0, 0, None, None), None
+    if rope is not None:
+        positions, cos, sin = rope
+        require_device(positions, cos, sin)
+        if positions.dtype != torch.int32 or positions.numel() != rows or \
+                not positions.is_contiguous():
+            raise ValueError("positions must be a contiguous int32 vector, one per id")
+        if cos.shape != sin.shape or cos.dim() != 2 or not (cos.is_contiguous() and
+                                                           sin.is_contiguous()) \
+                or cos.dtype != table.dtype or sin.dtype != table.dtype:
+            raise ValueError("cos and sin must be matching contiguous (max_pos, head_dim) tables "
+                             "of the embedding's dtype")
+        c = torch.empty((rows, cos.shape[1]), dtype=cos.dtype, device=cos.device)
+        sn = torch.empty_like(c)
+        rope_args = (positions.data_ptr(), cos.data_ptr(), sin.data_ptr(), cos.shape[0],
+                     cos.shape[1], c.data_ptr(), sn.data_ptr())
+        rows_out = (c, sn)
     call(
         "edgerag_embed_rmsnorm", ids.data_ptr(), rows, table.data_ptr(), table.stride(0), vocab,
         weight.data_ptr(), h_out.data_ptr(), h_out.stride(0), out.data_ptr(), out.stride(0),
-        width, float(eps), dtype_code(table.dtype), stream_ptr(table.device),
+        width, float(eps), *rope_args, dtype_code(table.dtype), stream_ptr(table.device),
     )
-    return h_out, out
+    return h_out, out, rows_out
 
 
 def rope_append(qkv: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,

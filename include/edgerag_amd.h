@@ -471,13 +471,17 @@ int edgerag_rmsnorm(const void* x, int64_t x_stride, const void* delta, int64_t 
  *   y[t]     = weight * dtype(h * rsqrt(mean(h^2) + eps))   as edgerag_rmsnorm computes it
  * An id outside [0, vocab) has no table row: that row's h and y are written as NaN (the
  * reference's nn.Embedding raises on such an id). Rows must be whole 16-byte chunks, at most
- * 8 x 256 of them (EDGERAG_EUNSUPPORTED otherwise). Replaces `embed_tokens(input_ids)`
- * (edgerag/core/model.py:109) followed by the first layer's input RMSNorm
- * (edgerag/core/layers.py:27-47).
+ * 8 x 256 of them (EDGERAG_EUNSUPPORTED otherwise). With positions != NULL the same launch also
+ * writes what edgerag_rope_rows writes: cos_out / sin_out [rows, head_dim] = the rows of the
+ * [max_pos, head_dim] tables at positions[t] (NaN rows outside the table; head_dim <= 256).
+ * Replaces `embed_tokens(input_ids)` (edgerag/core/model.py:109) followed by the first layer's
+ * input RMSNorm (edgerag/core/layers.py:27-47), and the step's rotary-row gather.
  */
 int edgerag_embed_rmsnorm(const int32_t* ids, int32_t rows, const void* table,
                           int64_t table_stride, int32_t vocab, const void* weight, void* h_out,
                           int64_t h_stride, void* y, int64_t y_stride, int32_t width, float eps,
+                          const int32_t* positions, const void* cos_table, const void* sin_table,
+                          int32_t max_pos, int32_t head_dim, void* cos_out, void* sin_out,
                           int32_t dtype, void* stream);
 
 /*

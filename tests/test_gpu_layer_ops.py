@@ -16,6 +16,11 @@ from tests.conftest import seeded
 pytestmark = pytest.mark.gpu
 
 
+def _same(a: torch.Tensor, b: torch.Tensor) -> bool:
+    """Equal values, NaN matching NaN."""
+    return bool(((a == b) | (a.isnan() & b.isnan())).all()) and a.shape == b.shape
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
 @pytest.mark.parametrize("width", [128, 2048, 8192, 1000])
 def test_add_rmsnorm(device, dtype, width) -> None:
@@ -49,15 +54,25 @@ def test_embed_rmsnorm_equals_lookup_then_rmsnorm(device, dtype, width) -> None:
     table = torch.randn(vocab, width, generator=g).to(dtype).to(device)
     w = (1 + 0.1 * torch.randn(width, generator=g)).to(dtype).to(device)
     ids = torch.tensor([3, 499, 0, 17, 3, 250, 1, 498], dtype=torch.int32)
-    h, y = kernels.embed_rmsnorm(ids.to(device), table, w, 1e-5)
+    h, y, none = kernels.embed_rmsnorm(ids.to(device), table, w, 1e-5)
+    assert none is None
     h_ref = table.index_select(0, ids.to(device))
     assert torch.equal(h, h_ref)
     assert torch.equal(y, kernels.rmsnorm(h_ref, w, 1e-5))
+    # With the rotary rows gathered in the same launch: what rope_rows writes, positions outside
+    # the table included (NaN rows); the embedding outputs unchanged.
+    cos = torch.randn(300, 64, generator=g).to(dtype).to(device)
+    sin = torch.randn(300, 64, generator=g).to(dtype).to(device)
+    pos = torch.tensor([0, 299, 5, 300, -1, 17, 17, 128], dtype=torch.int32).to(device)
+    h3, y3, (c3, s3) = kernels.embed_rmsnorm(ids.to(device), table, w, 1e-5, rope=(pos, cos, sin))
+    c_ref, s_ref = kernels.rope_rows(pos, cos, sin)
+    assert torch.equal(h3, h) and torch.equal(y3, y)
+    assert _same(c3, c_ref) and _same(s3, s_ref) and c3[[3, 4]].isnan().all()
     tol = {torch.float32: 1e-5, torch.float16: 2e-3, torch.bfloat16: 1.6e-2}[dtype]
     torch.testing.assert_close(y.cpu().float(), om.rms_norm(h_ref.cpu(), w.cpu(), 1e-5).float(),
                                rtol=tol, atol=tol)
     bad = torch.tensor([5, -1, vocab, 7], dtype=torch.int32)
-    h2, y2 = kernels.embed_rmsnorm(bad.to(device), table, w, 1e-5)
+    h2, y2, _ = kernels.embed_rmsnorm(bad.to(device), table, w, 1e-5)
     assert h2[[1, 2]].isnan().all() and y2[[1, 2]].isnan().all()
     assert torch.equal(h2[[0, 3]], table[[5, 7]]) and not y2[[0, 3]].isnan().any()
     assert not kernels.embed_rmsnorm_fits(torch.zeros(4, 13, device=device, dtype=torch.float16))
